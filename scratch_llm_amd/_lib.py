@@ -1,0 +1,121 @@
+"""ctypes binding of libsqx_hip.so (the C ABI declared in include/sqx.h).
+
+The library is loaded after torch so that the process maps one HIP runtime (torch's); every call
+passes device pointers from torch tensors and torch's current stream. Nothing here falls back to
+another implementation: a missing library, a CPU tensor or a non-zero status raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libsqx_hip.so"
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+DTYPE_F16 = 2
+
+_TORCH_TO_SQX = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
+
+_c_i = ctypes.c_int
+_c_i64 = ctypes.c_int64
+_c_p = ctypes.c_void_p
+
+# name -> (restype, argtypes). Kept in the order of include/sqx.h.
+_SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "sqx_last_error": (ctypes.c_char_p, []),
+    "sqx_abi_version": (_c_i, []),
+    "sqx_int4_quantize_sym": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "sqx_int4_pack": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
+    "sqx_int4_unpack": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
+    "sqx_int4_dequantize": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_int4_tiled_weight_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "sqx_int4_tiled_param_count": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "sqx_int4_tile": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_i, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p]),
+    "sqx_int4_tile_packed": (_c_i, [_c_p, _c_p, _c_i, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "sqx_int4_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i]),
+    "sqx_int4_linear_default_splits": (_c_i, [_c_i64, _c_i64, _c_i64]),
+    "sqx_int4_linear": (
+        _c_i,
+        [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p, _c_i64, _c_p],
+    ),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class SqxError(RuntimeError):
+    """A libsqx_hip.so call returned a non-zero status."""
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+                )
+            lib = ctypes.CDLL(os.fspath(LIB_PATH), mode=ctypes.RTLD_GLOBAL)
+            for name, (res, args) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def exported_names() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().sqx_last_error().decode(errors="replace")
+        if rc == -1 and "not divisible" in msg:
+            raise ValueError(msg)
+        raise SqxError(f"{what} failed (status {rc}): {msg}")
+
+
+def sqx_dtype(dt: torch.dtype) -> int:
+    try:
+        return _TORCH_TO_SQX[dt]
+    except KeyError:
+        raise TypeError(f"dtype {dt} is not supported by the HIP kernels") from None
+
+
+def require_device(*tensors: torch.Tensor | None, fn: str) -> torch.device:
+    """All tensors must live on one ROCm device; returns it. CPU tensors raise RuntimeError."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"{fn}: the MI355X kernels need device tensors, got a {t.device.type} tensor "
+                "(this library has no CPU path; use the reference implementation on CPU)"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"{fn}: tensors on different devices ({dev} vs {t.device})")
+    if dev is None:
+        raise RuntimeError(f"{fn}: no tensor argument")
+    return dev
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

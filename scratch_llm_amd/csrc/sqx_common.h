@@ -1,0 +1,119 @@
+// Shared helpers for the sqx HIP kernels (gfx950 / CDNA4 only).
+//
+// Every extern "C" entry point returns 0 on success or a negative SQX_E* code and records a
+// message retrievable with sqx_last_error() (thread-local). Kernels never allocate; callers pass
+// device pointers and a hipStream_t.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "../../include/sqx.h"
+
+namespace sqx {
+
+// ---------------------------------------------------------------- error reporting (host) ----
+void set_error(const char* fmt, ...);
+
+#define SQX_REQUIRE(cond, code, ...)        \
+  do {                                      \
+    if (!(cond)) {                          \
+      ::sqx::set_error(__VA_ARGS__);        \
+      return (code);                        \
+    }                                       \
+  } while (0)
+
+#define SQX_LAUNCH_CHECK(what)                                                        \
+  do {                                                                                \
+    hipError_t e_ = hipGetLastError();                                                \
+    if (e_ != hipSuccess) {                                                           \
+      ::sqx::set_error("%s: launch failed: %s", (what), hipGetErrorString(e_));       \
+      return SQX_E_HIP;                                                               \
+    }                                                                                 \
+  } while (0)
+
+inline hipStream_t as_stream(sqx_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------- vector types (device) -----
+typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
+typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
+typedef unsigned u32x4_t __attribute__((__vector_size__(4 * sizeof(unsigned))));
+
+// ---------------------------------------------------------------- scalar conversions --------
+// bf16 <-> fp32 by bit manipulation. fp32 -> bf16 is round-to-nearest-even with NaN kept quiet,
+// the same rounding torch's `.to(torch.bfloat16)` performs.
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t b) {
+  uint32_t u = static_cast<uint32_t>(b) << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ inline float f16_bits_to_f32(uint16_t b) {
+  _Float16 h;
+  __builtin_memcpy(&h, &b, 2);
+  return static_cast<float>(h);
+}
+
+__device__ inline uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = static_cast<_Float16>(f);  // round-to-nearest-even
+  uint16_t b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
+
+// Load element i of an array whose element type is given at run time (fp32 / bf16 / fp16) as fp32.
+// Every conversion here is exact.
+__device__ inline float load_as_f32(const void* p, int dtype, int64_t i) {
+  if (dtype == SQX_DTYPE_F32) return static_cast<const float*>(p)[i];
+  uint16_t b = static_cast<const uint16_t*>(p)[i];
+  return dtype == SQX_DTYPE_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+// Activation element traits for the MFMA paths: the 16-bit storage type, the "magic" exponent that
+// turns a 4-bit unsigned code u into the exactly representable value MAGIC + u by OR-ing it into
+// the mantissa, and the conversions of the fp32 accumulator back to storage.
+struct ActBF16 {
+  static constexpr uint32_t kMagicPair = 0x43004300u;  // bf16 128.0 in both halves
+  static constexpr float kMagic = 128.0f;
+  __device__ static inline float to_f32(uint16_t b) { return bf16_bits_to_f32(b); }
+  __device__ static inline uint16_t from_f32(float f) { return f32_to_bf16_bits(f); }
+  __device__ static inline uint32_t pair_from_f32(float v) {  // v exactly representable
+    uint32_t h = f32_to_bf16_bits(v);
+    return h | (h << 16);
+  }
+  __device__ static inline f32x4_t mfma(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+};
+
+struct ActF16 {
+  static constexpr uint32_t kMagicPair = 0x64006400u;  // fp16 1024.0 in both halves
+  static constexpr float kMagic = 1024.0f;
+  __device__ static inline float to_f32(uint16_t b) { return f16_bits_to_f32(b); }
+  __device__ static inline uint16_t from_f32(float f) { return f32_to_f16_bits(f); }
+  __device__ static inline uint32_t pair_from_f32(float v) {
+    uint32_t h = f32_to_f16_bits(v);
+    return h | (h << 16);
+  }
+  __device__ static inline f32x4_t mfma(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+};
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace sqx

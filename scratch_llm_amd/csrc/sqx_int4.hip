@@ -1,0 +1,605 @@
+// INT4 group-wise weights on gfx950: bit-exact quantize / pack / unpack / dequantize
+// (src/scratch_llm/quant/int4_group.py) and the fused dequant linear that streams tiled codes.
+//
+// Tiled layout (the HBM layout the linear reads; written by sqx_int4_tile):
+//   T = ceil(rows/16) row tiles, KB = ceil(cols/128) k-blocks of 128 columns.
+//   Block (t, kb) is 1024 contiguous bytes at ((t*KB + kb) * 1024). Lane L (0..63) of the wave
+//   that consumes the block owns bytes [16L, 16L+16) = four dwords. Dword i (0..3) holds the codes
+//   of row r = 16t + (L & 15), columns c = kb*128 + 32i + 8(L >> 4) + e (e = 0..7): element e sits in
+//   nibble e/2 when e is even and nibble 4 + e/2 when e is odd, so ((d >> 4p) & 0x000F000F) yields
+//   the column pair (2p, 2p+1) in the low/high 16-bit halves. Codes are stored unsigned:
+//   u = q + 8 for symmetric codes q in [-8, 7], u as given for asymmetric codes.
+//   Per-group parameters: Gp = KB * 128/group groups per row, stored [T][Gp][16] so one 64-byte
+//   line serves the 16 rows of a tile. Padding rows / columns carry a zero scale.
+//
+// Linear: one wave computes a 16-row tile for up to 16*MCH activation rows with
+// v_mfma_f32_16x16x32_{bf16,f16}. A = activations (rows = tokens), B = weights (columns = weight
+// rows). OR-ing a code into the mantissa of MAGIC (bf16 128.0 / fp16 1024.0) gives MAGIC + u
+// exactly, so B needs three VALU ops per column pair; a second set of MFMAs with the constant
+// B = -(MAGIC + zero) removes the offset, and the group scale is applied to the fp32 partial.
+#include "sqx_common.h"
+
+#include <float.h>
+
+namespace sqx {
+
+// ----------------------------------------------------------------------------------------------
+// quantize_groupwise_int4 (int4_group.py:108-129)
+// ----------------------------------------------------------------------------------------------
+// Fast path: group is a power of two in [8, 512]; each lane owns 8 consecutive elements, the
+// group's lanes are consecutive in the wave, and the absmax is reduced with xor shuffles.
+template <int LPG>
+__global__ __launch_bounds__(256) void int4_quantize_sym_kernel(const void* __restrict__ w, int w_dtype,
+                                                                int64_t n_elems, int64_t group,
+                                                                int8_t* __restrict__ q,
+                                                                float* __restrict__ scales) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t e0 = i * 8;
+  const bool live = e0 < n_elems;
+  float v[8];
+  float amax = 0.0f;
+  bool nan = false;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    v[e] = live ? load_as_f32(w, w_dtype, e0 + e) : 0.0f;
+    float a = fabsf(v[e]);
+    nan |= (a != a);
+    amax = fmaxf(amax, a);
+  }
+#pragma unroll
+  for (int off = 1; off < LPG; off <<= 1) {
+    amax = fmaxf(amax, __shfl_xor(amax, off));
+    nan |= (__shfl_xor((int)nan, off) != 0);
+  }
+  if (!live) return;
+  // torch: scales = (absmax / 7).clamp_min(finfo(fp32).tiny); amax propagates NaN.
+  float s = nan ? __builtin_nanf("") : __fdiv_rn(amax, 7.0f);
+  if (s < FLT_MIN) s = FLT_MIN;
+  uint64_t packed = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float r = __builtin_rintf(__fdiv_rn(v[e], s));  // round half to even, like torch.round
+    r = fminf(fmaxf(r, -8.0f), 7.0f);
+    int8_t c = (r == r) ? static_cast<int8_t>(r) : 0;  // NaN codes are unspecified upstream
+    packed |= static_cast<uint64_t>(static_cast<uint8_t>(c)) << (8 * e);
+  }
+  *reinterpret_cast<uint64_t*>(q + e0) = packed;
+  if ((threadIdx.x & (LPG - 1)) == 0) scales[e0 / group] = s;
+}
+
+// Generic path: any group size; one thread per group.
+__global__ __launch_bounds__(256) void int4_quantize_sym_generic_kernel(const void* __restrict__ w, int w_dtype,
+                                                                        int64_t n_groups, int64_t group,
+                                                                        int8_t* __restrict__ q,
+                                                                        float* __restrict__ scales) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= n_groups) return;
+  const int64_t base = g * group;
+  float amax = 0.0f;
+  bool nan = false;
+  for (int64_t e = 0; e < group; ++e) {
+    float a = fabsf(load_as_f32(w, w_dtype, base + e));
+    nan |= (a != a);
+    amax = fmaxf(amax, a);
+  }
+  float s = nan ? __builtin_nanf("") : __fdiv_rn(amax, 7.0f);
+  if (s < FLT_MIN) s = FLT_MIN;
+  for (int64_t e = 0; e < group; ++e) {
+    float r = __builtin_rintf(__fdiv_rn(load_as_f32(w, w_dtype, base + e), s));
+    r = fminf(fmaxf(r, -8.0f), 7.0f);
+    q[base + e] = (r == r) ? static_cast<int8_t>(r) : 0;
+  }
+  scales[g] = s;
+}
+
+// ----------------------------------------------------------------------------------------------
+// pack_int4 / unpack_int4 (int4_group.py:62-102)
+// ----------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void int4_pack_kernel(const int8_t* __restrict__ q, int64_t n,
+                                                        uint8_t* __restrict__ packed) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nb = (n + 1) / 2;
+  if (i >= nb) return;
+  const uint8_t hi = static_cast<uint8_t>(q[2 * i]) & 0xF;
+  const uint8_t lo = (2 * i + 1 < n) ? (static_cast<uint8_t>(q[2 * i + 1]) & 0xF) : 0;
+  packed[i] = static_cast<uint8_t>((hi << 4) | lo);
+}
+
+__device__ inline int8_t sext4(uint32_t nib) { return static_cast<int8_t>(nib >= 8 ? (int)nib - 16 : (int)nib); }
+
+__global__ __launch_bounds__(256) void int4_unpack_kernel(const uint8_t* __restrict__ packed, int64_t n,
+                                                          int8_t* __restrict__ q) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (2 * i >= n) return;
+  const uint32_t b = packed[i];
+  q[2 * i] = sext4(b >> 4);
+  if (2 * i + 1 < n) q[2 * i + 1] = sext4(b & 0xF);
+}
+
+// ----------------------------------------------------------------------------------------------
+// dequantize_groupwise_int4 (int4_group.py:132-142)
+// ----------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void int4_dequantize_kernel(const int8_t* __restrict__ q,
+                                                              const float* __restrict__ scales,
+                                                              int64_t n_elems, int64_t group,
+                                                              float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_elems) return;
+  out[i] = static_cast<float>(q[i]) * scales[i / group];
+}
+
+// ----------------------------------------------------------------------------------------------
+// Tile re-layout
+// ----------------------------------------------------------------------------------------------
+// One thread per output dword. SRC_PACKED reads the reference byte stream (high nibble = even
+// element), otherwise int8 codes. SIGNED stores u = q + 8.
+template <bool SRC_PACKED, bool SIGNED>
+__global__ __launch_bounds__(256) void int4_tile_weights_kernel(const void* __restrict__ src, int64_t rows,
+                                                                int64_t cols, int64_t KB, int64_t n_dwords,
+                                                                uint32_t* __restrict__ wt) {
+  const int64_t d = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= n_dwords) return;
+  const int i = static_cast<int>(d & 3);
+  const int L = static_cast<int>((d >> 2) & 63);
+  const int64_t blk = d >> 8;  // t*KB + kb
+  const int64_t t = blk / KB;
+  const int64_t kb = blk - t * KB;
+  const int64_t r = 16 * t + (L & 15);
+  const int64_t c0 = kb * 128 + 32 * i + 8 * (L >> 4);
+  uint32_t word = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t c = c0 + e;
+    uint32_t u = SIGNED ? 8u : 0u;
+    if (r < rows && c < cols) {
+      if (SRC_PACKED) {
+        const int64_t f = r * cols + c;
+        const uint32_t b = static_cast<const uint8_t*>(src)[f >> 1];
+        const uint32_t nib = (f & 1) ? (b & 0xF) : (b >> 4);
+        u = nib ^ 8u;  // two's-complement nibble q -> q + 8
+      } else {
+        const int8_t qv = static_cast<const int8_t*>(src)[r * cols + c];
+        u = SIGNED ? static_cast<uint32_t>(qv + 8) : static_cast<uint32_t>(qv);
+        u &= 0xF;
+      }
+    }
+    const int pos = (e & 1) ? (16 + 4 * (e >> 1)) : (4 * (e >> 1));
+    word |= u << pos;
+  }
+  wt[d] = word;
+}
+
+// One thread per tiled parameter element; param elements are 4 (F32) or 2 (BF16) bytes.
+template <typename P>
+__global__ __launch_bounds__(256) void int4_tile_params_kernel(const P* __restrict__ src, int64_t rows,
+                                                               int64_t n_groups, int64_t Gp, int64_t n_out,
+                                                               P* __restrict__ dst) {
+  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= n_out) return;
+  const int64_t nl = o & 15;
+  const int64_t tg = o >> 4;
+  const int64_t t = tg / Gp;
+  const int64_t g = tg - t * Gp;
+  const int64_t r = 16 * t + nl;
+  dst[o] = (r < rows && g < n_groups) ? src[r * n_groups + g] : P(0);
+}
+
+// ----------------------------------------------------------------------------------------------
+// The linear
+// ----------------------------------------------------------------------------------------------
+template <bool PBF16>
+__device__ inline float load_param(const void* p, int64_t idx) {
+  if (PBF16) return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[idx]);
+  return static_cast<const float*>(p)[idx];
+}
+
+template <class A, int GROUP, bool ASYM, bool PBF16, int MCH>
+__global__ __launch_bounds__(256) void int4_linear_kernel(
+    const u32x4_t* __restrict__ wt, const void* __restrict__ st, const void* __restrict__ zt,
+    const uint16_t* __restrict__ x, uint16_t* __restrict__ y, const uint16_t* __restrict__ bias,
+    float* __restrict__ part, int* __restrict__ cnt, int M, int N, int K, int T, int KB, int S,
+    int kb_per) {
+  constexpr int NG = 128 / GROUP;  // groups per k-block
+  constexpr int MPG = 4 / NG;      // MFMAs (of K = 32) per group
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int s = blockIdx.y;
+  const int kb0 = s * kb_per;
+  const int kb1 = min(KB, kb0 + kb_per);
+  const int nl = lane & 15;  // weight row within the tile (B column) == A row within a chunk
+  const int jg = lane >> 4;  // 8-column slice within each 32-column MFMA step
+  const int Gp = KB * NG;
+
+  f32x4_t yacc[MCH];
+  const uint16_t* xrow[MCH];
+  bool mok[MCH];
+#pragma unroll
+  for (int c = 0; c < MCH; ++c) {
+    yacc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int m = c * 16 + nl;
+    mok[c] = m < M;
+    xrow[c] = x + (int64_t)(mok[c] ? m : 0) * K + 8 * jg;
+  }
+  const u32x4_t* wp = wt + (int64_t)t * KB * 64 + lane;
+  const int64_t pbase = (int64_t)t * Gp * 16 + nl;
+  const uint32_t sym_off = A::pair_from_f32(-(A::kMagic + 8.0f));
+
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const u32x4_t w = __builtin_nontemporal_load(wp + (int64_t)kb * 64);
+    u32x4_t xv[MCH][4];
+#pragma unroll
+    for (int c = 0; c < MCH; ++c) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int k0 = kb * 128 + 32 * i + 8 * jg;
+        xv[c][i] = (mok[c] && k0 < K) ? *reinterpret_cast<const u32x4_t*>(xrow[c] + kb * 128 + 32 * i)
+                                       : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+    float sc[NG];
+    float zf[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const int64_t pi = pbase + (int64_t)(kb * NG + g) * 16;
+      sc[g] = load_param<PBF16>(st, pi);
+      zf[g] = ASYM ? load_param<PBF16>(zt, pi) : 8.0f;
+    }
+    u32x4_t b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t d = w[i];
+      b[i] = u32x4_t{(d & 0x000F000Fu) | A::kMagicPair, ((d >> 4) & 0x000F000Fu) | A::kMagicPair,
+                     ((d >> 8) & 0x000F000Fu) | A::kMagicPair, ((d >> 12) & 0x000F000Fu) | A::kMagicPair};
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const uint32_t off = ASYM ? A::pair_from_f32(-(A::kMagic + zf[g])) : sym_off;
+      const u32x4_t boff = u32x4_t{off, off, off, off};
+#pragma unroll
+      for (int c = 0; c < MCH; ++c) {
+        f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = g * MPG; i < (g + 1) * MPG; ++i) acc = A::mfma(xv[c][i], b[i], acc);
+#pragma unroll
+        for (int i = g * MPG; i < (g + 1) * MPG; ++i) acc = A::mfma(xv[c][i], boff, acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yacc[c][r] = fmaf(sc[g], acc[r], yacc[c][r]);
+      }
+    }
+  }
+
+  const int n = t * 16 + nl;
+  if (S == 1) {
+#pragma unroll
+    for (int c = 0; c < MCH; ++c) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = c * 16 + 4 * jg + r;
+        if (m < M && n < N) {
+          float v = yacc[c][r];
+          if (bias) v += A::to_f32(bias[n]);
+          y[(int64_t)m * N + n] = A::from_f32(v);
+        }
+      }
+    }
+    return;
+  }
+
+  // Split-K: publish this split's partial tile, then the last split to arrive sums all partials
+  // in split order (deterministic) and writes the output. The counter is reset for the next call.
+  float* mine = part + ((int64_t)t * S + s) * (16 * MCH * 16);
+#pragma unroll
+  for (int c = 0; c < MCH; ++c) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = c * 16 + 4 * jg + r;
+      if (m < M) mine[m * 16 + nl] = yacc[c][r];
+    }
+  }
+  __threadfence();
+  int prev = 0;
+  if (lane == 0) prev = atomicAdd(&cnt[t], 1);
+  prev = __shfl(prev, 0);
+  if (prev != S - 1) return;
+  __threadfence();
+  const float* all = part + (int64_t)t * S * (16 * MCH * 16);
+#pragma unroll
+  for (int c = 0; c < MCH; ++c) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = c * 16 + 4 * jg + r;
+      if (m < M) {
+        float v = 0.0f;
+        for (int ss = 0; ss < S; ++ss) v += all[(int64_t)ss * (16 * MCH * 16) + m * 16 + nl];
+        if (n < N) {
+          if (bias) v += A::to_f32(bias[n]);
+          y[(int64_t)m * N + n] = A::from_f32(v);
+        }
+      }
+    }
+  }
+  if (lane == 0) atomicExch(&cnt[t], 0);
+}
+
+static int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
+
+static int linear_mch(int64_t m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
+
+template <class A, int GROUP, bool ASYM, bool PBF16>
+static void launch_linear_g(int mch, dim3 grid, hipStream_t stream, const u32x4_t* wt, const void* st,
+                            const void* zt, const uint16_t* x, uint16_t* y, const uint16_t* bias,
+                            float* part, int* cnt, int M, int N, int K, int T, int KB, int S, int kb_per) {
+  if (mch == 1)
+    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 1>), grid, dim3(256), 0, stream, wt, st, zt,
+                       x, y, bias, part, cnt, M, N, K, T, KB, S, kb_per);
+  else if (mch == 2)
+    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 2>), grid, dim3(256), 0, stream, wt, st, zt,
+                       x, y, bias, part, cnt, M, N, K, T, KB, S, kb_per);
+  else
+    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 4>), grid, dim3(256), 0, stream, wt, st, zt,
+                       x, y, bias, part, cnt, M, N, K, T, KB, S, kb_per);
+}
+
+template <class A, bool ASYM, bool PBF16>
+static void launch_linear_a(int group, int mch, dim3 grid, hipStream_t stream, const u32x4_t* wt,
+                            const void* st, const void* zt, const uint16_t* x, uint16_t* y,
+                            const uint16_t* bias, float* part, int* cnt, int M, int N, int K, int T, int KB,
+                            int S, int kb_per) {
+  if (group == 128)
+    launch_linear_g<A, 128, ASYM, PBF16>(mch, grid, stream, wt, st, zt, x, y, bias, part, cnt, M, N, K, T, KB, S,
+                                         kb_per);
+  else if (group == 64)
+    launch_linear_g<A, 64, ASYM, PBF16>(mch, grid, stream, wt, st, zt, x, y, bias, part, cnt, M, N, K, T, KB, S,
+                                        kb_per);
+  else
+    launch_linear_g<A, 32, ASYM, PBF16>(mch, grid, stream, wt, st, zt, x, y, bias, part, cnt, M, N, K, T, KB, S,
+                                        kb_per);
+}
+
+}  // namespace sqx
+
+using namespace sqx;
+
+// ==============================================================================================
+// extern "C" entry points
+// ==============================================================================================
+static bool is_float_dtype(int d) { return d == SQX_DTYPE_F32 || d == SQX_DTYPE_BF16 || d == SQX_DTYPE_F16; }
+
+extern "C" int sqx_int4_quantize_sym(const void* w, int w_dtype, int64_t rows, int64_t cols, int64_t group,
+                                     int8_t* q, float* scales, sqx_stream_t stream) {
+  SQX_REQUIRE(w && q && scales, SQX_E_ARG, "sqx_int4_quantize_sym: null pointer");
+  SQX_REQUIRE(is_float_dtype(w_dtype), SQX_E_ARG, "sqx_int4_quantize_sym: unsupported w_dtype %d", w_dtype);
+  SQX_REQUIRE(rows >= 0 && cols >= 0 && group > 0, SQX_E_ARG, "sqx_int4_quantize_sym: bad shape");
+  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld",
+              (long long)cols, (long long)group);
+  const int64_t n = rows * cols;
+  if (n == 0) return SQX_OK;
+  hipStream_t s = as_stream(stream);
+  const bool fast = group >= 8 && group <= 512 && (group & (group - 1)) == 0 &&
+                    (reinterpret_cast<uintptr_t>(q) % 8 == 0);
+  if (fast) {
+    const int64_t threads = n / 8;
+    const dim3 grid(static_cast<unsigned>(ceil_div(threads, 256)));
+    switch (group / 8) {
+#define SQX_Q_CASE(L) \
+  case L: hipLaunchKernelGGL(int4_quantize_sym_kernel<L>, grid, dim3(256), 0, s, w, w_dtype, n, group, q, scales); break;
+      SQX_Q_CASE(1) SQX_Q_CASE(2) SQX_Q_CASE(4) SQX_Q_CASE(8) SQX_Q_CASE(16) SQX_Q_CASE(32) SQX_Q_CASE(64)
+#undef SQX_Q_CASE
+    }
+  } else {
+    const int64_t ng = n / group;
+    hipLaunchKernelGGL(int4_quantize_sym_generic_kernel, dim3(static_cast<unsigned>(ceil_div(ng, 256))), dim3(256),
+                       0, s, w, w_dtype, ng, group, q, scales);
+  }
+  SQX_LAUNCH_CHECK("sqx_int4_quantize_sym");
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_pack(const int8_t* q, int64_t n, uint8_t* packed, sqx_stream_t stream) {
+  SQX_REQUIRE(n >= 0, SQX_E_ARG, "sqx_int4_pack: negative length");
+  if (n == 0) return SQX_OK;
+  SQX_REQUIRE(q && packed, SQX_E_ARG, "sqx_int4_pack: null pointer");
+  const int64_t nb = (n + 1) / 2;
+  hipLaunchKernelGGL(int4_pack_kernel, dim3(static_cast<unsigned>(ceil_div(nb, 256))), dim3(256), 0,
+                     as_stream(stream), q, n, packed);
+  SQX_LAUNCH_CHECK("sqx_int4_pack");
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_unpack(const uint8_t* packed, int64_t n, int8_t* q, sqx_stream_t stream) {
+  SQX_REQUIRE(n >= 0, SQX_E_ARG, "sqx_int4_unpack: negative length");
+  if (n == 0) return SQX_OK;
+  SQX_REQUIRE(q && packed, SQX_E_ARG, "sqx_int4_unpack: null pointer");
+  const int64_t nb = (n + 1) / 2;
+  hipLaunchKernelGGL(int4_unpack_kernel, dim3(static_cast<unsigned>(ceil_div(nb, 256))), dim3(256), 0,
+                     as_stream(stream), packed, n, q);
+  SQX_LAUNCH_CHECK("sqx_int4_unpack");
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_dequantize(const int8_t* q, const float* scales, int64_t rows, int64_t cols,
+                                   int64_t group, float* out, sqx_stream_t stream) {
+  SQX_REQUIRE(rows >= 0 && cols >= 0 && group > 0 && cols % group == 0, SQX_E_ARG,
+              "sqx_int4_dequantize: bad shape [%lld, %lld] / group %lld", (long long)rows, (long long)cols,
+              (long long)group);
+  const int64_t n = rows * cols;
+  if (n == 0) return SQX_OK;
+  SQX_REQUIRE(q && scales && out, SQX_E_ARG, "sqx_int4_dequantize: null pointer");
+  hipLaunchKernelGGL(int4_dequantize_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0,
+                     as_stream(stream), q, scales, n, group, out);
+  SQX_LAUNCH_CHECK("sqx_int4_dequantize");
+  return SQX_OK;
+}
+
+extern "C" int64_t sqx_int4_tiled_weight_bytes(int64_t rows, int64_t cols) {
+  if (rows < 0 || cols < 0) return -1;
+  return ceil_div(rows, 16) * ceil_div(cols, 128) * 1024;
+}
+
+extern "C" int64_t sqx_int4_tiled_param_count(int64_t rows, int64_t cols, int64_t group) {
+  if (rows < 0 || cols < 0 || !(group == 32 || group == 64 || group == 128)) return -1;
+  return ceil_div(rows, 16) * ceil_div(cols, 128) * (128 / group) * 16;
+}
+
+static int tile_params(const void* src, int param_dtype, int64_t rows, int64_t cols, int64_t group, void* dst,
+                       hipStream_t s) {
+  const int64_t Gp = ceil_div(cols, 128) * (128 / group);
+  const int64_t n_out = ceil_div(rows, 16) * Gp * 16;
+  const dim3 grid(static_cast<unsigned>(ceil_div(n_out, 256)));
+  if (param_dtype == SQX_DTYPE_F32)
+    hipLaunchKernelGGL(int4_tile_params_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(src), rows,
+                       cols / group, Gp, n_out, static_cast<float*>(dst));
+  else
+    hipLaunchKernelGGL(int4_tile_params_kernel<uint16_t>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(src),
+                       rows, cols / group, Gp, n_out, static_cast<uint16_t*>(dst));
+  return SQX_OK;
+}
+
+static int check_tile_args(int64_t rows, int64_t cols, int64_t group, int param_dtype) {
+  SQX_REQUIRE(rows > 0 && cols > 0, SQX_E_ARG, "sqx_int4_tile: empty weight [%lld, %lld]", (long long)rows,
+              (long long)cols);
+  SQX_REQUIRE(group == 32 || group == 64 || group == 128, SQX_E_ARG,
+              "sqx_int4_tile: group_size %lld unsupported by the tiled kernels (32, 64 or 128)", (long long)group);
+  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld", (long long)cols,
+              (long long)group);
+  SQX_REQUIRE(param_dtype == SQX_DTYPE_F32 || param_dtype == SQX_DTYPE_BF16, SQX_E_ARG,
+              "sqx_int4_tile: param_dtype must be F32 or BF16");
+  SQX_REQUIRE(rows <= (int64_t)1 << 30 && cols <= (int64_t)1 << 30, SQX_E_ARG, "sqx_int4_tile: shape too large");
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_tile(const int8_t* codes, int code_kind, const void* scales, const void* zeros,
+                             int param_dtype, int64_t rows, int64_t cols, int64_t group, uint8_t* wt, void* st,
+                             void* zt, sqx_stream_t stream) {
+  int rc = check_tile_args(rows, cols, group, param_dtype);
+  if (rc) return rc;
+  SQX_REQUIRE(code_kind == 0 || code_kind == 1, SQX_E_ARG, "sqx_int4_tile: code_kind must be 0 or 1");
+  SQX_REQUIRE(codes && scales && wt && st, SQX_E_ARG, "sqx_int4_tile: null pointer");
+  SQX_REQUIRE(code_kind == 0 || (zeros && zt), SQX_E_ARG, "sqx_int4_tile: asymmetric codes need zeros and zt");
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0, SQX_E_ARG, "sqx_int4_tile: wt must be 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  const int64_t KB = ceil_div(cols, 128);
+  const int64_t n_dwords = ceil_div(rows, 16) * KB * 256;
+  const dim3 grid(static_cast<unsigned>(ceil_div(n_dwords, 256)));
+  if (code_kind == 0)
+    hipLaunchKernelGGL((int4_tile_weights_kernel<false, true>), grid, dim3(256), 0, s, codes, rows, cols, KB,
+                       n_dwords, reinterpret_cast<uint32_t*>(wt));
+  else
+    hipLaunchKernelGGL((int4_tile_weights_kernel<false, false>), grid, dim3(256), 0, s, codes, rows, cols, KB,
+                       n_dwords, reinterpret_cast<uint32_t*>(wt));
+  tile_params(scales, param_dtype, rows, cols, group, st, s);
+  if (code_kind == 1) tile_params(zeros, param_dtype, rows, cols, group, zt, s);
+  SQX_LAUNCH_CHECK("sqx_int4_tile");
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_tile_packed(const uint8_t* packed, const void* scales, int param_dtype, int64_t rows,
+                                    int64_t cols, int64_t group, uint8_t* wt, void* st, sqx_stream_t stream) {
+  int rc = check_tile_args(rows, cols, group, param_dtype);
+  if (rc) return rc;
+  SQX_REQUIRE(packed && scales && wt && st, SQX_E_ARG, "sqx_int4_tile_packed: null pointer");
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0, SQX_E_ARG, "sqx_int4_tile_packed: wt must be 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  const int64_t KB = ceil_div(cols, 128);
+  const int64_t n_dwords = ceil_div(rows, 16) * KB * 256;
+  hipLaunchKernelGGL((int4_tile_weights_kernel<true, true>), dim3(static_cast<unsigned>(ceil_div(n_dwords, 256))),
+                     dim3(256), 0, s, packed, rows, cols, KB, n_dwords, reinterpret_cast<uint32_t*>(wt));
+  tile_params(scales, param_dtype, rows, cols, group, st, s);
+  SQX_LAUNCH_CHECK("sqx_int4_tile_packed");
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_linear_default_splits(int64_t m, int64_t rows, int64_t cols) {
+  if (m <= 0 || rows <= 0 || cols <= 0) return 1;
+  const int64_t T = ceil_div(rows, 16);
+  const int64_t KB = ceil_div(cols, 128);
+  // Aim for ~2048 waves (8 per CU on 256 CUs) while keeping >= 2 k-blocks per wave.
+  int64_t s = 2048 / T;
+  if (s < 1) s = 1;
+  int64_t cap = KB / 2;
+  if (cap < 1) cap = 1;
+  if (s > cap) s = cap;
+  if (s > 64) s = 64;
+  return static_cast<int>(s);
+}
+
+extern "C" int64_t sqx_int4_linear_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int splits) {
+  if (m <= 0 || rows <= 0 || cols <= 0) return -1;
+  if (splits <= 0) splits = sqx_int4_linear_default_splits(m, rows, cols);
+  const int64_t KB = ceil_div(cols, 128);
+  if (splits > KB) splits = static_cast<int>(KB);
+  if (splits <= 1) return 0;
+  const int64_t T = ceil_div(rows, 16);
+  const int mch = linear_mch(m);
+  return align256(4 * T) + T * splits * (16 * mch * 16) * 4;
+}
+
+extern "C" int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
+                               int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
+                               int64_t group, int splits, void* workspace, int64_t workspace_bytes,
+                               sqx_stream_t stream) {
+  SQX_REQUIRE(m >= 0 && rows > 0 && cols > 0, SQX_E_ARG, "sqx_int4_linear: bad shape m=%lld rows=%lld cols=%lld",
+              (long long)m, (long long)rows, (long long)cols);
+  SQX_REQUIRE(group == 32 || group == 64 || group == 128, SQX_E_ARG,
+              "sqx_int4_linear: group_size %lld unsupported (32, 64 or 128)", (long long)group);
+  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld", (long long)cols,
+              (long long)group);
+  SQX_REQUIRE(act_dtype == SQX_DTYPE_BF16 || act_dtype == SQX_DTYPE_F16, SQX_E_ARG,
+              "sqx_int4_linear: activations must be BF16 or F16");
+  SQX_REQUIRE(param_dtype == SQX_DTYPE_F32 || param_dtype == SQX_DTYPE_BF16, SQX_E_ARG,
+              "sqx_int4_linear: param_dtype must be F32 or BF16");
+  SQX_REQUIRE(rows < ((int64_t)1 << 31) && cols < ((int64_t)1 << 31) && m < ((int64_t)1 << 31), SQX_E_ARG,
+              "sqx_int4_linear: shape too large");
+  if (m == 0) return SQX_OK;
+  SQX_REQUIRE(wt && st && x && y, SQX_E_ARG, "sqx_int4_linear: null pointer");
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, SQX_E_ARG,
+              "sqx_int4_linear: wt and x must be 16-byte aligned");
+  const bool asym = zt != nullptr;
+  const int64_t T = ceil_div(rows, 16);
+  const int64_t KB = ceil_div(cols, 128);
+  if (splits <= 0) splits = sqx_int4_linear_default_splits(m, rows, cols);
+  if (splits > KB) splits = static_cast<int>(KB);
+  const int kb_per = static_cast<int>(ceil_div(KB, splits));
+  splits = static_cast<int>(ceil_div(KB, kb_per));  // no empty splits
+  float* part = nullptr;
+  int* cnt = nullptr;
+  if (splits > 1) {
+    const int64_t need = sqx_int4_linear_workspace_bytes(m, rows, cols, splits);
+    SQX_REQUIRE(workspace && workspace_bytes >= need, SQX_E_SPACE,
+                "sqx_int4_linear: workspace of %lld bytes needed, %lld given", (long long)need,
+                (long long)workspace_bytes);
+    SQX_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, SQX_E_ARG,
+                "sqx_int4_linear: workspace must be 256-byte aligned");
+    cnt = static_cast<int*>(workspace);
+    part = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(4 * T));
+  }
+  hipStream_t s = as_stream(stream);
+  const dim3 grid(static_cast<unsigned>(ceil_div(T, 4)), static_cast<unsigned>(splits));
+  const u32x4_t* w4 = reinterpret_cast<const u32x4_t*>(wt);
+  const uint16_t* b16 = static_cast<const uint16_t*>(bias);
+  const int pbf = param_dtype == SQX_DTYPE_BF16;
+  // x is processed in passes of up to 64 rows (4 MFMA row chunks per wave).
+  for (int64_t m0 = 0; m0 < m; m0 += 64) {
+    const int mm = static_cast<int>(m - m0 < 64 ? m - m0 : 64);
+    const int mch = linear_mch(mm);
+    const uint16_t* xp = static_cast<const uint16_t*>(x) + m0 * cols;
+    uint16_t* yp = static_cast<uint16_t*>(y) + m0 * rows;
+    const int M = mm, N = static_cast<int>(rows), K = static_cast<int>(cols);
+    const int iT = static_cast<int>(T), iKB = static_cast<int>(KB);
+    const int g = static_cast<int>(group);
+#define SQX_LIN(ACT, ASYM, PBF)                                                                                    \
+  launch_linear_a<ACT, ASYM, PBF>(g, mch, grid, s, w4, st, zt, xp, yp, b16, part, cnt, M, N, K, iT, iKB, splits, \
+                                  kb_per)
+    if (act_dtype == SQX_DTYPE_BF16) {
+      if (asym) { if (pbf) SQX_LIN(ActBF16, true, true); else SQX_LIN(ActBF16, true, false); }
+      else { if (pbf) SQX_LIN(ActBF16, false, true); else SQX_LIN(ActBF16, false, false); }
+    } else {
+      if (asym) { if (pbf) SQX_LIN(ActF16, true, true); else SQX_LIN(ActF16, true, false); }
+      else { if (pbf) SQX_LIN(ActF16, false, true); else SQX_LIN(ActF16, false, false); }
+    }
+#undef SQX_LIN
+    SQX_LAUNCH_CHECK("sqx_int4_linear");
+  }
+  return SQX_OK;
+}

@@ -1,0 +1,302 @@
+"""Group-wise INT4 weights on MI355X — the API of ``scratch_llm.quant.int4_group``.
+
+Same names, signatures, defaults, return types and ``ValueError`` messages as
+``src/scratch_llm/quant/int4_group.py`` (cited per function), computed by the HIP kernels in
+``libsqx_hip.so`` on ROCm device tensors. CPU tensors raise ``RuntimeError``: this module has no
+host path.
+
+Format (reference): signed codes in ``[-8, 7]``; ``scale = max(absmax(group) / 7, FLT_MIN)`` per
+group of ``group_size`` consecutive input columns, fp32; packing puts the first element of a pair in
+the high nibble. The linear itself runs on a tiled copy of the codes (:class:`Int4Tiled`), built
+once per weight and cached for the functional entry point :func:`w4a16_linear`.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor
+
+from scratch_llm_amd import _lib
+from scratch_llm_amd.quant import _device
+
+__all__ = [
+    "GROUP_SIZE",
+    "INT4_QMAX",
+    "INT4_QMIN",
+    "Int4Tiled",
+    "dequantize_groupwise_int4",
+    "int4_linear_tiled",
+    "mse",
+    "pack_int4",
+    "quantize_groupwise_int4",
+    "sqnr_db",
+    "tile_int4",
+    "tile_int4_packed",
+    "unpack_int4",
+    "w4a16_linear",
+]
+
+GROUP_SIZE = 128
+INT4_QMIN = -8
+INT4_QMAX = 7
+
+# Group sizes the tiled linear kernels take (a group never straddles a 32-column MFMA step).
+TILED_GROUPS = (32, 64, 128)
+
+
+# --------------------------------------------------------------------------- #
+# Bit-exact nibble packing (int4_group.py:62-102)                              #
+# --------------------------------------------------------------------------- #
+def pack_int4(q: Tensor) -> Tensor:
+    """Pack a 1-D signed 4-bit tensor into ``uint8``, two nibbles per byte (int4_group.py:62-82).
+
+    The first element of each pair goes to the high nibble; an odd length gets a zero low nibble in
+    the last byte. Returns ``uint8`` of length ``ceil(len(q) / 2)`` on ``q``'s device.
+    """
+    if q.dim() != 1:
+        raise ValueError(f"pack_int4 expects a 1-D tensor, got shape {tuple(q.shape)}")
+    dev = _lib.require_device(q, fn="pack_int4")
+    n = q.numel()
+    q8 = q.to(torch.int8).contiguous()  # keeps the low 4 bits of any integer code
+    out = torch.empty((n + 1) // 2, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().sqx_int4_pack(_lib.ptr(q8), n, _lib.ptr(out), _lib.stream_ptr(dev)), "pack_int4")
+    return out
+
+
+def unpack_int4(packed: Tensor, n: int) -> Tensor:
+    """Inverse of :func:`pack_int4` (int4_group.py:85-102): high nibble first, sign-extended,
+    the first ``n`` values as ``int8``."""
+    if packed.dim() != 1:
+        raise ValueError(f"unpack_int4 expects a 1-D tensor, got shape {tuple(packed.shape)}")
+    dev = _lib.require_device(packed, fn="unpack_int4")
+    n = int(min(n, 2 * packed.numel()))
+    p8 = packed.to(torch.uint8).contiguous()
+    out = torch.empty(max(n, 0), dtype=torch.int8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().sqx_int4_unpack(_lib.ptr(p8), max(n, 0), _lib.ptr(out), _lib.stream_ptr(dev)),
+                   "unpack_int4")
+    return out
+
+
+# --------------------------------------------------------------------------- #
+# Group-wise symmetric INT4 quantizer (int4_group.py:108-142)                 #
+# --------------------------------------------------------------------------- #
+def quantize_groupwise_int4(w: Tensor, group_size: int = GROUP_SIZE) -> tuple[Tensor, Tensor]:
+    """Symmetric group-wise INT4 quantization of a 2-D weight ``[out, in]`` (int4_group.py:108-129).
+
+    Returns ``(q, scales)``: ``int8`` codes in ``[-8, 7]`` shaped like ``w`` and fp32 scales
+    ``[out, in // group_size]``, bit-identical to the reference on the same input.
+    """
+    if w.dim() != 2:
+        raise ValueError(f"expected a 2-D weight, got shape {tuple(w.shape)}")
+    out_features, in_features = w.shape
+    if in_features % group_size != 0:
+        raise ValueError(f"in_features={in_features} not divisible by group_size={group_size}")
+    dev = _lib.require_device(w, fn="quantize_groupwise_int4")
+    if w.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        w = w.to(torch.float32)
+    w = w.contiguous()
+    q = torch.empty(out_features, in_features, dtype=torch.int8, device=dev)
+    scales = torch.empty(out_features, in_features // group_size, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.load().sqx_int4_quantize_sym(
+            _lib.ptr(w), _lib.sqx_dtype(w.dtype), out_features, in_features, group_size, _lib.ptr(q),
+            _lib.ptr(scales), _lib.stream_ptr(dev),
+        )
+    _lib.check(rc, "quantize_groupwise_int4")
+    return q, scales
+
+
+def dequantize_groupwise_int4(q: Tensor, scales: Tensor, group_size: int = GROUP_SIZE) -> Tensor:
+    """fp32 weights ``q * scale`` from INT4 codes and per-group scales (int4_group.py:132-142)."""
+    out_features, in_features = q.shape
+    dev = _lib.require_device(q, scales, fn="dequantize_groupwise_int4")
+    q8 = q.to(torch.int8).contiguous()
+    s32 = scales.to(torch.float32).contiguous()
+    if s32.numel() != out_features * (in_features // group_size):
+        raise ValueError(
+            f"scales has {s32.numel()} elements, expected {out_features}x{in_features // group_size}"
+        )
+    out = torch.empty(out_features, in_features, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.load().sqx_int4_dequantize(
+            _lib.ptr(q8), _lib.ptr(s32), out_features, in_features, group_size, _lib.ptr(out), _lib.stream_ptr(dev)
+        )
+    _lib.check(rc, "dequantize_groupwise_int4")
+    return out
+
+
+# --------------------------------------------------------------------------- #
+# Tiled weights: the layout the linear kernels stream                          #
+# --------------------------------------------------------------------------- #
+@dataclass(frozen=True)
+class Int4Tiled:
+    """INT4 codes re-laid for the MI355X linear kernels.
+
+    ``wt``: uint8, 1 KiB per (16-row tile, 128-column block); ``st``/``zt``: per-group scale and
+    zero (``zt`` is None for symmetric codes) as ``[tiles][groups][16]``. ``rows``/``cols`` are the
+    logical weight shape ``[out, in]``.
+    """
+
+    wt: Tensor
+    st: Tensor
+    zt: Tensor | None
+    rows: int
+    cols: int
+    group_size: int
+
+    @property
+    def device(self) -> torch.device:
+        return self.wt.device
+
+    @property
+    def nbytes(self) -> int:
+        return self.wt.numel() + self.st.numel() * self.st.element_size() + (
+            0 if self.zt is None else self.zt.numel() * self.zt.element_size()
+        )
+
+
+def _check_tiled_group(group_size: int) -> None:
+    if group_size not in TILED_GROUPS:
+        raise ValueError(f"group_size={group_size} is not supported by the tiled kernels {TILED_GROUPS}")
+
+
+def tile_int4(
+    q: Tensor, scales: Tensor, zeros: Tensor | None = None, group_size: int = GROUP_SIZE
+) -> Int4Tiled:
+    """Re-lay INT4 codes ``[out, in]`` and their group parameters for the linear kernels.
+
+    Symmetric codes (``zeros is None``) are the reference's ``[-8, 7]`` codes with fp32 scales;
+    asymmetric codes are unsigned ``[0, 15]`` with per-group ``scales`` and ``zeros`` (fp32 or bf16).
+    """
+    if q.dim() != 2:
+        raise ValueError(f"expected 2-D codes, got shape {tuple(q.shape)}")
+    rows, cols = q.shape
+    if cols % group_size != 0:
+        raise ValueError(f"in_features={cols} not divisible by group_size={group_size}")
+    _check_tiled_group(group_size)
+    dev = _lib.require_device(q, scales, zeros, fn="tile_int4")
+    pdt = torch.float32 if zeros is None else scales.dtype
+    if pdt not in (torch.float32, torch.bfloat16):
+        pdt = torch.float32
+    s = scales.to(pdt).contiguous()
+    z = None if zeros is None else zeros.to(pdt).contiguous()
+    lib = _lib.load()
+    wt = torch.empty(lib.sqx_int4_tiled_weight_bytes(rows, cols), dtype=torch.uint8, device=dev)
+    npar = lib.sqx_int4_tiled_param_count(rows, cols, group_size)
+    st = torch.empty(npar, dtype=pdt, device=dev)
+    zt = None if z is None else torch.empty(npar, dtype=pdt, device=dev)
+    q8 = q.to(torch.int8).contiguous()
+    with torch.cuda.device(dev):
+        rc = lib.sqx_int4_tile(
+            _lib.ptr(q8), 0 if z is None else 1, _lib.ptr(s), _lib.ptr(z), _lib.sqx_dtype(pdt), rows, cols,
+            group_size, _lib.ptr(wt), _lib.ptr(st), _lib.ptr(zt), _lib.stream_ptr(dev),
+        )
+    _lib.check(rc, "tile_int4")
+    return Int4Tiled(wt, st, zt, rows, cols, group_size)
+
+
+def tile_int4_packed(packed: Tensor, scales: Tensor, shape: tuple[int, int], group_size: int = GROUP_SIZE) -> Int4Tiled:
+    """Re-lay the reference's packed byte stream (``pack_int4(q.reshape(-1))`` of symmetric codes of
+    ``shape = (out, in)``) for the linear kernels, without unpacking it first."""
+    rows, cols = shape
+    if cols % group_size != 0:
+        raise ValueError(f"in_features={cols} not divisible by group_size={group_size}")
+    _check_tiled_group(group_size)
+    if packed.numel() != (rows * cols + 1) // 2:
+        raise ValueError(f"packed has {packed.numel()} bytes, expected {(rows * cols + 1) // 2} for {shape}")
+    dev = _lib.require_device(packed, scales, fn="tile_int4_packed")
+    lib = _lib.load()
+    p8 = packed.to(torch.uint8).contiguous()
+    s = scales.to(torch.float32).contiguous()
+    wt = torch.empty(lib.sqx_int4_tiled_weight_bytes(rows, cols), dtype=torch.uint8, device=dev)
+    st = torch.empty(lib.sqx_int4_tiled_param_count(rows, cols, group_size), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.sqx_int4_tile_packed(
+            _lib.ptr(p8), _lib.ptr(s), _lib.DTYPE_F32, rows, cols, group_size, _lib.ptr(wt), _lib.ptr(st),
+            _lib.stream_ptr(dev),
+        )
+    _lib.check(rc, "tile_int4_packed")
+    return Int4Tiled(wt, st, None, rows, cols, group_size)
+
+
+def int4_linear_tiled(x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, splits: int | None = None) -> Tensor:
+    """``x @ W.T (+ bias)`` for a tiled INT4 weight ``W [out, in]``; ``x`` is ``[..., in]`` in bf16 or
+    fp16 and the result has ``x``'s dtype and shape ``[..., out]``. fp32 accumulation."""
+    *batch, k = x.shape
+    if k != tw.cols:
+        raise ValueError(f"x has in_features={k}, weight expects {tw.cols}")
+    dev = _lib.require_device(x, tw.wt, bias, fn="int4_linear_tiled")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"int4_linear_tiled takes bf16 or fp16 activations, got {x.dtype}")
+    x2 = x.reshape(-1, k)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    y = torch.empty(m, tw.rows, dtype=x.dtype, device=dev)
+    b = None if bias is None else bias.to(x.dtype).contiguous()
+    lib = _lib.load()
+    sp = 0 if splits is None else int(splits)
+    with torch.cuda.device(dev):
+        need = lib.sqx_int4_linear_workspace_bytes(max(m, 1), tw.rows, tw.cols, sp)
+        ws = _device.workspace(dev, need)
+        rc = lib.sqx_int4_linear(
+            _lib.ptr(tw.wt), _lib.ptr(tw.st), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype), _lib.ptr(x2),
+            _lib.sqx_dtype(x.dtype), _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size, sp,
+            _lib.ptr(ws), 0 if ws is None else ws.numel() * 4, _lib.stream_ptr(dev),
+        )
+    _lib.check(rc, "int4_linear_tiled")
+    return y.reshape(*batch, tw.rows)
+
+
+_tiled_cache = _device.TensorKeyedCache()
+
+
+# --------------------------------------------------------------------------- #
+# W4A16 linear (int4_group.py:148-164)                                         #
+# --------------------------------------------------------------------------- #
+def w4a16_linear(
+    x: Tensor,
+    q: Tensor,
+    scales: Tensor,
+    bias: Tensor | None = None,
+    group_size: int = GROUP_SIZE,
+) -> Tensor:
+    """W4A16 linear (int4_group.py:148-164): ``x [..., in]`` times INT4 weights ``q/scales``
+    describing ``[out, in]``; returns ``[..., out]`` in ``x``'s dtype.
+
+    bf16/fp16 activations with ``group_size`` in (32, 64, 128) run the fused dequant kernel on a
+    tiled copy of ``q`` that is built on first use and cached until ``q`` or ``scales`` changes.
+    Other cases dequantize on the GPU (fp32, exactly as the reference) and call the library GEMM.
+    """
+    dev = _lib.require_device(x, q, scales, bias, fn="w4a16_linear")
+    if x.dtype in (torch.bfloat16, torch.float16) and group_size in TILED_GROUPS:
+        if q.shape[1] % group_size != 0:
+            raise ValueError(f"in_features={q.shape[1]} not divisible by group_size={group_size}")
+        tw = _tiled_cache.get((q, scales), (group_size,), lambda: tile_int4(q, scales, None, group_size))
+        return int4_linear_tiled(x, tw, bias)
+    wdeq = dequantize_groupwise_int4(q, scales, group_size).to(x.dtype)
+    del dev
+    return torch.nn.functional.linear(x, wdeq, bias)
+
+
+# --------------------------------------------------------------------------- #
+# Error metrics (int4_group.py:170-183)                                        #
+# --------------------------------------------------------------------------- #
+def sqnr_db(ref: Tensor, approx: Tensor) -> float:
+    """Signal-to-quantization-noise ratio in dB: ``10*log10(P_signal/P_noise)`` (float64)."""
+    ref = ref.to(torch.float64)
+    approx = approx.to(torch.float64)
+    signal = ref.pow(2).sum()
+    noise = (ref - approx).pow(2).sum()
+    if noise.item() == 0.0:
+        return float("inf")
+    return float(10.0 * torch.log10(signal / noise).item())
+
+
+def mse(ref: Tensor, approx: Tensor) -> float:
+    """Mean squared error between two tensors (float64 accumulation)."""
+    return float((ref.to(torch.float64) - approx.to(torch.float64)).pow(2).mean().item())
