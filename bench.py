@@ -1,20 +1,25 @@
 #!/usr/bin/env python3
-"""W4A16 decode-GEMV benchmark on one MI355X (BASELINE.json metric, config 2 shapes).
+"""W4A16 decode-GEMV benchmark on one MI355X (BASELINE.json metric; config 2 shapes, config 5 layout).
 
-Workload ("step"): every quantized linear of one Llama-3-8B decode step at batch M (default 1) —
-32 layers x {q 4096->4096, k 4096->1024, v 4096->1024, o 4096->4096, gate 4096->14336,
-up 4096->14336, down 14336->4096} plus the int4 lm_head 4096->128256 — each an int4-g128 symmetric
-(reference format) weight, bf16 activations, through libsqx_hip.so's sqx_int4_linear. Weights are
-random N(0, 0.02) quantized on the GPU; 3.99 GB of distinct int4 weights per step keeps the 256 MB
-Infinity Cache from serving them. The step is captured once in a HIP graph and replayed.
+Step: every quantized linear of one Llama-3-8B decode step at batch M (default 1), laid out as a
+serving engine holds them: per layer a fused QKV projection 4096->6144 (q 4096 + k 1024 + v 1024
+rows), o 4096->4096, a fused gate/up projection 4096->28672 and down 14336->4096; 32 layers plus
+the lm_head 4096->128256. Every weight is int4 group-128 in the reference's symmetric format
+(codes in [-8, 7], fp32 scale per group), random N(0, 0.02) quantized on the GPU, bf16
+activations, through libsqx_hip.so's sqx_int4_linear. The step's 3.99 GB of distinct weights is
+15x the 256 MB Infinity Cache, so every step streams from HBM. The step is captured once in a HIP
+graph and replayed; `--layout unfused` times the seven separate projections per layer instead.
 
-value = algorithmic HBM bytes per step / time per step, where a linear's bytes are
+value = algorithmic HBM bytes per step / time per step; a linear's bytes are
 N*K/2 (codes) + 4*N*K/128 (fp32 scales) + 2*M*K (x) + 2*M*N (y).
 
-roofline: the dominant kernel (the int4 linear instance, the only kernel in the step), with its
-average launch duration measured by HIP events around each launch of an eager pass.
+per_shape: each Llama-3-8B linear shape timed on its own (HIP events around a graph of back-to-back
+launches on the launch stream), rotating over >= 1 GB of distinct weight tiles (views into the
+step's tiled weights: any 16-row-tile window of a tiled weight is a tiled weight).
+roofline: the dominant kernel of the step, the int4 linear launch that takes the largest share of
+the step (the fused gate/up projection), timed the same way.
 cpu_baseline: the reference's CPU path (torch dequantize + F.linear per call, restated in
-oracle/torch_path.py) timed on this host's cores over a bounded sample of the same workload.
+oracle/torch_path.py) over layer 0's seven projections, on this host's cores, for a bounded time.
 """
 
 from __future__ import annotations
@@ -32,17 +37,13 @@ if ROOT not in sys.path:
 
 METRIC = "W4A16 GEMV HBM GB/s (% peak) at Llama-3-8B shapes; decode tok/s at B=1"
 HBM_PEAK_GBS = 8000.0
-LAYER_SHAPES = [  # (name, N = out_features, K = in_features)
-    ("q", 4096, 4096),
-    ("k", 1024, 4096),
-    ("v", 1024, 4096),
-    ("o", 4096, 4096),
-    ("gate", 14336, 4096),
-    ("up", 14336, 4096),
-    ("down", 4096, 14336),
-]
-LM_HEAD = ("lm_head", 128256, 4096)
 GROUP = 128
+D_MODEL, D_FF, VOCAB = 4096, 14336, 128256
+# Llama-3-8B projections (name, N = out_features, K = in_features)
+UNFUSED = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+           ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+FUSED = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
+LM_HEAD = ("lm_head", VOCAB, D_MODEL)
 
 
 def algo_bytes(m: int, n: int, k: int) -> int:
@@ -70,10 +71,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--m", type=int, default=1, help="activation rows (decode batch)")
     ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--layout", choices=("fused", "unfused"), default="fused")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--eager-passes", type=int, default=3, help="event-timed eager passes for the roofline")
-    ap.add_argument("--splits", type=int, default=0, help="split-K override (0 = library default)")
+    ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape timing")
+    ap.add_argument("--kslices", type=int, default=0, help="waves per 16-row tile (0 = library default)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -99,66 +101,78 @@ def main() -> int:
     # ------------------------------------------------------------------ weights (quantized on GPU)
     t_setup = time.perf_counter()
     gen = torch.Generator(device=dev)
+    seed = 1000
+
+    def make(n: int, k: int):
+        nonlocal seed
+        gen.manual_seed(seed)
+        seed += 1
+        w = (torch.randn(n, k, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        qc, sc = q4.quantize_groupwise_int4(w)
+        del w
+        return qc, sc
+
+    shapes = FUSED if args.layout == "fused" else UNFUSED
     linears = []  # (name, N, K, Int4Tiled)
-    cpu_sample = []  # layer 0's reference-format codes/scales for the CPU baseline
+    cpu_sample = []  # layer 0's seven projections in the reference format, for the CPU baseline
     for layer in range(args.layers):
-        for name, n, k in LAYER_SHAPES:
-            gen.manual_seed(1000 + 7 * layer + len(linears) % 7)
-            w = (torch.randn(n, k, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
-            qc, sc = q4.quantize_groupwise_int4(w)
-            del w
+        for name, n, k in shapes:
+            qc, sc = make(n, k)
             linears.append((name, n, k, q4.tile_int4(qc, sc)))
             if layer == 0 and not args.no_cpu:
-                cpu_sample.append((name, n, k, qc.cpu(), sc.cpu()))
+                if args.layout == "fused":  # the fused rows are the seven projections stacked
+                    parts = {"qkv": (("q", 4096), ("k", 1024), ("v", 1024)), "gate_up": (("gate", 14336), ("up", 14336))}
+                    r0 = 0
+                    for pn, pr in parts.get(name, ((name, n),)):
+                        cpu_sample.append((pn, pr, k, qc[r0:r0 + pr].cpu(), sc[r0:r0 + pr].cpu()))
+                        r0 += pr
+                else:
+                    cpu_sample.append((name, n, k, qc.cpu(), sc.cpu()))
             del qc, sc
-    name, n, k = LM_HEAD
-    gen.manual_seed(999)
-    w = (torch.randn(n, k, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
-    qc, sc = q4.quantize_groupwise_int4(w)
-    del w
-    linears.append((name, n, k, q4.tile_int4(qc, sc)))
+    qc, sc = make(LM_HEAD[1], LM_HEAD[2])
+    linears.append((LM_HEAD[0], LM_HEAD[1], LM_HEAD[2], q4.tile_int4(qc, sc)))
     del qc, sc
     torch.cuda.synchronize()
-    log(f"setup: {len(linears)} int4 linears in {time.perf_counter() - t_setup:.1f}s")
+    log(f"setup: {len(linears)} int4 linears ({args.layout}) in {time.perf_counter() - t_setup:.1f}s")
 
     gen.manual_seed(2001)
-    xs = {kk: torch.randn(m, kk, device=dev, generator=gen).to(torch.bfloat16) for kk in (4096, 14336)}
+    xs = {kk: torch.randn(m, kk, device=dev, generator=gen).to(torch.bfloat16) for kk in (D_MODEL, D_FF)}
     ys = {}
-    for _, n, _, _ in linears:
+    for n in [n for _, n, _, _ in linears] + [n for _, n, _ in UNFUSED + FUSED]:
         ys.setdefault(n, torch.empty(m, n, device=dev, dtype=torch.bfloat16))
-    ws_need = max(lib.sqx_int4_linear_workspace_bytes(m, n, k, args.splits) for _, n, k, _ in linears)
-    ws = torch.zeros(max(ws_need, 256) // 4 + 64, device=dev, dtype=torch.int32)
-    ws_bytes = ws.numel() * 4
-
-    def launch_args(tw, n, k, stream_ptr):
-        return (
-            tw.wt.data_ptr(), tw.st.data_ptr(), None, _lib.DTYPE_F32, xs[k].data_ptr(), _lib.DTYPE_BF16,
-            ys[n].data_ptr(), None, m, n, k, GROUP, args.splits, ws.data_ptr(), ws_bytes, stream_ptr,
-        )
-
     fn = lib.sqx_int4_linear
+
+    def launch(wt_ptr, st_ptr, n, k, stream_ptr):
+        return fn(wt_ptr, st_ptr, None, _lib.DTYPE_F32, xs[k].data_ptr(), _lib.DTYPE_BF16, ys[n].data_ptr(), None,
+                  m, n, k, GROUP, args.kslices, stream_ptr)
 
     def run_step(stream_ptr: int, check: bool = False) -> None:
         for _, n, k, tw in linears:
-            rc = fn(*launch_args(tw, n, k, stream_ptr))
+            rc = launch(tw.wt.data_ptr(), tw.st.data_ptr(), n, k, stream_ptr)
             if check:
                 _lib.check(rc, "sqx_int4_linear")
 
     step_bytes = sum(algo_bytes(m, n, k) for _, n, k, _ in linears)
-    cur = torch.cuda.current_stream().cuda_stream
-    run_step(cur, check=True)
+    run_step(torch.cuda.current_stream().cuda_stream, check=True)
     torch.cuda.synchronize()
-    y_eager = {n: t.clone() for n, t in ys.items()}
+    written = {n for _, n, _, _ in linears}
+    y_eager = {n: ys[n].clone() for n in written}
 
     # ------------------------------------------------------------------ graph capture of one step
+    cap = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        run_step(torch.cuda.current_stream().cuda_stream)
+    with torch.cuda.graph(graph, stream=cap):
+        run_step(cap.cuda_stream)
     for t in ys.values():
         t.zero_()
-    graph.replay()
-    torch.cuda.synchronize()
-    graph_ok = all(torch.equal(ys[n], y_eager[n]) for n in ys)
+    graph_ok = True
+    for _ in range(3):  # replays with eager work and synchronisations between them
+        graph.replay()
+        torch.cuda.synchronize()
+        graph_ok &= all(torch.equal(ys[n], y_eager[n]) for n in written)
+        for t in ys.values():
+            t.zero_()
+        torch.cuda.synchronize()
     if not graph_ok:
         log("WARNING: graph replay differs from the eager step")
 
@@ -178,46 +192,58 @@ def main() -> int:
     value_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"graph step: {ms_per_step * 1e3:.1f} us, {value_gbs:.0f} GB/s, wall {wall:.3f}s")
 
-    # ------------------------------------------------------------------ per-launch events (roofline)
-    per = {}
-    tot_ms = 0.0
-    tot_bytes = 0
-    n_launch = 0
-    for _ in range(args.eager_passes):
-        pairs = []
-        try:
-            torch.cuda._sleep(200_000_000)  # keep the GPU busy while the pass is enqueued
-        except Exception:  # pragma: no cover - spin kernel unavailable
-            pass
-        for name, n, k, tw in linears:
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            fn(*launch_args(tw, n, k, cur))
-            b.record()
-            pairs.append((name, n, k, a, b))
+    # ------------------------------------------------------------------ per-shape kernel timing
+    def shape_time(n: int, k: int, reps: int = 3):
+        """us per launch of an (n, k) linear, over windows of the step's tiled weights with matching k."""
+        kb = -(-k // 128)
+        tiles = -(-n // 16)
+        tile_b, tile_p = kb * 1024, kb * 16
+        pool = []
+        for _, pn, pk, tw in linears:
+            if pk != k:
+                continue
+            for t0 in range(0, -(-pn // 16) - tiles + 1, tiles):
+                pool.append((tw.wt[t0 * tile_b:].data_ptr(), tw.st[t0 * tile_p:].data_ptr()))
+        need = max(8, min(len(pool), -(-(1 << 30) // (tiles * tile_b))))
+        step = max(1, len(pool) // need)
+        pool = pool[::step][:need]
+        s = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for wp, sp in pool:
+                launch(wp, sp, n, k, s.cuda_stream)
+        g.replay()
         torch.cuda.synchronize()
-        for name, n, k, a, b in pairs:
-            dt = a.elapsed_time(b)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            a.record(s)
+            for _ in range(reps):
+                g.replay()
+            b.record(s)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / (reps * len(pool))
+        return us, len(pool) * tiles * tile_b
+
+    per_shape = {}
+    if not args.no_shapes:
+        for name, n, k in UNFUSED + FUSED[:1] + FUSED[2:3] + [LM_HEAD]:
             key = f"{k}->{n}"
-            e = per.setdefault(key, {"ms": 0.0, "launches": 0, "bytes": 0})
-            e["ms"] += dt
-            e["launches"] += 1
-            e["bytes"] += algo_bytes(m, n, k)
-            tot_ms += dt
-            tot_bytes += algo_bytes(m, n, k)
-            n_launch += 1
-    per_shape = {
-        kk: {
-            "us_per_launch": round(v["ms"] / v["launches"] * 1e3, 3),
-            "gbs": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1),
-            "frac_of_8tbs": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        }
-        for kk, v in per.items()
-    }
-    avg_launch_s = tot_ms / n_launch * 1e-3
-    bytes_per_launch = tot_bytes / n_launch
-    achieved = bytes_per_launch / avg_launch_s / 1e9
-    log("per-shape:", json.dumps(per_shape))
+            if key in per_shape:
+                continue
+            us, pool_b = shape_time(n, k)
+            gbs = algo_bytes(m, n, k) / us / 1e3
+            per_shape[key] = {"name": name, "us": round(us, 3), "gbs": round(gbs, 1),
+                              "frac_of_8tbs": round(gbs / HBM_PEAK_GBS, 4), "rotated_mb": pool_b >> 20}
+        log("per-shape:", json.dumps(per_shape))
+
+    # dominant kernel: the launch shape with the largest share of the step
+    share = {}
+    for name, n, k, _ in linears:
+        share[(name, n, k)] = share.get((name, n, k), 0) + 1
+    dom = max(share, key=lambda s: share[s] * algo_bytes(m, s[1], s[2]))
+    dom_us, _ = shape_time(dom[1], dom[2], reps=5)
+    dom_bytes = algo_bytes(m, dom[1], dom[2])
+    achieved = dom_bytes / dom_us / 1e3
 
     # ------------------------------------------------------------------ measured copy bandwidth
     src = torch.empty(1 << 28, device=dev, dtype=torch.int32)
@@ -246,7 +272,7 @@ def main() -> int:
         passes = 0
         c_start = time.perf_counter()
         while True:
-            for name, n, k, qc, sc in cpu_sample:
+            for _, n, k, qc, sc in cpu_sample:
                 torch_path.w4a16_linear(xc[k], qc, sc, None, GROUP)
                 done_bytes += algo_bytes(m, n, k)
             passes += 1
@@ -259,12 +285,13 @@ def main() -> int:
             "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": (
-                f"{passes} passes over layer 0's 7 int4 linears (M={m}, bf16 x), torch CPU dequantize + "
+                f"{passes} passes over layer 0's seven int4 projections (M={m}, bf16 x): torch CPU dequantize + "
                 f"F.linear per call (oracle/torch_path.py), {c_el:.1f}s on '{cpu_model()}', os.cpu_count()={threads}"
             ),
         }
         log(f"cpu baseline: {cpu_baseline['value']} GB/s")
 
+    launches = len(linears)
     out = {
         "metric": METRIC,
         "value": round(value_gbs, 1),
@@ -280,20 +307,22 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": (
-                "int4-g128 W4A16 decode GEMV over all linears of a Llama-3-8B decode step "
-                f"({args.layers} layers x q,k,v,o,gate,up,down + lm_head), M={m}, HIP-graph replay"
+                f"int4-g128 W4A16 decode linears of a Llama-3-8B step ({args.layers} layers x "
+                + ("qkv,o,gate_up,down" if args.layout == "fused" else "q,k,v,o,gate,up,down")
+                + f" + lm_head), M={m}, HIP-graph replay"
             ),
             "m": m,
             "layers": args.layers,
+            "layout": args.layout,
             "group_size": GROUP,
-            "launches_per_step": len(linears),
+            "launches_per_step": launches,
             "bytes_per_step": step_bytes,
-            "splits": args.splits or "default",
+            "k_slices": args.kslices or "default",
         },
         "frac_of_hbm_peak": round(value_gbs / HBM_PEAK_GBS, 4),
         "frac_of_measured_copy": round(value_gbs / copy_gbs, 4),
         "measured_copy_gbs": round(copy_gbs, 1),
-        "decode_linear_tok_s": round(1000.0 / ms_per_step, 1),
+        "linear_only_tok_s": round(1000.0 / ms_per_step * m, 1),
         "graph_matches_eager": graph_ok,
         "per_shape": per_shape,
         "roofline": {
@@ -303,9 +332,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "sqx::int4_linear_kernel<ActBF16,128,false,false,1>",
-            "avg_launch_us": round(avg_launch_s * 1e6, 3),
-            "bytes_per_launch": round(bytes_per_launch),
+            "kernel": f"int4_linear_kernel (sqx_int4_linear) {dom[0]} {dom[2]}->{dom[1]}",
+            "avg_launch_us": round(dom_us, 3),
+            "bytes_per_launch": dom_bytes,
         },
         "cpu_baseline": cpu_baseline,
     }

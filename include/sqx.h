@@ -85,25 +85,21 @@ int sqx_int4_tile(const int8_t* codes, int code_kind, const void* scales, const 
 int sqx_int4_tile_packed(const uint8_t* packed, const void* scales, int param_dtype, int64_t rows,
                          int64_t cols, int64_t group, uint8_t* wt, void* st, sqx_stream_t stream);
 
-/* Workspace bytes sqx_int4_linear needs for the given shape and split count (0 when splits == 1).
- * The first 4*ceil(rows/16) bytes are tile counters that must be zero before the first call; the
- * kernel leaves them zero again, so one zero-filled workspace serves any number of calls on one
- * stream (calls that overlap on several streams need a workspace each). */
-int64_t sqx_int4_linear_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int splits);
-
-/* Split count the library picks for a shape when the caller passes splits <= 0. */
-int sqx_int4_linear_default_splits(int64_t m, int64_t rows, int64_t cols);
+/* Number of k-slices (waves per 16-row tile) the library picks for a shape when the caller passes
+ * k_slices <= 0. */
+int sqx_int4_linear_default_kslices(int64_t m, int64_t rows, int64_t cols);
 
 /* W4A16 linear (w4a16_linear, int4_group.py:148-164; awq_linear, awq.py:184-192 once the AWQ
  * channel scale is folded): y[m, r] = sum_c x[m, c] * w[r, c] (+ bias[r]), with
  * w[r, c] = (u - z) * s for the tiled codes u, zero z (8 for symmetric codes) and scale s of the
  * group. x: [m, cols] of act_dtype (BF16 or F16); y: [m, rows] of act_dtype; bias: [rows] of
  * act_dtype or NULL. wt/st/zt from sqx_int4_tile (zt NULL for symmetric codes). fp32 accumulation.
- * Any m >= 1 (processed 16 rows of x per pass). splits <= 0 picks the default. */
+ * Any m >= 1 (processed 64 rows of x per pass). One workgroup per 16-row tile; k_slices (1..16, or
+ * <= 0 for the default) waves split its columns and sum their partials in a fixed order, so results
+ * are deterministic for a given k_slices. Needs no workspace. */
 int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt, int param_dtype,
                     const void* x, int act_dtype, void* y, const void* bias, int64_t m, int64_t rows,
-                    int64_t cols, int64_t group, int splits, void* workspace,
-                    int64_t workspace_bytes, sqx_stream_t stream);
+                    int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -38,11 +38,10 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sqx_int4_tiled_param_count": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "sqx_int4_tile": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_i, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p]),
     "sqx_int4_tile_packed": (_c_i, [_c_p, _c_p, _c_i, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
-    "sqx_int4_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i]),
-    "sqx_int4_linear_default_splits": (_c_i, [_c_i64, _c_i64, _c_i64]),
+    "sqx_int4_linear_default_kslices": (_c_i, [_c_i64, _c_i64, _c_i64]),
     "sqx_int4_linear": (
         _c_i,
-        [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p, _c_i64, _c_p],
+        [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p],
     ),
 }
 

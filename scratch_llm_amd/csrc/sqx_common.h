@@ -114,6 +114,38 @@ struct ActF16 {
   }
 };
 
+// ---------------------------------------------------------------- buffer loads (device) -----
+// Raw buffer resources: SGPR base + 32-bit byte count. A load whose byte offset (voffset + soffset)
+// is at or beyond `bytes` returns zero without touching memory, which the kernels use for rows of
+// an MFMA operand beyond the last activation row. Word 3 is the gfx9 raw-buffer format.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ inline rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// aux bit 1 = nt (streaming: the line is not kept in the caches once used).
+template <int AUX = 0>
+__device__ inline u32x4_t bload128(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, AUX));
+}
+
+__device__ inline uint32_t bload32(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+
+__device__ inline uint32_t bload16(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+}
+
+// (a & mask) | bits in one VALU op. gfx9 VOP3 encodings take no literal constants, so the compiler
+// splits this into v_and + v_or; here the mask sits in an SGPR and `bits` in a VGPR.
+__device__ inline uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(bits));
+  return r;
+}
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace sqx

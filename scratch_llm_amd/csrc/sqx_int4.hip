@@ -21,6 +21,14 @@
 
 #include <float.h>
 
+// k-blocks per pipeline round for 1 and 2 MFMA row chunks (tuning knobs for sweeps).
+#ifndef SQX_INT4_U1
+#define SQX_INT4_U1 4
+#endif
+#ifndef SQX_INT4_U2
+#define SQX_INT4_U2 2
+#endif
+
 namespace sqx {
 
 // ----------------------------------------------------------------------------------------------
@@ -188,173 +196,245 @@ __global__ __launch_bounds__(256) void int4_tile_params_kernel(const P* __restri
 // The linear
 // ----------------------------------------------------------------------------------------------
 template <bool PBF16>
-__device__ inline float load_param(const void* p, int64_t idx) {
-  if (PBF16) return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[idx]);
-  return static_cast<const float*>(p)[idx];
+__device__ inline float load_param(rsrc_t r, uint32_t voff, uint32_t soff) {
+  if (PBF16) return bf16_bits_to_f32(static_cast<uint16_t>(bload16(r, voff, soff)));
+  return __builtin_bit_cast(float, bload32(r, voff, soff));
 }
 
-template <class A, int GROUP, bool ASYM, bool PBF16, int MCH>
-__global__ __launch_bounds__(256) void int4_linear_kernel(
-    const u32x4_t* __restrict__ wt, const void* __restrict__ st, const void* __restrict__ zt,
-    const uint16_t* __restrict__ x, uint16_t* __restrict__ y, const uint16_t* __restrict__ bias,
-    float* __restrict__ part, int* __restrict__ cnt, int M, int N, int K, int T, int KB, int S,
-    int kb_per) {
+// One workgroup computes one 16-row tile for up to 16*MCH activation rows. Its NW waves split the
+// tile's k-blocks into contiguous slices (wave w owns [w*kbw, min(KB, (w+1)*kbw))), each wave keeps
+// U weight blocks (U KiB per wave) in flight, and the per-wave partial tiles are summed through LDS
+// in wave order: no inter-workgroup communication, no global fences, deterministic results.
+// Weights and parameters are read through buffer resources: a per-lane constant plus a
+// wave-uniform SGPR offset.
+// Activations: with XLDS the workgroup first copies its M rows (zero-padded to KB*128 columns) into
+// LDS with full-width 16-byte loads and every MFMA A fragment is then an LDS read; rows at or beyond
+// M alias row M-1 (those output rows are computed and dropped). Without XLDS each fragment is a
+// buffer load, rows at or beyond M read as zero, and KTAIL (cols not a multiple of 128) zeroes the
+// last k-block's trailing 32-column steps.
+template <class A, int GROUP, bool ASYM, bool PBF16, int MCH, int U, bool KTAIL, bool XLDS>
+__global__ __launch_bounds__(1024) void int4_linear_kernel(
+    const uint8_t* __restrict__ wt, const void* __restrict__ st, const void* __restrict__ zt,
+    const uint16_t* __restrict__ x, uint16_t* __restrict__ y, const uint16_t* __restrict__ bias, int M, int N,
+    int K, int KB, int kbw) {
+  extern __shared__ f32x4_t smem[];  // [NW][MCH][64] partial accumulators, then (XLDS) the activations
+  f32x4_t* red = smem;
   constexpr int NG = 128 / GROUP;  // groups per k-block
   constexpr int MPG = 4 / NG;      // MFMAs (of K = 32) per group
+  constexpr int PB = PBF16 ? 2 : 4;
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  const int s = blockIdx.y;
-  const int kb0 = s * kb_per;
-  const int kb1 = min(KB, kb0 + kb_per);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int t = blockIdx.x;
+  const int kb0 = wave * kbw;
+  const int kb1 = min(KB, kb0 + kbw);
   const int nl = lane & 15;  // weight row within the tile (B column) == A row within a chunk
   const int jg = lane >> 4;  // 8-column slice within each 32-column MFMA step
   const int Gp = KB * NG;
 
+  const rsrc_t wr = make_rsrc(wt + (int64_t)t * KB * 1024, (uint32_t)KB * 1024u);
+  const uint32_t pbytes = (uint32_t)Gp * 16u * PB;
+  const rsrc_t sr = make_rsrc(static_cast<const char*>(st) + (int64_t)t * pbytes, pbytes);
+  const rsrc_t zr = ASYM ? make_rsrc(static_cast<const char*>(zt) + (int64_t)t * pbytes, pbytes) : sr;
+  const rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
+  const uint32_t wvo = (uint32_t)lane * 16u;
+  const uint32_t pvo = (uint32_t)nl * PB;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem + nw * MCH * 64);
+  const int xpitch = KB * 128 + 8;  // LDS row pitch in elements (16 bytes of padding per row)
+  uint32_t xvo[MCH];
   f32x4_t yacc[MCH];
-  const uint16_t* xrow[MCH];
-  bool mok[MCH];
 #pragma unroll
   for (int c = 0; c < MCH; ++c) {
     yacc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const int m = c * 16 + nl;
-    mok[c] = m < M;
-    xrow[c] = x + (int64_t)(mok[c] ? m : 0) * K + 8 * jg;
+    xvo[c] = XLDS ? (uint32_t)(min(c * 16 + nl, M - 1) * xpitch + 8 * jg)
+                  : ((uint32_t)(c * 16 + nl) * (uint32_t)K + 8u * jg) * 2u;
   }
-  const u32x4_t* wp = wt + (int64_t)t * KB * 64 + lane;
-  const int64_t pbase = (int64_t)t * Gp * 16 + nl;
+  const uint32_t kMask = 0x000F000Fu;
+  const uint32_t magic = A::kMagicPair;
   const uint32_t sym_off = A::pair_from_f32(-(A::kMagic + 8.0f));
 
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const u32x4_t w = __builtin_nontemporal_load(wp + (int64_t)kb * 64);
-    u32x4_t xv[MCH][4];
+  // Software pipeline over rounds of U k-blocks: the weights and parameters of round r+1 are
+  // requested before round r is computed. Buffer loads retire in issue order, so each round's
+  // activations are requested before the next round's weights; waiting for them leaves the next
+  // weights in flight.
+  u32x4_t w[U];
+  float sc[U][NG];
+  float zf[U][NG];
+  auto load_round = [&](int kr, u32x4_t (&wo)[U], float (&so)[U][NG], float (&zo)[U][NG]) {
 #pragma unroll
-    for (int c = 0; c < MCH; ++c) {
+    for (int u = 0; u < U; ++u) {
+      if (kr + u < kb1) {  // wave-uniform
+        wo[u] = bload128<2>(wr, wvo, (uint32_t)(kr + u) * 1024u);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int k0 = kb * 128 + 32 * i + 8 * jg;
-        xv[c][i] = (mok[c] && k0 < K) ? *reinterpret_cast<const u32x4_t*>(xrow[c] + kb * 128 + 32 * i)
-                                       : u32x4_t{0u, 0u, 0u, 0u};
+        for (int g = 0; g < NG; ++g) {
+          const uint32_t off = (uint32_t)((kr + u) * NG + g) * 16u * PB;
+          so[u][g] = load_param<PBF16>(sr, pvo, off);
+          zo[u][g] = ASYM ? load_param<PBF16>(zr, pvo, off) : 8.0f;
+        }
       }
     }
-    float sc[NG];
-    float zf[NG];
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      const int64_t pi = pbase + (int64_t)(kb * NG + g) * 16;
-      sc[g] = load_param<PBF16>(st, pi);
-      zf[g] = ASYM ? load_param<PBF16>(zt, pi) : 8.0f;
+  };
+  if (kb0 < kb1) load_round(kb0, w, sc, zf);
+  // The first weight round is in flight while the activations are copied into LDS.
+  if (XLDS) {
+    const int chunks_per_row = KB * 16;  // 16-byte chunks of a padded row
+    for (int idx = threadIdx.x; idx < M * chunks_per_row; idx += blockDim.x) {
+      const int r = idx / chunks_per_row;
+      const int col = (idx - r * chunks_per_row) * 8;
+      const u32x4_t v = col < K ? bload128(xr, (uint32_t)(r * K + col) * 2u, 0u) : u32x4_t{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4_t*>(xs + r * xpitch + col) = v;
     }
-    u32x4_t b[4];
+    __syncthreads();
+  }
+
+  for (int kb = kb0; kb < kb1; kb += U) {
+    // Global activation fragments of the whole round are requested ahead of the next round's
+    // weights (see above); LDS fragments are read per block, just before use.
+    u32x4_t xg[XLDS ? 1 : U][MCH][4];
+    if constexpr (!XLDS) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t d = w[i];
-      b[i] = u32x4_t{(d & 0x000F000Fu) | A::kMagicPair, ((d >> 4) & 0x000F000Fu) | A::kMagicPair,
-                     ((d >> 8) & 0x000F000Fu) | A::kMagicPair, ((d >> 12) & 0x000F000Fu) | A::kMagicPair};
+      for (int u = 0; u < U; ++u) {
+        if (kb + u < kb1) {
+#pragma unroll
+          for (int c = 0; c < MCH; ++c) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xg[u][c][i] = bload128(xr, xvo[c], (uint32_t)((kb + u) * 128 + 32 * i) * 2u);
+          }
+        }
+      }
+    }
+    u32x4_t wn[U];
+    float scn[U][NG];
+    float zfn[U][NG];
+    if (kb + U < kb1) load_round(kb + U, wn, scn, zfn);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (kb + u < kb1) {  // wave-uniform
+        const int kk = kb + u;
+        u32x4_t xv[MCH][4];
+#pragma unroll
+        for (int c = 0; c < MCH; ++c) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if constexpr (XLDS)
+              xv[c][i] = *reinterpret_cast<const u32x4_t*>(xs + xvo[c] + kk * 128 + 32 * i);
+            else
+              xv[c][i] = xg[u][c][i];
+          }
+        }
+        if (KTAIL && !XLDS && kk == KB - 1) {  // wave-uniform: steps past the last column read no activations
+          const int live_steps = (K - kk * 128) / 32;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (i >= live_steps) {
+#pragma unroll
+              for (int c = 0; c < MCH; ++c) xv[c][i] = u32x4_t{0u, 0u, 0u, 0u};
+            }
+          }
+        }
+        u32x4_t b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t d = w[u][i];
+          b[i] = u32x4_t{and_or(d, kMask, magic), and_or(d >> 4, kMask, magic), and_or(d >> 8, kMask, magic),
+                         and_or(d >> 12, kMask, magic)};
+        }
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const uint32_t off = ASYM ? A::pair_from_f32(-(A::kMagic + zf[u][g])) : sym_off;
+          const u32x4_t boff = u32x4_t{off, off, off, off};
+#pragma unroll
+          for (int c = 0; c < MCH; ++c) {
+            f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = g * MPG; i < (g + 1) * MPG; ++i) acc = A::mfma(xv[c][i], b[i], acc);
+#pragma unroll
+            for (int i = g * MPG; i < (g + 1) * MPG; ++i) acc = A::mfma(xv[c][i], boff, acc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) yacc[c][r] = fmaf(sc[u][g], acc[r], yacc[c][r]);
+          }
+        }
+      }
     }
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      const uint32_t off = ASYM ? A::pair_from_f32(-(A::kMagic + zf[g])) : sym_off;
-      const u32x4_t boff = u32x4_t{off, off, off, off};
+    for (int u = 0; u < U; ++u) {
+      w[u] = wn[u];
 #pragma unroll
-      for (int c = 0; c < MCH; ++c) {
-        f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = g * MPG; i < (g + 1) * MPG; ++i) acc = A::mfma(xv[c][i], b[i], acc);
-#pragma unroll
-        for (int i = g * MPG; i < (g + 1) * MPG; ++i) acc = A::mfma(xv[c][i], boff, acc);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) yacc[c][r] = fmaf(sc[g], acc[r], yacc[c][r]);
+      for (int g = 0; g < NG; ++g) {
+        sc[u][g] = scn[u][g];
+        zf[u][g] = zfn[u][g];
       }
     }
   }
 
-  const int n = t * 16 + nl;
-  if (S == 1) {
+  // Sum the NW partial tiles in wave order. Float j of a wave's block is (chunk c, lane l, row r).
 #pragma unroll
-    for (int c = 0; c < MCH; ++c) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = c * 16 + 4 * jg + r;
-        if (m < M && n < N) {
-          float v = yacc[c][r];
-          if (bias) v += A::to_f32(bias[n]);
-          y[(int64_t)m * N + n] = A::from_f32(v);
-        }
-      }
-    }
-    return;
-  }
-
-  // Split-K: publish this split's partial tile, then the last split to arrive sums all partials
-  // in split order (deterministic) and writes the output. The counter is reset for the next call.
-  float* mine = part + ((int64_t)t * S + s) * (16 * MCH * 16);
-#pragma unroll
-  for (int c = 0; c < MCH; ++c) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = c * 16 + 4 * jg + r;
-      if (m < M) mine[m * 16 + nl] = yacc[c][r];
+  for (int c = 0; c < MCH; ++c) red[(wave * MCH + c) * 64 + lane] = yacc[c];
+  __syncthreads();
+  constexpr int kOut = MCH * 64 * 4;
+  const float* rf = reinterpret_cast<const float*>(red);
+  for (int j = threadIdx.x; j < kOut; j += blockDim.x) {
+    float v = 0.0f;
+    for (int ww = 0; ww < nw; ++ww) v += rf[ww * kOut + j];
+    const int c = j >> 8;
+    const int l = (j >> 2) & 63;
+    const int m = c * 16 + 4 * (l >> 4) + (j & 3);
+    const int n = t * 16 + (l & 15);
+    if (m < M && n < N) {
+      if (bias) v += A::to_f32(bias[n]);
+      y[(int64_t)m * N + n] = A::from_f32(v);
     }
   }
-  __threadfence();
-  int prev = 0;
-  if (lane == 0) prev = atomicAdd(&cnt[t], 1);
-  prev = __shfl(prev, 0);
-  if (prev != S - 1) return;
-  __threadfence();
-  const float* all = part + (int64_t)t * S * (16 * MCH * 16);
-#pragma unroll
-  for (int c = 0; c < MCH; ++c) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = c * 16 + 4 * jg + r;
-      if (m < M) {
-        float v = 0.0f;
-        for (int ss = 0; ss < S; ++ss) v += all[(int64_t)ss * (16 * MCH * 16) + m * 16 + nl];
-        if (n < N) {
-          if (bias) v += A::to_f32(bias[n]);
-          y[(int64_t)m * N + n] = A::from_f32(v);
-        }
-      }
-    }
-  }
-  if (lane == 0) atomicExch(&cnt[t], 0);
 }
-
-static int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
 
 static int linear_mch(int64_t m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
 
-template <class A, int GROUP, bool ASYM, bool PBF16>
-static void launch_linear_g(int mch, dim3 grid, hipStream_t stream, const u32x4_t* wt, const void* st,
-                            const void* zt, const uint16_t* x, uint16_t* y, const uint16_t* bias,
-                            float* part, int* cnt, int M, int N, int K, int T, int KB, int S, int kb_per) {
-  if (mch == 1)
-    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 1>), grid, dim3(256), 0, stream, wt, st, zt,
-                       x, y, bias, part, cnt, M, N, K, T, KB, S, kb_per);
+// Largest LDS copy of the activations a workgroup makes (bytes); larger inputs read fragments
+// from global memory.
+static constexpr int64_t kXldsMax = 64 * 1024;
+
+static int64_t xlds_bytes(int64_t m, int64_t KB) { return m * (KB * 128 + 8) * 2; }
+
+template <class A, int GROUP, bool ASYM, bool PBF16, bool KTAIL>
+static void launch_linear_t(int mch, int nw, hipStream_t stream, const uint8_t* wt, const void* st,
+                            const void* zt, const uint16_t* x, uint16_t* y, const uint16_t* bias, int M, int N,
+                            int K, int T, int KB, int kbw) {
+  const dim3 grid(static_cast<unsigned>(T)), block(static_cast<unsigned>(64 * nw));
+  const size_t red = static_cast<size_t>(nw) * mch * 64 * sizeof(f32x4_t);
+  if (mch == 1 && xlds_bytes(M, KB) <= kXldsMax)
+    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 1, SQX_INT4_U1, KTAIL, true>), grid, block,
+                       red + xlds_bytes(M, KB), stream, wt, st, zt, x, y, bias, M, N, K, KB, kbw);
+  else if (mch == 1)
+    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 1, SQX_INT4_U1, KTAIL, false>), grid, block, red,
+                       stream, wt, st, zt, x, y, bias, M, N, K, KB, kbw);
   else if (mch == 2)
-    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 2>), grid, dim3(256), 0, stream, wt, st, zt,
-                       x, y, bias, part, cnt, M, N, K, T, KB, S, kb_per);
+    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 2, SQX_INT4_U2, KTAIL, false>), grid, block, red,
+                       stream, wt, st, zt, x, y, bias, M, N, K, KB, kbw);
   else
-    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 4>), grid, dim3(256), 0, stream, wt, st, zt,
-                       x, y, bias, part, cnt, M, N, K, T, KB, S, kb_per);
+    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 4, 1, KTAIL, false>), grid, block, red, stream,
+                       wt, st, zt, x, y, bias, M, N, K, KB, kbw);
+}
+
+template <class A, int GROUP, bool ASYM, bool PBF16>
+static void launch_linear_g(int mch, int nw, hipStream_t stream, const uint8_t* wt, const void* st,
+                            const void* zt, const uint16_t* x, uint16_t* y, const uint16_t* bias, int M, int N,
+                            int K, int T, int KB, int kbw) {
+  if (K % 128 == 0)
+    launch_linear_t<A, GROUP, ASYM, PBF16, false>(mch, nw, stream, wt, st, zt, x, y, bias, M, N, K, T, KB, kbw);
+  else
+    launch_linear_t<A, GROUP, ASYM, PBF16, true>(mch, nw, stream, wt, st, zt, x, y, bias, M, N, K, T, KB, kbw);
 }
 
 template <class A, bool ASYM, bool PBF16>
-static void launch_linear_a(int group, int mch, dim3 grid, hipStream_t stream, const u32x4_t* wt,
-                            const void* st, const void* zt, const uint16_t* x, uint16_t* y,
-                            const uint16_t* bias, float* part, int* cnt, int M, int N, int K, int T, int KB,
-                            int S, int kb_per) {
+static void launch_linear_a(int group, int mch, int nw, hipStream_t stream, const uint8_t* wt, const void* st,
+                            const void* zt, const uint16_t* x, uint16_t* y, const uint16_t* bias, int M, int N,
+                            int K, int T, int KB, int kbw) {
   if (group == 128)
-    launch_linear_g<A, 128, ASYM, PBF16>(mch, grid, stream, wt, st, zt, x, y, bias, part, cnt, M, N, K, T, KB, S,
-                                         kb_per);
+    launch_linear_g<A, 128, ASYM, PBF16>(mch, nw, stream, wt, st, zt, x, y, bias, M, N, K, T, KB, kbw);
   else if (group == 64)
-    launch_linear_g<A, 64, ASYM, PBF16>(mch, grid, stream, wt, st, zt, x, y, bias, part, cnt, M, N, K, T, KB, S,
-                                        kb_per);
+    launch_linear_g<A, 64, ASYM, PBF16>(mch, nw, stream, wt, st, zt, x, y, bias, M, N, K, T, KB, kbw);
   else
-    launch_linear_g<A, 32, ASYM, PBF16>(mch, grid, stream, wt, st, zt, x, y, bias, part, cnt, M, N, K, T, KB, S,
-                                        kb_per);
+    launch_linear_g<A, 32, ASYM, PBF16>(mch, nw, stream, wt, st, zt, x, y, bias, M, N, K, T, KB, kbw);
 }
 
 }  // namespace sqx
@@ -510,35 +590,23 @@ extern "C" int sqx_int4_tile_packed(const uint8_t* packed, const void* scales, i
   return SQX_OK;
 }
 
-extern "C" int sqx_int4_linear_default_splits(int64_t m, int64_t rows, int64_t cols) {
+extern "C" int sqx_int4_linear_default_kslices(int64_t m, int64_t rows, int64_t cols) {
   if (m <= 0 || rows <= 0 || cols <= 0) return 1;
   const int64_t T = ceil_div(rows, 16);
   const int64_t KB = ceil_div(cols, 128);
-  // Aim for ~2048 waves (8 per CU on 256 CUs) while keeping >= 2 k-blocks per wave.
-  int64_t s = 2048 / T;
-  if (s < 1) s = 1;
+  // Aim for ~4096 waves (16 per CU on 256 CUs), 4..16 waves per tile, >= 2 k-blocks per wave.
+  int64_t s = ceil_div(4096, T);
+  if (s < 4) s = 4;
+  if (s > 16) s = 16;
   int64_t cap = KB / 2;
   if (cap < 1) cap = 1;
   if (s > cap) s = cap;
-  if (s > 64) s = 64;
   return static_cast<int>(s);
-}
-
-extern "C" int64_t sqx_int4_linear_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int splits) {
-  if (m <= 0 || rows <= 0 || cols <= 0) return -1;
-  if (splits <= 0) splits = sqx_int4_linear_default_splits(m, rows, cols);
-  const int64_t KB = ceil_div(cols, 128);
-  if (splits > KB) splits = static_cast<int>(KB);
-  if (splits <= 1) return 0;
-  const int64_t T = ceil_div(rows, 16);
-  const int mch = linear_mch(m);
-  return align256(4 * T) + T * splits * (16 * mch * 16) * 4;
 }
 
 extern "C" int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
                                int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
-                               int64_t group, int splits, void* workspace, int64_t workspace_bytes,
-                               sqx_stream_t stream) {
+                               int64_t group, int k_slices, sqx_stream_t stream) {
   SQX_REQUIRE(m >= 0 && rows > 0 && cols > 0, SQX_E_ARG, "sqx_int4_linear: bad shape m=%lld rows=%lld cols=%lld",
               (long long)m, (long long)rows, (long long)cols);
   SQX_REQUIRE(group == 32 || group == 64 || group == 128, SQX_E_ARG,
@@ -551,6 +619,7 @@ extern "C" int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt
               "sqx_int4_linear: param_dtype must be F32 or BF16");
   SQX_REQUIRE(rows < ((int64_t)1 << 31) && cols < ((int64_t)1 << 31) && m < ((int64_t)1 << 31), SQX_E_ARG,
               "sqx_int4_linear: shape too large");
+  SQX_REQUIRE(k_slices <= 16, SQX_E_ARG, "sqx_int4_linear: k_slices %d > 16", k_slices);
   if (m == 0) return SQX_OK;
   SQX_REQUIRE(wt && st && x && y, SQX_E_ARG, "sqx_int4_linear: null pointer");
   SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, SQX_E_ARG,
@@ -558,25 +627,14 @@ extern "C" int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt
   const bool asym = zt != nullptr;
   const int64_t T = ceil_div(rows, 16);
   const int64_t KB = ceil_div(cols, 128);
-  if (splits <= 0) splits = sqx_int4_linear_default_splits(m, rows, cols);
-  if (splits > KB) splits = static_cast<int>(KB);
-  const int kb_per = static_cast<int>(ceil_div(KB, splits));
-  splits = static_cast<int>(ceil_div(KB, kb_per));  // no empty splits
-  float* part = nullptr;
-  int* cnt = nullptr;
-  if (splits > 1) {
-    const int64_t need = sqx_int4_linear_workspace_bytes(m, rows, cols, splits);
-    SQX_REQUIRE(workspace && workspace_bytes >= need, SQX_E_SPACE,
-                "sqx_int4_linear: workspace of %lld bytes needed, %lld given", (long long)need,
-                (long long)workspace_bytes);
-    SQX_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, SQX_E_ARG,
-                "sqx_int4_linear: workspace must be 256-byte aligned");
-    cnt = static_cast<int*>(workspace);
-    part = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(4 * T));
-  }
+  SQX_REQUIRE(T <= 0x7fffffff && KB * 1024 < ((int64_t)1 << 31) && 64 * cols * 2 < ((int64_t)1 << 31), SQX_E_ARG,
+              "sqx_int4_linear: shape too large for 32-bit buffer offsets");
+  int nw = k_slices <= 0 ? sqx_int4_linear_default_kslices(m, rows, cols) : k_slices;
+  if (nw > KB) nw = static_cast<int>(KB);
+  const int kbw = static_cast<int>(ceil_div(KB, nw));
+  nw = static_cast<int>(ceil_div(KB, kbw));  // no idle waves
   hipStream_t s = as_stream(stream);
-  const dim3 grid(static_cast<unsigned>(ceil_div(T, 4)), static_cast<unsigned>(splits));
-  const u32x4_t* w4 = reinterpret_cast<const u32x4_t*>(wt);
+  const uint8_t* w4 = wt;
   const uint16_t* b16 = static_cast<const uint16_t*>(bias);
   const int pbf = param_dtype == SQX_DTYPE_BF16;
   // x is processed in passes of up to 64 rows (4 MFMA row chunks per wave).
@@ -588,9 +646,8 @@ extern "C" int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt
     const int M = mm, N = static_cast<int>(rows), K = static_cast<int>(cols);
     const int iT = static_cast<int>(T), iKB = static_cast<int>(KB);
     const int g = static_cast<int>(group);
-#define SQX_LIN(ACT, ASYM, PBF)                                                                                    \
-  launch_linear_a<ACT, ASYM, PBF>(g, mch, grid, s, w4, st, zt, xp, yp, b16, part, cnt, M, N, K, iT, iKB, splits, \
-                                  kb_per)
+#define SQX_LIN(ACT, ASYM, PBF) \
+  launch_linear_a<ACT, ASYM, PBF>(g, mch, nw, s, w4, st, zt, xp, yp, b16, M, N, K, iT, iKB, kbw)
     if (act_dtype == SQX_DTYPE_BF16) {
       if (asym) { if (pbf) SQX_LIN(ActBF16, true, true); else SQX_LIN(ActBF16, true, false); }
       else { if (pbf) SQX_LIN(ActBF16, false, true); else SQX_LIN(ActBF16, false, false); }

@@ -1,5 +1,5 @@
-"""Device-side plumbing shared by the quant modules: split-K workspaces and the cache of tiled
-weights built for the functional linear entry points."""
+"""Device-side plumbing shared by the quant modules: the cache of tiled weights built for the
+functional linear entry points."""
 
 from __future__ import annotations
 
@@ -7,27 +7,6 @@ import threading
 import weakref
 
 import torch
-
-from scratch_llm_amd import _lib
-
-_ws_lock = threading.Lock()
-_workspaces: dict[tuple[int, int], torch.Tensor] = {}
-
-
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """A zero-initialised, 256-byte aligned int32 buffer of at least ``nbytes`` for the current
-    stream of ``device``. The linear kernels leave its counter prefix zero after every call, so the
-    buffer is reused across calls on that stream; a larger request replaces it with a fresh one."""
-    if nbytes <= 0:
-        return None
-    key = (device.index if device.index is not None else torch.cuda.current_device(), _lib.stream_ptr(device))
-    with _ws_lock:
-        buf = _workspaces.get(key)
-        if buf is None or buf.numel() * 4 < nbytes:
-            size = max(nbytes, 1 << 20)
-            buf = torch.zeros((size + 3) // 4, dtype=torch.int32, device=device)
-            _workspaces[key] = buf
-    return buf
 
 
 class TensorKeyedCache:

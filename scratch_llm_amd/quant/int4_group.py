@@ -223,9 +223,12 @@ def tile_int4_packed(packed: Tensor, scales: Tensor, shape: tuple[int, int], gro
     return Int4Tiled(wt, st, None, rows, cols, group_size)
 
 
-def int4_linear_tiled(x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, splits: int | None = None) -> Tensor:
+def int4_linear_tiled(x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, k_slices: int | None = None) -> Tensor:
     """``x @ W.T (+ bias)`` for a tiled INT4 weight ``W [out, in]``; ``x`` is ``[..., in]`` in bf16 or
-    fp16 and the result has ``x``'s dtype and shape ``[..., out]``. fp32 accumulation."""
+    fp16 and the result has ``x``'s dtype and shape ``[..., out]``. fp32 accumulation.
+
+    ``k_slices`` (1..16) overrides how many waves split each 16-row tile's columns; the partial sums
+    are added in a fixed order, so a given ``k_slices`` always gives the same bits."""
     *batch, k = x.shape
     if k != tw.cols:
         raise ValueError(f"x has in_features={k}, weight expects {tw.cols}")
@@ -239,14 +242,12 @@ def int4_linear_tiled(x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, spli
     y = torch.empty(m, tw.rows, dtype=x.dtype, device=dev)
     b = None if bias is None else bias.to(x.dtype).contiguous()
     lib = _lib.load()
-    sp = 0 if splits is None else int(splits)
+    ks = 0 if k_slices is None else int(k_slices)
     with torch.cuda.device(dev):
-        need = lib.sqx_int4_linear_workspace_bytes(max(m, 1), tw.rows, tw.cols, sp)
-        ws = _device.workspace(dev, need)
         rc = lib.sqx_int4_linear(
             _lib.ptr(tw.wt), _lib.ptr(tw.st), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype), _lib.ptr(x2),
-            _lib.sqx_dtype(x.dtype), _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size, sp,
-            _lib.ptr(ws), 0 if ws is None else ws.numel() * 4, _lib.stream_ptr(dev),
+            _lib.sqx_dtype(x.dtype), _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size, ks,
+            _lib.stream_ptr(dev),
         )
     _lib.check(rc, "int4_linear_tiled")
     return y.reshape(*batch, tw.rows)

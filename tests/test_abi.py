@@ -57,14 +57,20 @@ def test_argument_validation_without_device():
     assert lib.sqx_int4_tile(null, 0, null, null, 0, 16, 96, 96, null, null, null, null) == -1
     assert b"group_size" in lib.sqx_last_error()
     # activations must be bf16/fp16
-    rc = lib.sqx_int4_linear(null, null, null, 0, null, 0, null, null, 1, 16, 128, 128, 1, null, 0, null)
+    rc = lib.sqx_int4_linear(null, null, null, 0, null, 0, null, null, 1, 16, 128, 128, 1, null)
     assert rc == -1 and b"BF16 or F16" in lib.sqx_last_error()
-    # a split that needs a workspace and gets none
+    # more than 16 k-slices per tile
     rc = lib.sqx_int4_linear(
         ctypes.c_void_p(256), ctypes.c_void_p(256), null, 0, ctypes.c_void_p(256), 1, ctypes.c_void_p(256), null,
-        1, 64, 4096, 128, 8, null, 0, null,
+        1, 64, 4096, 128, 17, null,
     )
-    assert rc == -3 and b"workspace" in lib.sqx_last_error()
+    assert rc == -1 and b"k_slices" in lib.sqx_last_error()
+    # misaligned weight tiles
+    rc = lib.sqx_int4_linear(
+        ctypes.c_void_p(8), ctypes.c_void_p(256), null, 0, ctypes.c_void_p(256), 1, ctypes.c_void_p(256), null,
+        1, 64, 4096, 128, 0, null,
+    )
+    assert rc == -1 and b"aligned" in lib.sqx_last_error()
 
 
 def test_size_queries():
@@ -73,10 +79,9 @@ def test_size_queries():
     assert lib.sqx_int4_tiled_weight_bytes(1000, 96) == 63 * 1 * 1024
     assert lib.sqx_int4_tiled_param_count(4096, 4096, 128) == 4096 * 32
     assert lib.sqx_int4_tiled_param_count(4096, 4096, 96) == -1
-    assert lib.sqx_int4_linear_workspace_bytes(1, 4096, 4096, 1) == 0
-    s = lib.sqx_int4_linear_default_splits(1, 1024, 4096)
-    assert 1 <= s <= 32
-    assert lib.sqx_int4_linear_workspace_bytes(1, 1024, 4096, s) > 0
+    for rows, cols in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (128256, 4096), (16, 128)):
+        s = lib.sqx_int4_linear_default_kslices(1, rows, cols)
+        assert 1 <= s <= 16 and s <= max(1, cols // 256)
 
 
 def test_python_layer_rejects_cpu_tensors():

@@ -162,16 +162,16 @@ def test_linear_llama_shapes(q4, llama_weight, m):
     assert torch.equal(y, y2)
 
 
-@pytest.mark.parametrize("splits", [1, 2, 3, 8, 32])
-def test_linear_split_counts_deterministic(q4, splits):
+@pytest.mark.parametrize("splits", [1, 2, 3, 8, 16])
+def test_linear_kslice_counts_deterministic(q4, splits):
     n, k = 512, 4096
     w = _weight((n, k), 7).to(DEV)
     q, s = q4.quantize_groupwise_int4(w)
     tw = q4.tile_int4(q, s)
     x = _act(3, k, 8).to(DEV)
-    y = q4.int4_linear_tiled(x, tw, splits=splits)
-    y_again = q4.int4_linear_tiled(x, tw, splits=splits)
-    assert torch.equal(y, y_again)  # fixed-order split reduction
+    y = q4.int4_linear_tiled(x, tw, k_slices=splits)
+    y_again = q4.int4_linear_tiled(x, tw, k_slices=splits)
+    assert torch.equal(y, y_again)  # fixed-order reduction of the wave partials
     w_eff = R.round_bf16(R.dequantize_groupwise_int4(q.cpu().numpy(), s.cpu().numpy()))
     _check_linear(y, R.linear_f64(x.float().cpu().numpy(), w_eff), f"splits={splits}")
 
@@ -243,3 +243,19 @@ def test_linear_rejects_cpu_and_bad_shapes(q4):
     q, s = q4.quantize_groupwise_int4(w.to(DEV))
     with pytest.raises(ValueError):
         q4.int4_linear_tiled(torch.randn(2, 128, device=DEV, dtype=torch.bfloat16), q4.tile_int4(q, s))
+
+
+def test_linear_back_to_back_shapes(q4):
+    """Calls of different row-tile counts in sequence on one stream (regression: a former split-K
+    design shared per-tile counters between calls) give results independent of their order."""
+    outs = []
+    for n, k, seed in ((512, 4096, 40), (4096, 4096, 41), (1024, 8192, 42), (512, 4096, 40)):
+        print_case("back to back", n, k)
+        w = _weight((n, k), seed).to(DEV)
+        q, s = q4.quantize_groupwise_int4(w)
+        x = _act(2, k, seed).to(DEV)
+        y = q4.int4_linear_tiled(x, q4.tile_int4(q, s))
+        w_eff = R.round_bf16(R.dequantize_groupwise_int4(q.cpu().numpy(), s.cpu().numpy()))
+        _check_linear(y, R.linear_f64(x.float().cpu().numpy(), w_eff), f"{k}->{n}")
+        outs.append(y)
+    assert torch.equal(outs[0], outs[-1])
