@@ -26,6 +26,17 @@ enum {
   SQX_DTYPE_F16 = 2,
 };
 
+/* FP4 weight formats and the source of their scales for sqx_fp4_tile */
+enum {
+  SQX_FP4_MX = 0, /* MXFP4: E2M1 codes, E8M0 scale per 32 columns */
+  SQX_FP4_NV = 1, /* NVFP4: E2M1 codes, E4M3 scale per 16 columns, fp32 global scale */
+};
+enum {
+  SQX_FP4_SCALE_MX_F32 = 0,  /* MXFP4 s_block as fp32 powers of two [rows, cols/32] */
+  SQX_FP4_SCALE_MX_E8M0 = 1, /* MXFP4 scales as E8M0 bytes [rows, cols/32] (the on-disk form) */
+  SQX_FP4_SCALE_NV_F32 = 2,  /* NVFP4 s_block as fp32 E4M3 values [rows, cols/16] */
+};
+
 /* status codes */
 enum {
   SQX_OK = 0,
@@ -100,6 +111,92 @@ int sqx_int4_linear_default_kslices(int64_t m, int64_t rows, int64_t cols);
 int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt, int param_dtype,
                     const void* x, int act_dtype, void* y, const void* bias, int64_t m, int64_t rows,
                     int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
+
+/* AWQ linear (awq_linear, awq.py:184-192): the W4A16 linear of the codes of W*s with the per-input
+ * channel AWQ scale s folded into the activations, y = (x / s) @ (q*gs)^T; x / s is computed in fp32
+ * per element and rounded to act_dtype while the workgroup copies x into LDS. col_scale: fp32 [cols].
+ * Needs m <= 16 and m*cols*2 <= 64 KiB (larger inputs: divide x first, then sqx_int4_linear).
+ * Other arguments as sqx_int4_linear. */
+int sqx_int4_linear_colscaled(const uint8_t* wt, const void* st, const void* zt, int param_dtype,
+                              const void* x, int act_dtype, const float* col_scale, void* y,
+                              const void* bias, int64_t m, int64_t rows, int64_t cols, int64_t group,
+                              int k_slices, sqx_stream_t stream);
+
+/* ============================================================================================
+ * FP4: E2M1 codes with E4M3 (NVFP4) or E8M0 (MXFP4) block scales
+ * (src/scratch_llm/quant/nvfp4_mxfp4.py). Bit-exact with the reference's fp32 arithmetic.
+ * ============================================================================================ */
+
+/* e2m1_round_to_code (nvfp4_mxfp4.py:85-98): codes[i] = sign(x<0) << 3 | index of the nearest
+ * E2M1 magnitude by fp32 distance (first index on ties, NaN -> 0). x: n elements of dtype. */
+int sqx_e2m1_round(const void* x, int dtype, int64_t n, uint8_t* codes, sqx_stream_t stream);
+
+/* e2m1_decode (nvfp4_mxfp4.py:101-106): out[i] = +-FP4_MAGNITUDES[codes[i] & 7] (fp32). */
+int sqx_e2m1_decode(const uint8_t* codes, int64_t n, float* out, sqx_stream_t stream);
+
+/* pack_fp4 / unpack_fp4 (nvfp4_mxfp4.py:109-129): packed[i] = codes[2i] | codes[2i+1] << 4 (low nibble
+ * = even element); an odd n pads a zero code. packed: (n+1)/2 bytes. */
+int sqx_fp4_pack(const uint8_t* codes, int64_t n, uint8_t* packed, sqx_stream_t stream);
+int sqx_fp4_unpack(const uint8_t* packed, int64_t n, uint8_t* codes, sqx_stream_t stream);
+
+/* quantize_e4m3 (nvfp4_mxfp4.py:135-147) and quantize_e8m0 (:150-159), fp32 in and out. */
+int sqx_quantize_e4m3(const float* v, int64_t n, float* out, sqx_stream_t stream);
+int sqx_quantize_e8m0(const float* v, int64_t n, float* out, sqx_stream_t stream);
+
+/* mxfp4_quantize (nvfp4_mxfp4.py:257-265) of the flattened x (n elements, zero-padded to whole
+ * blocks): codes uint8 [n_blocks*block] (one code per byte, unpacked), s_block fp32 [n_blocks]
+ * (2**ceil(log2(max(amax/6, 1e-30))), exponent clamped to +-127), and optionally e8m0 uint8
+ * [n_blocks] (exponent + 127; NULL to skip). n_blocks = ceil(n / block). */
+int sqx_mxfp4_quantize(const void* x, int dtype, int64_t n, int64_t block, uint8_t* codes,
+                       float* s_block, uint8_t* e8m0, sqx_stream_t stream);
+
+/* mxfp4_dequantize (nvfp4_mxfp4.py:268-272): out[i] = decode(codes[i]) * s_block[i / block], i < n. */
+int sqx_mxfp4_dequantize(const uint8_t* codes, const float* s_block, int64_t n, int64_t block,
+                         float* out, sqx_stream_t stream);
+
+/* Workspace bytes sqx_nvfp4_quantize needs (partial maxima of |x|). */
+int64_t sqx_nvfp4_workspace_bytes(void);
+
+/* nvfp4_quantize (nvfp4_mxfp4.py:212-223): s_global = max(amax(|x|) / 2688, 1e-30) (written to the
+ * device fp32 *s_global), s_block[b] = quantize_e4m3(block_amax / 6 / s_global), codes =
+ * e2m1(x / max(s_global * s_block, 1e-30)). Layout as sqx_mxfp4_quantize. */
+int sqx_nvfp4_quantize(const void* x, int dtype, int64_t n, int64_t block, uint8_t* codes,
+                       float* s_block, float* s_global, void* workspace, int64_t workspace_bytes,
+                       sqx_stream_t stream);
+
+/* nvfp4_dequantize (nvfp4_mxfp4.py:226-231): out[i] = decode(codes[i]) * (s_global * s_block[i/block]). */
+int sqx_nvfp4_dequantize(const uint8_t* codes, const float* s_block, const float* s_global, int64_t n,
+                         int64_t block, float* out, sqx_stream_t stream);
+
+/* Bytes of the tiled FP4 weight and scale buffers sqx_fp4_tile writes for a [rows, cols] weight
+ * (no reference counterpart: the kernels' HBM layout). fmt: SQX_FP4_MX or SQX_FP4_NV. */
+int64_t sqx_fp4_tiled_weight_bytes(int64_t rows, int64_t cols);
+int64_t sqx_fp4_tiled_scale_bytes(int64_t rows, int64_t cols, int fmt);
+
+/* Re-lay an FP4 weight [rows, cols] for the linear kernels (no reference counterpart). codes: the
+ * E2M1 codes, unpacked (codes_packed = 0, one per byte) or in the reference's packed row-major
+ * stream (codes_packed = 1, pack_fp4 order, also the on-disk weight_packed of k3/checkpoint.py:92-144).
+ * scales by scale_kind, one per `block` columns of a row: SQX_FP4_SCALE_MX_F32 (s_block fp32
+ * [rows, cols/block], block a multiple of 32), SQX_FP4_SCALE_MX_E8M0 (bytes, same shape) or
+ * SQX_FP4_SCALE_NV_F32 (s_block fp32 E4M3 values [rows, cols/block], block a multiple of 16). */
+int sqx_fp4_tile(const uint8_t* codes, int codes_packed, const void* scales, int scale_kind, int64_t block,
+                 int64_t rows, int64_t cols, uint8_t* wt, uint8_t* st, sqx_stream_t stream);
+
+/* FP4 weight linear: y[m, r] = sum_c x[m, c] * W[r, c] (* *s_global for NVFP4) (+ bias[r]) with W the
+ * dequantized tiled weight: the config-4 MXFP4 linear F.linear(x, mxfp4_dequantize(W).to(x.dtype))
+ * (nvfp4_mxfp4.py:268-272 composed with F.linear) and the NVFP4 block-scaled linear
+ * (quant_linear_nvfp4, nvfp4_mxfp4.py:296-328). x: [m, cols] BF16 or F16; y: [m, rows] of act_dtype
+ * or F32 (y_dtype); bias: [rows] of act_dtype or NULL (needs y_dtype == act_dtype); s_global: the
+ * NVFP4 global scale, a device fp32 (NULL for MXFP4). fp32 accumulation; k_slices as
+ * sqx_int4_linear. */
+int sqx_fp4_linear(const uint8_t* wt, const uint8_t* st, int fmt, const float* s_global, const void* x,
+                   int act_dtype, void* y, int y_dtype, const void* bias, int64_t m, int64_t rows,
+                   int64_t cols, int k_slices, sqx_stream_t stream);
+
+/* fp32 activations as two bf16 rows (quant_linear_nvfp4 keeps x in fp32): hi = bf16(x),
+ * lo = bf16(x - hi); sqx_sum_halves: y[i] = y2[i] + y2[n + i] (the two rows' products). */
+int sqx_split_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, sqx_stream_t stream);
+int sqx_sum_halves(const float* y2, int64_t n, float* y, sqx_stream_t stream);
 
 #ifdef __cplusplus
 }

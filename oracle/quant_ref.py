@@ -19,12 +19,12 @@ Pinning (how each function is checked against the reference, in tests/test_oracl
   search_awq_scale ................ reference laws (AWQ beats naive > 1.4x, interior alpha);
                                     exact alpha choice parity unpinned (torch reduction order)
   e2m1_round_to_code / decode ..... grid self-map, saturation, [1.7,2.4,4.9,5.1] -> [1.5,2,4,6],
-                                    exhaustive tie table at every midpoint
+                                    golden vectors for ties, huge values, infinities and NaN
   pack_fp4 / unpack_fp4 ........... checkpoint named bytes 0x80/0x7F/0x21 (tests/test_k3_checkpoint.py:281-292)
   quantize_e4m3 ................... self-map + saturation known answers, exhaustive vs torch.float8_e4m3fn
-  quantize_e8m0 ................... powers-of-two self-map; binade midpoints: parity unpinned
-  e8m0_no_overflow_scale .......... closed form ceil(log2); golden vectors at powers of two from
-                                    tests/golden (generated from the reference in this container)
+  quantize_e8m0 ................... powers-of-two self-map; golden vectors at binade midpoints
+  e8m0_no_overflow_scale .......... golden vectors from the reference at powers of two (911 cases):
+                                    ceil of the correctly rounded fp32 log2 (tests/golden)
   nvfp4 / mxfp4 quantize .......... NVFP4 MSE < MXFP4 law; recorded 20.43 / 18.74 dB (bench/RESULTS.md:561)
   quant_linear_nvfp4 .............. == dequant-matmul within 1e-4 (law at tests/test_quant_nvfp4_mxfp4.py:183-193)
   dequantize_mxfp4 (checkpoint) ... bit-level decoder over all 256 bytes x scale codes
@@ -329,16 +329,19 @@ E4M3_MAX = 448.0  # nvfp4_mxfp4.py:69
 _FP4_MAX = 6.0
 _TINY = 1e-30
 _MAGS = np.array(FP4_MAGNITUDES, dtype=np.float32)
-# Decision points between neighbouring magnitudes; a value exactly on one goes to the lower side
-# (the reference takes torch.argmin's first index on ties, nvfp4_mxfp4.py:96).
-_MIDPOINTS = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], dtype=np.float32)
 
 
 def e2m1_round_to_code(x) -> np.ndarray:
-    """nvfp4_mxfp4.py:85-98 — nearest E2M1 magnitude (ties -> lower, > 6 saturates), sign bit = x < 0."""
+    """nvfp4_mxfp4.py:85-98 — index of the nearest E2M1 magnitude by fp32 distance |a - m|, the first
+    index on ties (torch.argmin), a NaN input giving index 0; sign bit = x < 0 (so -0 keeps no sign
+    bit, small negatives keep it). Distances are fp32, so inputs above ~2**25 tie at every anchor and
+    infinities and huge values map to magnitude index 0, exactly as the reference does."""
     xf = np.asarray(x, np.float32)
     a = np.abs(xf)
-    idx = np.searchsorted(_MIDPOINTS, a, side="left").astype(np.uint8)
+    with np.errstate(invalid="ignore", over="ignore"):
+        dist = np.abs(a[..., None] - _MAGS).astype(np.float32)
+    idx = np.argmin(dist, axis=-1).astype(np.uint8)  # first minimum; a NaN row gives index 0
+    idx = np.where(np.isnan(a), np.uint8(0), idx)
     sign = (xf < 0).astype(np.uint8)
     return (sign << 3) | idx
 
@@ -400,15 +403,20 @@ def ceil_log2_exact(v) -> np.ndarray:
     return e + (m != 0)
 
 
-def e8m0_no_overflow_exponent(amax) -> np.ndarray:
-    """nvfp4_mxfp4.py:162-174 — exponent of the MXFP4 block scale: clamp(ceil(log2(max(amax/6, 1e-30))), +-127).
+def log2_f32(v) -> np.ndarray:
+    """fp32 log2 correctly rounded (float64 log2, then one rounding to fp32), the value torch's CPU
+    log2 returns for fp32 inputs; pinned against the reference on 911 inputs near powers of two."""
+    with np.errstate(divide="ignore"):
+        return np.log2(np.asarray(v, np.float32).astype(np.float64)).astype(np.float32)
 
-    ceil(log2) is taken exactly here. The reference evaluates torch's fp32 log2 first, which rounds
-    to the integer k when amax/6 lies within about half an fp32 ulp of k above 2**k; tests pin that
-    window with golden vectors produced from the reference."""
+
+def e8m0_no_overflow_exponent(amax) -> np.ndarray:
+    """nvfp4_mxfp4.py:162-174 — exponent of the MXFP4 block scale:
+    clamp(ceil(log2(max(amax/6, 1e-30))), +-127) with log2 evaluated in fp32 (so amax/6 a few ulps
+    above 2**k gives k when the fp32 log2 rounds down onto k)."""
     t = np.asarray(amax, np.float32) / F32(_FP4_MAX)
     t = np.where(t < F32(_TINY), F32(_TINY), t).astype(np.float32)
-    return np.clip(ceil_log2_exact(t), -127, 127)
+    return np.clip(np.ceil(log2_f32(t)), -127, 127).astype(np.int64)
 
 
 def e8m0_no_overflow_scale(amax) -> np.ndarray:
@@ -416,11 +424,9 @@ def e8m0_no_overflow_scale(amax) -> np.ndarray:
 
 
 def quantize_e8m0(v) -> np.ndarray:
-    """nvfp4_mxfp4.py:150-159 — 2**clamp(rint(log2 v), +-127), 0 -> 0. log2 in float64 then rounded to
-    fp32 (correct rounding); ties of rint(log2) at binade midpoints are unpinned."""
+    """nvfp4_mxfp4.py:150-159 — 2**clamp(rint(log2 v), +-127) with fp32 log2, 0 -> 0."""
     vf = np.asarray(v, np.float32)
-    lg = np.log2(np.where(vf < F32(_TINY), F32(_TINY), vf).astype(np.float64)).astype(np.float32)
-    e = np.clip(np.rint(lg), -127, 127)
+    e = np.clip(np.rint(log2_f32(np.where(vf < F32(_TINY), F32(_TINY), vf))), -127, 127)
     return np.where(vf > 0, np.ldexp(np.float32(1.0), e.astype(np.int32)), F32(0.0)).astype(np.float32)
 
 

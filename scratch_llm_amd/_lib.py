@@ -19,6 +19,11 @@ LIB_PATH = Path(__file__).resolve().parent / "libsqx_hip.so"
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_F16 = 2
+FP4_MX = 0
+FP4_NV = 1
+FP4_SCALE_MX_F32 = 0
+FP4_SCALE_MX_E8M0 = 1
+FP4_SCALE_NV_F32 = 2
 
 _TORCH_TO_SQX = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
 
@@ -43,6 +48,30 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_i,
         [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p],
     ),
+    "sqx_int4_linear_colscaled": (
+        _c_i,
+        [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p],
+    ),
+    "sqx_e2m1_round": (_c_i, [_c_p, _c_i, _c_i64, _c_p, _c_p]),
+    "sqx_e2m1_decode": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
+    "sqx_fp4_pack": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
+    "sqx_fp4_unpack": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
+    "sqx_quantize_e4m3": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
+    "sqx_quantize_e8m0": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
+    "sqx_mxfp4_quantize": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p]),
+    "sqx_mxfp4_dequantize": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_nvfp4_workspace_bytes": (_c_i64, []),
+    "sqx_nvfp4_quantize": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p]),
+    "sqx_nvfp4_dequantize": (_c_i, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_fp4_tiled_weight_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "sqx_fp4_tiled_scale_bytes": (_c_i64, [_c_i64, _c_i64, _c_i]),
+    "sqx_fp4_tile": (_c_i, [_c_p, _c_i, _c_p, _c_i, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "sqx_fp4_linear": (
+        _c_i,
+        [_c_p, _c_p, _c_i, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_i, _c_p],
+    ),
+    "sqx_split_bf16": (_c_i, [_c_p, _c_i64, _c_p, _c_p, _c_p]),
+    "sqx_sum_halves": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
 }
 
 _lock = threading.Lock()

@@ -10,6 +10,8 @@
 #include <stdio.h>
 #include <stdarg.h>
 
+#include <algorithm>
+
 #include "../../include/sqx.h"
 
 namespace sqx {
@@ -41,6 +43,9 @@ typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
 typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
 typedef unsigned u32x4_t __attribute__((__vector_size__(4 * sizeof(unsigned))));
+typedef float f32x2_t __attribute__((__vector_size__(2 * sizeof(float))));
+typedef __bf16 bf16x2_t __attribute__((__vector_size__(2 * sizeof(__bf16))));
+typedef _Float16 f16x2_t __attribute__((__vector_size__(2 * sizeof(_Float16))));
 
 // ---------------------------------------------------------------- scalar conversions --------
 // bf16 <-> fp32 by bit manipulation. fp32 -> bf16 is round-to-nearest-even with NaN kept quiet,
@@ -97,6 +102,30 @@ struct ActBF16 {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
   }
+  // byte `sel` of d (two e2m1 codes, even element in the low nibble) times 2**exponent(scale)
+  __device__ static inline uint32_t fp4_pair_scaled(uint32_t d, float scale, int sel) {
+    switch (sel) {
+      case 0: return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 0));
+      case 1: return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 1));
+      case 2: return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 2));
+      default: return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 3));
+    }
+  }
+  // two floats exactly representable in bf16 -> one bf16 pair (upper halves of the fp32 bits)
+  __device__ static inline uint32_t pack_exact(float lo, float hi) {
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo), 0x07060302u);
+  }
+  __device__ static inline f32x2_t fp4_pair_f32(uint32_t d, int sel) { return fp4_pair_f32_any(d, sel); }
+
+
+  __device__ static inline f32x2_t fp4_pair_f32_any(uint32_t d, int sel) {
+    switch (sel) {
+      case 0: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 0);
+      case 1: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 1);
+      case 2: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 2);
+      default: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 3);
+    }
+  }
 };
 
 struct ActF16 {
@@ -112,6 +141,19 @@ struct ActF16 {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
   }
+  __device__ static inline uint32_t fp4_pair_scaled(uint32_t d, float scale, int sel) {
+    switch (sel) {
+      case 0: return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, scale, 0));
+      case 1: return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, scale, 1));
+      case 2: return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, scale, 2));
+      default: return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, scale, 3));
+    }
+  }
+  // two floats exactly representable in fp16 -> one fp16 pair (round-toward-zero is exact here)
+  __device__ static inline uint32_t pack_exact(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+  }
+  __device__ static inline f32x2_t fp4_pair_f32(uint32_t d, int sel) { return ActBF16::fp4_pair_f32(d, sel); }
 };
 
 // ---------------------------------------------------------------- buffer loads (device) -----
@@ -136,6 +178,10 @@ __device__ inline uint32_t bload32(rsrc_t r, uint32_t voff, uint32_t soff) {
 
 __device__ inline uint32_t bload16(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+}
+
+__device__ inline uint32_t bload8(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b8(r, (int)voff, (int)soff, 0);
 }
 
 // (a & mask) | bits in one VALU op. gfx9 VOP3 encodings take no literal constants, so the compiler

@@ -1,0 +1,230 @@
+// The decode linear shared by the weight formats (gfx950): y[m, n] = sum_k x[m, k] * W[n, k].
+//
+// Tiled weights: T = ceil(N/16) row tiles x KB = ceil(K/128) k-blocks; block (t, kb) is 1 KiB at
+// byte (t*KB + kb)*1024, and lane L of the consuming wave owns its 16 bytes at 16L. What those bytes
+// mean, and which per-block parameters go with them, is the weight format's policy W:
+//
+//   W::Args                        device pointers and scalars of one tiled weight (kernel argument)
+//   W::Ctx  W::ctx(args, t, KB, lane)   per-wave buffer resources for tile t
+//   W::P                           the parameters of one block, held in registers
+//   W::load(ctx, kb, w, p)         buffer loads of block kb: 16 weight bytes + parameters
+//   W::xk(i, jg)                   column offset within the block of the 8 activations that lane group
+//                                  jg (= lane >> 4) feeds to MFMA step i (the B layout decides it)
+//   W::mma<A, MCH>(w, p, xv, yacc) the MFMAs of one block for MCH 16-row activation chunks
+//   W::out_scale(args)             factor applied to every output (1 unless the format has one)
+//
+// Structure (one workgroup per 16-row tile, all of K):
+//  * NW waves split the tile's k-blocks into contiguous slices (wave w owns [w*kbw, (w+1)*kbw));
+//    the per-wave partials are summed through LDS in wave order. No inter-workgroup communication,
+//    no global fences: results are deterministic for a given NW.
+//  * Software pipeline: the next U blocks' weights are in flight while the current U are computed.
+//  * XLDS: the workgroup first copies its activation rows (zero-padded to KB*128 columns, optionally
+//    divided by a per-column scale) into LDS with full-width loads; MFMA A fragments are LDS reads and
+//    rows at or beyond M alias row M-1 (those outputs are dropped). Otherwise fragments are buffer
+//    loads (rows >= M read as zero) and KTAIL zeroes activation columns at or beyond K.
+#pragma once
+
+#include "sqx_common.h"
+
+namespace sqx {
+
+// Largest LDS copy of the activations a workgroup makes (bytes); larger inputs read fragments
+// from global memory.
+static constexpr int64_t kXldsMax = 64 * 1024;
+
+inline int64_t gemv_xlds_bytes(int64_t m, int64_t KB) { return m * (KB * 128 + 8) * 2; }
+
+inline int gemv_mch(int64_t m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
+
+// Waves per tile the library picks: ~4096 waves on 256 CUs, 4..16 per tile, >= 2 blocks per wave.
+inline int gemv_default_kslices(int64_t rows, int64_t cols) {
+  const int64_t T = ceil_div(rows, 16);
+  const int64_t KB = ceil_div(cols, 128);
+  int64_t s = ceil_div(4096, T);
+  if (s < 4) s = 4;
+  if (s > 16) s = 16;
+  int64_t cap = KB / 2;
+  if (cap < 1) cap = 1;
+  if (s > cap) s = cap;
+  return static_cast<int>(s);
+}
+
+template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32>
+__global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
+                                                    void* __restrict__ yv, const uint16_t* __restrict__ bias,
+                                                    const float* __restrict__ colscale, int M, int N, int K, int KB,
+                                                    int kbw) {
+  extern __shared__ f32x4_t smem[];  // [NW][MCH][64] partial accumulators, then (XLDS) the activations
+  f32x4_t* red = smem;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int t = blockIdx.x;
+  const int kb0 = wave * kbw;
+  const int kb1 = min(KB, kb0 + kbw);
+  const int nl = lane & 15;  // weight row within the tile (B column) == A row within a chunk
+  const int jg = lane >> 4;
+
+  const typename W::Ctx wc = W::ctx(wa, t, KB, lane);
+  const rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem + nw * MCH * 64);
+  const int xpitch = KB * 128 + 8;  // LDS row pitch in elements (16 bytes of padding per row)
+  uint32_t xvo[MCH];
+  f32x4_t yacc[MCH];
+#pragma unroll
+  for (int c = 0; c < MCH; ++c) {
+    yacc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    xvo[c] = XLDS ? (uint32_t)(min(c * 16 + nl, M - 1) * xpitch) : ((uint32_t)(c * 16 + nl) * (uint32_t)K) * 2u;
+  }
+
+  u32x4_t w[U];
+  typename W::P p[U];
+  auto load_round = [&](int kr, u32x4_t (&wo)[U], typename W::P (&po)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (kr + u < kb1) W::load(wc, kr + u, wo[u], po[u]);  // wave-uniform condition
+  };
+  if (kb0 < kb1) load_round(kb0, w, p);
+  // The first weight round is in flight while the activations are copied into LDS.
+  if (XLDS) {
+    const int chunks_per_row = KB * 16;  // 16-byte chunks of a padded row
+    for (int idx = threadIdx.x; idx < M * chunks_per_row; idx += blockDim.x) {
+      const int r = idx / chunks_per_row;
+      const int col = (idx - r * chunks_per_row) * 8;
+      u32x4_t v = col < K ? bload128(xr, (uint32_t)(r * K + col) * 2u, 0u) : u32x4_t{0u, 0u, 0u, 0u};
+      if (colscale != nullptr && col < K) {  // x / s per column, rounded back to the activation type
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = __fdiv_rn(A::to_f32(static_cast<uint16_t>(v[e] & 0xffffu)), colscale[col + 2 * e]);
+          const float hi = __fdiv_rn(A::to_f32(static_cast<uint16_t>(v[e] >> 16)), colscale[col + 2 * e + 1]);
+          v[e] = static_cast<uint32_t>(A::from_f32(lo)) | (static_cast<uint32_t>(A::from_f32(hi)) << 16);
+        }
+      }
+      *reinterpret_cast<u32x4_t*>(xs + r * xpitch + col) = v;
+    }
+    __syncthreads();
+  }
+
+  for (int kb = kb0; kb < kb1; kb += U) {
+    // Global activation fragments of the whole round are requested ahead of the next round's weights:
+    // buffer loads retire in issue order, so waiting for them leaves the next weights in flight.
+    u32x4_t xg[XLDS ? 1 : U][MCH][4];
+    if constexpr (!XLDS) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (kb + u < kb1) {
+#pragma unroll
+          for (int c = 0; c < MCH; ++c) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              xg[u][c][i] = bload128(xr, xvo[c] + 2u * W::xk(i, jg), (uint32_t)((kb + u) * 128) * 2u);
+          }
+        }
+      }
+    }
+    u32x4_t wn[U];
+    typename W::P pn[U];
+    if (kb + U < kb1) load_round(kb + U, wn, pn);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (kb + u < kb1) {  // wave-uniform
+        const int kk = kb + u;
+        u32x4_t xv[MCH][4];
+#pragma unroll
+        for (int c = 0; c < MCH; ++c) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if constexpr (XLDS)
+              xv[c][i] = *reinterpret_cast<const u32x4_t*>(xs + xvo[c] + kk * 128 + W::xk(i, jg));
+            else
+              xv[c][i] = xg[u][c][i];
+          }
+        }
+        if (KTAIL && !XLDS && kk == KB - 1) {  // activations at or beyond K must not enter the sums
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (kk * 128 + W::xk(i, jg) >= K) {
+#pragma unroll
+              for (int c = 0; c < MCH; ++c) xv[c][i] = u32x4_t{0u, 0u, 0u, 0u};
+            }
+          }
+        }
+        W::template mma<A, MCH>(w[u], p[u], xv, yacc);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      w[u] = wn[u];
+      p[u] = pn[u];
+    }
+  }
+
+  // Sum the NW partial tiles in wave order. Float j of a wave's block is (chunk c, lane l, row r).
+#pragma unroll
+  for (int c = 0; c < MCH; ++c) red[(wave * MCH + c) * 64 + lane] = yacc[c];
+  __syncthreads();
+  constexpr int kOut = MCH * 64 * 4;
+  const float* rf = reinterpret_cast<const float*>(red);
+  const float osc = W::out_scale(wa);
+  for (int j = threadIdx.x; j < kOut; j += blockDim.x) {
+    float v = 0.0f;
+    for (int ww = 0; ww < nw; ++ww) v += rf[ww * kOut + j];
+    const int c = j >> 8;
+    const int l = (j >> 2) & 63;
+    const int m = c * 16 + 4 * (l >> 4) + (j & 3);
+    const int n = t * 16 + (l & 15);
+    if (m < M && n < N) {
+      v *= osc;
+      if (bias) v += A::to_f32(bias[n]);
+      if constexpr (YF32)
+        static_cast<float*>(yv)[(int64_t)m * N + n] = v;
+      else
+        static_cast<uint16_t*>(yv)[(int64_t)m * N + n] = A::from_f32(v);
+    }
+  }
+}
+
+// Launch the GEMV for every 64-row pass of x. k_slices <= 0 picks the default. Returns 0 or the
+// HIP error of the launch.
+template <class A, class W, int U1, int U2, bool YF32>
+hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, const uint16_t* bias,
+                       const float* colscale, int64_t m, int64_t rows, int64_t cols, int k_slices,
+                       hipStream_t stream) {
+  const int64_t T = ceil_div(rows, 16);
+  const int64_t KB = ceil_div(cols, 128);
+  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols) : k_slices;
+  if (nw > KB) nw = static_cast<int>(KB);
+  const int kbw = static_cast<int>(ceil_div(KB, nw));
+  nw = static_cast<int>(ceil_div(KB, kbw));  // no idle waves
+  const bool ktail = cols % 128 != 0;
+  const dim3 grid(static_cast<unsigned>(T)), block(static_cast<unsigned>(64 * nw));
+  for (int64_t m0 = 0; m0 < m; m0 += 64) {
+    const int M = static_cast<int>(m - m0 < 64 ? m - m0 : 64);
+    const int mch = gemv_mch(M);
+    const uint16_t* xp = x + m0 * cols;
+    void* yp = static_cast<char*>(y) + m0 * rows * (YF32 ? 4 : 2);
+    const int N = static_cast<int>(rows), K = static_cast<int>(cols), iKB = static_cast<int>(KB);
+    const size_t red = static_cast<size_t>(nw) * mch * 64 * sizeof(f32x4_t);
+    const bool xlds = mch == 1 && gemv_xlds_bytes(M, KB) <= kXldsMax;
+    if (colscale != nullptr && !xlds) return hipErrorNotSupported;  // column scaling happens in the LDS copy
+#define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_)                                                                    \
+  hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32>), grid, block, LDS_, stream, wa, xp, yp, bias, \
+                     colscale, M, N, K, iKB, kbw)
+    if (xlds) {
+      const size_t lds = red + gemv_xlds_bytes(M, KB);
+      if (ktail) SQX_GEMV(1, U1, true, true, lds); else SQX_GEMV(1, U1, false, true, lds);
+    } else if (mch == 1) {
+      if (ktail) SQX_GEMV(1, U1, true, false, red); else SQX_GEMV(1, U1, false, false, red);
+    } else if (mch == 2) {
+      if (ktail) SQX_GEMV(2, U2, true, false, red); else SQX_GEMV(2, U2, false, false, red);
+    } else {
+      if (ktail) SQX_GEMV(4, 1, true, false, red); else SQX_GEMV(4, 1, false, false, red);
+    }
+#undef SQX_GEMV
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace sqx

@@ -17,7 +17,7 @@
 // rows). OR-ing a code into the mantissa of MAGIC (bf16 128.0 / fp16 1024.0) gives MAGIC + u
 // exactly, so B needs three VALU ops per column pair; a second set of MFMAs with the constant
 // B = -(MAGIC + zero) removes the offset, and the group scale is applied to the fp32 partial.
-#include "sqx_common.h"
+#include "sqx_gemv.h"
 
 #include <float.h>
 
@@ -193,248 +193,104 @@ __global__ __launch_bounds__(256) void int4_tile_params_kernel(const P* __restri
 }
 
 // ----------------------------------------------------------------------------------------------
-// The linear
+// The linear: the int4 weight policy of the shared GEMV (sqx_gemv.h)
 // ----------------------------------------------------------------------------------------------
+// Block layout: dword i of lane L holds the codes of row 16t + (L & 15), columns
+// 32i + 8(L >> 4) + e, element e in nibble e/2 (even e) or 4 + e/2 (odd e), stored unsigned.
+// v_and_or_b32(d >> 4p, 0x000F000F, MAGIC pair) turns the column pair (2p, 2p+1) into the 16-bit
+// pair (MAGIC + u) exactly (bf16 128 / fp16 1024 have an integer spacing of 1); a second MFMA
+// against the constant -(MAGIC + zero) removes the offset, and the group scale is applied to the
+// fp32 partial.
 template <bool PBF16>
 __device__ inline float load_param(rsrc_t r, uint32_t voff, uint32_t soff) {
   if (PBF16) return bf16_bits_to_f32(static_cast<uint16_t>(bload16(r, voff, soff)));
   return __builtin_bit_cast(float, bload32(r, voff, soff));
 }
 
-// One workgroup computes one 16-row tile for up to 16*MCH activation rows. Its NW waves split the
-// tile's k-blocks into contiguous slices (wave w owns [w*kbw, min(KB, (w+1)*kbw))), each wave keeps
-// U weight blocks (U KiB per wave) in flight, and the per-wave partial tiles are summed through LDS
-// in wave order: no inter-workgroup communication, no global fences, deterministic results.
-// Weights and parameters are read through buffer resources: a per-lane constant plus a
-// wave-uniform SGPR offset.
-// Activations: with XLDS the workgroup first copies its M rows (zero-padded to KB*128 columns) into
-// LDS with full-width 16-byte loads and every MFMA A fragment is then an LDS read; rows at or beyond
-// M alias row M-1 (those output rows are computed and dropped). Without XLDS each fragment is a
-// buffer load, rows at or beyond M read as zero, and KTAIL (cols not a multiple of 128) zeroes the
-// last k-block's trailing 32-column steps.
-template <class A, int GROUP, bool ASYM, bool PBF16, int MCH, int U, bool KTAIL, bool XLDS>
-__global__ __launch_bounds__(1024) void int4_linear_kernel(
-    const uint8_t* __restrict__ wt, const void* __restrict__ st, const void* __restrict__ zt,
-    const uint16_t* __restrict__ x, uint16_t* __restrict__ y, const uint16_t* __restrict__ bias, int M, int N,
-    int K, int KB, int kbw) {
-  extern __shared__ f32x4_t smem[];  // [NW][MCH][64] partial accumulators, then (XLDS) the activations
-  f32x4_t* red = smem;
-  constexpr int NG = 128 / GROUP;  // groups per k-block
-  constexpr int MPG = 4 / NG;      // MFMAs (of K = 32) per group
-  constexpr int PB = PBF16 ? 2 : 4;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = blockDim.x >> 6;
-  const int t = blockIdx.x;
-  const int kb0 = wave * kbw;
-  const int kb1 = min(KB, kb0 + kbw);
-  const int nl = lane & 15;  // weight row within the tile (B column) == A row within a chunk
-  const int jg = lane >> 4;  // 8-column slice within each 32-column MFMA step
-  const int Gp = KB * NG;
-
-  const rsrc_t wr = make_rsrc(wt + (int64_t)t * KB * 1024, (uint32_t)KB * 1024u);
-  const uint32_t pbytes = (uint32_t)Gp * 16u * PB;
-  const rsrc_t sr = make_rsrc(static_cast<const char*>(st) + (int64_t)t * pbytes, pbytes);
-  const rsrc_t zr = ASYM ? make_rsrc(static_cast<const char*>(zt) + (int64_t)t * pbytes, pbytes) : sr;
-  const rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
-  const uint32_t wvo = (uint32_t)lane * 16u;
-  const uint32_t pvo = (uint32_t)nl * PB;
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem + nw * MCH * 64);
-  const int xpitch = KB * 128 + 8;  // LDS row pitch in elements (16 bytes of padding per row)
-  uint32_t xvo[MCH];
-  f32x4_t yacc[MCH];
-#pragma unroll
-  for (int c = 0; c < MCH; ++c) {
-    yacc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    xvo[c] = XLDS ? (uint32_t)(min(c * 16 + nl, M - 1) * xpitch + 8 * jg)
-                  : ((uint32_t)(c * 16 + nl) * (uint32_t)K + 8u * jg) * 2u;
-  }
-  const uint32_t kMask = 0x000F000Fu;
-  const uint32_t magic = A::kMagicPair;
-  const uint32_t sym_off = A::pair_from_f32(-(A::kMagic + 8.0f));
-
-  // Software pipeline over rounds of U k-blocks: the weights and parameters of round r+1 are
-  // requested before round r is computed. Buffer loads retire in issue order, so each round's
-  // activations are requested before the next round's weights; waiting for them leaves the next
-  // weights in flight.
-  u32x4_t w[U];
-  float sc[U][NG];
-  float zf[U][NG];
-  auto load_round = [&](int kr, u32x4_t (&wo)[U], float (&so)[U][NG], float (&zo)[U][NG]) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (kr + u < kb1) {  // wave-uniform
-        wo[u] = bload128<2>(wr, wvo, (uint32_t)(kr + u) * 1024u);
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          const uint32_t off = (uint32_t)((kr + u) * NG + g) * 16u * PB;
-          so[u][g] = load_param<PBF16>(sr, pvo, off);
-          zo[u][g] = ASYM ? load_param<PBF16>(zr, pvo, off) : 8.0f;
-        }
-      }
-    }
+template <int GROUP, bool ASYM, bool PBF16>
+struct WInt4 {
+  static constexpr int NG = 128 / GROUP;  // groups per block
+  static constexpr int MPG = 4 / NG;      // MFMA steps (of 32 columns) per group
+  static constexpr int PB = PBF16 ? 2 : 4;
+  struct Args {
+    const uint8_t* wt;
+    const void* st;
+    const void* zt;
   };
-  if (kb0 < kb1) load_round(kb0, w, sc, zf);
-  // The first weight round is in flight while the activations are copied into LDS.
-  if (XLDS) {
-    const int chunks_per_row = KB * 16;  // 16-byte chunks of a padded row
-    for (int idx = threadIdx.x; idx < M * chunks_per_row; idx += blockDim.x) {
-      const int r = idx / chunks_per_row;
-      const int col = (idx - r * chunks_per_row) * 8;
-      const u32x4_t v = col < K ? bload128(xr, (uint32_t)(r * K + col) * 2u, 0u) : u32x4_t{0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4_t*>(xs + r * xpitch + col) = v;
-    }
-    __syncthreads();
+  struct Ctx {
+    rsrc_t wr, sr, zr;
+    uint32_t wvo, pvo;
+  };
+  struct P {
+    float sc[NG];
+    float zf[NG];
+  };
+  __device__ static Ctx ctx(const Args& a, int t, int KB, int lane) {
+    Ctx c;
+    c.wr = make_rsrc(a.wt + (int64_t)t * KB * 1024, (uint32_t)KB * 1024u);
+    const uint32_t pbytes = (uint32_t)KB * NG * 16u * PB;
+    c.sr = make_rsrc(static_cast<const char*>(a.st) + (int64_t)t * pbytes, pbytes);
+    c.zr = ASYM ? make_rsrc(static_cast<const char*>(a.zt) + (int64_t)t * pbytes, pbytes) : c.sr;
+    c.wvo = (uint32_t)lane * 16u;
+    c.pvo = (uint32_t)(lane & 15) * PB;
+    return c;
   }
-
-  for (int kb = kb0; kb < kb1; kb += U) {
-    // Global activation fragments of the whole round are requested ahead of the next round's
-    // weights (see above); LDS fragments are read per block, just before use.
-    u32x4_t xg[XLDS ? 1 : U][MCH][4];
-    if constexpr (!XLDS) {
+  __device__ static void load(const Ctx& c, int kb, u32x4_t& w, P& p) {
+    w = bload128<2>(c.wr, c.wvo, (uint32_t)kb * 1024u);
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (kb + u < kb1) {
-#pragma unroll
-          for (int c = 0; c < MCH; ++c) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) xg[u][c][i] = bload128(xr, xvo[c], (uint32_t)((kb + u) * 128 + 32 * i) * 2u);
-          }
-        }
-      }
+    for (int g = 0; g < NG; ++g) {
+      const uint32_t off = (uint32_t)(kb * NG + g) * 16u * PB;
+      p.sc[g] = load_param<PBF16>(c.sr, c.pvo, off);
+      p.zf[g] = ASYM ? load_param<PBF16>(c.zr, c.pvo, off) : 8.0f;
     }
-    u32x4_t wn[U];
-    float scn[U][NG];
-    float zfn[U][NG];
-    if (kb + U < kb1) load_round(kb + U, wn, scn, zfn);
+  }
+  __device__ static int xk(int i, int jg) { return 32 * i + 8 * jg; }
+  template <class A, int MCH>
+  __device__ static void mma(const u32x4_t& w, const P& p, const u32x4_t (&xv)[MCH][4], f32x4_t (&yacc)[MCH]) {
+    const uint32_t kMask = 0x000F000Fu;
+    const uint32_t magic = A::kMagicPair;
+    u32x4_t b[4];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (kb + u < kb1) {  // wave-uniform
-        const int kk = kb + u;
-        u32x4_t xv[MCH][4];
-#pragma unroll
-        for (int c = 0; c < MCH; ++c) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if constexpr (XLDS)
-              xv[c][i] = *reinterpret_cast<const u32x4_t*>(xs + xvo[c] + kk * 128 + 32 * i);
-            else
-              xv[c][i] = xg[u][c][i];
-          }
-        }
-        if (KTAIL && !XLDS && kk == KB - 1) {  // wave-uniform: steps past the last column read no activations
-          const int live_steps = (K - kk * 128) / 32;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if (i >= live_steps) {
-#pragma unroll
-              for (int c = 0; c < MCH; ++c) xv[c][i] = u32x4_t{0u, 0u, 0u, 0u};
-            }
-          }
-        }
-        u32x4_t b[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t d = w[u][i];
-          b[i] = u32x4_t{and_or(d, kMask, magic), and_or(d >> 4, kMask, magic), and_or(d >> 8, kMask, magic),
-                         and_or(d >> 12, kMask, magic)};
-        }
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          const uint32_t off = ASYM ? A::pair_from_f32(-(A::kMagic + zf[u][g])) : sym_off;
-          const u32x4_t boff = u32x4_t{off, off, off, off};
-#pragma unroll
-          for (int c = 0; c < MCH; ++c) {
-            f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int i = g * MPG; i < (g + 1) * MPG; ++i) acc = A::mfma(xv[c][i], b[i], acc);
-#pragma unroll
-            for (int i = g * MPG; i < (g + 1) * MPG; ++i) acc = A::mfma(xv[c][i], boff, acc);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) yacc[c][r] = fmaf(sc[u][g], acc[r], yacc[c][r]);
-          }
-        }
-      }
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t d = w[i];
+      b[i] = u32x4_t{and_or(d, kMask, magic), and_or(d >> 4, kMask, magic), and_or(d >> 8, kMask, magic),
+                     and_or(d >> 12, kMask, magic)};
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      w[u] = wn[u];
+    for (int g = 0; g < NG; ++g) {
+      const uint32_t off = A::pair_from_f32(-(A::kMagic + p.zf[g]));
+      const u32x4_t boff = u32x4_t{off, off, off, off};
 #pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        sc[u][g] = scn[u][g];
-        zf[u][g] = zfn[u][g];
+      for (int c = 0; c < MCH; ++c) {
+        f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = g * MPG; i < (g + 1) * MPG; ++i) acc = A::mfma(xv[c][i], b[i], acc);
+#pragma unroll
+        for (int i = g * MPG; i < (g + 1) * MPG; ++i) acc = A::mfma(xv[c][i], boff, acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yacc[c][r] = fmaf(p.sc[g], acc[r], yacc[c][r]);
       }
     }
   }
-
-  // Sum the NW partial tiles in wave order. Float j of a wave's block is (chunk c, lane l, row r).
-#pragma unroll
-  for (int c = 0; c < MCH; ++c) red[(wave * MCH + c) * 64 + lane] = yacc[c];
-  __syncthreads();
-  constexpr int kOut = MCH * 64 * 4;
-  const float* rf = reinterpret_cast<const float*>(red);
-  for (int j = threadIdx.x; j < kOut; j += blockDim.x) {
-    float v = 0.0f;
-    for (int ww = 0; ww < nw; ++ww) v += rf[ww * kOut + j];
-    const int c = j >> 8;
-    const int l = (j >> 2) & 63;
-    const int m = c * 16 + 4 * (l >> 4) + (j & 3);
-    const int n = t * 16 + (l & 15);
-    if (m < M && n < N) {
-      if (bias) v += A::to_f32(bias[n]);
-      y[(int64_t)m * N + n] = A::from_f32(v);
-    }
-  }
-}
-
-static int linear_mch(int64_t m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
-
-// Largest LDS copy of the activations a workgroup makes (bytes); larger inputs read fragments
-// from global memory.
-static constexpr int64_t kXldsMax = 64 * 1024;
-
-static int64_t xlds_bytes(int64_t m, int64_t KB) { return m * (KB * 128 + 8) * 2; }
-
-template <class A, int GROUP, bool ASYM, bool PBF16, bool KTAIL>
-static void launch_linear_t(int mch, int nw, hipStream_t stream, const uint8_t* wt, const void* st,
-                            const void* zt, const uint16_t* x, uint16_t* y, const uint16_t* bias, int M, int N,
-                            int K, int T, int KB, int kbw) {
-  const dim3 grid(static_cast<unsigned>(T)), block(static_cast<unsigned>(64 * nw));
-  const size_t red = static_cast<size_t>(nw) * mch * 64 * sizeof(f32x4_t);
-  if (mch == 1 && xlds_bytes(M, KB) <= kXldsMax)
-    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 1, SQX_INT4_U1, KTAIL, true>), grid, block,
-                       red + xlds_bytes(M, KB), stream, wt, st, zt, x, y, bias, M, N, K, KB, kbw);
-  else if (mch == 1)
-    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 1, SQX_INT4_U1, KTAIL, false>), grid, block, red,
-                       stream, wt, st, zt, x, y, bias, M, N, K, KB, kbw);
-  else if (mch == 2)
-    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 2, SQX_INT4_U2, KTAIL, false>), grid, block, red,
-                       stream, wt, st, zt, x, y, bias, M, N, K, KB, kbw);
-  else
-    hipLaunchKernelGGL((int4_linear_kernel<A, GROUP, ASYM, PBF16, 4, 1, KTAIL, false>), grid, block, red, stream,
-                       wt, st, zt, x, y, bias, M, N, K, KB, kbw);
-}
+  __device__ static float out_scale(const Args&) { return 1.0f; }
+};
 
 template <class A, int GROUP, bool ASYM, bool PBF16>
-static void launch_linear_g(int mch, int nw, hipStream_t stream, const uint8_t* wt, const void* st,
-                            const void* zt, const uint16_t* x, uint16_t* y, const uint16_t* bias, int M, int N,
-                            int K, int T, int KB, int kbw) {
-  if (K % 128 == 0)
-    launch_linear_t<A, GROUP, ASYM, PBF16, false>(mch, nw, stream, wt, st, zt, x, y, bias, M, N, K, T, KB, kbw);
-  else
-    launch_linear_t<A, GROUP, ASYM, PBF16, true>(mch, nw, stream, wt, st, zt, x, y, bias, M, N, K, T, KB, kbw);
+static hipError_t launch_int4(const uint8_t* wt, const void* st, const void* zt, const uint16_t* x, uint16_t* y,
+                              const uint16_t* bias, const float* colscale, int64_t m, int64_t rows, int64_t cols,
+                              int k_slices, hipStream_t s) {
+  using W = WInt4<GROUP, ASYM, PBF16>;
+  const typename W::Args a{wt, st, zt};
+  return gemv_launch<A, W, SQX_INT4_U1, SQX_INT4_U2, false>(a, x, y, bias, colscale, m, rows, cols, k_slices, s);
 }
 
 template <class A, bool ASYM, bool PBF16>
-static void launch_linear_a(int group, int mch, int nw, hipStream_t stream, const uint8_t* wt, const void* st,
-                            const void* zt, const uint16_t* x, uint16_t* y, const uint16_t* bias, int M, int N,
-                            int K, int T, int KB, int kbw) {
-  if (group == 128)
-    launch_linear_g<A, 128, ASYM, PBF16>(mch, nw, stream, wt, st, zt, x, y, bias, M, N, K, T, KB, kbw);
-  else if (group == 64)
-    launch_linear_g<A, 64, ASYM, PBF16>(mch, nw, stream, wt, st, zt, x, y, bias, M, N, K, T, KB, kbw);
-  else
-    launch_linear_g<A, 32, ASYM, PBF16>(mch, nw, stream, wt, st, zt, x, y, bias, M, N, K, T, KB, kbw);
+static hipError_t launch_int4_g(int group, const uint8_t* wt, const void* st, const void* zt, const uint16_t* x,
+                                uint16_t* y, const uint16_t* bias, const float* colscale, int64_t m, int64_t rows,
+                                int64_t cols, int k_slices, hipStream_t s) {
+  if (group == 128) return launch_int4<A, 128, ASYM, PBF16>(wt, st, zt, x, y, bias, colscale, m, rows, cols, k_slices, s);
+  if (group == 64) return launch_int4<A, 64, ASYM, PBF16>(wt, st, zt, x, y, bias, colscale, m, rows, cols, k_slices, s);
+  return launch_int4<A, 32, ASYM, PBF16>(wt, st, zt, x, y, bias, colscale, m, rows, cols, k_slices, s);
 }
 
 }  // namespace sqx
@@ -592,71 +448,70 @@ extern "C" int sqx_int4_tile_packed(const uint8_t* packed, const void* scales, i
 
 extern "C" int sqx_int4_linear_default_kslices(int64_t m, int64_t rows, int64_t cols) {
   if (m <= 0 || rows <= 0 || cols <= 0) return 1;
-  const int64_t T = ceil_div(rows, 16);
-  const int64_t KB = ceil_div(cols, 128);
-  // Aim for ~4096 waves (16 per CU on 256 CUs), 4..16 waves per tile, >= 2 k-blocks per wave.
-  int64_t s = ceil_div(4096, T);
-  if (s < 4) s = 4;
-  if (s > 16) s = 16;
-  int64_t cap = KB / 2;
-  if (cap < 1) cap = 1;
-  if (s > cap) s = cap;
-  return static_cast<int>(s);
+  return gemv_default_kslices(rows, cols);
+}
+
+static int int4_linear_impl(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
+                            int act_dtype, void* y, const void* bias, const float* colscale, int64_t m,
+                            int64_t rows, int64_t cols, int64_t group, int k_slices, sqx_stream_t stream,
+                            const char* fn) {
+  SQX_REQUIRE(m >= 0 && rows > 0 && cols > 0, SQX_E_ARG, "%s: bad shape m=%lld rows=%lld cols=%lld", fn,
+              (long long)m, (long long)rows, (long long)cols);
+  SQX_REQUIRE(group == 32 || group == 64 || group == 128, SQX_E_ARG, "%s: group_size %lld unsupported (32, 64 or 128)",
+              fn, (long long)group);
+  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld", (long long)cols,
+              (long long)group);
+  SQX_REQUIRE(act_dtype == SQX_DTYPE_BF16 || act_dtype == SQX_DTYPE_F16, SQX_E_ARG,
+              "%s: activations must be BF16 or F16", fn);
+  SQX_REQUIRE(param_dtype == SQX_DTYPE_F32 || param_dtype == SQX_DTYPE_BF16, SQX_E_ARG,
+              "%s: param_dtype must be F32 or BF16", fn);
+  SQX_REQUIRE(rows < ((int64_t)1 << 31) && m < ((int64_t)1 << 31) && ceil_div(cols, 128) * 1024 < ((int64_t)1 << 31) &&
+                  64 * cols * 2 < ((int64_t)1 << 31),
+              SQX_E_ARG, "%s: shape too large for 32-bit buffer offsets", fn);
+  SQX_REQUIRE(k_slices <= 16, SQX_E_ARG, "%s: k_slices %d > 16", fn, k_slices);
+  if (m == 0) return SQX_OK;
+  SQX_REQUIRE(wt && st && x && y, SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, SQX_E_ARG,
+              "%s: wt and x must be 16-byte aligned", fn);
+  if (colscale != nullptr) {
+    SQX_REQUIRE(m <= 16 && gemv_xlds_bytes(m, ceil_div(cols, 128)) <= kXldsMax, SQX_E_ARG,
+                "%s: per-column activation scaling needs m <= 16 and m*cols*2 <= %lld bytes", fn,
+                (long long)kXldsMax);
+  }
+  const bool asym = zt != nullptr;
+  const bool pbf = param_dtype == SQX_DTYPE_BF16;
+  hipStream_t s = as_stream(stream);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  uint16_t* yp = static_cast<uint16_t*>(y);
+  const uint16_t* b16 = static_cast<const uint16_t*>(bias);
+  const int g = static_cast<int>(group);
+  hipError_t e;
+#define SQX_LIN(ACT, ASYM, PBF) \
+  e = launch_int4_g<ACT, ASYM, PBF>(g, wt, st, zt, xp, yp, b16, colscale, m, rows, cols, k_slices, s)
+  if (act_dtype == SQX_DTYPE_BF16) {
+    if (asym) { if (pbf) SQX_LIN(ActBF16, true, true); else SQX_LIN(ActBF16, true, false); }
+    else { if (pbf) SQX_LIN(ActBF16, false, true); else SQX_LIN(ActBF16, false, false); }
+  } else {
+    if (asym) { if (pbf) SQX_LIN(ActF16, true, true); else SQX_LIN(ActF16, true, false); }
+    else { if (pbf) SQX_LIN(ActF16, false, true); else SQX_LIN(ActF16, false, false); }
+  }
+#undef SQX_LIN
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
 }
 
 extern "C" int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
                                int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
                                int64_t group, int k_slices, sqx_stream_t stream) {
-  SQX_REQUIRE(m >= 0 && rows > 0 && cols > 0, SQX_E_ARG, "sqx_int4_linear: bad shape m=%lld rows=%lld cols=%lld",
-              (long long)m, (long long)rows, (long long)cols);
-  SQX_REQUIRE(group == 32 || group == 64 || group == 128, SQX_E_ARG,
-              "sqx_int4_linear: group_size %lld unsupported (32, 64 or 128)", (long long)group);
-  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld", (long long)cols,
-              (long long)group);
-  SQX_REQUIRE(act_dtype == SQX_DTYPE_BF16 || act_dtype == SQX_DTYPE_F16, SQX_E_ARG,
-              "sqx_int4_linear: activations must be BF16 or F16");
-  SQX_REQUIRE(param_dtype == SQX_DTYPE_F32 || param_dtype == SQX_DTYPE_BF16, SQX_E_ARG,
-              "sqx_int4_linear: param_dtype must be F32 or BF16");
-  SQX_REQUIRE(rows < ((int64_t)1 << 31) && cols < ((int64_t)1 << 31) && m < ((int64_t)1 << 31), SQX_E_ARG,
-              "sqx_int4_linear: shape too large");
-  SQX_REQUIRE(k_slices <= 16, SQX_E_ARG, "sqx_int4_linear: k_slices %d > 16", k_slices);
-  if (m == 0) return SQX_OK;
-  SQX_REQUIRE(wt && st && x && y, SQX_E_ARG, "sqx_int4_linear: null pointer");
-  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, SQX_E_ARG,
-              "sqx_int4_linear: wt and x must be 16-byte aligned");
-  const bool asym = zt != nullptr;
-  const int64_t T = ceil_div(rows, 16);
-  const int64_t KB = ceil_div(cols, 128);
-  SQX_REQUIRE(T <= 0x7fffffff && KB * 1024 < ((int64_t)1 << 31) && 64 * cols * 2 < ((int64_t)1 << 31), SQX_E_ARG,
-              "sqx_int4_linear: shape too large for 32-bit buffer offsets");
-  int nw = k_slices <= 0 ? sqx_int4_linear_default_kslices(m, rows, cols) : k_slices;
-  if (nw > KB) nw = static_cast<int>(KB);
-  const int kbw = static_cast<int>(ceil_div(KB, nw));
-  nw = static_cast<int>(ceil_div(KB, kbw));  // no idle waves
-  hipStream_t s = as_stream(stream);
-  const uint8_t* w4 = wt;
-  const uint16_t* b16 = static_cast<const uint16_t*>(bias);
-  const int pbf = param_dtype == SQX_DTYPE_BF16;
-  // x is processed in passes of up to 64 rows (4 MFMA row chunks per wave).
-  for (int64_t m0 = 0; m0 < m; m0 += 64) {
-    const int mm = static_cast<int>(m - m0 < 64 ? m - m0 : 64);
-    const int mch = linear_mch(mm);
-    const uint16_t* xp = static_cast<const uint16_t*>(x) + m0 * cols;
-    uint16_t* yp = static_cast<uint16_t*>(y) + m0 * rows;
-    const int M = mm, N = static_cast<int>(rows), K = static_cast<int>(cols);
-    const int iT = static_cast<int>(T), iKB = static_cast<int>(KB);
-    const int g = static_cast<int>(group);
-#define SQX_LIN(ACT, ASYM, PBF) \
-  launch_linear_a<ACT, ASYM, PBF>(g, mch, nw, s, w4, st, zt, xp, yp, b16, M, N, K, iT, iKB, kbw)
-    if (act_dtype == SQX_DTYPE_BF16) {
-      if (asym) { if (pbf) SQX_LIN(ActBF16, true, true); else SQX_LIN(ActBF16, true, false); }
-      else { if (pbf) SQX_LIN(ActBF16, false, true); else SQX_LIN(ActBF16, false, false); }
-    } else {
-      if (asym) { if (pbf) SQX_LIN(ActF16, true, true); else SQX_LIN(ActF16, true, false); }
-      else { if (pbf) SQX_LIN(ActF16, false, true); else SQX_LIN(ActF16, false, false); }
-    }
-#undef SQX_LIN
-    SQX_LAUNCH_CHECK("sqx_int4_linear");
-  }
-  return SQX_OK;
+  return int4_linear_impl(wt, st, zt, param_dtype, x, act_dtype, y, bias, nullptr, m, rows, cols, group, k_slices,
+                          stream, "sqx_int4_linear");
+}
+
+extern "C" int sqx_int4_linear_colscaled(const uint8_t* wt, const void* st, const void* zt, int param_dtype,
+                                         const void* x, int act_dtype, const float* col_scale, void* y,
+                                         const void* bias, int64_t m, int64_t rows, int64_t cols, int64_t group,
+                                         int k_slices, sqx_stream_t stream) {
+  SQX_REQUIRE(col_scale != nullptr, SQX_E_ARG, "sqx_int4_linear_colscaled: null col_scale");
+  return int4_linear_impl(wt, st, zt, param_dtype, x, act_dtype, y, bias, col_scale, m, rows, cols, group, k_slices,
+                          stream, "sqx_int4_linear_colscaled");
 }
