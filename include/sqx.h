@@ -198,6 +198,57 @@ int sqx_fp4_linear(const uint8_t* wt, const uint8_t* st, int fmt, const float* s
 int sqx_split_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, sqx_stream_t stream);
 int sqx_sum_halves(const float* y2, int64_t n, float* y, sqx_stream_t stream);
 
+/* ============================================================================================
+ * INT8 (src/scratch_llm/quant/int8.py). The input is viewed as [A, B, C] with B the kept axis of the
+ * reference's `axis` argument (A = product of the dims before it, C = product of those after it);
+ * axis=None is A = C = 1, B = 1 over all elements. Scales (and zero-points) have B elements in the
+ * input's dtype, and every intermediate is rounded to that dtype where torch rounds it, so codes and
+ * scales are bit-exact with the reference for fp32, bf16 and fp16 inputs.
+ * ============================================================================================ */
+
+/* Workspace bytes a per-tensor (B == 1) quantize needs. */
+int64_t sqx_int8_workspace_bytes(void);
+
+/* quantize_symmetric (int8.py:102-125): s = max(amax(|x|) / 127, eps), q = clamp(rint(x / s), +-127).
+ * x: A*B*C elements of dtype; q: int8, same count; s: B elements of dtype. */
+int sqx_int8_quantize_sym(const void* x, int dtype, int64_t A, int64_t B, int64_t C, float eps,
+                          int8_t* q, void* s, void* workspace, int64_t workspace_bytes,
+                          sqx_stream_t stream);
+
+/* quantize_affine (int8.py:142-172): lo = min(min(x), 0), hi = max(max(x), 0),
+ * s = max((hi - lo) / 255, eps), z = clamp(rint(-lo / s), 0, 255), q = clamp(rint(x / s + z), 0, 255).
+ * q: uint8; s, z: B elements of dtype. */
+int sqx_int8_quantize_affine(const void* x, int dtype, int64_t A, int64_t B, int64_t C, float eps,
+                             uint8_t* q, void* s, void* z, void* workspace, int64_t workspace_bytes,
+                             sqx_stream_t stream);
+
+/* dequantize_symmetric (int8.py:128-130): out = q * s; dequantize_affine (int8.py:175-177):
+ * out = (q - z) * s; in the scale dtype, with the [A, B, C] view of sqx_int8_quantize_*. */
+int sqx_int8_dequantize_sym(const int8_t* q, int64_t A, int64_t B, int64_t C, const void* s, int dtype,
+                            void* out, sqx_stream_t stream);
+int sqx_int8_dequantize_affine(const uint8_t* q, int64_t A, int64_t B, int64_t C, const void* s,
+                               const void* z, int dtype, void* out, sqx_stream_t stream);
+
+/* w8a8_linear's integer GEMM and epilogue (int8.py:189-213): y[m, n] = fp32(sum_k qx[m,k] * qw[n,k])
+ * * (sx[m] * sw[n]) with int32 accumulation (k <= 131072) and the scale product in the promoted
+ * dtype of the two scales. qx: int8 [m, k]; qw: int8 [n, k]; sx: [m], sw: [n]; y: fp32 [m, n]. */
+int sqx_w8a8_gemm(const int8_t* qx, const void* sx, int sx_dtype, const int8_t* qw, const void* sw,
+                  int sw_dtype, float* y, int64_t m, int64_t n, int64_t k, sqx_stream_t stream);
+
+/* Bytes of the tiled int8 weight (16-row x 64-column blocks of 1 KiB; no reference counterpart). */
+int64_t sqx_int8_tiled_weight_bytes(int64_t rows, int64_t cols);
+
+/* Re-lay symmetric int8 codes q [rows, cols] for sqx_int8_linear (no reference counterpart). */
+int sqx_int8_tile(const int8_t* q, int64_t rows, int64_t cols, uint8_t* wt, sqx_stream_t stream);
+
+/* Int8 weight-only linear, BASELINE config 1 (quantize_symmetric(W, axis=0) + dequantize_symmetric,
+ * int8.py:102-130, composed with F.linear): y[m, r] = scale[r] * sum_c x[m, c] * q[r, c] (+ bias[r]).
+ * x: [m, cols] BF16 or F16 (cols % 8 == 0); y: [m, rows] of act_dtype; scale: fp32 [rows]; bias:
+ * [rows] of act_dtype or NULL. fp32 accumulation; k_slices as sqx_int4_linear. */
+int sqx_int8_linear(const uint8_t* wt, const float* scale, const void* x, int act_dtype, void* y,
+                    const void* bias, int64_t m, int64_t rows, int64_t cols, int k_slices,
+                    sqx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

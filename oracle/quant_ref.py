@@ -214,48 +214,57 @@ def _reduce_keep(x: np.ndarray, axis, fn):
     return fn(x, axis=dims, keepdims=True)
 
 
-def quantize_symmetric(x, axis=None, eps: float = 1e-12):
-    """int8.py:101-124 — s = max(amax/127, eps) in x's dtype (fp32 here); q = clamp(rint(x/s), +-127)."""
-    xf = np.asarray(x, np.float32)
-    amax = _reduce_keep(np.abs(xf), axis, np.max)
-    s = np.asarray(amax / F32(_SYM_QMAX), np.float32)
-    s = np.where(s < F32(eps), F32(eps), s).astype(np.float32)
-    q = np.clip(np.rint(xf / s), -_SYM_QMAX, _SYM_QMAX).astype(np.int8)
-    return q, s
+def quantize_symmetric(x, axis=None, eps: float = 1e-12, dtype: str = "f32"):
+    """int8.py:102-125 — computed in x's dtype (``dtype`` 'f32', 'bf16' or 'f16'; x holds values of
+    that dtype): s = max(rd(amax / 127), rd(eps)), q = clamp(rint(rd(x / s)), -127, 127), where rd
+    rounds an fp32 result to the dtype exactly where torch does. axis = the kept dim (keepdim)."""
+    xf = round_to(np.asarray(x, np.float32), dtype)
+    amax = np.asarray(_reduce_keep(np.abs(xf), axis, np.max), np.float32)
+    s = round_to(amax / F32(_SYM_QMAX), dtype)
+    e = round_to(np.float32(eps), dtype)
+    s = np.where(s < e, e, s).astype(np.float32)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        q = np.clip(np.rint(round_to(xf / s, dtype)), -_SYM_QMAX, _SYM_QMAX)
+    return np.nan_to_num(q).astype(np.int8), s
 
 
-def dequantize_symmetric(q, s) -> np.ndarray:
-    """int8.py:127-129."""
-    return np.asarray(q).astype(np.float32) * np.asarray(s, np.float32)
+def dequantize_symmetric(q, s, dtype: str = "f32") -> np.ndarray:
+    """int8.py:127-129 — q.to(s.dtype) * s, rounded to the scale dtype."""
+    return round_to(np.asarray(q).astype(np.float32) * np.asarray(s, np.float32), dtype)
 
 
-def quantize_affine(x, axis=None, eps: float = 1e-12):
-    """int8.py:141-171 — range widened to include 0; s=(max-min)/255; z=clamp(rint(-min/s),0,255);
-    q = clamp(rint(x/s + z), 0, 255)."""
-    xf = np.asarray(x, np.float32)
-    xmin = np.minimum(_reduce_keep(xf, axis, np.min), F32(0))
-    xmax = np.maximum(_reduce_keep(xf, axis, np.max), F32(0))
-    s = np.asarray((xmax - xmin) / F32(_AFF_QMAX), np.float32)
-    s = np.where(s < F32(eps), F32(eps), s).astype(np.float32)
-    z = np.clip(np.rint(-xmin / s), 0, _AFF_QMAX).astype(np.float32)
-    q = np.clip(np.rint(xf / s + z), 0, _AFF_QMAX).astype(np.uint8)
-    return q, s, z
+def quantize_affine(x, axis=None, eps: float = 1e-12, dtype: str = "f32"):
+    """int8.py:141-171 — in x's dtype: lo = min(min(x), 0), hi = max(max(x), 0);
+    s = max(rd(rd(hi - lo) / 255), rd(eps)); z = clamp(rint(rd(-lo / s)), 0, 255);
+    q = clamp(rint(rd(rd(x / s) + z)), 0, 255)."""
+    xf = round_to(np.asarray(x, np.float32), dtype)
+    xmin = np.minimum(np.asarray(_reduce_keep(xf, axis, np.min), np.float32), F32(0))
+    xmax = np.maximum(np.asarray(_reduce_keep(xf, axis, np.max), np.float32), F32(0))
+    s = round_to(round_to(xmax - xmin, dtype) / F32(_AFF_QMAX), dtype)
+    e = round_to(np.float32(eps), dtype)
+    s = np.where(s < e, e, s).astype(np.float32)
+    z = np.clip(np.rint(round_to(-xmin / s, dtype)), 0, _AFF_QMAX).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        q = np.clip(np.rint(round_to(round_to(xf / s, dtype) + z, dtype)), 0, _AFF_QMAX)
+    return np.nan_to_num(q).astype(np.uint8), s, z
 
 
-def dequantize_affine(q, s, z) -> np.ndarray:
-    """int8.py:174-176."""
-    return (np.asarray(q).astype(np.float32) - np.asarray(z, np.float32)) * np.asarray(s, np.float32)
+def dequantize_affine(q, s, z, dtype: str = "f32") -> np.ndarray:
+    """int8.py:174-176 — (q.to(s.dtype) - z) * s, each step rounded to the scale dtype."""
+    qf = np.asarray(q).astype(np.float32)
+    return round_to(round_to(qf - np.asarray(z, np.float32), dtype) * np.asarray(s, np.float32), dtype)
 
 
-def w8a8_linear(x, w) -> np.ndarray:
-    """int8.py:188-213 — per-token int8 x, per-row int8 w, exact integer accumulate, fp32 epilogue."""
+def w8a8_linear(x, w, dtype: str = "f32") -> np.ndarray:
+    """int8.py:188-213 — per-token int8 x, per-row int8 w, exact integer accumulate, fp32 epilogue
+    acc.to(fp32) * (s_x * s_w) with the scale product in the scales' dtype."""
     xf = np.asarray(x, np.float32)
     k = xf.shape[-1]
     x2 = xf.reshape(-1, k)
-    qx, sx = quantize_symmetric(x2, axis=0)
-    qw, sw = quantize_symmetric(np.asarray(w, np.float32), axis=0)
+    qx, sx = quantize_symmetric(x2, axis=0, dtype=dtype)
+    qw, sw = quantize_symmetric(np.asarray(w, np.float32), axis=0, dtype=dtype)
     acc = qx.astype(np.int64) @ qw.astype(np.int64).T
-    y = acc.astype(np.float32) * (sx * sw.reshape(1, -1))
+    y = acc.astype(np.float32) * round_to(sx * sw.reshape(1, -1), dtype)
     return y.reshape(*xf.shape[:-1], np.asarray(w).shape[0])
 
 

@@ -72,6 +72,18 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "sqx_split_bf16": (_c_i, [_c_p, _c_i64, _c_p, _c_p, _c_p]),
     "sqx_sum_halves": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
+    "sqx_int8_workspace_bytes": (_c_i64, []),
+    "sqx_int8_quantize_sym": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_p, _c_p, _c_p, _c_i64, _c_p]),
+    "sqx_int8_quantize_affine": (
+        _c_i,
+        [_c_p, _c_i, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p],
+    ),
+    "sqx_int8_dequantize_sym": (_c_i, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i, _c_p, _c_p]),
+    "sqx_int8_dequantize_affine": (_c_i, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i, _c_p, _c_p]),
+    "sqx_w8a8_gemm": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_p]),
+    "sqx_int8_tiled_weight_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "sqx_int8_tile": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_int8_linear": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i, _c_p]),
 }
 
 _lock = threading.Lock()

@@ -298,6 +298,7 @@ __global__ __launch_bounds__(256) void fp4_tile_scales_kernel(const void* __rest
 // Lane group jg feeds MFMA step i the 8 columns 32*jg + 8i .. +7 of the block: dword i of its chunk.
 template <bool NV>
 struct WFp4 {
+  static constexpr int KBLK = 128, STEPS = 4;
   struct Args {
     const uint8_t* wt;
     const uint8_t* st;
@@ -355,7 +356,7 @@ struct WFp4 {
       for (int c = 0; c < MCH; ++c) yacc[c] = A::mfma(xv[c][i], b, yacc[c]);
     }
   }
-  __device__ static float out_scale(const Args& a) { return NV ? *a.s_global : 1.0f; }
+  __device__ static float out_scale(const Args& a, int) { return NV ? *a.s_global : 1.0f; }
 };
 
 template <class A, bool NV, bool YF32>

@@ -1,9 +1,11 @@
 // The decode linear shared by the weight formats (gfx950): y[m, n] = sum_k x[m, k] * W[n, k].
 //
-// Tiled weights: T = ceil(N/16) row tiles x KB = ceil(K/128) k-blocks; block (t, kb) is 1 KiB at
-// byte (t*KB + kb)*1024, and lane L of the consuming wave owns its 16 bytes at 16L. What those bytes
-// mean, and which per-block parameters go with them, is the weight format's policy W:
+// Tiled weights: T = ceil(N/16) row tiles x KB = ceil(K/W::KBLK) k-blocks; block (t, kb) is 1 KiB
+// at byte (t*KB + kb)*1024 and covers W::KBLK columns (128 for 4-bit codes, 64 for 8-bit), and lane
+// L of the consuming wave owns its 16 bytes at 16L. What those bytes mean, and which per-block
+// parameters go with them, is the weight format's policy W:
 //
+//   W::KBLK, W::STEPS              columns per block, MFMA steps (of 32 columns) per block
 //   W::Args                        device pointers and scalars of one tiled weight (kernel argument)
 //   W::Ctx  W::ctx(args, t, KB, lane)   per-wave buffer resources for tile t
 //   W::P                           the parameters of one block, held in registers
@@ -11,7 +13,7 @@
 //   W::xk(i, jg)                   column offset within the block of the 8 activations that lane group
 //                                  jg (= lane >> 4) feeds to MFMA step i (the B layout decides it)
 //   W::mma<A, MCH>(w, p, xv, yacc) the MFMAs of one block for MCH 16-row activation chunks
-//   W::out_scale(args)             factor applied to every output (1 unless the format has one)
+//   W::out_scale(args, n)          factor applied to output column n (weight row n)
 //
 // Structure (one workgroup per 16-row tile, all of K):
 //  * NW waves split the tile's k-blocks into contiguous slices (wave w owns [w*kbw, (w+1)*kbw));
@@ -32,14 +34,14 @@ namespace sqx {
 // from global memory.
 static constexpr int64_t kXldsMax = 64 * 1024;
 
-inline int64_t gemv_xlds_bytes(int64_t m, int64_t KB) { return m * (KB * 128 + 8) * 2; }
+inline int64_t gemv_xlds_bytes(int64_t m, int64_t KB, int kblk = 128) { return m * (KB * kblk + 8) * 2; }
 
 inline int gemv_mch(int64_t m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
 
 // Waves per tile the library picks: ~4096 waves on 256 CUs, 4..16 per tile, >= 2 blocks per wave.
-inline int gemv_default_kslices(int64_t rows, int64_t cols) {
+inline int gemv_default_kslices(int64_t rows, int64_t cols, int kblk = 128) {
   const int64_t T = ceil_div(rows, 16);
-  const int64_t KB = ceil_div(cols, 128);
+  const int64_t KB = ceil_div(cols, kblk);
   int64_t s = ceil_div(4096, T);
   if (s < 4) s = 4;
   if (s > 16) s = 16;
@@ -67,8 +69,10 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
 
   const typename W::Ctx wc = W::ctx(wa, t, KB, lane);
   const rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
+  constexpr int KBLK = W::KBLK;
+  constexpr int STEPS = W::STEPS;
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem + nw * MCH * 64);
-  const int xpitch = KB * 128 + 8;  // LDS row pitch in elements (16 bytes of padding per row)
+  const int xpitch = KB * KBLK + 8;  // LDS row pitch in elements (16 bytes of padding per row)
   uint32_t xvo[MCH];
   f32x4_t yacc[MCH];
 #pragma unroll
@@ -87,7 +91,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
   if (kb0 < kb1) load_round(kb0, w, p);
   // The first weight round is in flight while the activations are copied into LDS.
   if (XLDS) {
-    const int chunks_per_row = KB * 16;  // 16-byte chunks of a padded row
+    const int chunks_per_row = KB * KBLK / 8;  // 16-byte chunks of a padded row
     for (int idx = threadIdx.x; idx < M * chunks_per_row; idx += blockDim.x) {
       const int r = idx / chunks_per_row;
       const int col = (idx - r * chunks_per_row) * 8;
@@ -108,7 +112,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
   for (int kb = kb0; kb < kb1; kb += U) {
     // Global activation fragments of the whole round are requested ahead of the next round's weights:
     // buffer loads retire in issue order, so waiting for them leaves the next weights in flight.
-    u32x4_t xg[XLDS ? 1 : U][MCH][4];
+    u32x4_t xg[XLDS ? 1 : U][MCH][STEPS];
     if constexpr (!XLDS) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -116,8 +120,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
 #pragma unroll
           for (int c = 0; c < MCH; ++c) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              xg[u][c][i] = bload128(xr, xvo[c] + 2u * W::xk(i, jg), (uint32_t)((kb + u) * 128) * 2u);
+            for (int i = 0; i < STEPS; ++i)
+              xg[u][c][i] = bload128(xr, xvo[c] + 2u * W::xk(i, jg), (uint32_t)((kb + u) * KBLK) * 2u);
           }
         }
       }
@@ -129,21 +133,21 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     for (int u = 0; u < U; ++u) {
       if (kb + u < kb1) {  // wave-uniform
         const int kk = kb + u;
-        u32x4_t xv[MCH][4];
+        u32x4_t xv[MCH][STEPS];
 #pragma unroll
         for (int c = 0; c < MCH; ++c) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
+          for (int i = 0; i < STEPS; ++i) {
             if constexpr (XLDS)
-              xv[c][i] = *reinterpret_cast<const u32x4_t*>(xs + xvo[c] + kk * 128 + W::xk(i, jg));
+              xv[c][i] = *reinterpret_cast<const u32x4_t*>(xs + xvo[c] + kk * KBLK + W::xk(i, jg));
             else
               xv[c][i] = xg[u][c][i];
           }
         }
         if (KTAIL && !XLDS && kk == KB - 1) {  // activations at or beyond K must not enter the sums
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if (kk * 128 + W::xk(i, jg) >= K) {
+          for (int i = 0; i < STEPS; ++i) {
+            if (kk * KBLK + W::xk(i, jg) >= K) {
 #pragma unroll
               for (int c = 0; c < MCH; ++c) xv[c][i] = u32x4_t{0u, 0u, 0u, 0u};
             }
@@ -165,7 +169,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
   __syncthreads();
   constexpr int kOut = MCH * 64 * 4;
   const float* rf = reinterpret_cast<const float*>(red);
-  const float osc = W::out_scale(wa);
   for (int j = threadIdx.x; j < kOut; j += blockDim.x) {
     float v = 0.0f;
     for (int ww = 0; ww < nw; ++ww) v += rf[ww * kOut + j];
@@ -174,7 +177,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     const int m = c * 16 + 4 * (l >> 4) + (j & 3);
     const int n = t * 16 + (l & 15);
     if (m < M && n < N) {
-      v *= osc;
+      v *= W::out_scale(wa, n);
       if (bias) v += A::to_f32(bias[n]);
       if constexpr (YF32)
         static_cast<float*>(yv)[(int64_t)m * N + n] = v;
@@ -190,13 +193,14 @@ template <class A, class W, int U1, int U2, bool YF32>
 hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, const uint16_t* bias,
                        const float* colscale, int64_t m, int64_t rows, int64_t cols, int k_slices,
                        hipStream_t stream) {
+  constexpr int KBLK = W::KBLK;
   const int64_t T = ceil_div(rows, 16);
-  const int64_t KB = ceil_div(cols, 128);
-  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols) : k_slices;
+  const int64_t KB = ceil_div(cols, KBLK);
+  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols, KBLK) : k_slices;
   if (nw > KB) nw = static_cast<int>(KB);
   const int kbw = static_cast<int>(ceil_div(KB, nw));
   nw = static_cast<int>(ceil_div(KB, kbw));  // no idle waves
-  const bool ktail = cols % 128 != 0;
+  const bool ktail = cols % KBLK != 0;
   const dim3 grid(static_cast<unsigned>(T)), block(static_cast<unsigned>(64 * nw));
   for (int64_t m0 = 0; m0 < m; m0 += 64) {
     const int M = static_cast<int>(m - m0 < 64 ? m - m0 : 64);
@@ -205,13 +209,13 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     void* yp = static_cast<char*>(y) + m0 * rows * (YF32 ? 4 : 2);
     const int N = static_cast<int>(rows), K = static_cast<int>(cols), iKB = static_cast<int>(KB);
     const size_t red = static_cast<size_t>(nw) * mch * 64 * sizeof(f32x4_t);
-    const bool xlds = mch == 1 && gemv_xlds_bytes(M, KB) <= kXldsMax;
+    const bool xlds = mch == 1 && gemv_xlds_bytes(M, KB, KBLK) <= kXldsMax;
     if (colscale != nullptr && !xlds) return hipErrorNotSupported;  // column scaling happens in the LDS copy
 #define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_)                                                                    \
   hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32>), grid, block, LDS_, stream, wa, xp, yp, bias, \
                      colscale, M, N, K, iKB, kbw)
     if (xlds) {
-      const size_t lds = red + gemv_xlds_bytes(M, KB);
+      const size_t lds = red + gemv_xlds_bytes(M, KB, KBLK);
       if (ktail) SQX_GEMV(1, U1, true, true, lds); else SQX_GEMV(1, U1, false, true, lds);
     } else if (mch == 1) {
       if (ktail) SQX_GEMV(1, U1, true, false, red); else SQX_GEMV(1, U1, false, false, red);

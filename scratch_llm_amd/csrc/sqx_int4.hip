@@ -209,6 +209,7 @@ __device__ inline float load_param(rsrc_t r, uint32_t voff, uint32_t soff) {
 
 template <int GROUP, bool ASYM, bool PBF16>
 struct WInt4 {
+  static constexpr int KBLK = 128, STEPS = 4;
   static constexpr int NG = 128 / GROUP;  // groups per block
   static constexpr int MPG = 4 / NG;      // MFMA steps (of 32 columns) per group
   static constexpr int PB = PBF16 ? 2 : 4;
@@ -272,7 +273,7 @@ struct WInt4 {
       }
     }
   }
-  __device__ static float out_scale(const Args&) { return 1.0f; }
+  __device__ static float out_scale(const Args&, int) { return 1.0f; }
 };
 
 template <class A, int GROUP, bool ASYM, bool PBF16>
