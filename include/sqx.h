@@ -112,6 +112,43 @@ int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt, int param
                     const void* x, int act_dtype, void* y, const void* bias, int64_t m, int64_t rows,
                     int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
 
+/* Build-defined asymmetric uint4, group-wise (BASELINE config 2's "asymmetric, bf16 scale/zero";
+ * no reference symbol: the 4-bit form of quantize_affine, int8.py:142-172, per group):
+ * lo = min(min(w_g), 0), hi = max(max(w_g), 0), s = max((hi - lo) / 15, 1e-12) (rounded to bf16 first
+ * when param_dtype is BF16), z = clamp(rint(-lo / s), 0, 15), q = clamp(rint(w / s + z), 0, 15).
+ * q: uint8 [rows, cols]; scales, zeros: [rows, cols/group] of param_dtype (F32 or BF16). */
+int sqx_int4_quantize_asym(const void* w, int w_dtype, int64_t rows, int64_t cols, int64_t group,
+                           int param_dtype, uint8_t* q, void* scales, void* zeros, sqx_stream_t stream);
+
+/* ============================================================================================
+ * AWQ (src/scratch_llm/quant/awq.py)
+ * ============================================================================================ */
+
+/* quantize_awq_int4 with a channel scale (awq.py:154-175): the group-int4 codes and scales of the fp32
+ * product w * chan_scale[col] (quantize_groupwise_int4 of W * s). Bit-exact. */
+int sqx_awq_quantize(const void* w, int w_dtype, const float* chan_scale, int64_t rows, int64_t cols,
+                     int64_t group, int8_t* q, float* scales, sqx_stream_t stream);
+
+/* _awq_dequant_weight (awq.py:115-119): w_eff = dequant(quantize(W * s)) / s, fp32 [rows, cols]. */
+int sqx_awq_fake_quant(const void* w, int w_dtype, const float* chan_scale, int64_t rows, int64_t cols,
+                       int64_t group, float* w_eff, sqx_stream_t stream);
+
+/* awq_dequantize (awq.py:178-181): out = q * group_scale / chan_scale[col], fp32 [rows, cols]. */
+int sqx_awq_dequantize(const int8_t* q, const float* group_scales, const float* chan_scale, int64_t rows,
+                       int64_t cols, int64_t group, float* out, sqx_stream_t stream);
+
+/* act_scale (awq.py:94-101): out[c] = mean_r |x[r, c]| (fp64 accumulation, one rounding to fp32). */
+int sqx_col_absmean(const void* x, int dtype, int64_t rows, int64_t cols, float* out, sqx_stream_t stream);
+
+/* The channel scale of one AWQ grid point (awq.py:104-112, 141-142):
+ * s = max(act ** ratio, 1e-4); out = s / sqrt(max(s) * min(s)). act, out: fp32 [n]. */
+int sqx_awq_scale(const float* act, int64_t n, float ratio, float* out, sqx_stream_t stream);
+
+/* out[r, c] = x[r, c] / s[c] rounded to act_dtype (BF16 or F16): the activations of the AWQ linear,
+ * which folds 1/s into x (awq.py:15-16). */
+int sqx_scale_columns(const void* x, int act_dtype, const float* s, int64_t rows, int64_t cols, void* out,
+                      sqx_stream_t stream);
+
 /* AWQ linear (awq_linear, awq.py:184-192): the W4A16 linear of the codes of W*s with the per-input
  * channel AWQ scale s folded into the activations, y = (x / s) @ (q*gs)^T; x / s is computed in fp32
  * per element and rounded to act_dtype while the workgroup copies x into LDS. col_scale: fp32 [cols].

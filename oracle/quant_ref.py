@@ -171,8 +171,10 @@ def mse(ref, approx) -> float:
 # ------------------------------------------------------------------------------------------------
 def quantize_groupwise_uint4_asym(w, group_size: int = GROUP_SIZE, param: str = "bf16"):
     """Per group: lo = min(min(w), 0), hi = max(max(w), 0); s = max((hi-lo)/15, 1e-12);
-    z = clamp(rint(-lo/s), 0, 15); q = clamp(rint(w/s + z), 0, 15). With ``param='bf16'`` the scale
-    is rounded to bf16 *before* codes are computed, so the stored (s, z) reproduce the codes."""
+    z = clamp(rint(-lo/s), 0, 15) (a zero zero-point is +0); q = clamp(rint(w/s + z), 0, 15). With
+    ``param='bf16'`` the scale is rounded to bf16 *before* codes are computed, so the stored (s, z)
+    reproduce the codes. Pinned by its invariants (zero exact, error <= s/2 in range), not by any
+    reference symbol."""
     w = np.asarray(w)
     rows, cols = w.shape
     if cols % group_size != 0:
@@ -185,7 +187,7 @@ def quantize_groupwise_uint4_asym(w, group_size: int = GROUP_SIZE, param: str = 
     s = np.where(s < F32(1e-12), F32(1e-12), s).astype(np.float32)
     if param == "bf16":
         s = round_bf16(s)
-    z = np.clip(np.rint(-lo / s), 0, 15).astype(np.float32)
+    z = (np.clip(np.rint(-lo / s), 0, 15) + F32(0)).astype(np.float32)  # +0, never -0, for zero groups
     q = np.clip(np.rint(wf / s + z), 0, 15).astype(np.int8)
     return q.reshape(rows, cols), s.reshape(rows, g), z.reshape(rows, g)
 

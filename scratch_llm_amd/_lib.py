@@ -84,6 +84,13 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sqx_int8_tiled_weight_bytes": (_c_i64, [_c_i64, _c_i64]),
     "sqx_int8_tile": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_int8_linear": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i, _c_p]),
+    "sqx_int4_quantize_asym": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_i64, _c_i, _c_p, _c_p, _c_p, _c_p]),
+    "sqx_awq_quantize": (_c_i, [_c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "sqx_awq_fake_quant": (_c_i, [_c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_awq_dequantize": (_c_i, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_col_absmean": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_awq_scale": (_c_i, [_c_p, _c_i64, ctypes.c_float, _c_p, _c_p]),
+    "sqx_scale_columns": (_c_i, [_c_p, _c_i, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
 }
 
 _lock = threading.Lock()

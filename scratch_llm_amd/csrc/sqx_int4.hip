@@ -36,20 +36,26 @@ namespace sqx {
 // ----------------------------------------------------------------------------------------------
 // Fast path: group is a power of two in [8, 512]; each lane owns 8 consecutive elements, the
 // group's lanes are consecutive in the wave, and the absmax is reduced with xor shuffles.
-template <int LPG>
+// COLMUL: the weight is first multiplied by a per-column fp32 scale (AWQ's W * s, awq.py:173, one
+// fp32 rounding). FAKE: instead of codes and scales, write the AWQ effective weight
+// dequant(q, s_g) / s (awq.py:115-119) in fp32.
+template <int LPG, bool COLMUL, bool FAKE>
 __global__ __launch_bounds__(256) void int4_quantize_sym_kernel(const void* __restrict__ w, int w_dtype,
-                                                                int64_t n_elems, int64_t group,
-                                                                int8_t* __restrict__ q,
-                                                                float* __restrict__ scales) {
+                                                                int64_t n_elems, int64_t cols, int64_t group,
+                                                                const float* __restrict__ colmul,
+                                                                int8_t* __restrict__ q, float* __restrict__ scales,
+                                                                float* __restrict__ weff) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t e0 = i * 8;
   const bool live = e0 < n_elems;
+  const int64_t c0 = COLMUL ? e0 % cols : 0;
   float v[8];
   float amax = 0.0f;
   bool nan = false;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     v[e] = live ? load_as_f32(w, w_dtype, e0 + e) : 0.0f;
+    if (COLMUL && live) v[e] = v[e] * colmul[c0 + e];
     float a = fabsf(v[e]);
     nan |= (a != a);
     amax = fmaxf(amax, a);
@@ -69,35 +75,137 @@ __global__ __launch_bounds__(256) void int4_quantize_sym_kernel(const void* __re
     float r = __builtin_rintf(__fdiv_rn(v[e], s));  // round half to even, like torch.round
     r = fminf(fmaxf(r, -8.0f), 7.0f);
     int8_t c = (r == r) ? static_cast<int8_t>(r) : 0;  // NaN codes are unspecified upstream
+    if (FAKE) weff[e0 + e] = __fdiv_rn(static_cast<float>(c) * s, colmul[c0 + e]);
     packed |= static_cast<uint64_t>(static_cast<uint8_t>(c)) << (8 * e);
   }
-  *reinterpret_cast<uint64_t*>(q + e0) = packed;
-  if ((threadIdx.x & (LPG - 1)) == 0) scales[e0 / group] = s;
+  if (!FAKE) {
+    *reinterpret_cast<uint64_t*>(q + e0) = packed;
+    if ((threadIdx.x & (LPG - 1)) == 0) scales[e0 / group] = s;
+  }
 }
 
-// Generic path: any group size; one thread per group.
+// Generic path: any group size; one thread per group (COLMUL / FAKE as above).
+template <bool COLMUL, bool FAKE>
 __global__ __launch_bounds__(256) void int4_quantize_sym_generic_kernel(const void* __restrict__ w, int w_dtype,
-                                                                        int64_t n_groups, int64_t group,
+                                                                        int64_t n_groups, int64_t cols, int64_t group,
+                                                                        const float* __restrict__ colmul,
                                                                         int8_t* __restrict__ q,
-                                                                        float* __restrict__ scales) {
+                                                                        float* __restrict__ scales,
+                                                                        float* __restrict__ weff) {
   const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= n_groups) return;
   const int64_t base = g * group;
+  const int64_t c0 = COLMUL ? base % cols : 0;
+  auto val = [&](int64_t e) {
+    const float v = load_as_f32(w, w_dtype, base + e);
+    return COLMUL ? v * colmul[c0 + e] : v;
+  };
   float amax = 0.0f;
   bool nan = false;
   for (int64_t e = 0; e < group; ++e) {
-    float a = fabsf(load_as_f32(w, w_dtype, base + e));
+    float a = fabsf(val(e));
     nan |= (a != a);
     amax = fmaxf(amax, a);
   }
   float s = nan ? __builtin_nanf("") : __fdiv_rn(amax, 7.0f);
   if (s < FLT_MIN) s = FLT_MIN;
   for (int64_t e = 0; e < group; ++e) {
-    float r = __builtin_rintf(__fdiv_rn(load_as_f32(w, w_dtype, base + e), s));
+    float r = __builtin_rintf(__fdiv_rn(val(e), s));
     r = fminf(fmaxf(r, -8.0f), 7.0f);
-    q[base + e] = (r == r) ? static_cast<int8_t>(r) : 0;
+    const int8_t c = (r == r) ? static_cast<int8_t>(r) : 0;
+    if (FAKE) weff[base + e] = __fdiv_rn(static_cast<float>(c) * s, colmul[c0 + e]);
+    else q[base + e] = c;
   }
-  scales[g] = s;
+  if (!FAKE) scales[g] = s;
+}
+
+// Build-defined asymmetric uint4 (no reference symbol; the 4-bit form of quantize_affine,
+// int8.py:142-172, per group): lo = min(min(w), 0), hi = max(max(w), 0), s = max((hi - lo) / 15,
+// 1e-12) (rounded to bf16 first when the parameters are stored as bf16), z = clamp(rint(-lo / s),
+// 0, 15), q = clamp(rint(w / s + z), 0, 15). One thread per group.
+template <bool PBF16>
+__global__ __launch_bounds__(256) void int4_quantize_asym_kernel(const void* __restrict__ w, int w_dtype,
+                                                                 int64_t n_groups, int64_t group,
+                                                                 uint8_t* __restrict__ q, void* __restrict__ scales,
+                                                                 void* __restrict__ zeros) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= n_groups) return;
+  const int64_t base = g * group;
+  float lo = 0.0f, hi = 0.0f;
+  for (int64_t e = 0; e < group; ++e) {
+    const float v = load_as_f32(w, w_dtype, base + e);
+    lo = (v < lo || v != v) ? v : lo;
+    hi = (v > hi || v != v) ? v : hi;
+  }
+  float s = __fdiv_rn(hi - lo, 15.0f);
+  if (s < 1e-12f) s = 1e-12f;
+  if (PBF16) s = bf16_bits_to_f32(f32_to_bf16_bits(s));
+  const float z = fminf(fmaxf(__builtin_rintf(__fdiv_rn(-lo, s)), 0.0f), 15.0f);
+  for (int64_t e = 0; e < group; ++e) {
+    const float r = fminf(fmaxf(__builtin_rintf(__fdiv_rn(load_as_f32(w, w_dtype, base + e), s) + z), 0.0f), 15.0f);
+    q[base + e] = static_cast<uint8_t>(r == r ? r : 0.0f);
+  }
+  if (PBF16) {
+    static_cast<uint16_t*>(scales)[g] = f32_to_bf16_bits(s);
+    static_cast<uint16_t*>(zeros)[g] = f32_to_bf16_bits(z);
+  } else {
+    static_cast<float*>(scales)[g] = s;
+    static_cast<float*>(zeros)[g] = z;
+  }
+}
+
+// awq_dequantize (awq.py:178-181): dequant(q, s_g) / s per column, fp32.
+__global__ __launch_bounds__(256) void awq_dequantize_kernel(const int8_t* __restrict__ q, const float* __restrict__ gs,
+                                                             const float* __restrict__ cs, int64_t n_elems,
+                                                             int64_t cols, int64_t group, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_elems) return;
+  out[i] = __fdiv_rn(static_cast<float>(q[i]) * gs[i / group], cs[i % cols]);
+}
+
+// act_scale (awq.py:94-101): mean over rows of |x| per column, accumulated in fp64 and rounded once.
+__global__ __launch_bounds__(256) void col_absmean_kernel(const void* __restrict__ x, int dtype, int64_t rows,
+                                                          int64_t cols, float* __restrict__ out) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= cols) return;
+  double acc = 0.0;
+  for (int64_t r = 0; r < rows; ++r) acc += fabs(static_cast<double>(load_as_f32(x, dtype, r * cols + c)));
+  out[c] = static_cast<float>(acc / static_cast<double>(rows));
+}
+
+// The AWQ channel scale for grid exponent `ratio` (awq.py:104-112, 141-142):
+// s = max(a ** ratio, 1e-4); s / sqrt(max(s) * min(s)). One workgroup.
+__global__ __launch_bounds__(1024) void awq_scale_kernel(const float* __restrict__ a, int64_t n, float ratio,
+                                                         float* __restrict__ out) {
+  __shared__ float rmax[1024], rmin[1024];
+  float mx = -INFINITY, mn = INFINITY;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    float v = ratio == 0.0f ? 1.0f : (ratio == 1.0f ? a[i] : powf(a[i], ratio));
+    if (v < 1e-4f) v = 1e-4f;
+    out[i] = v;
+    mx = fmaxf(mx, v);
+    mn = fminf(mn, v);
+  }
+  rmax[threadIdx.x] = mx;
+  rmin[threadIdx.x] = mn;
+  __syncthreads();
+  for (int s = 512; s > 0; s >>= 1) {
+    if (threadIdx.x < s) {
+      rmax[threadIdx.x] = fmaxf(rmax[threadIdx.x], rmax[threadIdx.x + s]);
+      rmin[threadIdx.x] = fminf(rmin[threadIdx.x], rmin[threadIdx.x + s]);
+    }
+    __syncthreads();
+  }
+  const float norm = sqrtf(rmax[0] * rmin[0]);
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = __fdiv_rn(out[i], norm);
+}
+
+// x / s per column, rounded back to the activation dtype (the AWQ linear folds 1/s into x).
+template <class A>
+__global__ __launch_bounds__(256) void scale_columns_kernel(const uint16_t* __restrict__ x, const float* __restrict__ s,
+                                                            int64_t n, int64_t cols, uint16_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = A::from_f32(__fdiv_rn(A::to_f32(x[i]), s[i % cols]));
 }
 
 // ----------------------------------------------------------------------------------------------
@@ -303,33 +411,132 @@ using namespace sqx;
 // ==============================================================================================
 static bool is_float_dtype(int d) { return d == SQX_DTYPE_F32 || d == SQX_DTYPE_BF16 || d == SQX_DTYPE_F16; }
 
-extern "C" int sqx_int4_quantize_sym(const void* w, int w_dtype, int64_t rows, int64_t cols, int64_t group,
-                                     int8_t* q, float* scales, sqx_stream_t stream) {
-  SQX_REQUIRE(w && q && scales, SQX_E_ARG, "sqx_int4_quantize_sym: null pointer");
-  SQX_REQUIRE(is_float_dtype(w_dtype), SQX_E_ARG, "sqx_int4_quantize_sym: unsupported w_dtype %d", w_dtype);
-  SQX_REQUIRE(rows >= 0 && cols >= 0 && group > 0, SQX_E_ARG, "sqx_int4_quantize_sym: bad shape");
-  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld",
-              (long long)cols, (long long)group);
+static int int4_quantize_impl(const void* w, int w_dtype, int64_t rows, int64_t cols, int64_t group,
+                              const float* colmul, int8_t* q, float* scales, float* weff, sqx_stream_t stream,
+                              const char* fn) {
+  SQX_REQUIRE(w && (weff || (q && scales)), SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(is_float_dtype(w_dtype), SQX_E_ARG, "%s: unsupported w_dtype %d", fn, w_dtype);
+  SQX_REQUIRE(rows >= 0 && cols >= 0 && group > 0, SQX_E_ARG, "%s: bad shape", fn);
+  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld", (long long)cols,
+              (long long)group);
   const int64_t n = rows * cols;
   if (n == 0) return SQX_OK;
   hipStream_t s = as_stream(stream);
   const bool fast = group >= 8 && group <= 512 && (group & (group - 1)) == 0 &&
-                    (reinterpret_cast<uintptr_t>(q) % 8 == 0);
+                    (weff != nullptr || reinterpret_cast<uintptr_t>(q) % 8 == 0);
+  const bool cm = colmul != nullptr;
+  const bool fk = weff != nullptr;
   if (fast) {
-    const int64_t threads = n / 8;
-    const dim3 grid(static_cast<unsigned>(ceil_div(threads, 256)));
-    switch (group / 8) {
+    const dim3 grid(static_cast<unsigned>(ceil_div(n / 8, 256)));
+#define SQX_Q_LAUNCH(L, CM, FK) \
+  hipLaunchKernelGGL((int4_quantize_sym_kernel<L, CM, FK>), grid, dim3(256), 0, s, w, w_dtype, n, cols, group, colmul, q, scales, weff)
 #define SQX_Q_CASE(L) \
-  case L: hipLaunchKernelGGL(int4_quantize_sym_kernel<L>, grid, dim3(256), 0, s, w, w_dtype, n, group, q, scales); break;
-      SQX_Q_CASE(1) SQX_Q_CASE(2) SQX_Q_CASE(4) SQX_Q_CASE(8) SQX_Q_CASE(16) SQX_Q_CASE(32) SQX_Q_CASE(64)
+  case L: if (fk) SQX_Q_LAUNCH(L, true, true); else if (cm) SQX_Q_LAUNCH(L, true, false); else SQX_Q_LAUNCH(L, false, false); break;
+    switch (group / 8) { SQX_Q_CASE(1) SQX_Q_CASE(2) SQX_Q_CASE(4) SQX_Q_CASE(8) SQX_Q_CASE(16) SQX_Q_CASE(32) SQX_Q_CASE(64) }
 #undef SQX_Q_CASE
-    }
+#undef SQX_Q_LAUNCH
   } else {
     const int64_t ng = n / group;
-    hipLaunchKernelGGL(int4_quantize_sym_generic_kernel, dim3(static_cast<unsigned>(ceil_div(ng, 256))), dim3(256),
-                       0, s, w, w_dtype, ng, group, q, scales);
+    const dim3 grid(static_cast<unsigned>(ceil_div(ng, 256)));
+    if (fk)
+      hipLaunchKernelGGL((int4_quantize_sym_generic_kernel<true, true>), grid, dim3(256), 0, s, w, w_dtype, ng, cols,
+                         group, colmul, q, scales, weff);
+    else if (cm)
+      hipLaunchKernelGGL((int4_quantize_sym_generic_kernel<true, false>), grid, dim3(256), 0, s, w, w_dtype, ng, cols,
+                         group, colmul, q, scales, weff);
+    else
+      hipLaunchKernelGGL((int4_quantize_sym_generic_kernel<false, false>), grid, dim3(256), 0, s, w, w_dtype, ng, cols,
+                         group, colmul, q, scales, weff);
   }
-  SQX_LAUNCH_CHECK("sqx_int4_quantize_sym");
+  SQX_LAUNCH_CHECK(fn);
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_quantize_sym(const void* w, int w_dtype, int64_t rows, int64_t cols, int64_t group,
+                                     int8_t* q, float* scales, sqx_stream_t stream) {
+  return int4_quantize_impl(w, w_dtype, rows, cols, group, nullptr, q, scales, nullptr, stream,
+                            "sqx_int4_quantize_sym");
+}
+
+extern "C" int sqx_awq_quantize(const void* w, int w_dtype, const float* chan_scale, int64_t rows, int64_t cols,
+                                int64_t group, int8_t* q, float* scales, sqx_stream_t stream) {
+  SQX_REQUIRE(chan_scale, SQX_E_ARG, "sqx_awq_quantize: null chan_scale");
+  return int4_quantize_impl(w, w_dtype, rows, cols, group, chan_scale, q, scales, nullptr, stream, "sqx_awq_quantize");
+}
+
+extern "C" int sqx_awq_fake_quant(const void* w, int w_dtype, const float* chan_scale, int64_t rows, int64_t cols,
+                                  int64_t group, float* w_eff, sqx_stream_t stream) {
+  SQX_REQUIRE(chan_scale && w_eff, SQX_E_ARG, "sqx_awq_fake_quant: null pointer");
+  return int4_quantize_impl(w, w_dtype, rows, cols, group, chan_scale, nullptr, nullptr, w_eff, stream,
+                            "sqx_awq_fake_quant");
+}
+
+extern "C" int sqx_awq_dequantize(const int8_t* q, const float* group_scales, const float* chan_scale, int64_t rows,
+                                  int64_t cols, int64_t group, float* out, sqx_stream_t stream) {
+  SQX_REQUIRE(rows >= 0 && cols > 0 && group > 0 && cols % group == 0, SQX_E_ARG, "sqx_awq_dequantize: bad shape");
+  const int64_t n = rows * cols;
+  if (n == 0) return SQX_OK;
+  SQX_REQUIRE(q && group_scales && chan_scale && out, SQX_E_ARG, "sqx_awq_dequantize: null pointer");
+  hipLaunchKernelGGL(awq_dequantize_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0,
+                     as_stream(stream), q, group_scales, chan_scale, n, cols, group, out);
+  SQX_LAUNCH_CHECK("sqx_awq_dequantize");
+  return SQX_OK;
+}
+
+extern "C" int sqx_col_absmean(const void* x, int dtype, int64_t rows, int64_t cols, float* out, sqx_stream_t stream) {
+  SQX_REQUIRE(is_float_dtype(dtype) && rows > 0 && cols >= 0, SQX_E_ARG, "sqx_col_absmean: bad dtype or shape");
+  if (cols == 0) return SQX_OK;
+  SQX_REQUIRE(x && out, SQX_E_ARG, "sqx_col_absmean: null pointer");
+  hipLaunchKernelGGL(col_absmean_kernel, dim3(static_cast<unsigned>(ceil_div(cols, 256))), dim3(256), 0,
+                     as_stream(stream), x, dtype, rows, cols, out);
+  SQX_LAUNCH_CHECK("sqx_col_absmean");
+  return SQX_OK;
+}
+
+extern "C" int sqx_awq_scale(const float* act, int64_t n, float ratio, float* out, sqx_stream_t stream) {
+  SQX_REQUIRE(n > 0 && act && out, SQX_E_ARG, "sqx_awq_scale: bad arguments");
+  hipLaunchKernelGGL(awq_scale_kernel, dim3(1), dim3(1024), 0, as_stream(stream), act, n, ratio, out);
+  SQX_LAUNCH_CHECK("sqx_awq_scale");
+  return SQX_OK;
+}
+
+extern "C" int sqx_scale_columns(const void* x, int act_dtype, const float* s, int64_t rows, int64_t cols, void* out,
+                                 sqx_stream_t stream) {
+  SQX_REQUIRE(act_dtype == SQX_DTYPE_BF16 || act_dtype == SQX_DTYPE_F16, SQX_E_ARG,
+              "sqx_scale_columns: activations must be BF16 or F16");
+  const int64_t n = rows * cols;
+  if (n == 0) return SQX_OK;
+  SQX_REQUIRE(x && s && out && cols > 0, SQX_E_ARG, "sqx_scale_columns: bad arguments");
+  const dim3 grid(static_cast<unsigned>(ceil_div(n, 256)));
+  if (act_dtype == SQX_DTYPE_BF16)
+    hipLaunchKernelGGL(scale_columns_kernel<ActBF16>, grid, dim3(256), 0, as_stream(stream),
+                       static_cast<const uint16_t*>(x), s, n, cols, static_cast<uint16_t*>(out));
+  else
+    hipLaunchKernelGGL(scale_columns_kernel<ActF16>, grid, dim3(256), 0, as_stream(stream),
+                       static_cast<const uint16_t*>(x), s, n, cols, static_cast<uint16_t*>(out));
+  SQX_LAUNCH_CHECK("sqx_scale_columns");
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_quantize_asym(const void* w, int w_dtype, int64_t rows, int64_t cols, int64_t group,
+                                      int param_dtype, uint8_t* q, void* scales, void* zeros, sqx_stream_t stream) {
+  SQX_REQUIRE(is_float_dtype(w_dtype), SQX_E_ARG, "sqx_int4_quantize_asym: unsupported w_dtype %d", w_dtype);
+  SQX_REQUIRE(param_dtype == SQX_DTYPE_F32 || param_dtype == SQX_DTYPE_BF16, SQX_E_ARG,
+              "sqx_int4_quantize_asym: param_dtype must be F32 or BF16");
+  SQX_REQUIRE(rows >= 0 && cols >= 0 && group > 0, SQX_E_ARG, "sqx_int4_quantize_asym: bad shape");
+  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld", (long long)cols,
+              (long long)group);
+  const int64_t ng = rows * cols / group;
+  if (ng == 0) return SQX_OK;
+  SQX_REQUIRE(w && q && scales && zeros, SQX_E_ARG, "sqx_int4_quantize_asym: null pointer");
+  const dim3 grid(static_cast<unsigned>(ceil_div(ng, 256)));
+  if (param_dtype == SQX_DTYPE_BF16)
+    hipLaunchKernelGGL(int4_quantize_asym_kernel<true>, grid, dim3(256), 0, as_stream(stream), w, w_dtype, ng, group, q,
+                       scales, zeros);
+  else
+    hipLaunchKernelGGL(int4_quantize_asym_kernel<false>, grid, dim3(256), 0, as_stream(stream), w, w_dtype, ng, group,
+                       q, scales, zeros);
+  SQX_LAUNCH_CHECK("sqx_int4_quantize_asym");
   return SQX_OK;
 }
 

@@ -31,6 +31,7 @@ __all__ = [
     "mse",
     "pack_int4",
     "quantize_groupwise_int4",
+    "quantize_groupwise_uint4_asym",
     "sqnr_db",
     "tile_int4",
     "tile_int4_packed",
@@ -108,6 +109,35 @@ def quantize_groupwise_int4(w: Tensor, group_size: int = GROUP_SIZE) -> tuple[Te
         )
     _lib.check(rc, "quantize_groupwise_int4")
     return q, scales
+
+
+def quantize_groupwise_uint4_asym(
+    w: Tensor, group_size: int = GROUP_SIZE, param_dtype: torch.dtype = torch.bfloat16
+) -> tuple[Tensor, Tensor, Tensor]:
+    """Asymmetric group-wise uint4 (BASELINE config 2's format; no reference symbol — the 4-bit form
+    of ``quantize_affine``, int8.py:142-172, per group of ``group_size`` input columns):
+    ``lo = min(min(w), 0)``, ``hi = max(max(w), 0)``, ``s = max((hi - lo) / 15, 1e-12)`` rounded to
+    ``param_dtype``, ``z = clamp(rint(-lo / s), 0, 15)``, ``q = clamp(rint(w / s + z), 0, 15)``.
+    Returns ``(q uint8 [out, in], scales, zeros [out, in // group_size] of param_dtype)``; the
+    dequantized weight is ``(q - z) * s``."""
+    if w.dim() != 2:
+        raise ValueError(f"expected a 2-D weight, got shape {tuple(w.shape)}")
+    rows, cols = w.shape
+    if cols % group_size != 0:
+        raise ValueError(f"in_features={cols} not divisible by group_size={group_size}")
+    if param_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"param_dtype must be float32 or bfloat16, got {param_dtype}")
+    dev = _lib.require_device(w, fn="quantize_groupwise_uint4_asym")
+    wc = w.contiguous() if w.dtype in (torch.float32, torch.bfloat16, torch.float16) else w.float().contiguous()
+    q = torch.empty(rows, cols, dtype=torch.uint8, device=dev)
+    s = torch.empty(rows, cols // group_size, dtype=param_dtype, device=dev)
+    z = torch.empty(rows, cols // group_size, dtype=param_dtype, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().sqx_int4_quantize_asym(wc.data_ptr(), _lib.sqx_dtype(wc.dtype), rows, cols, group_size,
+                                                      _lib.sqx_dtype(param_dtype), q.data_ptr(), s.data_ptr(),
+                                                      z.data_ptr(), _lib.stream_ptr(dev)),
+                   "quantize_groupwise_uint4_asym")
+    return q, s, z
 
 
 def dequantize_groupwise_int4(q: Tensor, scales: Tensor, group_size: int = GROUP_SIZE) -> Tensor:

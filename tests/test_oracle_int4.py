@@ -162,3 +162,26 @@ def test_asym_uint4_roundtrip_properties():
     # true zeros reconstruct exactly because z is an integer code (int8.py:142-172 invariant)
     zero_mask = w == 0.0
     assert np.all(wd[zero_mask] == 0.0)
+
+
+def test_uint4_asym_invariants():
+    """The build-defined asymmetric format has no reference symbol; its oracle is pinned by the
+    invariants of an affine quantizer (int8.py:142-172 at 4 bits): real zero reconstructs exactly,
+    codes stay in [0, 15], the zero-point is an integer in [0, 15], and every value reconstructs within
+    one step s: half a step of rounding, plus up to half a step where the rounded zero-point shifts
+    the grid and the top of the range clips (and the bf16 scale may sit 2**-9 below (hi - lo)/15)."""
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((64, 512)) * 0.05 + 0.01).astype(np.float32)
+    w[0, :128] = np.abs(w[0, :128])
+    w[1, :128] = 0.0
+    w[2, 5] = 0.0
+    for param in ("f32", "bf16"):
+        q, s, z = R.quantize_groupwise_uint4_asym(w, 128, param=param)
+        d = R.dequantize_groupwise_uint4_asym(q, s, z)
+        assert q.min() >= 0 and q.max() <= 15
+        assert np.all(z == np.rint(z)) and z.min() >= 0 and z.max() <= 15 and not np.signbit(z).any()
+        assert np.all(d[w == 0] == 0)
+        step = np.repeat(s, 128, axis=1)
+        assert np.all(np.abs(d - w) <= step * (1 + 2.0**-7))
+        inner = (w > -6 * step) & (w < 6 * step)  # well inside the range: rounding error only
+        assert np.all(np.abs(d - w)[inner] <= step[inner] / 2 * (1 + 1e-6))
