@@ -230,6 +230,23 @@ int sqx_fp4_linear(const uint8_t* wt, const uint8_t* st, int fmt, const float* s
                    int act_dtype, void* y, int y_dtype, const void* bias, int64_t m, int64_t rows,
                    int64_t cols, int k_slices, sqx_stream_t stream);
 
+/* mxfp4_quantize (nvfp4_mxfp4.py:257-265, block 32) of each row of x [m, k] (k a multiple of 32, so
+ * every block lies in one row), written in the tiled FP4 layout sqx_fp4_tile produces: xt
+ * (sqx_fp4_tiled_weight_bytes(m, k) bytes) and E8M0 scale bytes xst (sqx_fp4_tiled_scale_bytes(m, k,
+ * SQX_FP4_MX)). Codes and scales are bit-exact with the reference's; this is the activation side
+ * of the config-4 MXFP4 x MXFP4 linear. x: F32, BF16 or F16, 16-byte aligned. */
+int sqx_mxfp4_quantize_tiled(const void* x, int dtype, int64_t m, int64_t k, uint8_t* xt, uint8_t* xst,
+                             sqx_stream_t stream);
+
+/* MXFP4 x MXFP4 GEMM on the block-scaled fp4 MFMA: y[i, r] = sum_c X[i, c] W[r, c] (+ bias[r]) with
+ * X = mxfp4_dequantize of the tiled activations (xt, xst from sqx_mxfp4_quantize_tiled) and W of the
+ * tiled weight (wt, st from sqx_fp4_tile with MXFP4 scales). Replaces the config-4 composition
+ * F.linear(mxfp4_dequantize(mxfp4_quantize(x)), mxfp4_dequantize(W)) (nvfp4_mxfp4.py:257-272 with
+ * F.linear) and is the SURVEY's sqx_mxfp4_gemm export with act_fmt = MXFP4. fp32 accumulation;
+ * y [m, rows] of y_dtype (BF16, F16 or F32); bias (NULL or [rows] of y_dtype, not with F32). */
+int sqx_mxfp4_gemm(const uint8_t* xt, const uint8_t* xst, const uint8_t* wt, const uint8_t* wst, void* y,
+                   int y_dtype, const void* bias, int64_t m, int64_t rows, int64_t cols, sqx_stream_t stream);
+
 /* fp32 activations as two bf16 rows (quant_linear_nvfp4 keeps x in fp32): hi = bf16(x),
  * lo = bf16(x - hi); sqx_sum_halves: y[i] = y2[i] + y2[n + i] (the two rows' products). */
 int sqx_split_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, sqx_stream_t stream);

@@ -70,6 +70,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_i,
         [_c_p, _c_p, _c_i, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_i, _c_p],
     ),
+    "sqx_mxfp4_quantize_tiled": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "sqx_mxfp4_gemm": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_p]),
     "sqx_split_bf16": (_c_i, [_c_p, _c_i64, _c_p, _c_p, _c_p]),
     "sqx_sum_halves": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
     "sqx_int8_workspace_bytes": (_c_i64, []),

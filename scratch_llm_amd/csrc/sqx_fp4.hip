@@ -180,6 +180,67 @@ __global__ __launch_bounds__(256) void fp4_quantize_kernel(const void* __restric
   }
 }
 
+// mxfp4_quantize of the rows of x [m, k] (k % 32 == 0, so each of the reference's flattened
+// 32-blocks lies in one row) written straight into the tiled layout: one thread per 16-byte lane
+// chunk q of the padded [16 * ceil(m/16), 128 * KB] grid, i.e. row 16t + (L & 15), columns
+// 128kb + 32(L >> 4) .. +31, with its E8M0 scale at byte q of the scale buffer. Padding chunks get
+// code 0 and scale byte 0. x / 2**e is formed as x * 2**-e: the same single rounding of the same
+// real number (2**-e is exact for every e in [-99, 127], and NaN stays NaN).
+template <int DT>
+__global__ __launch_bounds__(256) void mxfp4_quantize_tiled_kernel(const void* __restrict__ x, int64_t m, int64_t k,
+                                                                   int64_t KB, int64_t n_chunks,
+                                                                   u32x4_t* __restrict__ xt,
+                                                                   uint8_t* __restrict__ xst) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= n_chunks) return;
+  const int L = static_cast<int>(q & 63);
+  const int64_t blk = q >> 6;
+  const int64_t t = blk / KB;
+  const int64_t kb = blk - t * KB;
+  const int64_t r = 16 * t + (L & 15);
+  const int64_t c0 = kb * 128 + 32 * (L >> 4);
+  uint32_t d[4] = {0u, 0u, 0u, 0u};
+  uint32_t sbyte = 0;
+  if (r < m && c0 < k) {
+    float v[32];
+    const int64_t base = r * k + c0;
+    if (DT == SQX_DTYPE_F32) {
+      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(static_cast<const float*>(x) + base);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const u32x4_t w = p[j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // copy the lane out first: __builtin_bit_cast of a vector subscript reads element 0
+          const uint32_t u = w[e];
+          v[4 * j + e] = __builtin_bit_cast(float, u);
+        }
+      }
+    } else {
+      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + base);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u32x4_t w = p[j];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint16_t h = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+          v[8 * j + e] = DT == SQX_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+        }
+      }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) amax = amax_step(amax, v[e]);
+    const int ex = mx_exponent(amax);
+    const float inv = ex == 128 ? __builtin_nanf("") : ldexpf(1.0f, -ex);
+#pragma unroll
+    for (int e = 0; e < 32; ++e) d[e >> 3] |= e2m1_code(v[e] * inv) << (4 * (e & 7));
+    sbyte = ex == 128 ? 255u : static_cast<uint32_t>(ex + 127);
+  }
+  xt[q] = u32x4_t{d[0], d[1], d[2], d[3]};
+  xst[q] = static_cast<uint8_t>(sbyte);
+}
+
 // NVFP4 global amax: P partial maxima, then s_global = max(amax / (448 * 6), 1e-30) from them.
 static constexpr int kAmaxParts = 512;
 
@@ -550,6 +611,33 @@ extern "C" int sqx_fp4_tile(const uint8_t* codes, int codes_packed, const void* 
   else
     hipLaunchKernelGGL(fp4_tile_scales_kernel<2>, grid_for(ns), dim3(256), 0, s, scales, rows, cols, block, KB, ns, st);
   SQX_LAUNCH_CHECK("sqx_fp4_tile");
+  return SQX_OK;
+}
+
+extern "C" int sqx_mxfp4_quantize_tiled(const void* x, int dtype, int64_t m, int64_t k, uint8_t* xt, uint8_t* xst,
+                                        sqx_stream_t stream) {
+  SQX_REQUIRE(is_float_dtype(dtype), SQX_E_ARG, "sqx_mxfp4_quantize_tiled: bad dtype %d", dtype);
+  SQX_REQUIRE(m >= 0 && k > 0 && k % 32 == 0 && m <= ((int64_t)1 << 31) && k <= ((int64_t)1 << 30), SQX_E_ARG,
+              "sqx_mxfp4_quantize_tiled: bad shape [%lld, %lld] (k must be a multiple of 32)", (long long)m,
+              (long long)k);
+  if (m == 0) return SQX_OK;
+  SQX_REQUIRE(x && xt && xst, SQX_E_ARG, "sqx_mxfp4_quantize_tiled: null pointer");
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(xt) % 16 == 0, SQX_E_ARG,
+              "sqx_mxfp4_quantize_tiled: x and xt must be 16-byte aligned");
+  const int64_t KB = ceil_div(k, 128);
+  const int64_t chunks = ceil_div(m, 16) * KB * 64;
+  hipStream_t s = as_stream(stream);
+  u32x4_t* x4 = reinterpret_cast<u32x4_t*>(xt);
+  if (dtype == SQX_DTYPE_BF16)
+    hipLaunchKernelGGL(mxfp4_quantize_tiled_kernel<SQX_DTYPE_BF16>, grid_for(chunks), dim3(256), 0, s, x, m, k, KB,
+                       chunks, x4, xst);
+  else if (dtype == SQX_DTYPE_F16)
+    hipLaunchKernelGGL(mxfp4_quantize_tiled_kernel<SQX_DTYPE_F16>, grid_for(chunks), dim3(256), 0, s, x, m, k, KB,
+                       chunks, x4, xst);
+  else
+    hipLaunchKernelGGL(mxfp4_quantize_tiled_kernel<SQX_DTYPE_F32>, grid_for(chunks), dim3(256), 0, s, x, m, k, KB,
+                       chunks, x4, xst);
+  SQX_LAUNCH_CHECK("sqx_mxfp4_quantize_tiled");
   return SQX_OK;
 }
 

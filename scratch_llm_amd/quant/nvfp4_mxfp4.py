@@ -7,7 +7,10 @@ to the reference: codes, block scales and global scale. CPU tensors raise ``Runt
 
 Beyond the reference API, :func:`mxfp4_linear` and :func:`nvfp4_linear` run the linear on a
 quantized weight without materialising it (``F.linear(x, dequant(W).to(x.dtype))``),
-and :func:`quant_linear_nvfp4` keeps the reference's signature.
+and :func:`quant_linear_nvfp4` keeps the reference's signature. Config 4's MXFP4-activation variant
+(``mxfp4_linear(..., quantize_activations=True)``) quantizes the activation rows into the same tiled
+layout (:func:`mxfp4_quantize_tiled`) and multiplies on CDNA4's block-scaled fp4 MFMA
+(:func:`mxfp4_gemm`).
 """
 
 from __future__ import annotations
@@ -29,8 +32,10 @@ __all__ = [
     "e2m1_round_to_code",
     "fp4_linear_tiled",
     "mxfp4_dequantize",
+    "mxfp4_gemm",
     "mxfp4_linear",
     "mxfp4_quantize",
+    "mxfp4_quantize_tiled",
     "nvfp4_dequantize",
     "nvfp4_linear",
     "nvfp4_quantize",
@@ -338,10 +343,71 @@ def _tiled(q: MXFP4Tensor | NVFP4Tensor) -> FP4Tiled:
     return _tiled_cache.get(keys, (type(q).__name__, tuple(q.shape), q.block), lambda: tile_fp4(q))
 
 
-def mxfp4_linear(x: Tensor, q: MXFP4Tensor, bias: Tensor | None = None) -> Tensor:
+def mxfp4_quantize_tiled(x: Tensor) -> FP4Tiled:
+    """``mxfp4_quantize`` (block 32) of each row of a 2-D ``x`` ``[m, k]`` (``k % 32 == 0``) written
+    straight into the tiled layout: the activation operand of :func:`mxfp4_gemm`. Codes and scales
+    are bit-identical to ``tile_fp4(mxfp4_quantize(x))``."""
+    if x.dim() != 2:
+        raise ValueError(f"expected 2-D activations [m, k], got shape {tuple(x.shape)}")
+    m, k = int(x.shape[0]), int(x.shape[1])
+    if k % 32 != 0:
+        raise ValueError(f"K={k} must be a multiple of 32 for per-row MXFP4 activation blocks")
+    dev = _lib.require_device(x, fn="mxfp4_quantize_tiled")
+    xc = _float_input(x, "mxfp4_quantize_tiled")
+    if not xc.is_contiguous() or xc.data_ptr() % 16:
+        xc = xc.contiguous()
+    lib = _lib.load()
+    xt = torch.empty(lib.sqx_fp4_tiled_weight_bytes(m, k), dtype=torch.uint8, device=dev)
+    xst = torch.empty(lib.sqx_fp4_tiled_scale_bytes(m, k, _lib.FP4_MX), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(lib.sqx_mxfp4_quantize_tiled(xc.data_ptr(), _lib.sqx_dtype(xc.dtype), m, k, xt.data_ptr(),
+                                                xst.data_ptr(), _stream(xc)), "mxfp4_quantize_tiled")
+    return FP4Tiled(xt, xst, _lib.FP4_MX, None, m, k)
+
+
+def mxfp4_gemm(xq: FP4Tiled, tw: FP4Tiled, bias: Tensor | None = None,
+               out_dtype: torch.dtype = torch.bfloat16) -> Tensor:
+    """``X @ W.T (+ bias)`` for tiled MXFP4 activations ``xq`` ``[m, k]`` and a tiled MXFP4 weight
+    ``tw`` ``[n, k]`` on the block-scaled fp4 MFMA (fp32 accumulation), ``[m, n]`` in ``out_dtype``
+    (bf16, fp16 or fp32; a bias needs bf16 or fp16)."""
+    if xq.fmt != _lib.FP4_MX or tw.fmt != _lib.FP4_MX:
+        raise ValueError("mxfp4_gemm takes MXFP4 operands on both sides")
+    if xq.cols != tw.cols:
+        raise ValueError(f"activations have in_features={xq.cols}, weight expects {tw.cols}")
+    if out_dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"mxfp4_gemm writes bf16, fp16 or fp32, not {out_dtype}")
+    dev = _lib.require_device(xq.wt, tw.wt, bias, fn="mxfp4_gemm")
+    if bias is not None and out_dtype == torch.float32:
+        raise ValueError("a bias needs a bf16 or fp16 output")
+    b = None if bias is None else bias.to(out_dtype).contiguous()
+    y = torch.empty(xq.rows, tw.rows, dtype=out_dtype, device=dev)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        _lib.check(lib.sqx_mxfp4_gemm(xq.wt.data_ptr(), xq.st.data_ptr(), tw.wt.data_ptr(), tw.st.data_ptr(), y.data_ptr(),
+                                      _lib.sqx_dtype(out_dtype), _lib.ptr(b), xq.rows, tw.rows, tw.cols, _stream(y)),
+                   "mxfp4_gemm")
+    return y
+
+
+def mxfp4_linear(x: Tensor, q: MXFP4Tensor, bias: Tensor | None = None, quantize_activations: bool = False) -> Tensor:
     """``F.linear(x, mxfp4_dequantize(q).to(x.dtype), bias)`` for an MXFP4 weight ``[out, in]``
-    (BASELINE config 4's composition), without materialising the weight. Output in ``x.dtype``."""
-    return fp4_linear_tiled(x, _tiled(q), bias)
+    (BASELINE config 4's composition), without materialising the weight. Output in ``x.dtype``.
+
+    ``quantize_activations=True`` is config 4's MXFP4-activation variant: each row of ``x`` goes
+    through ``mxfp4_quantize`` too, and the product of the two dequantized operands runs on the
+    block-scaled fp4 MFMA (exact products, fp32 accumulation). It matches the composition with
+    ``.to(x.dtype)`` wherever the dequantized values are representable in ``x.dtype`` (always for
+    bf16 and fp32)."""
+    tw = _tiled(q)
+    if not quantize_activations:
+        return fp4_linear_tiled(x, tw, bias)
+    *batch, k = x.shape
+    if k != tw.cols:
+        raise ValueError(f"x has in_features={k}, weight expects {tw.cols}")
+    if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise TypeError(f"the FP4 linear takes fp32, bf16 or fp16 activations, got {x.dtype}")
+    xq = mxfp4_quantize_tiled(x.reshape(-1, k))
+    return mxfp4_gemm(xq, tw, bias, x.dtype).reshape(*batch, tw.rows)
 
 
 def nvfp4_linear(x: Tensor, q: NVFP4Tensor, bias: Tensor | None = None) -> Tensor:
