@@ -247,6 +247,30 @@ int sqx_mxfp4_quantize_tiled(const void* x, int dtype, int64_t m, int64_t k, uin
 int sqx_mxfp4_gemm(const uint8_t* xt, const uint8_t* xst, const uint8_t* wt, const uint8_t* wst, void* y,
                    int y_dtype, const void* bias, int64_t m, int64_t rows, int64_t cols, sqx_stream_t stream);
 
+/* Prefill / large-batch W4A16 GEMM (SURVEY's sqx_int4_gemm): the same operation and tiled weight as
+ * sqx_int4_linear (w4a16_linear, int4_group.py:148-164, and the AWQ linear awq.py:184-192 on x / s),
+ * for any m, on the bf16 / fp16 MFMA with the weight tile decoded in registers to the reference's
+ * bf16(fp32((q - z) * s)). group: 32, 64 or 128; cols a multiple of 32 and of group. y [m, rows] in
+ * act_dtype; bias NULL or [rows] in act_dtype. ws: see sqx_gemm_workspace_bytes. */
+int sqx_int4_gemm(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
+                  int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols, int64_t group,
+                  void* ws, int64_t ws_bytes, sqx_stream_t stream);
+
+/* Workspace bytes the prefill GEMMs (sqx_int4_gemm, sqx_fp4_gemm) use for a shape: when few output
+ * tiles would leave CUs idle, the k range is split over workgroups that write fp32 partial sums to
+ * the workspace, added in a fixed order by a second kernel (deterministic). 0 = no split. A NULL or
+ * smaller workspace runs without the split (same result, slower for small m). */
+int64_t sqx_gemm_workspace_bytes(int64_t m, int64_t rows, int64_t cols);
+
+/* Prefill / large-batch FP4-weight GEMM with BF16 / F16 activations (SURVEY's sqx_mxfp4_gemm with
+ * act_fmt = bf16, and sqx_nvfp4_gemm): the same operation and tiled weight as sqx_fp4_linear (the
+ * config-4 F.linear(x, mxfp4_dequantize(W).to(x.dtype)) and the NVFP4 linear) on the 16-bit MFMA,
+ * each weight decoded in registers (MXFP4 exactly; NVFP4 as e2m1 * s_block with *s_global applied to
+ * the fp32 result). cols a multiple of 32; y_dtype act_dtype or F32; bias as sqx_fp4_linear. */
+int sqx_fp4_gemm(const uint8_t* wt, const uint8_t* st, int fmt, const float* s_global, const void* x,
+                 int act_dtype, void* y, int y_dtype, const void* bias, int64_t m, int64_t rows, int64_t cols,
+                 void* ws, int64_t ws_bytes, sqx_stream_t stream);
+
 /* fp32 activations as two bf16 rows (quant_linear_nvfp4 keeps x in fp32): hi = bf16(x),
  * lo = bf16(x - hi); sqx_sum_halves: y[i] = y2[i] + y2[n + i] (the two rows' products). */
 int sqx_split_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, sqx_stream_t stream);

@@ -72,6 +72,15 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "sqx_mxfp4_quantize_tiled": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "sqx_mxfp4_gemm": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_p]),
+    "sqx_gemm_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "sqx_int4_gemm": (
+        _c_i,
+        [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
+    ),
+    "sqx_fp4_gemm": (
+        _c_i,
+        [_c_p, _c_p, _c_i, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
+    ),
     "sqx_split_bf16": (_c_i, [_c_p, _c_i64, _c_p, _c_p, _c_p]),
     "sqx_sum_halves": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
     "sqx_int8_workspace_bytes": (_c_i64, []),
@@ -140,6 +149,16 @@ def sqx_dtype(dt: torch.dtype) -> int:
         return _TORCH_TO_SQX[dt]
     except KeyError:
         raise TypeError(f"dtype {dt} is not supported by the HIP kernels") from None
+
+
+def gemm_workspace(m: int, rows: int, cols: int, device: torch.device) -> torch.Tensor | None:
+    """fp32 split-K workspace the prefill GEMMs want for this shape (None when they do not split)."""
+    nb = int(load().sqx_gemm_workspace_bytes(m, rows, cols))
+    return None if nb <= 0 else torch.empty(nb // 4, dtype=torch.float32, device=device)
+
+
+def ws_args(ws: torch.Tensor | None) -> tuple[int | None, int]:
+    return (None, 0) if ws is None else (ws.data_ptr(), ws.numel() * 4)
 
 
 def require_device(*tensors: torch.Tensor | None, fn: str) -> torch.device:

@@ -111,6 +111,10 @@ struct ActBF16 {
       default: return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 3));
     }
   }
+  // two floats -> one bf16 pair, each rounded to nearest even (torch's .to(torch.bfloat16))
+  __device__ static inline uint32_t pack_rne(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+  }
   // two floats exactly representable in bf16 -> one bf16 pair (upper halves of the fp32 bits)
   __device__ static inline uint32_t pack_exact(float lo, float hi) {
     return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo), 0x07060302u);
@@ -148,6 +152,10 @@ struct ActF16 {
       case 2: return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, scale, 2));
       default: return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, scale, 3));
     }
+  }
+  // two floats -> one fp16 pair, each rounded to nearest even (torch's .to(torch.float16))
+  __device__ static inline uint32_t pack_rne(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t));
   }
   // two floats exactly representable in fp16 -> one fp16 pair (round-toward-zero is exact here)
   __device__ static inline uint32_t pack_exact(float lo, float hi) {
@@ -190,6 +198,25 @@ __device__ inline uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
   uint32_t r;
   asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(bits));
   return r;
+}
+
+// v_cvt_f32_ubyteN: byte SEL of d as fp32 in one instruction (the compiler forms a shift, a mask
+// and a conversion from the plain expression).
+template <int SEL>
+__device__ inline float ubyte_f32(uint32_t d) {
+  float f;
+  if (SEL == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(d));
+  if (SEL == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(d));
+  if (SEL == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(d));
+  if (SEL == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(d));
+  return f;
+}
+
+// OCP e4m3fn byte (as quantize_e4m3 values are stored in the tiled NVFP4 scales) -> fp32.
+__device__ inline float e4m3_value(uint32_t b) {
+  const uint32_t e = (b >> 3) & 15u;
+  const uint32_t m = b & 7u;
+  return e ? ldexpf(static_cast<float>(8u + m), static_cast<int>(e) - 10) : ldexpf(static_cast<float>(m), -9);
 }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

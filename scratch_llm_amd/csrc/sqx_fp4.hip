@@ -73,11 +73,6 @@ __device__ inline uint32_t e4m3_byte(float v) {
   return (static_cast<uint32_t>(e + 7) << 3) | mant;
 }
 
-__device__ inline float e4m3_value(uint32_t b) {
-  const uint32_t e = (b >> 3) & 15u;
-  const uint32_t m = b & 7u;
-  return e ? ldexpf(static_cast<float>(8u + m), static_cast<int>(e) - 10) : ldexpf(static_cast<float>(m), -9);
-}
 
 // quantize_e8m0 (:150-159): 2**clamp(rint(log2 v), +-127), 0 for v <= 0 (and NaN).
 __device__ inline float quantize_e8m0(float v) {

@@ -303,6 +303,386 @@ __global__ __launch_bounds__(128 * WN) void mxfp4_gemm_kernel(const uint8_t* __r
     }
 }
 
+
+// ==============================================================================================
+// Dequant GEMM: bf16 / fp16 activations x a tiled 4-bit weight (group INT4 or FP4)
+// ==============================================================================================
+// y[m, n] = sum_k x[m, k] W[n, k] (+ bias[n]) for x [M, K] row-major and W in the tiled layout of
+// sqx_int4.hip (group INT4, symmetric or asymmetric) or sqx_fp4.hip (MXFP4 / NVFP4): the prefill
+// form of w4a16_linear (int4_group.py:148-164), awq_linear (awq.py:184-192) and the config-4
+// FP4-weight linear. Each weight is decoded to the activation dtype in registers exactly as the
+// reference's dequantize(...).to(x.dtype) produces it: INT4 as the fp32 (q - z) * s rounded to
+// nearest even, FP4 as e2m1 * scale (exact; NVFP4's global scale multiplies the fp32 result).
+//
+// Tiling. A workgroup of 8 waves owns a 256 x 256 output tile; wave w computes rows
+// 128 (w / 4) .. +128 and columns 64 (w % 4) .. +64 as 8 x 4 tiles of v_mfma_f32_16x16x32 with the
+// weight as the first operand, so a lane's four accumulators are four consecutive output columns
+// of one row. A stage covers 64 k: the 256 activation rows (32 KiB, 16-byte chunks XOR-swizzled
+// by row so the operand reads of 8 consecutive rows hit distinct banks), the weight bytes of the
+// 16 row tiles for those 64 columns, and their scales; NSTAGE stages form a ring filled by
+// buffer -> LDS copies as in the MXFP4 GEMM. Every wave decodes its own 4 weight tiles per 32-k
+// MFMA step (the decode is shared by the wave's 8 row tiles).
+namespace dqg {
+constexpr int kTile = 256;
+constexpr int kBK = 64;
+constexpr int kXBytes = kTile * kBK * 2;  // activations of one stage
+constexpr int kWBytes = 16 * 512;         // 16 weight row tiles x 512 bytes
+constexpr int kPBytes = 4096;             // scales / zero-points of one stage
+constexpr int kStage = kXBytes + kWBytes + kPBytes;
+constexpr int kStages = 3;
+constexpr int kEpiPitch = 136;            // LDS bytes per row of a wave's 128 x 64 16-bit output tile
+constexpr int kLds = 8 * 128 * kEpiPitch; // 139264 >= kStages * kStage
+static_assert(kStages * kStage <= kLds, "stages fit the LDS allocation");
+}  // namespace dqg
+
+// Weight formats of the dequant GEMM.
+enum : int { kDqInt4 = 0, kDqMx = 1, kDqNv = 2 };
+
+template <int FMT, bool ASYM, bool PBF16, int GROUP>
+struct DqW {
+  // parameter bytes per stage and tile: INT4 scales (and zero-points) of the stage's groups;
+  // MXFP4 32 E8M0 bytes (lanes 32h..32h+31 of the 64-byte block), NVFP4 64 E4M3 bytes
+  static constexpr int PB = PBF16 ? 2 : 4;
+  static constexpr int kWInstr = FMT == kDqInt4 ? 4 : 1;  // weight copies per wave per stage
+  static constexpr int kPInstr = 2;                        // parameter copies per wave per stage
+  static constexpr int NGS = GROUP >= 64 ? 1 : 64 / GROUP;  // INT4 groups per stage
+  static constexpr int NP = FMT == kDqMx ? 2 : FMT == kDqNv ? 4 : (ASYM ? 2 : 1) * NGS * 16 * 16 * PB / 256;
+  static_assert(NP <= 16, "parameter copies fit two per wave");
+};
+
+template <class A, int FMT, bool ASYM, bool PBF16, int GROUP, int YKIND>
+__global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict__ x, const uint8_t* __restrict__ wt,
+                                                     const void* __restrict__ st, const void* __restrict__ zt,
+                                                     const float* __restrict__ s_global, void* __restrict__ y,
+                                                     const uint16_t* __restrict__ bias, int m, int n, int K, int KB,
+                                                     int tiles_m, int tiles_n, int lds16, int splits,
+                                                     float* __restrict__ ws) {
+  using P = DqW<FMT, ASYM, PBF16, GROUP>;
+  constexpr int group = GROUP;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int NS = dqg::kStages;
+  constexpr int kPerStage = 4 + P::kWInstr + P::kPInstr;  // buffer -> LDS copies per wave per stage
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int tm, tn;
+  // split-K: workgroup b computes split b % splits of tile b / splits (stages s0 .. s0+S-1)
+  const int tile = blockIdx.x / splits, split = blockIdx.x - tile * splits;
+  mx_tile_of(tile, tiles_m, tiles_n, tm, tn);
+  const int S_all = 2 * KB;  // stages of 64 columns (the tiled weight is padded to 128-column blocks)
+  const int Sp = (S_all + splits - 1) / splits;
+  const int s0 = split * Sp;
+  const int S = min(S_all, s0 + Sp) - s0;
+  const int wT = (n + 15) >> 4;
+  const int w_t0 = tn * 16;
+  const int Gp = KB * (128 / (FMT == kDqInt4 ? GROUP : 128));  // INT4 groups per row (padded)
+
+  const rsrc_t xr = make_rsrc(x, (uint32_t)((uint64_t)m * (uint64_t)K * 2u));
+  const rsrc_t wr = make_rsrc(wt, (uint32_t)wT * (uint32_t)KB * 1024u);
+  uint32_t pbytes;
+  if (FMT == kDqInt4) pbytes = (uint32_t)wT * (uint32_t)Gp * 16u * P::PB;
+  else pbytes = (uint32_t)wT * (uint32_t)KB * (FMT == kDqMx ? 64u : 128u);
+  const rsrc_t sr = make_rsrc(st, pbytes);
+  const rsrc_t zr = make_rsrc(ASYM ? zt : st, pbytes);
+  constexpr int np = P::NP;
+
+  // ---- copies of stage s into ring slot `slot`
+  auto issue = [&](int s, int slot) {
+    uint8_t* base = smem + slot * dqg::kStage;
+    const int kb = s >> 1, h = s & 1;
+    // activations: wave w copies rows 32w .. 32w+31 (8 rows of 8 chunks per instruction)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 32 * wave + 8 * j + (lane >> 3);
+      const int c = (lane & 7) ^ (r & 7);
+      const int R = tm * dqg::kTile + r, col = 64 * s + 8 * c;
+      const bool ok = (R < m) & (col < K);  // no short-circuit: a select, not a branch
+      const uint32_t off = ok ? ((uint32_t)R * (uint32_t)K + (uint32_t)col) * 2u : 0xFFFFFFF0u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(base + (32 * wave + 8 * j) * 128), 16, off, 0, 0, 0);
+    }
+    uint8_t* wbase = base + dqg::kXBytes;
+    if (FMT == kDqInt4) {
+      // tiles 2w, 2w+1: dwords 2h and 2h+1 of every lane's 16 bytes, 256 bytes per copy
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int f = 2 * wave + (j >> 1), i = 2 * h + (j & 1);
+        const int t = min(w_t0 + f, wT - 1);
+        const uint32_t off = ((uint32_t)t * (uint32_t)KB + (uint32_t)kb) * 1024u + (uint32_t)lane * 16u + (uint32_t)i * 4u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(wbase + f * 512 + (j & 1) * 256), 4, off, 0, 0, 0);
+      }
+    } else {
+      // tiles 2w (lanes 0-31) and 2w+1 (lanes 32-63): bytes 512h .. 512h+511 of their blocks
+      const int f = 2 * wave + (lane >> 5);
+      const int t = min(w_t0 + f, wT - 1);
+      const uint32_t off = ((uint32_t)t * (uint32_t)KB + (uint32_t)kb) * 1024u + 512u * (uint32_t)h + (uint32_t)(lane & 31) * 16u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(wbase + 2 * wave * 512), 16, off, 0, 0, 0);
+    }
+    uint8_t* pbase = base + dqg::kXBytes + dqg::kWBytes;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int pi = 2 * wave + j;  // parameter copy index; copies past np land in unused LDS
+      const int pr = pi < np ? pi : 0;
+      uint32_t off;
+      bool zsrc = false;
+      if (FMT == kDqInt4) {
+        // layout in LDS: [scales | zeros][group gi][tile f][row] of PB bytes; 256 bytes per copy
+        constexpr int TPI = 256 / (16 * P::PB);  // tiles per copy
+        const int per_kind = np / (ASYM ? 2 : 1);
+        zsrc = ASYM && pr >= per_kind;
+        const int q = pr - (zsrc ? per_kind : 0);
+        const int gi = q / (16 / TPI);
+        const int f = TPI * (q % (16 / TPI)) + lane / (64 / TPI);
+        const int t = min(w_t0 + f, wT - 1);
+        const int g = (64 * s) / group + gi;
+        off = ((uint32_t)t * (uint32_t)Gp + (uint32_t)g) * 16u * P::PB + (uint32_t)(lane % (64 / TPI)) * 4u;
+      } else if (FMT == kDqMx) {
+        const int f = 8 * pr + (lane >> 3);
+        const int t = min(w_t0 + f, wT - 1);
+        off = ((uint32_t)t * (uint32_t)KB + (uint32_t)kb) * 64u + 32u * (uint32_t)h + (uint32_t)(lane & 7) * 4u;
+      } else {
+        const int f = 4 * pr + (lane >> 4);
+        const int t = min(w_t0 + f, wT - 1);
+        off = ((uint32_t)t * (uint32_t)KB + (uint32_t)kb) * 128u + 64u * (uint32_t)h + (uint32_t)(lane & 15) * 4u;
+      }
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(zsrc ? zr : sr, (lds_void*)(pbase + pi * 256), 4, off, 0, 0, 0);
+    }
+  };
+
+  f32x4_t acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int wm = wave >> 2, wn = wave & 3;
+  const int nl = lane & 15, jg = lane >> 4;
+  // p0: the scale's fp32 bits, or for bf16 INT4 parameters bf16 scale | bf16 zero-point << 16;
+  // p1: fp32 zero-points (asymmetric INT4 with fp32 parameters only)
+  constexpr int kP1 = (FMT == kDqInt4 && ASYM && !PBF16) ? 4 : 1;
+  struct Raw {
+    u32x4_t xo[8];   // activation operands of the 8 row tiles
+    uint32_t wd[4];  // weight codes of the 4 column tiles
+    uint32_t p0[4], p1[kP1];
+  };
+  // operands of MFMA step q (32 columns) of the stage in ring slot `slot`
+  auto read = [&](int slot, int s, int q, Raw& o) {
+    const uint8_t* base = smem + slot * dqg::kStage;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      const int r = wm * 128 + 16 * mt + nl;
+      const int sl = (4 * q + jg) ^ (nl & 7);
+      o.xo[mt] = *reinterpret_cast<const u32x4_t*>(base + r * 128 + sl * 16);
+    }
+    const uint8_t* wb = base + dqg::kXBytes;
+    const uint8_t* pb = base + dqg::kXBytes + dqg::kWBytes;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int f = wn * 4 + nt;
+      if (FMT == kDqInt4) {
+        o.wd[nt] = *reinterpret_cast<const uint32_t*>(wb + f * 512 + q * 256 + lane * 4);
+        const int gi = GROUP >= 64 ? 0 : (32 * q) / GROUP;
+        constexpr int zoff = P::NGS * 16 * 16 * P::PB;
+        const int po = ((gi * 16 + f) * 16 + nl) * P::PB;
+        if (PBF16) {
+          const uint32_t sb = *reinterpret_cast<const uint16_t*>(pb + po);
+          o.p0[nt] = ASYM ? (sb | ((uint32_t)*reinterpret_cast<const uint16_t*>(pb + zoff + po) << 16)) : sb;
+        } else {
+          o.p0[nt] = *reinterpret_cast<const uint32_t*>(pb + po);
+          if (ASYM) o.p1[nt % kP1] = *reinterpret_cast<const uint32_t*>(pb + zoff + po);
+        }
+      } else {
+        const int ll = 16 * q + nl;  // lane of the 128-column block within the stage's half
+        o.wd[nt] = *reinterpret_cast<const uint32_t*>(wb + f * 512 + ll * 16 + jg * 4);
+        if (FMT == kDqMx) {
+          o.p0[nt] = (uint32_t)pb[f * 32 + ll] << 23;  // the fp32 2**(e - 127)
+        } else {
+          o.p0[nt] = __builtin_bit_cast(uint32_t, e4m3_value(pb[f * 64 + 2 * ll + (jg >> 1)]));
+        }
+      }
+    }
+    (void)s;
+  };
+  // weight operand of column tile nt: 8 consecutive k of row nl, in the activation dtype
+  auto decode = [&](const Raw& o, int nt) -> u32x4_t {
+    const uint32_t d = o.wd[nt];
+    if (FMT == kDqMx) {
+      const float sc = __builtin_bit_cast(float, o.p0[nt]);
+      return u32x4_t{A::fp4_pair_scaled(d, sc, 0), A::fp4_pair_scaled(d, sc, 1), A::fp4_pair_scaled(d, sc, 2),
+                     A::fp4_pair_scaled(d, sc, 3)};
+    }
+    float w[8];
+    if (FMT == kDqNv) {
+      const float sc = __builtin_bit_cast(float, o.p0[nt]);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const f32x2_t f = A::fp4_pair_f32(d, p);
+        w[2 * p] = f[0] * sc;
+        w[2 * p + 1] = f[1] * sc;
+      }
+      return u32x4_t{A::pack_exact(w[0], w[1]), A::pack_exact(w[2], w[3]), A::pack_exact(w[4], w[5]),
+                     A::pack_exact(w[6], w[7])};
+    }
+    // INT4: element e in nibble e/2 (even e) or 4 + e/2 (odd e); u as fp32, then fp32 (u - z) * s
+    const uint32_t lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
+    const float u[8] = {ubyte_f32<0>(lo), ubyte_f32<2>(lo), ubyte_f32<0>(hi), ubyte_f32<2>(hi),
+                        ubyte_f32<1>(lo), ubyte_f32<3>(lo), ubyte_f32<1>(hi), ubyte_f32<3>(hi)};
+    const float sc = PBF16 ? bf16_bits_to_f32((uint16_t)(o.p0[nt] & 0xffffu)) : __builtin_bit_cast(float, o.p0[nt]);
+    if (!ASYM || PBF16) {
+      // z * s is exact (z = 8, or z <= 15 and s has at most 8 significant bits), so the fma rounds
+      // the exact (u - z) * s once
+      const float zf = ASYM ? bf16_bits_to_f32((uint16_t)(o.p0[nt] >> 16)) : 8.0f;
+      const float c = -zf * sc;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[e] = fmaf(u[e], sc, c);
+    } else {
+      const float zf = __builtin_bit_cast(float, o.p1[nt % kP1]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[e] = (u[e] - zf) * sc;
+    }
+    return u32x4_t{A::pack_rne(w[0], w[1]), A::pack_rne(w[2], w[3]), A::pack_rne(w[4], w[5]), A::pack_rne(w[6], w[7])};
+  };
+  auto mma = [&](const Raw& o) {
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const u32x4_t b = decode(o, nt);
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) acc[mt][nt] = A::mfma(b, o.xo[mt], acc[mt][nt]);
+    }
+  };
+
+  // pipeline (as the MXFP4 GEMM): iteration s: read (s, 1) | MFMAs (s, 0) | wait for stage s+1,
+  // barrier | copy stage s+NS-1 into the slot of s-1 | read (s+1, 0) | MFMAs (s, 1)
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < S) issue(s0 + s, s);
+  if (S - 1 >= NS - 2) wait_vmcnt<kPerStage * (NS - 2)>();
+  else wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  Raw o0, o1;
+  read(0, 0, 0, o0);
+  int s = 0;
+  for (; s + NS - 1 < S; ++s) {
+    read(s % NS, s, 1, o1);
+    mma(o0);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<kPerStage * (NS - 3)>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(s0 + s + NS - 1, (s + NS - 1) % NS);
+    read((s + 1) % NS, s + 1, 0, o0);
+    mma(o1);
+  }
+  for (; s < S; ++s) {
+    read(s % NS, s, 1, o1);
+    mma(o0);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + 1 < S) read((s + 1) % NS, s + 1, 0, o0);
+    mma(o1);
+  }
+
+  // epilogue: acc[mt][nt][i] is y[m0 + 16mt + (l & 15)][n0 + 16nt + 4(l >> 4) + i]
+  const int m0 = tm * dqg::kTile + wm * 128;
+  const int n0 = tn * dqg::kTile + wn * 64;
+  if (splits > 1) {
+    // raw fp32 partial sums of this split; dq_reduce_kernel adds the splits in order
+    float* part = ws + (int64_t)split * m * n;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int col = n0 + 16 * nt + 4 * jg;
+      if (col >= n) continue;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const int row = m0 + 16 * mt + nl;
+        if (row >= m) continue;
+        float* dst = part + (int64_t)row * n + col;
+        if ((n & 3) == 0) {
+          *reinterpret_cast<f32x4_t*>(dst) = acc[mt][nt];
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (col + j < n) dst[j] = acc[mt][nt][j];
+        }
+      }
+    }
+    return;
+  }
+  const float gs = FMT == kDqNv ? *s_global : 1.0f;
+  if (YKIND != 2 && lds16) {
+    __builtin_amdgcn_s_barrier();  // every wave is done reading the stages
+    uint8_t* ep = smem + wave * 128 * dqg::kEpiPitch;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int cl = 16 * nt + 4 * jg;
+      float badd[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (bias) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (n0 + cl + j < n) badd[j] = YKIND == 1 ? f16_bits_to_f32(bias[n0 + cl + j]) : bf16_bits_to_f32(bias[n0 + cl + j]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const int rl = 16 * mt + nl;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = acc[mt][nt][j] * gs + badd[j];
+        const uint32_t lo = YKIND == 0 ? ActBF16::pack_rne(v[0], v[1]) : ActF16::pack_rne(v[0], v[1]);
+        const uint32_t hi = YKIND == 0 ? ActBF16::pack_rne(v[2], v[3]) : ActF16::pack_rne(v[2], v[3]);
+        *reinterpret_cast<u32x2_t*>(ep + rl * dqg::kEpiPitch + cl * 2) = u32x2_t{lo, hi};
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    const int cc = (lane & 7) * 8;
+#pragma unroll 4
+    for (int p = 0; p < 16; ++p) {
+      const int rl = 8 * p + (lane >> 3);
+      const int row = m0 + rl, col = n0 + cc;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ep + rl * dqg::kEpiPitch + cc * 2);
+      if (row >= m || col >= n) continue;
+      uint16_t* dst = static_cast<uint16_t*>(y) + (int64_t)row * n + col;
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(dst));
+    }
+    return;
+  }
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int col = n0 + 16 * nt + 4 * jg;
+    if (col >= n) continue;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      const int row = m0 + 16 * mt + nl;
+      if (row >= m) continue;
+      const int64_t o = (int64_t)row * n + col;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (col + j >= n) break;
+        float v = acc[mt][nt][j] * gs;
+        if (bias) v += YKIND == 1 ? f16_bits_to_f32(bias[col + j]) : bf16_bits_to_f32(bias[col + j]);
+        if (YKIND == 0) static_cast<uint16_t*>(y)[o + j] = f32_to_bf16_bits(v);
+        else if (YKIND == 1) static_cast<uint16_t*>(y)[o + j] = f32_to_f16_bits(v);
+        else static_cast<float*>(y)[o + j] = v;
+      }
+    }
+  }
+}
+
+// y[i] = (sum over splits, in order, of the fp32 partials) * gs (+ bias[i % n]), rounded to y's dtype.
+template <int YKIND>
+__global__ __launch_bounds__(256) void dq_reduce_kernel(const float* __restrict__ ws, int splits, int64_t mn, int n,
+                                                        const float* __restrict__ s_global,
+                                                        const uint16_t* __restrict__ bias, void* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= mn) return;
+  float v = 0.0f;
+  for (int s = 0; s < splits; ++s) v += ws[(int64_t)s * mn + i];
+  if (s_global) v *= *s_global;
+  if (bias) v += YKIND == 1 ? f16_bits_to_f32(bias[i % n]) : bf16_bits_to_f32(bias[i % n]);
+  if (YKIND == 0) static_cast<uint16_t*>(y)[i] = f32_to_bf16_bits(v);
+  else if (YKIND == 1) static_cast<uint16_t*>(y)[i] = f32_to_f16_bits(v);
+  else static_cast<float*>(y)[i] = v;
+}
+
 }  // namespace sqx
 
 using namespace sqx;
@@ -364,5 +744,137 @@ extern "C" int sqx_mxfp4_gemm(const uint8_t* xt, const uint8_t* xst, const uint8
   else if (y_dtype == SQX_DTYPE_F16) e = launch_mx<1>(xt, xst, wt, wst, y, b16, (int)m, (int)rows, (int)KB, s);
   else e = launch_mx<2>(xt, xst, wt, wst, y, b16, (int)m, (int)rows, (int)KB, s);
   SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "sqx_mxfp4_gemm: launch failed: %s", hipGetErrorString(e));
+  return SQX_OK;
+}
+
+namespace {
+// K splits for a shape: when the output tiles fill less than three quarters of the 256 CUs, enough
+// splits for one workgroup per CU, at least 4 stages (256 columns) per split, and no empty split.
+int dq_splits(int64_t m, int64_t rows, int64_t cols) {
+  const int64_t tiles = ceil_div(m, dqg::kTile) * ceil_div(rows, dqg::kTile);
+  const int64_t S = 2 * ceil_div(cols, 128);
+  if (tiles >= 192) return 1;
+  const int64_t want = std::min<int64_t>(std::min<int64_t>(ceil_div(256, tiles), S / 4), 16);
+  if (want < 2) return 1;
+  const int64_t per = ceil_div(S, want);
+  return (int)ceil_div(S, per);
+}
+
+template <class A, int FMT, bool ASYM, bool PBF16, int GROUP, int YK>
+hipError_t launch_dq(const uint16_t* x, const uint8_t* wt, const void* st, const void* zt, const float* s_global,
+                     void* y, const uint16_t* bias, int m, int n, int K, int KB, float* ws, int64_t ws_bytes,
+                     hipStream_t s) {
+  const int tiles_m = (m + dqg::kTile - 1) / dqg::kTile, tiles_n = (n + dqg::kTile - 1) / dqg::kTile;
+  int splits = dq_splits(m, n, K);
+  if (splits > 1 && (ws == nullptr || ws_bytes < (int64_t)splits * m * n * 4 || reinterpret_cast<uintptr_t>(ws) % 16))
+    splits = 1;  // no (or too small a) workspace: one pass per tile
+  auto kern = dq_gemm_kernel<A, FMT, ASYM, PBF16, GROUP, YK>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     dqg::kLds);
+  if (e != hipSuccess) return e;
+  const int lds16 = YK != 2 && (n % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n * splits)), dim3(512), dqg::kLds, s, x, wt, st, zt,
+                     s_global, y, bias, m, n, K, KB, tiles_m, tiles_n, lds16, splits, ws);
+  if (splits > 1) {
+    const int64_t mn = (int64_t)m * n;
+    hipLaunchKernelGGL(dq_reduce_kernel<YK>, dim3((unsigned)ceil_div(mn, 256)), dim3(256), 0, s, ws, splits, mn, n,
+                       FMT == kDqNv ? s_global : nullptr, bias, y);
+  }
+  return hipGetLastError();
+}
+
+// shape checks shared by the dequant GEMM entry points
+int dq_check(const char* fn, const void* x, const void* wt, const void* y, int64_t m, int64_t rows, int64_t cols) {
+  SQX_REQUIRE(m >= 0 && rows > 0 && cols > 0 && cols % 32 == 0, SQX_E_ARG,
+              "%s: bad shape m=%lld rows=%lld cols=%lld (cols must be a multiple of 32)", fn, (long long)m,
+              (long long)rows, (long long)cols);
+  SQX_REQUIRE(m * cols * 2 < ((int64_t)1 << 31) && ceil_div(rows, 16) * ceil_div(cols, 128) * 1024 < ((int64_t)1 << 31) &&
+                  ceil_div(m, 256) * ceil_div(rows, 256) < ((int64_t)1 << 31),
+              SQX_E_ARG, "%s: operands beyond 2 GiB (32-bit buffer offsets)", fn);
+  SQX_REQUIRE(m == 0 || (x && wt && y), SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(wt) % 16 == 0, SQX_E_ARG,
+              "%s: x and the tiled weight must be 16-byte aligned", fn);
+  return SQX_OK;
+}
+}  // namespace
+
+extern "C" int64_t sqx_gemm_workspace_bytes(int64_t m, int64_t rows, int64_t cols) {
+  if (m <= 0 || rows <= 0 || cols <= 0) return 0;
+  const int sp = dq_splits(m, rows, cols);
+  return sp > 1 ? (int64_t)sp * m * rows * 4 : 0;
+}
+
+extern "C" int sqx_int4_gemm(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
+                             int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
+                             int64_t group, void* ws, int64_t ws_bytes, sqx_stream_t stream) {
+  if (int rc = dq_check("sqx_int4_gemm", x, wt, y, m, rows, cols)) return rc;
+  SQX_REQUIRE(group == 32 || group == 64 || group == 128, SQX_E_ARG,
+              "sqx_int4_gemm: group %lld not one of 32, 64, 128", (long long)group);
+  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "sqx_int4_gemm: cols %lld not a multiple of group %lld", (long long)cols,
+              (long long)group);
+  SQX_REQUIRE(param_dtype == SQX_DTYPE_F32 || param_dtype == SQX_DTYPE_BF16, SQX_E_ARG,
+              "sqx_int4_gemm: param_dtype must be F32 or BF16");
+  SQX_REQUIRE(act_dtype == SQX_DTYPE_BF16 || act_dtype == SQX_DTYPE_F16, SQX_E_ARG,
+              "sqx_int4_gemm: activations must be BF16 or F16");
+  if (m == 0) return SQX_OK;
+  SQX_REQUIRE(st, SQX_E_ARG, "sqx_int4_gemm: null scales");
+  const bool asym = zt != nullptr, pbf = param_dtype == SQX_DTYPE_BF16;
+  const int KB = (int)ceil_div(cols, 128);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* b16 = static_cast<const uint16_t*>(bias);
+  hipStream_t s = as_stream(stream);
+  hipError_t e;
+#define SQX_DQG(ACT, AS, PB, G, YK) \
+  e = launch_dq<ACT, kDqInt4, AS, PB, G, YK>(xp, wt, st, zt, nullptr, y, b16, (int)m, (int)rows, (int)cols, KB, \
+                                             static_cast<float*>(ws), ws_bytes, s)
+#define SQX_DQ(ACT, AS, PB, YK)                               \
+  do {                                                        \
+    if (group == 32) SQX_DQG(ACT, AS, PB, 32, YK);            \
+    else if (group == 64) SQX_DQG(ACT, AS, PB, 64, YK);       \
+    else SQX_DQG(ACT, AS, PB, 128, YK);                       \
+  } while (0)
+  if (act_dtype == SQX_DTYPE_BF16) {
+    if (asym) { if (pbf) SQX_DQ(ActBF16, true, true, 0); else SQX_DQ(ActBF16, true, false, 0); }
+    else { if (pbf) SQX_DQ(ActBF16, false, true, 0); else SQX_DQ(ActBF16, false, false, 0); }
+  } else {
+    if (asym) { if (pbf) SQX_DQ(ActF16, true, true, 1); else SQX_DQ(ActF16, true, false, 1); }
+    else { if (pbf) SQX_DQ(ActF16, false, true, 1); else SQX_DQ(ActF16, false, false, 1); }
+  }
+#undef SQX_DQ
+#undef SQX_DQG
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "sqx_int4_gemm: launch failed: %s", hipGetErrorString(e));
+  return SQX_OK;
+}
+
+extern "C" int sqx_fp4_gemm(const uint8_t* wt, const uint8_t* st, int fmt, const float* s_global, const void* x,
+                            int act_dtype, void* y, int y_dtype, const void* bias, int64_t m, int64_t rows, int64_t cols,
+                            void* ws, int64_t ws_bytes, sqx_stream_t stream) {
+  if (int rc = dq_check("sqx_fp4_gemm", x, wt, y, m, rows, cols)) return rc;
+  SQX_REQUIRE(fmt == SQX_FP4_MX || fmt == SQX_FP4_NV, SQX_E_ARG, "sqx_fp4_gemm: bad fmt %d", fmt);
+  SQX_REQUIRE(act_dtype == SQX_DTYPE_BF16 || act_dtype == SQX_DTYPE_F16, SQX_E_ARG,
+              "sqx_fp4_gemm: activations must be BF16 or F16");
+  SQX_REQUIRE(y_dtype == act_dtype || y_dtype == SQX_DTYPE_F32, SQX_E_ARG,
+              "sqx_fp4_gemm: y_dtype must be the activation dtype or F32");
+  SQX_REQUIRE(bias == nullptr || y_dtype == act_dtype, SQX_E_ARG, "sqx_fp4_gemm: bias needs y in act_dtype");
+  if (m == 0) return SQX_OK;
+  SQX_REQUIRE(st && (fmt == SQX_FP4_MX || s_global), SQX_E_ARG, "sqx_fp4_gemm: null pointer");
+  const int KB = (int)ceil_div(cols, 128);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* b16 = static_cast<const uint16_t*>(bias);
+  hipStream_t s = as_stream(stream);
+  const bool yf = y_dtype == SQX_DTYPE_F32;
+  hipError_t e;
+#define SQX_DQ(ACT, F, YK) \
+  e = launch_dq<ACT, F, false, false, 128, YK>(xp, wt, st, nullptr, s_global, y, b16, (int)m, (int)rows, (int)cols, KB, \
+                                              static_cast<float*>(ws), ws_bytes, s)
+  if (act_dtype == SQX_DTYPE_BF16) {
+    if (fmt == SQX_FP4_MX) { if (yf) SQX_DQ(ActBF16, kDqMx, 2); else SQX_DQ(ActBF16, kDqMx, 0); }
+    else { if (yf) SQX_DQ(ActBF16, kDqNv, 2); else SQX_DQ(ActBF16, kDqNv, 0); }
+  } else {
+    if (fmt == SQX_FP4_MX) { if (yf) SQX_DQ(ActF16, kDqMx, 2); else SQX_DQ(ActF16, kDqMx, 1); }
+    else { if (yf) SQX_DQ(ActF16, kDqNv, 2); else SQX_DQ(ActF16, kDqNv, 1); }
+  }
+#undef SQX_DQ
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "sqx_fp4_gemm: launch failed: %s", hipGetErrorString(e));
   return SQX_OK;
 }

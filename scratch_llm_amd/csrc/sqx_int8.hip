@@ -260,16 +260,6 @@ __global__ __launch_bounds__(256) void w8a8_kernel(const int8_t* __restrict__ qx
 // ----------------------------------------------------------------------------------------------
 // Int8 weight-only linear: the GEMV policy
 // ----------------------------------------------------------------------------------------------
-template <int SEL>
-__device__ inline float ubyte_f32(uint32_t d) {  // v_cvt_f32_ubyteN: byte SEL of d as fp32
-  float f;
-  if (SEL == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(d));
-  if (SEL == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(d));
-  if (SEL == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(d));
-  if (SEL == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(d));
-  return f;
-}
-
 struct WInt8 {
   static constexpr int KBLK = 64, STEPS = 2;
   struct Args {

@@ -253,12 +253,21 @@ def tile_int4_packed(packed: Tensor, scales: Tensor, shape: tuple[int, int], gro
     return Int4Tiled(wt, st, None, rows, cols, group_size)
 
 
+# Activation rows from which the tiled linears switch from the streaming decode kernel to the
+# prefill GEMM.
+GEMM_MIN_M = 64
+
+
 def int4_linear_tiled(x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, k_slices: int | None = None) -> Tensor:
     """``x @ W.T (+ bias)`` for a tiled INT4 weight ``W [out, in]``; ``x`` is ``[..., in]`` in bf16 or
     fp16 and the result has ``x``'s dtype and shape ``[..., out]``. fp32 accumulation.
 
-    ``k_slices`` (1..16) overrides how many waves split each 16-row tile's columns; the partial sums
-    are added in a fixed order, so a given ``k_slices`` always gives the same bits."""
+    Up to ``GEMM_MIN_M - 1`` rows run the streaming decode kernel; from ``GEMM_MIN_M`` rows on (and
+    ``k_slices`` unset) the prefill GEMM, which decodes each weight tile once per 256 rows.
+
+    ``k_slices`` (1..16) overrides how many waves split each 16-row tile's columns in the decode
+    kernel; the partial sums are added in a fixed order, so a given ``k_slices`` always gives the
+    same bits."""
     *batch, k = x.shape
     if k != tw.cols:
         raise ValueError(f"x has in_features={k}, weight expects {tw.cols}")
@@ -274,11 +283,19 @@ def int4_linear_tiled(x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, k_sl
     lib = _lib.load()
     ks = 0 if k_slices is None else int(k_slices)
     with torch.cuda.device(dev):
-        rc = lib.sqx_int4_linear(
-            _lib.ptr(tw.wt), _lib.ptr(tw.st), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype), _lib.ptr(x2),
-            _lib.sqx_dtype(x.dtype), _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size, ks,
-            _lib.stream_ptr(dev),
-        )
+        if m >= GEMM_MIN_M and k_slices is None:
+            ws = _lib.gemm_workspace(m, tw.rows, tw.cols, dev)
+            rc = lib.sqx_int4_gemm(
+                _lib.ptr(tw.wt), _lib.ptr(tw.st), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype), _lib.ptr(x2),
+                _lib.sqx_dtype(x.dtype), _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size,
+                *_lib.ws_args(ws), _lib.stream_ptr(dev),
+            )
+        else:
+            rc = lib.sqx_int4_linear(
+                _lib.ptr(tw.wt), _lib.ptr(tw.st), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype), _lib.ptr(x2),
+                _lib.sqx_dtype(x.dtype), _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size, ks,
+                _lib.stream_ptr(dev),
+            )
     _lib.check(rc, "int4_linear_tiled")
     return y.reshape(*batch, tw.rows)
 

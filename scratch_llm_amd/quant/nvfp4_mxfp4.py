@@ -51,6 +51,9 @@ __all__ = [
 FP4_MAGNITUDES: tuple[float, ...] = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)
 E4M3_MAX = 448.0
 _TINY = 1e-30
+# Activation rows from which the tiled FP4 linear switches from the streaming decode kernel to the
+# prefill GEMM.
+GEMM_MIN_M = 64
 
 
 def _float_input(x: Tensor, fn: str) -> Tensor:
@@ -313,9 +316,15 @@ def fp4_linear_tiled(x: Tensor, tw: FP4Tiled, bias: Tensor | None = None, out_dt
             xs = torch.empty(2 * m, k, dtype=torch.bfloat16, device=dev)
             _lib.check(lib.sqx_split_bf16(xf.data_ptr(), m * k, xs.data_ptr(), xs[m:].data_ptr(), s), "fp4_linear")
             y2 = torch.empty(2 * m, tw.rows, dtype=torch.float32, device=dev)
-            _lib.check(lib.sqx_fp4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), tw.fmt, _lib.ptr(tw.s_global), xs.data_ptr(),
-                                          _lib.DTYPE_BF16, y2.data_ptr(), _lib.DTYPE_F32, None, 2 * m, tw.rows, tw.cols,
-                                          ks, s), "fp4_linear")
+            if 2 * m >= GEMM_MIN_M and k_slices is None:
+                ws = _lib.gemm_workspace(2 * m, tw.rows, tw.cols, dev)
+                _lib.check(lib.sqx_fp4_gemm(tw.wt.data_ptr(), tw.st.data_ptr(), tw.fmt, _lib.ptr(tw.s_global), xs.data_ptr(),
+                                            _lib.DTYPE_BF16, y2.data_ptr(), _lib.DTYPE_F32, None, 2 * m, tw.rows, tw.cols,
+                                            *_lib.ws_args(ws), s), "fp4_linear")
+            else:
+                _lib.check(lib.sqx_fp4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), tw.fmt, _lib.ptr(tw.s_global),
+                                              xs.data_ptr(), _lib.DTYPE_BF16, y2.data_ptr(), _lib.DTYPE_F32, None, 2 * m,
+                                              tw.rows, tw.cols, ks, s), "fp4_linear")
             y = torch.empty(m, tw.rows, dtype=torch.float32, device=dev)
             _lib.check(lib.sqx_sum_halves(y2.data_ptr(), m * tw.rows, y.data_ptr(), s), "fp4_linear")
             return y.reshape(*batch, tw.rows).to(out_dtype)
@@ -328,10 +337,16 @@ def fp4_linear_tiled(x: Tensor, tw: FP4Tiled, bias: Tensor | None = None, out_dt
         b = None if bias is None else bias.to(x.dtype).contiguous()
         if b is not None and yf32:
             raise ValueError("a bias needs the output in the activation dtype")
-        _lib.check(lib.sqx_fp4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), tw.fmt, _lib.ptr(tw.s_global), x2.data_ptr(),
-                                      _lib.sqx_dtype(x.dtype), y.data_ptr(),
-                                      _lib.DTYPE_F32 if yf32 else _lib.sqx_dtype(x.dtype), _lib.ptr(b), m, tw.rows,
-                                      tw.cols, ks, s), "fp4_linear")
+        ydt = _lib.DTYPE_F32 if yf32 else _lib.sqx_dtype(x.dtype)
+        if m >= GEMM_MIN_M and k_slices is None:
+            ws = _lib.gemm_workspace(m, tw.rows, tw.cols, dev)
+            _lib.check(lib.sqx_fp4_gemm(tw.wt.data_ptr(), tw.st.data_ptr(), tw.fmt, _lib.ptr(tw.s_global), x2.data_ptr(),
+                                        _lib.sqx_dtype(x.dtype), y.data_ptr(), ydt, _lib.ptr(b), m, tw.rows, tw.cols,
+                                        *_lib.ws_args(ws), s), "fp4_linear")
+        else:
+            _lib.check(lib.sqx_fp4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), tw.fmt, _lib.ptr(tw.s_global),
+                                          x2.data_ptr(), _lib.sqx_dtype(x.dtype), y.data_ptr(), ydt, _lib.ptr(b), m,
+                                          tw.rows, tw.cols, ks, s), "fp4_linear")
         return y.reshape(*batch, tw.rows).to(out_dtype)
 
 
