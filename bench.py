@@ -17,9 +17,16 @@ per_shape: each Llama-3-8B linear shape timed on its own (HIP events around a gr
 launches on the launch stream), rotating over >= 1 GB of distinct weight tiles (views into the
 step's tiled weights: any 16-row-tile window of a tiled weight is a tiled weight).
 roofline: the dominant kernel of the step, the int4 linear launch that takes the largest share of
-the step (the fused gate/up projection), timed the same way.
+the step (the fused gate/up projection), timed the same way; `traffic` is its HBM bytes per launch
+from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this benchmark recorded in
+profiles/int4_linear_gate_up_traffic.md (scaled by the counters' reading of a 1 GiB copy), for M = 1.
 cpu_baseline: the reference's CPU path (torch dequantize + F.linear per call, restated in
 oracle/torch_path.py) over layer 0's seven projections, on this host's cores, for a bounded time.
+
+prefill (not part of `value`): the prefill GEMMs at their BASELINE configs, HIP-event medians of
+back-to-back launches on inputs already in HBM: config 4's MXFP4 x MXFP4 GEMM at M = 4096 (both
+shapes) against the 10.1 PF dense fp4 MFMA peak, config 4's MXFP4-weight x bf16 GEMM at M = 4096
+and config 3's AWQ int4 GEMM at M = 2048 against the 2.5 PF bf16 peak.
 """
 
 from __future__ import annotations
@@ -76,6 +83,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape timing")
     ap.add_argument("--kslices", type=int, default=0, help="waves per 16-row tile (0 = library default)")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM measurements")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -291,6 +299,12 @@ def main() -> int:
         }
         log(f"cpu baseline: {cpu_baseline['value']} GB/s")
 
+    # ------------------------------------------------------------------ prefill GEMMs
+    prefill = None
+    if not args.no_prefill:
+        prefill = prefill_gemms(dev)
+        log("prefill:", json.dumps(prefill))
+
     launches = len(linears)
     out = {
         "metric": METRIC,
@@ -331,15 +345,88 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(dom, m),
             "kernel": f"int4_linear_kernel (sqx_int4_linear) {dom[0]} {dom[2]}->{dom[1]}",
             "avg_launch_us": round(dom_us, 3),
             "bytes_per_launch": dom_bytes,
         },
         "cpu_baseline": cpu_baseline,
+        "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def measured_traffic(dom, m: int):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    runs of this benchmark (profiles/int4_linear_gate_up_traffic.md), when the shape and M match."""
+    path = os.path.join(ROOT, "profiles", "int4_linear_gate_up_traffic.md")
+    try:
+        text = open(path).read()
+        blk = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+    except (OSError, IndexError, ValueError):
+        return None
+    if blk.get("shape") != f"{dom[2]}->{dom[1]}" or blk.get("m") != m:
+        return None
+    return int(blk["traffic_bytes_per_launch"])
+
+
+def _median_us(fn, reps: int = 10, warm: int = 3) -> float:
+    import torch
+
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in ev:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
+    return t[len(t) // 2]
+
+
+def prefill_gemms(dev) -> dict:
+    """The prefill GEMMs at BASELINE configs 3 and 4 (module docstring)."""
+    import torch
+
+    from scratch_llm_amd.quant import awq, nvfp4_mxfp4 as f4
+
+    FP4_PEAK, BF16_PEAK = 10.1e15, 2.5e15
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(1004)
+    for n, k in ((28672, 8192), (8192, 28672)):
+        m = 4096
+        w = torch.randn(n, k, generator=g, device=dev) * 0.02
+        tw = f4.tile_fp4(f4.mxfp4_quantize(w, 32))
+        del w
+        x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+        xq = f4.mxfp4_quantize_tiled(x)
+        us = _median_us(lambda: f4.mxfp4_gemm(xq, tw))
+        fl = 2.0 * m * n * k
+        res[f"mxfp4_x_mxfp4 {k}->{n} M={m}"] = {
+            "us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "frac_of_fp4_peak": round(fl / us * 1e6 / FP4_PEAK, 4),
+            "quantize_x_us": round(_median_us(lambda: f4.mxfp4_quantize_tiled(x)), 1)}
+        if n == 28672:
+            us = _median_us(lambda: f4.fp4_linear_tiled(x, tw))
+            res[f"mxfp4_w_bf16_x {k}->{n} M={m}"] = {
+                "us": round(us, 1), "tflops": round(fl / us / 1e6, 1),
+                "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4)}
+        del tw, x, xq
+        torch.cuda.empty_cache()
+    n, k, m = 14336, 4096, 2048
+    w = torch.randn(n, k, generator=g, device=dev) * 0.02
+    s = torch.exp(torch.empty(k, device=dev).uniform_(-0.6931, 0.6931, generator=g))
+    quant = awq.quantize_awq_int4(w, chan_scale=s)
+    x = torch.randn(m, k, generator=g, device=dev)
+    x[:, torch.randperm(k, generator=torch.Generator().manual_seed(k))[: k // 100].to(dev)] *= 20.0
+    x = x.to(torch.bfloat16)
+    us = _median_us(lambda: awq.awq_linear(x, quant))
+    fl = 2.0 * m * n * k
+    res[f"awq_int4_g128 {k}->{n} M={m}"] = {
+        "us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4)}
+    return res
 
 
 if __name__ == "__main__":
