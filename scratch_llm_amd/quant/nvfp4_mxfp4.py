@@ -31,8 +31,11 @@ __all__ = [
     "e2m1_decode",
     "e2m1_round_to_code",
     "fp4_linear_tiled",
+    "MXFP4_GROUP",
+    "dequantize_mxfp4",
     "mxfp4_dequantize",
     "mxfp4_gemm",
+    "mxfp4_pack_weight",
     "mxfp4_linear",
     "mxfp4_quantize",
     "mxfp4_quantize_tiled",
@@ -45,6 +48,7 @@ __all__ = [
     "quantize_e8m0",
     "sqnr_db",
     "tile_fp4",
+    "tile_mxfp4_packed",
     "unpack_fp4",
 ]
 
@@ -356,6 +360,82 @@ _tiled_cache = _device.TensorKeyedCache()
 def _tiled(q: MXFP4Tensor | NVFP4Tensor) -> FP4Tiled:
     keys = (q.codes, q.s_block) if isinstance(q, MXFP4Tensor) else (q.codes, q.s_block, q.s_global)
     return _tiled_cache.get(keys, (type(q).__name__, tuple(q.shape), q.block), lambda: tile_fp4(q))
+
+
+# --------------------------------------------------------------------------------------
+# The on-disk MXFP4 pair (compressed-tensors mxfp4-pack-quantized, k3/checkpoint.py:92-144)
+# --------------------------------------------------------------------------------------
+MXFP4_GROUP = 32
+_E8M0_NAN = 0xFF
+
+
+def _check_mxfp4_pair(weight_packed: Tensor, weight_scale: Tensor) -> tuple[int, int]:
+    """The reference loader's checks (k3/checkpoint.py:124-137), same messages."""
+    if weight_packed.dtype != torch.uint8 or weight_scale.dtype != torch.uint8:
+        raise ValueError(f"MXFP4 halves must be uint8; got {weight_packed.dtype}, {weight_scale.dtype}")
+    if weight_packed.ndim != 2:
+        raise ValueError(f"weight_packed must be [out, in/2]; got {tuple(weight_packed.shape)}")
+    rows, cols = int(weight_packed.shape[0]), 2 * int(weight_packed.shape[1])
+    groups = cols // MXFP4_GROUP
+    if cols % MXFP4_GROUP or tuple(weight_scale.shape) != (rows, groups):
+        raise ValueError(
+            f"weight_packed {tuple(weight_packed.shape)} encodes [{rows}, {cols}], which needs "
+            f"in % {MXFP4_GROUP} == 0 and weight_scale [{rows}, {groups}]; "
+            f"got weight_scale {tuple(weight_scale.shape)}"
+        )
+    if bool((weight_scale == _E8M0_NAN).any()):
+        raise ValueError("E8M0 scale 0xFF is NaN; refusing to load")
+    return rows, cols
+
+
+def mxfp4_pack_weight(q: MXFP4Tensor) -> tuple[Tensor, Tensor]:
+    """A 2-D MXFP4 weight (block 32) as the on-disk pair: ``weight_packed`` uint8 ``[out, in/2]`` (low
+    nibble = even element, ``pack_fp4`` order) and ``weight_scale`` uint8 E8M0 ``[out, in/32]``, the
+    exponent byte of each power-of-two block scale."""
+    if len(q.shape) != 2 or q.block != MXFP4_GROUP or int(q.shape[1]) % MXFP4_GROUP:
+        raise ValueError(f"the on-disk MXFP4 pair needs a 2-D weight with in % 32 == 0 and block 32, got "
+                         f"shape {tuple(q.shape)} and block {q.block}")
+    rows, cols = int(q.shape[0]), int(q.shape[1])
+    packed = pack_fp4(q.codes.reshape(-1)).reshape(rows, cols // 2)
+    # a normal power of two 2**e has exponent field e + 127 (scales are >= 2**-99, never subnormal)
+    e8 = ((q.s_block.to(torch.float32).contiguous().view(torch.int32) >> 23) & 0xFF).to(torch.uint8)
+    return packed, e8.reshape(rows, cols // MXFP4_GROUP)
+
+
+def tile_mxfp4_packed(weight_packed: Tensor, weight_scale: Tensor) -> FP4Tiled:
+    """The tiled layout of the linear kernels straight from the on-disk pair (no repack on the host)."""
+    rows, cols = _check_mxfp4_pair(weight_packed, weight_scale)
+    dev = _lib.require_device(weight_packed, weight_scale, fn="tile_mxfp4_packed")
+    lib = _lib.load()
+    wp, ws = weight_packed.contiguous(), weight_scale.contiguous()
+    wt = torch.empty(lib.sqx_fp4_tiled_weight_bytes(rows, cols), dtype=torch.uint8, device=dev)
+    st = torch.empty(lib.sqx_fp4_tiled_scale_bytes(rows, cols, _lib.FP4_MX), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(lib.sqx_fp4_tile(wp.data_ptr(), 1, ws.data_ptr(), _lib.FP4_SCALE_MX_E8M0, MXFP4_GROUP, rows, cols,
+                                    wt.data_ptr(), st.data_ptr(), _stream(wp)), "tile_mxfp4_packed")
+    return FP4Tiled(wt, st, _lib.FP4_MX, None, rows, cols)
+
+
+def dequantize_mxfp4(weight_packed: Tensor, weight_scale: Tensor, *, dtype: torch.dtype = torch.float32) -> Tensor:
+    """``w[r, c] = E2M1(code[r, c]) * 2**(weight_scale[r, c // 32] - 127)`` as ``[out, in]`` in ``dtype``
+    (k3/checkpoint.py:92-144): the E2M1 decode and the scaling run in the HIP kernels in fp32, where every
+    value below 2**128 is exact (E8M0 code 0 is 2**-127, a subnormal); values that overflow fp32, and
+    casts to ``dtype`` that change a value, raise ``ValueError`` as in the reference."""
+    rows, cols = _check_mxfp4_pair(weight_packed, weight_scale)
+    _lib.require_device(weight_packed, weight_scale, fn="dequantize_mxfp4")
+    codes = unpack_fp4(weight_packed.reshape(-1), rows * cols)
+    b = weight_scale.reshape(-1).to(torch.int32)
+    s_block = torch.where(b == 0, torch.full_like(b, 0x00400000), b << 23).view(torch.float32)
+    q = MXFP4Tensor(codes.reshape(-1, MXFP4_GROUP), s_block, torch.Size((rows, cols)), rows * cols, MXFP4_GROUP)
+    out = mxfp4_dequantize(q)
+    if not bool(torch.isfinite(out).all()):
+        raise ValueError(f"MXFP4 values are not exact in {dtype} (overflow or underflow)")
+    if dtype == torch.float32:
+        return out
+    cast = out.to(dtype)
+    if not torch.equal(cast.to(torch.float32), out):
+        raise ValueError(f"MXFP4 values are not exact in {dtype} (overflow or underflow)")
+    return cast
 
 
 def mxfp4_quantize_tiled(x: Tensor) -> FP4Tiled:

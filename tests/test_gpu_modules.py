@@ -1,0 +1,170 @@
+"""Drop-in modules on the MI355X: conversion of a model holding both nn.Linear and the reference's
+bias-free model.Linear shape, each module's forward against F.linear with its own
+``dequantized_weight()`` cast to the activation dtype (the reference composition), and the on-disk
+MXFP4 pair loaded straight into the kernel layout against the oracle restatement of
+k3/checkpoint.py:92-144 and the reference's named byte values (tests/test_k3_checkpoint.py:281-292).
+
+Tolerance: max-abs-rel <= 1e-2 (the north star's linear bar) and, elementwise, the bound the
+reference composition's own roundings imply: its bf16 weights are within 2**-9 of the dequantized
+weight (|dy| <= 2**-9 sum_k |x_k w_k|), fp32 accumulation adds at most (k/32 + 8) 2**-24 sum_k |x_k w_k|
+and the bf16 output half an ulp (2**-8 |y| allowed). AWQ rounds x / s to bf16 once more (another
+2**-9 sum_k |x_k w_k|)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from oracle import quant_ref as R
+from tests.conftest import print_case
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def mods():
+    from scratch_llm_amd import _lib
+    from scratch_llm_amd.quant import modules
+
+    _lib.load()
+    return modules
+
+
+class Linear(nn.Module):
+    """Shaped like the reference's model.Linear (model.py:125-133)."""
+
+    def __init__(self, i: int, o: int) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.randn(o, i) * 0.02)
+
+    def forward(self, x):
+        return x @ self.weight.T
+
+
+class Block(nn.Module):
+    def __init__(self, d: int, f: int) -> None:
+        super().__init__()
+        self.wq = Linear(d, d)
+        self.up = nn.Linear(d, f)
+        self.down = nn.Linear(f, d, bias=False)
+
+
+class Toy(nn.Module):
+    def __init__(self, d: int = 256, f: int = 512) -> None:
+        super().__init__()
+        self.embed = nn.Embedding(32, d)
+        self.blocks = nn.ModuleList([Block(d, f), Block(d, f)])
+        self.lm_head = nn.Linear(d, 32)
+
+
+EXPECTED = ["blocks.0.wq", "blocks.0.up", "blocks.0.down", "blocks.1.wq", "blocks.1.up", "blocks.1.down"]
+
+
+def _check(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, what: str,
+           weight_terms: int = 1) -> None:
+    """y against F.linear(x, w.to(bf16), bias) in float64 (x, w the values the reference multiplies)."""
+    x64 = x.double().cpu()
+    w64 = w.double().cpu()
+    y_ref = x64 @ w.to(torch.bfloat16).double().cpu().T
+    if bias is not None:
+        y_ref = y_ref + bias.double().cpu()
+    mag = x64.abs() @ w64.abs().T
+    k = x.shape[-1]
+    yv = y.double().cpu()
+    assert torch.isfinite(yv).all(), what
+    err = (yv - y_ref).abs()
+    rel = float(err.max() / y_ref.abs().max())
+    assert rel <= 1e-2, f"{what}: max-abs-rel {rel:.3e}"
+    bound = (weight_terms * 2.0**-9 + (k / 32 + 8) * 2.0**-24) * mag + 2.0**-8 * y_ref.abs() + 1e-30
+    assert float((err / bound).max()) <= 1.0, f"{what}: elementwise bound {float((err / bound).max()):.2f}x"
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8", "mxfp4", "mxfp4_act", "nvfp4"])
+@pytest.mark.parametrize("m", [1, 5, 96])
+def test_convert_and_forward(mods, fmt, m):
+    print_case("modules", fmt, f"m={m}")
+    torch.manual_seed(7)
+    model = Toy().to(DEV)
+    conv = {
+        "int4": lambda r: mods.convert_linears_to_int4(r),
+        "int8": lambda r: mods.convert_linears_to_int8(r),
+        "mxfp4": lambda r: mods.convert_linears_to_mxfp4(r),
+        "mxfp4_act": lambda r: mods.convert_linears_to_mxfp4(r, quantize_activations=True),
+        "nvfp4": lambda r: mods.convert_linears_to_nvfp4(r),
+    }[fmt]
+    assert conv(model) == EXPECTED
+    assert isinstance(model.lm_head, nn.Linear)
+    x = torch.randn(m, 256, device=DEV).to(torch.bfloat16)
+    for name in EXPECTED:
+        mod = model.get_submodule(name)
+        xin = x if mod.in_features == 256 else torch.randn(m, mod.in_features, device=DEV).to(torch.bfloat16)
+        y = mod(xin)
+        torch.cuda.synchronize()
+        assert y.shape == (m, mod.out_features) and y.dtype == torch.bfloat16
+        xr = xin
+        if fmt == "mxfp4_act":  # the reference composition also dequantizes the MXFP4-quantized activations
+            from scratch_llm_amd.quant import nvfp4_mxfp4 as f4
+
+            xr = f4.mxfp4_dequantize(f4.mxfp4_quantize(xin, 32)).to(torch.bfloat16)
+        _check(y, xr, mod.dequantized_weight(), mod.bias, f"{fmt} {name} m={m}")
+
+
+def test_awq_module(mods):
+    print_case("awq module")
+    torch.manual_seed(3)
+    model = Toy().to(DEV)
+    scales = {"wq": torch.exp(torch.empty(256, device=DEV).uniform_(-0.69, 0.69)),
+              "up": torch.exp(torch.empty(256, device=DEV).uniform_(-0.69, 0.69))}
+    calib = {"down": torch.randn(64, 512, device=DEV)}
+    names = mods.convert_linears_to_awq(model, scales, calib=calib)
+    assert names == EXPECTED
+    for name in EXPECTED:
+        mod = model.get_submodule(name)
+        x = torch.randn(9, mod.in_features, device=DEV).to(torch.bfloat16)
+        y = mod(x)
+        _check(y, x, mod.dequantized_weight(), mod.bias, f"awq {name}", weight_terms=2)
+
+
+def test_mxfp4_pair_loads_straight_into_the_kernel(mods):
+    """Every byte against every scale code (the pattern of tests/test_k3_checkpoint.py:260-277):
+    dequantized_weight() equals the oracle's k3 decode exactly, and the linear runs on the pair."""
+    from scratch_llm_amd.quant import nvfp4_mxfp4 as f4
+
+    n = 253  # scale codes 0..252: 6 * 2**(252 - 127) stays finite in fp32 and bf16
+    packed = torch.arange(256, dtype=torch.uint8).repeat(n, 1)
+    scale = ((torch.arange(n)[:, None] + torch.arange(16)[None, :]) % n).to(torch.uint8)
+    want = R.dequantize_mxfp4_checkpoint(packed.numpy(), scale.numpy())
+    mod = mods.MXFP4Linear.from_packed(packed.to(DEV), scale.to(DEV))
+    got = mod.dequantized_weight()
+    torch.cuda.synchronize()
+    assert got.dtype == torch.float32 and got.shape == (n, 512)
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), want.astype(np.float32).view(np.uint32))
+    # the named values: 0x80 = (+0, -0), 0x7F = (-6, +6), 0x21 = (1/2, 1); scale 0 is 2**-127
+    p = torch.zeros(3, 16, dtype=torch.uint8)
+    p[:, :3] = torch.tensor([0x80, 0x7F, 0x21], dtype=torch.uint8)
+    sc = torch.tensor([[127], [0], [252]], dtype=torch.uint8)
+    w = f4.dequantize_mxfp4(p.to(DEV), sc.to(DEV)).cpu()
+    assert w[0, :6].tolist() == [0.0, -0.0, -6.0, 6.0, 0.5, 1.0]
+    assert not w[0, 0].signbit() and w[0, 1].signbit()
+    assert w[1, 4].item() == 2.0**-128 and w[1, 3].item() == 6 * 2.0**-127
+    with pytest.raises(ValueError, match="not exact"):
+        f4.dequantize_mxfp4(torch.full((1, 16), 0x07, dtype=torch.uint8, device=DEV),
+                            torch.full((1, 1), 254, dtype=torch.uint8, device=DEV))
+    # a linear on realistic scales: the pair of a quantized N(0, 0.02) weight
+    wt = torch.randn(384, 1024, device=DEV) * 0.02
+    q = f4.mxfp4_quantize(wt, 32)
+    pk, e8 = f4.mxfp4_pack_weight(q)
+    lin = mods.MXFP4Linear.from_packed(pk, e8)
+    assert torch.equal(lin.dequantized_weight(), f4.mxfp4_dequantize(q))
+    x = torch.randn(7, 1024, device=DEV).to(torch.bfloat16)
+    _check(lin(x), x, f4.mxfp4_dequantize(q), None, "pair")
+
+
+def test_modules_refuse_cpu_input(mods):
+    model = Toy().to(DEV)
+    mods.convert_linears_to_int8(model)
+    with pytest.raises(RuntimeError):
+        model.blocks[0].up(torch.randn(2, 256))
