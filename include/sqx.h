@@ -327,6 +327,58 @@ int sqx_int8_linear(const uint8_t* wt, const float* scale, const void* x, int ac
                     const void* bias, int64_t m, int64_t rows, int64_t cols, int k_slices,
                     sqx_stream_t stream);
 
+/* ============================================================================================
+ * Decode step around the quantized linears: the ops that src/scratch_llm/
+ * model.py runs between the Linear calls of one token, against the dense slot KV cache of
+ * kv_cache.py:234-262 (BatchedKVCache). Activations are bf16 rows; lengths[b] (int32) is the slot's
+ * valid length before this step's write (SlotKVCache.lengths, kv_cache.py:126). All arithmetic is
+ * fp32 with one round-to-nearest-even to bf16 per written tensor.
+ * ============================================================================================ */
+
+/* RMSNorm (model.py:148-162) with the residual add before it (TransformerBlock.forward,
+ * model.py:394-403): with delta, h = bf16(x + delta) is written to h_out; without, h = x.
+ * y = bf16(h * (1 / sqrt(mean(h^2) + eps)) * w). x, delta, h_out, y: bf16 [rows, d]; w: bf16 [d];
+ * d % 8 == 0; 16-byte aligned. h_out must not alias x or delta. */
+int sqx_rmsnorm(const void* x, const void* delta, const void* w, float eps, int64_t rows, int64_t d,
+                void* h_out, void* y, sqx_stream_t stream);
+
+/* RoPE of q and k (RotaryPositionalEmbedding.forward, model.py:205-224: interleaved pairs, position
+ * lengths[b], fp32 cos/sin tables [rope_rows, hd/2]) and the cache write of SlotKVCache.write_decode
+ * (kv_cache.py:194-205, at min(lengths[b], tmax - 1)). qkv: bf16 [B, (H + 2 Hkv) hd] laid out
+ * [q | k | v]; q_out: bf16 [B, H, hd]; k_cache, v_cache: bf16 [B, Hkv, tmax, hd]. */
+int sqx_rope_kv(const void* qkv, const int* lengths, const float* cos_t, const float* sin_t,
+                int64_t rope_rows, int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax,
+                void* q_out, void* k_cache, void* v_cache, sqx_stream_t stream);
+
+/* Keys per workgroup of sqx_decode_attention, and the bytes of fp32 workspace it needs. */
+int sqx_attn_chunk(int64_t B, int64_t Hkv, int64_t tmax);
+int64_t sqx_attn_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t tmax);
+
+/* One-token GQA attention over the slot cache (MultiHeadSelfAttention.forward's SlotKVCache branch,
+ * model.py:281-305 and :313-349): out[b, h] = softmax(q[b,h] k[b,h/G]^T / sqrt(hd)) v[b,h/G] over the
+ * keys j <= lengths[b] (G = H / Hkv in {1, 2, 4, 8}; hd == 128). out: bf16 [B, H * hd]. Split over
+ * the keys into fp32 partials in ws (sqx_attn_workspace_bytes) and combined in a second launch. */
+int sqx_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* lengths,
+                         int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws,
+                         int64_t ws_bytes, sqx_stream_t stream);
+
+/* SwiGLU's gate (model.py:227-237): out = bf16(silu(g) * u) from gate_up = bf16 [B, 2F] laid out
+ * [g | u] (the w1 and w3 outputs side by side); out: bf16 [B, F]. */
+int sqx_silu_mul(const void* gate_up, int64_t B, int64_t F, void* out, sqx_stream_t stream);
+
+/* Embedding.forward (model.py:136-145): out[b] = table[tokens[b]]; table bf16 [V, d]. An id outside
+ * [0, V) gives a zero row (the reference raises; callers validate host-side ids). */
+int sqx_embed(const void* table, int64_t V, const int* tokens, int64_t B, int64_t d, void* out,
+              sqx_stream_t stream);
+
+/* Greedy pick (sampling.py:80-83, temperature 0): next_tok[b] = first index of the maximum of the bf16
+ * logits [B, V], NaN counting as the maximum (torch.argmax). */
+int sqx_argmax(const void* logits, int64_t B, int64_t V, int* next_tok, sqx_stream_t stream);
+
+/* SlotKVCache.advance(1) (kv_cache.py:207-213): lengths[b] += 1 where active[b] != 0 (every row when
+ * active is NULL). */
+int sqx_advance(int* lengths, const uint8_t* active, int64_t B, sqx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -102,6 +102,21 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sqx_col_absmean": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_awq_scale": (_c_i, [_c_p, _c_i64, ctypes.c_float, _c_p, _c_p]),
     "sqx_scale_columns": (_c_i, [_c_p, _c_i, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_rmsnorm": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "sqx_rope_kv": (
+        _c_i,
+        [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p],
+    ),
+    "sqx_attn_chunk": (_c_i, [_c_i64, _c_i64, _c_i64]),
+    "sqx_attn_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "sqx_decode_attention": (
+        _c_i,
+        [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p],
+    ),
+    "sqx_silu_mul": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_embed": (_c_i, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_argmax": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_advance": (_c_i, [_c_p, _c_p, _c_i64, _c_p]),
 }
 
 _lock = threading.Lock()

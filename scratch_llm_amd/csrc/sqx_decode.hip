@@ -1,0 +1,509 @@
+// The non-linear ops of one Llama-shaped decode step, fused for MI355X. They are
+// the callers around the quantized linears in src/scratch_llm/model.py: RMSNorm (:148-162), the
+// residual adds of TransformerBlock.forward (:394-403), RoPE (:185-224), SwiGLU's gate (:227-237),
+// decode attention against a slot KV cache (:262-366 with kv_cache.py:80-262) and the greedy pick of
+// sampling.py:80-86.
+//
+// Layouts: activation rows are bf16 [B, width]. The KV cache of one layer is two bf16 tensors
+// [B, Hkv, Tmax, hd] (kv_cache.py:234-262, BatchedKVCache). lengths[b] (int32) is the number of
+// valid positions of slot b before this step's write (kv_cache.py:126): the new key/value lands at
+// min(lengths[b], Tmax - 1), RoPE uses position lengths[b], and the row attends keys
+// j <= lengths[b] (write-then-mask, model.py:293-305). All arithmetic is fp32; each written tensor
+// is rounded to bf16 once (round to nearest even).
+#include "sqx_common.h"
+
+namespace sqx {
+
+// all-lane sums over 16 lanes (one DPP row) and over the wave
+__device__ inline float row16_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));  // row_ror:8
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));  // row_ror:4
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));   // quad_perm 2301
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));   // quad_perm 1032
+  return v;
+}
+
+__device__ inline float wave_sum(float v) {
+  v = row16_sum(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ inline float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ inline float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// ---------------------------------------------------------------------------------------------
+// Residual add + RMSNorm. With delta: h = bf16(x + delta) is written to h_out and normalised;
+// without: h = x. y = bf16(h * (1 / sqrt(mean(h^2) + eps)) * w), the product taken left to right in
+// fp32 as model.py:158-162 does. One workgroup of 256 threads per row; d % 8 == 0.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ delta,
+                                                      const uint16_t* __restrict__ w, float eps, int d,
+                                                      uint16_t* __restrict__ h_out, uint16_t* __restrict__ y) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * d;
+  float ss = 0.0f;
+  for (int c = threadIdx.x * 8; c < d; c += 256 * 8) {
+    u32x4_t v = *reinterpret_cast<const u32x4_t*>(xr + c);
+    if (delta != nullptr) {
+      const u32x4_t dv = *reinterpret_cast<const u32x4_t*>(delta + row * d + c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = ActBF16::pack_rne(bf16_lo(v[j]) + bf16_lo(dv[j]), bf16_hi(v[j]) + bf16_hi(dv[j]));
+      *reinterpret_cast<u32x4_t*>(h_out + row * d + c) = v;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a0 = bf16_lo(v[j]), a1 = bf16_hi(v[j]);
+      ss = fmaf(a0, a0, ss);
+      ss = fmaf(a1, a1, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float total = (red[0] + red[1]) + (red[2] + red[3]);
+  const float r = 1.0f / sqrtf(total / static_cast<float>(d) + eps);
+  const uint16_t* hr = delta != nullptr ? h_out + row * d : xr;
+  for (int c = threadIdx.x * 8; c < d; c += 256 * 8) {
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(hr + c);
+    const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(w + c);
+    u32x4_t o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = ActBF16::pack_rne(bf16_lo(v[j]) * r * bf16_lo(wv[j]), bf16_hi(v[j]) * r * bf16_hi(wv[j]));
+    *reinterpret_cast<u32x4_t*>(y + row * d + c) = o;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// RoPE + KV-cache write. The fused projection row is qkv = [q (H*hd) | k (Hkv*hd) | v (Hkv*hd)].
+// Pair (x_2i, x_2i+1) of a q or k head becomes (x_2i cos - x_2i+1 sin, x_2i sin + x_2i+1 cos) with
+// cos/sin the fp32 tables [rope_rows, hd/2] at position lengths[b] (model.py:196-224; the products
+// and sums are separate fp32 roundings, as the reference's tensor ops are). q goes to q_out
+// [B, H, hd]; k and v go into the cache at min(lengths[b], Tmax - 1). One thread per pair.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rope_kv_kernel(const uint16_t* __restrict__ qkv, const int* __restrict__ lengths,
+                                                      const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                                      int rope_rows, int H, int Hkv, int hd, int tmax,
+                                                      uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
+                                                      uint16_t* __restrict__ vc) {
+#pragma clang fp contract(off)
+  const int b = blockIdx.y;
+  const int width = (H + 2 * Hkv) * hd;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (2 * i >= width) return;
+  const int len = lengths[b];
+  const int p = min(max(len, 0), rope_rows - 1);
+  const int slot = min(max(len, 0), tmax - 1);
+  const uint32_t two = *reinterpret_cast<const uint32_t*>(qkv + static_cast<int64_t>(b) * width + 2 * i);
+  const int head = (2 * i) / hd, c = (2 * i) % hd;
+  if (head < H + Hkv) {
+    const float x0 = bf16_lo(two), x1 = bf16_hi(two);
+    const float cs = cos_t[static_cast<int64_t>(p) * (hd / 2) + c / 2];
+    const float sn = sin_t[static_cast<int64_t>(p) * (hd / 2) + c / 2];
+    const float e = x0 * cs - x1 * sn;
+    const float o = x0 * sn + x1 * cs;
+    const uint32_t r = ActBF16::pack_rne(e, o);
+    if (head < H) {
+      *reinterpret_cast<uint32_t*>(q_out + (static_cast<int64_t>(b) * H + head) * hd + c) = r;
+    } else {
+      const int64_t at = ((static_cast<int64_t>(b) * Hkv + (head - H)) * tmax + slot) * hd + c;
+      *reinterpret_cast<uint32_t*>(kc + at) = r;
+    }
+  } else {
+    const int64_t at = ((static_cast<int64_t>(b) * Hkv + (head - H - Hkv)) * tmax + slot) * hd + c;
+    *reinterpret_cast<uint32_t*>(vc + at) = two;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Decode attention, split over the keys (flash decoding). softmax(q k^T / sqrt(hd)) v over the keys
+// j <= lengths[b] of kv head kh for its G = H / Hkv query heads (GQA: query head h reads kv head
+// h / G, the repeat_interleave of model.py:315-318).
+//
+// Workgroup (chunk, kh, b) takes keys [chunk*C, chunk*C + C) and writes, per query head, the fp32
+// partial (m, l, o[hd]) of that range: m the maximum score (log2 units: scores are scaled by
+// log2(e) / sqrt(hd) so that the exponentials are exp2), l = sum 2^(s - m), o = sum 2^(s - m) v.
+// Each of the 4 waves walks its own quarter of the range 16 keys at a time: lane group kl = lane/16
+// holds keys base + 4u + kl (u < 4) and each lane 8 of the 128 dims, so one load instruction of the
+// wave reads 4 consecutive 256-byte key rows. A lane group keeps its own running (m, l, o); the
+// groups and the waves are merged at the end. hd must be 128.
+// ---------------------------------------------------------------------------------------------
+constexpr int kHd = 128;
+constexpr int kKeysPerStep = 16;
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+                                                           const uint16_t* __restrict__ vc, const int* __restrict__ lengths,
+                                                           int H, int Hkv, int tmax, int chunk, int nchunk,
+                                                           float qscale, float* __restrict__ part) {
+  const int ch = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  const int L = min(max(lengths[b], 0) + 1, tmax);
+  const int t0 = ch * chunk;
+  if (t0 >= L) return;  // the combine reads only chunks below L
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kl = lane >> 4, dl = lane & 15;
+  const int span = chunk / 4;
+  const int ws = t0 + wave * span, we = min(ws + span, L);
+
+  __shared__ float sm[4][G], sl[4][G];
+  __shared__ float so[4][G][kHd];
+
+  float qv[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(q + (static_cast<int64_t>(b) * H + kh * G + g) * kHd + dl * 8);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qv[g][2 * j] = bf16_lo(v[j]) * qscale;
+      qv[g][2 * j + 1] = bf16_hi(v[j]) * qscale;
+    }
+  }
+  float m[G], l[G], o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[g][j] = 0.0f;
+  }
+  const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd;
+  const uint16_t* kb = kc + head_off + dl * 8;
+  const uint16_t* vb = vc + head_off + dl * 8;
+
+  for (int base = ws; base < we; base += kKeysPerStep) {
+    u32x4_t kr[4], vr[4];
+    bool ok[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = base + 4 * u + kl;
+      ok[u] = t < we;
+      const int tc = ok[u] ? t : base;  // an in-range row; its score is masked below
+      kr[u] = *reinterpret_cast<const u32x4_t*>(kb + static_cast<int64_t>(tc) * kHd);
+      vr[u] = *reinterpret_cast<const u32x4_t*>(vb + static_cast<int64_t>(tc) * kHd);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float s[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc = fmaf(qv[g][2 * j], bf16_lo(kr[u][j]), acc);
+          acc = fmaf(qv[g][2 * j + 1], bf16_hi(kr[u][j]), acc);
+        }
+        s[u] = ok[u] ? row16_sum(acc) : -INFINITY;
+      }
+      const float mn = fmaxf(fmaxf(m[g], fmaxf(s[0], s[1])), fmaxf(s[2], s[3]));
+      // a group whose keys are all masked so far keeps m = -inf and adds nothing
+      const float a = mn == -INFINITY ? 1.0f : exp2f(m[g] - mn);
+      float p[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) p[u] = ok[u] ? exp2f(s[u] - mn) : 0.0f;
+      l[g] = fmaf(l[g], a, (p[0] + p[1]) + (p[2] + p[3]));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float e0 = o[g][2 * j] * a, e1 = o[g][2 * j + 1] * a;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          e0 = fmaf(p[u], bf16_lo(vr[u][j]), e0);
+          e1 = fmaf(p[u], bf16_hi(vr[u][j]), e1);
+        }
+        o[g][2 * j] = e0;
+        o[g][2 * j + 1] = e1;
+      }
+      m[g] = mn;
+    }
+  }
+  // merge the 4 lane groups of the wave (lane bits 4 and 5)
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int off = 16; off < 64; off <<= 1) {
+      const float mo = __shfl_xor(m[g], off, 64), lo = __shfl_xor(l[g], off, 64);
+      const float mn = fmaxf(m[g], mo);
+      const float a = m[g] == -INFINITY ? 0.0f : exp2f(m[g] - mn);
+      const float c = mo == -INFINITY ? 0.0f : exp2f(mo - mn);
+      l[g] = l[g] * a + lo * c;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[g][j] = o[g][j] * a + __shfl_xor(o[g][j], off, 64) * c;
+      m[g] = mn;
+    }
+  }
+  if (kl == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (dl == 0) {
+        sm[wave][g] = m[g];
+        sl[wave][g] = l[g];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) so[wave][g][dl * 8 + j] = o[g][j];
+    }
+  }
+  __syncthreads();
+  // merge the 4 waves: thread (g, dd) writes element dd of head g's partial
+  for (int idx = threadIdx.x; idx < G * kHd; idx += 256) {
+    const int g = idx / kHd, dd = idx % kHd;
+    const float M = fmaxf(fmaxf(sm[0][g], sm[1][g]), fmaxf(sm[2][g], sm[3][g]));
+    float lsum = 0.0f, osum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float a = sm[w][g] == -INFINITY ? 0.0f : exp2f(sm[w][g] - M);
+      lsum = fmaf(sl[w][g], a, lsum);
+      osum = fmaf(so[w][g][dd], a, osum);
+    }
+    float* pp = part + ((static_cast<int64_t>(b) * H + kh * G + g) * nchunk + ch) * (kHd + 2);
+    if (dd == 0) {
+      pp[0] = M;
+      pp[1] = lsum;
+    }
+    pp[2 + dd] = osum;
+  }
+}
+
+// out[b, h*hd + d] = bf16(sum_c 2^(m_c - M) o_c[d] / sum_c 2^(m_c - M) l_c) over the chunks c that
+// hold keys of row b. Row layout [B, H*hd] is the (B, 1, H*hd) view that o_proj takes (model.py:365).
+__global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ part, const int* __restrict__ lengths,
+                                                           int H, int tmax, int chunk, int nchunk,
+                                                           uint16_t* __restrict__ out) {
+  const int h = blockIdx.x, b = blockIdx.y, dd = threadIdx.x;
+  const int L = min(max(lengths[b], 0) + 1, tmax);
+  const int used = (L + chunk - 1) / chunk;
+  const float* base = part + (static_cast<int64_t>(b) * H + h) * nchunk * (kHd + 2);
+  float M = -INFINITY;
+  for (int c = 0; c < used; ++c) M = fmaxf(M, base[c * (kHd + 2)]);
+  float lsum = 0.0f, osum = 0.0f;
+  for (int c = 0; c < used; ++c) {
+    const float* p = base + c * (kHd + 2);
+    const float a = p[0] == -INFINITY ? 0.0f : exp2f(p[0] - M);
+    lsum = fmaf(p[1], a, lsum);
+    osum = fmaf(p[2 + dd], a, osum);
+  }
+  out[(static_cast<int64_t>(b) * H + h) * kHd + dd] = f32_to_bf16_bits(osum / lsum);
+}
+
+// ---------------------------------------------------------------------------------------------
+// SwiGLU gate: out = bf16(silu(g) * u), silu(g) = g / (1 + e^-g), from the fused projection row
+// [g (F) | u (F)] (model.py:227-237 with w1 = gate, w3 = up). Two elements per thread.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu, int F, int64_t n,
+                                                       uint16_t* __restrict__ out) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 2;
+  if (i >= n) return;
+  const int64_t b = i / F, c = i % F;
+  const uint32_t g2 = *reinterpret_cast<const uint32_t*>(gu + b * 2 * F + c);
+  const uint32_t u2 = *reinterpret_cast<const uint32_t*>(gu + b * 2 * F + F + c);
+  const float g0 = bf16_lo(g2), g1 = bf16_hi(g2);
+  const float r0 = g0 / (1.0f + __expf(-g0)) * bf16_lo(u2);
+  const float r1 = g1 / (1.0f + __expf(-g1)) * bf16_hi(u2);
+  *reinterpret_cast<uint32_t*>(out + i) = ActBF16::pack_rne(r0, r1);
+}
+
+// Embedding rows out[b] = table[tokens[b]] (model.py:136-145). An id outside [0, V) gives a zero row.
+__global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__ table, const int* __restrict__ tok,
+                                                    int64_t V, int d, uint16_t* __restrict__ out) {
+  const int b = blockIdx.x;
+  const int t = tok[b];
+  const bool ok = t >= 0 && t < V;
+  const uint16_t* src = table + (ok ? static_cast<int64_t>(t) : 0) * d;
+  for (int c = threadIdx.x * 8; c < d; c += 256 * 8) {
+    u32x4_t v = *reinterpret_cast<const u32x4_t*>(src + c);
+    if (!ok) v = u32x4_t{0, 0, 0, 0};
+    *reinterpret_cast<u32x4_t*>(out + static_cast<int64_t>(b) * d + c) = v;
+  }
+}
+
+// Greedy pick: next_tok[b] = the first index of the maximum of logits[b] (torch.argmax; a NaN
+// counts as the maximum, sampling.py:82-83).
+__device__ inline bool argmax_takes(float ov, int oi, float cv, int ci) {
+  const bool on = ov != ov, cn = cv != cv;
+  if (on || cn) return on && (!cn || oi < ci);
+  return ov > cv || (ov == cv && oi < ci);
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const uint16_t* __restrict__ logits, int64_t V,
+                                                     int* __restrict__ next_tok) {
+  __shared__ float bv[256];
+  __shared__ int bi[256];
+  const int b = blockIdx.x;
+  float best = -INFINITY;
+  int idx = 0x7fffffff;
+  for (int64_t v = threadIdx.x; v < V; v += 256) {
+    const float x = bf16_bits_to_f32(logits[static_cast<int64_t>(b) * V + v]);
+    if (argmax_takes(x, static_cast<int>(v), best, idx)) {
+      best = x;
+      idx = static_cast<int>(v);
+    }
+  }
+  bv[threadIdx.x] = best;
+  bi[threadIdx.x] = idx;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s && argmax_takes(bv[threadIdx.x + s], bi[threadIdx.x + s], bv[threadIdx.x], bi[threadIdx.x])) {
+      bv[threadIdx.x] = bv[threadIdx.x + s];
+      bi[threadIdx.x] = bi[threadIdx.x + s];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) next_tok[b] = bi[0];
+}
+
+// SlotKVCache.advance(1) (kv_cache.py:207-213): lengths[b] += 1 for active rows (all rows when
+// active is null).
+__global__ void advance_kernel(int* __restrict__ lengths, const uint8_t* __restrict__ active, int B) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < B && (active == nullptr || active[b] != 0)) lengths[b] += 1;
+}
+
+}  // namespace sqx
+
+using namespace sqx;
+
+// ==============================================================================================
+// extern "C" entry points
+// ==============================================================================================
+static bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+extern "C" int sqx_rmsnorm(const void* x, const void* delta, const void* w, float eps, int64_t rows, int64_t d,
+                           void* h_out, void* y, sqx_stream_t stream) {
+  SQX_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && rows < (int64_t(1) << 31) && d < (int64_t(1) << 30), SQX_E_ARG,
+              "sqx_rmsnorm: bad shape [%lld, %lld] (d must be a multiple of 8)", (long long)rows, (long long)d);
+  if (rows == 0) return SQX_OK;
+  SQX_REQUIRE(x && w && y && (delta == nullptr || h_out != nullptr), SQX_E_ARG, "sqx_rmsnorm: null pointer");
+  SQX_REQUIRE(al16(x) && al16(w) && al16(y) && al16(delta) && al16(h_out), SQX_E_ARG,
+              "sqx_rmsnorm: pointers must be 16-byte aligned");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(delta),
+                     static_cast<const uint16_t*>(w), eps, static_cast<int>(d), static_cast<uint16_t*>(h_out),
+                     static_cast<uint16_t*>(y));
+  SQX_LAUNCH_CHECK("sqx_rmsnorm");
+  return SQX_OK;
+}
+
+extern "C" int sqx_rope_kv(const void* qkv, const int* lengths, const float* cos_t, const float* sin_t,
+                           int64_t rope_rows, int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax,
+                           void* q_out, void* k_cache, void* v_cache, sqx_stream_t stream) {
+  SQX_REQUIRE(B >= 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && hd > 0 && hd % 2 == 0 && tmax > 0 && rope_rows > 0,
+              SQX_E_ARG, "sqx_rope_kv: bad shape");
+  SQX_REQUIRE(B < 65536 && (H + 2 * Hkv) * hd < (int64_t(1) << 30) && rope_rows < (int64_t(1) << 31) &&
+                  tmax < (int64_t(1) << 31),
+              SQX_E_ARG, "sqx_rope_kv: shape too large");
+  if (B == 0) return SQX_OK;
+  SQX_REQUIRE(qkv && lengths && cos_t && sin_t && q_out && k_cache && v_cache, SQX_E_ARG, "sqx_rope_kv: null pointer");
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(qkv) % 4 == 0 && reinterpret_cast<uintptr_t>(q_out) % 4 == 0 &&
+                  reinterpret_cast<uintptr_t>(k_cache) % 4 == 0 && reinterpret_cast<uintptr_t>(v_cache) % 4 == 0,
+              SQX_E_ARG, "sqx_rope_kv: bf16 buffers must be 4-byte aligned");
+  const int64_t pairs = (H + 2 * Hkv) * hd / 2;
+  hipLaunchKernelGGL(rope_kv_kernel, dim3(static_cast<unsigned>(ceil_div(pairs, 256)), static_cast<unsigned>(B)),
+                     dim3(256), 0, as_stream(stream), static_cast<const uint16_t*>(qkv), lengths, cos_t, sin_t,
+                     static_cast<int>(rope_rows), static_cast<int>(H), static_cast<int>(Hkv), static_cast<int>(hd),
+                     static_cast<int>(tmax), static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache),
+                     static_cast<uint16_t*>(v_cache));
+  SQX_LAUNCH_CHECK("sqx_rope_kv");
+  return SQX_OK;
+}
+
+// Keys per workgroup: the smallest of 64..512 that still gives about 2048 workgroups.
+extern "C" int sqx_attn_chunk(int64_t B, int64_t Hkv, int64_t tmax) {
+  int c = 64;
+  while (c < 512 && B * Hkv * ceil_div(tmax, 2 * c) >= 2048) c *= 2;
+  return c;
+}
+
+extern "C" int64_t sqx_attn_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t tmax) {
+  if (B <= 0 || H <= 0 || Hkv <= 0 || tmax <= 0) return 0;
+  return B * H * ceil_div(tmax, sqx_attn_chunk(B, Hkv, tmax)) * (kHd + 2) * 4;
+}
+
+extern "C" int sqx_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* lengths,
+                                    int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax, void* out,
+                                    void* ws, int64_t ws_bytes, sqx_stream_t stream) {
+  SQX_REQUIRE(hd == kHd, SQX_E_ARG, "sqx_decode_attention: head_dim %lld is not supported (128)", (long long)hd);
+  SQX_REQUIRE(B >= 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && tmax > 0, SQX_E_ARG, "sqx_decode_attention: bad shape");
+  SQX_REQUIRE(B < 65536 && Hkv < 65536 && tmax < (int64_t(1) << 30), SQX_E_ARG, "sqx_decode_attention: shape too large");
+  const int G = static_cast<int>(H / Hkv);
+  SQX_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, SQX_E_ARG,
+              "sqx_decode_attention: %d query heads per kv head (1, 2, 4 or 8 are built)", G);
+  if (B == 0) return SQX_OK;
+  SQX_REQUIRE(q && k_cache && v_cache && lengths && out && ws, SQX_E_ARG, "sqx_decode_attention: null pointer");
+  SQX_REQUIRE(ws_bytes >= sqx_attn_workspace_bytes(B, H, Hkv, tmax), SQX_E_SPACE,
+              "sqx_decode_attention: workspace of %lld bytes, %lld needed", (long long)ws_bytes,
+              (long long)sqx_attn_workspace_bytes(B, H, Hkv, tmax));
+  SQX_REQUIRE(al16(q) && al16(k_cache) && al16(v_cache) && al16(ws), SQX_E_ARG,
+              "sqx_decode_attention: q, caches and workspace must be 16-byte aligned");
+  const int chunk = sqx_attn_chunk(B, Hkv, tmax);
+  const int nchunk = static_cast<int>(ceil_div(tmax, chunk));
+  hipStream_t s = as_stream(stream);
+  const float qscale = 1.4426950408889634f / sqrtf(static_cast<float>(hd));  // log2(e) / sqrt(hd)
+  const dim3 grid(static_cast<unsigned>(nchunk), static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
+  const auto* qp = static_cast<const uint16_t*>(q);
+  const auto* kp = static_cast<const uint16_t*>(k_cache);
+  const auto* vp = static_cast<const uint16_t*>(v_cache);
+  float* w = static_cast<float*>(ws);
+  const int iH = static_cast<int>(H), iK = static_cast<int>(Hkv), iT = static_cast<int>(tmax);
+#define SQX_ATTN(G_) \
+  hipLaunchKernelGGL(attn_partial_kernel<G_>, grid, dim3(256), 0, s, qp, kp, vp, lengths, iH, iK, iT, chunk, nchunk, qscale, w)
+  switch (G) {
+    case 1: SQX_ATTN(1); break;
+    case 2: SQX_ATTN(2); break;
+    case 4: SQX_ATTN(4); break;
+    default: SQX_ATTN(8); break;
+  }
+#undef SQX_ATTN
+  SQX_LAUNCH_CHECK("sqx_decode_attention");
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(B)), dim3(kHd), 0, s, w,
+                     lengths, iH, iT, chunk, nchunk, static_cast<uint16_t*>(out));
+  SQX_LAUNCH_CHECK("sqx_decode_attention");
+  return SQX_OK;
+}
+
+extern "C" int sqx_silu_mul(const void* gate_up, int64_t B, int64_t F, void* out, sqx_stream_t stream) {
+  SQX_REQUIRE(B >= 0 && F > 0 && F % 2 == 0 && B * F < (int64_t(1) << 40), SQX_E_ARG,
+              "sqx_silu_mul: bad shape (F must be even)");
+  if (B == 0) return SQX_OK;
+  SQX_REQUIRE(gate_up && out, SQX_E_ARG, "sqx_silu_mul: null pointer");
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(gate_up) % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 4 == 0, SQX_E_ARG,
+              "sqx_silu_mul: pointers must be 4-byte aligned");
+  const int64_t n = B * F;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(ceil_div(n / 2, 256))), dim3(256), 0,
+                     as_stream(stream), static_cast<const uint16_t*>(gate_up), static_cast<int>(F), n,
+                     static_cast<uint16_t*>(out));
+  SQX_LAUNCH_CHECK("sqx_silu_mul");
+  return SQX_OK;
+}
+
+extern "C" int sqx_embed(const void* table, int64_t V, const int* tokens, int64_t B, int64_t d, void* out,
+                         sqx_stream_t stream) {
+  SQX_REQUIRE(B >= 0 && V > 0 && d > 0 && d % 8 == 0 && B < (int64_t(1) << 31) && d < (int64_t(1) << 30), SQX_E_ARG,
+              "sqx_embed: bad shape (d must be a multiple of 8)");
+  if (B == 0) return SQX_OK;
+  SQX_REQUIRE(table && tokens && out, SQX_E_ARG, "sqx_embed: null pointer");
+  SQX_REQUIRE(al16(table) && al16(out), SQX_E_ARG, "sqx_embed: table and out must be 16-byte aligned");
+  hipLaunchKernelGGL(embed_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint16_t*>(table), tokens, V, static_cast<int>(d), static_cast<uint16_t*>(out));
+  SQX_LAUNCH_CHECK("sqx_embed");
+  return SQX_OK;
+}
+
+extern "C" int sqx_argmax(const void* logits, int64_t B, int64_t V, int* next_tok, sqx_stream_t stream) {
+  SQX_REQUIRE(B >= 0 && V > 0 && B < (int64_t(1) << 31) && V < (int64_t(1) << 31), SQX_E_ARG, "sqx_argmax: bad shape");
+  if (B == 0) return SQX_OK;
+  SQX_REQUIRE(logits && next_tok, SQX_E_ARG, "sqx_argmax: null pointer");
+  hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint16_t*>(logits), V, next_tok);
+  SQX_LAUNCH_CHECK("sqx_argmax");
+  return SQX_OK;
+}
+
+extern "C" int sqx_advance(int* lengths, const uint8_t* active, int64_t B, sqx_stream_t stream) {
+  SQX_REQUIRE(B >= 0 && B < (int64_t(1) << 31), SQX_E_ARG, "sqx_advance: bad B");
+  if (B == 0) return SQX_OK;
+  SQX_REQUIRE(lengths != nullptr, SQX_E_ARG, "sqx_advance: null lengths");
+  hipLaunchKernelGGL(advance_kernel, dim3(static_cast<unsigned>(ceil_div(B, 256))), dim3(256), 0, as_stream(stream),
+                     lengths, active, static_cast<int>(B));
+  SQX_LAUNCH_CHECK("sqx_advance");
+  return SQX_OK;
+}

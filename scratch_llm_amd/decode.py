@@ -1,0 +1,311 @@
+"""One decode step of a Llama-shaped model whose linears are INT4-g128, on MI355X.
+
+The reference decodes by calling ``TransformerLM.forward`` (src/scratch_llm/model.py:439-505) with
+one token per row against a slot KV cache (kv_cache.py:80-262, dense ``BatchedKVCache`` storage)
+and picking the next token greedily (sampling.py:80-83); with the quantized drop-ins every Linear
+is ``w4a16_linear`` (int4_group.py:148-164). This module is that step on the library's kernels:
+
+* the INT4 linears on the tiled weights (the streaming decode kernel below 64 rows, the
+  dequant-GEMM from 64 rows), with q|k|v fused into one projection and gate|up into another
+  (concatenating rows keeps every group scale: groups run along the input dimension);
+* everything between them from sqx_decode.hip: residual add + RMSNorm, RoPE + cache write,
+  split-key GQA attention, SiLU-gate, embedding rows, greedy pick, ``advance``.
+
+A step allocates nothing: :class:`DecodeState` holds the cache and every buffer for one batch
+size, so :meth:`Int4DecodeLM.capture` can record the whole step in a HIP graph whose replays
+decode token after token (the pick of one replay is the input of the next).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Callable
+
+import torch
+from torch import Tensor
+
+from scratch_llm_amd import _lib
+from scratch_llm_amd.quant import int4_group as i4
+
+__all__ = ["DecodeConfig", "DecodeState", "Int4DecodeLM", "LLAMA3_8B", "rope_tables"]
+
+
+@dataclass(frozen=True)
+class DecodeConfig:
+    """Architecture of the decoded model (the fields of model.py:57-112 that a decode step reads)."""
+
+    vocab_size: int = 128256
+    d_model: int = 4096
+    n_layers: int = 32
+    n_heads: int = 32
+    n_kv_heads: int = 8
+    d_ff: int = 14336
+    context_length: int = 2048
+    rope_theta: float = 10000.0
+    norm_eps: float = 1e-5
+    group_size: int = 128
+
+    @property
+    def head_dim(self) -> int:
+        return self.d_model // self.n_heads
+
+    def validate(self) -> None:
+        if self.d_model % self.n_heads != 0:
+            raise ValueError(f"d_model={self.d_model} not divisible by n_heads={self.n_heads}")
+        if self.n_heads % self.n_kv_heads != 0:
+            raise ValueError(f"n_heads={self.n_heads} not divisible by n_kv_heads={self.n_kv_heads}")
+        if self.head_dim != 128:
+            raise ValueError(f"head_dim={self.head_dim}: the decode attention kernel is built for 128")
+        if self.n_heads // self.n_kv_heads not in (1, 2, 4, 8):
+            raise ValueError(f"{self.n_heads // self.n_kv_heads} query heads per kv head (1, 2, 4 or 8 are built)")
+        for name, k in (("d_model", self.d_model), ("d_ff", self.d_ff)):
+            if k % self.group_size != 0:
+                raise ValueError(f"{name}={k} not divisible by group_size={self.group_size}")
+
+
+LLAMA3_8B = DecodeConfig()
+
+
+def rope_tables(head_dim: int, max_seq_len: int, theta: float) -> tuple[Tensor, Tensor]:
+    """cos/sin [max_seq_len, head_dim/2] fp32, computed on the host exactly as the reference's
+    RotaryPositionalEmbedding buffers are (model.py:196-202, built on the CPU at construction)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2).float() / head_dim))
+    positions = torch.arange(max_seq_len).float()
+    freqs = torch.outer(positions, inv_freq)
+    return freqs.cos(), freqs.sin()
+
+
+@dataclass
+class _Layer:
+    attn_norm: Tensor
+    wqkv: i4.Int4Tiled
+    wo: i4.Int4Tiled
+    ffn_norm: Tensor
+    w13: i4.Int4Tiled
+    w2: i4.Int4Tiled
+
+
+class DecodeState:
+    """The slot cache and the step's buffers for one batch size (BatchedKVCache, kv_cache.py:234-262).
+
+    ``k``/``v``: bf16 ``[n_layers, B, Hkv, max_ctx, hd]``; ``lengths`` int32 ``[B]`` (valid positions
+    before the next write); ``active`` uint8 ``[B]`` (rows that ``advance`` bumps); ``tokens`` int32
+    ``[B]``: the step's input ids, overwritten by its greedy picks; ``logits`` bf16 ``[B, vocab]``.
+    """
+
+    def __init__(self, model: "Int4DecodeLM", batch: int, max_ctx: int) -> None:
+        cfg, dev = model.cfg, model.device
+        if batch < 1 or max_ctx < 1:
+            raise ValueError("batch and max_ctx must be >= 1")
+        if max_ctx > cfg.context_length:
+            raise ValueError(f"max_ctx={max_ctx} exceeds context_length={cfg.context_length}")
+        self.batch, self.max_ctx = batch, max_ctx
+        hkv, hd, d = cfg.n_kv_heads, cfg.head_dim, cfg.d_model
+        shape = (cfg.n_layers, batch, hkv, max_ctx, hd)
+        self.k = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+        self.v = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+        self.lengths = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.active = torch.ones(batch, dtype=torch.uint8, device=dev)
+        self.tokens = torch.zeros(batch, dtype=torch.int32, device=dev)
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.x = [torch.empty(batch, d, **bf), torch.empty(batch, d, **bf)]  # residual stream (ping-pong)
+        self.h = torch.empty(batch, d, **bf)  # normalised input of the next projection
+        self.delta = torch.empty(batch, d, **bf)  # o_proj / w2 output
+        self.qkv = torch.empty(batch, (cfg.n_heads + 2 * hkv) * hd, **bf)
+        self.q = torch.empty(batch, cfg.n_heads * hd, **bf)
+        self.attn = torch.empty(batch, cfg.n_heads * hd, **bf)
+        self.gu = torch.empty(batch, 2 * cfg.d_ff, **bf)
+        self.act = torch.empty(batch, cfg.d_ff, **bf)
+        self.logits = torch.empty(batch, cfg.vocab_size, **bf)
+        lib = _lib.load()
+        nb = int(lib.sqx_attn_workspace_bytes(batch, cfg.n_heads, hkv, max_ctx))
+        self.attn_ws = torch.empty(max(nb // 4, 4), dtype=torch.float32, device=dev)
+        gw = 0
+        if batch >= i4.GEMM_MIN_M:
+            for tw in model.linears():
+                gw = max(gw, int(lib.sqx_gemm_workspace_bytes(batch, tw.rows, tw.cols)))
+        self.gemm_ws = torch.empty(max(gw // 4, 4), dtype=torch.float32, device=dev) if gw > 0 else None
+
+    def set_lengths(self, lengths) -> None:
+        """Set every slot's valid length (a host list or tensor), e.g. after filling the cache."""
+        t = torch.as_tensor(lengths, dtype=torch.int32)
+        if t.shape != (self.batch,) or bool((t < 0).any()) or bool((t > self.max_ctx).any()):
+            raise ValueError(f"lengths must be {self.batch} values in [0, {self.max_ctx}]")
+        self.lengths.copy_(t)
+
+    def set_tokens(self, tokens, vocab_size: int) -> None:
+        t = torch.as_tensor(tokens, dtype=torch.int64)
+        if t.shape != (self.batch,):
+            raise ValueError(f"expected {self.batch} token ids, got shape {tuple(t.shape)}")
+        if t.device.type == "cpu" and (bool((t < 0).any()) or bool((t >= vocab_size).any())):
+            raise IndexError(f"token id out of range [0, {vocab_size})")
+        self.tokens.copy_(t.to(torch.int32))
+
+
+class Int4DecodeLM:
+    """A TransformerLM (model.py:439-505) with every Linear, the LM head included, in the reference's
+    symmetric INT4-g128 format, decoding on one MI355X."""
+
+    def __init__(self, cfg: DecodeConfig, embed: Tensor, layers: list[_Layer], final_norm: Tensor,
+                 lm_head: i4.Int4Tiled) -> None:
+        cfg.validate()
+        self.cfg = cfg
+        self.embed = embed
+        self.layers = layers
+        self.final_norm = final_norm
+        self.lm_head = lm_head
+        self.device = embed.device
+        cos, sin = rope_tables(cfg.head_dim, cfg.context_length, cfg.rope_theta)
+        self.cos = cos.to(self.device)
+        self.sin = sin.to(self.device)
+
+    # ------------------------------------------------------------------ construction
+    @classmethod
+    def from_state_dict(cls, cfg: DecodeConfig, get: Callable[[str], Tensor], device: torch.device | str) -> "Int4DecodeLM":
+        """Quantize a float model given by its reference parameter names (``token_emb.weight``,
+        ``blocks.{i}.attn.{q,k,v,o}_proj.weight``, ``blocks.{i}.ffn.{w1,w2,w3}.weight``,
+        ``blocks.{i}.{attn,ffn}_norm.weight``, ``final_norm.weight``, ``lm_head.weight``; model.py:
+        125-133, 148-156, 227-253, 372-392, 439-452). ``get(name)`` returns the tensor; each weight
+        is quantized on the device with quantize_groupwise_int4 (bit-exact with int4_group.py:108-129)."""
+        cfg.validate()
+        dev = torch.device(device)
+        g = cfg.group_size
+
+        def qw(*names: str) -> i4.Int4Tiled:
+            qs = [i4.quantize_groupwise_int4(get(n).to(dev, torch.float32), g) for n in names]
+            q = torch.cat([a for a, _ in qs]) if len(qs) > 1 else qs[0][0]
+            s = torch.cat([b for _, b in qs]) if len(qs) > 1 else qs[0][1]
+            return i4.tile_int4(q, s, None, g)
+
+        def vec(name: str) -> Tensor:
+            return get(name).to(dev, torch.bfloat16).contiguous()
+
+        layers = []
+        for i in range(cfg.n_layers):
+            p = f"blocks.{i}."
+            layers.append(_Layer(
+                attn_norm=vec(p + "attn_norm.weight"),
+                wqkv=qw(p + "attn.q_proj.weight", p + "attn.k_proj.weight", p + "attn.v_proj.weight"),
+                wo=qw(p + "attn.o_proj.weight"),
+                ffn_norm=vec(p + "ffn_norm.weight"),
+                w13=qw(p + "ffn.w1.weight", p + "ffn.w3.weight"),
+                w2=qw(p + "ffn.w2.weight"),
+            ))
+        embed = get("token_emb.weight").to(dev, torch.bfloat16).contiguous()
+        return cls(cfg, embed, layers, vec("final_norm.weight"), qw("lm_head.weight"))
+
+    @classmethod
+    def random_init(cls, cfg: DecodeConfig, device: torch.device | str, seed: int = 0, std: float = 0.02) -> "Int4DecodeLM":
+        """Synthetic weights of the configured shape: linears ~N(0, std) in fp32, generated and
+        quantized one at a time on the device; embedding ~N(0, 1); norm gains 1 (model.py:153)."""
+        dev = torch.device(device)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        hd = cfg.head_dim
+        shapes = {
+            "attn.q_proj.weight": (cfg.n_heads * hd, cfg.d_model),
+            "attn.k_proj.weight": (cfg.n_kv_heads * hd, cfg.d_model),
+            "attn.v_proj.weight": (cfg.n_kv_heads * hd, cfg.d_model),
+            "attn.o_proj.weight": (cfg.d_model, cfg.n_heads * hd),
+            "ffn.w1.weight": (cfg.d_ff, cfg.d_model),
+            "ffn.w3.weight": (cfg.d_ff, cfg.d_model),
+            "ffn.w2.weight": (cfg.d_model, cfg.d_ff),
+        }
+
+        def get(name: str) -> Tensor:
+            if name.endswith("norm.weight"):
+                return torch.ones(cfg.d_model, device=dev)
+            if name == "token_emb.weight":
+                return torch.randn(cfg.vocab_size, cfg.d_model, device=dev, generator=gen)
+            if name == "lm_head.weight":
+                return torch.randn(cfg.vocab_size, cfg.d_model, device=dev, generator=gen) * std
+            return torch.randn(shapes[name.split(".", 2)[2]], device=dev, generator=gen) * std
+
+        return cls.from_state_dict(cfg, get, dev)
+
+    # ------------------------------------------------------------------ queries
+    def linears(self) -> list[i4.Int4Tiled]:
+        out = []
+        for ly in self.layers:
+            out += [ly.wqkv, ly.wo, ly.w13, ly.w2]
+        return out + [self.lm_head]
+
+    def weight_bytes(self) -> int:
+        """HBM bytes one step streams for weights (tiled codes, scales, norm gains)."""
+        return sum(tw.nbytes for tw in self.linears()) + sum(
+            ly.attn_norm.numel() * 2 + ly.ffn_norm.numel() * 2 for ly in self.layers
+        ) + self.final_norm.numel() * 2
+
+    def new_state(self, batch: int, max_ctx: int | None = None) -> DecodeState:
+        return DecodeState(self, batch, self.cfg.context_length if max_ctx is None else max_ctx)
+
+    # ------------------------------------------------------------------ the step
+    def _linear(self, st: DecodeState, tw: i4.Int4Tiled, x: Tensor, y: Tensor, stream: int) -> None:
+        lib = _lib.load()
+        m = st.batch
+        if m >= i4.GEMM_MIN_M:
+            rc = lib.sqx_int4_gemm(
+                tw.wt.data_ptr(), tw.st.data_ptr(), None, _lib.DTYPE_F32, x.data_ptr(), _lib.DTYPE_BF16,
+                y.data_ptr(), None, m, tw.rows, tw.cols, tw.group_size, *_lib.ws_args(st.gemm_ws), stream,
+            )
+        else:
+            rc = lib.sqx_int4_linear(
+                tw.wt.data_ptr(), tw.st.data_ptr(), None, _lib.DTYPE_F32, x.data_ptr(), _lib.DTYPE_BF16,
+                y.data_ptr(), None, m, tw.rows, tw.cols, tw.group_size, 0, stream,
+            )
+        _lib.check(rc, "int4 linear")
+
+    def step(self, st: DecodeState, tokens=None) -> Tensor:
+        """Decode one token per row: logits of ``st.tokens`` (or ``tokens``) at each row's position,
+        written to ``st.logits``; the greedy picks replace ``st.tokens``; active rows advance. Returns
+        ``st.tokens``. Only device work is issued (no host synchronisation)."""
+        cfg, lib = self.cfg, _lib.load()
+        if tokens is not None:
+            st.set_tokens(tokens, cfg.vocab_size)
+        _lib.require_device(st.tokens, self.embed, fn="Int4DecodeLM.step")
+        B, d, H, Hkv, hd, T = st.batch, cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, st.max_ctx
+        s = _lib.stream_ptr(self.device)
+        ck = _lib.check
+        with torch.cuda.device(self.device):
+            ck(lib.sqx_embed(self.embed.data_ptr(), cfg.vocab_size, st.tokens.data_ptr(), B, d, st.x[0].data_ptr(), s),
+               "embed")
+            cur, delta = 0, None
+            for li, ly in enumerate(self.layers):
+                for norm, sub in ((ly.attn_norm, 0), (ly.ffn_norm, 1)):
+                    if delta is None:
+                        ck(lib.sqx_rmsnorm(st.x[cur].data_ptr(), None, norm.data_ptr(), cfg.norm_eps, B, d, None,
+                                           st.h.data_ptr(), s), "rmsnorm")
+                    else:
+                        ck(lib.sqx_rmsnorm(st.x[cur].data_ptr(), delta, norm.data_ptr(), cfg.norm_eps, B, d,
+                                           st.x[1 - cur].data_ptr(), st.h.data_ptr(), s), "rmsnorm")
+                        cur = 1 - cur
+                    if sub == 0:
+                        self._linear(st, ly.wqkv, st.h, st.qkv, s)
+                        ck(lib.sqx_rope_kv(st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(),
+                                           self.sin.data_ptr(), cfg.context_length, B, H, Hkv, hd, T,
+                                           st.q.data_ptr(), st.k[li].data_ptr(), st.v[li].data_ptr(), s), "rope_kv")
+                        ck(lib.sqx_decode_attention(st.q.data_ptr(), st.k[li].data_ptr(), st.v[li].data_ptr(),
+                                                    st.lengths.data_ptr(), B, H, Hkv, hd, T, st.attn.data_ptr(),
+                                                    st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention")
+                        self._linear(st, ly.wo, st.attn, st.delta, s)
+                    else:
+                        self._linear(st, ly.w13, st.h, st.gu, s)
+                        ck(lib.sqx_silu_mul(st.gu.data_ptr(), B, cfg.d_ff, st.act.data_ptr(), s), "silu_mul")
+                        self._linear(st, ly.w2, st.act, st.delta, s)
+                    delta = st.delta.data_ptr()
+            ck(lib.sqx_rmsnorm(st.x[cur].data_ptr(), delta, self.final_norm.data_ptr(), cfg.norm_eps, B, d,
+                               st.x[1 - cur].data_ptr(), st.h.data_ptr(), s), "rmsnorm")
+            self._linear(st, self.lm_head, st.h, st.logits, s)
+            ck(lib.sqx_argmax(st.logits.data_ptr(), B, cfg.vocab_size, st.tokens.data_ptr(), s), "argmax")
+            ck(lib.sqx_advance(st.lengths.data_ptr(), st.active.data_ptr(), B, s), "advance")
+        return st.tokens
+
+    def capture(self, st: DecodeState) -> torch.cuda.CUDAGraph:
+        """Record one :meth:`step` on ``st`` in a HIP graph. Each ``replay()`` decodes the next token
+        from ``st.tokens`` and the cache as they are at that moment. Capturing runs nothing, so ``st``
+        is unchanged."""
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.device(self.device), torch.cuda.graph(g):
+            self.step(st)
+        return g

@@ -1,0 +1,311 @@
+"""Decode step on the MI355X: each kernel of sqx_decode.hip through the C ABI
+against the CPU restatement of the reference op (oracle/decode_ref.py), then the whole step of
+scratch_llm_amd.decode against the oracle's bf16 composition and fp32 run of the same INT4 model.
+
+Bars:
+  residual add, RoPE, cache write, embedding, argmax, advance: bit-exact (same fp32 operations,
+    one rounding to bf16).
+  RMSNorm: within one bf16 ulp of the reference formula evaluated on the CPU (the mean's summation
+    order and 1/sqrt differ), and bit-exact on at least 99 % of elements.
+  attention, SiLU-gate: |err| <= 2**-8 |ref| + 1e-5 max|v| against float64 (one bf16 rounding of
+    an fp32 computation).
+  decode step: logits no further from the fp32 run than 2x the reference bf16 composition's own
+    distance (plus 2**-9 of the logit range), and greedy picks equal to fp32's wherever fp32's
+    top-2 margin exceeds 4x the observed error.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import decode_ref as D
+from tests.conftest import print_case
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from scratch_llm_amd import _lib
+
+    return _lib.load()
+
+
+def _s():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ok(lib, rc):
+    assert rc == 0, lib.sqx_last_error().decode()
+
+
+def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    a = x.abs().clamp_min(2.0**-126)
+    return torch.exp2(torch.floor(torch.log2(a)) - 7)
+
+
+# ---------------------------------------------------------------------------------------------
+# kernels
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,d", [(1, 4096), (7, 1024), (64, 4096), (3, 8)])
+def test_rmsnorm(lib, rows, d):
+    print_case("rmsnorm", rows, d)
+    g = torch.Generator().manual_seed(rows * 7 + d)
+    x = (torch.randn(rows, d, generator=g) * 3).bfloat16()
+    dl = torch.randn(rows, d, generator=g).bfloat16()
+    w = (1 + 0.1 * torch.randn(d, generator=g)).bfloat16()
+    xd, dd, wd = x.to(DEV), dl.to(DEV), w.to(DEV)
+    h, y, y0 = (torch.empty(rows, d, dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    _ok(lib, lib.sqx_rmsnorm(xd.data_ptr(), dd.data_ptr(), wd.data_ptr(), 1e-5, rows, d, h.data_ptr(), y.data_ptr(), _s()))
+    _ok(lib, lib.sqx_rmsnorm(xd.data_ptr(), None, wd.data_ptr(), 1e-5, rows, d, None, y0.data_ptr(), _s()))
+    torch.cuda.synchronize()
+    assert torch.equal(h.cpu(), x + dl)  # bf16 + bf16: fp32 sum, one rounding (model.py:402)
+    for got, src in ((y.cpu(), x + dl), (y0.cpu(), x)):
+        want = D.rmsnorm(src, w, 1e-5)
+        diff = (got.float() - want.float()).abs()
+        assert bool((diff <= _bf16_ulp(want.float())).all())
+        assert float((diff == 0).float().mean()) >= 0.99
+
+
+@pytest.mark.parametrize("H,Hkv", [(32, 8), (8, 8), (16, 2)])
+def test_rope_kv(lib, H, Hkv):
+    print_case("rope_kv", H, Hkv)
+    hd, T, ctx = 128, 40, 64
+    lengths = [3, 0, T - 1, T + 5, 63][: 5]
+    B = len(lengths)
+    g = torch.Generator().manual_seed(H + Hkv)
+    qkv = (torch.randn(B, (H + 2 * Hkv) * hd, generator=g) * 2).bfloat16()
+    cos, sin = D.rope_tables(hd, ctx, 10000.0)
+    kc = torch.randn(B, Hkv, T, hd, generator=g).bfloat16()
+    vc = torch.randn(B, Hkv, T, hd, generator=g).bfloat16()
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    q = torch.empty(B, H, hd, dtype=torch.bfloat16, device=DEV)
+    ln = torch.tensor(lengths, dtype=torch.int32, device=DEV)
+    cd, sd = cos.to(DEV), sin.to(DEV)
+    _ok(lib, lib.sqx_rope_kv(qkv.to(DEV).data_ptr(), ln.data_ptr(), cd.data_ptr(), sd.data_ptr(), ctx, B, H, Hkv, hd,
+                             T, q.data_ptr(), kd.data_ptr(), vd.data_ptr(), _s()))
+    torch.cuda.synchronize()
+    pos = torch.tensor(lengths).unsqueeze(1)
+    qr = D.rope(qkv[:, : H * hd].view(B, 1, H, hd).transpose(1, 2), pos, cos, sin)
+    kr = D.rope(qkv[:, H * hd: (H + Hkv) * hd].view(B, 1, Hkv, hd).transpose(1, 2), pos, cos, sin)
+    vr = qkv[:, (H + Hkv) * hd:].view(B, 1, Hkv, hd).transpose(1, 2)
+    assert torch.equal(q.cpu(), qr[:, :, 0])
+    want_k, want_v = kc.clone(), vc.clone()
+    cache = D.RefCache([want_k], [want_v], torch.tensor(lengths), torch.ones(B, dtype=torch.bool))
+    cache.write_decode(0, kr, vr)
+    assert torch.equal(kd.cpu(), want_k)
+    assert torch.equal(vd.cpu(), want_v)
+
+
+def _attn_case(lib, B, H, Hkv, T, lengths, seed):
+    hd = 128
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, H, hd, generator=g) * 2).bfloat16()
+    k = (torch.randn(B, Hkv, T, hd, generator=g) * 2).bfloat16()
+    v = torch.randn(B, Hkv, T, hd, generator=g).bfloat16()
+    ln = torch.tensor(lengths, dtype=torch.int32, device=DEV)
+    out = torch.empty(B, H * hd, dtype=torch.bfloat16, device=DEV)
+    nb = lib.sqx_attn_workspace_bytes(B, H, Hkv, T)
+    ws = torch.empty(nb // 4, dtype=torch.float32, device=DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    _ok(lib, lib.sqx_decode_attention(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), ln.data_ptr(), B, H, Hkv, hd, T,
+                                      out.data_ptr(), ws.data_ptr(), nb, _s()))
+    torch.cuda.synchronize()
+    G = H // Hkv
+    got = out.cpu().view(B, H, hd).double()
+    for b in range(B):
+        L = min(max(lengths[b], 0) + 1, T)
+        kk = k[b, :, :L].double().repeat_interleave(G, dim=0)
+        vv = v[b, :, :L].double().repeat_interleave(G, dim=0)
+        s = torch.einsum("hd,htd->ht", q[b].double(), kk) / math.sqrt(hd)
+        p = torch.softmax(s, dim=-1)
+        want = torch.einsum("ht,htd->hd", p, vv)
+        err = (got[b] - want).abs()
+        bound = 2.0**-8 * want.abs() + 1e-5 * vv.abs().max()
+        assert float((err / bound).max()) <= 1.0, f"row {b} (L={L}): {float((err / bound).max()):.2f}x the bound"
+
+
+@pytest.mark.parametrize("H,Hkv", [(32, 8), (8, 8), (16, 8), (16, 2)])
+def test_attention_ragged(lib, H, Hkv):
+    print_case("attention", H, Hkv)
+    T = 300
+    _attn_case(lib, 6, H, Hkv, T, [0, 1, 16, 255, T - 1, T + 7], seed=H * 10 + Hkv)
+
+
+@pytest.mark.parametrize("B", [1, 8, 64])
+def test_attention_config5_context(lib, B):
+    """Llama-3-8B heads at the config-5 context: 2048 keys (lengths 2047), plus ragged rows."""
+    print_case("attention config5", B)
+    T = 2048
+    lengths = [T - 1] * B
+    if B > 1:
+        lengths[1] = 1000
+    _attn_case(lib, B, 32, 8, T, lengths, seed=B)
+
+
+def test_attention_rejects_bad_shapes(lib):
+    ws = torch.empty(16, dtype=torch.float32, device=DEV)
+    assert lib.sqx_decode_attention(ws.data_ptr(), ws.data_ptr(), ws.data_ptr(), ws.data_ptr(), 1, 32, 8, 64, 16, ws.data_ptr(),
+                                    ws.data_ptr(), 64, _s()) == -1
+    assert lib.sqx_decode_attention(ws.data_ptr(), ws.data_ptr(), ws.data_ptr(), ws.data_ptr(), 1, 48, 8, 128, 16,
+                                    ws.data_ptr(), ws.data_ptr(), 64, _s()) == -1
+    assert lib.sqx_decode_attention(ws.data_ptr(), ws.data_ptr(), ws.data_ptr(), ws.data_ptr(), 4, 32, 8, 128, 2048,
+                                    ws.data_ptr(), ws.data_ptr(), 64, _s()) == -3
+
+
+@pytest.mark.parametrize("B,F", [(1, 14336), (5, 96), (64, 2048)])
+def test_silu_mul(lib, B, F):
+    print_case("silu_mul", B, F)
+    g = torch.Generator().manual_seed(F)
+    gu = (torch.randn(B, 2 * F, generator=g) * 4).bfloat16()
+    gu[0, :4] = torch.tensor([0.0, -0.0, 80.0, -80.0]).bfloat16()
+    out = torch.empty(B, F, dtype=torch.bfloat16, device=DEV)
+    _ok(lib, lib.sqx_silu_mul(gu.to(DEV).data_ptr(), B, F, out.data_ptr(), _s()))
+    torch.cuda.synchronize()
+    gg, uu = gu[:, :F].double(), gu[:, F:].double()
+    want = gg * torch.sigmoid(gg) * uu
+    err = (out.cpu().double() - want).abs()
+    assert bool((err <= 2.0**-8 * want.abs() + 1e-30).all())
+
+
+def test_embed_argmax_advance(lib):
+    print_case("embed/argmax/advance")
+    V, d, B = 1000, 256, 5
+    table = torch.randn(V, d).bfloat16()
+    tok = torch.tensor([0, 999, 17, -1, 1000], dtype=torch.int32)
+    td = table.to(DEV)
+    out = torch.empty(B, d, dtype=torch.bfloat16, device=DEV)
+    _ok(lib, lib.sqx_embed(td.data_ptr(), V, tok.to(DEV).data_ptr(), B, d, out.data_ptr(), _s()))
+    torch.cuda.synchronize()
+    o = out.cpu()
+    assert torch.equal(o[:3], table[tok[:3].long()])
+    assert not o[3:].any()  # out-of-range ids give zero rows
+    # argmax: first index of the maximum, NaN wins, at the config-5 vocabulary
+    for Vv in (128256, 7, 300):
+        lg = torch.randn(6, Vv).bfloat16()
+        lg[1, :] = 0.0  # all tied -> 0
+        lg[2, Vv // 3] = 100.0
+        lg[2, Vv - 1] = 100.0  # tie -> the first
+        lg[3, Vv // 2] = float("nan")
+        lg[3, Vv - 1] = float("nan")
+        lg[4, :] = float("-inf")
+        nt = torch.empty(6, dtype=torch.int32, device=DEV)
+        _ok(lib, lib.sqx_argmax(lg.to(DEV).data_ptr(), 6, Vv, nt.data_ptr(), _s()))
+        torch.cuda.synchronize()
+        assert nt.cpu().tolist() == lg.float().argmax(dim=-1).tolist()
+    # advance: named values of tests/test_batched_cache.py:91-103
+    ln = torch.tensor([4, 2, 0], dtype=torch.int32, device=DEV)
+    act = torch.tensor([1, 0, 1], dtype=torch.uint8, device=DEV)
+    _ok(lib, lib.sqx_advance(ln.data_ptr(), act.data_ptr(), 3, _s()))
+    torch.cuda.synchronize()
+    assert ln.cpu().tolist() == [5, 2, 1]
+    _ok(lib, lib.sqx_advance(ln.data_ptr(), None, 3, _s()))
+    torch.cuda.synchronize()
+    assert ln.cpu().tolist() == [6, 3, 2]
+
+
+# ---------------------------------------------------------------------------------------------
+# the whole step
+# ---------------------------------------------------------------------------------------------
+SMALL = dict(vocab=1000, d_model=1024, n_layers=2, n_heads=8, n_kv_heads=2, d_ff=2048)
+
+
+@pytest.fixture(scope="module")
+def small():
+    from scratch_llm_amd.decode import DecodeConfig, Int4DecodeLM
+
+    p = D.random_params(**SMALL, seed=11, std=0.05)
+    cfg = DecodeConfig(vocab_size=SMALL["vocab"], d_model=SMALL["d_model"], n_layers=SMALL["n_layers"],
+                       n_heads=SMALL["n_heads"], n_kv_heads=SMALL["n_kv_heads"], d_ff=SMALL["d_ff"],
+                       context_length=64)
+    model = Int4DecodeLM.from_state_dict(cfg, lambda n: p[n], DEV)
+    refs = {dt: D.int4_model(p, n_layers=cfg.n_layers, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
+                             context_length=cfg.context_length, dtype=dt) for dt in (torch.bfloat16, torch.float32)}
+    return model, refs
+
+
+def _run_and_compare(model, refs, B, steps, seed, max_ctx=48):
+    g = torch.Generator().manual_seed(seed)
+    st = model.new_state(B, max_ctx)
+    caches = {dt: D.RefCache.empty(r, B, max_ctx, dt) for dt, r in refs.items()}
+    tok = torch.randint(0, model.cfg.vocab_size, (B,), generator=g)
+    for t in range(steps):
+        print_case("decode step", f"B={B}", f"t={t}")
+        nxt = model.step(st, tok)
+        torch.cuda.synchronize()
+        got = st.logits.float().cpu()
+        l16 = D.decode_step(refs[torch.bfloat16], caches[torch.bfloat16], tok, torch.bfloat16).float()
+        l32 = D.decode_step(refs[torch.float32], caches[torch.float32], tok, torch.float32)
+        scale = float(l32.abs().max())
+        e_hip = float((got - l32).abs().max())
+        e_ref = float((l16 - l32).abs().max())
+        assert e_hip <= 2 * e_ref + 2.0**-9 * scale, f"t={t}: |hip-f32| {e_hip:.4g} vs |bf16 ref-f32| {e_ref:.4g}"
+        top2 = l32.topk(2, dim=-1).values
+        sure = (top2[:, 0] - top2[:, 1]) > 4 * e_hip
+        picks = nxt.cpu().long()
+        assert torch.equal(picks[sure], l32.argmax(-1)[sure]), f"t={t}: greedy picks differ"
+        assert st.lengths.cpu().tolist() == caches[torch.float32].lengths.tolist()
+        tok = picks
+    return st
+
+
+@pytest.mark.parametrize("B", [1, 3, 64])
+def test_decode_step_matches_reference(small, B):
+    model, refs = small
+    _run_and_compare(model, refs, B, steps=6 if B < 64 else 3, seed=B)
+
+
+def test_graph_replays_equal_eager_steps(small):
+    """A captured step replayed token after token gives the bits of eager steps from the same state."""
+    model, _ = small
+    print_case("graph replay")
+    B, steps = 4, 5
+    a, b = model.new_state(B, 32), model.new_state(B, 32)
+    tok = torch.tensor([5, 17, 300, 999])
+    a.set_tokens(tok, model.cfg.vocab_size)
+    b.set_tokens(tok, model.cfg.vocab_size)
+    graph = model.capture(b)
+    for t in range(steps):
+        model.step(a)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(a.logits, b.logits), f"replay {t}"
+        assert torch.equal(a.tokens, b.tokens) and torch.equal(a.lengths, b.lengths)
+    assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
+    assert b.lengths.cpu().tolist() == [steps] * B
+
+
+def test_inactive_slots_do_not_leak(small):
+    """tests/test_batched_cache.py:186-213 on the device: garbage in inactive slots changes no bit of
+    an active row, and advance leaves inactive rows where they were."""
+    model, _ = small
+    print_case("poisoned slots")
+    a, b = model.new_state(4, 32), model.new_state(4, 32)
+    for s in (a, b):
+        s.active.copy_(torch.tensor([1, 0, 1, 0], dtype=torch.uint8))
+        s.set_lengths([3, 9, 0, 31])
+    b.k[:, 1].normal_()
+    b.v[:, 3].normal_()
+    tok = torch.tensor([1, 2, 3, 4])
+    for _ in range(3):
+        model.step(a, tok)
+        model.step(b, tok)
+        torch.cuda.synchronize()
+        for r in (0, 2):
+            assert torch.equal(a.logits[r], b.logits[r])
+        tok = a.tokens.cpu()
+    assert a.lengths.cpu().tolist() == [6, 9, 3, 31]
+
+
+def test_step_rejects_bad_tokens(small):
+    model, _ = small
+    st = model.new_state(2, 16)
+    with pytest.raises(IndexError):
+        model.step(st, [0, model.cfg.vocab_size])
+    with pytest.raises(ValueError):
+        model.step(st, [0, 1, 2])
