@@ -362,6 +362,14 @@ int sqx_decode_attention(const void* q, const void* k_cache, const void* v_cache
                          int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws,
                          int64_t ws_bytes, sqx_stream_t stream);
 
+/* sqx_rope_kv and sqx_decode_attention in one pass: qkv is the fused projection row of
+ * sqx_rope_kv; q and the new key are rotated in registers, the new key/value take the place of cache
+ * row min(lengths[b], tmax - 1) and are written there. Same results, bit for bit, as the two calls. */
+int sqx_decode_attention_rope(const void* qkv, const int* lengths, const float* cos_t, const float* sin_t,
+                              int64_t rope_rows, void* k_cache, void* v_cache, int64_t B, int64_t H,
+                              int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws, int64_t ws_bytes,
+                              sqx_stream_t stream);
+
 /* SwiGLU's gate (model.py:227-237): out = bf16(silu(g) * u) from gate_up = bf16 [B, 2F] laid out
  * [g | u] (the w1 and w3 outputs side by side); out: bf16 [B, F]. */
 int sqx_silu_mul(const void* gate_up, int64_t B, int64_t F, void* out, sqx_stream_t stream);

@@ -133,13 +133,33 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const uint16_t* __restrict
 constexpr int kHd = 128;
 constexpr int kKeysPerStep = 16;
 
-template <int G>
-__global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-                                                           const uint16_t* __restrict__ vc, const int* __restrict__ lengths,
-                                                           int H, int Hkv, int tmax, int chunk, int nchunk,
+// RoPE of one lane's 8 consecutive dims (4 pairs) with the pair's cos/sin, rounded to bf16 as the
+// reference's rotated q and k are (separate fp32 products and sums, model.py:218-224).
+__device__ inline u32x4_t rope8(u32x4_t v, const float (&cs)[4], const float (&sn)[4]) {
+#pragma clang fp contract(off)
+  u32x4_t r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float x0 = bf16_lo(v[j]), x1 = bf16_hi(v[j]);
+    r[j] = ActBF16::pack_rne(x0 * cs[j] - x1 * sn[j], x0 * sn[j] + x1 * cs[j]);
+  }
+  return r;
+}
+
+// ROPE: q is the fused projection row [q | k | v] (width (H + 2 Hkv) * hd) and the kernel also does
+// sqx_rope_kv's work: q and the new key are rotated in registers, the new key/value stand in for
+// cache row min(lengths[b], tmax - 1) (which the workgroup holding that row writes to the cache).
+// Otherwise q is the rotated [B, H, hd] tensor and the cache already holds this step's key.
+template <int G, bool ROPE>
+__global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ kc,
+                                                           uint16_t* __restrict__ vc, const int* __restrict__ lengths,
+                                                           const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                                           int rope_rows, int H, int Hkv, int tmax, int chunk, int nchunk,
                                                            float qscale, float* __restrict__ part) {
   const int ch = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
-  const int L = min(max(lengths[b], 0) + 1, tmax);
+  const int len = max(lengths[b], 0);
+  const int L = min(len + 1, tmax);
+  const int slot = min(len, tmax - 1);
   const int t0 = ch * chunk;
   if (t0 >= L) return;  // the combine reads only chunks below L
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -150,10 +170,24 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
   __shared__ float sm[4][G], sl[4][G];
   __shared__ float so[4][G][kHd];
 
+  const uint16_t* qrow = q + static_cast<int64_t>(b) * (ROPE ? H + 2 * Hkv : H) * kHd + dl * 8;
+  float cs[4], sn[4];
+  u32x4_t knew{}, vnew{};
+  if constexpr (ROPE) {
+    const int64_t pr = static_cast<int64_t>(min(len, rope_rows - 1)) * (kHd / 2) + dl * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      cs[j] = cos_t[pr + j];
+      sn[j] = sin_t[pr + j];
+    }
+    knew = rope8(*reinterpret_cast<const u32x4_t*>(qrow + (H + kh) * kHd), cs, sn);
+    vnew = *reinterpret_cast<const u32x4_t*>(qrow + (H + Hkv + kh) * kHd);
+  }
   float qv[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(q + (static_cast<int64_t>(b) * H + kh * G + g) * kHd + dl * 8);
+    u32x4_t v = *reinterpret_cast<const u32x4_t*>(qrow + (kh * G + g) * kHd);
+    if constexpr (ROPE) v = rope8(v, cs, sn);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       qv[g][2 * j] = bf16_lo(v[j]) * qscale;
@@ -171,6 +205,12 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
   const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd;
   const uint16_t* kb = kc + head_off + dl * 8;
   const uint16_t* vb = vc + head_off + dl * 8;
+  if constexpr (ROPE) {
+    if (ch == slot / chunk && wave == 0 && kl == 0) {  // one 256-byte row each, from this workgroup only
+      *reinterpret_cast<u32x4_t*>(kc + head_off + static_cast<int64_t>(slot) * kHd + dl * 8) = knew;
+      *reinterpret_cast<u32x4_t*>(vc + head_off + static_cast<int64_t>(slot) * kHd + dl * 8) = vnew;
+    }
+  }
 
   for (int base = ws; base < we; base += kKeysPerStep) {
     u32x4_t kr[4], vr[4];
@@ -182,6 +222,17 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
       const int tc = ok[u] ? t : base;  // an in-range row; its score is masked below
       kr[u] = *reinterpret_cast<const u32x4_t*>(kb + static_cast<int64_t>(tc) * kHd);
       vr[u] = *reinterpret_cast<const u32x4_t*>(vb + static_cast<int64_t>(tc) * kHd);
+    }
+    if constexpr (ROPE) {
+      if (slot >= base && slot < base + kKeysPerStep) {  // wave-uniform: this step holds the new key
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (base + 4 * u + kl == slot) {
+            kr[u] = knew;
+            vr[u] = vnew;
+          }
+        }
+      }
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -266,23 +317,53 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
 
 // out[b, h*hd + d] = bf16(sum_c 2^(m_c - M) o_c[d] / sum_c 2^(m_c - M) l_c) over the chunks c that
 // hold keys of row b. Row layout [B, H*hd] is the (B, 1, H*hd) view that o_proj takes (model.py:365).
-__global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ part, const int* __restrict__ lengths,
+// One workgroup of 256 threads per (head, row): the chunk maxima and weights are formed in parallel
+// (one chunk per thread), then two halves of the workgroup sum alternate chunks of o.
+constexpr int kMaxChunks = 1024;
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part, const int* __restrict__ lengths,
                                                            int H, int tmax, int chunk, int nchunk,
                                                            uint16_t* __restrict__ out) {
-  const int h = blockIdx.x, b = blockIdx.y, dd = threadIdx.x;
+  __shared__ float sa[kMaxChunks];
+  __shared__ float red[2][4];
+  __shared__ float so[kHd];
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int L = min(max(lengths[b], 0) + 1, tmax);
   const int used = (L + chunk - 1) / chunk;
   const float* base = part + (static_cast<int64_t>(b) * H + h) * nchunk * (kHd + 2);
-  float M = -INFINITY;
-  for (int c = 0; c < used; ++c) M = fmaxf(M, base[c * (kHd + 2)]);
-  float lsum = 0.0f, osum = 0.0f;
-  for (int c = 0; c < used; ++c) {
-    const float* p = base + c * (kHd + 2);
-    const float a = p[0] == -INFINITY ? 0.0f : exp2f(p[0] - M);
-    lsum = fmaf(p[1], a, lsum);
-    osum = fmaf(p[2 + dd], a, osum);
+  float mx = -INFINITY;
+  for (int c = tid; c < used; c += 256) {
+    const float m = base[c * (kHd + 2)];
+    sa[c] = m;
+    mx = fmaxf(mx, m);
   }
-  out[(static_cast<int64_t>(b) * H + h) * kHd + dd] = f32_to_bf16_bits(osum / lsum);
+  mx = wave_max(mx);
+  if (lane == 0) red[0][wave] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  float ls = 0.0f;
+  for (int c = tid; c < used; c += 256) {
+    const float a = sa[c] == -INFINITY ? 0.0f : exp2f(sa[c] - M);
+    sa[c] = a;
+    ls = fmaf(base[c * (kHd + 2) + 1], a, ls);
+  }
+  ls = wave_sum(ls);
+  if (lane == 0) red[1][wave] = ls;
+  __syncthreads();
+  const float lsum = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  const int dd = tid & (kHd - 1), half = tid >> 7;
+  float os = 0.0f;
+#pragma unroll 8
+  for (int c = half; c < used; c += 2) os = fmaf(base[c * (kHd + 2) + 2 + dd], sa[c], os);
+  if (half == 1) so[dd] = os;
+  __syncthreads();
+  if (half == 0) out[(static_cast<int64_t>(b) * H + h) * kHd + dd] = f32_to_bf16_bits((os + so[dd]) / lsum);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -324,31 +405,55 @@ __device__ inline bool argmax_takes(float ov, int oi, float cv, int ci) {
   return ov > cv || (ov == cv && oi < ci);
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(const uint16_t* __restrict__ logits, int64_t V,
-                                                     int* __restrict__ next_tok) {
-  __shared__ float bv[256];
-  __shared__ int bi[256];
-  const int b = blockIdx.x;
+// One workgroup of 1024 threads per row. VEC: the row is read in 16-byte pieces (V % 8 == 0 and a
+// 16-byte aligned base), four pieces in flight per thread.
+template <bool VEC>
+__global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict__ logits, int64_t V,
+                                                      int* __restrict__ next_tok) {
+  __shared__ float bv[16];
+  __shared__ int bi[16];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint16_t* row = logits + static_cast<int64_t>(b) * V;
   float best = -INFINITY;
   int idx = 0x7fffffff;
-  for (int64_t v = threadIdx.x; v < V; v += 256) {
-    const float x = bf16_bits_to_f32(logits[static_cast<int64_t>(b) * V + v]);
-    if (argmax_takes(x, static_cast<int>(v), best, idx)) {
+  auto take = [&](float x, int v) {
+    if (argmax_takes(x, v, best, idx)) {
       best = x;
-      idx = static_cast<int>(v);
+      idx = v;
+    }
+  };
+  if constexpr (VEC) {
+    const int64_t nv = V / 8;
+#pragma unroll 4
+    for (int64_t c = tid; c < nv; c += 1024) {
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(row + 8 * c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        take(bf16_lo(w[j]), static_cast<int>(8 * c + 2 * j));
+        take(bf16_hi(w[j]), static_cast<int>(8 * c + 2 * j + 1));
+      }
+    }
+  } else {
+    for (int64_t v = tid; v < V; v += 1024) take(bf16_bits_to_f32(row[v]), static_cast<int>(v));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (argmax_takes(ov, oi, best, idx)) {
+      best = ov;
+      idx = oi;
     }
   }
-  bv[threadIdx.x] = best;
-  bi[threadIdx.x] = idx;
+  if (lane == 0) {
+    bv[wave] = best;
+    bi[wave] = idx;
+  }
   __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s && argmax_takes(bv[threadIdx.x + s], bi[threadIdx.x + s], bv[threadIdx.x], bi[threadIdx.x])) {
-      bv[threadIdx.x] = bv[threadIdx.x + s];
-      bi[threadIdx.x] = bi[threadIdx.x + s];
-    }
-    __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 16; ++w) take(bv[w], bi[w]);
+    next_tok[b] = idx;
   }
-  if (threadIdx.x == 0) next_tok[b] = bi[0];
 }
 
 // SlotKVCache.advance(1) (kv_cache.py:207-213): lengths[b] += 1 for active rows (all rows when
@@ -418,46 +523,76 @@ extern "C" int64_t sqx_attn_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, i
   return B * H * ceil_div(tmax, sqx_attn_chunk(B, Hkv, tmax)) * (kHd + 2) * 4;
 }
 
-extern "C" int sqx_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* lengths,
-                                    int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax, void* out,
-                                    void* ws, int64_t ws_bytes, sqx_stream_t stream) {
-  SQX_REQUIRE(hd == kHd, SQX_E_ARG, "sqx_decode_attention: head_dim %lld is not supported (128)", (long long)hd);
-  SQX_REQUIRE(B >= 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && tmax > 0, SQX_E_ARG, "sqx_decode_attention: bad shape");
-  SQX_REQUIRE(B < 65536 && Hkv < 65536 && tmax < (int64_t(1) << 30), SQX_E_ARG, "sqx_decode_attention: shape too large");
+static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, const int* lengths, const float* cos_t,
+                                 const float* sin_t, int64_t rope_rows, int64_t B, int64_t H, int64_t Hkv, int64_t hd,
+                                 int64_t tmax, void* out, void* ws, int64_t ws_bytes, sqx_stream_t stream,
+                                 const char* fn) {
+  const bool rope = cos_t != nullptr;
+  SQX_REQUIRE(hd == kHd, SQX_E_ARG, "%s: head_dim %lld is not supported (128)", fn, (long long)hd);
+  SQX_REQUIRE(B >= 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && tmax > 0, SQX_E_ARG, "%s: bad shape", fn);
+  SQX_REQUIRE(B < 65536 && Hkv < 65536 && tmax < (int64_t(1) << 30) && (H + 2 * Hkv) * hd < (int64_t(1) << 30),
+              SQX_E_ARG, "%s: shape too large", fn);
   const int G = static_cast<int>(H / Hkv);
-  SQX_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, SQX_E_ARG,
-              "sqx_decode_attention: %d query heads per kv head (1, 2, 4 or 8 are built)", G);
+  SQX_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, SQX_E_ARG, "%s: %d query heads per kv head (1, 2, 4 or 8 are built)",
+              fn, G);
+  SQX_REQUIRE(!rope || (sin_t != nullptr && rope_rows > 0 && rope_rows < (int64_t(1) << 31)), SQX_E_ARG,
+              "%s: bad RoPE tables", fn);
   if (B == 0) return SQX_OK;
-  SQX_REQUIRE(q && k_cache && v_cache && lengths && out && ws, SQX_E_ARG, "sqx_decode_attention: null pointer");
-  SQX_REQUIRE(ws_bytes >= sqx_attn_workspace_bytes(B, H, Hkv, tmax), SQX_E_SPACE,
-              "sqx_decode_attention: workspace of %lld bytes, %lld needed", (long long)ws_bytes,
-              (long long)sqx_attn_workspace_bytes(B, H, Hkv, tmax));
+  SQX_REQUIRE(q && k_cache && v_cache && lengths && out && ws, SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(ws_bytes >= sqx_attn_workspace_bytes(B, H, Hkv, tmax), SQX_E_SPACE, "%s: workspace of %lld bytes, %lld needed",
+              fn, (long long)ws_bytes, (long long)sqx_attn_workspace_bytes(B, H, Hkv, tmax));
   SQX_REQUIRE(al16(q) && al16(k_cache) && al16(v_cache) && al16(ws), SQX_E_ARG,
-              "sqx_decode_attention: q, caches and workspace must be 16-byte aligned");
+              "%s: q, caches and workspace must be 16-byte aligned", fn);
   const int chunk = sqx_attn_chunk(B, Hkv, tmax);
   const int nchunk = static_cast<int>(ceil_div(tmax, chunk));
+  SQX_REQUIRE(nchunk <= kMaxChunks, SQX_E_ARG, "%s: %d key chunks of %d (at most %d)", fn, nchunk, chunk, kMaxChunks);
   hipStream_t s = as_stream(stream);
   const float qscale = 1.4426950408889634f / sqrtf(static_cast<float>(hd));  // log2(e) / sqrt(hd)
   const dim3 grid(static_cast<unsigned>(nchunk), static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
   const auto* qp = static_cast<const uint16_t*>(q);
-  const auto* kp = static_cast<const uint16_t*>(k_cache);
-  const auto* vp = static_cast<const uint16_t*>(v_cache);
+  auto* kp = static_cast<uint16_t*>(k_cache);
+  auto* vp = static_cast<uint16_t*>(v_cache);
   float* w = static_cast<float*>(ws);
   const int iH = static_cast<int>(H), iK = static_cast<int>(Hkv), iT = static_cast<int>(tmax);
-#define SQX_ATTN(G_) \
-  hipLaunchKernelGGL(attn_partial_kernel<G_>, grid, dim3(256), 0, s, qp, kp, vp, lengths, iH, iK, iT, chunk, nchunk, qscale, w)
-  switch (G) {
-    case 1: SQX_ATTN(1); break;
-    case 2: SQX_ATTN(2); break;
-    case 4: SQX_ATTN(4); break;
-    default: SQX_ATTN(8); break;
+  const int rr = static_cast<int>(rope_rows);
+#define SQX_ATTN(G_, R_)                                                                                          \
+  hipLaunchKernelGGL((attn_partial_kernel<G_, R_>), grid, dim3(256), 0, s, qp, kp, vp, lengths, cos_t, sin_t, rr, iH, iK, \
+                     iT, chunk, nchunk, qscale, w)
+#define SQX_ATTN_G(R_)            \
+  switch (G) {                    \
+    case 1: SQX_ATTN(1, R_); break; \
+    case 2: SQX_ATTN(2, R_); break; \
+    case 4: SQX_ATTN(4, R_); break; \
+    default: SQX_ATTN(8, R_); break; \
   }
+  if (rope) {
+    SQX_ATTN_G(true)
+  } else {
+    SQX_ATTN_G(false)
+  }
+#undef SQX_ATTN_G
 #undef SQX_ATTN
-  SQX_LAUNCH_CHECK("sqx_decode_attention");
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(B)), dim3(kHd), 0, s, w,
+  SQX_LAUNCH_CHECK(fn);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(B)), dim3(256), 0, s, w,
                      lengths, iH, iT, chunk, nchunk, static_cast<uint16_t*>(out));
-  SQX_LAUNCH_CHECK("sqx_decode_attention");
+  SQX_LAUNCH_CHECK(fn);
   return SQX_OK;
+}
+
+extern "C" int sqx_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* lengths,
+                                    int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax, void* out,
+                                    void* ws, int64_t ws_bytes, sqx_stream_t stream) {
+  return decode_attention_impl(q, const_cast<void*>(k_cache), const_cast<void*>(v_cache), lengths, nullptr, nullptr, 0, B,
+                               H, Hkv, hd, tmax, out, ws, ws_bytes, stream, "sqx_decode_attention");
+}
+
+extern "C" int sqx_decode_attention_rope(const void* qkv, const int* lengths, const float* cos_t, const float* sin_t,
+                                         int64_t rope_rows, void* k_cache, void* v_cache, int64_t B, int64_t H,
+                                         int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws, int64_t ws_bytes,
+                                         sqx_stream_t stream) {
+  SQX_REQUIRE(cos_t != nullptr, SQX_E_ARG, "sqx_decode_attention_rope: null cos table");
+  return decode_attention_impl(qkv, k_cache, v_cache, lengths, cos_t, sin_t, rope_rows, B, H, Hkv, hd, tmax, out, ws,
+                               ws_bytes, stream, "sqx_decode_attention_rope");
 }
 
 extern "C" int sqx_silu_mul(const void* gate_up, int64_t B, int64_t F, void* out, sqx_stream_t stream) {
@@ -492,8 +627,11 @@ extern "C" int sqx_argmax(const void* logits, int64_t B, int64_t V, int* next_to
   SQX_REQUIRE(B >= 0 && V > 0 && B < (int64_t(1) << 31) && V < (int64_t(1) << 31), SQX_E_ARG, "sqx_argmax: bad shape");
   if (B == 0) return SQX_OK;
   SQX_REQUIRE(logits && next_tok, SQX_E_ARG, "sqx_argmax: null pointer");
-  hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, as_stream(stream),
-                     static_cast<const uint16_t*>(logits), V, next_tok);
+  const auto* lp = static_cast<const uint16_t*>(logits);
+  if (V % 8 == 0 && al16(logits))
+    hipLaunchKernelGGL(argmax_kernel<true>, dim3(static_cast<unsigned>(B)), dim3(1024), 0, as_stream(stream), lp, V, next_tok);
+  else
+    hipLaunchKernelGGL(argmax_kernel<false>, dim3(static_cast<unsigned>(B)), dim3(1024), 0, as_stream(stream), lp, V, next_tok);
   SQX_LAUNCH_CHECK("sqx_argmax");
   return SQX_OK;
 }

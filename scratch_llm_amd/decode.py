@@ -8,8 +8,8 @@ is ``w4a16_linear`` (int4_group.py:148-164). This module is that step on the lib
 * the INT4 linears on the tiled weights (the streaming decode kernel below 64 rows, the
   dequant-GEMM from 64 rows), with q|k|v fused into one projection and gate|up into another
   (concatenating rows keeps every group scale: groups run along the input dimension);
-* everything between them from sqx_decode.hip: residual add + RMSNorm, RoPE + cache write,
-  split-key GQA attention, SiLU-gate, embedding rows, greedy pick, ``advance``.
+* everything between them from sqx_decode.hip: residual add + RMSNorm, split-key GQA attention
+  with RoPE and the cache write folded in, SiLU-gate, embedding rows, greedy pick, ``advance``.
 
 A step allocates nothing: :class:`DecodeState` holds the cache and every buffer for one batch
 size, so :meth:`Int4DecodeLM.capture` can record the whole step in a HIP graph whose replays
@@ -112,7 +112,6 @@ class DecodeState:
         self.h = torch.empty(batch, d, **bf)  # normalised input of the next projection
         self.delta = torch.empty(batch, d, **bf)  # o_proj / w2 output
         self.qkv = torch.empty(batch, (cfg.n_heads + 2 * hkv) * hd, **bf)
-        self.q = torch.empty(batch, cfg.n_heads * hd, **bf)
         self.attn = torch.empty(batch, cfg.n_heads * hd, **bf)
         self.gu = torch.empty(batch, 2 * cfg.d_ff, **bf)
         self.act = torch.empty(batch, cfg.d_ff, **bf)
@@ -281,12 +280,10 @@ class Int4DecodeLM:
                         cur = 1 - cur
                     if sub == 0:
                         self._linear(st, ly.wqkv, st.h, st.qkv, s)
-                        ck(lib.sqx_rope_kv(st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(),
-                                           self.sin.data_ptr(), cfg.context_length, B, H, Hkv, hd, T,
-                                           st.q.data_ptr(), st.k[li].data_ptr(), st.v[li].data_ptr(), s), "rope_kv")
-                        ck(lib.sqx_decode_attention(st.q.data_ptr(), st.k[li].data_ptr(), st.v[li].data_ptr(),
-                                                    st.lengths.data_ptr(), B, H, Hkv, hd, T, st.attn.data_ptr(),
-                                                    st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention")
+                        ck(lib.sqx_decode_attention_rope(
+                            st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
+                            cfg.context_length, st.k[li].data_ptr(), st.v[li].data_ptr(), B, H, Hkv, hd, T,
+                            st.attn.data_ptr(), st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention")
                         self._linear(st, ly.wo, st.attn, st.delta, s)
                     else:
                         self._linear(st, ly.w13, st.h, st.gu, s)

@@ -147,6 +147,46 @@ def test_attention_config5_context(lib, B):
     _attn_case(lib, B, 32, 8, T, lengths, seed=B)
 
 
+@pytest.mark.parametrize("B,H,Hkv,T", [(5, 32, 8, 300), (1, 32, 8, 2048), (3, 16, 16, 64), (64, 32, 8, 2048)])
+def test_fused_rope_attention_equals_two_calls(lib, B, H, Hkv, T):
+    """sqx_decode_attention_rope == sqx_rope_kv then sqx_decode_attention, bit for bit (output and cache),
+    with the new key anywhere in a chunk, at position 0, and at a full slot (lengths >= T)."""
+    print_case("fused rope attention", B, H, Hkv, T)
+    hd, ctx = 128, max(T + 16, 64)
+    g = torch.Generator().manual_seed(B * 1000 + T)
+    lengths = torch.randint(0, T, (B,), generator=g)
+    lengths[0] = T - 1
+    if B > 1:
+        lengths[1] = 0
+    if B > 2:
+        lengths[2] = T + 9  # a full slot: writes row T - 1, attends all T keys, RoPE at position T + 9
+    qkv = (torch.randn(B, (H + 2 * Hkv) * hd, generator=g) * 2).bfloat16().to(DEV)
+    cache = torch.randn(2, B, Hkv, T, hd, generator=g).bfloat16().to(DEV)
+    cos, sin = (t.to(DEV) for t in D.rope_tables(hd, ctx, 10000.0))
+    ln = lengths.to(torch.int32).to(DEV)
+    nb = lib.sqx_attn_workspace_bytes(B, H, Hkv, T)
+    ws = torch.empty(nb // 4, dtype=torch.float32, device=DEV)
+    outs, caches = [], []
+    for fused in (False, True):
+        kc, vc = cache[0].clone(), cache[1].clone()
+        out = torch.empty(B, H * hd, dtype=torch.bfloat16, device=DEV)
+        if fused:
+            _ok(lib, lib.sqx_decode_attention_rope(qkv.data_ptr(), ln.data_ptr(), cos.data_ptr(), sin.data_ptr(), ctx,
+                                                   kc.data_ptr(), vc.data_ptr(), B, H, Hkv, hd, T, out.data_ptr(),
+                                                   ws.data_ptr(), nb, _s()))
+        else:
+            q = torch.empty(B, H, hd, dtype=torch.bfloat16, device=DEV)
+            _ok(lib, lib.sqx_rope_kv(qkv.data_ptr(), ln.data_ptr(), cos.data_ptr(), sin.data_ptr(), ctx, B, H, Hkv, hd, T,
+                                     q.data_ptr(), kc.data_ptr(), vc.data_ptr(), _s()))
+            _ok(lib, lib.sqx_decode_attention(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), ln.data_ptr(), B, H, Hkv, hd, T,
+                                              out.data_ptr(), ws.data_ptr(), nb, _s()))
+        torch.cuda.synchronize()
+        outs.append(out)
+        caches.append((kc, vc))
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
+
+
 def test_attention_rejects_bad_shapes(lib):
     ws = torch.empty(16, dtype=torch.float32, device=DEV)
     assert lib.sqx_decode_attention(ws.data_ptr(), ws.data_ptr(), ws.data_ptr(), ws.data_ptr(), 1, 32, 8, 64, 16, ws.data_ptr(),
