@@ -112,6 +112,25 @@ int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt, int param
                     const void* x, int act_dtype, void* y, const void* bias, int64_t m, int64_t rows,
                     int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
 
+/* 1 when sqx_int4_linear_rmsnorm / sqx_int4_linear_silu take m activation rows of cols columns
+ * (m <= 8, cols % 8 == 0, the rows fit the kernel's 64 KiB LDS copy), else 0. */
+int sqx_int4_prologue_fits(int64_t m, int64_t cols);
+
+/* A decode-step linear with the residual add and RMSNorm in front of it (TransformerBlock.forward,
+ * model.py:394-403, then RMSNorm, model.py:158-162, then w4a16_linear): h = bf16(x + delta) (written
+ * to h_out; delta NULL means h = x and h_out unused), x' = bf16(h * (1 / sqrt(mean(h^2) + eps)) * gain),
+ * y = x' @ W^T. Symmetric codes with fp32 scales (sqx_int4_tile code_kind 0), bf16 x/delta/gain/h_out/y
+ * ([m, cols], [cols] for gain). Bit-identical to sqx_rmsnorm followed by sqx_int4_linear. */
+int sqx_int4_linear_rmsnorm(const uint8_t* wt, const float* st, const void* x, const void* delta,
+                            const void* gain, float eps, void* h_out, void* y, int64_t m, int64_t rows,
+                            int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
+
+/* SwiGLU's down projection with its gate in front (model.py:227-237): y = bf16(silu(g) * u) @ W^T with
+ * gate_up = bf16 [m, 2 cols] laid out [g | u]. Bit-identical to sqx_silu_mul followed by
+ * sqx_int4_linear. Same weight format as sqx_int4_linear_rmsnorm. */
+int sqx_int4_linear_silu(const uint8_t* wt, const float* st, const void* gate_up, void* y, int64_t m,
+                         int64_t rows, int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
+
 /* Build-defined asymmetric uint4, group-wise (BASELINE config 2's "asymmetric, bf16 scale/zero";
  * no reference symbol: the 4-bit form of quantize_affine, int8.py:142-172, per group):
  * lo = min(min(w_g), 0), hi = max(max(w_g), 0), s = max((hi - lo) / 15, 1e-12) (rounded to bf16 first
@@ -338,7 +357,7 @@ int sqx_int8_linear(const uint8_t* wt, const float* scale, const void* x, int ac
 /* RMSNorm (model.py:148-162) with the residual add before it (TransformerBlock.forward,
  * model.py:394-403): with delta, h = bf16(x + delta) is written to h_out; without, h = x.
  * y = bf16(h * (1 / sqrt(mean(h^2) + eps)) * w). x, delta, h_out, y: bf16 [rows, d]; w: bf16 [d];
- * d % 8 == 0; 16-byte aligned. h_out must not alias x or delta. */
+ * d % 8 == 0, d <= 16384; 16-byte aligned. h_out must not alias x or delta. */
 int sqx_rmsnorm(const void* x, const void* delta, const void* w, float eps, int64_t rows, int64_t d,
                 void* h_out, void* y, sqx_stream_t stream);
 
@@ -380,8 +399,11 @@ int sqx_embed(const void* table, int64_t V, const int* tokens, int64_t B, int64_
               sqx_stream_t stream);
 
 /* Greedy pick (sampling.py:80-83, temperature 0): next_tok[b] = first index of the maximum of the bf16
- * logits [B, V], NaN counting as the maximum (torch.argmax). */
-int sqx_argmax(const void* logits, int64_t B, int64_t V, int* next_tok, sqx_stream_t stream);
+ * logits [B, V], NaN counting as the maximum (torch.argmax). Rows are split over up to 64 workgroups
+ * whose partial picks go through ws (sqx_argmax_workspace_bytes) to a second, one-wave-per-row pass. */
+int64_t sqx_argmax_workspace_bytes(int64_t B, int64_t V);
+int sqx_argmax(const void* logits, int64_t B, int64_t V, int* next_tok, void* ws, int64_t ws_bytes,
+               sqx_stream_t stream);
 
 /* SlotKVCache.advance(1) (kv_cache.py:207-213): lengths[b] += 1 where active[b] != 0 (every row when
  * active is NULL). */

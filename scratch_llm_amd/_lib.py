@@ -52,6 +52,12 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_i,
         [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p],
     ),
+    "sqx_int4_prologue_fits": (_c_i, [_c_i64, _c_i64]),
+    "sqx_int4_linear_rmsnorm": (
+        _c_i,
+        [_c_p, _c_p, _c_p, _c_p, _c_p, ctypes.c_float, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p],
+    ),
+    "sqx_int4_linear_silu": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p]),
     "sqx_e2m1_round": (_c_i, [_c_p, _c_i, _c_i64, _c_p, _c_p]),
     "sqx_e2m1_decode": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
     "sqx_fp4_pack": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
@@ -119,7 +125,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "sqx_silu_mul": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_embed": (_c_i, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
-    "sqx_argmax": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_argmax_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "sqx_argmax": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p]),
     "sqx_advance": (_c_i, [_c_p, _c_p, _c_i64, _c_p]),
 }
 

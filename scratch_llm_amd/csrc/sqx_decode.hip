@@ -10,69 +10,75 @@
 // min(lengths[b], Tmax - 1), RoPE uses position lengths[b], and the row attends keys
 // j <= lengths[b] (write-then-mask, model.py:293-305). All arithmetic is fp32; each written tensor
 // is rounded to bf16 once (round to nearest even).
+#include <algorithm>
+
 #include "sqx_common.h"
 
 namespace sqx {
 
-// all-lane sums over 16 lanes (one DPP row) and over the wave
-__device__ inline float row16_sum(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));  // row_ror:8
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));  // row_ror:4
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));   // quad_perm 2301
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));   // quad_perm 1032
-  return v;
-}
-
-__device__ inline float wave_sum(float v) {
-  v = row16_sum(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
-}
-
-__device__ inline float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
-__device__ inline float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
-
 // ---------------------------------------------------------------------------------------------
 // Residual add + RMSNorm. With delta: h = bf16(x + delta) is written to h_out and normalised;
 // without: h = x. y = bf16(h * (1 / sqrt(mean(h^2) + eps)) * w), the product taken left to right in
-// fp32 as model.py:158-162 does. One workgroup of 256 threads per row; d % 8 == 0.
+// fp32 as model.py:158-162 does. One workgroup of 256 threads per row; d % 8 == 0, d <= 16384.
 // ---------------------------------------------------------------------------------------------
+template <int NCH>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ delta,
                                                       const uint16_t* __restrict__ w, float eps, int d,
                                                       uint16_t* __restrict__ h_out, uint16_t* __restrict__ y) {
+  // Thread t owns columns 8t + 2048i (i < NCH): every load of the row, the delta and the gain is
+  // issued before the first use, and the row stays in registers between the two passes.
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
-  const uint16_t* xr = x + row * d;
-  float ss = 0.0f;
-  for (int c = threadIdx.x * 8; c < d; c += 256 * 8) {
-    u32x4_t v = *reinterpret_cast<const u32x4_t*>(xr + c);
-    if (delta != nullptr) {
-      const u32x4_t dv = *reinterpret_cast<const u32x4_t*>(delta + row * d + c);
+  const int tid = threadIdx.x;
+  u32x4_t v[NCH], wv[NCH];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = ActBF16::pack_rne(bf16_lo(v[j]) + bf16_lo(dv[j]), bf16_hi(v[j]) + bf16_hi(dv[j]));
-      *reinterpret_cast<u32x4_t*>(h_out + row * d + c) = v;
+  for (int i = 0; i < NCH; ++i) {
+    const int c = tid * 8 + i * 2048;
+    if (c < d) {
+      v[i] = *reinterpret_cast<const u32x4_t*>(x + row * d + c);
+      wv[i] = *reinterpret_cast<const u32x4_t*>(w + c);
     }
+  }
+  if (delta != nullptr) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float a0 = bf16_lo(v[j]), a1 = bf16_hi(v[j]);
-      ss = fmaf(a0, a0, ss);
-      ss = fmaf(a1, a1, ss);
+    for (int i = 0; i < NCH; ++i) {
+      const int c = tid * 8 + i * 2048;
+      if (c < d) {
+        const u32x4_t dv = *reinterpret_cast<const u32x4_t*>(delta + row * d + c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          v[i][j] = ActBF16::pack_rne(bf16_lo(v[i][j]) + bf16_lo(dv[j]), bf16_hi(v[i][j]) + bf16_hi(dv[j]));
+        *reinterpret_cast<u32x4_t*>(h_out + row * d + c) = v[i];
+      }
+    }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    if (tid * 8 + i * 2048 < d) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a0 = bf16_lo(v[i][j]), a1 = bf16_hi(v[i][j]);
+        ss = fmaf(a0, a0, ss);
+        ss = fmaf(a1, a1, ss);
+      }
     }
   }
   ss = wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   const float total = (red[0] + red[1]) + (red[2] + red[3]);
   const float r = 1.0f / sqrtf(total / static_cast<float>(d) + eps);
-  const uint16_t* hr = delta != nullptr ? h_out + row * d : xr;
-  for (int c = threadIdx.x * 8; c < d; c += 256 * 8) {
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(hr + c);
-    const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(w + c);
-    u32x4_t o;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o[j] = ActBF16::pack_rne(bf16_lo(v[j]) * r * bf16_lo(wv[j]), bf16_hi(v[j]) * r * bf16_hi(wv[j]));
-    *reinterpret_cast<u32x4_t*>(y + row * d + c) = o;
+  for (int i = 0; i < NCH; ++i) {
+    const int c = tid * 8 + i * 2048;
+    if (c < d) {
+      u32x4_t o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = ActBF16::pack_rne(bf16_lo(v[i][j]) * r * bf16_lo(wv[i][j]), bf16_hi(v[i][j]) * r * bf16_hi(wv[i][j]));
+      *reinterpret_cast<u32x4_t*>(y + row * d + c) = o;
+    }
   }
 }
 
@@ -405,15 +411,17 @@ __device__ inline bool argmax_takes(float ov, int oi, float cv, int ci) {
   return ov > cv || (ov == cv && oi < ci);
 }
 
-// One workgroup of 1024 threads per row. VEC: the row is read in 16-byte pieces (V % 8 == 0 and a
-// 16-byte aligned base), four pieces in flight per thread.
+// Partial pick over a span of one row: workgroup (blk, b) of 256 threads reduces elements
+// [blk * span, blk * span + span) to (value, index) in part[b, blk]. VEC: 16-byte loads (span and
+// V multiples of 8, 16-byte aligned rows).
 template <bool VEC>
-__global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict__ logits, int64_t V,
-                                                      int* __restrict__ next_tok) {
-  __shared__ float bv[16];
-  __shared__ int bi[16];
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const uint16_t* __restrict__ logits, int64_t V, int span,
+                                                             int nblk, float* __restrict__ pv, int* __restrict__ pi) {
+  __shared__ float bv[4];
+  __shared__ int bi[4];
+  const int blk = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint16_t* row = logits + static_cast<int64_t>(b) * V;
+  const int64_t e0 = static_cast<int64_t>(blk) * span, e1 = min<int64_t>(V, e0 + span);
   float best = -INFINITY;
   int idx = 0x7fffffff;
   auto take = [&](float x, int v) {
@@ -423,19 +431,42 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
     }
   };
   if constexpr (VEC) {
-    const int64_t nv = V / 8;
-#pragma unroll 4
-    for (int64_t c = tid; c < nv; c += 1024) {
-      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(row + 8 * c);
+#pragma unroll 2
+    for (int64_t c = e0 + 8 * tid; c < e1; c += 8 * 256) {
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(row + c);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        take(bf16_lo(w[j]), static_cast<int>(8 * c + 2 * j));
-        take(bf16_hi(w[j]), static_cast<int>(8 * c + 2 * j + 1));
+        take(bf16_lo(w[j]), static_cast<int>(c + 2 * j));
+        take(bf16_hi(w[j]), static_cast<int>(c + 2 * j + 1));
       }
     }
   } else {
-    for (int64_t v = tid; v < V; v += 1024) take(bf16_bits_to_f32(row[v]), static_cast<int>(v));
+    for (int64_t v = e0 + tid; v < e1; v += 256) take(bf16_bits_to_f32(row[v]), static_cast<int>(v));
   }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    take(ov, oi);
+  }
+  if (lane == 0) {
+    bv[wave] = best;
+    bi[wave] = idx;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; ++w) take(bv[w], bi[w]);
+    pv[static_cast<int64_t>(b) * nblk + blk] = best;
+    pi[static_cast<int64_t>(b) * nblk + blk] = idx;
+  }
+}
+
+// next_tok[b] = the pick among row b's nblk (<= 64) partials: one wave per row.
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ pv, const int* __restrict__ pi,
+                                                          int nblk, int* __restrict__ next_tok) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  float best = lane < nblk ? pv[static_cast<int64_t>(b) * nblk + lane] : -INFINITY;
+  int idx = lane < nblk ? pi[static_cast<int64_t>(b) * nblk + lane] : 0x7fffffff;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(best, o, 64);
@@ -445,15 +476,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
       idx = oi;
     }
   }
-  if (lane == 0) {
-    bv[wave] = best;
-    bi[wave] = idx;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    for (int w = 1; w < 16; ++w) take(bv[w], bi[w]);
-    next_tok[b] = idx;
-  }
+  if (lane == 0) next_tok[b] = idx;
 }
 
 // SlotKVCache.advance(1) (kv_cache.py:207-213): lengths[b] += 1 for active rows (all rows when
@@ -474,16 +497,23 @@ static bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 
 
 extern "C" int sqx_rmsnorm(const void* x, const void* delta, const void* w, float eps, int64_t rows, int64_t d,
                            void* h_out, void* y, sqx_stream_t stream) {
-  SQX_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && rows < (int64_t(1) << 31) && d < (int64_t(1) << 30), SQX_E_ARG,
-              "sqx_rmsnorm: bad shape [%lld, %lld] (d must be a multiple of 8)", (long long)rows, (long long)d);
+  SQX_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && rows < (int64_t(1) << 31) && d <= 16384, SQX_E_ARG,
+              "sqx_rmsnorm: bad shape [%lld, %lld] (d a multiple of 8, at most 16384)", (long long)rows, (long long)d);
   if (rows == 0) return SQX_OK;
   SQX_REQUIRE(x && w && y && (delta == nullptr || h_out != nullptr), SQX_E_ARG, "sqx_rmsnorm: null pointer");
   SQX_REQUIRE(al16(x) && al16(w) && al16(y) && al16(delta) && al16(h_out), SQX_E_ARG,
               "sqx_rmsnorm: pointers must be 16-byte aligned");
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, as_stream(stream),
-                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(delta),
-                     static_cast<const uint16_t*>(w), eps, static_cast<int>(d), static_cast<uint16_t*>(h_out),
-                     static_cast<uint16_t*>(y));
+  const int nch = static_cast<int>(ceil_div(d, 2048));
+#define SQX_RMS(N_)                                                                                             \
+  hipLaunchKernelGGL(rmsnorm_kernel<N_>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, as_stream(stream),     \
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(delta),                       \
+                     static_cast<const uint16_t*>(w), eps, static_cast<int>(d), static_cast<uint16_t*>(h_out), \
+                     static_cast<uint16_t*>(y))
+  if (nch <= 1) SQX_RMS(1);
+  else if (nch <= 2) SQX_RMS(2);
+  else if (nch <= 4) SQX_RMS(4);
+  else SQX_RMS(8);
+#undef SQX_RMS
   SQX_LAUNCH_CHECK("sqx_rmsnorm");
   return SQX_OK;
 }
@@ -623,15 +653,36 @@ extern "C" int sqx_embed(const void* table, int64_t V, const int* tokens, int64_
   return SQX_OK;
 }
 
-extern "C" int sqx_argmax(const void* logits, int64_t B, int64_t V, int* next_tok, sqx_stream_t stream) {
-  SQX_REQUIRE(B >= 0 && V > 0 && B < (int64_t(1) << 31) && V < (int64_t(1) << 31), SQX_E_ARG, "sqx_argmax: bad shape");
+static int argmax_blocks(int64_t V) { return static_cast<int>(std::min<int64_t>(64, ceil_div(V, 4096))); }
+
+extern "C" int64_t sqx_argmax_workspace_bytes(int64_t B, int64_t V) {
+  if (B <= 0 || V <= 0) return 0;
+  return B * argmax_blocks(V) * 8;
+}
+
+extern "C" int sqx_argmax(const void* logits, int64_t B, int64_t V, int* next_tok, void* ws, int64_t ws_bytes,
+                          sqx_stream_t stream) {
+  SQX_REQUIRE(B >= 0 && V > 0 && B < 65536 && V < (int64_t(1) << 31), SQX_E_ARG, "sqx_argmax: bad shape");
   if (B == 0) return SQX_OK;
-  SQX_REQUIRE(logits && next_tok, SQX_E_ARG, "sqx_argmax: null pointer");
+  SQX_REQUIRE(logits && next_tok && ws, SQX_E_ARG, "sqx_argmax: null pointer");
+  SQX_REQUIRE(ws_bytes >= sqx_argmax_workspace_bytes(B, V), SQX_E_SPACE, "sqx_argmax: workspace of %lld bytes, %lld needed",
+              (long long)ws_bytes, (long long)sqx_argmax_workspace_bytes(B, V));
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(ws) % 4 == 0, SQX_E_ARG, "sqx_argmax: workspace must be 4-byte aligned");
+  const int nblk = argmax_blocks(V);
+  const bool vec = V % 8 == 0 && al16(logits);
+  int span = static_cast<int>(ceil_div(V, nblk));
+  if (vec) span = (span + 7) / 8 * 8;
+  float* pv = static_cast<float*>(ws);
+  int* pi = reinterpret_cast<int*>(pv + B * nblk);
   const auto* lp = static_cast<const uint16_t*>(logits);
-  if (V % 8 == 0 && al16(logits))
-    hipLaunchKernelGGL(argmax_kernel<true>, dim3(static_cast<unsigned>(B)), dim3(1024), 0, as_stream(stream), lp, V, next_tok);
+  const dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>(B));
+  if (vec)
+    hipLaunchKernelGGL(argmax_partial_kernel<true>, grid, dim3(256), 0, as_stream(stream), lp, V, span, nblk, pv, pi);
   else
-    hipLaunchKernelGGL(argmax_kernel<false>, dim3(static_cast<unsigned>(B)), dim3(1024), 0, as_stream(stream), lp, V, next_tok);
+    hipLaunchKernelGGL(argmax_partial_kernel<false>, grid, dim3(256), 0, as_stream(stream), lp, V, span, nblk, pv, pi);
+  SQX_LAUNCH_CHECK("sqx_argmax");
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(static_cast<unsigned>(B)), dim3(64), 0, as_stream(stream), pv, pi, nblk,
+                     next_tok);
   SQX_LAUNCH_CHECK("sqx_argmax");
   return SQX_OK;
 }

@@ -51,11 +51,29 @@ inline int gemv_default_kslices(int64_t rows, int64_t cols, int kblk = 128) {
   return static_cast<int>(s);
 }
 
-template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32>
+// What the LDS copy of the activations computes on the way in (XLDS only, bf16 activations):
+//   kProPlain    x as given (optionally divided by a per-column scale);
+//   kProResNorm  the decode step's residual add + RMSNorm: h = bf16(x + delta) (delta optional; workgroup
+//                0 writes h to h_out), then bf16(h * (1 / sqrt(mean(h^2) + eps)) * gain). The sums use
+//                the thread mapping and order of the standalone RMSNorm kernel (256 threads, 8 columns
+//                each per 2048), so the result is bit-identical to running that kernel first;
+//   kProSiluGate x is the fused gate|up row [M, 2K]: bf16(silu(g) * u), as the standalone SiLU kernel.
+enum { kProPlain = 0, kProResNorm = 1, kProSiluGate = 2 };
+static constexpr int kProMaxRows = 8;
+
+struct ProArgs {
+  const uint16_t* delta;  // kProResNorm: residual delta [M, K] or null
+  const uint16_t* gain;   // kProResNorm: RMSNorm gain [K]
+  uint16_t* h_out;        // kProResNorm: x + delta [M, K] (written when delta is given)
+  float eps;
+};
+
+template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32, int PRO = kProPlain>
 __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
                                                     void* __restrict__ yv, const uint16_t* __restrict__ bias,
                                                     const float* __restrict__ colscale, int M, int N, int K, int KB,
-                                                    int kbw) {
+                                                    int kbw, const ProArgs pa) {
+  static_assert(PRO == kProPlain || (XLDS && MCH == 1), "activation prologues need the LDS copy");
   extern __shared__ f32x4_t smem[];  // [NW][MCH][64] partial accumulators, then (XLDS) the activations
   f32x4_t* red = smem;
   const int lane = threadIdx.x & 63;
@@ -68,7 +86,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
   const int jg = lane >> 4;
 
   const typename W::Ctx wc = W::ctx(wa, t, KB, lane);
-  const rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
+  const rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * (PRO == kProSiluGate ? 4u : 2u));
   constexpr int KBLK = W::KBLK;
   constexpr int STEPS = W::STEPS;
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem + nw * MCH * 64);
@@ -90,7 +108,94 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
   };
   if (kb0 < kb1) load_round(kb0, w, p);
   // The first weight round is in flight while the activations are copied into LDS.
-  if (XLDS) {
+  if constexpr (PRO == kProResNorm) {
+    // The 256 threads of the standalone kernel are emulated by "virtual threads" vt (in passes when
+    // the workgroup is smaller; a workgroup is a whole number of waves, so a virtual wave is a real
+    // one). Pass 1: h, its sum of squares per row, h -> LDS.
+    __shared__ float pro_red[kProMaxRows][4];
+    const int tid = threadIdx.x;
+    for (int base = 0; base < 256; base += blockDim.x) {
+      const int vt = base + tid;
+      float ss[kProMaxRows];
+#pragma unroll
+      for (int r = 0; r < kProMaxRows; ++r) {
+        ss[r] = 0.0f;
+        if (r < M && vt < 256) {
+          for (int c = vt * 8; c < K; c += 256 * 8) {
+            u32x4_t v = bload128(xr, (uint32_t)(r * K + c) * 2u, 0u);
+            if (pa.delta != nullptr) {
+              const u32x4_t dv = *reinterpret_cast<const u32x4_t*>(pa.delta + (int64_t)r * K + c);
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                v[j] = ActBF16::pack_rne(bf16_lo(v[j]) + bf16_lo(dv[j]), bf16_hi(v[j]) + bf16_hi(dv[j]));
+              if (blockIdx.x == 0) *reinterpret_cast<u32x4_t*>(pa.h_out + (int64_t)r * K + c) = v;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float a0 = bf16_lo(v[j]), a1 = bf16_hi(v[j]);
+              ss[r] = fmaf(a0, a0, ss[r]);
+              ss[r] = fmaf(a1, a1, ss[r]);
+            }
+            *reinterpret_cast<u32x4_t*>(xs + r * xpitch + c) = v;
+          }
+        }
+      }
+      if (vt < 256) {  // whole waves
+#pragma unroll
+        for (int r = 0; r < kProMaxRows; ++r) {
+          if (r < M) {
+            const float t = wave_sum(ss[r]);
+            if ((vt & 63) == 0) pro_red[r][vt >> 6] = t;
+          }
+        }
+      }
+    }
+    // zero the padding columns of the LDS rows
+    for (int idx = tid; idx < M * (KB * KBLK - K) / 8; idx += blockDim.x) {
+      const int per = (KB * KBLK - K) / 8;
+      const int r = idx / per;
+      *reinterpret_cast<u32x4_t*>(xs + r * xpitch + K + (idx - r * per) * 8) = u32x4_t{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+    // pass 2: normalise in place with the row's factor and the gain
+    for (int vt = tid; vt < 256; vt += blockDim.x) {
+#pragma unroll
+      for (int r = 0; r < kProMaxRows; ++r) {
+        if (r < M) {
+          const float tot = (pro_red[r][0] + pro_red[r][1]) + (pro_red[r][2] + pro_red[r][3]);
+          const float rr = 1.0f / sqrtf(tot / static_cast<float>(K) + pa.eps);
+          for (int c = vt * 8; c < K; c += 256 * 8) {
+            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xs + r * xpitch + c);
+            const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(pa.gain + c);
+            u32x4_t o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              o[j] = ActBF16::pack_rne(bf16_lo(v[j]) * rr * bf16_lo(wv[j]), bf16_hi(v[j]) * rr * bf16_hi(wv[j]));
+            *reinterpret_cast<u32x4_t*>(xs + r * xpitch + c) = o;
+          }
+        }
+      }
+    }
+    __syncthreads();
+  } else if constexpr (PRO == kProSiluGate) {
+    const int chunks_per_row = KB * KBLK / 8;
+    for (int idx = threadIdx.x; idx < M * chunks_per_row; idx += blockDim.x) {
+      const int r = idx / chunks_per_row;
+      const int col = (idx - r * chunks_per_row) * 8;
+      u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
+      if (col < K) {
+        const u32x4_t g2 = bload128(xr, (uint32_t)(r * 2 * K + col) * 2u, 0u);
+        const u32x4_t u2 = bload128(xr, (uint32_t)(r * 2 * K + K + col) * 2u, 0u);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float g0 = bf16_lo(g2[j]), g1 = bf16_hi(g2[j]);
+          v[j] = ActBF16::pack_rne(g0 / (1.0f + __expf(-g0)) * bf16_lo(u2[j]), g1 / (1.0f + __expf(-g1)) * bf16_hi(u2[j]));
+        }
+      }
+      *reinterpret_cast<u32x4_t*>(xs + r * xpitch + col) = v;
+    }
+    __syncthreads();
+  } else if (XLDS) {
     const int chunks_per_row = KB * KBLK / 8;  // 16-byte chunks of a padded row
     for (int idx = threadIdx.x; idx < M * chunks_per_row; idx += blockDim.x) {
       const int r = idx / chunks_per_row;
@@ -189,10 +294,10 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
 
 // Launch the GEMV for every 64-row pass of x. k_slices <= 0 picks the default. Returns 0 or the
 // HIP error of the launch.
-template <class A, class W, int U1, int U2, bool YF32>
+template <class A, class W, int U1, int U2, bool YF32, int PRO = kProPlain>
 hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, const uint16_t* bias,
                        const float* colscale, int64_t m, int64_t rows, int64_t cols, int k_slices,
-                       hipStream_t stream) {
+                       hipStream_t stream, const ProArgs& pa = ProArgs{nullptr, nullptr, nullptr, 0.0f}) {
   constexpr int KBLK = W::KBLK;
   const int64_t T = ceil_div(rows, 16);
   const int64_t KB = ceil_div(cols, KBLK);
@@ -211,10 +316,14 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     const size_t red = static_cast<size_t>(nw) * mch * 64 * sizeof(f32x4_t);
     const bool xlds = mch == 1 && gemv_xlds_bytes(M, KB, KBLK) <= kXldsMax;
     if (colscale != nullptr && !xlds) return hipErrorNotSupported;  // column scaling happens in the LDS copy
-#define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_)                                                                    \
-  hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32>), grid, block, LDS_, stream, wa, xp, yp, bias, \
-                     colscale, M, N, K, iKB, kbw)
-    if (xlds) {
+#define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_)                                                                          \
+  hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO>), grid, block, LDS_, stream, wa, xp, yp, bias, \
+                     colscale, M, N, K, iKB, kbw, pa)
+    if constexpr (PRO != kProPlain) {
+      if (!xlds || m > kProMaxRows || cols % 8 != 0) return hipErrorNotSupported;  // the caller checks first
+      const size_t lds = red + gemv_xlds_bytes(M, KB, KBLK);
+      if (ktail) SQX_GEMV(1, U1, true, true, lds); else SQX_GEMV(1, U1, false, true, lds);
+    } else if (xlds) {
       const size_t lds = red + gemv_xlds_bytes(M, KB, KBLK);
       if (ktail) SQX_GEMV(1, U1, true, true, lds); else SQX_GEMV(1, U1, false, true, lds);
     } else if (mch == 1) {

@@ -393,6 +393,24 @@ static hipError_t launch_int4(const uint8_t* wt, const void* st, const void* zt,
   return gemv_launch<A, W, SQX_INT4_U1, SQX_INT4_U2, false>(a, x, y, bias, colscale, m, rows, cols, k_slices, s);
 }
 
+// The decode step's fused linears (symmetric codes, fp32 scales, bf16 activations): the residual
+// add + RMSNorm, or the SiLU gate, computed in the LDS copy of the activations.
+template <int PRO>
+static hipError_t launch_int4_pro(int group, const uint8_t* wt, const float* st, const uint16_t* x, uint16_t* y,
+                                  int64_t m, int64_t rows, int64_t cols, int k_slices, hipStream_t s, const ProArgs& pa) {
+#define SQX_PRO(G_)                                                                                              \
+  {                                                                                                              \
+    using W = WInt4<G_, false, false>;                                                                           \
+    const typename W::Args a{wt, st, nullptr};                                                                   \
+    return gemv_launch<ActBF16, W, SQX_INT4_U1, SQX_INT4_U2, false, PRO>(a, x, y, nullptr, nullptr, m, rows, cols, \
+                                                                         k_slices, s, pa);                      \
+  }
+  if (group == 128) SQX_PRO(128)
+  if (group == 64) SQX_PRO(64)
+  SQX_PRO(32)
+#undef SQX_PRO
+}
+
 template <class A, bool ASYM, bool PBF16>
 static hipError_t launch_int4_g(int group, const uint8_t* wt, const void* st, const void* zt, const uint16_t* x,
                                 uint16_t* y, const uint16_t* bias, const float* colscale, int64_t m, int64_t rows,
@@ -722,4 +740,58 @@ extern "C" int sqx_int4_linear_colscaled(const uint8_t* wt, const void* st, cons
   SQX_REQUIRE(col_scale != nullptr, SQX_E_ARG, "sqx_int4_linear_colscaled: null col_scale");
   return int4_linear_impl(wt, st, zt, param_dtype, x, act_dtype, y, bias, col_scale, m, rows, cols, group, k_slices,
                           stream, "sqx_int4_linear_colscaled");
+}
+
+extern "C" int sqx_int4_prologue_fits(int64_t m, int64_t cols) {
+  return m >= 1 && m <= kProMaxRows && cols % 8 == 0 && cols > 0 &&
+         gemv_xlds_bytes(m, ceil_div(cols, 128)) <= kXldsMax;
+}
+
+static int int4_pro_check(const uint8_t* wt, const float* st, const void* x, void* y, int64_t m, int64_t rows,
+                          int64_t cols, int64_t group, int k_slices, const char* fn) {
+  SQX_REQUIRE(rows > 0 && cols > 0 && rows < ((int64_t)1 << 31), SQX_E_ARG, "%s: bad shape", fn);
+  SQX_REQUIRE(group == 32 || group == 64 || group == 128, SQX_E_ARG, "%s: group_size %lld unsupported (32, 64 or 128)",
+              fn, (long long)group);
+  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld", (long long)cols,
+              (long long)group);
+  SQX_REQUIRE(sqx_int4_prologue_fits(m, cols), SQX_E_ARG,
+              "%s: m=%lld, cols=%lld: the fused prologue needs m <= %d and the rows in 64 KiB of LDS", fn, (long long)m,
+              (long long)cols, kProMaxRows);
+  SQX_REQUIRE(k_slices <= 16, SQX_E_ARG, "%s: k_slices %d > 16", fn, k_slices);
+  SQX_REQUIRE(wt && st && x && y, SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, SQX_E_ARG,
+              "%s: wt and x must be 16-byte aligned", fn);
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_linear_rmsnorm(const uint8_t* wt, const float* st, const void* x, const void* delta,
+                                       const void* gain, float eps, void* h_out, void* y, int64_t m, int64_t rows,
+                                       int64_t cols, int64_t group, int k_slices, sqx_stream_t stream) {
+  const char* fn = "sqx_int4_linear_rmsnorm";
+  const int rc = int4_pro_check(wt, st, x, y, m, rows, cols, group, k_slices, fn);
+  if (rc != SQX_OK) return rc;
+  SQX_REQUIRE(gain != nullptr && (delta == nullptr || h_out != nullptr), SQX_E_ARG, "%s: null gain or h_out", fn);
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(gain) % 16 == 0 && reinterpret_cast<uintptr_t>(delta) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(h_out) % 16 == 0,
+              SQX_E_ARG, "%s: gain, delta and h_out must be 16-byte aligned", fn);
+  const ProArgs pa{static_cast<const uint16_t*>(delta), static_cast<const uint16_t*>(gain), static_cast<uint16_t*>(h_out),
+                   eps};
+  const hipError_t e = launch_int4_pro<kProResNorm>(static_cast<int>(group), wt, st, static_cast<const uint16_t*>(x),
+                                                    static_cast<uint16_t*>(y), m, rows, cols, k_slices,
+                                                    as_stream(stream), pa);
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_linear_silu(const uint8_t* wt, const float* st, const void* gate_up, void* y, int64_t m,
+                                    int64_t rows, int64_t cols, int64_t group, int k_slices, sqx_stream_t stream) {
+  const char* fn = "sqx_int4_linear_silu";
+  const int rc = int4_pro_check(wt, st, gate_up, y, m, rows, cols, group, k_slices, fn);
+  if (rc != SQX_OK) return rc;
+  const hipError_t e = launch_int4_pro<kProSiluGate>(static_cast<int>(group), wt, st,
+                                                     static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(y),
+                                                     m, rows, cols, k_slices, as_stream(stream),
+                                                     ProArgs{nullptr, nullptr, nullptr, 0.0f});
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
 }

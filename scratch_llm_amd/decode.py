@@ -119,6 +119,8 @@ class DecodeState:
         lib = _lib.load()
         nb = int(lib.sqx_attn_workspace_bytes(batch, cfg.n_heads, hkv, max_ctx))
         self.attn_ws = torch.empty(max(nb // 4, 4), dtype=torch.float32, device=dev)
+        nb = int(lib.sqx_argmax_workspace_bytes(batch, cfg.vocab_size))
+        self.argmax_ws = torch.empty(max(nb // 4, 4), dtype=torch.float32, device=dev)
         gw = 0
         if batch >= i4.GEMM_MIN_M:
             for tw in model.linears():
@@ -154,6 +156,12 @@ class Int4DecodeLM:
         self.final_norm = final_norm
         self.lm_head = lm_head
         self.device = embed.device
+        # Which small-batch prologues run inside the linears. The SiLU gate pays (one launch fewer, and
+        # a 256-workgroup down projection recomputes it cheaply); the norm does not (every workgroup of
+        # the wide qkv / gate-up / lm_head projections would recompute the whole row's norm), so it
+        # stays a kernel of its own unless asked for.
+        self.fuse_norm = False
+        self.fuse_silu = True
         cos, sin = rope_tables(cfg.head_dim, cfg.context_length, cfg.rope_theta)
         self.cos = cos.to(self.device)
         self.sin = sin.to(self.device)
@@ -254,6 +262,25 @@ class Int4DecodeLM:
             )
         _lib.check(rc, "int4 linear")
 
+    def _norm_linear(self, st: DecodeState, cur: int, delta: int | None, gain: Tensor, tw: i4.Int4Tiled, y: Tensor,
+                     stream: int) -> int:
+        """RMSNorm of the residual stream (after adding ``delta`` when given) feeding ``tw``; returns the
+        index of the buffer that holds the residual stream afterwards. Small batches run it as one
+        kernel when ``fuse_norm`` is set (the norm computed in the linear's LDS copy of the activations),
+        otherwise as two."""
+        cfg, lib, B, d = self.cfg, _lib.load(), st.batch, self.cfg.d_model
+        nxt = cur if delta is None else 1 - cur
+        h_out = None if delta is None else st.x[nxt].data_ptr()
+        if self.fuse_norm and lib.sqx_int4_prologue_fits(B, d):
+            _lib.check(lib.sqx_int4_linear_rmsnorm(
+                tw.wt.data_ptr(), tw.st.data_ptr(), st.x[cur].data_ptr(), delta, gain.data_ptr(), cfg.norm_eps, h_out,
+                y.data_ptr(), B, tw.rows, tw.cols, tw.group_size, 0, stream), "rmsnorm + int4 linear")
+        else:
+            _lib.check(lib.sqx_rmsnorm(st.x[cur].data_ptr(), delta, gain.data_ptr(), cfg.norm_eps, B, d, h_out,
+                                       st.h.data_ptr(), stream), "rmsnorm")
+            self._linear(st, tw, st.h, y, stream)
+        return nxt
+
     def step(self, st: DecodeState, tokens=None) -> Tensor:
         """Decode one token per row: logits of ``st.tokens`` (or ``tokens``) at each row's position,
         written to ``st.logits``; the greedy picks replace ``st.tokens``; active rows advance. Returns
@@ -265,35 +292,30 @@ class Int4DecodeLM:
         B, d, H, Hkv, hd, T = st.batch, cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, st.max_ctx
         s = _lib.stream_ptr(self.device)
         ck = _lib.check
+        fuse_silu = self.fuse_silu and lib.sqx_int4_prologue_fits(B, cfg.d_ff)
         with torch.cuda.device(self.device):
             ck(lib.sqx_embed(self.embed.data_ptr(), cfg.vocab_size, st.tokens.data_ptr(), B, d, st.x[0].data_ptr(), s),
                "embed")
             cur, delta = 0, None
             for li, ly in enumerate(self.layers):
-                for norm, sub in ((ly.attn_norm, 0), (ly.ffn_norm, 1)):
-                    if delta is None:
-                        ck(lib.sqx_rmsnorm(st.x[cur].data_ptr(), None, norm.data_ptr(), cfg.norm_eps, B, d, None,
-                                           st.h.data_ptr(), s), "rmsnorm")
-                    else:
-                        ck(lib.sqx_rmsnorm(st.x[cur].data_ptr(), delta, norm.data_ptr(), cfg.norm_eps, B, d,
-                                           st.x[1 - cur].data_ptr(), st.h.data_ptr(), s), "rmsnorm")
-                        cur = 1 - cur
-                    if sub == 0:
-                        self._linear(st, ly.wqkv, st.h, st.qkv, s)
-                        ck(lib.sqx_decode_attention_rope(
-                            st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
-                            cfg.context_length, st.k[li].data_ptr(), st.v[li].data_ptr(), B, H, Hkv, hd, T,
-                            st.attn.data_ptr(), st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention")
-                        self._linear(st, ly.wo, st.attn, st.delta, s)
-                    else:
-                        self._linear(st, ly.w13, st.h, st.gu, s)
-                        ck(lib.sqx_silu_mul(st.gu.data_ptr(), B, cfg.d_ff, st.act.data_ptr(), s), "silu_mul")
-                        self._linear(st, ly.w2, st.act, st.delta, s)
-                    delta = st.delta.data_ptr()
-            ck(lib.sqx_rmsnorm(st.x[cur].data_ptr(), delta, self.final_norm.data_ptr(), cfg.norm_eps, B, d,
-                               st.x[1 - cur].data_ptr(), st.h.data_ptr(), s), "rmsnorm")
-            self._linear(st, self.lm_head, st.h, st.logits, s)
-            ck(lib.sqx_argmax(st.logits.data_ptr(), B, cfg.vocab_size, st.tokens.data_ptr(), s), "argmax")
+                cur = self._norm_linear(st, cur, delta, ly.attn_norm, ly.wqkv, st.qkv, s)
+                ck(lib.sqx_decode_attention_rope(
+                    st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
+                    cfg.context_length, st.k[li].data_ptr(), st.v[li].data_ptr(), B, H, Hkv, hd, T,
+                    st.attn.data_ptr(), st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention")
+                self._linear(st, ly.wo, st.attn, st.delta, s)
+                delta = st.delta.data_ptr()
+                cur = self._norm_linear(st, cur, delta, ly.ffn_norm, ly.w13, st.gu, s)
+                if fuse_silu:
+                    ck(lib.sqx_int4_linear_silu(ly.w2.wt.data_ptr(), ly.w2.st.data_ptr(), st.gu.data_ptr(),
+                                                st.delta.data_ptr(), B, ly.w2.rows, ly.w2.cols, ly.w2.group_size, 0, s),
+                       "silu + int4 linear")
+                else:
+                    ck(lib.sqx_silu_mul(st.gu.data_ptr(), B, cfg.d_ff, st.act.data_ptr(), s), "silu_mul")
+                    self._linear(st, ly.w2, st.act, st.delta, s)
+            cur = self._norm_linear(st, cur, delta, self.final_norm, self.lm_head, st.logits, s)
+            ck(lib.sqx_argmax(st.logits.data_ptr(), B, cfg.vocab_size, st.tokens.data_ptr(), st.argmax_ws.data_ptr(),
+                              st.argmax_ws.numel() * 4, s), "argmax")
             ck(lib.sqx_advance(st.lengths.data_ptr(), st.active.data_ptr(), B, s), "advance")
         return st.tokens
 

@@ -187,6 +187,70 @@ def test_fused_rope_attention_equals_two_calls(lib, B, H, Hkv, T):
     assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
 
 
+def _tiled(n, k, group, seed):
+    from scratch_llm_amd.quant import int4_group as i4
+
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(n, k, generator=g) * 0.05).to(DEV)
+    q, s = i4.quantize_groupwise_int4(w, group)
+    return i4.tile_int4(q, s, None, group)
+
+
+@pytest.mark.parametrize("m,k,group,with_delta", [(1, 4096, 128, True), (3, 4096, 128, False), (7, 4096, 64, True),
+                                                  (2, 1056, 32, True), (8, 1024, 128, True)])
+def test_linear_rmsnorm_equals_two_calls(lib, m, k, group, with_delta):
+    """sqx_int4_linear_rmsnorm == sqx_rmsnorm then sqx_int4_linear, bit for bit (y and the residual)."""
+    print_case("linear+rmsnorm", m, k, group, with_delta)
+    n = 528
+    tw = _tiled(n, k, group, seed=m + k)
+    g = torch.Generator().manual_seed(k)
+    x = (torch.randn(m, k, generator=g) * 2).bfloat16().to(DEV)
+    dl = torch.randn(m, k, generator=g).bfloat16().to(DEV) if with_delta else None
+    gain = (1 + 0.1 * torch.randn(k, generator=g)).bfloat16().to(DEV)
+    assert lib.sqx_int4_prologue_fits(m, k) == 1
+    h1, h2 = (torch.empty(m, k, dtype=torch.bfloat16, device=DEV) for _ in range(2))
+    hn = torch.empty(m, k, dtype=torch.bfloat16, device=DEV)
+    y1, y2 = (torch.empty(m, n, dtype=torch.bfloat16, device=DEV) for _ in range(2))
+    dp = None if dl is None else dl.data_ptr()
+    _ok(lib, lib.sqx_rmsnorm(x.data_ptr(), dp, gain.data_ptr(), 1e-5, m, k, h1.data_ptr() if dl is not None else None,
+                             hn.data_ptr(), _s()))
+    _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, hn.data_ptr(), 1, y1.data_ptr(), None, m, n,
+                                 k, group, 0, _s()))
+    _ok(lib, lib.sqx_int4_linear_rmsnorm(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), dp, gain.data_ptr(), 1e-5,
+                                         h2.data_ptr() if dl is not None else None, y2.data_ptr(), m, n, k, group, 0, _s()))
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    if dl is not None:
+        assert torch.equal(h1, h2)
+
+
+@pytest.mark.parametrize("m,f", [(1, 14336), (2, 14336), (5, 2048)])
+def test_linear_silu_equals_two_calls(lib, m, f):
+    print_case("linear+silu", m, f)
+    n = 4096 if f == 14336 else 1000
+    tw = _tiled(n, f, 128, seed=f)
+    gu = (torch.randn(m, 2 * f, generator=torch.Generator().manual_seed(m)) * 3).bfloat16().to(DEV)
+    act = torch.empty(m, f, dtype=torch.bfloat16, device=DEV)
+    y1, y2 = (torch.empty(m, n, dtype=torch.bfloat16, device=DEV) for _ in range(2))
+    _ok(lib, lib.sqx_silu_mul(gu.data_ptr(), m, f, act.data_ptr(), _s()))
+    _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, act.data_ptr(), 1, y1.data_ptr(), None, m, n,
+                                 f, 128, 0, _s()))
+    _ok(lib, lib.sqx_int4_linear_silu(tw.wt.data_ptr(), tw.st.data_ptr(), gu.data_ptr(), y2.data_ptr(), m, n, f, 128, 0,
+                                      _s()))
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+
+
+def test_fused_prologue_refuses_what_does_not_fit(lib):
+    assert lib.sqx_int4_prologue_fits(8, 4096) == 0  # 8 rows of 4096 exceed the 64 KiB copy
+    assert lib.sqx_int4_prologue_fits(3, 14336) == 0
+    assert lib.sqx_int4_prologue_fits(9, 128) == 0
+    tw = _tiled(64, 4096, 128, seed=1)
+    x = torch.zeros(8, 4096, dtype=torch.bfloat16, device=DEV)
+    assert lib.sqx_int4_linear_rmsnorm(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), None, x.data_ptr(), 1e-5, None,
+                                       x.data_ptr(), 8, 64, 4096, 128, 0, _s()) == -1
+
+
 def test_attention_rejects_bad_shapes(lib):
     ws = torch.empty(16, dtype=torch.float32, device=DEV)
     assert lib.sqx_decode_attention(ws.data_ptr(), ws.data_ptr(), ws.data_ptr(), ws.data_ptr(), 1, 32, 8, 64, 16, ws.data_ptr(),
@@ -234,7 +298,18 @@ def test_embed_argmax_advance(lib):
         lg[3, Vv - 1] = float("nan")
         lg[4, :] = float("-inf")
         nt = torch.empty(6, dtype=torch.int32, device=DEV)
-        _ok(lib, lib.sqx_argmax(lg.to(DEV).data_ptr(), 6, Vv, nt.data_ptr(), _s()))
+        nb = lib.sqx_argmax_workspace_bytes(6, Vv)
+        ws = torch.empty(nb // 4, dtype=torch.float32, device=DEV)
+        _ok(lib, lib.sqx_argmax(lg.to(DEV).data_ptr(), 6, Vv, nt.data_ptr(), ws.data_ptr(), nb, _s()))
+        if Vv == 128256:  # a row split over many workgroups: the max in the last one, and a tie across two
+            lg2 = torch.zeros(2, Vv).bfloat16()
+            lg2[0, Vv - 3] = 5.0
+            lg2[1, 10] = 7.0
+            lg2[1, Vv - 9] = 7.0
+            nt2 = torch.empty(2, dtype=torch.int32, device=DEV)
+            _ok(lib, lib.sqx_argmax(lg2.to(DEV).data_ptr(), 2, Vv, nt2.data_ptr(), ws.data_ptr(), nb, _s()))
+            torch.cuda.synchronize()
+            assert nt2.cpu().tolist() == [Vv - 3, 10]
         torch.cuda.synchronize()
         assert nt.cpu().tolist() == lg.float().argmax(dim=-1).tolist()
     # advance: named values of tests/test_batched_cache.py:91-103
@@ -297,6 +372,27 @@ def _run_and_compare(model, refs, B, steps, seed, max_ctx=48):
 def test_decode_step_matches_reference(small, B):
     model, refs = small
     _run_and_compare(model, refs, B, steps=6 if B < 64 else 3, seed=B)
+
+
+@pytest.mark.parametrize("B", [1, 2, 5])
+def test_fused_step_equals_unfused_step(small, B):
+    """The norm and SiLU gate folded into the linears change no bit of the step."""
+    model, _ = small
+    print_case("fused vs unfused step", B)
+    a, b = model.new_state(B, 32), model.new_state(B, 32)
+    tok = torch.arange(B) * 97 % model.cfg.vocab_size
+    try:
+        for t in range(4):
+            model.fuse_norm = model.fuse_silu = True
+            model.step(a, tok if t == 0 else None)
+            model.fuse_norm = model.fuse_silu = False
+            model.step(b, tok if t == 0 else None)
+            torch.cuda.synchronize()
+            assert torch.equal(a.logits, b.logits), f"step {t}"
+            assert torch.equal(a.tokens, b.tokens)
+        assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
+    finally:
+        model.fuse_norm, model.fuse_silu = False, True
 
 
 def test_graph_replays_equal_eager_steps(small):
