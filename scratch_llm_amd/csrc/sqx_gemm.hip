@@ -7,9 +7,10 @@
 // F.linear(mxfp4_dequantize(x), mxfp4_dequantize(W)) (nvfp4_mxfp4.py:257-272 composed with F.linear)
 // without materialising either operand: every product of two dequantized values is exact in fp32.
 //
-// Tiling. One workgroup (4 waves) owns a 256 (m) x 256 (n) output tile; wave w computes the
-// 128 x 128 quarter (w >> 1, w & 1) as 4 x 4 MFMA tiles of 32 x 32 held in 256 accumulation
-// registers. A k-step covers one 128-column FP4 block: 16 fragments (1 KiB each, 16 rows x 128
+// Tiling. One workgroup owns a 256 (m) x 256 (n) output tile. With the default WN = 4 it has eight
+// waves (two per SIMD); wave w computes the 128 x 64 part (w / 4, w % 4) as 4 x 2 MFMA tiles of
+// 32 x 32 held in 128 accumulation registers (WN = 2: four waves of 128 x 128, 4 x 4 tiles, 256
+// registers). A k-step covers one 128-column FP4 block: 16 fragments (1 KiB each, 16 rows x 128
 // columns) of X and 16 of W plus their 64-byte scale blocks, 34 KiB, copied global -> LDS by
 // buffer loads that write LDS directly (no VGPR round trip) into a ring of NSTAGE stages, NSTAGE-1
 // k-steps ahead of the MFMAs. A 32 x 64 MFMA operand (rows 32r.., k-half h) is read from two
