@@ -347,6 +347,53 @@ int sqx_int8_linear(const uint8_t* wt, const float* scale, const void* x, int ac
                     sqx_stream_t stream);
 
 /* ============================================================================================
+ * FP8 E4M3 (src/scratch_llm/quant/fp8_weights.py, fp8_kv_per_head.py). Codes are OCP e4m3fn bytes
+ * (torch.float8_e4m3fn); every quantizer is saturating_cast_e4m3 (clamp to +-448, round to nearest
+ * even; fp8_weights.py:117-124) of fp32(x) / scale, bit-exact with the reference.
+ * ============================================================================================ */
+
+/* quantize_per_channel (fp8_weights.py:133-143) of a weight [rows, cols], or quantize_per_token
+ * (:146-155) of activations [rows, cols]: scale[r] = max(amax_c |x[r, c]| / 448, 1 / (448 * 512)) in
+ * fp32, codes[r, c] = saturating_cast(fp32(x[r, c]) / scale[r]). x: F32 / BF16 / F16. */
+int sqx_fp8_quantize_rows(const void* x, int dtype, int64_t rows, int64_t cols, uint8_t* codes, float* scale,
+                          sqx_stream_t stream);
+
+/* dequantize (fp8_weights.py:158-160): out[r, c] = fp32(codes[r, c]) * scale[r]; out fp32. */
+int sqx_fp8_dequantize_rows(const uint8_t* codes, const float* scale, int64_t rows, int64_t cols, float* out,
+                            sqx_stream_t stream);
+
+/* per_head_amax / per_head_scale (fp8_kv_per_head.py:77-91) of a KV block x [B, H, inner]
+ * (inner = T * D): amax[h] = max over (b, t, d) of |x| and scale[h] = max(amax[h] / 448,
+ * 1 / (448 * 512)), fp32 [H] each (either pointer may be NULL). */
+int sqx_fp8_head_scale(const void* x, int dtype, int64_t B, int64_t H, int64_t inner, float* amax, float* scale,
+                       sqx_stream_t stream);
+
+/* quantize_per_head (fp8_kv_per_head.py:93-96): codes = saturating_cast(fp32(x) / scale[h]) over
+ * [B, H, inner]. saturated (NULL or one uint64 in device memory): incremented by the number of
+ * elements with |x| > 448 * scale[h] (saturated_count, :104-107). */
+int sqx_fp8_quantize_heads(const void* x, int dtype, int64_t B, int64_t H, int64_t inner, const float* scale,
+                           uint8_t* codes, unsigned long long* saturated, sqx_stream_t stream);
+
+/* dequantize_per_head (fp8_kv_per_head.py:99-101): out = fp32(codes) * scale[h], fp32 [B, H, inner]. */
+int sqx_fp8_dequantize_heads(const uint8_t* codes, const float* scale, int64_t B, int64_t H, int64_t inner,
+                             float* out, sqx_stream_t stream);
+
+/* Bytes of the tiled FP8 weight and its re-lay from codes [rows, cols] (no reference counterpart:
+ * 1 KiB blocks of 16 rows x 64 columns). */
+int64_t sqx_fp8_tiled_weight_bytes(int64_t rows, int64_t cols);
+int sqx_fp8_tile(const uint8_t* codes, int64_t rows, int64_t cols, uint8_t* wt, sqx_stream_t stream);
+
+/* fp8_linear (fp8_weights.py:211-262): x [m, cols] (F32 / BF16 / F16) is quantized per token,
+ * y[i, r] = (sum_c qx[i, c] * qw[r, c]) * s_x[i] * w_scale[r] (+ bias[r]) with exact products and fp32
+ * accumulation; y [m, rows] of y_dtype (BF16, or F32 without bias); bias BF16 or NULL. wt from
+ * sqx_fp8_tile; w_scale fp32 [rows]. cols % 8 == 0. ws: sqx_fp8_linear_workspace_bytes(m, cols) bytes
+ * (the quantized activations), 16-byte aligned. */
+int64_t sqx_fp8_linear_workspace_bytes(int64_t m, int64_t cols);
+int sqx_fp8_linear(const uint8_t* wt, const float* w_scale, const void* x, int act_dtype, void* y, int y_dtype,
+                   const void* bias, int64_t m, int64_t rows, int64_t cols, int k_slices, void* ws,
+                   int64_t ws_bytes, sqx_stream_t stream);
+
+/* ============================================================================================
  * Decode step around the quantized linears: the ops that src/scratch_llm/
  * model.py runs between the Linear calls of one token, against the dense slot KV cache of
  * kv_cache.py:234-262 (BatchedKVCache). Activations are bf16 rows; lengths[b] (int32) is the slot's

@@ -108,6 +108,18 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sqx_col_absmean": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_awq_scale": (_c_i, [_c_p, _c_i64, ctypes.c_float, _c_p, _c_p]),
     "sqx_scale_columns": (_c_i, [_c_p, _c_i, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_fp8_quantize_rows": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "sqx_fp8_dequantize_rows": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_fp8_head_scale": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "sqx_fp8_quantize_heads": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p]),
+    "sqx_fp8_dequantize_heads": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_fp8_tiled_weight_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "sqx_fp8_tile": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_fp8_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "sqx_fp8_linear": (
+        _c_i,
+        [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_i, _c_p, _c_i64, _c_p],
+    ),
     "sqx_rmsnorm": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "sqx_rope_kv": (
         _c_i,

@@ -1,0 +1,342 @@
+// FP8 E4M3 (OCP e4m3fn: bias 7, no infinities, NaN = S.1111.111) on gfx950: the quantizers of
+// src/scratch_llm/quant/fp8_weights.py (per output channel, per token) and fp8_kv_per_head.py (per
+// head), bit-exact with the reference's torch casts, and the W8A8 linear (fp8_linear).
+//
+// The linear. fp8_linear multiplies per-token E4M3 activations by per-channel E4M3 weights with fp32
+// accumulation and applies s_x[m] * s_w[n] (fp8_weights.py:14-31, 211-262). Every E4M3 value is exact
+// in bf16 and every product of two is exact in fp32, so this build decodes both operands to bf16
+// (v_cvt_pk_f32_fp8, exact for all 256 codes) and runs the bf16 MFMA: the only rounding left is the
+// fp32 accumulation and the output cast, which keeps the result inside the reference's derived bound
+// (|ref| eps_out/2 + sqrt(K) eps_f32 sum|x w|). The block-scaled fp8 MFMA aligns a step's 128
+// products to the largest with a limited-width adder (measured error up to 1.4e-4 of sum|x w| per
+// step) and does not meet that bound, nor does the library GEMM built on it.
+//
+// Tiled FP8 weights: block (t, kb) = 1 KiB covering 16 rows x 64 columns; lane L owns the 16 codes of
+// row 16t + (L & 15), columns kb*64 + 16(L >> 4) + e, code e in byte e. Padding holds code 0.
+#include "sqx_gemv.h"
+
+namespace sqx {
+
+constexpr float kE4M3Max = 448.0f;
+// MIN_SCALE = 1 / (448 * 512) (fp8_weights.py:100), as the fp32 value torch compares against.
+constexpr float kFp8MinScale = static_cast<float>(1.0 / (448.0 * 512.0));
+
+// saturating_cast_e4m3 (fp8_weights.py:117-124): clamp to +-448, then round to nearest even. NaN
+// stays NaN (0x7f with the input's sign, as torch's cast encodes it).
+__device__ inline uint32_t e4m3_encode_sat(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  if (v != v) return sign | 0x7fu;
+  const float a = fminf(fabsf(v), kE4M3Max);
+  uint32_t code;
+  if (a < 0.015625f) {  // below the smallest normal 2**-6: multiples of 2**-9 (code 8 is 2**-6 itself)
+    code = static_cast<uint32_t>(rintf(a * 512.0f));
+  } else {
+    const uint32_t b = __builtin_bit_cast(uint32_t, a);
+    const int e = static_cast<int>(b >> 23) - 127;  // -6 .. 8
+    const uint32_t mant = b & 0x7fffffu;
+    const uint32_t r = mant + 0x7ffffu + ((mant >> 20) & 1u);  // 23 -> 3 bits, ties to even
+    code = (static_cast<uint32_t>(e + 7) << 3) + (r >> 20);    // a mantissa carry bumps the exponent
+  }
+  return sign | code;
+}
+
+// NaN-propagating maximum (torch's amax): once a NaN is seen it stays.
+__device__ inline float nan_max(float acc, float a) { return (a > acc || a != a) ? a : acc; }
+
+template <int DT>
+__device__ inline float load_f(const void* p, int64_t i) {
+  if (DT == SQX_DTYPE_F32) return static_cast<const float*>(p)[i];
+  const uint16_t b = static_cast<const uint16_t*>(p)[i];
+  return DT == SQX_DTYPE_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+__device__ inline float block_max_256(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = nan_max(v, __shfl_xor(v, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) r = nan_max(r, red[w]);
+  return r;
+}
+
+// quantize_per_channel / quantize_per_token (fp8_weights.py:127-155): per row of x [rows, cols],
+// s = max(amax(|x|) / 448, MIN_SCALE) in fp32, codes = saturating_cast(fp32(x) / s). One workgroup
+// of 256 threads per row. Codes go to codes[r * cpitch + c] (cols <= cpitch, padding zero-filled),
+// and, when vals is given, the codes' exact values as bf16 to vals[r * cpitch + c] (the activation
+// operand of the linear).
+template <int DT>
+__global__ __launch_bounds__(256) void fp8_quantize_rows_kernel(const void* __restrict__ x, int64_t cols, int64_t cpitch,
+                                                                uint8_t* __restrict__ codes, float* __restrict__ scale,
+                                                                uint16_t* __restrict__ vals) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const int64_t base = r * cols;
+  float am = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) am = nan_max(am, fabsf(load_f<DT>(x, base + c)));
+  am = block_max_256(am, red);
+  const float q = __fdiv_rn(am, kE4M3Max);
+  const float s = q != q ? q : fmaxf(q, kFp8MinScale);
+  if (threadIdx.x == 0) scale[r] = s;
+  for (int64_t c = threadIdx.x; c < cpitch; c += 256) {
+    uint32_t code = 0;
+    if (c < cols) code = e4m3_encode_sat(__fdiv_rn(load_f<DT>(x, base + c), s));
+    if (codes != nullptr) codes[r * cpitch + c] = static_cast<uint8_t>(code);
+    if (vals != nullptr) {
+      const float d = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(code), false)[0];
+      vals[r * cpitch + c] = static_cast<uint16_t>(__builtin_bit_cast(uint32_t, d) >> 16);  // exact
+    }
+  }
+}
+
+// dequantize (fp8_weights.py:158-160) and dequantize_per_head (fp8_kv_per_head.py:99-101):
+// out[i] = fp32(code[i]) * scale[(i / inner) % nscale] (per-row scales: inner = cols, nscale = rows;
+// per-head scales of [B, H, inner]: nscale = H).
+__global__ __launch_bounds__(256) void fp8_dequantize_kernel(const uint8_t* __restrict__ codes, const float* __restrict__ scale,
+                                                             int64_t n, int64_t inner, int64_t nscale,
+                                                             float* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float d = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(codes[i]), false)[0];
+  out[i] = d * scale[(i / inner) % nscale];
+}
+
+// Per-head amax over (batch, tokens, head_dim) of x [B, H, inner] (fp8_kv_per_head.py:77-91), then
+// scale = max(amax / 448, MIN_SCALE). One workgroup per head.
+template <int DT>
+__global__ __launch_bounds__(256) void fp8_head_scale_kernel(const void* __restrict__ x, int64_t B, int64_t H, int64_t inner,
+                                                             float* __restrict__ amax, float* __restrict__ scale) {
+  __shared__ float red[4];
+  const int64_t h = blockIdx.x;
+  float am = 0.0f;
+  for (int64_t b = 0; b < B; ++b) {
+    const int64_t base = (b * H + h) * inner;
+    for (int64_t c = threadIdx.x; c < inner; c += 256) am = nan_max(am, fabsf(load_f<DT>(x, base + c)));
+  }
+  am = block_max_256(am, red);
+  const float q = __fdiv_rn(am, kE4M3Max);
+  if (threadIdx.x == 0) {
+    if (amax != nullptr) amax[h] = am;
+    if (scale != nullptr) scale[h] = q != q ? q : fmaxf(q, kFp8MinScale);
+  }
+}
+
+// quantize_per_head (fp8_kv_per_head.py:93-96): codes = saturating_cast(fp32(x) / scale[h]) for
+// x [B, H, inner]; sat (optional) counts the elements the clamp moved (|x| > 448 * scale, :104-107).
+template <int DT>
+__global__ __launch_bounds__(256) void fp8_quantize_heads_kernel(const void* __restrict__ x, int64_t n, int64_t H,
+                                                                 int64_t inner, const float* __restrict__ scale,
+                                                                 uint8_t* __restrict__ codes, unsigned long long* __restrict__ sat) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  bool over = false;
+  if (i < n) {
+    const float v = load_f<DT>(x, i);
+    const float s = scale[(i / inner) % H];
+    codes[i] = static_cast<uint8_t>(e4m3_encode_sat(__fdiv_rn(v, s)));
+    over = fabsf(v) > kE4M3Max * s;
+  }
+  if (sat != nullptr) {
+    const unsigned long long cnt = __popcll(__ballot(over));
+    if ((threadIdx.x & 63) == 0 && cnt != 0) atomicAdd(sat, cnt);
+  }
+}
+
+// One thread per dword of the tiled weight (layout in the file comment).
+__global__ __launch_bounds__(256) void fp8_tile_kernel(const uint8_t* __restrict__ q, int64_t rows, int64_t cols, int64_t KB,
+                                                       int64_t n_dwords, uint32_t* __restrict__ wt) {
+  const int64_t d = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (d >= n_dwords) return;
+  const int i = static_cast<int>(d & 3);
+  const int L = static_cast<int>((d >> 2) & 63);
+  const int64_t blk = d >> 8;
+  const int64_t t = blk / KB;
+  const int64_t kb = blk - t * KB;
+  const int64_t r = 16 * t + (L & 15);
+  const int64_t c0 = kb * 64 + 16 * (L >> 4) + 4 * i;
+  uint32_t word = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t c = c0 + e;
+    const uint32_t u = (r < rows && c < cols) ? static_cast<uint32_t>(q[r * cols + c]) : 0u;
+    word |= u << (8 * e);
+  }
+  wt[d] = word;
+}
+
+// GEMV weight policy: E4M3 codes decoded exactly to bf16 (two per v_cvt_pk_f32_fp8), bf16 MFMA
+// against the activations' E4M3 values (as bf16), and s_x[m] * s_w[n] on the fp32 result.
+struct WFp8 {
+  static constexpr int KBLK = 64, STEPS = 2;
+  static constexpr bool kRowScale = true;
+  struct Args {
+    const uint8_t* wt;
+    const float* wscale;  // [rows]
+    const float* xscale;  // [m]
+  };
+  struct Ctx {
+    rsrc_t wr;
+    uint32_t wvo;
+  };
+  struct P {};
+  __device__ static Ctx ctx(const Args& a, int t, int KB, int lane) {
+    return Ctx{make_rsrc(a.wt + (int64_t)t * KB * 1024, (uint32_t)KB * 1024u), (uint32_t)lane * 16u};
+  }
+  __device__ static void load(const Ctx& c, int kb, u32x4_t& w, P&) { w = bload128<2>(c.wr, c.wvo, (uint32_t)kb * 1024u); }
+  __device__ static int xk(int i, int jg) { return 16 * jg + 8 * i; }
+  template <bool HI>
+  __device__ static uint32_t pair(uint32_t d) {  // bytes 0,1 (HI false) or 2,3 of d as a bf16 pair
+    const f32x2_t f = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(d), HI);
+    return ActBF16::pack_exact(f[0], f[1]);
+  }
+  template <class A, int MCH>
+  __device__ static void mma(const u32x4_t& w, const P&, const u32x4_t (&xv)[MCH][STEPS], f32x4_t (&yacc)[MCH]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t d0 = w[2 * i], d1 = w[2 * i + 1];
+      const u32x4_t b = {pair<false>(d0), pair<true>(d0), pair<false>(d1), pair<true>(d1)};
+#pragma unroll
+      for (int c = 0; c < MCH; ++c) yacc[c] = A::mfma(xv[c][i], b, yacc[c]);
+    }
+  }
+  __device__ static float out_scale(const Args& a, int n) { return a.wscale[n]; }
+  __device__ static float row_scale(const Args& a, int m) { return a.xscale[m]; }
+  static Args rows_from(const Args& a, int64_t m0) { return Args{a.wt, a.wscale, a.xscale + m0}; }
+};
+
+}  // namespace sqx
+
+using namespace sqx;
+
+// ==============================================================================================
+// extern "C" entry points
+// ==============================================================================================
+static bool fp8_float_dtype(int d) { return d == SQX_DTYPE_F32 || d == SQX_DTYPE_BF16 || d == SQX_DTYPE_F16; }
+
+#define SQX_FP8_DT(DT_, KERNEL, GRID, ...)                                                                  \
+  switch (DT_) {                                                                                            \
+    case SQX_DTYPE_F32: hipLaunchKernelGGL((KERNEL<SQX_DTYPE_F32>), GRID, dim3(256), 0, __VA_ARGS__); break;  \
+    case SQX_DTYPE_BF16: hipLaunchKernelGGL((KERNEL<SQX_DTYPE_BF16>), GRID, dim3(256), 0, __VA_ARGS__); break; \
+    default: hipLaunchKernelGGL((KERNEL<SQX_DTYPE_F16>), GRID, dim3(256), 0, __VA_ARGS__); break;           \
+  }
+
+extern "C" int sqx_fp8_quantize_rows(const void* x, int dtype, int64_t rows, int64_t cols, uint8_t* codes, float* scale,
+                                     sqx_stream_t stream) {
+  SQX_REQUIRE(fp8_float_dtype(dtype), SQX_E_ARG, "sqx_fp8_quantize_rows: unsupported dtype %d", dtype);
+  SQX_REQUIRE(rows >= 0 && cols >= 0 && rows < (int64_t(1) << 31), SQX_E_ARG, "sqx_fp8_quantize_rows: bad shape");
+  if (rows == 0) return SQX_OK;
+  SQX_REQUIRE(x && codes && scale, SQX_E_ARG, "sqx_fp8_quantize_rows: null pointer");
+  SQX_FP8_DT(dtype, fp8_quantize_rows_kernel, dim3(static_cast<unsigned>(rows)), as_stream(stream), x, cols, cols, codes,
+             scale, static_cast<uint16_t*>(nullptr));
+  SQX_LAUNCH_CHECK("sqx_fp8_quantize_rows");
+  return SQX_OK;
+}
+
+extern "C" int sqx_fp8_dequantize_rows(const uint8_t* codes, const float* scale, int64_t rows, int64_t cols, float* out,
+                                       sqx_stream_t stream) {
+  SQX_REQUIRE(rows >= 0 && cols >= 0, SQX_E_ARG, "sqx_fp8_dequantize_rows: bad shape");
+  const int64_t n = rows * cols;
+  if (n == 0) return SQX_OK;
+  SQX_REQUIRE(codes && scale && out, SQX_E_ARG, "sqx_fp8_dequantize_rows: null pointer");
+  hipLaunchKernelGGL(fp8_dequantize_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, as_stream(stream),
+                     codes, scale, n, cols, rows, out);
+  SQX_LAUNCH_CHECK("sqx_fp8_dequantize_rows");
+  return SQX_OK;
+}
+
+extern "C" int sqx_fp8_head_scale(const void* x, int dtype, int64_t B, int64_t H, int64_t inner, float* amax, float* scale,
+                                  sqx_stream_t stream) {
+  SQX_REQUIRE(fp8_float_dtype(dtype), SQX_E_ARG, "sqx_fp8_head_scale: unsupported dtype %d", dtype);
+  SQX_REQUIRE(B >= 0 && H >= 0 && inner >= 0 && H < (int64_t(1) << 31), SQX_E_ARG, "sqx_fp8_head_scale: bad shape");
+  if (H == 0) return SQX_OK;
+  SQX_REQUIRE((amax || scale) && (x || B * inner == 0), SQX_E_ARG, "sqx_fp8_head_scale: null pointer");
+  SQX_FP8_DT(dtype, fp8_head_scale_kernel, dim3(static_cast<unsigned>(H)), as_stream(stream), x, B, H, inner, amax, scale);
+  SQX_LAUNCH_CHECK("sqx_fp8_head_scale");
+  return SQX_OK;
+}
+
+extern "C" int sqx_fp8_quantize_heads(const void* x, int dtype, int64_t B, int64_t H, int64_t inner, const float* scale,
+                                      uint8_t* codes, unsigned long long* saturated, sqx_stream_t stream) {
+  SQX_REQUIRE(fp8_float_dtype(dtype), SQX_E_ARG, "sqx_fp8_quantize_heads: unsupported dtype %d", dtype);
+  SQX_REQUIRE(B >= 0 && H > 0 && inner >= 0, SQX_E_ARG, "sqx_fp8_quantize_heads: bad shape");
+  const int64_t n = B * H * inner;
+  if (n == 0) return SQX_OK;
+  SQX_REQUIRE(x && scale && codes, SQX_E_ARG, "sqx_fp8_quantize_heads: null pointer");
+  SQX_FP8_DT(dtype, fp8_quantize_heads_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), as_stream(stream), x, n, H,
+             inner, scale, codes, saturated);
+  SQX_LAUNCH_CHECK("sqx_fp8_quantize_heads");
+  return SQX_OK;
+}
+
+extern "C" int sqx_fp8_dequantize_heads(const uint8_t* codes, const float* scale, int64_t B, int64_t H, int64_t inner,
+                                        float* out, sqx_stream_t stream) {
+  SQX_REQUIRE(B >= 0 && H > 0 && inner > 0, SQX_E_ARG, "sqx_fp8_dequantize_heads: bad shape");
+  const int64_t n = B * H * inner;
+  if (n == 0) return SQX_OK;
+  SQX_REQUIRE(codes && scale && out, SQX_E_ARG, "sqx_fp8_dequantize_heads: null pointer");
+  hipLaunchKernelGGL(fp8_dequantize_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, as_stream(stream),
+                     codes, scale, n, inner, H, out);
+  SQX_LAUNCH_CHECK("sqx_fp8_dequantize_heads");
+  return SQX_OK;
+}
+
+extern "C" int64_t sqx_fp8_tiled_weight_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return ceil_div(rows, 16) * ceil_div(cols, 64) * 1024;
+}
+
+extern "C" int sqx_fp8_tile(const uint8_t* codes, int64_t rows, int64_t cols, uint8_t* wt, sqx_stream_t stream) {
+  SQX_REQUIRE(rows > 0 && cols > 0, SQX_E_ARG, "sqx_fp8_tile: bad shape");
+  SQX_REQUIRE(codes && wt, SQX_E_ARG, "sqx_fp8_tile: null pointer");
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 4 == 0, SQX_E_ARG, "sqx_fp8_tile: wt must be 4-byte aligned");
+  const int64_t KB = ceil_div(cols, 64);
+  const int64_t nd = sqx_fp8_tiled_weight_bytes(rows, cols) / 4;
+  hipLaunchKernelGGL(fp8_tile_kernel, dim3(static_cast<unsigned>(ceil_div(nd, 256))), dim3(256), 0, as_stream(stream),
+                     codes, rows, cols, KB, nd, reinterpret_cast<uint32_t*>(wt));
+  SQX_LAUNCH_CHECK("sqx_fp8_tile");
+  return SQX_OK;
+}
+
+// Workspace of sqx_fp8_linear: the activations' E4M3 values as bf16 [m, cols] (rounded up to 256
+// bytes), then their per-token scales [m].
+static int64_t fp8_vals_bytes(int64_t m, int64_t cols) { return (m * cols * 2 + 255) / 256 * 256; }
+
+extern "C" int64_t sqx_fp8_linear_workspace_bytes(int64_t m, int64_t cols) {
+  if (m <= 0 || cols <= 0) return 0;
+  return fp8_vals_bytes(m, cols) + m * 4;
+}
+
+extern "C" int sqx_fp8_linear(const uint8_t* wt, const float* w_scale, const void* x, int act_dtype, void* y, int y_dtype,
+                              const void* bias, int64_t m, int64_t rows, int64_t cols, int k_slices, void* ws,
+                              int64_t ws_bytes, sqx_stream_t stream) {
+  const char* fn = "sqx_fp8_linear";
+  SQX_REQUIRE(fp8_float_dtype(act_dtype), SQX_E_ARG, "%s: unsupported activation dtype %d", fn, act_dtype);
+  SQX_REQUIRE(y_dtype == SQX_DTYPE_BF16 || y_dtype == SQX_DTYPE_F32, SQX_E_ARG, "%s: output must be BF16 or F32", fn);
+  SQX_REQUIRE(m >= 0 && rows > 0 && cols > 0 && cols % 8 == 0 && rows < (int64_t(1) << 31) && m < (int64_t(1) << 31),
+              SQX_E_ARG, "%s: bad shape m=%lld rows=%lld cols=%lld (cols %% 8 == 0)", fn, (long long)m, (long long)rows,
+              (long long)cols);
+  SQX_REQUIRE(ceil_div(cols, 64) * 1024 < (int64_t(1) << 31) && 64 * cols * 2 < (int64_t(1) << 31), SQX_E_ARG,
+              "%s: shape too large for 32-bit buffer offsets", fn);
+  SQX_REQUIRE(k_slices <= 16, SQX_E_ARG, "%s: k_slices %d > 16", fn, k_slices);
+  if (m == 0) return SQX_OK;
+  SQX_REQUIRE(wt && w_scale && x && y && ws, SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(ws_bytes >= sqx_fp8_linear_workspace_bytes(m, cols), SQX_E_SPACE, "%s: workspace of %lld bytes, %lld needed",
+              fn, (long long)ws_bytes, (long long)sqx_fp8_linear_workspace_bytes(m, cols));
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(ws) % 16 == 0, SQX_E_ARG,
+              "%s: wt and the workspace must be 16-byte aligned", fn);
+  SQX_REQUIRE(bias == nullptr || y_dtype == SQX_DTYPE_BF16, SQX_E_ARG, "%s: bias needs a BF16 output", fn);
+  hipStream_t s = as_stream(stream);
+  uint16_t* vals = static_cast<uint16_t*>(ws);
+  float* xs = reinterpret_cast<float*>(static_cast<char*>(ws) + fp8_vals_bytes(m, cols));
+  SQX_FP8_DT(act_dtype, fp8_quantize_rows_kernel, dim3(static_cast<unsigned>(m)), s, x, cols, cols,
+             static_cast<uint8_t*>(nullptr), xs, vals);
+  SQX_LAUNCH_CHECK(fn);
+  const WFp8::Args a{wt, w_scale, xs};
+  const uint16_t* b16 = static_cast<const uint16_t*>(bias);
+  const hipError_t e = y_dtype == SQX_DTYPE_F32
+                           ? gemv_launch<ActBF16, WFp8, 4, 2, true>(a, vals, y, b16, nullptr, m, rows, cols, k_slices, s)
+                           : gemv_launch<ActBF16, WFp8, 4, 2, false>(a, vals, y, b16, nullptr, m, rows, cols, k_slices, s);
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
+}

@@ -26,6 +26,8 @@
 //    loads (rows >= M read as zero) and KTAIL zeroes activation columns at or beyond K.
 #pragma once
 
+#include <type_traits>
+
 #include "sqx_common.h"
 
 namespace sqx {
@@ -50,6 +52,13 @@ inline int gemv_default_kslices(int64_t rows, int64_t cols, int kblk = 128) {
   if (s > cap) s = cap;
   return static_cast<int>(s);
 }
+
+// Weight policies with a per-row (token) factor of the output declare `kRowScale = true` and
+// `row_scale(args, m)`; `rows_from(args, m0)` moves that factor's pointer to the pass starting at row m0.
+template <class W, class = void>
+struct has_row_scale : std::false_type {};
+template <class W>
+struct has_row_scale<W, std::void_t<decltype(W::kRowScale)>> : std::integral_constant<bool, W::kRowScale> {};
 
 // What the LDS copy of the activations computes on the way in (XLDS only, bf16 activations):
 //   kProPlain    x as given (optionally divided by a per-column scale);
@@ -282,7 +291,10 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     const int m = c * 16 + 4 * (l >> 4) + (j & 3);
     const int n = t * 16 + (l & 15);
     if (m < M && n < N) {
-      v *= W::out_scale(wa, n);
+      if constexpr (has_row_scale<W>::value)
+        v = v * W::row_scale(wa, m) * W::out_scale(wa, n);
+      else
+        v *= W::out_scale(wa, n);
       if (bias) v += A::to_f32(bias[n]);
       if constexpr (YF32)
         static_cast<float*>(yv)[(int64_t)m * N + n] = v;
@@ -309,6 +321,8 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
   const dim3 grid(static_cast<unsigned>(T)), block(static_cast<unsigned>(64 * nw));
   for (int64_t m0 = 0; m0 < m; m0 += 64) {
     const int M = static_cast<int>(m - m0 < 64 ? m - m0 : 64);
+    typename W::Args wp = wa;
+    if constexpr (has_row_scale<W>::value) wp = W::rows_from(wa, m0);
     const int mch = gemv_mch(M);
     const uint16_t* xp = x + m0 * cols;
     void* yp = static_cast<char*>(y) + m0 * rows * (YF32 ? 4 : 2);
@@ -317,7 +331,7 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     const bool xlds = mch == 1 && gemv_xlds_bytes(M, KB, KBLK) <= kXldsMax;
     if (colscale != nullptr && !xlds) return hipErrorNotSupported;  // column scaling happens in the LDS copy
 #define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_)                                                                          \
-  hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO>), grid, block, LDS_, stream, wa, xp, yp, bias, \
+  hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO>), grid, block, LDS_, stream, wp, xp, yp, bias, \
                      colscale, M, N, K, iKB, kbw, pa)
     if constexpr (PRO != kProPlain) {
       if (!xlds || m > kProMaxRows || cols % 8 != 0) return hipErrorNotSupported;  // the caller checks first
