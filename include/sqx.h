@@ -436,6 +436,20 @@ int sqx_decode_attention_rope(const void* qkv, const int* lengths, const float* 
                               int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws, int64_t ws_bytes,
                               sqx_stream_t stream);
 
+/* The two attention calls above on an FP8 cache (the per-head E4M3 cache of fp8_kv_per_head.py:120-223
+ * as the slot cache): k/v hold E4M3 codes [B, Hkv, tmax, hd] (one byte each) with fp32 scales
+ * k_scale, v_scale [Hkv]; attention runs on code * scale. The _rope variant quantizes the new key and
+ * value with those scales (quantize_per_head: saturating_cast(fp32(x) / scale)) and uses and stores the
+ * codes. */
+int sqx_decode_attention_fp8kv(const void* q, const void* k_codes, const void* v_codes, const float* k_scale,
+                               const float* v_scale, const int* lengths, int64_t B, int64_t H, int64_t Hkv,
+                               int64_t hd, int64_t tmax, void* out, void* ws, int64_t ws_bytes,
+                               sqx_stream_t stream);
+int sqx_decode_attention_rope_fp8kv(const void* qkv, const int* lengths, const float* cos_t, const float* sin_t,
+                                    int64_t rope_rows, void* k_codes, void* v_codes, const float* k_scale,
+                                    const float* v_scale, int64_t B, int64_t H, int64_t Hkv, int64_t hd,
+                                    int64_t tmax, void* out, void* ws, int64_t ws_bytes, sqx_stream_t stream);
+
 /* SwiGLU's gate (model.py:227-237): out = bf16(silu(g) * u) from gate_up = bf16 [B, 2F] laid out
  * [g | u] (the w1 and w3 outputs side by side); out: bf16 [B, F]. */
 int sqx_silu_mul(const void* gate_up, int64_t B, int64_t F, void* out, sqx_stream_t stream);

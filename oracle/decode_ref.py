@@ -23,6 +23,8 @@ Pinning (tests/test_oracle_decode.py):
   rmsnorm ................... closed form on constant rows
   rows ...................... bit-identical active rows whatever inactive slots hold
                               (tests/test_batched_cache.py:186-213)
+  fp8 cache ................. written values are the dequantized codes of the FP8 oracle
+                              (oracle/fp8_ref.py, pinned to torch's float8_e4m3fn cast)
 """
 
 from __future__ import annotations
@@ -55,26 +57,42 @@ class RefModel:
 
 @dataclass
 class RefCache:
-    """BatchedKVCache (kv_cache.py:234-262): k/v per layer [B, Hkv, max_ctx, hd]; lengths, active."""
+    """BatchedKVCache (kv_cache.py:234-262): k/v per layer [B, Hkv, max_ctx, hd]; lengths, active.
+
+    With ``k_scale``/``v_scale`` (per layer, ``[Hkv]`` fp32) it is the per-head FP8 cache of
+    fp8_kv_per_head.py:93-101 in the slot layout: a written key or value is stored as
+    ``(saturating_cast(fp32(x) / scale) * scale).to(dtype)``, the dequantized code the attention reads."""
 
     k: list[Tensor]
     v: list[Tensor]
     lengths: Tensor
     active: Tensor
+    k_scale: list[Tensor] | None = None
+    v_scale: list[Tensor] | None = None
 
     @classmethod
-    def empty(cls, m: RefModel, batch: int, max_ctx: int, dtype: torch.dtype) -> "RefCache":
+    def empty(cls, m: RefModel, batch: int, max_ctx: int, dtype: torch.dtype, k_scale=None, v_scale=None) -> "RefCache":
         shape = (batch, m.n_kv_heads, max_ctx, m.head_dim)
         return cls([torch.zeros(shape, dtype=dtype) for _ in range(m.n_layers)],
                    [torch.zeros(shape, dtype=dtype) for _ in range(m.n_layers)],
-                   torch.zeros(batch, dtype=torch.long), torch.ones(batch, dtype=torch.bool))
+                   torch.zeros(batch, dtype=torch.long), torch.ones(batch, dtype=torch.bool), k_scale, v_scale)
+
+    @staticmethod
+    def _fp8(x: Tensor, scale: Tensor) -> Tensor:
+        s = scale.to(torch.float32).view(1, -1, 1)
+        codes = (x.to(torch.float32) / s).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+        return (codes.to(torch.float32) * s).to(x.dtype)
 
     def write_decode(self, layer: int, k_new: Tensor, v_new: Tensor) -> None:
         """kv_cache.py:194-205 + :259-261: row b lands at min(lengths[b], max_ctx - 1)."""
         pos = self.lengths.clamp(max=self.k[layer].shape[2] - 1)
         rows = torch.arange(self.lengths.shape[0])
-        self.k[layer][rows, :, pos] = k_new[:, :, 0]
-        self.v[layer][rows, :, pos] = v_new[:, :, 0]
+        k, v = k_new[:, :, 0], v_new[:, :, 0]
+        if self.k_scale is not None:
+            k = self._fp8(k, self.k_scale[layer])
+            v = self._fp8(v, self.v_scale[layer])
+        self.k[layer][rows, :, pos] = k
+        self.v[layer][rows, :, pos] = v
 
     def advance(self) -> None:
         """kv_cache.py:207-213."""

@@ -152,16 +152,66 @@ __device__ inline u32x4_t rope8(u32x4_t v, const float (&cs)[4], const float (&s
   return r;
 }
 
+typedef uint32_t u32x2v_t __attribute__((__vector_size__(8)));
+
+// One lane's 8 dims of a cache row: 16 bytes of bf16, or 8 bytes of E4M3 codes (KV8).
+template <bool KV8>
+struct KvRow;
+template <>
+struct KvRow<false> {
+  using T = u32x4_t;
+  static constexpr int kBytes = 2;  // per element
+  // element j (0..7) as fp32: rows stay packed in registers and are unpacked at each use
+  __device__ static float at(const T& r, int j) { return (j & 1) ? bf16_hi(r[j >> 1]) : bf16_lo(r[j >> 1]); }
+};
+template <>
+struct KvRow<true> {
+  using T = u32x2v_t;
+  static constexpr int kBytes = 1;
+  __device__ static void to_f32(const T& r, float (&f)[8]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(r[j]), false);
+      const f32x2_t b = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(r[j]), true);
+      f[4 * j] = a[0];
+      f[4 * j + 1] = a[1];
+      f[4 * j + 2] = b[0];
+      f[4 * j + 3] = b[1];
+    }
+  }
+  // E4M3 codes of 8 bf16 values divided by the head's scale (quantize_per_head, fp8_kv_per_head.py:93-96)
+  __device__ static T encode(const u32x4_t& v, float s) {
+    T r;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t c0 = e4m3_encode_sat(__fdiv_rn(bf16_lo(v[2 * j]), s));
+      const uint32_t c1 = e4m3_encode_sat(__fdiv_rn(bf16_hi(v[2 * j]), s));
+      const uint32_t c2 = e4m3_encode_sat(__fdiv_rn(bf16_lo(v[2 * j + 1]), s));
+      const uint32_t c3 = e4m3_encode_sat(__fdiv_rn(bf16_hi(v[2 * j + 1]), s));
+      r[j] = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+    }
+    return r;
+  }
+};
+
 // ROPE: q is the fused projection row [q | k | v] (width (H + 2 Hkv) * hd) and the kernel also does
 // sqx_rope_kv's work: q and the new key are rotated in registers, the new key/value stand in for
 // cache row min(lengths[b], tmax - 1) (which the workgroup holding that row writes to the cache).
 // Otherwise q is the rotated [B, H, hd] tensor and the cache already holds this step's key.
-template <int G, bool ROPE>
-__global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ kc,
-                                                           uint16_t* __restrict__ vc, const int* __restrict__ lengths,
+// KV8: the cache holds E4M3 codes with one scale per kv head (kscale/vscale [Hkv], the per-head FP8
+// cache of fp8_kv_per_head.py): attention runs on the dequantized values code * scale, with the K
+// scale folded into q and the V scale applied to the partial output; the new key/value are quantized
+// with the head's scales before they are used or stored.
+template <int G, bool ROPE, bool KV8>
+__global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __restrict__ q, uint8_t* __restrict__ kc,
+                                                           uint8_t* __restrict__ vc, const int* __restrict__ lengths,
                                                            const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                                           const float* __restrict__ kscale, const float* __restrict__ vscale,
                                                            int rope_rows, int H, int Hkv, int tmax, int chunk, int nchunk,
                                                            float qscale, float* __restrict__ part) {
+  using R = KvRow<KV8>;
+  using Row = typename R::T;
+  constexpr int ES = R::kBytes;
   const int ch = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
   const int len = max(lengths[b], 0);
   const int L = min(len + 1, tmax);
@@ -176,9 +226,11 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
   __shared__ float sm[4][G], sl[4][G];
   __shared__ float so[4][G][kHd];
 
+  const float ks = KV8 ? kscale[kh] : 1.0f;
+  const float vs = KV8 ? vscale[kh] : 1.0f;
   const uint16_t* qrow = q + static_cast<int64_t>(b) * (ROPE ? H + 2 * Hkv : H) * kHd + dl * 8;
   float cs[4], sn[4];
-  u32x4_t knew{}, vnew{};
+  Row knew{}, vnew{};
   if constexpr (ROPE) {
     const int64_t pr = static_cast<int64_t>(min(len, rope_rows - 1)) * (kHd / 2) + dl * 4;
 #pragma unroll
@@ -186,9 +238,17 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
       cs[j] = cos_t[pr + j];
       sn[j] = sin_t[pr + j];
     }
-    knew = rope8(*reinterpret_cast<const u32x4_t*>(qrow + (H + kh) * kHd), cs, sn);
-    vnew = *reinterpret_cast<const u32x4_t*>(qrow + (H + Hkv + kh) * kHd);
+    const u32x4_t kb16 = rope8(*reinterpret_cast<const u32x4_t*>(qrow + (H + kh) * kHd), cs, sn);
+    const u32x4_t vb16 = *reinterpret_cast<const u32x4_t*>(qrow + (H + Hkv + kh) * kHd);
+    if constexpr (KV8) {
+      knew = R::encode(kb16, ks);
+      vnew = R::encode(vb16, vs);
+    } else {
+      knew = kb16;
+      vnew = vb16;
+    }
   }
+  const float qs = qscale * ks;
   float qv[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -196,8 +256,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
     if constexpr (ROPE) v = rope8(v, cs, sn);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      qv[g][2 * j] = bf16_lo(v[j]) * qscale;
-      qv[g][2 * j + 1] = bf16_hi(v[j]) * qscale;
+      qv[g][2 * j] = bf16_lo(v[j]) * qs;
+      qv[g][2 * j + 1] = bf16_hi(v[j]) * qs;
     }
   }
   float m[G], l[G], o[G][8];
@@ -208,26 +268,26 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[g][j] = 0.0f;
   }
-  const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd;
-  const uint16_t* kb = kc + head_off + dl * 8;
-  const uint16_t* vb = vc + head_off + dl * 8;
+  const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd * ES;  // bytes
+  const uint8_t* kb = kc + head_off + dl * 8 * ES;
+  const uint8_t* vb = vc + head_off + dl * 8 * ES;
   if constexpr (ROPE) {
-    if (ch == slot / chunk && wave == 0 && kl == 0) {  // one 256-byte row each, from this workgroup only
-      *reinterpret_cast<u32x4_t*>(kc + head_off + static_cast<int64_t>(slot) * kHd + dl * 8) = knew;
-      *reinterpret_cast<u32x4_t*>(vc + head_off + static_cast<int64_t>(slot) * kHd + dl * 8) = vnew;
+    if (ch == slot / chunk && wave == 0 && kl == 0) {  // one cache row each, from this workgroup only
+      *reinterpret_cast<Row*>(kc + head_off + (static_cast<int64_t>(slot) * kHd + dl * 8) * ES) = knew;
+      *reinterpret_cast<Row*>(vc + head_off + (static_cast<int64_t>(slot) * kHd + dl * 8) * ES) = vnew;
     }
   }
 
   for (int base = ws; base < we; base += kKeysPerStep) {
-    u32x4_t kr[4], vr[4];
+    Row kr[4], vr[4];
     bool ok[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int t = base + 4 * u + kl;
       ok[u] = t < we;
       const int tc = ok[u] ? t : base;  // an in-range row; its score is masked below
-      kr[u] = *reinterpret_cast<const u32x4_t*>(kb + static_cast<int64_t>(tc) * kHd);
-      vr[u] = *reinterpret_cast<const u32x4_t*>(vb + static_cast<int64_t>(tc) * kHd);
+      kr[u] = *reinterpret_cast<const Row*>(kb + static_cast<int64_t>(tc) * kHd * ES);
+      vr[u] = *reinterpret_cast<const Row*>(vb + static_cast<int64_t>(tc) * kHd * ES);
     }
     if constexpr (ROPE) {
       if (slot >= base && slot < base + kKeysPerStep) {  // wave-uniform: this step holds the new key
@@ -240,6 +300,21 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
         }
       }
     }
+    // E4M3 rows are expanded to fp32 once per step (two codes per conversion); bf16 rows are read in place
+    float kf[KV8 ? 4 : 1][8], vf[KV8 ? 4 : 1][8];
+    if constexpr (KV8) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        R::to_f32(kr[u], kf[u]);
+        R::to_f32(vr[u], vf[u]);
+      }
+    }
+    auto kval = [&](int u, int j) -> float {
+      if constexpr (KV8) return kf[u][j]; else return R::at(kr[u], j);
+    };
+    auto vval = [&](int u, int j) -> float {
+      if constexpr (KV8) return vf[u][j]; else return R::at(vr[u], j);
+    };
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float s[4];
@@ -247,10 +322,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
       for (int u = 0; u < 4; ++u) {
         float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc = fmaf(qv[g][2 * j], bf16_lo(kr[u][j]), acc);
-          acc = fmaf(qv[g][2 * j + 1], bf16_hi(kr[u][j]), acc);
-        }
+        for (int j = 0; j < 8; ++j) acc = fmaf(qv[g][j], kval(u, j), acc);
         s[u] = ok[u] ? row16_sum(acc) : -INFINITY;
       }
       const float mn = fmaxf(fmaxf(m[g], fmaxf(s[0], s[1])), fmaxf(s[2], s[3]));
@@ -261,15 +333,11 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
       for (int u = 0; u < 4; ++u) p[u] = ok[u] ? exp2f(s[u] - mn) : 0.0f;
       l[g] = fmaf(l[g], a, (p[0] + p[1]) + (p[2] + p[3]));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float e0 = o[g][2 * j] * a, e1 = o[g][2 * j + 1] * a;
+      for (int j = 0; j < 8; ++j) {
+        float e = o[g][j] * a;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          e0 = fmaf(p[u], bf16_lo(vr[u][j]), e0);
-          e1 = fmaf(p[u], bf16_hi(vr[u][j]), e1);
-        }
-        o[g][2 * j] = e0;
-        o[g][2 * j + 1] = e1;
+        for (int u = 0; u < 4; ++u) e = fmaf(p[u], vval(u, j), e);
+        o[g][j] = e;
       }
       m[g] = mn;
     }
@@ -317,7 +385,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
       pp[0] = M;
       pp[1] = lsum;
     }
-    pp[2 + dd] = osum;
+    pp[2 + dd] = KV8 ? osum * vs : osum;
   }
 }
 
@@ -554,10 +622,12 @@ extern "C" int64_t sqx_attn_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, i
 }
 
 static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, const int* lengths, const float* cos_t,
-                                 const float* sin_t, int64_t rope_rows, int64_t B, int64_t H, int64_t Hkv, int64_t hd,
-                                 int64_t tmax, void* out, void* ws, int64_t ws_bytes, sqx_stream_t stream,
-                                 const char* fn) {
+                                 const float* sin_t, int64_t rope_rows, const float* kscale, const float* vscale,
+                                 int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws,
+                                 int64_t ws_bytes, sqx_stream_t stream, const char* fn) {
   const bool rope = cos_t != nullptr;
+  const bool kv8 = kscale != nullptr;
+  SQX_REQUIRE(!kv8 || vscale != nullptr, SQX_E_ARG, "%s: null V scale", fn);
   SQX_REQUIRE(hd == kHd, SQX_E_ARG, "%s: head_dim %lld is not supported (128)", fn, (long long)hd);
   SQX_REQUIRE(B >= 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && tmax > 0, SQX_E_ARG, "%s: bad shape", fn);
   SQX_REQUIRE(B < 65536 && Hkv < 65536 && tmax < (int64_t(1) << 30) && (H + 2 * Hkv) * hd < (int64_t(1) << 30),
@@ -580,25 +650,25 @@ static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, co
   const float qscale = 1.4426950408889634f / sqrtf(static_cast<float>(hd));  // log2(e) / sqrt(hd)
   const dim3 grid(static_cast<unsigned>(nchunk), static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
   const auto* qp = static_cast<const uint16_t*>(q);
-  auto* kp = static_cast<uint16_t*>(k_cache);
-  auto* vp = static_cast<uint16_t*>(v_cache);
+  auto* kp = static_cast<uint8_t*>(k_cache);
+  auto* vp = static_cast<uint8_t*>(v_cache);
   float* w = static_cast<float*>(ws);
   const int iH = static_cast<int>(H), iK = static_cast<int>(Hkv), iT = static_cast<int>(tmax);
   const int rr = static_cast<int>(rope_rows);
-#define SQX_ATTN(G_, R_)                                                                                          \
-  hipLaunchKernelGGL((attn_partial_kernel<G_, R_>), grid, dim3(256), 0, s, qp, kp, vp, lengths, cos_t, sin_t, rr, iH, iK, \
-                     iT, chunk, nchunk, qscale, w)
-#define SQX_ATTN_G(R_)            \
-  switch (G) {                    \
-    case 1: SQX_ATTN(1, R_); break; \
-    case 2: SQX_ATTN(2, R_); break; \
-    case 4: SQX_ATTN(4, R_); break; \
-    default: SQX_ATTN(8, R_); break; \
+#define SQX_ATTN(G_, R_, K8_)                                                                                       \
+  hipLaunchKernelGGL((attn_partial_kernel<G_, R_, K8_>), grid, dim3(256), 0, s, qp, kp, vp, lengths, cos_t, sin_t, kscale, \
+                     vscale, rr, iH, iK, iT, chunk, nchunk, qscale, w)
+#define SQX_ATTN_G(R_, K8_)                \
+  switch (G) {                             \
+    case 1: SQX_ATTN(1, R_, K8_); break;   \
+    case 2: SQX_ATTN(2, R_, K8_); break;   \
+    case 4: SQX_ATTN(4, R_, K8_); break;   \
+    default: SQX_ATTN(8, R_, K8_); break;  \
   }
   if (rope) {
-    SQX_ATTN_G(true)
+    if (kv8) { SQX_ATTN_G(true, true) } else { SQX_ATTN_G(true, false) }
   } else {
-    SQX_ATTN_G(false)
+    if (kv8) { SQX_ATTN_G(false, true) } else { SQX_ATTN_G(false, false) }
   }
 #undef SQX_ATTN_G
 #undef SQX_ATTN
@@ -612,8 +682,8 @@ static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, co
 extern "C" int sqx_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* lengths,
                                     int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax, void* out,
                                     void* ws, int64_t ws_bytes, sqx_stream_t stream) {
-  return decode_attention_impl(q, const_cast<void*>(k_cache), const_cast<void*>(v_cache), lengths, nullptr, nullptr, 0, B,
-                               H, Hkv, hd, tmax, out, ws, ws_bytes, stream, "sqx_decode_attention");
+  return decode_attention_impl(q, const_cast<void*>(k_cache), const_cast<void*>(v_cache), lengths, nullptr, nullptr, 0,
+                               nullptr, nullptr, B, H, Hkv, hd, tmax, out, ws, ws_bytes, stream, "sqx_decode_attention");
 }
 
 extern "C" int sqx_decode_attention_rope(const void* qkv, const int* lengths, const float* cos_t, const float* sin_t,
@@ -621,8 +691,29 @@ extern "C" int sqx_decode_attention_rope(const void* qkv, const int* lengths, co
                                          int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws, int64_t ws_bytes,
                                          sqx_stream_t stream) {
   SQX_REQUIRE(cos_t != nullptr, SQX_E_ARG, "sqx_decode_attention_rope: null cos table");
-  return decode_attention_impl(qkv, k_cache, v_cache, lengths, cos_t, sin_t, rope_rows, B, H, Hkv, hd, tmax, out, ws,
-                               ws_bytes, stream, "sqx_decode_attention_rope");
+  return decode_attention_impl(qkv, k_cache, v_cache, lengths, cos_t, sin_t, rope_rows, nullptr, nullptr, B, H, Hkv, hd,
+                               tmax, out, ws, ws_bytes, stream, "sqx_decode_attention_rope");
+}
+
+extern "C" int sqx_decode_attention_fp8kv(const void* q, const void* k_codes, const void* v_codes, const float* k_scale,
+                                          const float* v_scale, const int* lengths, int64_t B, int64_t H, int64_t Hkv,
+                                          int64_t hd, int64_t tmax, void* out, void* ws, int64_t ws_bytes,
+                                          sqx_stream_t stream) {
+  SQX_REQUIRE(k_scale != nullptr && v_scale != nullptr, SQX_E_ARG, "sqx_decode_attention_fp8kv: null scale");
+  return decode_attention_impl(q, const_cast<void*>(k_codes), const_cast<void*>(v_codes), lengths, nullptr, nullptr, 0,
+                               k_scale, v_scale, B, H, Hkv, hd, tmax, out, ws, ws_bytes, stream,
+                               "sqx_decode_attention_fp8kv");
+}
+
+extern "C" int sqx_decode_attention_rope_fp8kv(const void* qkv, const int* lengths, const float* cos_t,
+                                               const float* sin_t, int64_t rope_rows, void* k_codes, void* v_codes,
+                                               const float* k_scale, const float* v_scale, int64_t B, int64_t H,
+                                               int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws,
+                                               int64_t ws_bytes, sqx_stream_t stream) {
+  SQX_REQUIRE(cos_t != nullptr && k_scale != nullptr && v_scale != nullptr, SQX_E_ARG,
+              "sqx_decode_attention_rope_fp8kv: null table or scale");
+  return decode_attention_impl(qkv, k_codes, v_codes, lengths, cos_t, sin_t, rope_rows, k_scale, v_scale, B, H, Hkv, hd,
+                               tmax, out, ws, ws_bytes, stream, "sqx_decode_attention_rope_fp8kv");
 }
 
 extern "C" int sqx_silu_mul(const void* gate_up, int64_t B, int64_t F, void* out, sqx_stream_t stream) {

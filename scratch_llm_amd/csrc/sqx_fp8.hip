@@ -17,30 +17,6 @@
 
 namespace sqx {
 
-constexpr float kE4M3Max = 448.0f;
-// MIN_SCALE = 1 / (448 * 512) (fp8_weights.py:100), as the fp32 value torch compares against.
-constexpr float kFp8MinScale = static_cast<float>(1.0 / (448.0 * 512.0));
-
-// saturating_cast_e4m3 (fp8_weights.py:117-124): clamp to +-448, then round to nearest even. NaN
-// stays NaN (0x7f with the input's sign, as torch's cast encodes it).
-__device__ inline uint32_t e4m3_encode_sat(float v) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, v);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  if (v != v) return sign | 0x7fu;
-  const float a = fminf(fabsf(v), kE4M3Max);
-  uint32_t code;
-  if (a < 0.015625f) {  // below the smallest normal 2**-6: multiples of 2**-9 (code 8 is 2**-6 itself)
-    code = static_cast<uint32_t>(rintf(a * 512.0f));
-  } else {
-    const uint32_t b = __builtin_bit_cast(uint32_t, a);
-    const int e = static_cast<int>(b >> 23) - 127;  // -6 .. 8
-    const uint32_t mant = b & 0x7fffffu;
-    const uint32_t r = mant + 0x7ffffu + ((mant >> 20) & 1u);  // 23 -> 3 bits, ties to even
-    code = (static_cast<uint32_t>(e + 7) << 3) + (r >> 20);    // a mantissa carry bumps the exponent
-  }
-  return sign | code;
-}
-
 // NaN-propagating maximum (torch's amax): once a NaN is seen it stays.
 __device__ inline float nan_max(float acc, float a) { return (a > acc || a != a) ? a : acc; }
 

@@ -88,22 +88,32 @@ class _Layer:
 class DecodeState:
     """The slot cache and the step's buffers for one batch size (BatchedKVCache, kv_cache.py:234-262).
 
-    ``k``/``v``: bf16 ``[n_layers, B, Hkv, max_ctx, hd]``; ``lengths`` int32 ``[B]`` (valid positions
-    before the next write); ``active`` uint8 ``[B]`` (rows that ``advance`` bumps); ``tokens`` int32
-    ``[B]``: the step's input ids, overwritten by its greedy picks; ``logits`` bf16 ``[B, vocab]``.
+    ``k``/``v``: ``[n_layers, B, Hkv, max_ctx, hd]``, bf16, or with ``kv_dtype="fp8"`` E4M3 codes (uint8)
+    with fp32 per-(layer, kv head) scales ``k_scale``/``v_scale`` ``[n_layers, Hkv]`` (the per-head FP8
+    cache of fp8_kv_per_head.py; set them with :meth:`set_kv_scales` before decoding, static after).
+    ``lengths`` int32 ``[B]`` (valid positions before the next write); ``active`` uint8 ``[B]`` (rows that
+    ``advance`` bumps); ``tokens`` int32 ``[B]``: the step's input ids, overwritten by its greedy picks;
+    ``logits`` bf16 ``[B, vocab]``.
     """
 
-    def __init__(self, model: "Int4DecodeLM", batch: int, max_ctx: int) -> None:
+    def __init__(self, model: "Int4DecodeLM", batch: int, max_ctx: int, kv_dtype: str = "bf16") -> None:
         cfg, dev = model.cfg, model.device
         if batch < 1 or max_ctx < 1:
             raise ValueError("batch and max_ctx must be >= 1")
         if max_ctx > cfg.context_length:
             raise ValueError(f"max_ctx={max_ctx} exceeds context_length={cfg.context_length}")
-        self.batch, self.max_ctx = batch, max_ctx
+        if kv_dtype not in ("bf16", "fp8"):
+            raise ValueError(f"kv_dtype must be 'bf16' or 'fp8', got {kv_dtype!r}")
+        self.batch, self.max_ctx, self.kv_dtype = batch, max_ctx, kv_dtype
         hkv, hd, d = cfg.n_kv_heads, cfg.head_dim, cfg.d_model
         shape = (cfg.n_layers, batch, hkv, max_ctx, hd)
-        self.k = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
-        self.v = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+        kvt = torch.bfloat16 if kv_dtype == "bf16" else torch.uint8
+        self.k = torch.zeros(shape, dtype=kvt, device=dev)
+        self.v = torch.zeros(shape, dtype=kvt, device=dev)
+        self.k_scale = self.v_scale = None
+        if kv_dtype == "fp8":
+            self.k_scale = torch.ones(cfg.n_layers, hkv, dtype=torch.float32, device=dev)
+            self.v_scale = torch.ones(cfg.n_layers, hkv, dtype=torch.float32, device=dev)
         self.lengths = torch.zeros(batch, dtype=torch.int32, device=dev)
         self.active = torch.ones(batch, dtype=torch.uint8, device=dev)
         self.tokens = torch.zeros(batch, dtype=torch.int32, device=dev)
@@ -126,6 +136,33 @@ class DecodeState:
             for tw in model.linears():
                 gw = max(gw, int(lib.sqx_gemm_workspace_bytes(batch, tw.rows, tw.cols)))
         self.gemm_ws = torch.empty(max(gw // 4, 4), dtype=torch.float32, device=dev) if gw > 0 else None
+
+    def set_kv_scales(self, layer: int, k_scale: Tensor, v_scale: Tensor) -> None:
+        """Install a layer's per-head scales (``(Hkv,)`` or ``(1, Hkv, 1, 1)``, e.g. ``per_head_scale`` of a
+        calibration block; fp8_kv_per_head.py:160-173)."""
+        if self.kv_dtype != "fp8":
+            raise ValueError("per-head scales belong to an fp8 cache")
+        for dst, src in ((self.k_scale, k_scale), (self.v_scale, v_scale)):
+            if src.numel() != dst.shape[1]:
+                raise ValueError(f"scale must have {dst.shape[1]} elements (one per kv head), got {tuple(src.shape)}")
+            dst[layer].copy_(src.reshape(-1).to(torch.float32))
+
+    def write_kv(self, layer: int, k: Tensor, v: Tensor, start: int = 0) -> None:
+        """Store a block ``[B, Hkv, T, hd]`` of keys and values at positions ``start..start+T`` of every slot
+        (a prefill's output): copied for a bf16 cache, quantized with the layer's scales for an fp8 one."""
+        t = k.shape[2]
+        if k.shape != v.shape or k.shape[0] != self.batch or start < 0 or start + t > self.max_ctx:
+            raise ValueError(f"block {tuple(k.shape)} does not fit the cache at {start}")
+        if self.kv_dtype == "bf16":
+            self.k[layer, :, :, start:start + t].copy_(k)
+            self.v[layer, :, :, start:start + t].copy_(v)
+            return
+        from scratch_llm_amd.quant import fp8_kv_per_head as kv8
+
+        ks = self.k_scale[layer].view(1, -1, 1, 1)
+        vs = self.v_scale[layer].view(1, -1, 1, 1)
+        self.k[layer, :, :, start:start + t].copy_(kv8.quantize_per_head(k, ks).view(torch.uint8))
+        self.v[layer, :, :, start:start + t].copy_(kv8.quantize_per_head(v, vs).view(torch.uint8))
 
     def set_lengths(self, lengths) -> None:
         """Set every slot's valid length (a host list or tensor), e.g. after filling the cache."""
@@ -243,8 +280,8 @@ class Int4DecodeLM:
             ly.attn_norm.numel() * 2 + ly.ffn_norm.numel() * 2 for ly in self.layers
         ) + self.final_norm.numel() * 2
 
-    def new_state(self, batch: int, max_ctx: int | None = None) -> DecodeState:
-        return DecodeState(self, batch, self.cfg.context_length if max_ctx is None else max_ctx)
+    def new_state(self, batch: int, max_ctx: int | None = None, kv_dtype: str = "bf16") -> DecodeState:
+        return DecodeState(self, batch, self.cfg.context_length if max_ctx is None else max_ctx, kv_dtype)
 
     # ------------------------------------------------------------------ the step
     def _linear(self, st: DecodeState, tw: i4.Int4Tiled, x: Tensor, y: Tensor, stream: int) -> None:
@@ -299,10 +336,17 @@ class Int4DecodeLM:
             cur, delta = 0, None
             for li, ly in enumerate(self.layers):
                 cur = self._norm_linear(st, cur, delta, ly.attn_norm, ly.wqkv, st.qkv, s)
-                ck(lib.sqx_decode_attention_rope(
-                    st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
-                    cfg.context_length, st.k[li].data_ptr(), st.v[li].data_ptr(), B, H, Hkv, hd, T,
-                    st.attn.data_ptr(), st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention")
+                if st.kv_dtype == "fp8":
+                    ck(lib.sqx_decode_attention_rope_fp8kv(
+                        st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
+                        cfg.context_length, st.k[li].data_ptr(), st.v[li].data_ptr(), st.k_scale[li].data_ptr(),
+                        st.v_scale[li].data_ptr(), B, H, Hkv, hd, T, st.attn.data_ptr(), st.attn_ws.data_ptr(),
+                        st.attn_ws.numel() * 4, s), "attention")
+                else:
+                    ck(lib.sqx_decode_attention_rope(
+                        st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
+                        cfg.context_length, st.k[li].data_ptr(), st.v[li].data_ptr(), B, H, Hkv, hd, T,
+                        st.attn.data_ptr(), st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention")
                 self._linear(st, ly.wo, st.attn, st.delta, s)
                 delta = st.delta.data_ptr()
                 cur = self._norm_linear(st, cur, delta, ly.ffn_norm, ly.w13, st.gu, s)

@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -445,3 +446,149 @@ def test_step_rejects_bad_tokens(small):
         model.step(st, [0, model.cfg.vocab_size])
     with pytest.raises(ValueError):
         model.step(st, [0, 1, 2])
+
+
+# ---------------------------------------------------------------------------------------------
+# FP8 (per-head E4M3) KV cache
+# ---------------------------------------------------------------------------------------------
+def _valid_codes(shape, g):
+    """Random E4M3 codes without the NaN encodings."""
+    mag = torch.randint(0, 0x7F, shape, generator=g, dtype=torch.int32)
+    sign = torch.randint(0, 2, shape, generator=g, dtype=torch.int32) << 7
+    return (mag | sign).to(torch.uint8)
+
+
+@pytest.mark.parametrize("H,Hkv,T", [(32, 8, 2048), (8, 8, 300), (16, 2, 77)])
+def test_attention_fp8kv_brute_force(lib, H, Hkv, T):
+    from oracle import fp8_ref as F8
+
+    print_case("attention fp8 kv", H, Hkv, T)
+    hd, B = 128, 4
+    g = torch.Generator().manual_seed(H + T)
+    lengths = [T - 1, 0, T // 3, T + 4]
+    q = (torch.randn(B, H, hd, generator=g) * 2).bfloat16()
+    kc, vc = _valid_codes((B, Hkv, T, hd), g), _valid_codes((B, Hkv, T, hd), g)
+    ks = torch.rand(Hkv, generator=g) * 0.01 + 0.001
+    vs = torch.rand(Hkv, generator=g) * 0.01 + 0.001
+    out = torch.empty(B, H * hd, dtype=torch.bfloat16, device=DEV)
+    nb = lib.sqx_attn_workspace_bytes(B, H, Hkv, T)
+    ws = torch.empty(nb // 4, dtype=torch.float32, device=DEV)
+    ln = torch.tensor(lengths, dtype=torch.int32, device=DEV)
+    kd, vd, ksd, vsd = kc.to(DEV), vc.to(DEV), ks.to(DEV), vs.to(DEV)
+    _ok(lib, lib.sqx_decode_attention_fp8kv(q.to(DEV).data_ptr(), kd.data_ptr(), vd.data_ptr(), ksd.data_ptr(),
+                                            vsd.data_ptr(), ln.data_ptr(), B, H, Hkv, hd, T, out.data_ptr(),
+                                            ws.data_ptr(), nb, _s()))
+    torch.cuda.synchronize()
+    kdeq = torch.from_numpy(F8.e4m3_decode(kc.numpy())).double() * ks.double().view(1, Hkv, 1, 1)
+    vdeq = torch.from_numpy(F8.e4m3_decode(vc.numpy())).double() * vs.double().view(1, Hkv, 1, 1)
+    G = H // Hkv
+    got = out.cpu().view(B, H, hd).double()
+    for b in range(B):
+        L = min(max(lengths[b], 0) + 1, T)
+        kk = kdeq[b, :, :L].repeat_interleave(G, dim=0)
+        vv = vdeq[b, :, :L].repeat_interleave(G, dim=0)
+        p = torch.softmax(torch.einsum("hd,htd->ht", q[b].double(), kk) / math.sqrt(hd), dim=-1)
+        want = torch.einsum("ht,htd->hd", p, vv)
+        bound = 2.0**-8 * want.abs() + 1e-5 * vv.abs().max()
+        assert float(((got[b] - want).abs() / bound).max()) <= 1.0, f"row {b}"
+
+
+@pytest.mark.parametrize("B,T", [(5, 300), (64, 2048)])
+def test_fused_rope_fp8kv_equals_separate_steps(lib, B, T):
+    """sqx_decode_attention_rope_fp8kv == (RoPE, quantize the new row with the head scales, then
+    sqx_decode_attention_fp8kv), bit for bit: output and every cache byte."""
+    from oracle import fp8_ref as F8
+
+    print_case("fused rope fp8 kv", B, T)
+    H, Hkv, hd, ctx = 32, 8, 128, T + 16
+    g = torch.Generator().manual_seed(B + T)
+    lengths = torch.randint(0, T, (B,), generator=g)
+    lengths[0], lengths[1] = T - 1, 0
+    lengths[2] = T + 3
+    qkv = (torch.randn(B, (H + 2 * Hkv) * hd, generator=g) * 2).bfloat16()
+    kc, vc = _valid_codes((B, Hkv, T, hd), g), _valid_codes((B, Hkv, T, hd), g)
+    ks = torch.rand(Hkv, generator=g) * 0.02 + 0.002
+    vs = torch.rand(Hkv, generator=g) * 0.02 + 0.002
+    cos, sin = (t.to(DEV) for t in D.rope_tables(hd, ctx, 10000.0))
+    ln = lengths.to(torch.int32).to(DEV)
+    nb = lib.sqx_attn_workspace_bytes(B, H, Hkv, T)
+    ws = torch.empty(nb // 4, dtype=torch.float32, device=DEV)
+    ksd, vsd = ks.to(DEV), vs.to(DEV)
+    # fused
+    k1, v1 = kc.to(DEV), vc.to(DEV)
+    o1 = torch.empty(B, H * hd, dtype=torch.bfloat16, device=DEV)
+    _ok(lib, lib.sqx_decode_attention_rope_fp8kv(qkv.to(DEV).data_ptr(), ln.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                                 ctx, k1.data_ptr(), v1.data_ptr(), ksd.data_ptr(), vsd.data_ptr(), B, H,
+                                                 Hkv, hd, T, o1.data_ptr(), ws.data_ptr(), nb, _s()))
+    # separate: RoPE into bf16 scratch, quantize the new rows on the host oracle, attention on the codes
+    q = torch.empty(B, H, hd, dtype=torch.bfloat16, device=DEV)
+    kb = torch.zeros(B, Hkv, T, hd, dtype=torch.bfloat16, device=DEV)
+    vb = torch.zeros_like(kb)
+    _ok(lib, lib.sqx_rope_kv(qkv.to(DEV).data_ptr(), ln.data_ptr(), cos.data_ptr(), sin.data_ptr(), ctx, B, H, Hkv, hd,
+                             T, q.data_ptr(), kb.data_ptr(), vb.data_ptr(), _s()))
+    torch.cuda.synchronize()
+    k2, v2 = kc.clone(), vc.clone()
+    slot = lengths.clamp(max=T - 1)
+    for b in range(B):
+        for src, dst, sc in ((kb, k2, ks), (vb, v2, vs)):
+            row = src[b, :, int(slot[b])].float().cpu().numpy()  # [Hkv, hd]
+            dst[b, :, int(slot[b])] = torch.from_numpy(
+                F8.e4m3_encode_sat(row / sc.numpy()[:, None].astype(np.float32)))
+    k2d, v2d = k2.to(DEV), v2.to(DEV)
+    o2 = torch.empty_like(o1)
+    _ok(lib, lib.sqx_decode_attention_fp8kv(q.data_ptr(), k2d.data_ptr(), v2d.data_ptr(), ksd.data_ptr(), vsd.data_ptr(),
+                                            ln.data_ptr(), B, H, Hkv, hd, T, o2.data_ptr(), ws.data_ptr(), nb, _s()))
+    torch.cuda.synchronize()
+    assert torch.equal(k1.cpu(), k2) and torch.equal(v1.cpu(), v2)
+    assert torch.equal(o1, o2)
+
+
+def _fp8_scales(n_layers, hkv):
+    return [torch.full((hkv,), 0.02) for _ in range(n_layers)], [torch.full((hkv,), 0.015) for _ in range(n_layers)]
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_decode_step_fp8kv_matches_reference(small, B):
+    model, refs = small
+    print_case("decode step fp8 kv", B)
+    cfg = model.cfg
+    ks, vs = _fp8_scales(cfg.n_layers, cfg.n_kv_heads)
+    st = model.new_state(B, 48, kv_dtype="fp8")
+    for li in range(cfg.n_layers):
+        st.set_kv_scales(li, ks[li].to(DEV), vs[li].to(DEV))
+    caches = {dt: D.RefCache.empty(r, B, 48, dt, k_scale=ks, v_scale=vs) for dt, r in refs.items()}
+    tok = torch.randint(0, cfg.vocab_size, (B,), generator=torch.Generator().manual_seed(B))
+    for t in range(6):
+        nxt = model.step(st, tok)
+        torch.cuda.synchronize()
+        got = st.logits.float().cpu()
+        l16 = D.decode_step(refs[torch.bfloat16], caches[torch.bfloat16], tok, torch.bfloat16).float()
+        l32 = D.decode_step(refs[torch.float32], caches[torch.float32], tok, torch.float32)
+        scale = float(l32.abs().max())
+        e_hip, e_ref = float((got - l32).abs().max()), float((l16 - l32).abs().max())
+        assert e_hip <= 2 * e_ref + 2.0**-9 * scale, f"t={t}: {e_hip:.4g} vs {e_ref:.4g}"
+        top2 = l32.topk(2, dim=-1).values
+        sure = (top2[:, 0] - top2[:, 1]) > 4 * e_hip
+        assert torch.equal(nxt.cpu().long()[sure], l32.argmax(-1)[sure])
+        tok = nxt.cpu().long()
+    assert st.k.dtype == torch.uint8 and st.k.element_size() == 1
+
+
+def test_fp8kv_graph_replays_equal_eager(small):
+    model, _ = small
+    print_case("fp8 kv graph replay")
+    cfg = model.cfg
+    ks, vs = _fp8_scales(cfg.n_layers, cfg.n_kv_heads)
+    a, b = model.new_state(4, 32, kv_dtype="fp8"), model.new_state(4, 32, kv_dtype="fp8")
+    for s in (a, b):
+        for li in range(cfg.n_layers):
+            s.set_kv_scales(li, ks[li].to(DEV), vs[li].to(DEV))
+        s.set_tokens(torch.tensor([5, 17, 300, 999]), cfg.vocab_size)
+    graph = model.capture(b)
+    for t in range(4):
+        model.step(a)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(a.logits, b.logits), f"replay {t}"
+    assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)

@@ -155,3 +155,23 @@ def test_bf16_composition_stays_near_fp32():
         a = D.decode_step(m16, c16, torch.tensor(tok), torch.bfloat16).float()
         b = D.decode_step(m32, c32, torch.tensor(tok), torch.float32)
         assert float((a - b).abs().max() / b.abs().max()) < 5e-2
+
+
+def test_fp8_cache_write_is_the_fp8_oracles_round_trip():
+    """The FP8 slot cache stores exactly dequantize_per_head(quantize_per_head(x, s), s)."""
+    import numpy as np
+
+    from oracle import fp8_ref as F8
+
+    g = torch.Generator().manual_seed(12)
+    k = torch.randn(3, 2, 1, 16, generator=g) * 5
+    s = torch.tensor([0.01, 0.002])
+    m, _ = _model()
+    m.n_kv_heads, m.head_dim, m.n_layers = 2, 16, 1
+    cache = D.RefCache.empty(m, 3, 4, torch.float32, k_scale=[s], v_scale=[s])
+    cache.write_decode(0, k, k)
+    want = F8.dequantize_per_head(F8.quantize_per_head(k.numpy(), s.view(1, 2, 1, 1).numpy()),
+                                  s.view(1, 2, 1, 1).numpy())
+    assert np.array_equal(cache.k[0][:, :, 0].numpy(), want[:, :, 0])
+    ceiling = float(torch.tensor(448.0) * s[0])  # the fp32 product the dequantization forms
+    assert float(cache.k[0][:, 0, 0].abs().max()) == ceiling  # saturated values land on the head's ceiling
