@@ -32,6 +32,11 @@ replayed token after token. Per B: ms per step, tok/s (B / step time), HBM bytes
 + KV) and the time share of each linear kind (a graph of that kind's launches over all layers,
 timed alone, over the step time).
 
+fp8_w8a8 (not part of `value`): the FP8 E4M3 W8A8 linear (per-token activations, per-channel weights)
+at Llama-3-8B decode shapes, M = 1 and 16, HIP-event medians over >= 1 GB of rotating weights, next
+to hipBLASLt's rowwise torch._scaled_mm (the reference's fp8_linear on ROCm) on the same operands,
+with each one's error against the float64 oracle in units of the reference's derived bound.
+
 prefill (not part of `value`): the prefill GEMMs at their BASELINE configs, HIP-event medians of
 back-to-back launches on inputs already in HBM: config 4's MXFP4 x MXFP4 GEMM at M = 4096 (both
 shapes) against the 10.1 PF dense fp4 MFMA peak, config 4's MXFP4-weight x bf16 GEMM at M = 4096
@@ -95,6 +100,8 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM measurements")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode-step measurement")
     ap.add_argument("--decode-batches", default="1,8,32,64", help="batch sizes of the decode-step measurement")
+    ap.add_argument("--decode-fp8kv-batches", default="32,64", help="batch sizes also timed with the FP8 KV cache")
+    ap.add_argument("--no-fp8", action="store_true", help="skip the FP8 W8A8 linear measurement")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -321,11 +328,17 @@ def main() -> int:
         prefill = prefill_gemms(dev)
         log("prefill:", json.dumps(prefill))
 
+    fp8 = None
+    if not args.no_fp8:
+        fp8 = fp8_linears(dev)
+        log("fp8:", json.dumps(fp8))
+
     decode = None
     if not args.no_decode:
         del linears, cpu_sample
         torch.cuda.empty_cache()
-        decode = decode_steps(dev, [int(b) for b in args.decode_batches.split(",") if b])
+        decode = decode_steps(dev, [int(b) for b in args.decode_batches.split(",") if b],
+                              [int(b) for b in args.decode_fp8kv_batches.split(",") if b])
         log("decode:", json.dumps(decode))
 
     launches = len(share_launches)
@@ -377,6 +390,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu_baseline,
         "decode": decode,
+        "fp8_w8a8": fp8,
         "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
@@ -413,8 +427,9 @@ def _median_us(fn, reps: int = 10, warm: int = 3) -> float:
     return t[len(t) // 2]
 
 
-def decode_steps(dev, batches: list[int], steps: int = 20, warmup: int = 3) -> dict:
-    """BASELINE config 5 (module docstring): the captured decode step per batch size."""
+def decode_steps(dev, batches: list[int], fp8_batches: list[int], steps: int = 20, warmup: int = 3) -> dict:
+    """BASELINE config 5 (module docstring): the captured decode step per batch size; for the batch
+    sizes in ``fp8_batches`` also with the per-head FP8 KV cache (entries ``B=..,kv=fp8``)."""
     import torch
 
     from scratch_llm_amd import _lib
@@ -439,10 +454,18 @@ def decode_steps(dev, batches: list[int], steps: int = 20, warmup: int = 3) -> d
         return a.elapsed_time(b) / reps
 
     res = {}
-    for B in batches:
-        st = model.new_state(B, ctx)
-        st.k.normal_(generator=g)
-        st.v.normal_(generator=g)
+    runs = [(B, "bf16") for B in batches] + [(B, "fp8") for B in fp8_batches]
+    for B, kvd in runs:
+        st = model.new_state(B, ctx, kv_dtype=kvd)
+        if kvd == "bf16":
+            st.k.normal_(generator=g)
+            st.v.normal_(generator=g)
+        else:  # valid E4M3 codes (no NaN encodings) at a fixed per-head scale
+            for li in range(cfg.n_layers):
+                st.k[li].random_(0, 0x7F, generator=g)
+                st.v[li].random_(0, 0x7F, generator=g)
+            st.k_scale.fill_(0.01)
+            st.v_scale.fill_(0.01)
         st.set_lengths([ctx - 1] * B)
         st.set_tokens(torch.randint(0, cfg.vocab_size, (B,), generator=torch.Generator().manual_seed(B)), cfg.vocab_size)
         model.step(st)
@@ -454,6 +477,21 @@ def decode_steps(dev, batches: list[int], steps: int = 20, warmup: int = 3) -> d
         torch.cuda.synchronize()
         ms = timed(graph, steps)
         del graph
+        kv = 2 * cfg.n_layers * B * cfg.n_kv_heads * ctx * cfg.head_dim * (2 if kvd == "bf16" else 1)
+        byts = model.weight_bytes() + kv
+        key = f"B={B}" if kvd == "bf16" else f"B={B},kv=fp8"
+        res[key] = {
+            "ms_per_step": round(ms, 4),
+            "tok_s": round(B / (ms * 1e-3), 1),
+            "hbm_bytes_per_step": byts,
+            "gbs": round(byts / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        log(f"decode B={B} kv={kvd}: {ms:.3f} ms/step, {B / (ms * 1e-3):.1f} tok/s")
+        if kvd != "bf16":
+            del st
+            torch.cuda.empty_cache()
+            continue
         # time share of each linear kind: that kind's launches over all layers, captured and timed alone
         s_parts = {}
         silu = model.fuse_silu and lib.sqx_int4_prologue_fits(B, cfg.d_ff)
@@ -477,22 +515,96 @@ def decode_steps(dev, batches: list[int], steps: int = 20, warmup: int = 3) -> d
             torch.cuda.synchronize()
             s_parts[name] = timed(gk, 5)
             del gk
-        kv = 2 * cfg.n_layers * B * cfg.n_kv_heads * ctx * cfg.head_dim * 2
-        byts = model.weight_bytes() + kv
-        res[f"B={B}"] = {
-            "ms_per_step": round(ms, 4),
-            "tok_s": round(B / (ms * 1e-3), 1),
-            "hbm_bytes_per_step": byts,
-            "gbs": round(byts / (ms * 1e-3) / 1e9, 1),
-            "frac_of_hbm_peak": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "linear_share": {k: round(v / ms, 4) for k, v in s_parts.items()},
-            "linears_ms": round(sum(s_parts.values()), 4),
-        }
-        log(f"decode B={B}: {ms:.3f} ms/step, {B / (ms * 1e-3):.1f} tok/s")
+        res[key]["linear_share"] = {k: round(v / ms, 4) for k, v in s_parts.items()}
+        res[key]["linears_ms"] = round(sum(s_parts.values()), 4)
         del st
         torch.cuda.empty_cache()
     del model
     torch.cuda.empty_cache()
+    return res
+
+
+def _graph_us(launch_all, reps: int = 5) -> float:
+    """us per launch of a captured sequence of launches (launch_all(stream) issues them and returns the
+    count), replayed ``reps`` times between HIP events."""
+    import torch
+
+    cs = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cs):
+        n = launch_all(cs.cuda_stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / (reps * n)
+
+
+def fp8_linears(dev) -> dict:
+    """FP8 E4M3 W8A8 linears (fp8_weights.py semantics) at the Llama-3-8B decode shapes: the library's
+    sqx_fp8_linear (per-token activation quantize + exact-product GEMV, one weight pass), and
+    hipBLASLt's rowwise torch._scaled_mm (the reference's fp8_linear path on ROCm) on the same codes
+    and scales, each timed as a captured graph of back-to-back launches over >= 1 GB of weights, with
+    the max error of each against the float64 oracle in units of the reference's derived bound
+    (|ref| eps_bf16 / 2 + sqrt(K) eps_f32 sum|x w|)."""
+    import math
+
+    import torch
+
+    from scratch_llm_amd import _lib
+    from scratch_llm_amd.quant import fp8_weights as f8
+
+    lib = _lib.load()
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(1006)
+    for n, k in ((4096, 4096), (28672, 4096), (4096, 14336)):
+        copies = max(2, min(24, int(1.2e9 // (n * k))))
+        ws = []
+        for _ in range(copies):
+            w = (torch.randn(n, k, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            codes, scale = f8.quantize_per_channel(w)
+            ws.append((codes, scale, f8.tile_fp8(codes, scale)))
+            del w
+        for m in (1, 16):
+            x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            wsp = torch.empty(int(lib.sqx_fp8_linear_workspace_bytes(m, k)) // 4 + 4, dtype=torch.float32, device=dev)
+
+            def ours(stream):
+                for _, _, tw in ws:
+                    lib.sqx_fp8_linear(tw.wt.data_ptr(), tw.scale.data_ptr(), x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(),
+                                       _lib.DTYPE_BF16, None, m, n, k, 0, wsp.data_ptr(), wsp.numel() * 4, stream)
+                return copies
+
+            us = _graph_us(ours)
+            byts = n * k + 4 * n + 2 * m * k + 2 * m * n
+            entry = {"us": round(us, 2), "gbs": round(byts / us / 1e3, 1),
+                     "frac_of_hbm_peak": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
+            codes, scale, tw = ws[0]
+            xq, xs = f8.quantize_per_token(x)
+            ref = (xq.double() * xs.double()) @ (codes.double() * scale.double()).t()
+            mag = (xq.double() * xs.double()).abs() @ (codes.double() * scale.double()).abs().t()
+            bound = ref.abs() * 2.0**-8 + mag * math.sqrt(k) * 2.0**-23
+            entry["err_over_bound"] = round(float(((f8.fp8_linear_tiled(x, tw).double() - ref).abs() / bound).max()), 3)
+            try:
+                def theirs(stream):
+                    for c, s_, _ in ws:
+                        torch._scaled_mm(xq, c.t(), scale_a=xs, scale_b=s_.t(), out_dtype=torch.bfloat16)
+                    return copies
+
+                entry["hipblaslt_scaled_mm_us"] = round(_graph_us(theirs), 2)
+                out = torch._scaled_mm(xq, codes.t(), scale_a=xs, scale_b=scale.t(), out_dtype=torch.bfloat16)
+                out = (out[0] if isinstance(out, tuple) else out).double()
+                entry["hipblaslt_err_over_bound"] = round(float(((out - ref).abs() / bound).max()), 3)
+            except Exception as e:  # noqa: BLE001 - the comparison is informational
+                entry["hipblaslt_scaled_mm_us"] = f"unavailable: {type(e).__name__}: {str(e)[:80]}"
+            res[f"{k}->{n} M={m}"] = entry
+        del ws
+        torch.cuda.empty_cache()
     return res
 
 

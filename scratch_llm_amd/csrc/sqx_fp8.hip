@@ -17,6 +17,8 @@
 
 namespace sqx {
 
+typedef uint32_t u32x2v_t __attribute__((__vector_size__(8)));
+
 // NaN-propagating maximum (torch's amax): once a NaN is seen it stays.
 __device__ inline float nan_max(float acc, float a) { return (a > acc || a != a) ? a : acc; }
 
@@ -63,6 +65,64 @@ __global__ __launch_bounds__(256) void fp8_quantize_rows_kernel(const void* __re
     if (vals != nullptr) {
       const float d = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(code), false)[0];
       vals[r * cpitch + c] = static_cast<uint16_t>(__builtin_bit_cast(uint32_t, d) >> 16);  // exact
+    }
+  }
+}
+
+// The same quantizer for 16-bit rows with cols % 8 == 0: 1024 threads per row, 16-byte loads, the row
+// held in registers between the amax and the encode (thread t owns 8-column chunks t + 1024 i, i < NCH).
+template <int DT, int NCH>
+__global__ __launch_bounds__(1024) void fp8_quantize_rows16_kernel(const uint16_t* __restrict__ x, int64_t cols,
+                                                                   uint8_t* __restrict__ codes, float* __restrict__ scale,
+                                                                   uint16_t* __restrict__ vals) {
+  __shared__ float red[16];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t nch = cols / 8;
+  u32x4_t v[NCH];
+  float am = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int64_t c = tid + 1024 * i;
+    if (c < nch) {
+      v[i] = *reinterpret_cast<const u32x4_t*>(x + r * cols + 8 * c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = DT == SQX_DTYPE_BF16 ? bf16_lo(v[i][j]) : f16_bits_to_f32(static_cast<uint16_t>(v[i][j]));
+        const float hi = DT == SQX_DTYPE_BF16 ? bf16_hi(v[i][j]) : f16_bits_to_f32(static_cast<uint16_t>(v[i][j] >> 16));
+        am = nan_max(nan_max(am, fabsf(lo)), fabsf(hi));
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) am = nan_max(am, __shfl_xor(am, o, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = am;
+  __syncthreads();
+  float tot = red[0];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) tot = nan_max(tot, red[w]);
+  const float q = __fdiv_rn(tot, kE4M3Max);
+  const float s = q != q ? q : fmaxf(q, kFp8MinScale);
+  if (tid == 0) scale[r] = s;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int64_t c = tid + 1024 * i;
+    if (c < nch) {
+      uint32_t cw[2] = {0u, 0u};
+      u32x4_t vw;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = DT == SQX_DTYPE_BF16 ? bf16_lo(v[i][j]) : f16_bits_to_f32(static_cast<uint16_t>(v[i][j]));
+        const float hi = DT == SQX_DTYPE_BF16 ? bf16_hi(v[i][j]) : f16_bits_to_f32(static_cast<uint16_t>(v[i][j] >> 16));
+        const uint32_t c0 = e4m3_encode_sat(__fdiv_rn(lo, s));
+        const uint32_t c1 = e4m3_encode_sat(__fdiv_rn(hi, s));
+        cw[j >> 1] |= (c0 | (c1 << 8)) << (16 * (j & 1));
+        const uint32_t pair = c0 | (c1 << 8);
+        const f32x2_t d = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(pair), false);
+        vw[j] = ActBF16::pack_exact(d[0], d[1]);
+      }
+      if (codes != nullptr) *reinterpret_cast<u32x2v_t*>(codes + r * cols + 8 * c) = u32x2v_t{cw[0], cw[1]};
+      if (vals != nullptr) *reinterpret_cast<u32x4_t*>(vals + r * cols + 8 * c) = vw;
     }
   }
 }
@@ -197,14 +257,37 @@ static bool fp8_float_dtype(int d) { return d == SQX_DTYPE_F32 || d == SQX_DTYPE
     default: hipLaunchKernelGGL((KERNEL<SQX_DTYPE_F16>), GRID, dim3(256), 0, __VA_ARGS__); break;           \
   }
 
+// Per-row quantize into codes (optional) and bf16 values (optional): the 1024-thread register kernel
+// for 16-bit rows with cols % 8 == 0 and cols <= 32768, else the generic one.
+static void fp8_quantize_rows_launch(const void* x, int dtype, int64_t rows, int64_t cols, uint8_t* codes, float* scale,
+                                     uint16_t* vals, hipStream_t s) {
+  const bool vec = dtype != SQX_DTYPE_F32 && cols % 8 == 0 && cols <= 32768 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   (codes == nullptr || reinterpret_cast<uintptr_t>(codes) % 8 == 0) &&
+                   (vals == nullptr || reinterpret_cast<uintptr_t>(vals) % 16 == 0);
+  if (vec) {
+    const int nch = static_cast<int>(ceil_div(cols / 8, 1024));
+    const auto* xp = static_cast<const uint16_t*>(x);
+    const dim3 grid(static_cast<unsigned>(rows));
+#define SQX_Q16(DT_, N_) hipLaunchKernelGGL((fp8_quantize_rows16_kernel<DT_, N_>), grid, dim3(1024), 0, s, xp, cols, codes, scale, vals)
+#define SQX_Q16N(DT_)                   \
+  if (nch <= 1) SQX_Q16(DT_, 1);        \
+  else if (nch <= 2) SQX_Q16(DT_, 2);   \
+  else SQX_Q16(DT_, 4);
+    if (dtype == SQX_DTYPE_BF16) { SQX_Q16N(SQX_DTYPE_BF16) } else { SQX_Q16N(SQX_DTYPE_F16) }
+#undef SQX_Q16N
+#undef SQX_Q16
+    return;
+  }
+  SQX_FP8_DT(dtype, fp8_quantize_rows_kernel, dim3(static_cast<unsigned>(rows)), s, x, cols, cols, codes, scale, vals);
+}
+
 extern "C" int sqx_fp8_quantize_rows(const void* x, int dtype, int64_t rows, int64_t cols, uint8_t* codes, float* scale,
                                      sqx_stream_t stream) {
   SQX_REQUIRE(fp8_float_dtype(dtype), SQX_E_ARG, "sqx_fp8_quantize_rows: unsupported dtype %d", dtype);
   SQX_REQUIRE(rows >= 0 && cols >= 0 && rows < (int64_t(1) << 31), SQX_E_ARG, "sqx_fp8_quantize_rows: bad shape");
   if (rows == 0) return SQX_OK;
   SQX_REQUIRE(x && codes && scale, SQX_E_ARG, "sqx_fp8_quantize_rows: null pointer");
-  SQX_FP8_DT(dtype, fp8_quantize_rows_kernel, dim3(static_cast<unsigned>(rows)), as_stream(stream), x, cols, cols, codes,
-             scale, static_cast<uint16_t*>(nullptr));
+  fp8_quantize_rows_launch(x, dtype, rows, cols, codes, scale, nullptr, as_stream(stream));
   SQX_LAUNCH_CHECK("sqx_fp8_quantize_rows");
   return SQX_OK;
 }
@@ -305,8 +388,7 @@ extern "C" int sqx_fp8_linear(const uint8_t* wt, const float* w_scale, const voi
   hipStream_t s = as_stream(stream);
   uint16_t* vals = static_cast<uint16_t*>(ws);
   float* xs = reinterpret_cast<float*>(static_cast<char*>(ws) + fp8_vals_bytes(m, cols));
-  SQX_FP8_DT(act_dtype, fp8_quantize_rows_kernel, dim3(static_cast<unsigned>(m)), s, x, cols, cols,
-             static_cast<uint8_t*>(nullptr), xs, vals);
+  fp8_quantize_rows_launch(x, act_dtype, m, cols, nullptr, xs, vals, s);
   SQX_LAUNCH_CHECK(fn);
   const WFp8::Args a{wt, w_scale, xs};
   const uint16_t* b16 = static_cast<const uint16_t*>(bias);

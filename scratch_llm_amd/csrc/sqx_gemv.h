@@ -40,13 +40,12 @@ inline int64_t gemv_xlds_bytes(int64_t m, int64_t KB, int kblk = 128) { return m
 
 inline int gemv_mch(int64_t m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
 
-// Waves per tile the library picks: ~4096 waves on 256 CUs, 4..16 per tile, >= 2 blocks per wave.
+// Waves per tile the library picks (measured at M = 1 on the Llama-3-8B shapes): 16 for up to 256
+// tiles, 8 up to 2048 tiles, 4 beyond; at least 2 blocks per wave.
 inline int gemv_default_kslices(int64_t rows, int64_t cols, int kblk = 128) {
   const int64_t T = ceil_div(rows, 16);
   const int64_t KB = ceil_div(cols, kblk);
-  int64_t s = ceil_div(4096, T);
-  if (s < 4) s = 4;
-  if (s > 16) s = 16;
+  int64_t s = T <= 256 ? 16 : (T <= 2048 ? 8 : 4);
   int64_t cap = KB / 2;
   if (cap < 1) cap = 1;
   if (s > cap) s = cap;
