@@ -96,8 +96,8 @@ int sqx_int4_tile(const int8_t* codes, int code_kind, const void* scales, const 
 int sqx_int4_tile_packed(const uint8_t* packed, const void* scales, int param_dtype, int64_t rows,
                          int64_t cols, int64_t group, uint8_t* wt, void* st, sqx_stream_t stream);
 
-/* Number of k-slices (waves per 16-row tile) the library picks for a shape when the caller passes
- * k_slices <= 0. */
+/* Number of k-slices (waves per 16-row tile) the decode GEMV takes when sqx_int4_linear runs it
+ * with k_slices <= 0; passing this value explicitly always selects the GEMV. */
 int sqx_int4_linear_default_kslices(int64_t m, int64_t rows, int64_t cols);
 
 /* W4A16 linear (w4a16_linear, int4_group.py:148-164; awq_linear, awq.py:184-192 once the AWQ
@@ -105,12 +105,33 @@ int sqx_int4_linear_default_kslices(int64_t m, int64_t rows, int64_t cols);
  * w[r, c] = (u - z) * s for the tiled codes u, zero z (8 for symmetric codes) and scale s of the
  * group. x: [m, cols] of act_dtype (BF16 or F16); y: [m, rows] of act_dtype; bias: [rows] of
  * act_dtype or NULL. wt/st/zt from sqx_int4_tile (zt NULL for symmetric codes). fp32 accumulation.
- * Any m >= 1 (processed 64 rows of x per pass). One workgroup per 16-row tile; k_slices (1..16, or
- * <= 0 for the default) waves split its columns and sum their partials in a fixed order, so results
- * are deterministic for a given k_slices. Needs no workspace. */
+ * Any m >= 1. k_slices 1..16 runs the decode GEMV (one workgroup per 16-row tile, k_slices waves
+ * splitting its columns, 64 rows of x per pass). k_slices <= 0 lets the library pick by shape: for
+ * 2..64 rows the decode-regime kernels of sqx_int4_skinny (without K splits) where they are faster,
+ * otherwise the GEMV with sqx_int4_linear_default_kslices. Sums run in a fixed order, so a call is
+ * deterministic for a given shape and k_slices. Needs no workspace. */
 int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt, int param_dtype,
                     const void* x, int act_dtype, void* y, const void* bias, int64_t m, int64_t rows,
                     int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
+
+/* The same W4A16 linear for 1 <= m <= 64 activation rows (the decode regime of batched serving) with
+ * an explicit launch shape. Each wave owns `tiles` (1, 2 or 4) 16-row weight tiles and applies each
+ * k-block's activation fragments to all of them; the codes' offset is removed through per-group
+ * activation sums. waves = 0: the LDS-staged variant (four waves with their own tiles share the
+ * activations through LDS; one more wave copies them); waves = 1..8: that many waves split each
+ * workgroup's k-blocks (tiles 2 or 4). splits >= 1 workgroups split K further and write fp32 partials
+ * to ws, added in split order by a second kernel. tiles or splits <= 0, or waves < 0, pick the
+ * library default (splits > 1 only when ws is given); with all three left to the library, shapes
+ * where the decode GEMV is faster run it (sqx_int4_linear's GEMV form). The library may lower
+ * `tiles` where the registers would not hold it. Deterministic for a given shape. ws: 16-byte aligned,
+ * sqx_int4_skinny_workspace_bytes(m, rows, cols, splits) bytes (0 when splits resolves to 1; splits
+ * <= 0 asks for the default's). Other arguments and results as sqx_int4_linear. No counterpart in the
+ * reference (a launch shape of w4a16_linear, int4_group.py:148-164). */
+int64_t sqx_int4_skinny_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int splits);
+int sqx_int4_skinny(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
+                    int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
+                    int64_t group, int tiles, int waves, int splits, void* ws, int64_t ws_bytes,
+                    sqx_stream_t stream);
 
 /* 1 when sqx_int4_linear_rmsnorm / sqx_int4_linear_silu take m activation rows of cols columns
  * (m <= 8, cols % 8 == 0, the rows fit the kernel's 64 KiB LDS copy), else 0. */
@@ -120,14 +141,15 @@ int sqx_int4_prologue_fits(int64_t m, int64_t cols);
  * model.py:394-403, then RMSNorm, model.py:158-162, then w4a16_linear): h = bf16(x + delta) (written
  * to h_out; delta NULL means h = x and h_out unused), x' = bf16(h * (1 / sqrt(mean(h^2) + eps)) * gain),
  * y = x' @ W^T. Symmetric codes with fp32 scales (sqx_int4_tile code_kind 0), bf16 x/delta/gain/h_out/y
- * ([m, cols], [cols] for gain). Bit-identical to sqx_rmsnorm followed by sqx_int4_linear. */
+ * ([m, cols], [cols] for gain). Runs the decode GEMV: bit-identical to sqx_rmsnorm followed by
+ * sqx_int4_linear with the same k_slices (k_slices <= 0: sqx_int4_linear_default_kslices). */
 int sqx_int4_linear_rmsnorm(const uint8_t* wt, const float* st, const void* x, const void* delta,
                             const void* gain, float eps, void* h_out, void* y, int64_t m, int64_t rows,
                             int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
 
 /* SwiGLU's down projection with its gate in front (model.py:227-237): y = bf16(silu(g) * u) @ W^T with
- * gate_up = bf16 [m, 2 cols] laid out [g | u]. Bit-identical to sqx_silu_mul followed by
- * sqx_int4_linear. Same weight format as sqx_int4_linear_rmsnorm. */
+ * gate_up = bf16 [m, 2 cols] laid out [g | u]. Bit-identical to sqx_silu_mul followed by the GEMV
+ * form of sqx_int4_linear, as for sqx_int4_linear_rmsnorm, whose weight format it takes. */
 int sqx_int4_linear_silu(const uint8_t* wt, const float* st, const void* gate_up, void* y, int64_t m,
                          int64_t rows, int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
 

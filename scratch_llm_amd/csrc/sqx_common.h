@@ -43,6 +43,7 @@ typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
 typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
 typedef unsigned u32x4_t __attribute__((__vector_size__(4 * sizeof(unsigned))));
+typedef uint32_t u32x2v_t __attribute__((__vector_size__(8)));
 typedef float f32x2_t __attribute__((__vector_size__(2 * sizeof(float))));
 typedef __bf16 bf16x2_t __attribute__((__vector_size__(2 * sizeof(__bf16))));
 typedef _Float16 f16x2_t __attribute__((__vector_size__(2 * sizeof(_Float16))));
@@ -218,6 +219,21 @@ __device__ inline float e4m3_value(uint32_t b) {
   const uint32_t m = b & 7u;
   return e ? ldexpf(static_cast<float>(8u + m), static_cast<int>(e) - 10) : ldexpf(static_cast<float>(m), -9);
 }
+
+// LDS pointers for the buffer loads that write LDS directly.
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt[3:0] in bits
+// 3:0 and vmcnt[5:4] in bits 15:14; expcnt and lgkmcnt at their maxima).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier that also orders LDS accesses for the compiler (the memory clobber), without
+// waiting for outstanding global loads: loads into registers stay in flight across it.
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

@@ -152,8 +152,6 @@ __device__ inline u32x4_t rope8(u32x4_t v, const float (&cs)[4], const float (&s
   return r;
 }
 
-typedef uint32_t u32x2v_t __attribute__((__vector_size__(8)));
-
 // One lane's 8 dims of a cache row: 16 bytes of bf16, or 8 bytes of E4M3 codes (KV8).
 template <bool KV8>
 struct KvRow;

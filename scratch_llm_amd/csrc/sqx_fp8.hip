@@ -17,8 +17,6 @@
 
 namespace sqx {
 
-typedef uint32_t u32x2v_t __attribute__((__vector_size__(8)));
-
 // NaN-propagating maximum (torch's amax): once a NaN is seen it stays.
 __device__ inline float nan_max(float acc, float a) { return (a > acc || a != a) ? a : acc; }
 

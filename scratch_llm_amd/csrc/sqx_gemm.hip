@@ -27,7 +27,6 @@ namespace sqx {
 
 typedef int i32x8_t __attribute__((__vector_size__(8 * sizeof(int))));
 typedef float f32x16_t __attribute__((__vector_size__(16 * sizeof(float))));
-typedef __attribute__((address_space(3))) void lds_void;
 typedef unsigned u32x2_t __attribute__((__vector_size__(2 * sizeof(unsigned))));
 
 namespace mxg {
@@ -86,13 +85,6 @@ __device__ inline void mx_issue_step(uint8_t* stage, int wave, int lane, int kb,
   }
 }
 
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt[3:0] in bits
-// 3:0 and vmcnt[5:4] in bits 15:14; expcnt and lgkmcnt at their maxima).
-template <int N>
-__device__ inline void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // WN: waves along n (2: four waves of 128 x 128; 4: eight waves of 128 x 64, two per SIMD).
 template <int NSTAGE, int YKIND, int WN>  // YKIND: 0 = bf16, 1 = fp16, 2 = fp32

@@ -18,6 +18,7 @@
 // exactly, so B needs three VALU ops per column pair; a second set of MFMAs with the constant
 // B = -(MAGIC + zero) removes the offset, and the group scale is applied to the fp32 partial.
 #include "sqx_gemv.h"
+#include "sqx_skinny.h"
 
 #include <float.h>
 
@@ -334,12 +335,14 @@ struct WInt4 {
     float sc[NG];
     float zf[NG];
   };
-  __device__ static Ctx ctx(const Args& a, int t, int KB, int lane) {
+  __device__ static Ctx ctx(const Args& a, int t, int KB, int lane) { return ctx_tiles(a, t, 1, KB, lane); }
+  // tiles t .. t+nt-1: tile r's block kb is block r*KB + kb of the range
+  __device__ static Ctx ctx_tiles(const Args& a, int t, int nt, int KB, int lane) {
     Ctx c;
-    c.wr = make_rsrc(a.wt + (int64_t)t * KB * 1024, (uint32_t)KB * 1024u);
+    c.wr = make_rsrc(a.wt + (int64_t)t * KB * 1024, (uint32_t)nt * (uint32_t)KB * 1024u);
     const uint32_t pbytes = (uint32_t)KB * NG * 16u * PB;
-    c.sr = make_rsrc(static_cast<const char*>(a.st) + (int64_t)t * pbytes, pbytes);
-    c.zr = ASYM ? make_rsrc(static_cast<const char*>(a.zt) + (int64_t)t * pbytes, pbytes) : c.sr;
+    c.sr = make_rsrc(static_cast<const char*>(a.st) + (int64_t)t * pbytes, (uint32_t)nt * pbytes);
+    c.zr = ASYM ? make_rsrc(static_cast<const char*>(a.zt) + (int64_t)t * pbytes, (uint32_t)nt * pbytes) : c.sr;
     c.wvo = (uint32_t)lane * 16u;
     c.pvo = (uint32_t)(lane & 15) * PB;
     return c;
@@ -382,6 +385,23 @@ struct WInt4 {
     }
   }
   __device__ static float out_scale(const Args&, int) { return 1.0f; }
+
+  // The skinny linear's hooks: B fragment of step i as (magic + code) pairs, the value each
+  // activation must be charged back per group (magic + zero point), and the group scale.
+  template <class A>
+  __device__ static u32x4_t bfrag(const u32x4_t& w, int i) {
+    const uint32_t d = w[i];
+    const uint32_t kMask = 0x000F000Fu;
+    const uint32_t magic = A::kMagicPair;
+    return u32x4_t{and_or(d, kMask, magic), and_or(d >> 4, kMask, magic), and_or(d >> 8, kMask, magic),
+                   and_or(d >> 12, kMask, magic)};
+  }
+  static constexpr bool kConstOffset = !ASYM;
+  template <class A>
+  __device__ static float const_offset() { return A::kMagic + 8.0f; }
+  template <class A>
+  __device__ static float offset(const P& p, int g) { return A::kMagic + p.zf[g]; }
+  __device__ static float scale(const P& p, int g) { return p.sc[g]; }
 };
 
 template <class A, int GROUP, bool ASYM, bool PBF16>
@@ -409,6 +429,22 @@ static hipError_t launch_int4_pro(int group, const uint8_t* wt, const float* st,
   if (group == 64) SQX_PRO(64)
   SQX_PRO(32)
 #undef SQX_PRO
+}
+
+template <class A, bool ASYM, bool PBF16>
+static hipError_t launch_int4_skinny(int group, const uint8_t* wt, const void* st, const void* zt, const uint16_t* x,
+                                     uint16_t* y, const uint16_t* bias, int64_t m, int64_t rows, int64_t cols,
+                                     SkinnyShape sh, float* ws, int64_t ws_bytes, hipStream_t s) {
+#define SQX_SKG(G_)                                                                                  \
+  {                                                                                                  \
+    using W = WInt4<G_, ASYM, PBF16>;                                                                \
+    const typename W::Args a{wt, st, zt};                                                            \
+    return skinny_launch<A, W>(a, x, y, bias, m, rows, cols, sh, ws, ws_bytes, s);                   \
+  }
+  if (group == 128) SQX_SKG(128)
+  if (group == 64) SQX_SKG(64)
+  SQX_SKG(32)
+#undef SQX_SKG
 }
 
 template <class A, bool ASYM, bool PBF16>
@@ -677,6 +713,11 @@ extern "C" int sqx_int4_linear_default_kslices(int64_t m, int64_t rows, int64_t 
   return gemv_default_kslices(rows, cols);
 }
 
+static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
+                            int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
+                            int64_t group, SkinnyShape sh, void* ws, int64_t ws_bytes, sqx_stream_t stream,
+                            const char* fn);
+
 static int int4_linear_impl(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
                             int act_dtype, void* y, const void* bias, const float* colscale, int64_t m,
                             int64_t rows, int64_t cols, int64_t group, int k_slices, sqx_stream_t stream,
@@ -703,6 +744,12 @@ static int int4_linear_impl(const uint8_t* wt, const void* st, const void* zt, i
     SQX_REQUIRE(m <= 16 && gemv_xlds_bytes(m, ceil_div(cols, 128)) <= kXldsMax, SQX_E_ARG,
                 "%s: per-column activation scaling needs m <= 16 and m*cols*2 <= %lld bytes", fn,
                 (long long)kXldsMax);
+  }
+  if (k_slices <= 0 && colscale == nullptr && m >= 2 && m <= 64) {  // the decode-regime kernels (no K split)
+    const SkinnyShape sh = skinny_default_shape(m, rows, cols, 128, false);
+    if (!sh.gemv)
+      return int4_skinny_impl(wt, st, zt, param_dtype, x, act_dtype, y, bias, m, rows, cols, group, sh, nullptr, 0,
+                              stream, fn);
   }
   const bool asym = zt != nullptr;
   const bool pbf = param_dtype == SQX_DTYPE_BF16;
@@ -740,6 +787,85 @@ extern "C" int sqx_int4_linear_colscaled(const uint8_t* wt, const void* st, cons
   SQX_REQUIRE(col_scale != nullptr, SQX_E_ARG, "sqx_int4_linear_colscaled: null col_scale");
   return int4_linear_impl(wt, st, zt, param_dtype, x, act_dtype, y, bias, col_scale, m, rows, cols, group, k_slices,
                           stream, "sqx_int4_linear_colscaled");
+}
+
+// The 1..64-row linear with an explicit launch shape: tiles (1, 2 or 4) row tiles per wave; waves 0
+// for the LDS-staged variant, 1..8 for waves splitting K; splits >= 1 workgroups along K. tiles or
+// splits <= 0, or waves < 0, pick the library default.
+static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
+                            int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
+                            int64_t group, SkinnyShape sh, void* ws, int64_t ws_bytes, sqx_stream_t stream,
+                            const char* fn) {
+  SQX_REQUIRE(m >= 0 && m <= 64 && rows > 0 && cols > 0, SQX_E_ARG,
+              "%s: bad shape m=%lld rows=%lld cols=%lld (m <= 64)", fn, (long long)m, (long long)rows,
+              (long long)cols);
+  SQX_REQUIRE(group == 32 || group == 64 || group == 128, SQX_E_ARG, "%s: group_size %lld unsupported (32, 64 or 128)",
+              fn, (long long)group);
+  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld", (long long)cols,
+              (long long)group);
+  SQX_REQUIRE(act_dtype == SQX_DTYPE_BF16 || act_dtype == SQX_DTYPE_F16, SQX_E_ARG,
+              "%s: activations must be BF16 or F16", fn);
+  SQX_REQUIRE(param_dtype == SQX_DTYPE_F32 || param_dtype == SQX_DTYPE_BF16, SQX_E_ARG,
+              "%s: param_dtype must be F32 or BF16", fn);
+  SQX_REQUIRE(rows < ((int64_t)1 << 31) && ceil_div(rows, 16) * ceil_div(cols, 128) * 1024 < ((int64_t)1 << 31) &&
+                  64 * cols * 2 < ((int64_t)1 << 31),
+              SQX_E_ARG, "%s: shape too large for 32-bit buffer offsets", fn);
+  SQX_REQUIRE(sh.waves >= 0 && sh.waves <= kSkinnyMaxWaves && sh.S >= 1 &&
+                  (sh.R == 2 || sh.R == 4 || (sh.R == 1 && sh.waves == 0)),
+              SQX_E_ARG, "%s: bad launch shape (tiles %d, waves %d, splits %d)", fn, sh.R, sh.waves, sh.S);
+  if (m == 0) return SQX_OK;
+  SQX_REQUIRE(wt && st && x && y, SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, SQX_E_ARG,
+              "%s: wt and x must be 16-byte aligned", fn);
+  {
+    const int S = skinny_splits(ceil_div(cols, 128), sh.S);
+    SQX_REQUIRE(S == 1 || (ws != nullptr && ws_bytes >= skinny_workspace_bytes(m, rows, (int)S) &&
+                           reinterpret_cast<uintptr_t>(ws) % 16 == 0),
+                SQX_E_ARG, "%s: %lld splits need a 16-byte aligned workspace of %lld bytes", fn, (long long)S,
+                (long long)skinny_workspace_bytes(m, rows, (int)S));
+  }
+  const bool asym = zt != nullptr;
+  const bool pbf = param_dtype == SQX_DTYPE_BF16;
+  hipStream_t s = as_stream(stream);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  uint16_t* yp = static_cast<uint16_t*>(y);
+  const uint16_t* b16 = static_cast<const uint16_t*>(bias);
+  float* wsp = static_cast<float*>(ws);
+  const int g = static_cast<int>(group);
+  hipError_t e;
+#define SQX_SKL(ACT, ASYM, PBF) \
+  e = launch_int4_skinny<ACT, ASYM, PBF>(g, wt, st, zt, xp, yp, b16, m, rows, cols, sh, wsp, ws_bytes, s)
+  if (act_dtype == SQX_DTYPE_BF16) {
+    if (asym) { if (pbf) SQX_SKL(ActBF16, true, true); else SQX_SKL(ActBF16, true, false); }
+    else { if (pbf) SQX_SKL(ActBF16, false, true); else SQX_SKL(ActBF16, false, false); }
+  } else {
+    if (asym) { if (pbf) SQX_SKL(ActF16, true, true); else SQX_SKL(ActF16, true, false); }
+    else { if (pbf) SQX_SKL(ActF16, false, true); else SQX_SKL(ActF16, false, false); }
+  }
+#undef SQX_SKL
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
+}
+
+extern "C" int64_t sqx_int4_skinny_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int splits) {
+  if (m <= 0 || m > 64 || rows <= 0 || cols <= 0) return 0;
+  const int S = splits > 0 ? splits : skinny_default_shape(m, rows, cols, 128, true).S;
+  return skinny_workspace_bytes(m, rows, skinny_splits(ceil_div(cols, 128), S));
+}
+
+extern "C" int sqx_int4_skinny(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
+                               int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
+                               int64_t group, int tiles, int waves, int splits, void* ws, int64_t ws_bytes,
+                               sqx_stream_t stream) {
+  SkinnyShape sh = skinny_default_shape(m, rows, cols, 128, ws != nullptr);
+  if (tiles <= 0 && waves < 0 && splits <= 0 && sh.gemv)  // the library's choice for this shape: the GEMV
+    return int4_linear_impl(wt, st, zt, param_dtype, x, act_dtype, y, bias, nullptr, m, rows, cols, group,
+                            sqx_int4_linear_default_kslices(m, rows, cols), stream, "sqx_int4_skinny");
+  if (tiles > 0) sh.R = tiles;
+  if (waves >= 0) sh.waves = waves;
+  if (splits > 0) sh.S = splits;
+  return int4_skinny_impl(wt, st, zt, param_dtype, x, act_dtype, y, bias, m, rows, cols, group, sh, ws, ws_bytes,
+                          stream, "sqx_int4_skinny");
 }
 
 extern "C" int sqx_int4_prologue_fits(int64_t m, int64_t cols) {

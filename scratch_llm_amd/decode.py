@@ -29,6 +29,10 @@ from scratch_llm_amd.quant import int4_group as i4
 
 __all__ = ["DecodeConfig", "DecodeState", "Int4DecodeLM", "LLAMA3_8B", "rope_tables"]
 
+# Batches of 2..64 rows run the linears through sqx_int4_skinny's shape choice (the GEMV or a
+# decode-regime kernel, K split into the state's workspace); larger batches run the prefill GEMM.
+_SKINNY_MAX_M = 64
+
 
 @dataclass(frozen=True)
 class DecodeConfig:
@@ -132,8 +136,10 @@ class DecodeState:
         nb = int(lib.sqx_argmax_workspace_bytes(batch, cfg.vocab_size))
         self.argmax_ws = torch.empty(max(nb // 4, 4), dtype=torch.float32, device=dev)
         gw = 0
-        if batch >= i4.GEMM_MIN_M:
-            for tw in model.linears():
+        for tw in model.linears():  # K splits of the decode-regime linears, or the prefill GEMM's
+            if 2 <= batch <= _SKINNY_MAX_M:
+                gw = max(gw, int(lib.sqx_int4_skinny_workspace_bytes(batch, tw.rows, tw.cols, 0)))
+            elif batch > _SKINNY_MAX_M:
                 gw = max(gw, int(lib.sqx_gemm_workspace_bytes(batch, tw.rows, tw.cols)))
         self.gemm_ws = torch.empty(max(gw // 4, 4), dtype=torch.float32, device=dev) if gw > 0 else None
 
@@ -287,7 +293,12 @@ class Int4DecodeLM:
     def _linear(self, st: DecodeState, tw: i4.Int4Tiled, x: Tensor, y: Tensor, stream: int) -> None:
         lib = _lib.load()
         m = st.batch
-        if m >= i4.GEMM_MIN_M:
+        if 2 <= m <= _SKINNY_MAX_M:  # the library picks the GEMV or a decode-regime kernel by shape
+            rc = lib.sqx_int4_skinny(
+                tw.wt.data_ptr(), tw.st.data_ptr(), None, _lib.DTYPE_F32, x.data_ptr(), _lib.DTYPE_BF16,
+                y.data_ptr(), None, m, tw.rows, tw.cols, tw.group_size, 0, -1, 0, *_lib.ws_args(st.gemm_ws), stream,
+            )
+        elif m > _SKINNY_MAX_M:
             rc = lib.sqx_int4_gemm(
                 tw.wt.data_ptr(), tw.st.data_ptr(), None, _lib.DTYPE_F32, x.data_ptr(), _lib.DTYPE_BF16,
                 y.data_ptr(), None, m, tw.rows, tw.cols, tw.group_size, *_lib.ws_args(st.gemm_ws), stream,

@@ -300,6 +300,41 @@ def int4_linear_tiled(x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, k_sl
     return y.reshape(*batch, tw.rows)
 
 
+def int4_linear_skinny(
+    x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, *, tiles: int = 0, waves: int = -1, splits: int = 0
+) -> Tensor:
+    """``x @ W.T (+ bias)`` for 1..64 rows of ``x`` on the decode-regime kernels with an explicit
+    launch shape: ``tiles`` (1, 2 or 4) 16-row weight tiles per wave; ``waves`` 0 for the variant that
+    stages activations through LDS (4 waves, each with its own tiles), 1..8 for waves splitting K;
+    ``splits`` workgroups along K (fp32 partials added in split order). ``tiles``/``splits`` 0 and
+    ``waves`` -1 pick the library default. A given shape always gives the same bits."""
+    *batch, k = x.shape
+    if k != tw.cols:
+        raise ValueError(f"x has in_features={k}, weight expects {tw.cols}")
+    dev = _lib.require_device(x, tw.wt, bias, fn="int4_linear_skinny")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"int4_linear_skinny takes bf16 or fp16 activations, got {x.dtype}")
+    x2 = x.reshape(-1, k)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    if m > 64:
+        raise ValueError(f"int4_linear_skinny takes at most 64 rows, got {m}")
+    y = torch.empty(m, tw.rows, dtype=x.dtype, device=dev)
+    b = None if bias is None else bias.to(x.dtype).contiguous()
+    lib = _lib.load()
+    nb = int(lib.sqx_int4_skinny_workspace_bytes(m, tw.rows, tw.cols, int(splits)))
+    ws = torch.empty(nb // 4, dtype=torch.float32, device=dev) if nb > 0 else None
+    with torch.cuda.device(dev):
+        rc = lib.sqx_int4_skinny(
+            _lib.ptr(tw.wt), _lib.ptr(tw.st), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype), _lib.ptr(x2),
+            _lib.sqx_dtype(x.dtype), _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size, int(tiles),
+            int(waves), int(splits), *_lib.ws_args(ws), _lib.stream_ptr(dev),
+        )
+    _lib.check(rc, "int4_linear_skinny")
+    return y.reshape(*batch, tw.rows)
+
+
 _tiled_cache = _device.TensorKeyedCache()
 
 

@@ -215,8 +215,9 @@ def test_linear_rmsnorm_equals_two_calls(lib, m, k, group, with_delta):
     dp = None if dl is None else dl.data_ptr()
     _ok(lib, lib.sqx_rmsnorm(x.data_ptr(), dp, gain.data_ptr(), 1e-5, m, k, h1.data_ptr() if dl is not None else None,
                              hn.data_ptr(), _s()))
+    ks = lib.sqx_int4_linear_default_kslices(m, n, k)  # the GEMV the fused kernel runs
     _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, hn.data_ptr(), 1, y1.data_ptr(), None, m, n,
-                                 k, group, 0, _s()))
+                                 k, group, ks, _s()))
     _ok(lib, lib.sqx_int4_linear_rmsnorm(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), dp, gain.data_ptr(), 1e-5,
                                          h2.data_ptr() if dl is not None else None, y2.data_ptr(), m, n, k, group, 0, _s()))
     torch.cuda.synchronize()
@@ -234,8 +235,9 @@ def test_linear_silu_equals_two_calls(lib, m, f):
     act = torch.empty(m, f, dtype=torch.bfloat16, device=DEV)
     y1, y2 = (torch.empty(m, n, dtype=torch.bfloat16, device=DEV) for _ in range(2))
     _ok(lib, lib.sqx_silu_mul(gu.data_ptr(), m, f, act.data_ptr(), _s()))
+    ks = lib.sqx_int4_linear_default_kslices(m, n, f)  # the GEMV the fused kernel runs
     _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, act.data_ptr(), 1, y1.data_ptr(), None, m, n,
-                                 f, 128, 0, _s()))
+                                 f, 128, ks, _s()))
     _ok(lib, lib.sqx_int4_linear_silu(tw.wt.data_ptr(), tw.st.data_ptr(), gu.data_ptr(), y2.data_ptr(), m, n, f, 128, 0,
                                       _s()))
     torch.cuda.synchronize()
