@@ -33,12 +33,17 @@ replayed token after token. Per B: ms per step, tok/s (B / step time), HBM bytes
 timed alone, over the step time).
 
 fp8_w8a8 (not part of `value`): the FP8 E4M3 W8A8 linear (per-token activations, per-channel weights)
-at Llama-3-8B decode shapes, M = 1 and 16, HIP-event medians over >= 1 GB of rotating weights, next
+at Llama-3-8B decode shapes, M = 1 and 16, captured graphs over >= 1 GB of rotating weights, next
 to hipBLASLt's rowwise torch._scaled_mm (the reference's fp8_linear on ROCm) on the same operands,
 with each one's error against the float64 oracle in units of the reference's derived bound.
 
-prefill (not part of `value`): the prefill GEMMs at their BASELINE configs, HIP-event medians of
-back-to-back launches on inputs already in HBM: config 4's MXFP4 x MXFP4 GEMM at M = 4096 (both
+baseline_configs (not part of `value`): every case BASELINE configs 1-4 name (int8 weight-only
+4096x4096 at M = 1, 16; int4 g128 asymmetric at the four Llama-3-8B shapes, M = 1, 4, 8; AWQ at the
+same shapes, M = 64, 512, 2048; MXFP4 at the Llama-3-70B MLP shapes, M = 1 and 128, bf16 and MXFP4
+activations), each in GB/s or TFLOP/s against its roofline.
+
+prefill (not part of `value`): the prefill GEMMs at their BASELINE configs, captured graphs of
+back-to-back calls on inputs already in HBM: config 4's MXFP4 x MXFP4 GEMM at M = 4096 (both
 shapes) against the 10.1 PF dense fp4 MFMA peak, config 4's MXFP4-weight x bf16 GEMM at M = 4096
 and config 3's AWQ int4 GEMM at M = 2048 against the 2.5 PF bf16 peak.
 """
@@ -102,6 +107,7 @@ def main() -> int:
     ap.add_argument("--decode-batches", default="1,8,32,64", help="batch sizes of the decode-step measurement")
     ap.add_argument("--decode-fp8kv-batches", default="32,64", help="batch sizes also timed with the FP8 KV cache")
     ap.add_argument("--no-fp8", action="store_true", help="skip the FP8 W8A8 linear measurement")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config cases of BASELINE configs 1-4")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -333,6 +339,11 @@ def main() -> int:
         fp8 = fp8_linears(dev)
         log("fp8:", json.dumps(fp8))
 
+    configs = None
+    if not args.no_configs:
+        configs = baseline_configs(dev)
+        log("configs:", json.dumps(configs))
+
     decode = None
     if not args.no_decode:
         del linears, cpu_sample
@@ -392,6 +403,7 @@ def main() -> int:
         "decode": decode,
         "fp8_w8a8": fp8,
         "prefill": prefill,
+        "baseline_configs": configs,
     }
     print(json.dumps(out), flush=True)
     return 0
@@ -411,20 +423,30 @@ def measured_traffic(dom, m: int):
     return int(blk["traffic_bytes_per_launch"])
 
 
-def _median_us(fn, reps: int = 10, warm: int = 3) -> float:
+def _graph_call_us(fn, calls: int = 4, reps: int = 5) -> float:
+    """us per call of ``fn`` (device work on the current stream, any host-side allocation graph-safe),
+    captured ``calls`` times back to back in one HIP graph and replayed ``reps`` times between HIP
+    events: GPU time without the host's launch gaps."""
     import torch
 
-    for _ in range(warm):
-        fn()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        fn()  # warm any lazily built state outside the capture
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for a, b in ev:
-        a.record()
-        fn()
-        b.record()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cs):
+        for _ in range(calls):
+            fn()
+    graph.replay()
     torch.cuda.synchronize()
-    t = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
-    return t[len(t) // 2]
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / (reps * calls)
 
 
 def decode_steps(dev, batches: list[int], fp8_batches: list[int], steps: int = 20, warmup: int = 3) -> dict:
@@ -624,13 +646,13 @@ def prefill_gemms(dev) -> dict:
         del w
         x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
         xq = f4.mxfp4_quantize_tiled(x)
-        us = _median_us(lambda: f4.mxfp4_gemm(xq, tw))
+        us = _graph_call_us(lambda: f4.mxfp4_gemm(xq, tw))
         fl = 2.0 * m * n * k
         res[f"mxfp4_x_mxfp4 {k}->{n} M={m}"] = {
             "us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "frac_of_fp4_peak": round(fl / us * 1e6 / FP4_PEAK, 4),
-            "quantize_x_us": round(_median_us(lambda: f4.mxfp4_quantize_tiled(x)), 1)}
+            "quantize_x_us": round(_graph_call_us(lambda: f4.mxfp4_quantize_tiled(x)), 1)}
         if n == 28672:
-            us = _median_us(lambda: f4.fp4_linear_tiled(x, tw))
+            us = _graph_call_us(lambda: f4.fp4_linear_tiled(x, tw))
             res[f"mxfp4_w_bf16_x {k}->{n} M={m}"] = {
                 "us": round(us, 1), "tflops": round(fl / us / 1e6, 1),
                 "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4)}
@@ -643,10 +665,127 @@ def prefill_gemms(dev) -> dict:
     x = torch.randn(m, k, generator=g, device=dev)
     x[:, torch.randperm(k, generator=torch.Generator().manual_seed(k))[: k // 100].to(dev)] *= 20.0
     x = x.to(torch.bfloat16)
-    us = _median_us(lambda: awq.awq_linear(x, quant))
+    us = _graph_call_us(lambda: awq.awq_linear(x, quant))
     fl = 2.0 * m * n * k
     res[f"awq_int4_g128 {k}->{n} M={m}"] = {
         "us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4)}
+    return res
+
+
+def baseline_configs(dev) -> dict:
+    """Every case of BASELINE.json's configs 1-4 on one GPU (config 5 is ``decode``; config 4 at M = 4096
+    and config 3's M = 2048 on 4096->14336 are also in ``prefill``). Memory-bound cases (M <= 16, the
+    MXFP4 GEMV at M = 1) are timed as a captured graph of back-to-back launches over >= 1 GB of
+    rotating weights and reported in GB/s of algorithmic bytes; GEMMs as captured graphs of
+    back-to-back calls (no host launch gaps) in TFLOP/s against the dtype's dense peak. Weights ~N(0, 0.02), activations bf16 ~N(0, 1) as the configs
+    state; config 3's activation scale ~log-uniform[0.5, 2] and 1% of channels x20."""
+    import torch
+
+    from scratch_llm_amd import _lib
+    from scratch_llm_amd.quant import awq, int4_group as i4, int8 as q8, nvfp4_mxfp4 as f4
+
+    lib = _lib.load()
+    BF16_PEAK, FP4_PEAK = 2.5e15, 10.1e15
+    g = torch.Generator(device=dev).manual_seed(1007)
+    res = {"config1_int8_weight_only": {}, "config2_int4_g128_asym": {}, "config3_awq_int4_g128": {},
+           "config4_mxfp4": {}}
+
+    def rotating(n, k, make, per_weight_bytes):
+        copies = max(2, min(40, int(1.2e9 // per_weight_bytes)))
+        return [make(torch.randn(n, k, generator=g, device=dev) * 0.02) for _ in range(copies)]
+
+    def gbs_entry(us, byts):
+        return {"us": round(us, 2), "gbs": round(byts / us / 1e3, 1),
+                "frac_of_hbm_peak": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+    # config 1: int8 weight-only 4096x4096, per-output-channel symmetric, M in {1, 16}
+    n = k = 4096
+    tws = rotating(n, k, lambda w: q8.tile_int8(*q8.quantize_symmetric(w, axis=0)), n * k)
+    for m in (1, 16):
+        x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+
+        def run(stream):
+            for tw in tws:
+                lib.sqx_int8_linear(tw.wt.data_ptr(), tw.scale.data_ptr(), x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(),
+                                    None, m, n, k, 0, stream)
+            return len(tws)
+
+        res["config1_int8_weight_only"][f"{k}->{n} M={m}"] = gbs_entry(_graph_us(run), n * k + 4 * n + 2 * m * k + 2 * m * n)
+    del tws
+    torch.cuda.empty_cache()
+
+    # config 2: int4 g128 asymmetric (uint4 codes, bf16 scale and zero per group), M in {1, 4, 8}
+    for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
+        def make(w):
+            q, s_, z = i4.quantize_groupwise_uint4_asym(w, 128, torch.bfloat16)
+            return i4.tile_int4(q, s_, z, 128)
+
+        tws = rotating(n, k, make, n * k // 2)
+        for m in (1, 4, 8):
+            x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+
+            def run(stream):
+                for tw in tws:
+                    lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), tw.zt.data_ptr(), _lib.DTYPE_BF16,
+                                        x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(), None, m, n, k, 128, 0, stream)
+                return len(tws)
+
+            byts = n * k // 2 + 2 * 2 * n * k // 128 + 2 * m * k + 2 * m * n
+            res["config2_int4_g128_asym"][f"{k}->{n} M={m}"] = gbs_entry(_graph_us(run), byts)
+        del tws
+        torch.cuda.empty_cache()
+
+    # config 3: AWQ int4 g128 prefill GEMM, M in {64, 512, 2048}
+    for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
+        w = torch.randn(n, k, generator=g, device=dev) * 0.02
+        sc = torch.exp(torch.empty(k, device=dev).uniform_(-0.6931, 0.6931, generator=g))
+        quant = awq.quantize_awq_int4(w, chan_scale=sc)
+        del w
+        for m in (64, 512, 2048):
+            x = torch.randn(m, k, generator=g, device=dev)
+            x[:, torch.randperm(k, generator=torch.Generator().manual_seed(k))[: k // 100].to(dev)] *= 20.0
+            x = x.to(torch.bfloat16)
+            us = _graph_call_us(lambda: awq.awq_linear(x, quant))
+            fl = 2.0 * m * n * k
+            res["config3_awq_int4_g128"][f"{k}->{n} M={m}"] = {
+                "us": round(us, 1), "tflops": round(fl / us / 1e6, 1),
+                "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4)}
+        del quant
+        torch.cuda.empty_cache()
+
+    # config 4: MXFP4 weights (e2m1 + e8m0 per 32 along K), bf16 or MXFP4 activations, M in {1, 128}
+    for n, k in ((28672, 8192), (8192, 28672)):
+        tws = rotating(n, k, lambda w: f4.tile_fp4(f4.mxfp4_quantize(w, 32)), n * k // 2)
+        x1 = torch.randn(1, k, generator=g, device=dev).to(torch.bfloat16)
+        y1 = torch.empty(1, n, dtype=torch.bfloat16, device=dev)
+
+        def run(stream):
+            for tw in tws:
+                lib.sqx_fp4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), tw.fmt, _lib.ptr(tw.s_global), x1.data_ptr(),
+                                   _lib.DTYPE_BF16, y1.data_ptr(), _lib.DTYPE_BF16, None, 1, n, k, 0, stream)
+            return len(tws)
+
+        byts = n * k // 2 + n * k // 32 + 2 * k + 2 * n
+        res["config4_mxfp4"][f"bf16_x {k}->{n} M=1"] = gbs_entry(_graph_us(run), byts)
+        tw = tws[0]
+        del tws[1:]
+        m = 128
+        x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+        fl = 2.0 * m * n * k
+        us = _graph_call_us(lambda: f4.fp4_linear_tiled(x, tw))
+        res["config4_mxfp4"][f"bf16_x {k}->{n} M={m}"] = {
+            "us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4),
+            "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1)}
+        xq = f4.mxfp4_quantize_tiled(x)
+        us = _graph_call_us(lambda: f4.mxfp4_gemm(xq, tw))
+        res["config4_mxfp4"][f"mxfp4_x {k}->{n} M={m}"] = {
+            "us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "frac_of_fp4_peak": round(fl / us * 1e6 / FP4_PEAK, 4),
+            "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1),
+            "quantize_x_us": round(_graph_call_us(lambda: f4.mxfp4_quantize_tiled(x)), 1)}
+        del tw, tws
+        torch.cuda.empty_cache()
     return res
 
 

@@ -31,7 +31,7 @@ __all__ = ["DecodeConfig", "DecodeState", "Int4DecodeLM", "LLAMA3_8B", "rope_tab
 
 # Batches of 2..64 rows run the linears through sqx_int4_skinny's shape choice (the GEMV or a
 # decode-regime kernel, K split into the state's workspace); larger batches run the prefill GEMM.
-_SKINNY_MAX_M = 64
+_SKINNY_MAX_M = i4.GEMM_MIN_M - 1
 
 
 @dataclass(frozen=True)

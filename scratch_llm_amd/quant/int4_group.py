@@ -253,21 +253,24 @@ def tile_int4_packed(packed: Tensor, scales: Tensor, shape: tuple[int, int], gro
     return Int4Tiled(wt, st, None, rows, cols, group_size)
 
 
-# Activation rows from which the tiled linears switch from the streaming decode kernel to the
-# prefill GEMM.
-GEMM_MIN_M = 64
+# Activation rows from which the tiled linears switch from the decode-regime kernels (the streaming
+# GEMV at one row; for 2..64 rows the library's choice among the GEMV and the row-tiled kernels, with
+# K split into a workspace) to the prefill GEMM.
+GEMM_MIN_M = 65
 
 
 def int4_linear_tiled(x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, k_slices: int | None = None) -> Tensor:
     """``x @ W.T (+ bias)`` for a tiled INT4 weight ``W [out, in]``; ``x`` is ``[..., in]`` in bf16 or
     fp16 and the result has ``x``'s dtype and shape ``[..., out]``. fp32 accumulation.
 
-    Up to ``GEMM_MIN_M - 1`` rows run the streaming decode kernel; from ``GEMM_MIN_M`` rows on (and
-    ``k_slices`` unset) the prefill GEMM, which decodes each weight tile once per 256 rows.
+    With ``k_slices`` unset: one row runs the streaming decode GEMV; 2..``GEMM_MIN_M - 1`` rows the
+    library's choice for the shape (the GEMV or a row-tiled decode kernel, K possibly split into a
+    workspace, ``sqx_int4_skinny``); from ``GEMM_MIN_M`` rows on the prefill GEMM, which decodes each
+    weight tile once per 256 rows to the reference's bf16 weights.
 
-    ``k_slices`` (1..16) overrides how many waves split each 16-row tile's columns in the decode
-    kernel; the partial sums are added in a fixed order, so a given ``k_slices`` always gives the
-    same bits."""
+    ``k_slices`` (1..16) forces the decode GEMV with that many waves splitting each 16-row tile's
+    columns. Every path adds its partial sums in a fixed order, so a call's bits depend only on the
+    shape and ``k_slices``."""
     *batch, k = x.shape
     if k != tw.cols:
         raise ValueError(f"x has in_features={k}, weight expects {tw.cols}")
@@ -283,7 +286,15 @@ def int4_linear_tiled(x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, k_sl
     lib = _lib.load()
     ks = 0 if k_slices is None else int(k_slices)
     with torch.cuda.device(dev):
-        if m >= GEMM_MIN_M and k_slices is None:
+        if 2 <= m < GEMM_MIN_M and k_slices is None:
+            nb = int(lib.sqx_int4_skinny_workspace_bytes(m, tw.rows, tw.cols, 0))
+            ws = torch.empty(nb // 4, dtype=torch.float32, device=dev) if nb > 0 else None
+            rc = lib.sqx_int4_skinny(
+                _lib.ptr(tw.wt), _lib.ptr(tw.st), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype), _lib.ptr(x2),
+                _lib.sqx_dtype(x.dtype), _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size, 0, -1, 0,
+                *_lib.ws_args(ws), _lib.stream_ptr(dev),
+            )
+        elif m >= GEMM_MIN_M and k_slices is None:
             ws = _lib.gemm_workspace(m, tw.rows, tw.cols, dev)
             rc = lib.sqx_int4_gemm(
                 _lib.ptr(tw.wt), _lib.ptr(tw.st), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype), _lib.ptr(x2),
