@@ -115,23 +115,23 @@ int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt, int param
                     int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
 
 /* The same W4A16 linear for 1 <= m <= 64 activation rows (the decode regime of batched serving) with
- * an explicit launch shape. Each wave owns `tiles` (1, 2 or 4) 16-row weight tiles and applies each
- * k-block's activation fragments to all of them; the codes' offset is removed through per-group
- * activation sums. waves = 0: the LDS-staged variant (four waves with their own tiles share the
- * activations through LDS; one more wave copies them); waves = 1..8: that many waves split each
- * workgroup's k-blocks (tiles 2 or 4). splits >= 1 workgroups split K further and write fp32 partials
- * to ws, added in split order by a second kernel. tiles or splits <= 0, or waves < 0, pick the
- * library default (splits > 1 only when ws is given); with all three left to the library, shapes
- * where the decode GEMV is faster run it (sqx_int4_linear's GEMV form). The library may lower
- * `tiles` where the registers would not hold it. Deterministic for a given shape. ws: 16-byte aligned,
- * sqx_int4_skinny_workspace_bytes(m, rows, cols, splits) bytes (0 when splits resolves to 1; splits
- * <= 0 asks for the default's). Other arguments and results as sqx_int4_linear. No counterpart in the
- * reference (a launch shape of w4a16_linear, int4_group.py:148-164). */
+ * an explicit launch shape. Each wave owns `tiles` 16-row weight tiles and applies each k-block's
+ * activation fragments to all of them; the codes' offset is removed through per-group activation
+ * sums. variant 0: `waves` (1..8) split each workgroup's k-blocks, tiles 2 or 4. variant 1: the
+ * activations are staged through LDS and shared by `waves` compute waves (4, or 8 as two k-groups)
+ * that own disjoint tiles (tiles 1, 2 or 4). splits >= 1 workgroups split K further and write fp32
+ * partials to ws, added in split order by a second kernel. variant < 0 is the library's choice for
+ * the shape, the decode GEMV included when tiles, waves and splits are all <= 0; tiles, waves or
+ * splits <= 0 pick the default of the variant (splits > 1 only when ws is given). The library may
+ * lower `tiles` where the registers would not hold it. Deterministic for a given shape. ws: 16-byte
+ * aligned, sqx_int4_skinny_workspace_bytes(m, rows, cols, splits) bytes (0 when splits resolves to
+ * 1; splits <= 0 asks for the library choice's). Other arguments and results as sqx_int4_linear. No
+ * counterpart in the reference (a launch shape of w4a16_linear, int4_group.py:148-164). */
 int64_t sqx_int4_skinny_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int splits);
 int sqx_int4_skinny(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
                     int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
-                    int64_t group, int tiles, int waves, int splits, void* ws, int64_t ws_bytes,
-                    sqx_stream_t stream);
+                    int64_t group, int variant, int tiles, int waves, int splits, void* ws,
+                    int64_t ws_bytes, sqx_stream_t stream);
 
 /* 1 when sqx_int4_linear_rmsnorm / sqx_int4_linear_silu take m activation rows of cols columns
  * (m <= 8, cols % 8 == 0, the rows fit the kernel's 64 KiB LDS copy), else 0. */

@@ -55,8 +55,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sqx_int4_skinny_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i]),
     "sqx_int4_skinny": (
         _c_i,
-        [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_i, _c_i, _c_p,
-         _c_i64, _c_p],
+        [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_i, _c_i, _c_i,
+         _c_p, _c_i64, _c_p],
     ),
     "sqx_int4_prologue_fits": (_c_i, [_c_i64, _c_i64]),
     "sqx_int4_linear_rmsnorm": (

@@ -397,6 +397,7 @@ struct WInt4 {
                    and_or(d >> 12, kMask, magic)};
   }
   static constexpr bool kConstOffset = !ASYM;
+  static constexpr int kLoads = 1 + NG * (ASYM ? 2 : 1);  // buffer loads of one block (codes + parameters)
   template <class A>
   __device__ static float const_offset() { return A::kMagic + 8.0f; }
   template <class A>
@@ -789,9 +790,10 @@ extern "C" int sqx_int4_linear_colscaled(const uint8_t* wt, const void* st, cons
                           stream, "sqx_int4_linear_colscaled");
 }
 
-// The 1..64-row linear with an explicit launch shape: tiles (1, 2 or 4) row tiles per wave; waves 0
-// for the LDS-staged variant, 1..8 for waves splitting K; splits >= 1 workgroups along K. tiles or
-// splits <= 0, or waves < 0, pick the library default.
+// The 1..64-row linear with an explicit launch shape: variant 0 (waves splitting K, 2 or 4 tiles
+// per wave, 1..8 waves) or 1 (LDS-staged, 1, 2 or 4 tiles per wave, 4 or 8 compute waves), splits
+// >= 1 workgroups along K. variant < 0 is the library's choice for the shape (the GEMV included when
+// no other argument is given); tiles, waves or splits <= 0 pick the default of the variant.
 static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
                             int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
                             int64_t group, SkinnyShape sh, void* ws, int64_t ws_bytes, sqx_stream_t stream,
@@ -810,9 +812,11 @@ static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, i
   SQX_REQUIRE(rows < ((int64_t)1 << 31) && ceil_div(rows, 16) * ceil_div(cols, 128) * 1024 < ((int64_t)1 << 31) &&
                   64 * cols * 2 < ((int64_t)1 << 31),
               SQX_E_ARG, "%s: shape too large for 32-bit buffer offsets", fn);
-  SQX_REQUIRE(sh.waves >= 0 && sh.waves <= kSkinnyMaxWaves && sh.S >= 1 &&
-                  (sh.R == 2 || sh.R == 4 || (sh.R == 1 && sh.waves == 0)),
-              SQX_E_ARG, "%s: bad launch shape (tiles %d, waves %d, splits %d)", fn, sh.R, sh.waves, sh.S);
+  SQX_REQUIRE(sh.S >= 1 &&
+                  ((sh.variant == 0 && (sh.R == 2 || sh.R == 4) && sh.waves >= 1 && sh.waves <= kSkinnyMaxWaves) ||
+                   (sh.variant == 1 && (sh.R == 1 || sh.R == 2 || sh.R == 4) && (sh.waves == 4 || sh.waves == 8))),
+              SQX_E_ARG, "%s: bad launch shape (variant %d, tiles %d, waves %d, splits %d)", fn, sh.variant, sh.R,
+              sh.waves, sh.S);
   if (m == 0) return SQX_OK;
   SQX_REQUIRE(wt && st && x && y, SQX_E_ARG, "%s: null pointer", fn);
   SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, SQX_E_ARG,
@@ -855,14 +859,17 @@ extern "C" int64_t sqx_int4_skinny_workspace_bytes(int64_t m, int64_t rows, int6
 
 extern "C" int sqx_int4_skinny(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
                                int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
-                               int64_t group, int tiles, int waves, int splits, void* ws, int64_t ws_bytes,
-                               sqx_stream_t stream) {
+                               int64_t group, int variant, int tiles, int waves, int splits, void* ws,
+                               int64_t ws_bytes, sqx_stream_t stream) {
   SkinnyShape sh = skinny_default_shape(m, rows, cols, 128, ws != nullptr);
-  if (tiles <= 0 && waves < 0 && splits <= 0 && sh.gemv)  // the library's choice for this shape: the GEMV
+  if (variant < 0 && tiles <= 0 && waves <= 0 && splits <= 0 && sh.gemv)  // the library's choice: the GEMV
     return int4_linear_impl(wt, st, zt, param_dtype, x, act_dtype, y, bias, nullptr, m, rows, cols, group,
                             sqx_int4_linear_default_kslices(m, rows, cols), stream, "sqx_int4_skinny");
+  if (variant >= 0 && (variant != sh.variant || sh.gemv))  // the variant's own defaults
+    sh = variant == 0 ? SkinnyShape{0, 2, 8, 1, false} : SkinnyShape{1, 2, 4, 1, false};
+  if (variant > 1) sh.variant = variant;  // refused below
   if (tiles > 0) sh.R = tiles;
-  if (waves >= 0) sh.waves = waves;
+  if (waves > 0) sh.waves = waves;
   if (splits > 0) sh.S = splits;
   return int4_skinny_impl(wt, st, zt, param_dtype, x, act_dtype, y, bias, m, rows, cols, group, sh, ws, ws_bytes,
                           stream, "sqx_int4_skinny");

@@ -222,88 +222,84 @@ __global__ __launch_bounds__((64 * skinny_max_waves(MCH, R, W::NG, W::kConstOffs
 }
 
 // Variant with the activations staged through LDS. A workgroup owns 4R row tiles and a range of n
-// k-blocks; it has 4 compute waves (R tiles each, disjoint, so no reduction across waves) and one
-// copy wave.
-//  * The copy wave moves each k-block of activations (all M rows, 256 bytes a row) into a ring of NS
-//    LDS stages with buffer loads that write LDS directly, 16 bytes a lane in whole row segments. It
-//    issues nothing else, so its vmcnt waits count exactly its own copies. Slot (row r, 16-byte chunk
-//    q) holds chunk q ^ (r & 15) of the row: the 16 rows a fragment read touches fall in 16 different
-//    bank groups. Rows at or beyond M and columns at or beyond K are copied as zeros.
-//  * Compute waves keep the weights of the next D k-blocks in flight in a register ring (the
-//    compiler waits for each block's loads where they are used) and read activation fragments from
-//    LDS.
-//  * Step s starts with barrier B_s, which every wave reaches once per step. Before it the copy wave
-//    waits for its copy of block s; after it, it refills the slot of block s-1 (read by every compute
-//    wave before B_s) with block s+NS-1.
-template <class A, class W, int MCH, int R, int D>
-__global__ __launch_bounds__(320) void skinny_lds_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
-                                                         void* __restrict__ out, const uint16_t* __restrict__ bias,
-                                                         int M, int N, int K, int KB, int T, int kbs, int split_out) {
+// k-blocks. It has 4 x KG compute waves: wave (kg, tg) owns tiles tg*R .. tg*R+R-1 of the group and
+// the kg-th of KG equal parts of the k-range, so KG = 2 puts two compute waves on each SIMD without
+// more workgroups; at the end the second k-group's partial sums are added to the first's through
+// LDS in a fixed order.
+//  * Each k-group stages its k-blocks of activations (all M rows, 256 bytes a row) in its own ring
+//    of NS LDS stages, with buffer loads that write LDS directly, 16 bytes a lane in whole row
+//    segments; every wave of the group copies MCH of the block's 1 KiB pieces. Slot (row r, chunk
+//    q) holds chunk q ^ (r & 15) of the row, so the 16 rows a fragment read touches fall in 16
+//    different bank groups. Rows at or beyond M and columns at or beyond K are copied as zeros.
+//  * Every wave keeps the weights of the next D k-blocks in flight in a register ring.
+//  * Every step issues the same loads in the same order (copy of block s+2, then the ring refill of
+//    block s+D; past the k-group's last block, zero-size buffer resources and out-of-range offsets
+//    keep the count without touching memory), so at step s the copy of block s is complete once at
+//    most 2 x (ring loads) + MCH loads are outstanding. After that wait the barrier B_s tells every
+//    wave that block s is in LDS and that the slot of block s-1 may be refilled.
+template <class A, class W, int MCH, int R, int D, int KG>
+__global__ __launch_bounds__(256 * KG) void skinny_lds_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
+                                                              void* __restrict__ out, const uint16_t* __restrict__ bias,
+                                                              int M, int N, int K, int KB, int T, int kbs,
+                                                              int split_out) {
   constexpr int KBLK = W::KBLK;
   static_assert(KBLK == 128, "an activation row of a block is 16 chunks of 16 bytes");
+  static_assert(D >= 2, "the issue order assumes a ring of at least two blocks");
   constexpr int STEPS = W::STEPS;
+  constexpr int NG = W::NG;
   constexpr int kStage = MCH * 16 * 256;
-  constexpr int kCopies = MCH * 4;  // 1 KiB copies per block (4 rows each)
   constexpr int NS = 3;
+  constexpr int kWaitN = 2 * R * W::kLoads + MCH;  // loads issued after a block's copy by its step
+  static_assert(kWaitN < 64, "vmcnt is 6 bits");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_skinny[];
-  uint8_t* smem = smem_skinny;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tg = wave & 3;
+  const int kg = wave >> 2;
   const int ks0 = blockIdx.y * kbs;
-  const int n = min(KB, ks0 + kbs) - ks0;
-  // Step s reads k-block ks0 + (s + rot) mod n. Workgroups resident together start at different
+  const int n = min(KB, ks0 + kbs) - ks0;  // k-blocks of this split
+  const int nh = (n + KG - 1) / KG;        // steps every wave walks
+  const int k0 = ks0 + kg * nh;            // the k-group's first block
+  const int nk = max(0, min(nh, n - kg * nh));  // its real blocks; later steps load zeros
+  // Step s reads block k0 + (s + rot) mod nk. Workgroups resident together start at different
   // blocks: their tiles are KB KiB apart, so in lockstep they would read addresses equal modulo that
   // stride and crowd the same HBM channels.
-  const int rot = n > 0 ? static_cast<int>(blockIdx.x % static_cast<unsigned>(n)) : 0;
+  const int rot = nk > 0 ? static_cast<int>(blockIdx.x % static_cast<unsigned>(nk)) : 0;
   auto kb_of = [&](int s) {
     int j = s + rot;
-    if (j >= n) j -= n;
-    return ks0 + j;
+    if (j >= nk) j -= nk;
+    return k0 + j;
+  };
+  uint8_t* ring = smem_skinny + kg * NS * kStage;
+  const rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
+  auto issue_x = [&](int s, int slot) {  // this wave's MCH copies of step s
+    const bool live = s < nk;
+    const int kb = live ? kb_of(s) : 0;
+    uint8_t* base = ring + slot * kStage;
+#pragma unroll
+    for (int q = 0; q < MCH; ++q) {
+      const int j = tg + 4 * q;  // rows 4j .. 4j+3
+      const int r = 4 * j + (lane >> 4);
+      const int col = kb * KBLK + 8 * ((lane & 15) ^ (r & 15));
+      const bool ok = live & (r < M) & (col < K);  // a select, not a branch
+      const uint32_t off = ok ? ((uint32_t)r * (uint32_t)K + (uint32_t)col) * 2u : 0xFFFFFFF0u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(base + j * 1024), 16, off, 0, 0, 0);
+    }
   };
 
-  if (wave == 4) {  // the copy wave
-    const rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
-    auto issue_x = [&](int kb, int slot) {
-      uint8_t* base = smem + slot * kStage;
-#pragma unroll
-      for (int j = 0; j < kCopies; ++j) {  // rows 4j .. 4j+3
-        const int r = 4 * j + (lane >> 4);
-        const int col = kb * KBLK + 8 * ((lane & 15) ^ (r & 15));
-        const bool ok = (r < M) & (col < K);  // a select, not a branch
-        const uint32_t off = ok ? ((uint32_t)r * (uint32_t)K + (uint32_t)col) * 2u : 0xFFFFFFF0u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(base + j * 1024), 16, off, 0, 0, 0);
-      }
-    };
-#pragma unroll
-    for (int s = 0; s < NS - 1; ++s)
-      if (s < n) issue_x(kb_of(s), s);
-    for (int s = 0; s < n; ++s) {
-      // copies issued after block s: blocks s+1 .. min(s+NS-2, n-1)
-      if (s + 1 < n) wait_vmcnt<kCopies>();  // NS = 3: at most one later block
-      else wait_vmcnt<0>();
-      lds_barrier();  // B_s
-      __builtin_amdgcn_sched_barrier(0);
-      if (s + NS - 1 < n) issue_x(kb_of(s + NS - 1), (s + NS - 1) % NS);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    return;
-  }
-
   // the wave's first tile and tile count, pinned to scalar registers (they size buffer resources)
-  const int tw0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + wave) * R);
+  const int tw0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + tg) * R);
   const int nt = __builtin_amdgcn_readfirstlane(max(0, min(R, T - tw0)));
   const int nl = lane & 15;
   const int jg = lane >> 4;
   const typename W::Ctx wc = W::ctx_tiles(wa, nt > 0 ? tw0 : 0, nt, KB, lane);
+  const typename W::Ctx wnull = W::ctx_tiles(wa, 0, 0, KB, lane);  // zero-size: its loads return zero
   const uint32_t ones = A::pair_from_f32(1.0f);
   const u32x4_t onev = u32x4_t{ones, ones, ones, ones};
-
   // With one offset for every group, the sum chain multiplies by -(magic + 8) directly and its result
   // seeds the main chains; per-group zero points scale the plain sum per tile.
   const uint32_t sumc = W::kConstOffset ? A::pair_from_f32(-W::template const_offset<A>()) : ones;
   const u32x4_t sumv = u32x4_t{sumc, sumc, sumc, sumc};
-  constexpr int NG = W::NG;
-  constexpr int MPG = W::MPG;
 
   f32x4_t yacc[R][MCH];
 #pragma unroll
@@ -312,23 +308,30 @@ __global__ __launch_bounds__(320) void skinny_lds_kernel(const typename W::Args 
     for (int c = 0; c < MCH; ++c) yacc[r][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   u32x4_t wring[D][R];
   typename W::P pring[D][R];
+  auto load_step = [&](int s, int slot) {  // exactly R * W::kLoads loads
+    const bool live = s < nk;
+    const typename W::Ctx& c = live ? wc : wnull;
+    const int kb = live ? kb_of(s) : 0;
 #pragma unroll
-  for (int d = 0; d < D; ++d)
+    for (int r = 0; r < R; ++r) W::load(c, r * KB + kb, wring[slot][r], pring[slot][r]);
+  };
+  // prologue in the steady state's issue order: ring blocks 0 .. D-3 first (older than every copy),
+  // then copy 0, ring D-2, copy 1, ring D-1
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      wring[d][r] = u32x4_t{0u, 0u, 0u, 0u};
-      pring[d][r] = typename W::P{};
-    }
-#pragma unroll
-  for (int d = 0; d < D; ++d)
-    if (d < n) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) W::load(wc, r * KB + kb_of(d), wring[d][r], pring[d][r]);
-    }
+  for (int d = 0; d < D - 2; ++d) load_step(d, d);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_x(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  load_step(D - 2, D - 2);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_x(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  load_step(D - 1, D - 1);
+
   // Software pipeline (one group per block): the weights of step s+1 are decoded while the MFMAs
-  // of step s run, so the decode's VALU work issues between independent MFMAs. Ring slot t % D holds
-  // step t; at the start of step s, slot s % D (decoded during step s-1) is refilled with step s+D.
-  // Blocks with several groups decode each step's weights at its start instead.
+  // of step s run, so the decode's VALU work issues between independent MFMAs. Blocks with several
+  // groups decode each step's weights at its start instead. Ring slot t % D holds step t; it is
+  // refilled with step t+D at the start of step t (after its decode).
   constexpr bool PIPE = NG == 1;
   u32x4_t bcur[R][STEPS];
   typename W::P pcur[R];
@@ -341,14 +344,15 @@ __global__ __launch_bounds__(320) void skinny_lds_kernel(const typename W::Args 
     }
   }
 
-  for (int s0 = 0; s0 < n; s0 += D) {
+  for (int s0 = 0; s0 < nh; s0 += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int s = s0 + d;
-      if (s >= n) break;  // wave-uniform; every wave still meets n barriers
+      if (s >= nh) break;  // workgroup-uniform: every wave meets nh barriers
       const int dn = (d + 1) % D;  // ring slot of step s+1 (a constant once the loop is unrolled)
       __builtin_amdgcn_sched_barrier(0);
-      lds_barrier();  // B_s: block s is in LDS
+      wait_vmcnt<kWaitN>();
+      lds_barrier();  // B_s: block s is in this k-group's ring
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (!PIPE) {
 #pragma unroll
@@ -358,11 +362,11 @@ __global__ __launch_bounds__(320) void skinny_lds_kernel(const typename W::Args 
           pcur[r] = pring[d][r];
         }
       }
-      if (s + D < n) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) W::load(wc, r * KB + kb_of(s + D), wring[d][r], pring[d][r]);
-      }
-      const uint8_t* st = smem + (s % NS) * kStage;
+      issue_x(s + 2, (s + 2) % NS);
+      __builtin_amdgcn_sched_barrier(0);
+      load_step(s + D, d);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint8_t* st = ring + (s % NS) * kStage;
       u32x4_t xv[MCH][STEPS];
 #pragma unroll
       for (int c = 0; c < MCH; ++c) {
@@ -426,16 +430,31 @@ __global__ __launch_bounds__(320) void skinny_lds_kernel(const typename W::Args 
           for (int i = 0; i < STEPS; ++i) bcur[r][i] = bnext[r][i];
           pcur[r] = pnext[r];
         }
-        // interleave: the fragment reads first, then one MFMA per two VALU instructions
-#pragma unroll
-        for (int k = 0; k < MCH * STEPS; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-#pragma unroll
-        for (int k = 0; k < STEPS * MCH * (1 + R); ++k) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-        }
       }
     }
+  }
+  // Every copy has landed (nothing may still write LDS) before the ring is reused or freed.
+  wait_vmcnt<0>();
+
+  if constexpr (KG == 2) {  // the second k-group's sums join the first's, in that order
+    f32x4_t* red = reinterpret_cast<f32x4_t*>(smem_skinny);
+    lds_barrier();  // every wave is done with the rings
+    if (kg == 1) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int c = 0; c < MCH; ++c) red[((tg * R + r) * MCH + c) * 64 + lane] = yacc[r][c];
+    }
+    lds_barrier();
+    if (kg == 1) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int c = 0; c < MCH; ++c) {
+        const f32x4_t v = red[((tg * R + r) * MCH + c) * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) yacc[r][c][j] += v[j];
+      }
   }
 
   // yacc[r][c][j] is y[c*16 + 4(l >> 4) + j][(tw0 + r)*16 + (l & 15)]
@@ -499,46 +518,62 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
 }
 
 // The launch shape the library picks for an m-row linear (m <= 64) over rows x cols weights, from
-// a measured sweep of the Llama-3-8B shapes (4096 -> 1024..128256, 14336 -> 4096; m = 8..64):
-//   m <= 16       waves splitting K: 4 tiles x 4 waves from 1024 row tiles on, 2 x 8 from 384; below
-//                 that the decode GEMV is faster, except for long K (>= 64 blocks) with a workspace
-//                 (2 x 8 waves, 2 splits);
-//   m <= 32       the LDS-staged variant from 1024 tiles on (2 tiles per wave from 4096 tiles, else
-//                 1); below: long K with a workspace -> LDS-staged, 1 tile, 8 splits; otherwise waves
-//                 splitting K, 2 x 8 (2 splits from a workspace when fewer than 384 tiles);
-//   m <= 64       the LDS-staged variant: 2 tiles per wave from 1024 tiles on; below, with a
-//                 workspace, 1 tile per wave (2 for long K) and K split until about 192 workgroups.
+// measured sweeps of the Llama-3-8B shapes (4096 -> 1024..128256, 14336 -> 4096; m = 8..64):
+//   m <= 16       waves splitting K: 4 tiles x 4 waves from 1024 row tiles, 2 x 8 from 384; from 4096
+//                 tiles the LDS-staged variant (4 tiles, 4 waves); below 384 tiles the decode GEMV,
+//                 except for long K (>= 64 blocks) with a workspace (2 x 8 waves, 2 splits);
+//   m <= 32       the LDS-staged variant from 1024 tiles (1 tile per wave, 8 compute waves, or 4 from
+//                 4096 tiles); below: long K with a workspace -> LDS-staged, 1 tile, 8 waves, K split
+//                 to about 192 workgroups; otherwise waves splitting K, 2 x 8 (2 splits from a
+//                 workspace when fewer than 384 tiles);
+//   m <= 64       the LDS-staged variant with 8 compute waves (4 from 4096 tiles): 2 tiles per wave
+//                 from 1024 tiles; below, 1 tile per wave (2 for long K) and, with a workspace, K split
+//                 to about 192 workgroups.
 struct SkinnyShape {
-  int R;      // row tiles per wave: 1, 2 or 4 (the K-split variant: 2 or 4)
-  int waves;  // 0: the LDS-staged variant (4 waves, each its own tiles); 1..8: waves splitting K
-  int S;      // workgroups along K (S > 1 needs a workspace of S*m*rows fp32)
-  bool gemv;  // the decode GEMV is the better kernel for this shape
+  int variant;  // 0: waves splitting K (skinny_kernel); 1: LDS-staged (skinny_lds_kernel)
+  int R;        // row tiles per wave: 1, 2 or 4 (the K-split variant: 2 or 4)
+  int waves;    // K-split: 1..8 waves per workgroup; LDS-staged: 4 or 8 compute waves (1 or 2 k-groups)
+  int S;        // workgroups along K (S > 1 needs a workspace of S*m*rows fp32)
+  bool gemv;    // the decode GEMV is the better kernel for this shape
 };
 
 inline SkinnyShape skinny_default_shape(int64_t m, int64_t rows, int64_t cols, int kblk, bool have_ws) {
   const int64_t T = ceil_div(rows, 16);
   const int64_t KB = ceil_div(cols, kblk);
-  SkinnyShape s{2, 8, 1, false};
+  SkinnyShape s{0, 2, 8, 1, false};
+  auto split_to_192 = [&]() {  // K splits until about 192 workgroups, >= 4 k-blocks per k-group
+    if (!have_ws) return;
+    const int64_t wgs = ceil_div(T, 4 * s.R);
+    const int64_t kg = s.variant == 1 ? s.waves / 4 : 1;
+    while (wgs * s.S < 192 && KB / (2 * s.S * kg) >= 4) s.S *= 2;
+  };
   if (m <= 1) {
     s.gemv = true;
   } else if (m <= 16) {
-    if (T >= 1024) s = SkinnyShape{4, 4, 1, false};
-    else if (T >= 384) s = SkinnyShape{2, 8, 1, false};
-    else if (have_ws && KB >= 64) s = SkinnyShape{2, 8, 2, false};
+    if (T >= 4096) s = SkinnyShape{1, 4, 4, 1, false};
+    else if (T >= 1024) s = SkinnyShape{0, 4, 4, 1, false};
+    else if (T >= 384) s = SkinnyShape{0, 2, 8, 1, false};
+    else if (have_ws && KB >= 64) s = SkinnyShape{0, 2, 8, 2, false};
     else s.gemv = true;
   } else if (m <= 32) {
-    if (T >= 1024) s = SkinnyShape{T >= 4096 ? 2 : 1, 0, 1, false};
-    else if (have_ws && KB >= 64) s = SkinnyShape{1, 0, 8, false};
-    else s = SkinnyShape{2, 8, (have_ws && T < 384) ? 2 : 1, false};
-  } else {
-    if (T >= 1024) {
-      s = SkinnyShape{2, 0, 1, false};
+    if (T >= 4096) {
+      s = SkinnyShape{1, 1, 4, 1, false};
+    } else if (T >= 1024) {
+      s = SkinnyShape{1, 1, 8, 1, false};
+    } else if (have_ws && KB >= 64) {
+      s = SkinnyShape{1, 1, 8, 1, false};
+      split_to_192();
     } else {
-      s = SkinnyShape{KB >= 64 ? 2 : 1, 0, 1, false};
-      if (have_ws) {
-        const int64_t wgs = ceil_div(T, 4 * s.R);
-        while (wgs * s.S < 192 && KB / (2 * s.S) >= 4) s.S *= 2;
-      }
+      s = SkinnyShape{0, 2, 8, (have_ws && T < 384) ? 2 : 1, false};
+    }
+  } else {
+    if (T >= 4096) {
+      s = SkinnyShape{1, 2, 4, 1, false};
+    } else if (T >= 1024) {
+      s = SkinnyShape{1, 2, 8, 1, false};
+    } else {
+      s = SkinnyShape{1, KB >= 64 ? 2 : 1, 8, 1, false};
+      split_to_192();
     }
   }
   return s;
@@ -556,10 +591,10 @@ inline int skinny_splits(int64_t KB, int S) {
 // The LDS-staged variant: R (1, 2 or 4) tiles per wave, 4 waves per workgroup, S splits along K.
 template <class A, class W>
 hipError_t skinny_lds_launch(const typename W::Args& wa, const uint16_t* x, uint16_t* y, const uint16_t* bias,
-                             int64_t m, int64_t rows, int64_t cols, int R, int S, float* ws, int64_t ws_bytes,
+                             int64_t m, int64_t rows, int64_t cols, int R, int KG, int S, float* ws, int64_t ws_bytes,
                              hipStream_t stream) {
   constexpr int KBLK = W::KBLK;
-  if (m < 1 || m > 64 || (R != 1 && R != 2 && R != 4) || S < 1) return hipErrorInvalidValue;
+  if (m < 1 || m > 64 || (R != 1 && R != 2 && R != 4) || (KG != 1 && KG != 2) || S < 1) return hipErrorInvalidValue;
   // per-group zero points with two or four groups per block hold more parameters per tile: fewer
   // tiles per wave keep the registers within two waves per SIMD
   constexpr int kMaxR = (W::NG == 1 || W::kConstOffset) ? 4 : (W::NG == 2 ? 2 : 1);
@@ -578,13 +613,19 @@ hipError_t skinny_lds_launch(const typename W::Args& wa, const uint16_t* x, uint
   const bool split = S > 1;
   if (split && (ws == nullptr || ws_bytes < skinny_workspace_bytes(m, rows, S))) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(ceil_div(T, 4 * R)), static_cast<unsigned>(S));
-  const size_t lds = static_cast<size_t>(3) * mch * 16 * 256;
+  const size_t lds = static_cast<size_t>(KG) * 3 * mch * 16 * 256;
   void* o = split ? static_cast<void*>(ws) : static_cast<void*>(y);
   const int M = static_cast<int>(m), N = static_cast<int>(rows), K = static_cast<int>(cols), iKB = static_cast<int>(KB),
             iT = static_cast<int>(T);
-#define SQX_SL(MCH_, R_)                                                                                          \
-  hipLaunchKernelGGL((skinny_lds_kernel<A, W, MCH_, R_, skinny_ring<R_>()>), grid, dim3(320), lds, stream, wa, x, o, bias, M, \
-                     N, K, iKB, iT, kbs, split ? 1 : 0)
+#define SQX_SL(MCH_, R_)                                                                                            \
+  do {                                                                                                              \
+    if (KG == 1)                                                                                                    \
+      hipLaunchKernelGGL((skinny_lds_kernel<A, W, MCH_, R_, skinny_ring<R_>(), 1>), grid, dim3(256), lds, stream, wa, \
+                         x, o, bias, M, N, K, iKB, iT, kbs, split ? 1 : 0);                                        \
+    else                                                                                                            \
+      hipLaunchKernelGGL((skinny_lds_kernel<A, W, MCH_, R_, skinny_ring<R_>(), 2>), grid, dim3(512), lds, stream, wa, \
+                         x, o, bias, M, N, K, iKB, iT, kbs, split ? 1 : 0);                                        \
+  } while (0)
   if (mch == 1) {
     if (R == 1) SQX_SL(1, 1);
     else if constexpr (kMaxR >= 2) {
@@ -613,7 +654,8 @@ template <class A, class W>
 hipError_t skinny_launch(const typename W::Args& wa, const uint16_t* x, uint16_t* y, const uint16_t* bias, int64_t m,
                          int64_t rows, int64_t cols, SkinnyShape sh, float* ws, int64_t ws_bytes, hipStream_t stream) {
   constexpr int KBLK = W::KBLK;
-  if (sh.waves == 0) return skinny_lds_launch<A, W>(wa, x, y, bias, m, rows, cols, sh.R, sh.S, ws, ws_bytes, stream);
+  if (sh.variant == 1)
+    return skinny_lds_launch<A, W>(wa, x, y, bias, m, rows, cols, sh.R, sh.waves / 4, sh.S, ws, ws_bytes, stream);
   if (m < 1 || m > 64 || sh.waves < 1 || sh.waves > kSkinnyMaxWaves || (sh.R != 2 && sh.R != 4) || sh.S < 1)
     return hipErrorInvalidValue;
   const int64_t T = ceil_div(rows, 16);

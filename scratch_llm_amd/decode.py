@@ -296,7 +296,8 @@ class Int4DecodeLM:
         if 2 <= m <= _SKINNY_MAX_M:  # the library picks the GEMV or a decode-regime kernel by shape
             rc = lib.sqx_int4_skinny(
                 tw.wt.data_ptr(), tw.st.data_ptr(), None, _lib.DTYPE_F32, x.data_ptr(), _lib.DTYPE_BF16,
-                y.data_ptr(), None, m, tw.rows, tw.cols, tw.group_size, 0, -1, 0, *_lib.ws_args(st.gemm_ws), stream,
+                y.data_ptr(), None, m, tw.rows, tw.cols, tw.group_size, -1, 0, 0, 0, *_lib.ws_args(st.gemm_ws),
+                stream,
             )
         elif m > _SKINNY_MAX_M:
             rc = lib.sqx_int4_gemm(

@@ -291,7 +291,7 @@ def int4_linear_tiled(x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, k_sl
             ws = torch.empty(nb // 4, dtype=torch.float32, device=dev) if nb > 0 else None
             rc = lib.sqx_int4_skinny(
                 _lib.ptr(tw.wt), _lib.ptr(tw.st), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype), _lib.ptr(x2),
-                _lib.sqx_dtype(x.dtype), _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size, 0, -1, 0,
+                _lib.sqx_dtype(x.dtype), _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size, -1, 0, 0, 0,
                 *_lib.ws_args(ws), _lib.stream_ptr(dev),
             )
         elif m >= GEMM_MIN_M and k_slices is None:
@@ -312,13 +312,14 @@ def int4_linear_tiled(x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, k_sl
 
 
 def int4_linear_skinny(
-    x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, *, tiles: int = 0, waves: int = -1, splits: int = 0
+    x: Tensor, tw: Int4Tiled, bias: Tensor | None = None, *, variant: int = -1, tiles: int = 0, waves: int = 0,
+    splits: int = 0,
 ) -> Tensor:
     """``x @ W.T (+ bias)`` for 1..64 rows of ``x`` on the decode-regime kernels with an explicit
-    launch shape: ``tiles`` (1, 2 or 4) 16-row weight tiles per wave; ``waves`` 0 for the variant that
-    stages activations through LDS (4 waves, each with its own tiles), 1..8 for waves splitting K;
-    ``splits`` workgroups along K (fp32 partials added in split order). ``tiles``/``splits`` 0 and
-    ``waves`` -1 pick the library default. A given shape always gives the same bits."""
+    launch shape (``sqx_int4_skinny``): ``variant`` 0 = waves splitting K (``tiles`` 2 or 4 per wave,
+    ``waves`` 1..8), 1 = activations staged through LDS (``tiles`` 1, 2 or 4 per wave, ``waves`` 4 or
+    8 compute waves); ``splits`` workgroups along K (fp32 partials added in split order). -1 / 0
+    pick the library's choice. A given shape always gives the same bits."""
     *batch, k = x.shape
     if k != tw.cols:
         raise ValueError(f"x has in_features={k}, weight expects {tw.cols}")
@@ -339,8 +340,8 @@ def int4_linear_skinny(
     with torch.cuda.device(dev):
         rc = lib.sqx_int4_skinny(
             _lib.ptr(tw.wt), _lib.ptr(tw.st), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype), _lib.ptr(x2),
-            _lib.sqx_dtype(x.dtype), _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size, int(tiles),
-            int(waves), int(splits), *_lib.ws_args(ws), _lib.stream_ptr(dev),
+            _lib.sqx_dtype(x.dtype), _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size, int(variant),
+            int(tiles), int(waves), int(splits), *_lib.ws_args(ws), _lib.stream_ptr(dev),
         )
     _lib.check(rc, "int4_linear_skinny")
     return y.reshape(*batch, tw.rows)

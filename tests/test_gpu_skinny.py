@@ -41,11 +41,14 @@ def _sym(q4, n, k, group, seed, std=0.05):
     return q4.tile_int4(q, s, None, group), w_eff
 
 
-SHAPES = [(2, 1, 1), (4, 1, 1), (2, 8, 1), (4, 8, 1), (2, 3, 2), (4, 4, 3), (2, 8, 4), (4, 2, 7),
-          (1, 0, 1), (2, 0, 1), (4, 0, 1), (1, 0, 3), (2, 0, 2), (4, 0, 4)]  # (tiles, waves, splits)
+SHAPES = [  # (variant, tiles, waves, splits): 0 = waves splitting K, 1 = LDS-staged (4 or 8 compute waves)
+    (0, 2, 1, 1), (0, 4, 1, 1), (0, 2, 8, 1), (0, 4, 8, 1), (0, 2, 3, 2), (0, 4, 4, 3), (0, 2, 8, 4), (0, 4, 2, 7),
+    (1, 1, 4, 1), (1, 2, 4, 1), (1, 4, 4, 1), (1, 1, 4, 3), (1, 2, 4, 2), (1, 4, 4, 4),
+    (1, 1, 8, 1), (1, 2, 8, 1), (1, 4, 8, 2), (1, 2, 8, 3),
+]
 
 
-@pytest.mark.parametrize("tiles,waves,splits", SHAPES, ids=lambda v: str(v))
+@pytest.mark.parametrize("variant,tiles,waves,splits", SHAPES, ids=lambda v: str(v))
 @pytest.mark.parametrize(
     "n,k,group,m",
     [
@@ -57,14 +60,14 @@ SHAPES = [(2, 1, 1), (4, 1, 1), (2, 8, 1), (4, 8, 1), (2, 3, 2), (4, 4, 3), (2, 
         (96, 2048, 128, 1),
     ],
 )
-def test_skinny_matches_oracle(q4, n, k, group, m, tiles, waves, splits):
-    print_case("skinny", n, k, group, m, tiles, waves, splits)
+def test_skinny_matches_oracle(q4, n, k, group, m, variant, tiles, waves, splits):
+    print_case("skinny", n, k, group, m, variant, tiles, waves, splits)
     tw, w_eff = _sym(q4, n, k, group, n + k + m)
     x = _act(m, k, 3 * m + k).to(DEV)
-    y = q4.int4_linear_skinny(x, tw, tiles=tiles, waves=waves, splits=splits)
+    y = q4.int4_linear_skinny(x, tw, variant=variant, tiles=tiles, waves=waves, splits=splits)
     torch.cuda.synchronize()
     _check_linear(y, R.linear_f64(x.float().cpu().numpy(), w_eff), f"{k}->{n} g{group} M={m}")
-    again = q4.int4_linear_skinny(x, tw, tiles=tiles, waves=waves, splits=splits)
+    again = q4.int4_linear_skinny(x, tw, variant=variant, tiles=tiles, waves=waves, splits=splits)
     assert torch.equal(y, again)  # fixed-order sums
 
 
@@ -91,12 +94,12 @@ def test_skinny_asymmetric_fp16_bias(q4):
         for dt, rnd in ((torch.bfloat16, "bf16"), (torch.float16, "f16")):
             x = _act(40, k, group, dtype=dt).to(DEV)
             bias = torch.randn(n, dtype=dt, device=DEV)
-            for tiles, waves, splits in ((2, 4, 1), (4, 2, 2), (1, 0, 1), (4, 0, 2)):
-                print_case("skinny asym", group, param, dt, tiles, waves, splits)
-                y = q4.int4_linear_skinny(x, tw, bias, tiles=tiles, waves=waves, splits=splits)
+            for variant, tiles, waves, splits in ((0, 2, 4, 1), (0, 4, 2, 2), (1, 1, 4, 1), (1, 4, 4, 2), (1, 2, 8, 1)):
+                print_case("skinny asym", group, param, dt, variant, tiles, waves, splits)
+                y = q4.int4_linear_skinny(x, tw, bias, variant=variant, tiles=tiles, waves=waves, splits=splits)
                 assert y.dtype == dt
                 y_ref = R.linear_f64(x.float().cpu().numpy(), R.round_to(w_eff, rnd), bias.float().cpu().numpy())
-                _check_linear(y, y_ref, f"asym g{group} {param} {dt} {tiles},{waves},{splits}")
+                _check_linear(y, y_ref, f"asym g{group} {param} {dt} {variant},{tiles},{waves},{splits}")
 
 
 def test_skinny_zero_row_is_bias_and_shapes_agree(q4):
@@ -107,7 +110,7 @@ def test_skinny_zero_row_is_bias_and_shapes_agree(q4):
     tw = q4.tile_int4(q, s)
     x = _act(m, k, 6).to(DEV)
     bias = torch.randn(n, dtype=torch.bfloat16, device=DEV)
-    outs = [q4.int4_linear_skinny(x, tw, bias, tiles=r, waves=wv, splits=sp) for r, wv, sp in SHAPES]
+    outs = [q4.int4_linear_skinny(x, tw, bias, variant=v, tiles=r, waves=wv, splits=sp) for v, r, wv, sp in SHAPES]
     for y in outs:
         assert torch.equal(y[:, 9], bias[9].expand(m))
     ref = outs[0].float()
@@ -130,13 +133,16 @@ def test_skinny_rejects(q4):
     args = (tw.wt.data_ptr(), tw.st.data_ptr(), None, _lib.sqx_dtype(tw.st.dtype), x.data_ptr(),
             _lib.sqx_dtype(x.dtype), y.data_ptr(), None, 8, 64, 256, 128)
     st = torch.cuda.current_stream().cuda_stream
-    assert lib.sqx_int4_skinny(*args, 3, 0, 1, None, 0, st) == E_ARG  # tiles 1, 2 or 4
+    assert lib.sqx_int4_skinny(*args, 1, 3, 4, 1, None, 0, st) == E_ARG  # tiles 1, 2 or 4
     assert "bad launch shape" in lib.sqx_last_error().decode()
-    assert lib.sqx_int4_skinny(*args, 1, 2, 1, None, 0, st) == E_ARG  # waves splitting K: tiles 2 or 4
-    assert lib.sqx_int4_skinny(*args, 2, 9, 1, None, 0, st) == E_ARG  # waves <= 8
-    assert lib.sqx_int4_skinny(*args, 2, 1, 2, None, 0, st) == E_ARG  # splits need a workspace
+    assert lib.sqx_int4_skinny(*args, 0, 1, 2, 1, None, 0, st) == E_ARG  # waves splitting K: tiles 2 or 4
+    assert lib.sqx_int4_skinny(*args, 0, 2, 9, 1, None, 0, st) == E_ARG  # waves <= 8
+    assert lib.sqx_int4_skinny(*args, 1, 2, 6, 1, None, 0, st) == E_ARG  # LDS-staged: 4 or 8 compute waves
+    assert lib.sqx_int4_skinny(*args, 2, 2, 4, 1, None, 0, st) == E_ARG  # no variant 2
+    assert lib.sqx_int4_skinny(*args, 0, 2, 1, 2, None, 0, st) == E_ARG  # splits need a workspace
     assert "workspace" in lib.sqx_last_error().decode()
     assert lib.sqx_int4_skinny_workspace_bytes(8, 64, 256, 2) == 2 * 8 * 64 * 4
     assert lib.sqx_int4_skinny_workspace_bytes(8, 64, 256, 1) == 0
-    assert lib.sqx_int4_skinny(*args, 2, 1, 1, None, 0, st) == 0
+    assert lib.sqx_int4_skinny(*args, 0, 2, 1, 1, None, 0, st) == 0
+    assert lib.sqx_int4_skinny(*args, 1, 1, 8, 1, None, 0, st) == 0
     torch.cuda.synchronize()
