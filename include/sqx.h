@@ -283,12 +283,28 @@ int sqx_mxfp4_quantize_tiled(const void* x, int dtype, int64_t m, int64_t k, uin
  * X = mxfp4_dequantize of the tiled activations (xt, xst from sqx_mxfp4_quantize_tiled) and W of the
  * tiled weight (wt, st from sqx_fp4_tile with MXFP4 scales). Replaces the config-4 composition
  * F.linear(mxfp4_dequantize(mxfp4_quantize(x)), mxfp4_dequantize(W)) (nvfp4_mxfp4.py:257-272 with
- * F.linear) and is the SURVEY's sqx_mxfp4_gemm export with act_fmt = MXFP4. fp32 accumulation;
- * y [m, rows] of y_dtype (BF16, F16 or F32); bias (NULL or [rows] of y_dtype, not with F32). */
+ * F.linear); this is the mxfp4 GEMM export with act_fmt = MXFP4. fp32 accumulation;
+ * y [m, rows] of y_dtype (BF16, F16 or F32); bias (NULL or [rows] of y_dtype, not with F32).
+ * One pass per 256 x 256 output tile: for few output tiles (small m) use sqx_mxfp4_gemm_ws. */
 int sqx_mxfp4_gemm(const uint8_t* xt, const uint8_t* xst, const uint8_t* wt, const uint8_t* wst, void* y,
                    int y_dtype, const void* bias, int64_t m, int64_t rows, int64_t cols, sqx_stream_t stream);
 
-/* Prefill / large-batch W4A16 GEMM (SURVEY's sqx_int4_gemm): the same operation and tiled weight as
+/* Workspace bytes sqx_mxfp4_gemm_ws needs for a shape and a number of K splits (splits <= 0: the
+ * automatic choice; 0 bytes when that is one split). */
+int64_t sqx_mxfp4_gemm_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int splits);
+
+/* sqx_mxfp4_gemm with the k range split over `splits` workgroups per output tile (1..16; <= 0: the
+ * automatic choice, which splits when the output tiles leave CUs idle and falls back to one pass when
+ * ws is NULL or too small). Each split writes fp32 partial sums to ws ([splits][m][rows], 16-byte
+ * aligned); a second kernel adds them in split order, adds the bias and rounds to y_dtype, so the
+ * result is deterministic for a given shape and split count and differs from the one-pass result
+ * only by the order of the fp32 additions. An explicit split count that leaves a split empty is
+ * refused (SQX_E_ARG); a workspace smaller than it needs returns SQX_E_SPACE. */
+int sqx_mxfp4_gemm_ws(const uint8_t* xt, const uint8_t* xst, const uint8_t* wt, const uint8_t* wst, void* y,
+                      int y_dtype, const void* bias, int64_t m, int64_t rows, int64_t cols, int splits, void* ws,
+                      int64_t ws_bytes, sqx_stream_t stream);
+
+/* Prefill / large-batch W4A16 GEMM (the int4 GEMM export): the same operation and tiled weight as
  * sqx_int4_linear (w4a16_linear, int4_group.py:148-164, and the AWQ linear awq.py:184-192 on x / s),
  * for any m, on the bf16 / fp16 MFMA with the weight tile decoded in registers to the reference's
  * bf16(fp32((q - z) * s)). group: 32, 64 or 128; cols a multiple of 32 and of group. y [m, rows] in
@@ -303,8 +319,8 @@ int sqx_int4_gemm(const uint8_t* wt, const void* st, const void* zt, int param_d
  * smaller workspace runs without the split (same result, slower for small m). */
 int64_t sqx_gemm_workspace_bytes(int64_t m, int64_t rows, int64_t cols);
 
-/* Prefill / large-batch FP4-weight GEMM with BF16 / F16 activations (SURVEY's sqx_mxfp4_gemm with
- * act_fmt = bf16, and sqx_nvfp4_gemm): the same operation and tiled weight as sqx_fp4_linear (the
+/* Prefill / large-batch FP4-weight GEMM with BF16 / F16 activations (the mxfp4 GEMM export with
+ * act_fmt = bf16, and the nvfp4 GEMM): the same operation and tiled weight as sqx_fp4_linear (the
  * config-4 F.linear(x, mxfp4_dequantize(W).to(x.dtype)) and the NVFP4 linear) on the 16-bit MFMA,
  * each weight decoded in registers (MXFP4 exactly; NVFP4 as e2m1 * s_block with *s_global applied to
  * the fp32 result). cols a multiple of 32; y_dtype act_dtype or F32; bias as sqx_fp4_linear. */

@@ -84,6 +84,9 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "sqx_mxfp4_quantize_tiled": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "sqx_mxfp4_gemm": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_p]),
+    "sqx_mxfp4_gemm_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i]),
+    "sqx_mxfp4_gemm_ws": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_i, _c_p, _c_i64,
+                                 _c_p]),
     "sqx_gemm_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "sqx_int4_gemm": (
         _c_i,

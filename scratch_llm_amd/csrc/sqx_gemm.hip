@@ -92,8 +92,9 @@ __global__ __launch_bounds__(128 * WN) void mxfp4_gemm_kernel(const uint8_t* __r
                                                         const uint8_t* __restrict__ xst,
                                                         const uint8_t* __restrict__ wt,
                                                         const uint8_t* __restrict__ wst, void* __restrict__ y,
-                                                        const uint16_t* __restrict__ bias, int m, int n, int KB,
-                                                        int tiles_m, int tiles_n, int vec, int lds16) {
+                                                        const uint16_t* __restrict__ bias, int m, int n, int KBall,
+                                                        int tiles_m, int tiles_n, int vec, int lds16, int kps,
+                                                        int64_t split_stride) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int NW = 2 * WN;              // waves
   constexpr int CT = 8 / WN;              // 32-column MFMA tiles per wave
@@ -104,10 +105,15 @@ __global__ __launch_bounds__(128 * WN) void mxfp4_gemm_kernel(const uint8_t* __r
   mx_tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
 
   const int xT = (m + 15) >> 4, wT = (n + 15) >> 4;  // 16-row tiles of each operand
-  const rsrc_t xr = make_rsrc(xt, (uint32_t)xT * (uint32_t)KB * 1024u);
-  const rsrc_t xsr = make_rsrc(xst, (uint32_t)xT * (uint32_t)KB * 64u);
-  const rsrc_t wr = make_rsrc(wt, (uint32_t)wT * (uint32_t)KB * 1024u);
-  const rsrc_t wsr = make_rsrc(wst, (uint32_t)wT * (uint32_t)KB * 64u);
+  const rsrc_t xr = make_rsrc(xt, (uint32_t)xT * (uint32_t)KBall * 1024u);
+  const rsrc_t xsr = make_rsrc(xst, (uint32_t)xT * (uint32_t)KBall * 64u);
+  const rsrc_t wr = make_rsrc(wt, (uint32_t)wT * (uint32_t)KBall * 1024u);
+  const rsrc_t wsr = make_rsrc(wst, (uint32_t)wT * (uint32_t)KBall * 64u);
+  // K split: workgroups with blockIdx.y = j take k-steps [j*kps, (j+1)*kps) and write fp32 partials
+  // at y + j*split_stride (YKIND 2)
+  const int kbeg = blockIdx.y * kps;
+  const int KB = min(KBall, kbeg + kps) - kbeg;
+  if (YKIND == 2) y = static_cast<float*>(y) + (int64_t)blockIdx.y * split_stride;
   const int x_t0 = tm * mxg::kFrags, w_t0 = tn * mxg::kFrags;
 
   f32x16_t acc[4][CT];
@@ -163,7 +169,8 @@ __global__ __launch_bounds__(128 * WN) void mxfp4_gemm_kernel(const uint8_t* __r
 #pragma unroll
   for (int s = 0; s < NSTAGE - 1; ++s)
     if (s < KB)
-      mx_issue_step<NW>(smem + s * mxg::kStage, wave, lane, s, KB, xr, xsr, wr, wsr, x_t0, xT - 1, w_t0, wT - 1);
+      mx_issue_step<NW>(smem + s * mxg::kStage, wave, lane, kbeg + s, KBall, xr, xsr, wr, wsr, x_t0, xT - 1, w_t0,
+                        wT - 1);
   if (KB - 1 >= NSTAGE - 2) wait_vmcnt<kPerStep * (NSTAGE - 2)>();  // step 0 landed for this wave ...
   else wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();  // ... and for every wave
@@ -180,7 +187,8 @@ __global__ __launch_bounds__(128 * WN) void mxfp4_gemm_kernel(const uint8_t* __r
     wait_vmcnt<kPerStep * (NSTAGE - 3)>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    mx_issue_step<NW>(smem + ((kb + NSTAGE - 1) % NSTAGE) * mxg::kStage, wave, lane, kb + NSTAGE - 1, KB, xr, xsr, wr,
+    mx_issue_step<NW>(smem + ((kb + NSTAGE - 1) % NSTAGE) * mxg::kStage, wave, lane, kbeg + kb + NSTAGE - 1, KBall, xr,
+                      xsr, wr,
                   wsr, x_t0, xT - 1, w_t0, wT - 1);
     read_ops(smem + ((kb + 1) % NSTAGE) * mxg::kStage, 0, o0);
     mma(o1);
@@ -689,55 +697,134 @@ using namespace sqx;
 namespace {
 constexpr int kMxStages = 4;
 
+// K splits of the MXFP4 GEMM for a shape, from a cost model fitted to measurements of 128..512-row
+// products at Llama shapes. One 256 x 256 workgroup fills a CU (its four operand stages take 136 KiB
+// of LDS), so S splits run in ceil(tiles * S / 256) rounds of ceil(KB / S) k-steps. A k-step takes
+// about 0.7 us with the chip nearly idle and 1.25 us with every CU loading (HBM shared); each split
+// adds an fp32 partial of the output, written once and read back once (8 bytes per output element
+// at about 5 TB/s). S minimises the sum, at most 16.
+int mx_splits(int64_t m, int64_t rows, int64_t cols) {
+  const int64_t tiles = ceil_div(m, mxg::kTile) * ceil_div(rows, mxg::kTile), KB = ceil_div(cols, 128);
+  int best = 1;
+  double best_us = 0.0;
+  for (int S = 1; S <= 16 && S <= KB; ++S) {
+    const int64_t per = ceil_div(KB, S);
+    if (ceil_div(KB, per) != S) continue;  // the last split would be empty
+    const int64_t wgs = tiles * S, rounds = ceil_div(wgs, 256);
+    const double busy = rounds > 1 ? 1.0 : (double)wgs / 256.0;
+    double us = (double)rounds * (double)per * (0.7 + 0.55 * busy);
+    if (S > 1) us += (double)S * (double)m * (double)rows * 8.0 / 5e6;
+    if (S == 1 || us < best_us) best = S, best_us = us;
+  }
+  return best;
+}
+
+// splits > 1: fp32 partials into ws ([splits][m][n], 16-byte aligned, checked by the caller), then
+// the in-order reduce adds the splits and the bias and rounds to y's dtype.
 template <int YK>
 hipError_t launch_mx(const uint8_t* xt, const uint8_t* xst, const uint8_t* wt, const uint8_t* wst, void* y,
-                     const uint16_t* bias, int m, int n, int KB, hipStream_t s) {
+                     const uint16_t* bias, int m, int n, int KB, int splits, float* ws, hipStream_t s) {
   const int tiles_m = (m + mxg::kTile - 1) / mxg::kTile, tiles_n = (n + mxg::kTile - 1) / mxg::kTile;
   const size_t lds = (size_t)kMxStages * mxg::kStage;
-  auto kern = mxfp4_gemm_kernel<kMxStages, YK, SQX_MX_WN>;
+  const int kps = (KB + splits - 1) / splits;
+  auto kern = splits > 1 ? mxfp4_gemm_kernel<kMxStages, 2, SQX_MX_WN> : mxfp4_gemm_kernel<kMxStages, YK, SQX_MX_WN>;
   // more than 64 KiB of dynamic LDS has to be allowed per kernel
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)lds);
   if (e != hipSuccess) return e;
+  void* out = splits > 1 ? static_cast<void*>(ws) : y;
   // four-column vector stores need every row start aligned to the store width
-  const int esize = YK == 2 ? 4 : 2;
-  const int vec = (n % 4 == 0) && (reinterpret_cast<uintptr_t>(y) % (4 * esize) == 0);
+  const int esize = (YK == 2 || splits > 1) ? 4 : 2;
+  const int vec = (n % 4 == 0) && (reinterpret_cast<uintptr_t>(out) % (4 * esize) == 0);
   // the LDS-staged 16-bit epilogue stores 8 columns (16 bytes) per lane
-  const int lds16 = YK != 2 && (n % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
-  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n)), dim3(128 * SQX_MX_WN), lds, s, xt, xst, wt, wst, y, bias, m, n,
-                     KB, tiles_m, tiles_n, vec, lds16);
+  const int lds16 = YK != 2 && splits == 1 && (n % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n), (unsigned)splits), dim3(128 * SQX_MX_WN), lds, s, xt,
+                     xst, wt, wst, out, splits > 1 ? nullptr : bias, m, n, KB, tiles_m, tiles_n, vec, lds16, kps,
+                     (int64_t)m * n);
+  if (splits > 1) {
+    const int64_t mn = (int64_t)m * n;
+    hipLaunchKernelGGL(dq_reduce_kernel<YK>, dim3((unsigned)ceil_div(mn, 256)), dim3(256), 0, s, ws, splits, mn, n,
+                       nullptr, bias, y);
+  }
   return hipGetLastError();
+}
+
+int mx_check(const char* fn, const uint8_t* xt, const uint8_t* xst, const uint8_t* wt, const uint8_t* wst,
+             const void* y, int y_dtype, const void* bias, int64_t m, int64_t rows, int64_t cols) {
+  SQX_REQUIRE(m >= 0 && rows > 0 && cols > 0 && cols % 32 == 0, SQX_E_ARG,
+              "%s: bad shape m=%lld rows=%lld cols=%lld (cols must be a multiple of 32)", fn, (long long)m,
+              (long long)rows, (long long)cols);
+  SQX_REQUIRE(y_dtype == SQX_DTYPE_BF16 || y_dtype == SQX_DTYPE_F16 || y_dtype == SQX_DTYPE_F32, SQX_E_ARG,
+              "%s: bad y_dtype %d", fn, y_dtype);
+  SQX_REQUIRE(bias == nullptr || y_dtype != SQX_DTYPE_F32, SQX_E_ARG, "%s: bias is BF16/F16 and needs y of that dtype",
+              fn);
+  const int64_t KB = ceil_div(cols, 128);
+  SQX_REQUIRE(ceil_div(m, 16) * KB * 1024 < ((int64_t)1 << 31) && ceil_div(rows, 16) * KB * 1024 < ((int64_t)1 << 31),
+              SQX_E_ARG, "%s: tiled operand beyond 2 GiB (32-bit buffer offsets)", fn);
+  SQX_REQUIRE(m * rows < ((int64_t)1 << 62) && ceil_div(m, 256) * ceil_div(rows, 256) < ((int64_t)1 << 31), SQX_E_ARG,
+              "%s: too many output tiles", fn);
+  if (m == 0) return SQX_OK;
+  SQX_REQUIRE(xt && xst && wt && wst && y, SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(xt) % 16 == 0 && reinterpret_cast<uintptr_t>(wt) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(xst) % 4 == 0 && reinterpret_cast<uintptr_t>(wst) % 4 == 0,
+              SQX_E_ARG, "%s: tiled codes must be 16-byte and scales 4-byte aligned", fn);
+  return SQX_OK;
+}
+
+int mx_run(const char* fn, const uint8_t* xt, const uint8_t* xst, const uint8_t* wt, const uint8_t* wst, void* y,
+           int y_dtype, const void* bias, int64_t m, int64_t rows, int64_t cols, int splits, float* ws,
+           hipStream_t s) {
+  const uint16_t* b16 = static_cast<const uint16_t*>(bias);
+  const int KB = (int)ceil_div(cols, 128);
+  hipError_t e;
+  if (y_dtype == SQX_DTYPE_BF16) e = launch_mx<0>(xt, xst, wt, wst, y, b16, (int)m, (int)rows, KB, splits, ws, s);
+  else if (y_dtype == SQX_DTYPE_F16) e = launch_mx<1>(xt, xst, wt, wst, y, b16, (int)m, (int)rows, KB, splits, ws, s);
+  else e = launch_mx<2>(xt, xst, wt, wst, y, b16, (int)m, (int)rows, KB, splits, ws, s);
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
 }
 }  // namespace
 
 extern "C" int sqx_mxfp4_gemm(const uint8_t* xt, const uint8_t* xst, const uint8_t* wt, const uint8_t* wst, void* y,
                               int y_dtype, const void* bias, int64_t m, int64_t rows, int64_t cols,
                               sqx_stream_t stream) {
-  SQX_REQUIRE(m >= 0 && rows > 0 && cols > 0 && cols % 32 == 0, SQX_E_ARG,
-              "sqx_mxfp4_gemm: bad shape m=%lld rows=%lld cols=%lld (cols must be a multiple of 32)", (long long)m,
-              (long long)rows, (long long)cols);
-  SQX_REQUIRE(y_dtype == SQX_DTYPE_BF16 || y_dtype == SQX_DTYPE_F16 || y_dtype == SQX_DTYPE_F32, SQX_E_ARG,
-              "sqx_mxfp4_gemm: bad y_dtype %d", y_dtype);
-  SQX_REQUIRE(bias == nullptr || y_dtype != SQX_DTYPE_F32, SQX_E_ARG,
-              "sqx_mxfp4_gemm: bias is BF16/F16 and needs y of that dtype");
-  const int64_t KB = ceil_div(cols, 128);
-  SQX_REQUIRE(ceil_div(m, 16) * KB * 1024 < ((int64_t)1 << 31) && ceil_div(rows, 16) * KB * 1024 < ((int64_t)1 << 31),
-              SQX_E_ARG, "sqx_mxfp4_gemm: tiled operand beyond 2 GiB (32-bit buffer offsets)");
-  SQX_REQUIRE(m * rows < ((int64_t)1 << 62) && ceil_div(m, 256) * ceil_div(rows, 256) < ((int64_t)1 << 31), SQX_E_ARG,
-              "sqx_mxfp4_gemm: too many output tiles");
+  if (int rc = mx_check("sqx_mxfp4_gemm", xt, xst, wt, wst, y, y_dtype, bias, m, rows, cols)) return rc;
   if (m == 0) return SQX_OK;
-  SQX_REQUIRE(xt && xst && wt && wst && y, SQX_E_ARG, "sqx_mxfp4_gemm: null pointer");
-  SQX_REQUIRE(reinterpret_cast<uintptr_t>(xt) % 16 == 0 && reinterpret_cast<uintptr_t>(wt) % 16 == 0 &&
-                  reinterpret_cast<uintptr_t>(xst) % 4 == 0 && reinterpret_cast<uintptr_t>(wst) % 4 == 0,
-              SQX_E_ARG, "sqx_mxfp4_gemm: tiled codes must be 16-byte and scales 4-byte aligned");
-  hipStream_t s = as_stream(stream);
-  const uint16_t* b16 = static_cast<const uint16_t*>(bias);
-  hipError_t e;
-  if (y_dtype == SQX_DTYPE_BF16) e = launch_mx<0>(xt, xst, wt, wst, y, b16, (int)m, (int)rows, (int)KB, s);
-  else if (y_dtype == SQX_DTYPE_F16) e = launch_mx<1>(xt, xst, wt, wst, y, b16, (int)m, (int)rows, (int)KB, s);
-  else e = launch_mx<2>(xt, xst, wt, wst, y, b16, (int)m, (int)rows, (int)KB, s);
-  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "sqx_mxfp4_gemm: launch failed: %s", hipGetErrorString(e));
-  return SQX_OK;
+  return mx_run("sqx_mxfp4_gemm", xt, xst, wt, wst, y, y_dtype, bias, m, rows, cols, 1, nullptr, as_stream(stream));
+}
+
+extern "C" int64_t sqx_mxfp4_gemm_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int splits) {
+  if (m <= 0 || rows <= 0 || cols <= 0) return 0;
+  const int sp = splits > 0 ? splits : mx_splits(m, rows, cols);
+  return sp > 1 ? (int64_t)sp * m * rows * 4 : 0;
+}
+
+extern "C" int sqx_mxfp4_gemm_ws(const uint8_t* xt, const uint8_t* xst, const uint8_t* wt, const uint8_t* wst, void* y,
+                                 int y_dtype, const void* bias, int64_t m, int64_t rows, int64_t cols, int splits,
+                                 void* ws, int64_t ws_bytes, sqx_stream_t stream) {
+  const char* fn = "sqx_mxfp4_gemm_ws";
+  if (int rc = mx_check(fn, xt, xst, wt, wst, y, y_dtype, bias, m, rows, cols)) return rc;
+  const int64_t KB = ceil_div(cols, 128);
+  SQX_REQUIRE(splits <= 16, SQX_E_ARG, "%s: splits %d above 16", fn, splits);
+  if (m == 0) return SQX_OK;
+  int sp = splits;
+  if (sp <= 0) {  // automatic: without a large enough workspace, one pass per tile
+    sp = mx_splits(m, rows, cols);
+    if (sp > 1 && (ws == nullptr || ws_bytes < (int64_t)sp * m * rows * 4 || reinterpret_cast<uintptr_t>(ws) % 16))
+      sp = 1;
+  } else {
+    SQX_REQUIRE(ceil_div(KB, ceil_div(KB, sp)) == sp, SQX_E_ARG,
+                "%s: %d splits of %lld k-steps of 128 columns would leave one empty", fn, sp, (long long)KB);
+    if (sp > 1) {
+      SQX_REQUIRE(ws && reinterpret_cast<uintptr_t>(ws) % 16 == 0, SQX_E_ARG,
+                  "%s: splits > 1 need a 16-byte aligned workspace", fn);
+      SQX_REQUIRE(ws_bytes >= (int64_t)sp * m * rows * 4, SQX_E_SPACE, "%s: workspace of %lld bytes, %lld needed", fn,
+                  (long long)ws_bytes, (long long)sp * m * rows * 4);
+    }
+  }
+  SQX_REQUIRE(sp == 1 || (int64_t)sp * m * rows < ((int64_t)1 << 40), SQX_E_ARG, "%s: workspace too large", fn);
+  return mx_run(fn, xt, xst, wt, wst, y, y_dtype, bias, m, rows, cols, sp, static_cast<float*>(ws),
+                as_stream(stream));
 }
 
 namespace {

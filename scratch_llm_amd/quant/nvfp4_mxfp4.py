@@ -461,10 +461,14 @@ def mxfp4_quantize_tiled(x: Tensor) -> FP4Tiled:
 
 
 def mxfp4_gemm(xq: FP4Tiled, tw: FP4Tiled, bias: Tensor | None = None,
-               out_dtype: torch.dtype = torch.bfloat16) -> Tensor:
+               out_dtype: torch.dtype = torch.bfloat16, *, splits: int = 0) -> Tensor:
     """``X @ W.T (+ bias)`` for tiled MXFP4 activations ``xq`` ``[m, k]`` and a tiled MXFP4 weight
     ``tw`` ``[n, k]`` on the block-scaled fp4 MFMA (fp32 accumulation), ``[m, n]`` in ``out_dtype``
-    (bf16, fp16 or fp32; a bias needs bf16 or fp16)."""
+    (bf16, fp16 or fp32; a bias needs bf16 or fp16).
+
+    ``splits`` > 1 splits the k range over that many workgroups per output tile, through an fp32
+    workspace summed in split order (deterministic); 0 lets the library choose (it splits when the
+    output tiles would leave CUs idle, i.e. small ``m``)."""
     if xq.fmt != _lib.FP4_MX or tw.fmt != _lib.FP4_MX:
         raise ValueError("mxfp4_gemm takes MXFP4 operands on both sides")
     if xq.cols != tw.cols:
@@ -477,10 +481,12 @@ def mxfp4_gemm(xq: FP4Tiled, tw: FP4Tiled, bias: Tensor | None = None,
     b = None if bias is None else bias.to(out_dtype).contiguous()
     y = torch.empty(xq.rows, tw.rows, dtype=out_dtype, device=dev)
     lib = _lib.load()
+    nws = lib.sqx_mxfp4_gemm_workspace_bytes(xq.rows, tw.rows, tw.cols, int(splits))
+    ws = torch.empty(nws, dtype=torch.uint8, device=dev) if nws > 0 else None
     with torch.cuda.device(dev):
-        _lib.check(lib.sqx_mxfp4_gemm(xq.wt.data_ptr(), xq.st.data_ptr(), tw.wt.data_ptr(), tw.st.data_ptr(), y.data_ptr(),
-                                      _lib.sqx_dtype(out_dtype), _lib.ptr(b), xq.rows, tw.rows, tw.cols, _stream(y)),
-                   "mxfp4_gemm")
+        _lib.check(lib.sqx_mxfp4_gemm_ws(xq.wt.data_ptr(), xq.st.data_ptr(), tw.wt.data_ptr(), tw.st.data_ptr(),
+                                         y.data_ptr(), _lib.sqx_dtype(out_dtype), _lib.ptr(b), xq.rows, tw.rows,
+                                         tw.cols, int(splits), _lib.ptr(ws), nws, _stream(y)), "mxfp4_gemm")
     return y
 
 

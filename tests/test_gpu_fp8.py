@@ -1,4 +1,4 @@
-"""FP8 E4M3 on the MI355X (SURVEY row: fp8_weights.py W8A8 and fp8_kv_per_head.py quantizers): codes,
+"""FP8 E4M3 on the MI355X (fp8_weights.py W8A8 and fp8_kv_per_head.py quantizers): codes,
 scales and counts bit-exact against the numpy oracle (oracle/fp8_ref.py); the W8A8 linear against
 the float64 oracle within the reference's own derived bound (tests/quant/test_s1_s_r2.py:510-539):
 

@@ -103,11 +103,12 @@ def test_mxfp4_quantize_tiled_matches_tile_of_quantize(f4):
 
 
 def _check_gemm(y: torch.Tensor, y_ref: np.ndarray, mag: np.ndarray, out_dtype: torch.dtype, what: str,
-                k: int) -> None:
+                k: int, splits: int = 1) -> None:
+    """``splits`` K splits add one fp32 rounding each when their partials are summed."""
     yv = y.float().cpu().numpy().astype(np.float64)
     assert np.isfinite(yv).all(), f"{what}: non-finite output"
     err = np.abs(yv - y_ref)
-    acc_bound = (k / 32 + 8) * 2.0**-24 * mag + 1e-30
+    acc_bound = (k / 32 + 8 + splits) * 2.0**-24 * mag + 1e-30
     if out_dtype == torch.float32:
         worst = float((err / acc_bound).max())
         assert worst <= 1.0, f"{what}: fp32 output off by {worst:.2f}x the accumulation bound"
@@ -153,7 +154,95 @@ def test_mxfp4_gemm_matches_oracle(f4, m, n, k):
             continue
         y = f4.mxfp4_gemm(xq, tw, out_dtype=out_dtype)
         torch.cuda.synchronize()
-        _check_gemm(y, y_ref, mag, out_dtype, f"mxfp4_gemm {m}x{n}x{k} {out_dtype}", k)
+        _check_gemm(y, y_ref, mag, out_dtype, f"mxfp4_gemm {m}x{n}x{k} {out_dtype}", k, splits=16)
+
+
+SPLIT_SHAPES = [  # (m, n, k, splits): k-steps of 128 columns per split down to one, ragged last split
+    (40, 300, 1024, 2),  # two splits of four k-steps
+    (64, 1000, 1056, 3),  # KB = 9: splits of 3, the last with a 32-column block
+    (17, 520, 2048, 4),  # KB = 16: 4+4+4+4 (5 would leave one empty: see the rejects test)
+    (128, 512, 4096, 8),  # 8 splits of 4 steps
+    (300, 260, 1024, 8),  # one k-step per split (shorter than the pipeline), ragged m and n
+    (1, 64, 2048, 16),  # sixteen splits of one step, one row
+]
+
+
+@pytest.mark.parametrize("m,n,k,splits", SPLIT_SHAPES)
+def test_mxfp4_gemm_split_k(f4, m, n, k, splits):
+    """K split into fp32 partials summed in order: within the accumulation bound of the oracle
+    product (one more rounding per split), deterministic, and equal to the one-pass result to fp32
+    rounding."""
+    from scratch_llm_amd import _lib
+
+    print_case("mxfp4_gemm split-K", f"m={m}", f"n={n}", f"k={k}", f"splits={splits}")
+    x = _values((m, k), 70 + m)
+    w = (np.random.default_rng(3 + n).standard_normal((n, k)) * 0.02).astype(np.float32)
+    _, _, xd = oracle_rows(x)
+    _, _, wd = oracle_rows(w)
+    b = np.random.default_rng(9).standard_normal(n).astype(np.float32)
+    xq = f4.mxfp4_quantize_tiled(_dev(x, torch.float32))
+    tw = f4.tile_fp4(f4.mxfp4_quantize(_dev(w, torch.float32), 32))
+    lib = _lib.load()
+    assert lib.sqx_mxfp4_gemm_workspace_bytes(m, n, k, splits) == splits * m * n * 4
+    for out_dtype in (torch.float32, torch.bfloat16):
+        bias = None if out_dtype == torch.float32 else _dev(b, torch.bfloat16)
+        bb = np.zeros(n) if bias is None else R.round_bf16(b).astype(np.float64)
+        y_ref = xd @ wd.T + bb[None, :]
+        mag = np.abs(xd) @ np.abs(wd).T + np.abs(bb)[None, :]
+        y = f4.mxfp4_gemm(xq, tw, bias, out_dtype=out_dtype, splits=splits)
+        again = f4.mxfp4_gemm(xq, tw, bias, out_dtype=out_dtype, splits=splits)
+        one = f4.mxfp4_gemm(xq, tw, bias, out_dtype=out_dtype, splits=1)
+        torch.cuda.synchronize()
+        _check_gemm(y, y_ref, mag, out_dtype, f"split {splits} {m}x{n}x{k} {out_dtype}", k, splits=splits)
+        assert torch.equal(y, again), "split-K result not deterministic"
+        if out_dtype == torch.float32:
+            d = (y - one).abs().double().cpu().numpy()
+            assert (d <= (2 * splits + 2) * 2.0**-24 * mag + 1e-30).all(), "split and one-pass differ beyond rounding"
+
+
+def test_mxfp4_gemm_one_pass_entry_point(f4):
+    """sqx_mxfp4_gemm (no workspace) is the one-split form of sqx_mxfp4_gemm_ws, bit for bit."""
+    from scratch_llm_amd import _lib
+
+    m, n, k = 96, 640, 2048
+    print_case("mxfp4_gemm one-pass entry", f"m={m}", f"n={n}", f"k={k}")
+    xq = f4.mxfp4_quantize_tiled(torch.randn(m, k, device=DEV))
+    tw = f4.tile_fp4(f4.mxfp4_quantize(torch.randn(n, k, device=DEV) * 0.02, 32))
+    bias = torch.randn(n, device=DEV, dtype=torch.bfloat16)
+    y = torch.empty(m, n, device=DEV, dtype=torch.bfloat16)
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.sqx_mxfp4_gemm(xq.wt.data_ptr(), xq.st.data_ptr(), tw.wt.data_ptr(), tw.st.data_ptr(), y.data_ptr(),
+                              _lib.sqx_dtype(torch.bfloat16), bias.data_ptr(), m, n, k, st) == 0
+    y1 = f4.mxfp4_gemm(xq, tw, bias, splits=1)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y1)
+
+
+def test_mxfp4_gemm_split_rejects(f4):
+    from scratch_llm_amd import _lib
+
+    m, n, k = 8, 64, 2048  # KB = 16
+    xq = f4.mxfp4_quantize_tiled(torch.randn(m, k, device=DEV))
+    tw = f4.tile_fp4(f4.mxfp4_quantize(torch.randn(n, k, device=DEV), 32))
+    y = torch.empty(m, n, device=DEV, dtype=torch.bfloat16)
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    ws = torch.empty(lib.sqx_mxfp4_gemm_workspace_bytes(m, n, k, 4), device=DEV, dtype=torch.uint8)
+    args = (xq.wt.data_ptr(), xq.st.data_ptr(), tw.wt.data_ptr(), tw.st.data_ptr(), y.data_ptr(),
+            _lib.sqx_dtype(torch.bfloat16), None, m, n, k)
+    assert lib.sqx_mxfp4_gemm_ws(*args, 5, ws.data_ptr(), ws.numel(), st) == -1  # 4+4+4+4+0: one empty
+    assert "empty" in lib.sqx_last_error().decode()
+    assert lib.sqx_mxfp4_gemm_ws(*args, 17, ws.data_ptr(), ws.numel(), st) == -1
+    assert lib.sqx_mxfp4_gemm_ws(*args, 4, None, 0, st) == -1
+    assert lib.sqx_mxfp4_gemm_ws(*args, 4, ws.data_ptr(), ws.numel() - 4, st) == -3  # SQX_E_SPACE
+    assert lib.sqx_mxfp4_gemm_ws(*args, 4, ws.data_ptr() + 4, ws.numel() - 4, st) == -1  # alignment
+    # automatic splitting without a workspace runs one pass
+    assert lib.sqx_mxfp4_gemm_ws(*args, 0, None, 0, st) == 0
+    y0 = y.clone()
+    assert lib.sqx_mxfp4_gemm_ws(*args, 1, None, 0, st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y, y0)
 
 
 def test_mxfp4_gemm_bias(f4):
@@ -193,11 +282,12 @@ def test_mxfp4_linear_quantized_activations(f4, m):
     _check_gemm(y.reshape(-1, n), y_ref, np.abs(xd) @ np.abs(wd).T, torch.bfloat16, "mxfp4_linear act-quant", k)
 
 
+@pytest.mark.parametrize("m", [4096, 128])
 @pytest.mark.parametrize("n,k", [(28672, 8192), (8192, 28672)])
-def test_mxfp4_gemm_config4_sampled(f4, n, k):
-    """Config 4 at full size (M = 4096): weights ~N(0, 0.02), activations ~N(0, 1) bf16, both
-    MXFP4; 24 rows x 160 columns of y against the oracle."""
-    m = 4096
+def test_mxfp4_gemm_config4_sampled(f4, n, k, m):
+    """Config 4 at full size (M = 4096, and M = 128, where the k range is split automatically):
+    weights ~N(0, 0.02), activations ~N(0, 1) bf16, both MXFP4; 24 rows x 160 columns of y against
+    the oracle."""
     print_case("mxfp4_gemm config4", f"m={m}", f"n={n}", f"k={k}")
     g = torch.Generator(device=DEV).manual_seed(1000 + n)
     w = torch.randn(n, k, generator=g, device=DEV) * 0.02
@@ -213,7 +303,7 @@ def test_mxfp4_gemm_config4_sampled(f4, n, k):
     _, _, wd = oracle_rows(w[torch.from_numpy(ci).to(DEV)].cpu().numpy())
     y_ref = xd @ wd.T
     ys = y[torch.from_numpy(ri).to(DEV)][:, torch.from_numpy(ci).to(DEV)]
-    _check_gemm(ys, y_ref, np.abs(xd) @ np.abs(wd).T, torch.bfloat16, f"config4 {m}x{n}x{k}", k)
+    _check_gemm(ys, y_ref, np.abs(xd) @ np.abs(wd).T, torch.bfloat16, f"config4 {m}x{n}x{k}", k, splits=16)
     del w, x, tw, xq, y
     torch.cuda.empty_cache()
 
