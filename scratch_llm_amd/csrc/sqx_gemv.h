@@ -14,6 +14,9 @@
 //                                  jg (= lane >> 4) feeds to MFMA step i (the B layout decides it)
 //   W::mma<A, MCH>(w, p, xv, yacc) the MFMAs of one block for MCH 16-row activation chunks
 //   W::out_scale(args, n)          factor applied to output column n (weight row n)
+//   W::kSumOffset, W::NG, W::mma_one<A>(w, p, xv, sig, y0)   (optional) formats whose codes carry
+//                                  an offset that costs sum(x) per group: the one-row form, given the
+//                                  activation sums sig[g] of the block's NG groups
 //
 // Structure (one workgroup per 16-row tile, all of K):
 //  * NW waves split the tile's k-blocks into contiguous slices (wave w owns [w*kbw, (w+1)*kbw));
@@ -24,6 +27,12 @@
 //    divided by a per-column scale) into LDS with full-width loads; MFMA A fragments are LDS reads and
 //    rows at or beyond M alias row M-1 (those outputs are dropped). Otherwise fragments are buffer
 //    loads (rows >= M read as zero) and KTAIL zeroes activation columns at or beyond K.
+//  * ONE (one activation row, formats with kSumOffset): the offset term of each group is
+//    -(offset) * sum(x over the group), so the activation sums are formed once per round of four
+//    blocks by one MFMA whose 16 A rows hold the round's 16 chunks of 32 activations (against a
+//    B of ones), instead of an MFMA chain per block against the constant offset. ONE = 2 also
+//    drops the workgroup's copy of the activations: each wave loads only its own k-slice (issued
+//    before its weights) into its own LDS area, so no workgroup barrier precedes the MFMAs.
 #pragma once
 
 #include <type_traits>
@@ -55,6 +64,19 @@ inline int gemv_default_kslices(int64_t rows, int64_t cols, int kblk = 128) {
 // Weight policies with a per-row (token) factor of the output declare `kRowScale = true` and
 // `row_scale(args, m)`; `rows_from(args, m0)` moves that factor's pointer to the pass starting at row m0.
 template <class W, class = void>
+struct has_sum_offset : std::false_type {};
+template <class W>
+struct has_sum_offset<W, std::void_t<decltype(W::kSumOffset)>> : std::integral_constant<bool, W::kSumOffset> {};
+// largest k-slice (in blocks) of a wave that loads its own activations (ONE = 2): four 16-byte loads a lane
+static constexpr int kOneMaxKbw = 16;
+template <class W, class = void>
+struct ng_of : std::integral_constant<int, 1> {};
+template <class W>
+struct ng_of<W, std::void_t<decltype(W::NG)>> : std::integral_constant<int, W::NG> {};
+template <class W>
+inline constexpr int kNgOf = ng_of<W>::value;
+
+template <class W, class = void>
 struct has_row_scale : std::false_type {};
 template <class W>
 struct has_row_scale<W, std::void_t<decltype(W::kRowScale)>> : std::integral_constant<bool, W::kRowScale> {};
@@ -76,12 +98,14 @@ struct ProArgs {
   float eps;
 };
 
-template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32, int PRO = kProPlain>
+template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32, int PRO = kProPlain, int ONE = 0>
 __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
                                                     void* __restrict__ yv, const uint16_t* __restrict__ bias,
                                                     const float* __restrict__ colscale, int M, int N, int K, int KB,
                                                     int kbw, const ProArgs pa) {
   static_assert(PRO == kProPlain || (XLDS && MCH == 1), "activation prologues need the LDS copy");
+  static_assert(ONE == 0 || (XLDS && MCH == 1 && U == 4), "the one-row form reads four-block rounds from LDS");
+  static_assert(ONE != 2 || PRO == kProPlain, "a prologue needs the workgroup's copy of the activations");
   extern __shared__ f32x4_t smem[];  // [NW][MCH][64] partial accumulators, then (XLDS) the activations
   f32x4_t* red = smem;
   const int lane = threadIdx.x & 63;
@@ -107,6 +131,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     xvo[c] = XLDS ? (uint32_t)(min(c * 16 + nl, M - 1) * xpitch) : ((uint32_t)(c * 16 + nl) * (uint32_t)K) * 2u;
   }
 
+  [[maybe_unused]] float y1 = 0.0f;  // ONE: the row's partial for this lane's weight row (lanes 0..15)
   u32x4_t w[U];
   typename W::P p[U];
   auto load_round = [&](int kr, u32x4_t (&wo)[U], typename W::P (&po)[U]) {
@@ -114,9 +139,34 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     for (int u = 0; u < U; ++u)
       if (kr + u < kb1) W::load(wc, kr + u, wo[u], po[u]);  // wave-uniform condition
   };
-  if (kb0 < kb1) load_round(kb0, w, p);
+  // ONE = 2: this wave's activations from column kb0*KBLK of the single row, nx loads of 16 bytes a
+  // lane (nx KiB, ceil(kbw*KBLK/512)), requested ahead of the weights. Every load and store of it is
+  // wave-uniform and the first weight round is unconditional (blocks past kb1 are clamped to kb1-1 and
+  // left unused), so the wait before the LDS store counts exactly the weight loads still in flight.
+  // Columns past the wave's slice read the next wave's activations (unused) or, past K, zero.
+  constexpr int kXw = ONE == 2 ? kOneMaxKbw * KBLK / 8 / 64 : 1;
+  const int nx = (kbw * (KBLK / 8) + 63) / 64;
+  u32x4_t xw[kXw];
+  uint16_t* xwave = xs + (ONE == 2 ? wave * nx * 512 : 0);  // this wave's LDS slice (ONE = 2)
+  if constexpr (ONE == 2) {
+#pragma unroll
+    for (int i = 0; i < kXw; ++i)
+      if (i < nx) xw[i] = bload128(xr, (uint32_t)(kb0 * KBLK + 8 * (lane + 64 * i)) * 2u, 0u);
+#pragma unroll
+    for (int u = 0; u < U; ++u) W::load(wc, min(kb0 + u, kb1 - 1), w[u], p[u]);
+  } else {
+    if (kb0 < kb1) load_round(kb0, w, p);
+  }
   // The first weight round is in flight while the activations are copied into LDS.
-  if constexpr (PRO == kProResNorm) {
+  if constexpr (ONE == 2) {
+#pragma unroll
+    for (int i = 0; i < kXw; ++i)
+      if (i < nx) *reinterpret_cast<u32x4_t*>(xwave + 8 * (lane + 64 * i)) = xw[i];
+    // LDS operations of one wave execute in issue order; only the compiler must not move the
+    // fragment reads above the stores
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+  } else if constexpr (PRO == kProResNorm) {
     // The 256 threads of the standalone kernel are emulated by "virtual threads" vt (in passes when
     // the workgroup is smaller; a workgroup is a whole number of waves, so a virtual wave is a real
     // one). Pass 1: h, its sum of squares per row, h -> LDS.
@@ -242,6 +292,31 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     u32x4_t wn[U];
     typename W::P pn[U];
     if (kb + U < kb1) load_round(kb + U, wn, pn);
+    // ONE: activation sums of the round's blocks. A row r = 4b + c of the MFMA holds chunk c (32
+    // columns) of block kb + b, so lane l receives the four chunk sums of block kb + (l >> 4).
+    [[maybe_unused]] float sig[U][ONE ? kNgOf<W> : 1];
+    if constexpr (ONE != 0) {
+      const int r = lane & 15, b = r >> 2;
+      const uint16_t* xrow = ONE == 2 ? xwave + (kb - kb0) * KBLK : xs + kb * KBLK;
+      u32x4_t a2 = u32x4_t{0u, 0u, 0u, 0u};
+      if (kb + b < kb1) a2 = *reinterpret_cast<const u32x4_t*>(xrow + b * KBLK + 32 * (r & 3) + 8 * jg);
+      const uint32_t one = A::pair_from_f32(1.0f);
+      const f32x4_t cs = A::mfma(a2, u32x4_t{one, one, one, one}, f32x4_t{0.f, 0.f, 0.f, 0.f});
+      constexpr int NG = kNgOf<W>;
+      float gs[NG];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        float v = 0.0f;
+#pragma unroll
+        for (int i = g * (4 / NG); i < (g + 1) * (4 / NG); ++i) v += cs[i];
+        gs[g] = v;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+          sig[u][g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gs[g]), 16 * u));
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (kb + u < kb1) {  // wave-uniform
@@ -251,7 +326,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
         for (int c = 0; c < MCH; ++c) {
 #pragma unroll
           for (int i = 0; i < STEPS; ++i) {
-            if constexpr (XLDS)
+            if constexpr (ONE == 2)
+              xv[c][i] = *reinterpret_cast<const u32x4_t*>(xwave + (kk - kb0) * KBLK + W::xk(i, jg));
+            else if constexpr (XLDS)
               xv[c][i] = *reinterpret_cast<const u32x4_t*>(xs + xvo[c] + kk * KBLK + W::xk(i, jg));
             else
               xv[c][i] = xg[u][c][i];
@@ -266,7 +343,11 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
             }
           }
         }
-        W::template mma<A, MCH>(w[u], p[u], xv, yacc);
+        if constexpr (ONE != 0) {
+          if constexpr (has_sum_offset<W>::value) W::template mma_one<A>(w[u], p[u], xv[0], sig[u], y1);
+        } else {
+          W::template mma<A, MCH>(w[u], p[u], xv, yacc);
+        }
       }
     }
 #pragma unroll
@@ -276,6 +357,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     }
   }
 
+  if constexpr (ONE != 0) yacc[0][0] = y1;
   // Sum the NW partial tiles in wave order. Float j of a wave's block is (chunk c, lane l, row r).
 #pragma unroll
   for (int c = 0; c < MCH; ++c) red[(wave * MCH + c) * 64 + lane] = yacc[c];
@@ -329,16 +411,35 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     const size_t red = static_cast<size_t>(nw) * mch * 64 * sizeof(f32x4_t);
     const bool xlds = mch == 1 && gemv_xlds_bytes(M, KB, KBLK) <= kXldsMax;
     if (colscale != nullptr && !xlds) return hipErrorNotSupported;  // column scaling happens in the LDS copy
-#define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_)                                                                          \
-  hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO>), grid, block, LDS_, stream, wp, xp, yp, bias, \
-                     colscale, M, N, K, iKB, kbw, pa)
-    if constexpr (PRO != kProPlain) {
-      if (!xlds || m > kProMaxRows || cols % 8 != 0) return hipErrorNotSupported;  // the caller checks first
+#define SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, ONE_)                                                              \
+  hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO, ONE_>), grid, block, LDS_, stream, wp, xp, yp, \
+                     bias, colscale, M, N, K, iKB, kbw, pa)
+#define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_) SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, 0)
+    // the one-row form for formats whose offset costs sum(x) per group: 2 = each wave loads its own
+    // k-slice of the activations, 1 = from the workgroup's LDS copy (prologues, column scales)
+    constexpr bool kOneOk = has_sum_offset<W>::value && U1 == 4;
+    int one_mode = 0;
+    if (kOneOk && M == 1 && xlds)
+      one_mode = (PRO == kProPlain && colscale == nullptr && kbw <= kOneMaxKbw) ? 2 : 1;
+    if (PRO != kProPlain && (!xlds || m > kProMaxRows || cols % 8 != 0))
+      return hipErrorNotSupported;  // the caller checks first
+    if (one_mode != 0) {
+      if constexpr (kOneOk) {
+        if (one_mode == 2) {
+          const size_t lds = red + static_cast<size_t>(nw) * ((kbw * (KBLK / 8) + 63) / 64) * 1024;
+          if constexpr (PRO == kProPlain) {
+            if (ktail) SQX_GEMV1(1, U1, true, true, lds, 2); else SQX_GEMV1(1, U1, false, true, lds, 2);
+          }
+        } else {
+          const size_t lds = red + gemv_xlds_bytes(M, KB, KBLK);
+          if (ktail) SQX_GEMV1(1, U1, true, true, lds, 1); else SQX_GEMV1(1, U1, false, true, lds, 1);
+        }
+      }
+    } else if (PRO != kProPlain || xlds) {
       const size_t lds = red + gemv_xlds_bytes(M, KB, KBLK);
       if (ktail) SQX_GEMV(1, U1, true, true, lds); else SQX_GEMV(1, U1, false, true, lds);
-    } else if (xlds) {
-      const size_t lds = red + gemv_xlds_bytes(M, KB, KBLK);
-      if (ktail) SQX_GEMV(1, U1, true, true, lds); else SQX_GEMV(1, U1, false, true, lds);
+    } else if constexpr (PRO != kProPlain) {
+      return hipErrorNotSupported;
     } else if (mch == 1) {
       if (ktail) SQX_GEMV(1, U1, true, false, red); else SQX_GEMV(1, U1, false, false, red);
     } else if (mch == 2) {
@@ -347,6 +448,7 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
       if (ktail) SQX_GEMV(4, 1, true, false, red); else SQX_GEMV(4, 1, false, false, red);
     }
 #undef SQX_GEMV
+#undef SQX_GEMV1
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

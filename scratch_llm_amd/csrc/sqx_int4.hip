@@ -384,6 +384,29 @@ struct WInt4 {
       }
     }
   }
+  // One activation row (the GEMV's ONE form): the code chains only, with the offset charged
+  // through the groups' activation sums sig[g]; y0 is the row's output for this lane's weight row.
+  static constexpr bool kSumOffset = true;
+  template <class A>
+  __device__ static void mma_one(const u32x4_t& w, const P& p, const u32x4_t (&xv)[4], const float (&sig)[NG],
+                                 float& y0) {
+    const uint32_t kMask = 0x000F000Fu;
+    const uint32_t magic = A::kMagicPair;
+    u32x4_t b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t d = w[i];
+      b[i] = u32x4_t{and_or(d, kMask, magic), and_or(d >> 4, kMask, magic), and_or(d >> 8, kMask, magic),
+                     and_or(d >> 12, kMask, magic)};
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = g * MPG; i < (g + 1) * MPG; ++i) acc = A::mfma(xv[i], b[i], acc);
+      y0 = fmaf(p.sc[g], fmaf(-(A::kMagic + p.zf[g]), sig[g], acc[0]), y0);
+    }
+  }
   __device__ static float out_scale(const Args&, int) { return 1.0f; }
 
   // The skinny linear's hooks: B fragment of step i as (magic + code) pairs, the value each
