@@ -395,7 +395,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(dom, m),
-            "kernel": f"int4_linear_kernel (sqx_int4_linear) {dom[0]} {dom[2]}->{dom[1]}",
+            "kernel": f"gemv_kernel<ActBF16, WInt4<128,false,false>> (sqx_int4_linear) {dom[0]} {dom[2]}->{dom[1]}",
             "avg_launch_us": round(dom_us, 3),
             "bytes_per_launch": dom_bytes,
         },
