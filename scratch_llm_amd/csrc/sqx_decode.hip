@@ -200,7 +200,10 @@ struct KvRow<true> {
 // cache of fp8_kv_per_head.py): attention runs on the dequantized values code * scale, with the K
 // scale folded into q and the V scale applied to the partial output; the new key/value are quantized
 // with the head's scales before they are used or stored.
-template <int G, bool ROPE, bool KV8>
+// PF: the first step's rows are requested before the row length is known (one global round trip
+// fewer per workgroup; it keeps those registers live through the query set-up, which costs the bf16
+// variants a wave per SIMD, so it pays where workgroups are few or the rows are E4M3).
+template <int G, bool ROPE, bool KV8, bool PF>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __restrict__ q, uint8_t* __restrict__ kc,
                                                            uint8_t* __restrict__ vc, const int* __restrict__ lengths,
                                                            const float* __restrict__ cos_t, const float* __restrict__ sin_t,
@@ -211,15 +214,31 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
   using Row = typename R::T;
   constexpr int ES = R::kBytes;
   const int ch = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kl = lane >> 4, dl = lane & 15;
+  const int t0 = ch * chunk;
+  const int span = chunk / 4;
+  const int ws = t0 + wave * span;
+  const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd * ES;  // bytes
+  const uint8_t* kb = kc + head_off + dl * 8 * ES;
+  const uint8_t* vb = vc + head_off + dl * 8 * ES;
+  // PF: the first step's rows are requested before the row's length is known (rows clamped into the
+  // cache; rows past the attended range are masked, and their values zeroed, once it is), so they
+  // travel with the length and the query instead of after them.
+  Row kr[4], vr[4];
+  if constexpr (PF) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int tc = min(ws + 4 * u + kl, tmax - 1);
+      kr[u] = *reinterpret_cast<const Row*>(kb + static_cast<int64_t>(tc) * kHd * ES);
+      vr[u] = *reinterpret_cast<const Row*>(vb + static_cast<int64_t>(tc) * kHd * ES);
+    }
+  }
   const int len = max(lengths[b], 0);
   const int L = min(len + 1, tmax);
   const int slot = min(len, tmax - 1);
-  const int t0 = ch * chunk;
   if (t0 >= L) return;  // the combine reads only chunks below L
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int kl = lane >> 4, dl = lane & 15;
-  const int span = chunk / 4;
-  const int ws = t0 + wave * span, we = min(ws + span, L);
+  const int we = min(ws + span, L);
 
   __shared__ float sm[4][G], sl[4][G];
   __shared__ float so[4][G][kHd];
@@ -266,9 +285,6 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[g][j] = 0.0f;
   }
-  const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd * ES;  // bytes
-  const uint8_t* kb = kc + head_off + dl * 8 * ES;
-  const uint8_t* vb = vc + head_off + dl * 8 * ES;
   if constexpr (ROPE) {
     if (ch == slot / chunk && wave == 0 && kl == 0) {  // one cache row each, from this workgroup only
       *reinterpret_cast<Row*>(kc + head_off + (static_cast<int64_t>(slot) * kHd + dl * 8) * ES) = knew;
@@ -277,15 +293,21 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
   }
 
   for (int base = ws; base < we; base += kKeysPerStep) {
-    Row kr[4], vr[4];
     bool ok[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int t = base + 4 * u + kl;
-      ok[u] = t < we;
-      const int tc = ok[u] ? t : base;  // an in-range row; its score is masked below
-      kr[u] = *reinterpret_cast<const Row*>(kb + static_cast<int64_t>(tc) * kHd * ES);
-      vr[u] = *reinterpret_cast<const Row*>(vb + static_cast<int64_t>(tc) * kHd * ES);
+    for (int u = 0; u < 4; ++u) ok[u] = base + 4 * u + kl < we;
+    if (PF && base == ws) {
+      // the prefetched rows: a masked row may hold anything, and its weight 0 must not meet a NaN
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (!ok[u]) vr[u] = Row{};
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int tc = ok[u] ? base + 4 * u + kl : base;  // an in-range row; its score is masked below
+        kr[u] = *reinterpret_cast<const Row*>(kb + static_cast<int64_t>(tc) * kHd * ES);
+        vr[u] = *reinterpret_cast<const Row*>(vb + static_cast<int64_t>(tc) * kHd * ES);
+      }
     }
     if constexpr (ROPE) {
       if (slot >= base && slot < base + kKeysPerStep) {  // wave-uniform: this step holds the new key
@@ -653,9 +675,18 @@ static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, co
   float* w = static_cast<float*>(ws);
   const int iH = static_cast<int>(H), iK = static_cast<int>(Hkv), iT = static_cast<int>(tmax);
   const int rr = static_cast<int>(rope_rows);
-#define SQX_ATTN(G_, R_, K8_)                                                                                       \
-  hipLaunchKernelGGL((attn_partial_kernel<G_, R_, K8_>), grid, dim3(256), 0, s, qp, kp, vp, lengths, cos_t, sin_t, kscale, \
-                     vscale, rr, iH, iK, iT, chunk, nchunk, qscale, w)
+  // early row loads: always for E4M3 rows; for bf16 rows when the grid fits the CUs at two
+  // workgroups each (the bf16 variants lose a wave per SIMD to them)
+  const bool pf = kv8 || static_cast<int64_t>(nchunk) * Hkv * B <= 512;
+#define SQX_ATTN(G_, R_, K8_)                                                                                          \
+  do {                                                                                                             \
+    if (pf)                                                                                                        \
+      hipLaunchKernelGGL((attn_partial_kernel<G_, R_, K8_, true>), grid, dim3(256), 0, s, qp, kp, vp, lengths, cos_t, \
+                         sin_t, kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, w);                           \
+    else                                                                                                           \
+      hipLaunchKernelGGL((attn_partial_kernel<G_, R_, K8_, false>), grid, dim3(256), 0, s, qp, kp, vp, lengths,     \
+                         cos_t, sin_t, kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, w);                    \
+  } while (0)
 #define SQX_ATTN_G(R_, K8_)                \
   switch (G) {                             \
     case 1: SQX_ATTN(1, R_, K8_); break;   \

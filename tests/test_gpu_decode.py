@@ -130,6 +130,46 @@ def _attn_case(lib, B, H, Hkv, T, lengths, seed):
         assert float((err / bound).max()) <= 1.0, f"row {b} (L={L}): {float((err / bound).max()):.2f}x the bound"
 
 
+def test_attention_early_rows_equal_late_rows(lib):
+    """Small grids request their first rows before the row length is known (B = 2 here: 512
+    workgroups) and larger ones after it (B = 8: 2048), with the same 64-key chunks: rows 0 and 1
+    agree bit for bit, and cache rows past each length, filled with NaN, reach neither."""
+    print_case("attention early rows")
+    B, H, Hkv, T, hd = 8, 32, 8, 2048, 128
+    g = torch.Generator().manual_seed(77)
+    q = (torch.randn(B, H, hd, generator=g) * 2).bfloat16().to(DEV)
+    k = (torch.randn(B, Hkv, T, hd, generator=g) * 2).bfloat16()
+    v = torch.randn(B, Hkv, T, hd, generator=g).bfloat16()
+    lengths = [1000, 37, 2047, 5, 640, 63, 64, 1500]
+    for b, n in enumerate(lengths):
+        k[b, :, n + 1:] = float("nan")
+        v[b, :, n + 1:] = float("nan")
+    kd, vd = k.to(DEV), v.to(DEV)
+    ln = torch.tensor(lengths, dtype=torch.int32, device=DEV)
+    outs = {}
+    for nb_rows in (2, 8):
+        assert lib.sqx_attn_chunk(nb_rows, Hkv, T) == 64
+        out = torch.empty(nb_rows, H * hd, dtype=torch.bfloat16, device=DEV)
+        nb = lib.sqx_attn_workspace_bytes(nb_rows, H, Hkv, T)
+        ws = torch.empty(nb // 4, dtype=torch.float32, device=DEV)
+        _ok(lib, lib.sqx_decode_attention(q.data_ptr(), kd.data_ptr(), vd.data_ptr(), ln.data_ptr(), nb_rows, H, Hkv,
+                                          hd, T, out.data_ptr(), ws.data_ptr(), nb, _s()))
+        torch.cuda.synchronize()
+        outs[nb_rows] = out.cpu()
+    assert torch.isfinite(outs[8].float()).all()
+    assert torch.equal(outs[2], outs[8][:2])
+    G = H // Hkv
+    got = outs[8].view(B, H, hd).double()
+    for b in range(B):
+        L = lengths[b] + 1
+        kk = k[b, :, :L].double().repeat_interleave(G, dim=0)
+        vv = v[b, :, :L].double().repeat_interleave(G, dim=0)
+        p = torch.softmax(torch.einsum("hd,htd->ht", q[b].cpu().double(), kk) / math.sqrt(hd), dim=-1)
+        want = torch.einsum("ht,htd->hd", p, vv)
+        bound = 2.0**-8 * want.abs() + 1e-5 * vv.abs().max()
+        assert float(((got[b] - want).abs() / bound).max()) <= 1.0, f"row {b}"
+
+
 @pytest.mark.parametrize("H,Hkv", [(32, 8), (8, 8), (16, 8), (16, 2)])
 def test_attention_ragged(lib, H, Hkv):
     print_case("attention", H, Hkv)
