@@ -266,15 +266,22 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
     }
   }
   const float qs = qscale * ks;
-  float qv[G][8];
+  // bf16 rows: the query stays in bf16 pairs and a score is sum(q k) by v_dot2c_f32_bf16 (exact
+  // products, fp32 sums), scaled once; E4M3 rows: the scaled query in fp32 against decoded codes
+  [[maybe_unused]] float qv[KV8 ? G : 1][8];
+  [[maybe_unused]] u32x4_t qb[KV8 ? 1 : G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     u32x4_t v = *reinterpret_cast<const u32x4_t*>(qrow + (kh * G + g) * kHd);
     if constexpr (ROPE) v = rope8(v, cs, sn);
+    if constexpr (KV8) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      qv[g][2 * j] = bf16_lo(v[j]) * qs;
-      qv[g][2 * j + 1] = bf16_hi(v[j]) * qs;
+      for (int j = 0; j < 4; ++j) {
+        qv[g][2 * j] = bf16_lo(v[j]) * qs;
+        qv[g][2 * j + 1] = bf16_hi(v[j]) * qs;
+      }
+    } else {
+      qb[g] = v;
     }
   }
   float m[G], l[G], o[G][8];
@@ -341,9 +348,20 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         float acc = 0.0f;
+        if constexpr (KV8) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc = fmaf(qv[g][j], kval(u, j), acc);
-        s[u] = ok[u] ? row16_sum(acc) : -INFINITY;
+          for (int j = 0; j < 8; ++j) acc = fmaf(qv[g][j], kval(u, j), acc);
+          s[u] = ok[u] ? row16_sum(acc) : -INFINITY;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            // elements go through scalars: hipcc's bit_cast of a vector element reads element 0
+            const uint32_t qj = qb[g][j], kj = kr[u][j];
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qj), __builtin_bit_cast(bf16x2_t, kj),
+                                                  acc, false);
+          }
+          s[u] = ok[u] ? row16_sum(acc) * qs : -INFINITY;
+        }
       }
       const float mn = fmaxf(fmaxf(m[g], fmaxf(s[0], s[1])), fmaxf(s[2], s[3]));
       // a group whose keys are all masked so far keeps m = -inf and adds nothing
