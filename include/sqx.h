@@ -153,6 +153,35 @@ int sqx_int4_linear_rmsnorm(const uint8_t* wt, const float* st, const void* x, c
 int sqx_int4_linear_silu(const uint8_t* wt, const float* st, const void* gate_up, void* y, int64_t m,
                          int64_t rows, int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
 
+/* The one-row decode step with the RMSNorm between the linears folded away (model.py:365-372, the
+ * block's h = x + attn(attn_norm(x)) and h + ffn(ffn_norm(h))). A linear that feeds the residual
+ * stream ends in the residual add and leaves the sums of squares the next norm needs; the linear
+ * after the norm forms the norm from those sums while it loads its activations. m must be 1.
+ *
+ * sqx_int4_linear_residual: res_out = bf16(res + bf16(x @ W^T)) [rows] (res_out may be res), and
+ * ss_out[t] = sum of res_out[16t .. 16t+15]^2 (fp32, ceil(rows/16) entries). The linear is the GEMV
+ * form of sqx_int4_linear with the same k_slices, bit for bit, and the add rounds as the reference's
+ * bf16 tensor add. Weight format as sqx_int4_linear_rmsnorm. */
+int sqx_int4_linear_residual(const uint8_t* wt, const float* st, const void* x, const void* res, void* res_out,
+                             float* ss_out, int64_t m, int64_t rows, int64_t cols, int64_t group, int k_slices,
+                             sqx_stream_t stream);
+
+/* sqx_int4_linear_silu with the residual epilogue of sqx_int4_linear_residual (the MLP's down
+ * projection). */
+int sqx_int4_linear_silu_residual(const uint8_t* wt, const float* st, const void* gate_up, const void* res,
+                                  void* res_out, float* ss_out, int64_t m, int64_t rows, int64_t cols, int64_t group,
+                                  int k_slices, sqx_stream_t stream);
+
+/* y = rmsnorm(h) @ W^T for one row h [cols] whose sums of squares per 16 columns are ss [nss],
+ * nss = ceil(cols/16) <= 512 (as sqx_int4_linear_residual leaves them): the norm is the reference's
+ * RMSNorm (model.py:160-172), bf16(h * (1 / sqrt(sum(ss) / cols + eps)) * gain), with the fp32 sum of
+ * squares added in the tiles' order rather than sqx_rmsnorm's, so the normalised row can differ from
+ * sqx_rmsnorm's by rounding. gain bf16 [cols], 16-byte aligned. At most 16 k-blocks of 128 columns
+ * per wave (the k_slices default satisfies it up to cols = 8192). */
+int sqx_int4_linear_rmsnorm_sumsq(const uint8_t* wt, const float* st, const void* h, const float* ss, int64_t nss,
+                                  const void* gain, float eps, void* y, int64_t m, int64_t rows, int64_t cols,
+                                  int64_t group, int k_slices, sqx_stream_t stream);
+
 /* Build-defined asymmetric uint4, group-wise (BASELINE config 2's "asymmetric, bf16 scale/zero";
  * no reference symbol: the 4-bit form of quantize_affine, int8.py:142-172, per group):
  * lo = min(min(w_g), 0), hi = max(max(w_g), 0), s = max((hi - lo) / 15, 1e-12) (rounded to bf16 first

@@ -87,25 +87,41 @@ struct has_row_scale<W, std::void_t<decltype(W::kRowScale)>> : std::integral_con
 //                0 writes h to h_out), then bf16(h * (1 / sqrt(mean(h^2) + eps)) * gain). The sums use
 //                the thread mapping and order of the standalone RMSNorm kernel (256 threads, 8 columns
 //                each per 2048), so the result is bit-identical to running that kernel first;
-//   kProSiluGate x is the fused gate|up row [M, 2K]: bf16(silu(g) * u), as the standalone SiLU kernel.
-enum { kProPlain = 0, kProResNorm = 1, kProSiluGate = 2 };
+//   kProSiluGate x is the fused gate|up row [M, 2K]: bf16(silu(g) * u), as the standalone SiLU kernel;
+//   kProNormSum  (one row) x is the residual stream h and ss_in[0..nss) the sums of h^2 over its 16-column
+//                tiles, as the residual epilogue of the linear that wrote h leaves them:
+//                bf16(h * (1 / sqrt(sum(ss_in) / K + eps)) * gain), the standalone kernel's arithmetic
+//                with the sum of squares added in another order.
+// RES (one row): the residual epilogue. The output is res_out = bf16(res + bf16(x W^T)) (the decode
+// step's h = x + o_proj(...), model.py:365-372), and ss_out[t] is the sum of its squares over tile t.
+enum { kProPlain = 0, kProResNorm = 1, kProSiluGate = 2, kProNormSum = 3 };
 static constexpr int kProMaxRows = 8;
+static constexpr int kNormSumMax = 512;  // tiles of sums of squares a kProNormSum prologue reads (K <= 8192)
 
 struct ProArgs {
   const uint16_t* delta;  // kProResNorm: residual delta [M, K] or null
-  const uint16_t* gain;   // kProResNorm: RMSNorm gain [K]
+  const uint16_t* gain;   // kProResNorm, kProNormSum: RMSNorm gain [K]
   uint16_t* h_out;        // kProResNorm: x + delta [M, K] (written when delta is given)
   float eps;
+  const float* ss_in;     // kProNormSum: sums of squares of x per 16-column tile [nss]
+  int nss;
+  const uint16_t* res;    // RES: residual [N]
+  uint16_t* res_out;      // RES: res + the linear's output [N] (may be res)
+  float* ss_out;          // RES: sum of res_out^2 per 16-row tile [ceil(N / 16)]
 };
 
-template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32, int PRO = kProPlain, int ONE = 0>
+template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32, int PRO = kProPlain, int ONE = 0,
+          bool RES = false>
 __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
                                                     void* __restrict__ yv, const uint16_t* __restrict__ bias,
                                                     const float* __restrict__ colscale, int M, int N, int K, int KB,
                                                     int kbw, const ProArgs pa) {
   static_assert(PRO == kProPlain || (XLDS && MCH == 1), "activation prologues need the LDS copy");
   static_assert(ONE == 0 || (XLDS && MCH == 1 && U == 4), "the one-row form reads four-block rounds from LDS");
-  static_assert(ONE != 2 || PRO == kProPlain, "a prologue needs the workgroup's copy of the activations");
+  static_assert(ONE != 2 || PRO == kProPlain || PRO == kProNormSum,
+                "a prologue over the whole row needs the workgroup's copy of the activations");
+  static_assert(PRO != kProNormSum || ONE == 2, "the norm from tile sums runs in each wave's own slice");
+  static_assert(!RES || (ONE != 0 && !YF32), "the residual epilogue is a one-row, 16-bit form");
   extern __shared__ f32x4_t smem[];  // [NW][MCH][64] partial accumulators, then (XLDS) the activations
   f32x4_t* red = smem;
   const int lane = threadIdx.x & 63;
@@ -148,10 +164,22 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
   const int nx = (kbw * (KBLK / 8) + 63) / 64;
   u32x4_t xw[kXw];
   uint16_t* xwave = xs + (ONE == 2 ? wave * nx * 512 : 0);  // this wave's LDS slice (ONE = 2)
+  [[maybe_unused]] u32x4_t gw[PRO == kProNormSum ? kXw : 1];
+  [[maybe_unused]] u32x4_t ssv[PRO == kProNormSum ? kNormSumMax / 256 : 1];
   if constexpr (ONE == 2) {
 #pragma unroll
     for (int i = 0; i < kXw; ++i)
       if (i < nx) xw[i] = bload128(xr, (uint32_t)(kb0 * KBLK + 8 * (lane + 64 * i)) * 2u, 0u);
+    if constexpr (PRO == kProNormSum) {
+      const rsrc_t gr = make_rsrc(pa.gain, (uint32_t)K * 2u);
+      const rsrc_t sr = make_rsrc(pa.ss_in, (uint32_t)pa.nss * 4u);
+#pragma unroll
+      for (int i = 0; i < kXw; ++i)
+        if (i < nx) gw[i] = bload128(gr, (uint32_t)(kb0 * KBLK + 8 * (lane + 64 * i)) * 2u, 0u);
+#pragma unroll
+      for (int i = 0; i < kNormSumMax / 256; ++i)  // four sums a lane per load; past nss the resource reads zero
+        if (i * 256 < pa.nss) ssv[i] = bload128(sr, (uint32_t)(lane + 64 * i) * 16u, 0u);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) W::load(wc, min(kb0 + u, kb1 - 1), w[u], p[u]);
   } else {
@@ -159,6 +187,30 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
   }
   // The first weight round is in flight while the activations are copied into LDS.
   if constexpr (ONE == 2) {
+    if constexpr (PRO == kProNormSum) {
+      // the row's sum of squares from the tile sums: a fixed order, the same in every wave and lane
+      float t = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kNormSumMax / 256; ++i)
+        if (i * 256 < pa.nss) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t se = ssv[i][e];
+            t += __builtin_bit_cast(float, se);
+          }
+        }
+      t = wave_sum(t);
+      const float r = 1.0f / sqrtf(t / static_cast<float>(K) + pa.eps);
+#pragma unroll
+      for (int i = 0; i < kXw; ++i)
+        if (i < nx) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t h2 = xw[i][j], g2 = gw[i][j];
+            xw[i][j] = ActBF16::pack_rne(bf16_lo(h2) * r * bf16_lo(g2), bf16_hi(h2) * r * bf16_hi(g2));
+          }
+        }
+    }
 #pragma unroll
     for (int i = 0; i < kXw; ++i)
       if (i < nx) *reinterpret_cast<u32x4_t*>(xwave + 8 * (lane + 64 * i)) = xw[i];
@@ -371,23 +423,36 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     const int l = (j >> 2) & 63;
     const int m = c * 16 + 4 * (l >> 4) + (j & 3);
     const int n = t * 16 + (l & 15);
+    [[maybe_unused]] float hsq = 0.0f;
     if (m < M && n < N) {
       if constexpr (has_row_scale<W>::value)
         v = v * W::row_scale(wa, m) * W::out_scale(wa, n);
       else
         v *= W::out_scale(wa, n);
       if (bias) v += A::to_f32(bias[n]);
-      if constexpr (YF32)
+      if constexpr (RES) {
+        const float h = A::to_f32(A::from_f32(A::to_f32(pa.res[n]) + A::to_f32(A::from_f32(v))));
+        pa.res_out[n] = A::from_f32(h);
+        hsq = h * h;
+      } else if constexpr (YF32) {
         static_cast<float*>(yv)[(int64_t)m * N + n] = v;
-      else
+      } else {
         static_cast<uint16_t*>(yv)[(int64_t)m * N + n] = A::from_f32(v);
+      }
+    }
+    if constexpr (RES) {
+      // the row's 16 outputs sit in wave 0 (j = 4l, l < 16); their squares summed in a fixed order
+      if (j < 64) {
+        hsq = wave_sum(hsq);
+        if (j == 0) pa.ss_out[t] = hsq;
+      }
     }
   }
 }
 
 // Launch the GEMV for every 64-row pass of x. k_slices <= 0 picks the default. Returns 0 or the
 // HIP error of the launch.
-template <class A, class W, int U1, int U2, bool YF32, int PRO = kProPlain>
+template <class A, class W, int U1, int U2, bool YF32, int PRO = kProPlain, bool RES = false>
 hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, const uint16_t* bias,
                        const float* colscale, int64_t m, int64_t rows, int64_t cols, int k_slices,
                        hipStream_t stream, const ProArgs& pa = ProArgs{nullptr, nullptr, nullptr, 0.0f}) {
@@ -412,29 +477,35 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     const bool xlds = mch == 1 && gemv_xlds_bytes(M, KB, KBLK) <= kXldsMax;
     if (colscale != nullptr && !xlds) return hipErrorNotSupported;  // column scaling happens in the LDS copy
 #define SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, ONE_)                                                              \
-  hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO, ONE_>), grid, block, LDS_, stream, wp, xp, yp, \
-                     bias, colscale, M, N, K, iKB, kbw, pa)
+  hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO, ONE_, RES>), grid, block, LDS_, stream, wp, xp, \
+                     yp, bias, colscale, M, N, K, iKB, kbw, pa)
 #define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_) SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, 0)
     // the one-row form for formats whose offset costs sum(x) per group: 2 = each wave loads its own
     // k-slice of the activations, 1 = from the workgroup's LDS copy (prologues, column scales)
     constexpr bool kOneOk = has_sum_offset<W>::value && U1 == 4;
     int one_mode = 0;
     if (kOneOk && M == 1 && xlds)
-      one_mode = (PRO == kProPlain && colscale == nullptr && kbw <= kOneMaxKbw) ? 2 : 1;
+      one_mode = ((PRO == kProPlain || PRO == kProNormSum) && colscale == nullptr && kbw <= kOneMaxKbw) ? 2 : 1;
     if (PRO != kProPlain && (!xlds || m > kProMaxRows || cols % 8 != 0))
       return hipErrorNotSupported;  // the caller checks first
+    // one-row forms only: the norm from tile sums, the residual epilogue
+    if ((PRO == kProNormSum && one_mode != 2) || (RES && one_mode == 0)) return hipErrorNotSupported;
     if (one_mode != 0) {
       if constexpr (kOneOk) {
         if (one_mode == 2) {
           const size_t lds = red + static_cast<size_t>(nw) * ((kbw * (KBLK / 8) + 63) / 64) * 1024;
-          if constexpr (PRO == kProPlain) {
+          if constexpr (PRO == kProPlain || PRO == kProNormSum) {
             if (ktail) SQX_GEMV1(1, U1, true, true, lds, 2); else SQX_GEMV1(1, U1, false, true, lds, 2);
           }
         } else {
           const size_t lds = red + gemv_xlds_bytes(M, KB, KBLK);
-          if (ktail) SQX_GEMV1(1, U1, true, true, lds, 1); else SQX_GEMV1(1, U1, false, true, lds, 1);
+          if constexpr (PRO != kProNormSum) {
+            if (ktail) SQX_GEMV1(1, U1, true, true, lds, 1); else SQX_GEMV1(1, U1, false, true, lds, 1);
+          }
         }
       }
+    } else if constexpr (RES || PRO == kProNormSum) {
+      return hipErrorNotSupported;
     } else if (PRO != kProPlain || xlds) {
       const size_t lds = red + gemv_xlds_bytes(M, KB, KBLK);
       if (ktail) SQX_GEMV(1, U1, true, true, lds); else SQX_GEMV(1, U1, false, true, lds);

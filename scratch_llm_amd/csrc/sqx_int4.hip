@@ -439,20 +439,28 @@ static hipError_t launch_int4(const uint8_t* wt, const void* st, const void* zt,
 
 // The decode step's fused linears (symmetric codes, fp32 scales, bf16 activations): the residual
 // add + RMSNorm, or the SiLU gate, computed in the LDS copy of the activations.
-template <int PRO>
-static hipError_t launch_int4_pro(int group, const uint8_t* wt, const float* st, const uint16_t* x, uint16_t* y,
-                                  int64_t m, int64_t rows, int64_t cols, int k_slices, hipStream_t s, const ProArgs& pa) {
-#define SQX_PRO(G_)                                                                                              \
-  {                                                                                                              \
-    using W = WInt4<G_, false, false>;                                                                           \
-    const typename W::Args a{wt, st, nullptr};                                                                   \
-    return gemv_launch<ActBF16, W, SQX_INT4_U1, SQX_INT4_U2, false, PRO>(a, x, y, nullptr, nullptr, m, rows, cols, \
-                                                                         k_slices, s, pa);                      \
+// RES: the residual epilogue (one row): y is unused, pa.res_out and pa.ss_out are written.
+template <int PRO, bool RES>
+static hipError_t launch_int4_pro_res(int group, const uint8_t* wt, const float* st, const uint16_t* x, uint16_t* y,
+                                      int64_t m, int64_t rows, int64_t cols, int k_slices, hipStream_t s,
+                                      const ProArgs& pa) {
+#define SQX_PRO(G_)                                                                                                 \
+  {                                                                                                                 \
+    using W = WInt4<G_, false, false>;                                                                              \
+    const typename W::Args a{wt, st, nullptr};                                                                      \
+    return gemv_launch<ActBF16, W, SQX_INT4_U1, SQX_INT4_U2, false, PRO, RES>(a, x, y, nullptr, nullptr, m, rows,   \
+                                                                              cols, k_slices, s, pa);              \
   }
   if (group == 128) SQX_PRO(128)
   if (group == 64) SQX_PRO(64)
   SQX_PRO(32)
 #undef SQX_PRO
+}
+
+template <int PRO>
+static hipError_t launch_int4_pro(int group, const uint8_t* wt, const float* st, const uint16_t* x, uint16_t* y,
+                                  int64_t m, int64_t rows, int64_t cols, int k_slices, hipStream_t s, const ProArgs& pa) {
+  return launch_int4_pro_res<PRO, false>(group, wt, st, x, y, m, rows, cols, k_slices, s, pa);
 }
 
 template <class A, bool ASYM, bool PBF16>
@@ -948,6 +956,81 @@ extern "C" int sqx_int4_linear_silu(const uint8_t* wt, const float* st, const vo
                                                      static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(y),
                                                      m, rows, cols, k_slices, as_stream(stream),
                                                      ProArgs{nullptr, nullptr, nullptr, 0.0f});
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
+}
+
+// Arguments of the one-row residual epilogue shared by the two entry points that end in it.
+static int int4_res_check(const void* res, const void* res_out, const float* ss_out, int64_t m, const char* fn) {
+  SQX_REQUIRE(m == 1, SQX_E_ARG, "%s: the residual epilogue is the one-row (decode) form, m=%lld", fn, (long long)m);
+  SQX_REQUIRE(res && res_out && ss_out, SQX_E_ARG, "%s: null residual or sums", fn);
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_linear_residual(const uint8_t* wt, const float* st, const void* x, const void* res,
+                                        void* res_out, float* ss_out, int64_t m, int64_t rows, int64_t cols,
+                                        int64_t group, int k_slices, sqx_stream_t stream) {
+  const char* fn = "sqx_int4_linear_residual";
+  int rc = int4_pro_check(wt, st, x, res_out, m, rows, cols, group, k_slices, fn);
+  if (rc == SQX_OK) rc = int4_res_check(res, res_out, ss_out, m, fn);
+  if (rc != SQX_OK) return rc;
+  ProArgs pa{};
+  pa.res = static_cast<const uint16_t*>(res);
+  pa.res_out = static_cast<uint16_t*>(res_out);
+  pa.ss_out = ss_out;
+  const hipError_t e = launch_int4_pro_res<kProPlain, true>(static_cast<int>(group), wt, st,
+                                                            static_cast<const uint16_t*>(x), nullptr, m, rows, cols,
+                                                            k_slices, as_stream(stream), pa);
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_linear_silu_residual(const uint8_t* wt, const float* st, const void* gate_up, const void* res,
+                                             void* res_out, float* ss_out, int64_t m, int64_t rows, int64_t cols,
+                                             int64_t group, int k_slices, sqx_stream_t stream) {
+  const char* fn = "sqx_int4_linear_silu_residual";
+  int rc = int4_pro_check(wt, st, gate_up, res_out, m, rows, cols, group, k_slices, fn);
+  if (rc == SQX_OK) rc = int4_res_check(res, res_out, ss_out, m, fn);
+  if (rc != SQX_OK) return rc;
+  ProArgs pa{};
+  pa.res = static_cast<const uint16_t*>(res);
+  pa.res_out = static_cast<uint16_t*>(res_out);
+  pa.ss_out = ss_out;
+  const hipError_t e = launch_int4_pro_res<kProSiluGate, true>(static_cast<int>(group), wt, st,
+                                                               static_cast<const uint16_t*>(gate_up), nullptr, m,
+                                                               rows, cols, k_slices, as_stream(stream), pa);
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_linear_rmsnorm_sumsq(const uint8_t* wt, const float* st, const void* h, const float* ss,
+                                            int64_t nss, const void* gain, float eps, void* y, int64_t m,
+                                            int64_t rows, int64_t cols, int64_t group, int k_slices,
+                                            sqx_stream_t stream) {
+  const char* fn = "sqx_int4_linear_rmsnorm_sumsq";
+  const int rc = int4_pro_check(wt, st, h, y, m, rows, cols, group, k_slices, fn);
+  if (rc != SQX_OK) return rc;
+  SQX_REQUIRE(m == 1, SQX_E_ARG, "%s: the norm from tile sums is the one-row (decode) form, m=%lld", fn, (long long)m);
+  SQX_REQUIRE(nss == ceil_div(cols, 16) && nss <= kNormSumMax, SQX_E_ARG,
+              "%s: %lld sums of squares for %lld columns (one per 16 columns, at most %d)", fn, (long long)nss,
+              (long long)cols, kNormSumMax);
+  SQX_REQUIRE(ss && gain, SQX_E_ARG, "%s: null sums or gain", fn);
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(gain) % 16 == 0 && reinterpret_cast<uintptr_t>(ss) % 4 == 0, SQX_E_ARG,
+              "%s: gain must be 16-byte and the sums 4-byte aligned", fn);
+  const int64_t KB = ceil_div(cols, 128);
+  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols) : k_slices;
+  if (nw > KB) nw = static_cast<int>(KB);
+  SQX_REQUIRE(ceil_div(KB, nw) <= kOneMaxKbw, SQX_E_ARG,
+              "%s: %lld k-blocks over %d waves: at most %d per wave (raise k_slices)", fn, (long long)KB, nw,
+              kOneMaxKbw);
+  ProArgs pa{};
+  pa.gain = static_cast<const uint16_t*>(gain);
+  pa.eps = eps;
+  pa.ss_in = ss;
+  pa.nss = static_cast<int>(nss);
+  const hipError_t e = launch_int4_pro<kProNormSum>(static_cast<int>(group), wt, st, static_cast<const uint16_t*>(h),
+                                                    static_cast<uint16_t*>(y), m, rows, cols, k_slices,
+                                                    as_stream(stream), pa);
   SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return SQX_OK;
 }

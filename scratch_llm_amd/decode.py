@@ -125,6 +125,9 @@ class DecodeState:
         self.x = [torch.empty(batch, d, **bf), torch.empty(batch, d, **bf)]  # residual stream (ping-pong)
         self.h = torch.empty(batch, d, **bf)  # normalised input of the next projection
         self.delta = torch.empty(batch, d, **bf)  # o_proj / w2 output
+        # one-row steps: sums of squares of the residual stream per 16 columns, left by the linear that
+        # wrote it for the norm in the next linear
+        self.ss = torch.empty(-(-d // 16), dtype=torch.float32, device=dev)
         self.qkv = torch.empty(batch, (cfg.n_heads + 2 * hkv) * hd, **bf)
         self.attn = torch.empty(batch, cfg.n_heads * hd, **bf)
         self.gu = torch.empty(batch, 2 * cfg.d_ff, **bf)
@@ -205,6 +208,11 @@ class Int4DecodeLM:
         # stays a kernel of its own unless asked for.
         self.fuse_norm = False
         self.fuse_silu = True
+        # One-row steps: the o and down projections end in the residual add and leave the sums of
+        # squares per 16 columns, from which the next projection (qkv, gate/up) forms the norm while it
+        # loads its activations, so the norms inside the layers cost no launch (all but the first
+        # layer's and the final one).
+        self.fuse_norm_sums = True
         cos, sin = rope_tables(cfg.head_dim, cfg.context_length, cfg.rope_theta)
         self.cos = cos.to(self.device)
         self.sin = sin.to(self.device)
@@ -330,6 +338,15 @@ class Int4DecodeLM:
             self._linear(st, tw, st.h, y, stream)
         return nxt
 
+    def _norm_sums_linear(self, st: DecodeState, h: Tensor, gain: Tensor, tw: i4.Int4Tiled, y: Tensor,
+                          stream: int) -> None:
+        """One row: ``tw`` applied to RMSNorm(h), the norm formed from ``st.ss`` (the sums of squares the
+        residual epilogue left) inside the linear."""
+        lib = _lib.load()
+        _lib.check(lib.sqx_int4_linear_rmsnorm_sumsq(
+            tw.wt.data_ptr(), tw.st.data_ptr(), h.data_ptr(), st.ss.data_ptr(), st.ss.numel(), gain.data_ptr(),
+            self.cfg.norm_eps, y.data_ptr(), 1, tw.rows, tw.cols, tw.group_size, 0, stream), "rmsnorm (sums) + int4 linear")
+
     def step(self, st: DecodeState, tokens=None) -> Tensor:
         """Decode one token per row: logits of ``st.tokens`` (or ``tokens``) at each row's position,
         written to ``st.logits``; the greedy picks replace ``st.tokens``; active rows advance. Returns
@@ -342,12 +359,17 @@ class Int4DecodeLM:
         s = _lib.stream_ptr(self.device)
         ck = _lib.check
         fuse_silu = self.fuse_silu and lib.sqx_int4_prologue_fits(B, cfg.d_ff)
+        sums = (self.fuse_norm_sums and B == 1 and d <= 8192 and lib.sqx_int4_prologue_fits(1, d)
+                and lib.sqx_int4_prologue_fits(1, cfg.d_ff))
         with torch.cuda.device(self.device):
             ck(lib.sqx_embed(self.embed.data_ptr(), cfg.vocab_size, st.tokens.data_ptr(), B, d, st.x[0].data_ptr(), s),
                "embed")
-            cur, delta = 0, None
+            cur, delta, have_ss = 0, None, False
             for li, ly in enumerate(self.layers):
-                cur = self._norm_linear(st, cur, delta, ly.attn_norm, ly.wqkv, st.qkv, s)
+                if have_ss:
+                    self._norm_sums_linear(st, st.x[cur], ly.attn_norm, ly.wqkv, st.qkv, s)
+                else:
+                    cur = self._norm_linear(st, cur, delta, ly.attn_norm, ly.wqkv, st.qkv, s)
                 if st.kv_dtype == "fp8":
                     ck(lib.sqx_decode_attention_rope_fp8kv(
                         st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
@@ -359,6 +381,18 @@ class Int4DecodeLM:
                         st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
                         cfg.context_length, st.k[li].data_ptr(), st.v[li].data_ptr(), B, H, Hkv, hd, T,
                         st.attn.data_ptr(), st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention")
+                if sums:
+                    ck(lib.sqx_int4_linear_residual(ly.wo.wt.data_ptr(), ly.wo.st.data_ptr(), st.attn.data_ptr(),
+                                                    st.x[cur].data_ptr(), st.x[1 - cur].data_ptr(), st.ss.data_ptr(),
+                                                    1, ly.wo.rows, ly.wo.cols, ly.wo.group_size, 0, s), "o + residual")
+                    cur = 1 - cur
+                    self._norm_sums_linear(st, st.x[cur], ly.ffn_norm, ly.w13, st.gu, s)
+                    ck(lib.sqx_int4_linear_silu_residual(ly.w2.wt.data_ptr(), ly.w2.st.data_ptr(), st.gu.data_ptr(),
+                                                         st.x[cur].data_ptr(), st.x[1 - cur].data_ptr(),
+                                                         st.ss.data_ptr(), 1, ly.w2.rows, ly.w2.cols,
+                                                         ly.w2.group_size, 0, s), "silu + down + residual")
+                    cur, have_ss = 1 - cur, True
+                    continue
                 self._linear(st, ly.wo, st.attn, st.delta, s)
                 delta = st.delta.data_ptr()
                 cur = self._norm_linear(st, cur, delta, ly.ffn_norm, ly.w13, st.gu, s)
@@ -369,7 +403,9 @@ class Int4DecodeLM:
                 else:
                     ck(lib.sqx_silu_mul(st.gu.data_ptr(), B, cfg.d_ff, st.act.data_ptr(), s), "silu_mul")
                     self._linear(st, ly.w2, st.act, st.delta, s)
-            cur = self._norm_linear(st, cur, delta, self.final_norm, self.lm_head, st.logits, s)
+            # the final norm stays a kernel of its own: in front of the 8016-tile lm_head every wave would
+            # re-read its slice of the gain, which costs more than the launch it saves
+            cur = self._norm_linear(st, cur, None if have_ss else delta, self.final_norm, self.lm_head, st.logits, s)
             ck(lib.sqx_argmax(st.logits.data_ptr(), B, cfg.vocab_size, st.tokens.data_ptr(), st.argmax_ws.data_ptr(),
                               st.argmax_ws.numel() * 4, s), "argmax")
             ck(lib.sqx_advance(st.lengths.data_ptr(), st.active.data_ptr(), B, s), "advance")

@@ -284,6 +284,92 @@ def test_linear_silu_equals_two_calls(lib, m, f):
     assert torch.equal(y1, y2)
 
 
+@pytest.mark.parametrize("n,k,group,silu", [(4096, 4096, 128, False), (4096, 14336, 128, True), (1000, 1056, 32, False),
+                                            (200, 2048, 64, True)])
+def test_linear_residual_equals_two_calls(lib, n, k, group, silu):
+    """sqx_int4_linear_residual / _silu_residual: the residual stream bit for bit as the GEMV form of
+    the linear followed by the bf16 add, and the sums of squares per 16 outputs against float64
+    (fp32 sums of 16 squares: 16 roundings of at most 2**-24 of the sum)."""
+    print_case("linear+residual", n, k, group, silu)
+    tw = _tiled(n, k, group, seed=n + k)
+    g = torch.Generator().manual_seed(n)
+    x = (torch.randn(1, 2 * k if silu else k, generator=g) * 2).bfloat16().to(DEV)
+    res = (torch.randn(1, n, generator=g) * 3).bfloat16().to(DEV)
+    act = torch.empty(1, k, dtype=torch.bfloat16, device=DEV)
+    y = torch.empty(1, n, dtype=torch.bfloat16, device=DEV)
+    out = torch.empty(1, n, dtype=torch.bfloat16, device=DEV)
+    nt = -(-n // 16)
+    ss = torch.full((nt,), float("nan"), dtype=torch.float32, device=DEV)
+    src = x
+    if silu:
+        _ok(lib, lib.sqx_silu_mul(x.data_ptr(), 1, k, act.data_ptr(), _s()))
+        src = act
+    ks = lib.sqx_int4_linear_default_kslices(1, n, k)
+    _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, src.data_ptr(), 1, y.data_ptr(), None, 1,
+                                 n, k, group, ks, _s()))
+    fn = lib.sqx_int4_linear_silu_residual if silu else lib.sqx_int4_linear_residual
+    _ok(lib, fn(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), res.data_ptr(), out.data_ptr(), ss.data_ptr(), 1, n, k,
+                group, 0, _s()))
+    torch.cuda.synchronize()
+    want = (res.float() + y.float()).bfloat16()  # the reference's bf16 add
+    assert torch.equal(out, want)
+    h = torch.zeros(nt * 16, dtype=torch.float64)
+    h[:n] = out.cpu().double()[0]
+    ref = (h * h).view(nt, 16).sum(1)
+    got = ss.cpu().double()
+    assert torch.isfinite(got).all()
+    assert float(((got - ref).abs() / (16 * 2.0**-24 * ref + 1e-30)).max()) <= 1.0
+
+
+@pytest.mark.parametrize("n,k,group", [(6144, 4096, 128), (28672, 4096, 128), (1000, 1056, 32), (40000, 4096, 128)])
+def test_linear_rmsnorm_sumsq(lib, n, k, group):
+    """sqx_int4_linear_rmsnorm_sumsq against sqx_rmsnorm then sqx_int4_linear (the same norm with the
+    sum of squares in another order), with the sums as sqx_int4_linear_residual leaves them: the
+    normalised row within one bf16 ulp, so y within the linear bar of the two-call result."""
+    from tests.test_gpu_int4 import _check_linear
+
+    from oracle import quant_ref as R
+    from scratch_llm_amd.quant import int4_group as i4
+
+    print_case("linear+rmsnorm from sums", n, k, group)
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(n + group)) * 0.05).to(DEV)
+    q, sc = i4.quantize_groupwise_int4(w, group)
+    tw = i4.tile_int4(q, sc, None, group)
+    del w
+    g = torch.Generator().manual_seed(k + n)
+    h = (torch.randn(1, k, generator=g) * 2).bfloat16().to(DEV)
+    gain = (1 + 0.1 * torch.randn(k, generator=g)).bfloat16().to(DEV)
+    nt = -(-k // 16)
+    hp = torch.zeros(nt * 16, dtype=torch.float32)
+    hp[:k] = h.cpu().float()[0]
+    ss = (hp * hp).view(nt, 16).sum(1).to(DEV)  # fp32 tile sums, as the residual epilogue writes them
+    hn = torch.empty(1, k, dtype=torch.bfloat16, device=DEV)
+    y1, y2 = (torch.empty(1, n, dtype=torch.bfloat16, device=DEV) for _ in range(2))
+    _ok(lib, lib.sqx_rmsnorm(h.data_ptr(), None, gain.data_ptr(), 1e-5, 1, k, None, hn.data_ptr(), _s()))
+    _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, hn.data_ptr(), 1, y1.data_ptr(), None, 1, n,
+                                 k, group, 0, _s()))
+    _ok(lib, lib.sqx_int4_linear_rmsnorm_sumsq(tw.wt.data_ptr(), tw.st.data_ptr(), h.data_ptr(), ss.data_ptr(), nt,
+                                               gain.data_ptr(), 1e-5, y2.data_ptr(), 1, n, k, group, 0, _s()))
+    torch.cuda.synchronize()
+    if n <= 28672:  # float64 product of the two-call form's normalised row and the dequantized weight
+        w_eff = R.round_bf16(R.dequantize_groupwise_int4(q.cpu().numpy(), sc.cpu().numpy(), group))
+        _check_linear(y2, R.linear_f64(hn.float().cpu().numpy(), w_eff), f"rmsnorm from sums {k}->{n}")
+    d = (y1.float() - y2.float()).abs()
+    assert float(d.max()) <= 2.0**-6 * float(y1.float().abs().max())
+
+
+def test_residual_forms_refuse(lib):
+    tw = _tiled(64, 4096, 128, seed=3)
+    x = torch.zeros(2, 4096, dtype=torch.bfloat16, device=DEV)
+    ss = torch.zeros(256, dtype=torch.float32, device=DEV)
+    assert lib.sqx_int4_linear_residual(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
+                                        ss.data_ptr(), 2, 64, 4096, 128, 0, _s()) == -1
+    assert "one-row" in lib.sqx_last_error().decode()
+    assert lib.sqx_int4_linear_rmsnorm_sumsq(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), ss.data_ptr(), 255,
+                                             x.data_ptr(), 1e-5, x.data_ptr(), 1, 64, 4096, 128, 0, _s()) == -1
+    assert "sums of squares" in lib.sqx_last_error().decode()
+
+
 def test_fused_prologue_refuses_what_does_not_fit(lib):
     assert lib.sqx_int4_prologue_fits(8, 4096) == 0  # 8 rows of 4096 exceed the 64 KiB copy
     assert lib.sqx_int4_prologue_fits(3, 14336) == 0
@@ -425,6 +511,7 @@ def test_fused_step_equals_unfused_step(small, B):
     a, b = model.new_state(B, 32), model.new_state(B, 32)
     tok = torch.arange(B) * 97 % model.cfg.vocab_size
     try:
+        model.fuse_norm_sums = False  # its norm adds the sum of squares in another order (tested below)
         for t in range(4):
             model.fuse_norm = model.fuse_silu = True
             model.step(a, tok if t == 0 else None)
@@ -435,7 +522,19 @@ def test_fused_step_equals_unfused_step(small, B):
             assert torch.equal(a.tokens, b.tokens)
         assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
     finally:
-        model.fuse_norm, model.fuse_silu = False, True
+        model.fuse_norm, model.fuse_silu, model.fuse_norm_sums = False, True, True
+
+
+def test_norm_sums_step_matches_reference_both_ways(small):
+    """One row with the norms folded into the residual epilogues (the default) and without: both
+    within the reference bar of the step oracle at every step (_run_and_compare), from the same tokens."""
+    model, refs = small
+    try:
+        for flag in (True, False):
+            model.fuse_norm_sums = flag
+            _run_and_compare(model, refs, 1, steps=5, seed=11)
+    finally:
+        model.fuse_norm_sums = True
 
 
 def test_graph_replays_equal_eager_steps(small):
