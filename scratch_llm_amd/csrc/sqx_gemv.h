@@ -32,7 +32,8 @@
 //    blocks by one MFMA whose 16 A rows hold the round's 16 chunks of 32 activations (against a
 //    B of ones), instead of an MFMA chain per block against the constant offset. ONE = 2 also
 //    drops the workgroup's copy of the activations: each wave loads only its own k-slice (issued
-//    before its weights) into its own LDS area, so no workgroup barrier precedes the MFMAs.
+//    before its weights) into its own LDS area, so no workgroup barrier precedes the MFMAs; the SiLU
+//    gate and the norm from tile sums (kProNormSum) are applied to that slice on the way in.
 #pragma once
 
 #include <type_traits>
@@ -118,7 +119,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
                                                     int kbw, const ProArgs pa) {
   static_assert(PRO == kProPlain || (XLDS && MCH == 1), "activation prologues need the LDS copy");
   static_assert(ONE == 0 || (XLDS && MCH == 1 && U == 4), "the one-row form reads four-block rounds from LDS");
-  static_assert(ONE != 2 || PRO == kProPlain || PRO == kProNormSum,
+  static_assert(ONE != 2 || PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate,
                 "a prologue over the whole row needs the workgroup's copy of the activations");
   static_assert(PRO != kProNormSum || ONE == 2, "the norm from tile sums runs in each wave's own slice");
   static_assert(!RES || (ONE != 0 && !YF32), "the residual epilogue is a one-row, 16-bit form");
@@ -164,12 +165,17 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
   const int nx = (kbw * (KBLK / 8) + 63) / 64;
   u32x4_t xw[kXw];
   uint16_t* xwave = xs + (ONE == 2 ? wave * nx * 512 : 0);  // this wave's LDS slice (ONE = 2)
-  [[maybe_unused]] u32x4_t gw[PRO == kProNormSum ? kXw : 1];
+  [[maybe_unused]] u32x4_t gw[PRO == kProNormSum || PRO == kProSiluGate ? kXw : 1];  // gain, or the up half
   [[maybe_unused]] u32x4_t ssv[PRO == kProNormSum ? kNormSumMax / 256 : 1];
   if constexpr (ONE == 2) {
 #pragma unroll
     for (int i = 0; i < kXw; ++i)
       if (i < nx) xw[i] = bload128(xr, (uint32_t)(kb0 * KBLK + 8 * (lane + 64 * i)) * 2u, 0u);
+    if constexpr (PRO == kProSiluGate) {  // xw holds the gate half [0, K) of the row, gw the up half
+#pragma unroll
+      for (int i = 0; i < kXw; ++i)
+        if (i < nx) gw[i] = bload128(xr, (uint32_t)(K + kb0 * KBLK + 8 * (lane + 64 * i)) * 2u, 0u);
+    }
     if constexpr (PRO == kProNormSum) {
       const rsrc_t gr = make_rsrc(pa.gain, (uint32_t)K * 2u);
       const rsrc_t sr = make_rsrc(pa.ss_in, (uint32_t)pa.nss * 4u);
@@ -187,6 +193,21 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
   }
   // The first weight round is in flight while the activations are copied into LDS.
   if constexpr (ONE == 2) {
+    if constexpr (PRO == kProSiluGate) {  // bf16(silu(g) * u) as the standalone SiLU kernel; 0 past K
+#pragma unroll
+      for (int i = 0; i < kXw; ++i)
+        if (i < nx) {
+          const bool in = kb0 * KBLK + 8 * (lane + 64 * i) < K;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t g2 = xw[i][j], u2 = gw[i][j];
+            const float g0 = bf16_lo(g2), g1 = bf16_hi(g2);
+            const uint32_t v = ActBF16::pack_rne(g0 / (1.0f + __expf(-g0)) * bf16_lo(u2),
+                                                 g1 / (1.0f + __expf(-g1)) * bf16_hi(u2));
+            xw[i][j] = in ? v : 0u;
+          }
+        }
+    }
     if constexpr (PRO == kProNormSum) {
       // the row's sum of squares from the tile sums: a fixed order, the same in every wave and lane
       float t = 0.0f;
@@ -485,7 +506,10 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     constexpr bool kOneOk = has_sum_offset<W>::value && U1 == 4;
     int one_mode = 0;
     if (kOneOk && M == 1 && xlds)
-      one_mode = ((PRO == kProPlain || PRO == kProNormSum) && colscale == nullptr && kbw <= kOneMaxKbw) ? 2 : 1;
+      one_mode = ((PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate) && colscale == nullptr &&
+                  kbw <= kOneMaxKbw)
+                     ? 2
+                     : 1;
     if (PRO != kProPlain && (!xlds || m > kProMaxRows || cols % 8 != 0))
       return hipErrorNotSupported;  // the caller checks first
     // one-row forms only: the norm from tile sums, the residual epilogue
@@ -494,7 +518,7 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
       if constexpr (kOneOk) {
         if (one_mode == 2) {
           const size_t lds = red + static_cast<size_t>(nw) * ((kbw * (KBLK / 8) + 63) / 64) * 1024;
-          if constexpr (PRO == kProPlain || PRO == kProNormSum) {
+          if constexpr (PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate) {
             if (ktail) SQX_GEMV1(1, U1, true, true, lds, 2); else SQX_GEMV1(1, U1, false, true, lds, 2);
           }
         } else {
