@@ -122,7 +122,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
   static_assert(ONE != 2 || PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate,
                 "a prologue over the whole row needs the workgroup's copy of the activations");
   static_assert(PRO != kProNormSum || ONE == 2, "the norm from tile sums runs in each wave's own slice");
-  static_assert(!RES || (ONE != 0 && !YF32), "the residual epilogue is a one-row, 16-bit form");
+  static_assert(!RES || ONE != 0, "the residual epilogue is a one-row form");
+  static_assert(ONE == 0 || !YF32, "the one-row form writes 16-bit outputs");
   extern __shared__ f32x4_t smem[];  // [NW][MCH][64] partial accumulators, then (XLDS) the activations
   f32x4_t* red = smem;
   const int lane = threadIdx.x & 63;
@@ -430,7 +431,40 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     }
   }
 
-  if constexpr (ONE != 0) yacc[0][0] = y1;
+  if constexpr (ONE != 0) {
+    // One row: lane l < 16 of each wave holds the partial of output t*16 + l. Wave 0 sums them in
+    // wave order (the order of the general path below) and applies the epilogue.
+    float* rf1 = reinterpret_cast<float*>(red);
+    if (lane < 16) rf1[wave * 16 + lane] = y1;
+    __syncthreads();
+    if (wave == 0) {
+      const int n = t * 16 + lane;
+      const bool own = lane < 16 && n < N;
+      float v = 0.0f;
+      if (lane < 16)
+        for (int ww = 0; ww < nw; ++ww) v += rf1[ww * 16 + lane];
+      [[maybe_unused]] float hsq = 0.0f;
+      if (own) {
+        if constexpr (has_row_scale<W>::value)
+          v = v * W::row_scale(wa, 0) * W::out_scale(wa, n);
+        else
+          v *= W::out_scale(wa, n);
+        if (bias) v += A::to_f32(bias[n]);
+        if constexpr (RES) {
+          const float h = A::to_f32(A::from_f32(A::to_f32(pa.res[n]) + A::to_f32(A::from_f32(v))));
+          pa.res_out[n] = A::from_f32(h);
+          hsq = h * h;
+        } else {
+          static_cast<uint16_t*>(yv)[n] = A::from_f32(v);
+        }
+      }
+      if constexpr (RES) {
+        hsq = wave_sum(hsq);
+        if (lane == 0) pa.ss_out[t] = hsq;
+      }
+    }
+    return;
+  }
   // Sum the NW partial tiles in wave order. Float j of a wave's block is (chunk c, lane l, row r).
 #pragma unroll
   for (int c = 0; c < MCH; ++c) red[(wave * MCH + c) * 64 + lane] = yacc[c];
@@ -444,29 +478,16 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     const int l = (j >> 2) & 63;
     const int m = c * 16 + 4 * (l >> 4) + (j & 3);
     const int n = t * 16 + (l & 15);
-    [[maybe_unused]] float hsq = 0.0f;
     if (m < M && n < N) {
       if constexpr (has_row_scale<W>::value)
         v = v * W::row_scale(wa, m) * W::out_scale(wa, n);
       else
         v *= W::out_scale(wa, n);
       if (bias) v += A::to_f32(bias[n]);
-      if constexpr (RES) {
-        const float h = A::to_f32(A::from_f32(A::to_f32(pa.res[n]) + A::to_f32(A::from_f32(v))));
-        pa.res_out[n] = A::from_f32(h);
-        hsq = h * h;
-      } else if constexpr (YF32) {
+      if constexpr (YF32)
         static_cast<float*>(yv)[(int64_t)m * N + n] = v;
-      } else {
+      else
         static_cast<uint16_t*>(yv)[(int64_t)m * N + n] = A::from_f32(v);
-      }
-    }
-    if constexpr (RES) {
-      // the row's 16 outputs sit in wave 0 (j = 4l, l < 16); their squares summed in a fixed order
-      if (j < 64) {
-        hsq = wave_sum(hsq);
-        if (j == 0) pa.ss_out[t] = hsq;
-      }
     }
   }
 }
