@@ -133,6 +133,18 @@ int sqx_int4_skinny(const uint8_t* wt, const void* st, const void* zt, int param
                     int64_t group, int variant, int tiles, int waves, int splits, void* ws,
                     int64_t ws_bytes, sqx_stream_t stream);
 
+/* The K-split count of the library's launch shape for sqx_int4_skinny with a workspace (1 when that
+ * shape does not split, the GEMV included). No counterpart in the reference (launch planning). */
+int sqx_int4_skinny_default_splits(int64_t m, int64_t rows, int64_t cols);
+
+/* sqx_int4_skinny with the library's shape (which must split K: sqx_int4_skinny_default_splits >= 2),
+ * stopping before its reduce: the fp32 partials [S][m][rows] stay in ws, to be added in split order
+ * by the consumer (sqx_rmsnorm_partials). No bias. No counterpart in the reference (it fuses the
+ * linear's last kernel into the decode step's residual add + RMSNorm, model.py:365-372). */
+int sqx_int4_skinny_partials(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
+                             int act_dtype, int64_t m, int64_t rows, int64_t cols, int64_t group, void* ws,
+                             int64_t ws_bytes, sqx_stream_t stream);
+
 /* 1 when sqx_int4_linear_rmsnorm / sqx_int4_linear_silu take m activation rows of cols columns
  * (m <= 8, cols % 8 == 0, the rows fit the kernel's 64 KiB LDS copy), else 0. */
 int sqx_int4_prologue_fits(int64_t m, int64_t cols);
@@ -474,6 +486,13 @@ int sqx_fp8_linear(const uint8_t* wt, const float* w_scale, const void* x, int a
  * d % 8 == 0, d <= 16384; 16-byte aligned. h_out must not alias x or delta. */
 int sqx_rmsnorm(const void* x, const void* delta, const void* w, float eps, int64_t rows, int64_t d,
                 void* h_out, void* y, sqx_stream_t stream);
+
+/* sqx_rmsnorm with delta given as the S fp32 partials [S][rows][d] of a K-split linear
+ * (sqx_int4_skinny_partials): delta = bf16(sum of the partials in split order), the bits that
+ * linear's own reduce writes, so the result is bit-identical to sqx_int4_skinny followed by
+ * sqx_rmsnorm. h_out receives x + delta. */
+int sqx_rmsnorm_partials(const void* x, const float* part, int splits, const void* w, float eps, int64_t rows,
+                         int64_t d, void* h_out, void* y, sqx_stream_t stream);
 
 /* RoPE of q and k (RotaryPositionalEmbedding.forward, model.py:205-224: interleaved pairs, position
  * lengths[b], fp32 cos/sin tables [rope_rows, hd/2]) and the cache write of SlotKVCache.write_decode

@@ -58,6 +58,9 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_i, _c_i, _c_i,
          _c_p, _c_i64, _c_p],
     ),
+    "sqx_int4_skinny_default_splits": (_c_i, [_c_i64, _c_i64, _c_i64]),
+    "sqx_int4_skinny_partials": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
+                                        _c_p]),
     "sqx_int4_prologue_fits": (_c_i, [_c_i64, _c_i64]),
     "sqx_int4_linear_rmsnorm": (
         _c_i,
@@ -135,6 +138,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_i, _c_p, _c_i64, _c_p],
     ),
     "sqx_rmsnorm": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "sqx_rmsnorm_partials": (_c_i, [_c_p, _c_p, _c_i, _c_p, ctypes.c_float, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "sqx_rope_kv": (
         _c_i,
         [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p],

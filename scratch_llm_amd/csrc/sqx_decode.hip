@@ -20,11 +20,15 @@ namespace sqx {
 // Residual add + RMSNorm. With delta: h = bf16(x + delta) is written to h_out and normalised;
 // without: h = x. y = bf16(h * (1 / sqrt(mean(h^2) + eps)) * w), the product taken left to right in
 // fp32 as model.py:158-162 does. One workgroup of 256 threads per row; d % 8 == 0, d <= 16384.
+// PART: delta is the bf16 rounding of the sum, in split order, of S fp32 partials [S][rows][d] at
+// part (a K-split linear's workspace), exactly as that linear's own reduce would have written it.
 // ---------------------------------------------------------------------------------------------
-template <int NCH>
+template <int NCH, bool PART = false, int PS = 0>  // PS: the split count when known at compile time
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ delta,
                                                       const uint16_t* __restrict__ w, float eps, int d,
-                                                      uint16_t* __restrict__ h_out, uint16_t* __restrict__ y) {
+                                                      uint16_t* __restrict__ h_out, uint16_t* __restrict__ y,
+                                                      const float* __restrict__ part = nullptr, int S = 0,
+                                                      int64_t pstride = 0) {
   // Thread t owns columns 8t + 2048i (i < NCH): every load of the row, the delta and the gain is
   // issued before the first use, and the row stays in registers between the two passes.
   __shared__ float red[4];
@@ -39,12 +43,50 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
       wv[i] = *reinterpret_cast<const u32x4_t*>(w + c);
     }
   }
-  if (delta != nullptr) {
+  if (PART || delta != nullptr) {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int c = tid * 8 + i * 2048;
       if (c < d) {
-        const u32x4_t dv = *reinterpret_cast<const u32x4_t*>(delta + row * d + c);
+        u32x4_t dv;
+        if constexpr (PART) {
+          const float* p0 = part + row * d + c;
+          f32x4_t a = *reinterpret_cast<const f32x4_t*>(p0), b = *reinterpret_cast<const f32x4_t*>(p0 + 4);
+          if constexpr (PS > 1) {  // every split's loads in flight together, then the sums in order
+            f32x4_t pa[PS - 1], pb[PS - 1];
+#pragma unroll
+            for (int s = 1; s < PS; ++s) {
+              pa[s - 1] = *reinterpret_cast<const f32x4_t*>(p0 + s * pstride);
+              pb[s - 1] = *reinterpret_cast<const f32x4_t*>(p0 + s * pstride + 4);
+            }
+#pragma unroll
+            for (int s = 1; s < PS; ++s)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                a[j] += pa[s - 1][j];
+                b[j] += pb[s - 1][j];
+              }
+          } else {
+            for (int s = 1; s < S; ++s) {
+              const f32x4_t a2 = *reinterpret_cast<const f32x4_t*>(p0 + s * pstride);
+              const f32x4_t b2 = *reinterpret_cast<const f32x4_t*>(p0 + s * pstride + 4);
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                a[j] += a2[j];
+                b[j] += b2[j];
+              }
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            dv[j] = static_cast<uint32_t>(f32_to_bf16_bits(a[2 * j])) |
+                    (static_cast<uint32_t>(f32_to_bf16_bits(a[2 * j + 1])) << 16);
+            dv[2 + j] = static_cast<uint32_t>(f32_to_bf16_bits(b[2 * j])) |
+                        (static_cast<uint32_t>(f32_to_bf16_bits(b[2 * j + 1])) << 16);
+          }
+        } else {
+          dv = *reinterpret_cast<const u32x4_t*>(delta + row * d + c);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           v[i][j] = ActBF16::pack_rne(bf16_lo(v[i][j]) + bf16_lo(dv[j]), bf16_hi(v[i][j]) + bf16_hi(dv[j]));
@@ -621,6 +663,39 @@ extern "C" int sqx_rmsnorm(const void* x, const void* delta, const void* w, floa
   else SQX_RMS(8);
 #undef SQX_RMS
   SQX_LAUNCH_CHECK("sqx_rmsnorm");
+  return SQX_OK;
+}
+
+extern "C" int sqx_rmsnorm_partials(const void* x, const float* part, int splits, const void* w, float eps,
+                                    int64_t rows, int64_t d, void* h_out, void* y, sqx_stream_t stream) {
+  const char* fn = "sqx_rmsnorm_partials";
+  SQX_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && rows < (int64_t(1) << 31) && d <= 16384, SQX_E_ARG,
+              "%s: bad shape [%lld, %lld] (d a multiple of 8, at most 16384)", fn, (long long)rows, (long long)d);
+  SQX_REQUIRE(splits >= 1 && splits <= 64, SQX_E_ARG, "%s: %d splits (1..64)", fn, splits);
+  if (rows == 0) return SQX_OK;
+  SQX_REQUIRE(x && part && w && y && h_out, SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(al16(x) && al16(part) && al16(w) && al16(y) && al16(h_out), SQX_E_ARG,
+              "%s: pointers must be 16-byte aligned", fn);
+  const int nch = static_cast<int>(ceil_div(d, 2048));
+#define SQX_RMS1(N_, PS_)                                                                                        \
+  hipLaunchKernelGGL((rmsnorm_kernel<N_, true, PS_>), dim3(static_cast<unsigned>(rows)), dim3(256), 0,             \
+                     as_stream(stream), static_cast<const uint16_t*>(x), nullptr, static_cast<const uint16_t*>(w), eps, \
+                     static_cast<int>(d), static_cast<uint16_t*>(h_out), static_cast<uint16_t*>(y), part, splits,   \
+                     rows * d)
+#define SQX_RMS(N_)                                  \
+  do {                                               \
+    if (splits == 2) SQX_RMS1(N_, 2);                \
+    else if (splits == 4) SQX_RMS1(N_, 4);           \
+    else if (splits == 8) SQX_RMS1(N_, 8);           \
+    else SQX_RMS1(N_, 0);                            \
+  } while (0)
+  if (nch <= 1) SQX_RMS(1);
+  else if (nch <= 2) SQX_RMS(2);
+  else if (nch <= 4) SQX_RMS(4);
+  else SQX_RMS(8);
+#undef SQX_RMS
+#undef SQX_RMS1
+  SQX_LAUNCH_CHECK(fn);
   return SQX_OK;
 }
 

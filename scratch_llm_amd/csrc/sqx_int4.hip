@@ -466,12 +466,13 @@ static hipError_t launch_int4_pro(int group, const uint8_t* wt, const float* st,
 template <class A, bool ASYM, bool PBF16>
 static hipError_t launch_int4_skinny(int group, const uint8_t* wt, const void* st, const void* zt, const uint16_t* x,
                                      uint16_t* y, const uint16_t* bias, int64_t m, int64_t rows, int64_t cols,
-                                     SkinnyShape sh, float* ws, int64_t ws_bytes, hipStream_t s) {
+                                     SkinnyShape sh, float* ws, int64_t ws_bytes, hipStream_t s,
+                                     bool reduce = true) {
 #define SQX_SKG(G_)                                                                                  \
   {                                                                                                  \
     using W = WInt4<G_, ASYM, PBF16>;                                                                \
     const typename W::Args a{wt, st, zt};                                                            \
-    return skinny_launch<A, W>(a, x, y, bias, m, rows, cols, sh, ws, ws_bytes, s);                   \
+    return skinny_launch<A, W>(a, x, y, bias, m, rows, cols, sh, ws, ws_bytes, s, reduce);           \
   }
   if (group == 128) SQX_SKG(128)
   if (group == 64) SQX_SKG(64)
@@ -748,7 +749,7 @@ extern "C" int sqx_int4_linear_default_kslices(int64_t m, int64_t rows, int64_t 
 static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
                             int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
                             int64_t group, SkinnyShape sh, void* ws, int64_t ws_bytes, sqx_stream_t stream,
-                            const char* fn);
+                            const char* fn, bool reduce = true);
 
 static int int4_linear_impl(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
                             int act_dtype, void* y, const void* bias, const float* colscale, int64_t m,
@@ -828,7 +829,7 @@ extern "C" int sqx_int4_linear_colscaled(const uint8_t* wt, const void* st, cons
 static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
                             int act_dtype, void* y, const void* bias, int64_t m, int64_t rows, int64_t cols,
                             int64_t group, SkinnyShape sh, void* ws, int64_t ws_bytes, sqx_stream_t stream,
-                            const char* fn) {
+                            const char* fn, bool reduce) {
   SQX_REQUIRE(m >= 0 && m <= 64 && rows > 0 && cols > 0, SQX_E_ARG,
               "%s: bad shape m=%lld rows=%lld cols=%lld (m <= 64)", fn, (long long)m, (long long)rows,
               (long long)cols);
@@ -849,7 +850,7 @@ static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, i
               SQX_E_ARG, "%s: bad launch shape (variant %d, tiles %d, waves %d, splits %d)", fn, sh.variant, sh.R,
               sh.waves, sh.S);
   if (m == 0) return SQX_OK;
-  SQX_REQUIRE(wt && st && x && y, SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(wt && st && x && (y || !reduce), SQX_E_ARG, "%s: null pointer", fn);
   SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, SQX_E_ARG,
               "%s: wt and x must be 16-byte aligned", fn);
   {
@@ -869,7 +870,7 @@ static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, i
   const int g = static_cast<int>(group);
   hipError_t e;
 #define SQX_SKL(ACT, ASYM, PBF) \
-  e = launch_int4_skinny<ACT, ASYM, PBF>(g, wt, st, zt, xp, yp, b16, m, rows, cols, sh, wsp, ws_bytes, s)
+  e = launch_int4_skinny<ACT, ASYM, PBF>(g, wt, st, zt, xp, yp, b16, m, rows, cols, sh, wsp, ws_bytes, s, reduce)
   if (act_dtype == SQX_DTYPE_BF16) {
     if (asym) { if (pbf) SQX_SKL(ActBF16, true, true); else SQX_SKL(ActBF16, true, false); }
     else { if (pbf) SQX_SKL(ActBF16, false, true); else SQX_SKL(ActBF16, false, false); }
@@ -880,6 +881,28 @@ static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, i
 #undef SQX_SKL
   SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return SQX_OK;
+}
+
+// Splits of the library's launch shape for m rows with a workspace (1 when it runs without a split,
+// including the GEMV it picks for some shapes).
+extern "C" int sqx_int4_skinny_default_splits(int64_t m, int64_t rows, int64_t cols) {
+  if (m < 2 || m > 64 || rows <= 0 || cols <= 0) return 1;
+  const SkinnyShape sh = skinny_default_shape(m, rows, cols, 128, true);
+  return sh.gemv ? 1 : skinny_splits(ceil_div(cols, 128), sh.S);
+}
+
+extern "C" int sqx_int4_skinny_partials(const uint8_t* wt, const void* st, const void* zt, int param_dtype,
+                                        const void* x, int act_dtype, int64_t m, int64_t rows, int64_t cols,
+                                        int64_t group, void* ws, int64_t ws_bytes, sqx_stream_t stream) {
+  const char* fn = "sqx_int4_skinny_partials";
+  SQX_REQUIRE(m >= 2 && m <= 64 && rows > 0 && cols > 0, SQX_E_ARG, "%s: bad shape m=%lld (2..64 rows)", fn,
+              (long long)m);
+  const SkinnyShape sh = skinny_default_shape(m, rows, cols, 128, true);
+  SQX_REQUIRE(!sh.gemv && skinny_splits(ceil_div(cols, 128), sh.S) >= 2, SQX_E_ARG,
+              "%s: the library's shape for m=%lld rows=%lld cols=%lld does not split K (sqx_int4_skinny_default_splits "
+              "is 1)", fn, (long long)m, (long long)rows, (long long)cols);
+  return int4_skinny_impl(wt, st, zt, param_dtype, x, act_dtype, nullptr, nullptr, m, rows, cols, group, sh, ws,
+                          ws_bytes, stream, fn, false);
 }
 
 extern "C" int64_t sqx_int4_skinny_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int splits) {

@@ -592,7 +592,7 @@ inline int skinny_splits(int64_t KB, int S) {
 template <class A, class W>
 hipError_t skinny_lds_launch(const typename W::Args& wa, const uint16_t* x, uint16_t* y, const uint16_t* bias,
                              int64_t m, int64_t rows, int64_t cols, int R, int KG, int S, float* ws, int64_t ws_bytes,
-                             hipStream_t stream) {
+                             hipStream_t stream, bool reduce = true) {
   constexpr int KBLK = W::KBLK;
   if (m < 1 || m > 64 || (R != 1 && R != 2 && R != 4) || (KG != 1 && KG != 2) || S < 1) return hipErrorInvalidValue;
   // per-group zero points with two or four groups per block hold more parameters per tile: fewer
@@ -641,7 +641,7 @@ hipError_t skinny_lds_launch(const typename W::Args& wa, const uint16_t* x, uint
   }
 #undef SQX_SL
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || !split) return e;
+  if (e != hipSuccess || !split || !reduce) return e;
   const int64_t quads = ceil_div(m * rows, 4);
   hipLaunchKernelGGL(skinny_reduce_kernel<A>, dim3(static_cast<unsigned>(ceil_div(quads, 256))), dim3(256), 0, stream,
                      ws, S, M, N, bias, y);
@@ -651,11 +651,15 @@ hipError_t skinny_lds_launch(const typename W::Args& wa, const uint16_t* x, uint
 // Launch the skinny linear for m <= 64 rows. Returns hipErrorInvalidValue when the shape does not
 // fit (the entry points check first) or the HIP error of a launch.
 template <class A, class W>
+// reduce = false with K splits: the fp32 partials [S][m][rows] stay in ws (y is not written); the
+// consumer adds them in split order as skinny_reduce_kernel does.
 hipError_t skinny_launch(const typename W::Args& wa, const uint16_t* x, uint16_t* y, const uint16_t* bias, int64_t m,
-                         int64_t rows, int64_t cols, SkinnyShape sh, float* ws, int64_t ws_bytes, hipStream_t stream) {
+                         int64_t rows, int64_t cols, SkinnyShape sh, float* ws, int64_t ws_bytes, hipStream_t stream,
+                         bool reduce = true) {
   constexpr int KBLK = W::KBLK;
   if (sh.variant == 1)
-    return skinny_lds_launch<A, W>(wa, x, y, bias, m, rows, cols, sh.R, sh.waves / 4, sh.S, ws, ws_bytes, stream);
+    return skinny_lds_launch<A, W>(wa, x, y, bias, m, rows, cols, sh.R, sh.waves / 4, sh.S, ws, ws_bytes, stream,
+                                   reduce);
   if (m < 1 || m > 64 || sh.waves < 1 || sh.waves > kSkinnyMaxWaves || (sh.R != 2 && sh.R != 4) || sh.S < 1)
     return hipErrorInvalidValue;
   const int64_t T = ceil_div(rows, 16);
@@ -694,7 +698,7 @@ hipError_t skinny_launch(const typename W::Args& wa, const uint16_t* x, uint16_t
   }
 #undef SQX_SK
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || !split) return e;
+  if (e != hipSuccess || !split || !reduce) return e;
   const int64_t quads = ceil_div(m * rows, 4);
   hipLaunchKernelGGL(skinny_reduce_kernel<A>, dim3(static_cast<unsigned>(ceil_div(quads, 256))), dim3(256), 0, stream,
                      ws, S, M, N, bias, y);

@@ -213,6 +213,9 @@ class Int4DecodeLM:
         # loads its activations, so the norms inside the layers cost no launch (all but the first
         # layer's and the final one).
         self.fuse_norm_sums = True
+        # Batched steps: when the o / down projection splits K, its fp32 partials go straight to the
+        # next residual add + RMSNorm, which adds them in the linear's own order (no reduce launch).
+        self.fuse_split_norm = True
         cos, sin = rope_tables(cfg.head_dim, cfg.context_length, cfg.rope_theta)
         self.cos = cos.to(self.device)
         self.sin = sin.to(self.device)
@@ -319,16 +322,35 @@ class Int4DecodeLM:
             )
         _lib.check(rc, "int4 linear")
 
+    def _delta_linear(self, st: DecodeState, tw: i4.Int4Tiled, x: Tensor, stream: int) -> tuple[int, int]:
+        """A linear whose output is the residual delta: ``(pointer, 0)`` to the bf16 delta, or
+        ``(workspace, S)`` when its launch splits K into S fp32 partials left for the norm to add."""
+        lib, B = _lib.load(), st.batch
+        if self.fuse_split_norm and 2 <= B <= _SKINNY_MAX_M:
+            S = lib.sqx_int4_skinny_default_splits(B, tw.rows, tw.cols)
+            if S >= 2:
+                _lib.check(lib.sqx_int4_skinny_partials(
+                    tw.wt.data_ptr(), tw.st.data_ptr(), None, _lib.DTYPE_F32, x.data_ptr(), _lib.DTYPE_BF16, B,
+                    tw.rows, tw.cols, tw.group_size, *_lib.ws_args(st.gemm_ws), stream), "int4 linear (partials)")
+                return st.gemm_ws.data_ptr(), S
+        self._linear(st, tw, x, st.delta, stream)
+        return st.delta.data_ptr(), 0
+
     def _norm_linear(self, st: DecodeState, cur: int, delta: int | None, gain: Tensor, tw: i4.Int4Tiled, y: Tensor,
-                     stream: int) -> int:
-        """RMSNorm of the residual stream (after adding ``delta`` when given) feeding ``tw``; returns the
-        index of the buffer that holds the residual stream afterwards. Small batches run it as one
-        kernel when ``fuse_norm`` is set (the norm computed in the linear's LDS copy of the activations),
-        otherwise as two."""
+                     stream: int, splits: int = 0) -> int:
+        """RMSNorm of the residual stream (after adding ``delta`` when given: a bf16 row, or with
+        ``splits`` >= 2 the fp32 partials of a K-split linear) feeding ``tw``; returns the index of the
+        buffer that holds the residual stream afterwards. Small batches run it as one kernel when
+        ``fuse_norm`` is set (the norm computed in the linear's LDS copy of the activations), otherwise
+        as two."""
         cfg, lib, B, d = self.cfg, _lib.load(), st.batch, self.cfg.d_model
         nxt = cur if delta is None else 1 - cur
         h_out = None if delta is None else st.x[nxt].data_ptr()
-        if self.fuse_norm and lib.sqx_int4_prologue_fits(B, d):
+        if splits >= 2:
+            _lib.check(lib.sqx_rmsnorm_partials(st.x[cur].data_ptr(), delta, splits, gain.data_ptr(), cfg.norm_eps, B, d,
+                                                h_out, st.h.data_ptr(), stream), "rmsnorm (partials)")
+            self._linear(st, tw, st.h, y, stream)
+        elif self.fuse_norm and lib.sqx_int4_prologue_fits(B, d):
             _lib.check(lib.sqx_int4_linear_rmsnorm(
                 tw.wt.data_ptr(), tw.st.data_ptr(), st.x[cur].data_ptr(), delta, gain.data_ptr(), cfg.norm_eps, h_out,
                 y.data_ptr(), B, tw.rows, tw.cols, tw.group_size, 0, stream), "rmsnorm + int4 linear")
@@ -364,12 +386,12 @@ class Int4DecodeLM:
         with torch.cuda.device(self.device):
             ck(lib.sqx_embed(self.embed.data_ptr(), cfg.vocab_size, st.tokens.data_ptr(), B, d, st.x[0].data_ptr(), s),
                "embed")
-            cur, delta, have_ss = 0, None, False
+            cur, delta, dsplit, have_ss = 0, None, 0, False
             for li, ly in enumerate(self.layers):
                 if have_ss:
                     self._norm_sums_linear(st, st.x[cur], ly.attn_norm, ly.wqkv, st.qkv, s)
                 else:
-                    cur = self._norm_linear(st, cur, delta, ly.attn_norm, ly.wqkv, st.qkv, s)
+                    cur = self._norm_linear(st, cur, delta, ly.attn_norm, ly.wqkv, st.qkv, s, dsplit)
                 if st.kv_dtype == "fp8":
                     ck(lib.sqx_decode_attention_rope_fp8kv(
                         st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
@@ -393,19 +415,20 @@ class Int4DecodeLM:
                                                          ly.w2.group_size, 0, s), "silu + down + residual")
                     cur, have_ss = 1 - cur, True
                     continue
-                self._linear(st, ly.wo, st.attn, st.delta, s)
-                delta = st.delta.data_ptr()
-                cur = self._norm_linear(st, cur, delta, ly.ffn_norm, ly.w13, st.gu, s)
+                delta, dsplit = self._delta_linear(st, ly.wo, st.attn, s)
+                cur = self._norm_linear(st, cur, delta, ly.ffn_norm, ly.w13, st.gu, s, dsplit)
                 if fuse_silu:
                     ck(lib.sqx_int4_linear_silu(ly.w2.wt.data_ptr(), ly.w2.st.data_ptr(), st.gu.data_ptr(),
                                                 st.delta.data_ptr(), B, ly.w2.rows, ly.w2.cols, ly.w2.group_size, 0, s),
                        "silu + int4 linear")
+                    delta, dsplit = st.delta.data_ptr(), 0
                 else:
                     ck(lib.sqx_silu_mul(st.gu.data_ptr(), B, cfg.d_ff, st.act.data_ptr(), s), "silu_mul")
-                    self._linear(st, ly.w2, st.act, st.delta, s)
+                    delta, dsplit = self._delta_linear(st, ly.w2, st.act, s)
             # the final norm stays a kernel of its own: in front of the 8016-tile lm_head every wave would
             # re-read its slice of the gain, which costs more than the launch it saves
-            cur = self._norm_linear(st, cur, None if have_ss else delta, self.final_norm, self.lm_head, st.logits, s)
+            cur = self._norm_linear(st, cur, None if have_ss else delta, self.final_norm, self.lm_head, st.logits, s,
+                                    0 if have_ss else dsplit)
             ck(lib.sqx_argmax(st.logits.data_ptr(), B, cfg.vocab_size, st.tokens.data_ptr(), st.argmax_ws.data_ptr(),
                               st.argmax_ws.numel() * 4, s), "argmax")
             ck(lib.sqx_advance(st.lengths.data_ptr(), st.active.data_ptr(), B, s), "advance")

@@ -525,6 +525,67 @@ def test_fused_step_equals_unfused_step(small, B):
         model.fuse_norm, model.fuse_silu, model.fuse_norm_sums = False, True, True
 
 
+@pytest.mark.parametrize("B", [20, 64])
+def test_split_partials_norm_step_equals_reduce_step(small, B):
+    """The K-split o / down partials added by the norm (no reduce launch) change no bit of the step:
+    at B = 20 both o and down split in the small model, at B = 64 down does."""
+    from scratch_llm_amd import _lib
+
+    model, _ = small
+    lib = _lib.load()
+    cfg = model.cfg
+    splits = [lib.sqx_int4_skinny_default_splits(B, cfg.d_model, cfg.n_heads * cfg.head_dim),
+              lib.sqx_int4_skinny_default_splits(B, cfg.d_model, cfg.d_ff)]
+    assert max(splits) >= 2, splits
+    print_case("split partials norm step", B, splits)
+    a, b = model.new_state(B, 32), model.new_state(B, 32)
+    tok = torch.arange(B) * 31 % cfg.vocab_size
+    try:
+        for t in range(3):
+            model.fuse_split_norm = True
+            model.step(a, tok if t == 0 else None)
+            model.fuse_split_norm = False
+            model.step(b, tok if t == 0 else None)
+            torch.cuda.synchronize()
+            assert torch.equal(a.logits, b.logits), f"step {t}"
+            assert torch.equal(a.tokens, b.tokens)
+        assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
+    finally:
+        model.fuse_split_norm = True
+
+
+def test_rmsnorm_partials_equals_reduce_then_norm(lib):
+    """sqx_int4_skinny_partials + sqx_rmsnorm_partials == sqx_int4_skinny (its own reduce) + sqx_rmsnorm,
+    bit for bit, and the partials form refuses a shape whose launch does not split."""
+    m, n, k = 48, 4096, 14336
+    S = lib.sqx_int4_skinny_default_splits(m, n, k)
+    print_case("rmsnorm partials", m, n, k, S)
+    assert S >= 2
+    tw = _tiled(n, k, 128, seed=9)
+    g = torch.Generator().manual_seed(9)
+    x = (torch.randn(m, k, generator=g)).bfloat16().to(DEV)
+    res = (torch.randn(m, n, generator=g) * 2).bfloat16().to(DEV)
+    gain = (1 + 0.1 * torch.randn(n, generator=g)).bfloat16().to(DEV)
+    nb = lib.sqx_int4_skinny_workspace_bytes(m, n, k, 0)
+    ws = torch.empty(nb // 4, dtype=torch.float32, device=DEV)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    h1, h2, o1, o2 = (torch.empty(m, n, dtype=torch.bfloat16, device=DEV) for _ in range(4))
+    _ok(lib, lib.sqx_int4_skinny(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, x.data_ptr(), 1, y.data_ptr(), None, m, n,
+                                 k, 128, -1, 0, 0, 0, ws.data_ptr(), nb, _s()))
+    _ok(lib, lib.sqx_rmsnorm(res.data_ptr(), y.data_ptr(), gain.data_ptr(), 1e-5, m, n, h1.data_ptr(), o1.data_ptr(),
+                             _s()))
+    _ok(lib, lib.sqx_int4_skinny_partials(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, x.data_ptr(), 1, m, n, k, 128,
+                                          ws.data_ptr(), nb, _s()))
+    _ok(lib, lib.sqx_rmsnorm_partials(res.data_ptr(), ws.data_ptr(), S, gain.data_ptr(), 1e-5, m, n, h2.data_ptr(),
+                                      o2.data_ptr(), _s()))
+    torch.cuda.synchronize()
+    assert torch.equal(h1, h2) and torch.equal(o1, o2)
+    assert lib.sqx_int4_skinny_default_splits(4, 6144, 4096) == 1
+    assert lib.sqx_int4_skinny_partials(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, x.data_ptr(), 1, 4, 6144, 4096,
+                                        128, ws.data_ptr(), nb, _s()) == -1
+    assert "does not split" in lib.sqx_last_error().decode()
+
+
 def test_norm_sums_step_matches_reference_both_ways(small):
     """One row with the norms folded into the residual epilogues (the default) and without: both
     within the reference bar of the step oracle at every step (_run_and_compare), from the same tokens."""
