@@ -308,23 +308,15 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
     }
   }
   const float qs = qscale * ks;
-  // bf16 rows: the query stays in bf16 pairs and a score is sum(q k) by v_dot2c_f32_bf16 (exact
-  // products, fp32 sums), scaled once; E4M3 rows: the scaled query in fp32 against decoded codes
-  [[maybe_unused]] float qv[KV8 ? G : 1][8];
-  [[maybe_unused]] u32x4_t qb[KV8 ? 1 : G];
+  // The query stays in bf16 pairs and a score is sum(q k) by v_dot2c_f32_bf16 (exact products, fp32
+  // sums), scaled once by qscale (and the K scale); E4M3 keys are decoded to bf16 pairs for it, which
+  // every E4M3 value is exactly.
+  u32x4_t qb[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     u32x4_t v = *reinterpret_cast<const u32x4_t*>(qrow + (kh * G + g) * kHd);
     if constexpr (ROPE) v = rope8(v, cs, sn);
-    if constexpr (KV8) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        qv[g][2 * j] = bf16_lo(v[j]) * qs;
-        qv[g][2 * j + 1] = bf16_hi(v[j]) * qs;
-      }
-    } else {
-      qb[g] = v;
-    }
+    qb[g] = v;
   }
   float m[G], l[G], o[G][8];
 #pragma unroll
@@ -369,18 +361,22 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
         }
       }
     }
-    // E4M3 rows are expanded to fp32 once per step (two codes per conversion); bf16 rows are read in place
-    float kf[KV8 ? 4 : 1][8], vf[KV8 ? 4 : 1][8];
+    // E4M3 rows: keys to bf16 pairs and values to fp32, once per step (two codes per conversion);
+    // bf16 rows are read in place
+    u32x4_t kb2[KV8 ? 4 : 1];
+    float vf[KV8 ? 4 : 1][8];
     if constexpr (KV8) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        R::to_f32(kr[u], kf[u]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t w = kr[u][h];  // through a scalar: hipcc's element access of a vector value
+          kb2[u][2 * h] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+          kb2[u][2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
+        }
         R::to_f32(vr[u], vf[u]);
       }
     }
-    auto kval = [&](int u, int j) -> float {
-      if constexpr (KV8) return kf[u][j]; else return R::at(kr[u], j);
-    };
     auto vval = [&](int u, int j) -> float {
       if constexpr (KV8) return vf[u][j]; else return R::at(vr[u], j);
     };
@@ -392,18 +388,21 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
         float acc = 0.0f;
         if constexpr (KV8) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc = fmaf(qv[g][j], kval(u, j), acc);
-          s[u] = ok[u] ? row16_sum(acc) : -INFINITY;
+          for (int j = 0; j < 4; ++j) {
+            // elements go through scalars: hipcc's bit_cast of a vector element reads element 0
+            const uint32_t qj = qb[g][j], kj = kb2[u][j];
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qj), __builtin_bit_cast(bf16x2_t, kj),
+                                                  acc, false);
+          }
         } else {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            // elements go through scalars: hipcc's bit_cast of a vector element reads element 0
             const uint32_t qj = qb[g][j], kj = kr[u][j];
             acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qj), __builtin_bit_cast(bf16x2_t, kj),
                                                   acc, false);
           }
-          s[u] = ok[u] ? row16_sum(acc) * qs : -INFINITY;
         }
+        s[u] = ok[u] ? row16_sum(acc) * qs : -INFINITY;
       }
       const float mn = fmaxf(fmaxf(m[g], fmaxf(s[0], s[1])), fmaxf(s[2], s[3]));
       // a group whose keys are all masked so far keeps m = -inf and adds nothing
