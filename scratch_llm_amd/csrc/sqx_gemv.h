@@ -431,9 +431,11 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     }
   }
 
-  if constexpr (ONE != 0) {
-    // One row: lane l < 16 of each wave holds the partial of output t*16 + l. Wave 0 sums them in
-    // wave order (the order of the general path below) and applies the epilogue.
+  // One row, grids that fit the chip in about one round: lane l < 16 of each wave holds the partial of
+  // output t*16 + l, and wave 0 sums them in wave order (the order of the general path below, so the
+  // bits are the same) and applies the epilogue. Larger grids measured faster with the general path,
+  // where four waves share the sums.
+  if (ONE != 0 && gridDim.x < 1024) {
     float* rf1 = reinterpret_cast<float*>(red);
     if (lane < 16) rf1[wave * 16 + lane] = y1;
     __syncthreads();
@@ -465,6 +467,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     }
     return;
   }
+  if constexpr (ONE != 0) yacc[0][0] = y1;
   // Sum the NW partial tiles in wave order. Float j of a wave's block is (chunk c, lane l, row r).
 #pragma unroll
   for (int c = 0; c < MCH; ++c) red[(wave * MCH + c) * 64 + lane] = yacc[c];
@@ -478,16 +481,29 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     const int l = (j >> 2) & 63;
     const int m = c * 16 + 4 * (l >> 4) + (j & 3);
     const int n = t * 16 + (l & 15);
+    [[maybe_unused]] float hsq = 0.0f;
     if (m < M && n < N) {
       if constexpr (has_row_scale<W>::value)
         v = v * W::row_scale(wa, m) * W::out_scale(wa, n);
       else
         v *= W::out_scale(wa, n);
       if (bias) v += A::to_f32(bias[n]);
-      if constexpr (YF32)
+      if constexpr (RES) {
+        const float h = A::to_f32(A::from_f32(A::to_f32(pa.res[n]) + A::to_f32(A::from_f32(v))));
+        pa.res_out[n] = A::from_f32(h);
+        hsq = h * h;
+      } else if constexpr (YF32) {
         static_cast<float*>(yv)[(int64_t)m * N + n] = v;
-      else
+      } else {
         static_cast<uint16_t*>(yv)[(int64_t)m * N + n] = A::from_f32(v);
+      }
+    }
+    if constexpr (RES) {
+      // the row's 16 outputs sit in wave 0 (j = 4l, l < 16); their squares summed in a fixed order
+      if (j < 64) {
+        hsq = wave_sum(hsq);
+        if (j == 0) pa.ss_out[t] = hsq;
+      }
     }
   }
 }
