@@ -24,7 +24,7 @@ static constexpr float kTiny = 1e-30f;  // _TINY
 // e2m1_round_to_code (:85-98): the first index of the smallest fp32 distance |a - m| over the eight
 // magnitudes (torch.argmin), so exact midpoints go to the lower magnitude and inputs whose distances
 // all round equal (above ~2**25, infinities) and NaN take index 0; sign bit = x < 0.
-__device__ inline uint32_t e2m1_code(float x) {
+__device__ inline uint32_t e2m1_code_argmin(float x) {
   const float a = fabsf(x);
   uint32_t idx = 0;
   float best = a;
@@ -37,6 +37,20 @@ __device__ inline uint32_t e2m1_code(float x) {
     }
   }
   return (x < 0.0f ? 8u : 0u) | idx;
+}
+
+// The same code in ~10 instructions instead of ~28. Below 2**22 every distance |a - m| is exact in
+// fp32 (a and the magnitudes are multiples of a's ulp), so the first minimum is the number of
+// midpoints between consecutive magnitudes (0.25 0.75 1.25 1.75 2.5 3.5 5) strictly below a, found
+// by a three-level comparison; larger inputs, infinities and NaN take the argmin above. Checked
+// equal to e2m1_code_argmin on all 2**32 fp32 bit patterns.
+__device__ inline uint32_t e2m1_code(float x) {
+  const float a = fabsf(x);
+  if (!(a < 4194304.0f)) return e2m1_code_argmin(x);
+  const bool hi = a > 1.75f;
+  const bool b1 = a > (hi ? 3.5f : 0.75f);
+  const bool b0 = a > (hi ? (b1 ? 5.0f : 2.5f) : (b1 ? 1.25f : 0.25f));
+  return (x < 0.0f ? 8u : 0u) | (hi ? 4u : 0u) | (b1 ? 2u : 0u) | (b0 ? 1u : 0u);
 }
 
 __device__ inline float e2m1_value(uint32_t c) {

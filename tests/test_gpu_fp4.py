@@ -90,6 +90,25 @@ def test_e2m1_round_and_decode_bitexact(f4, ref_vectors):
     assert np.array_equal(f4.e2m1_round_to_code(xb.to(DEV)).cpu().numpy(), R.e2m1_round_to_code(xb.float().numpy()))
 
 
+def test_e2m1_round_boundaries_bitexact(f4):
+    """The device rounding decides by comparisons with the midpoints below 2**22 and by fp32
+    distances above: every value within 64 ulps of each midpoint, each magnitude and each power of two
+    from 2**18 to 2**30 (the switch and the range where the reference's distances round), both signs,
+    plus subnormals and specials, against the oracle's argmin."""
+    anchors = np.float32([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0] +
+                         [2.0**e for e in range(18, 31)] + [3.0 * 2.0**e for e in range(18, 30)])
+    bits_ = anchors.view(np.int32)[:, None] + np.arange(-64, 65, dtype=np.int32)[None, :]
+    x = bits_.reshape(-1).view(np.float32)
+    sub = np.arange(1, 4096, dtype=np.int32).view(np.float32)
+    specials = np.float32([np.inf, np.nan, 0.0, np.finfo(np.float32).max, np.finfo(np.float32).tiny])
+    x = np.concatenate([x, sub, specials])
+    x = np.concatenate([x, -x])
+    c = f4.e2m1_round_to_code(dev(x)).cpu().numpy()
+    want = R.e2m1_round_to_code(x)
+    bad = np.flatnonzero(c != want)
+    assert bad.size == 0, f"{bad.size} codes differ, first at x={x[bad[0]]!r}: {c[bad[0]]} vs {want[bad[0]]}"
+
+
 @pytest.mark.parametrize("n", [1, 2, 3, 17, 4096, 4097, 1 << 20])
 def test_fp4_pack_unpack_bitexact(f4, n):
     rng = np.random.default_rng(n)
