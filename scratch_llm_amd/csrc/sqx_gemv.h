@@ -366,30 +366,30 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     u32x4_t wn[U];
     typename W::P pn[U];
     if (kb + U < kb1) load_round(kb + U, wn, pn);
-    // ONE: activation sums of the round's blocks. A row r = 4b + c of the MFMA holds chunk c (32
-    // columns) of block kb + b, so lane l receives the four chunk sums of block kb + (l >> 4).
+    // ONE: activation sums of the round's blocks. With CPB chunks of 32 columns per block, row
+    // r = CPB*b + c of the MFMA holds chunk c of block kb + b; lane l receives rows 4(l >> 4) .. +3,
+    // i.e. the chunk sums of block u at lane group CPB*u/4, elements CPB*u%4 onward.
+    constexpr int CPB = KBLK / 32;
+    static_assert(ONE == 0 || (CPB * U <= 16 && 4 % CPB == 0), "a round's chunks fill the 16 MFMA rows");
     [[maybe_unused]] float sig[U][ONE ? kNgOf<W> : 1];
     if constexpr (ONE != 0) {
-      const int r = lane & 15, b = r >> 2;
+      const int r = lane & 15, b = r / CPB;
       const uint16_t* xrow = ONE == 2 ? xwave + (kb - kb0) * KBLK : xs + kb * KBLK;
       u32x4_t a2 = u32x4_t{0u, 0u, 0u, 0u};
-      if (kb + b < kb1) a2 = *reinterpret_cast<const u32x4_t*>(xrow + b * KBLK + 32 * (r & 3) + 8 * jg);
+      if (b < U && kb + b < kb1) a2 = *reinterpret_cast<const u32x4_t*>(xrow + b * KBLK + 32 * (r % CPB) + 8 * jg);
       const uint32_t one = A::pair_from_f32(1.0f);
       const f32x4_t cs = A::mfma(a2, u32x4_t{one, one, one, one}, f32x4_t{0.f, 0.f, 0.f, 0.f});
       constexpr int NG = kNgOf<W>;
-      float gs[NG];
-#pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        float v = 0.0f;
-#pragma unroll
-        for (int i = g * (4 / NG); i < (g + 1) * (4 / NG); ++i) v += cs[i];
-        gs[g] = v;
-      }
+      constexpr int CPG = CPB / NG;  // chunks per group
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int g = 0; g < NG; ++g)
-          sig[u][g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gs[g]), 16 * u));
+        for (int g = 0; g < NG; ++g) {
+          float v = 0.0f;
+#pragma unroll
+          for (int i = 0; i < CPG; ++i) v += cs[(CPB * u) % 4 + g * CPG + i];
+          sig[u][g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * ((CPB * u) / 4)));
+        }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {

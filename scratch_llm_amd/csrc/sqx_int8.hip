@@ -292,6 +292,23 @@ struct WInt8 {
       }
     }
   }
+  // One activation row (the GEMV's ONE form): the code chains only, with the offset -128 charged
+  // through the block's activation sum sig[0].
+  static constexpr bool kSumOffset = true;
+  static constexpr int NG = 1;
+  template <class A>
+  __device__ static void mma_one(const u32x4_t& w, const P&, const u32x4_t (&xv)[STEPS], const float (&sig)[NG],
+                                 float& y0) {
+    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t d0 = w[2 * i], d1 = w[2 * i + 1];
+      const u32x4_t b = {A::pack_exact(ubyte_f32<0>(d0), ubyte_f32<1>(d0)), A::pack_exact(ubyte_f32<2>(d0), ubyte_f32<3>(d0)),
+                         A::pack_exact(ubyte_f32<0>(d1), ubyte_f32<1>(d1)), A::pack_exact(ubyte_f32<2>(d1), ubyte_f32<3>(d1))};
+      acc = A::mfma(xv[i], b, acc);
+    }
+    y0 += fmaf(-128.0f, sig[0], acc[0]);
+  }
   __device__ static float out_scale(const Args& a, int n) { return a.scale[n]; }
 };
 
