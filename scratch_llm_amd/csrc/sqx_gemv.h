@@ -33,7 +33,10 @@
 //    B of ones), instead of an MFMA chain per block against the constant offset. ONE = 2 also
 //    drops the workgroup's copy of the activations: each wave loads only its own k-slice (issued
 //    before its weights) into its own LDS area, so no workgroup barrier precedes the MFMAs; the SiLU
-//    gate and the norm from tile sums (kProNormSum) are applied to that slice on the way in.
+//    gate and the norm from tile sums (kProNormSum) are applied to that slice on the way in. ONE = 3
+//    is ONE = 2 held to 64 VGPRs (8 waves per SIMD, a few registers spilled): for grids of more than
+//    1024 tiles whose waves make a single round it hides more latency (gate/up 13.1 -> 12.2 us),
+//    while for multi-round waves the spills cost more than the occupancy gives.
 #pragma once
 
 #include <type_traits>
@@ -113,15 +116,15 @@ struct ProArgs {
 
 template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32, int PRO = kProPlain, int ONE = 0,
           bool RES = false>
-__global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ? 8 : 1))) void gemv_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
                                                     void* __restrict__ yv, const uint16_t* __restrict__ bias,
                                                     const float* __restrict__ colscale, int M, int N, int K, int KB,
                                                     int kbw, const ProArgs pa) {
   static_assert(PRO == kProPlain || (XLDS && MCH == 1), "activation prologues need the LDS copy");
   static_assert(ONE == 0 || (XLDS && MCH == 1 && U == 4), "the one-row form reads four-block rounds from LDS");
-  static_assert(ONE != 2 || PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate,
+  static_assert(ONE < 2 || PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate,
                 "a prologue over the whole row needs the workgroup's copy of the activations");
-  static_assert(PRO != kProNormSum || ONE == 2, "the norm from tile sums runs in each wave's own slice");
+  static_assert(PRO != kProNormSum || ONE >= 2, "the norm from tile sums runs in each wave's own slice");
   static_assert(!RES || ONE != 0, "the residual epilogue is a one-row form");
   static_assert(ONE == 0 || !YF32, "the one-row form writes 16-bit outputs");
   extern __shared__ f32x4_t smem[];  // [NW][MCH][64] partial accumulators, then (XLDS) the activations
@@ -162,13 +165,13 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
   // wave-uniform and the first weight round is unconditional (blocks past kb1 are clamped to kb1-1 and
   // left unused), so the wait before the LDS store counts exactly the weight loads still in flight.
   // Columns past the wave's slice read the next wave's activations (unused) or, past K, zero.
-  constexpr int kXw = ONE == 2 ? kOneMaxKbw * KBLK / 8 / 64 : 1;
+  constexpr int kXw = ONE >= 2 ? kOneMaxKbw * KBLK / 8 / 64 : 1;
   const int nx = (kbw * (KBLK / 8) + 63) / 64;
   u32x4_t xw[kXw];
-  uint16_t* xwave = xs + (ONE == 2 ? wave * nx * 512 : 0);  // this wave's LDS slice (ONE = 2)
+  uint16_t* xwave = xs + (ONE >= 2 ? wave * nx * 512 : 0);  // this wave's LDS slice (ONE = 2)
   [[maybe_unused]] u32x4_t gw[PRO == kProNormSum || PRO == kProSiluGate ? kXw : 1];  // gain, or the up half
   [[maybe_unused]] u32x4_t ssv[PRO == kProNormSum ? kNormSumMax / 256 : 1];
-  if constexpr (ONE == 2) {
+  if constexpr (ONE >= 2) {
 #pragma unroll
     for (int i = 0; i < kXw; ++i)
       if (i < nx) xw[i] = bload128(xr, (uint32_t)(kb0 * KBLK + 8 * (lane + 64 * i)) * 2u, 0u);
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     if (kb0 < kb1) load_round(kb0, w, p);
   }
   // The first weight round is in flight while the activations are copied into LDS.
-  if constexpr (ONE == 2) {
+  if constexpr (ONE >= 2) {
     if constexpr (PRO == kProSiluGate) {  // bf16(silu(g) * u) as the standalone SiLU kernel; 0 past K
 #pragma unroll
       for (int i = 0; i < kXw; ++i)
@@ -374,7 +377,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
     [[maybe_unused]] float sig[U][ONE ? kNgOf<W> : 1];
     if constexpr (ONE != 0) {
       const int r = lane & 15, b = r / CPB;
-      const uint16_t* xrow = ONE == 2 ? xwave + (kb - kb0) * KBLK : xs + kb * KBLK;
+      const uint16_t* xrow = ONE >= 2 ? xwave + (kb - kb0) * KBLK : xs + kb * KBLK;
       u32x4_t a2 = u32x4_t{0u, 0u, 0u, 0u};
       if (b < U && kb + b < kb1) a2 = *reinterpret_cast<const u32x4_t*>(xrow + b * KBLK + 32 * (r % CPB) + 8 * jg);
       const uint32_t one = A::pair_from_f32(1.0f);
@@ -400,7 +403,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const typename W::Args wa, c
         for (int c = 0; c < MCH; ++c) {
 #pragma unroll
           for (int i = 0; i < STEPS; ++i) {
-            if constexpr (ONE == 2)
+            if constexpr (ONE >= 2)
               xv[c][i] = *reinterpret_cast<const u32x4_t*>(xwave + (kk - kb0) * KBLK + W::xk(i, jg));
             else if constexpr (XLDS)
               xv[c][i] = *reinterpret_cast<const u32x4_t*>(xs + xvo[c] + kk * KBLK + W::xk(i, jg));
@@ -555,7 +558,13 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
       if constexpr (kOneOk) {
         if (one_mode == 2) {
           const size_t lds = red + static_cast<size_t>(nw) * ((kbw * (KBLK / 8) + 63) / 64) * 1024;
-          if constexpr (PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate) {
+          if constexpr (PRO == kProPlain) {
+            if (kbw <= U1 && T > 1024) {  // one round per wave, several rounds of workgroups
+              if (ktail) SQX_GEMV1(1, U1, true, true, lds, 3); else SQX_GEMV1(1, U1, false, true, lds, 3);
+            } else {
+              if (ktail) SQX_GEMV1(1, U1, true, true, lds, 2); else SQX_GEMV1(1, U1, false, true, lds, 2);
+            }
+          } else if constexpr (PRO == kProNormSum || PRO == kProSiluGate) {
             if (ktail) SQX_GEMV1(1, U1, true, true, lds, 2); else SQX_GEMV1(1, U1, false, true, lds, 2);
           }
         } else {
