@@ -13,8 +13,8 @@ graph and replayed; `--layout unfused` times the seven separate projections per 
 value = algorithmic HBM bytes per step / time per step; a linear's bytes are
 N*K/2 (codes) + 4*N*K/128 (fp32 scales) + 2*M*K (x) + 2*M*N (y).
 
-per_shape: each Llama-3-8B linear shape timed on its own (HIP events around a graph of back-to-back
-launches on the launch stream), rotating over >= 1 GB of distinct weight tiles (views into the
+per_shape: each Llama-3-8B linear shape timed on its own (HIP events around each replay of a graph of
+back-to-back launches on the launch stream; two untimed replays, then the median replay), rotating over >= 1 GB of distinct weight tiles (views into the
 step's tiled weights: any 16-row-tile window of a tiled weight is a tiled weight).
 roofline: the dominant kernel of the step, the int4 linear launch that takes the largest share of
 the step (the fused gate/up projection), timed the same way; `traffic` is its HBM bytes per launch
@@ -229,7 +229,7 @@ def main() -> int:
     log(f"graph step: {ms_per_step * 1e3:.1f} us, {value_gbs:.0f} GB/s, wall {wall:.3f}s")
 
     # ------------------------------------------------------------------ per-shape kernel timing
-    def shape_time(n: int, k: int, reps: int = 3):
+    def shape_time(n: int, k: int, reps: int = 5):
         """us per launch of an (n, k) linear, over windows of the step's tiled weights with matching k."""
         kb = -(-k // 128)
         tiles = -(-n // 16)
@@ -248,16 +248,20 @@ def main() -> int:
         with torch.cuda.graph(g, stream=s):
             for wp, sp in pool:
                 launch(wp, sp, n, k, s.cuda_stream)
-        g.replay()
+        # two untimed replays, then the median of per-replay times: the first replays of a fresh
+        # graph run several percent slow
+        for _ in range(2):
+            g.replay()
         torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
         with torch.cuda.stream(s):
-            a.record(s)
-            for _ in range(reps):
+            ev[0].record(s)
+            for i in range(reps):
                 g.replay()
-            b.record(s)
+                ev[i + 1].record(s)
         torch.cuda.synchronize()
-        us = a.elapsed_time(b) * 1e3 / (reps * len(pool))
+        times = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(reps))
+        us = times[reps // 2] * 1e3 / len(pool)
         return us, len(pool) * tiles * tile_b
 
     per_shape = {}
@@ -278,7 +282,7 @@ def main() -> int:
     for name, n, k, _ in linears:
         share[(name, n, k)] = share.get((name, n, k), 0) + 1
     dom = max(share, key=lambda s: share[s] * algo_bytes(m, s[1], s[2]))
-    dom_us, _ = shape_time(dom[1], dom[2], reps=5)
+    dom_us, _ = shape_time(dom[1], dom[2], reps=9)
     dom_bytes = algo_bytes(m, dom[1], dom[2])
     achieved = dom_bytes / dom_us / 1e3
 
