@@ -360,6 +360,20 @@ int sqx_int4_gemm(const uint8_t* wt, const void* st, const void* zt, int param_d
  * smaller workspace runs without the split (same result, slower for small m). */
 int64_t sqx_gemm_workspace_bytes(int64_t m, int64_t rows, int64_t cols);
 
+/* W4A16 linear with fp32 activations (w4a16_linear, int4_group.py:157-164, and awq_linear,
+ * awq.py:184-192, which accept any x.dtype and then run F.linear in fp32): x [m, cols] fp32,
+ * optionally divided by col_scale [cols] (the AWQ channel scale; NULL for none), splits into the
+ * bf16 rows a = bf16(v), b = bf16(v - a), c = bf16(v - a - b), whose sum is v exactly for normal v;
+ * the 3m rows run through the int4 decode GEMV with fp32 outputs (exact code products, fp32 group
+ * scales, 64 rows per pass over the weight; the prefill GEMM's bf16 weight decode is not
+ * fp32-faithful), and y [m, rows] fp32 = (y_a + y_b) + y_c (+ bias [rows] fp32, or NULL). Weight
+ * arguments as sqx_int4_linear. ws: device workspace of at least
+ * sqx_int4_linear_f32_workspace_bytes(m, rows, cols), 256-byte aligned. */
+int64_t sqx_int4_linear_f32_workspace_bytes(int64_t m, int64_t rows, int64_t cols);
+int sqx_int4_linear_f32(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const float* x,
+                        const float* col_scale, float* y, const float* bias, int64_t m, int64_t rows, int64_t cols,
+                        int64_t group, void* ws, int64_t ws_bytes, sqx_stream_t stream);
+
 /* Prefill / large-batch FP4-weight GEMM with BF16 / F16 activations (the mxfp4 GEMM export with
  * act_fmt = bf16, and the nvfp4 GEMM): the same operation and tiled weight as sqx_fp4_linear (the
  * config-4 F.linear(x, mxfp4_dequantize(W).to(x.dtype)) and the NVFP4 linear) on the 16-bit MFMA,

@@ -100,6 +100,11 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_i,
         [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
     ),
+    "sqx_int4_linear_f32_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "sqx_int4_linear_f32": (
+        _c_i,
+        [_c_p, _c_p, _c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
+    ),
     "sqx_fp4_gemm": (
         _c_i,
         [_c_p, _c_p, _c_i, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p],

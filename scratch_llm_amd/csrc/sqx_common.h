@@ -38,6 +38,11 @@ void set_error(const char* fmt, ...);
 
 inline hipStream_t as_stream(sqx_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// The int4 decode GEMV with fp32 outputs and no bias, for bf16 activation rows (sqx_int4.hip); the
+// fp32-activation linear (sqx_gemm.hip) runs its hi/lo rows through it.
+hipError_t int4_gemv_f32out(const uint8_t* wt, const void* st, const void* zt, bool pbf16, const uint16_t* x,
+                            float* y, int64_t m, int64_t rows, int64_t cols, int group, hipStream_t s);
+
 // ---------------------------------------------------------------- vector types (device) -----
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));

@@ -958,3 +958,83 @@ extern "C" int sqx_fp4_gemm(const uint8_t* wt, const uint8_t* st, int fmt, const
   SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "sqx_fp4_gemm: launch failed: %s", hipGetErrorString(e));
   return SQX_OK;
 }
+
+// ----------------------------------------------------------------------------------------------
+// fp32 activations for the int4 linear (w4a16_linear / awq_linear with x in fp32): x (optionally
+// divided by a per-column scale in fp32) splits into three bf16 rows a = bf16(v), b = bf16(v - a),
+// c = bf16(v - a - b), whose sum is v exactly for every normal fp32 v (8 significant bits each); the
+// 3m rows go through the decode GEMV with fp32 outputs (exact code products, the fp32 group scale
+// applied to each group's partial sum, 64 rows per pass over the weight), and
+// y = (y_a + y_b) + y_c (+ bias) in fp32. The prefill GEMM is not used here: it decodes each weight
+// to bf16, which the fp32 reference does not.
+// ----------------------------------------------------------------------------------------------
+namespace {
+__global__ __launch_bounds__(256) void split3_cols_kernel(const float* __restrict__ x, const float* __restrict__ cs,
+                                                          int64_t n, int64_t cols, uint16_t* __restrict__ parts) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = cs ? x[i] / cs[i % cols] : x[i];
+  const uint16_t a = f32_to_bf16_bits(v);
+  const float r1 = v - bf16_bits_to_f32(a);  // exact (Sterbenz)
+  const uint16_t b = f32_to_bf16_bits(r1);
+  parts[i] = a;
+  parts[n + i] = b;
+  parts[2 * n + i] = f32_to_bf16_bits(r1 - bf16_bits_to_f32(b));
+}
+
+__global__ __launch_bounds__(256) void sum3_rows_bias_kernel(const float* __restrict__ y3, int64_t n, int64_t cols,
+                                                             const float* __restrict__ bias, float* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float v = (y3[i] + y3[n + i]) + y3[2 * n + i];
+  if (bias) v += bias[i % cols];
+  y[i] = v;
+}
+
+constexpr int64_t kAlign = 256;
+int64_t align_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+}  // namespace
+
+// workspace of sqx_int4_linear_f32: the three bf16 parts of x [3m, cols], then y3 [3m, rows] fp32
+extern "C" int64_t sqx_int4_linear_f32_workspace_bytes(int64_t m, int64_t rows, int64_t cols) {
+  if (m <= 0 || rows <= 0 || cols <= 0) return 0;
+  return align_up(3 * m * cols * 2) + align_up(3 * m * rows * 4);
+}
+
+extern "C" int sqx_int4_linear_f32(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const float* x,
+                                   const float* col_scale, float* y, const float* bias, int64_t m, int64_t rows,
+                                   int64_t cols, int64_t group, void* ws, int64_t ws_bytes, sqx_stream_t stream) {
+  const char* fn = "sqx_int4_linear_f32";
+  SQX_REQUIRE(m >= 0 && rows > 0 && cols > 0, SQX_E_ARG, "%s: bad shape m=%lld rows=%lld cols=%lld", fn, (long long)m,
+              (long long)rows, (long long)cols);
+  SQX_REQUIRE(group == 32 || group == 64 || group == 128, SQX_E_ARG, "%s: group_size %lld unsupported (32, 64 or 128)",
+              fn, (long long)group);
+  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld", (long long)cols,
+              (long long)group);
+  SQX_REQUIRE(param_dtype == SQX_DTYPE_F32 || param_dtype == SQX_DTYPE_BF16, SQX_E_ARG,
+              "%s: param_dtype must be F32 or BF16", fn);
+  SQX_REQUIRE(rows < ((int64_t)1 << 31) && 64 * cols * 2 < ((int64_t)1 << 31) &&
+                  ceil_div(cols, 128) * 1024 < ((int64_t)1 << 31),
+              SQX_E_ARG, "%s: shape too large for 32-bit buffer offsets", fn);
+  if (m == 0) return SQX_OK;
+  SQX_REQUIRE(wt && st && x && y && ws, SQX_E_ARG, "%s: null pointer", fn);
+  const int64_t need = sqx_int4_linear_f32_workspace_bytes(m, rows, cols);
+  SQX_REQUIRE(ws_bytes >= need, SQX_E_SPACE, "%s: workspace of %lld bytes, needs %lld", fn, (long long)ws_bytes,
+              (long long)need);
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(ws) % kAlign == 0, SQX_E_ARG,
+              "%s: wt must be 16-byte and ws 256-byte aligned", fn);
+  hipStream_t s = as_stream(stream);
+  char* wsb = static_cast<char*>(ws);
+  uint16_t* parts = reinterpret_cast<uint16_t*>(wsb);
+  float* y3 = reinterpret_cast<float*>(wsb + align_up(3 * m * cols * 2));
+  const int64_t nx = m * cols, ny = m * rows;
+  hipLaunchKernelGGL(split3_cols_kernel, dim3((unsigned)ceil_div(nx, 256)), dim3(256), 0, s, x, col_scale, nx, cols,
+                     parts);
+  SQX_LAUNCH_CHECK(fn);
+  const hipError_t e =
+      int4_gemv_f32out(wt, st, zt, param_dtype == SQX_DTYPE_BF16, parts, y3, 3 * m, rows, cols, (int)group, s);
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  hipLaunchKernelGGL(sum3_rows_bias_kernel, dim3((unsigned)ceil_div(ny, 256)), dim3(256), 0, s, y3, ny, rows, bias, y);
+  SQX_LAUNCH_CHECK(fn);
+  return SQX_OK;
+}

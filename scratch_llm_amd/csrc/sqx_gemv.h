@@ -543,7 +543,7 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
 #define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_) SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, 0)
     // the one-row form for formats whose offset costs sum(x) per group: 2 = each wave loads its own
     // k-slice of the activations, 1 = from the workgroup's LDS copy (prologues, column scales)
-    constexpr bool kOneOk = has_sum_offset<W>::value && U1 == 4;
+    constexpr bool kOneOk = has_sum_offset<W>::value && U1 == 4 && !YF32;
     int one_mode = 0;
     if (kOneOk && M == 1 && xlds)
       one_mode = ((PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate) && colscale == nullptr &&

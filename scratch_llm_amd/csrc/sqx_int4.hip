@@ -428,13 +428,32 @@ struct WInt4 {
   __device__ static float scale(const P& p, int g) { return p.sc[g]; }
 };
 
-template <class A, int GROUP, bool ASYM, bool PBF16>
-static hipError_t launch_int4(const uint8_t* wt, const void* st, const void* zt, const uint16_t* x, uint16_t* y,
+template <class A, int GROUP, bool ASYM, bool PBF16, bool YF32 = false>
+static hipError_t launch_int4(const uint8_t* wt, const void* st, const void* zt, const uint16_t* x, void* y,
                               const uint16_t* bias, const float* colscale, int64_t m, int64_t rows, int64_t cols,
                               int k_slices, hipStream_t s) {
   using W = WInt4<GROUP, ASYM, PBF16>;
   const typename W::Args a{wt, st, zt};
-  return gemv_launch<A, W, SQX_INT4_U1, SQX_INT4_U2, false>(a, x, y, bias, colscale, m, rows, cols, k_slices, s);
+  return gemv_launch<A, W, SQX_INT4_U1, SQX_INT4_U2, YF32>(a, x, y, bias, colscale, m, rows, cols, k_slices, s);
+}
+
+// The decode GEMV with fp32 outputs and no bias (bf16 activation rows; the fp32-activation linear
+// runs its hi/lo rows through it).
+hipError_t int4_gemv_f32out(const uint8_t* wt, const void* st, const void* zt, bool pbf16, const uint16_t* x,
+                            float* y, int64_t m, int64_t rows, int64_t cols, int group, hipStream_t s) {
+#define SQX_F32G(G_)                                                                                             \
+  {                                                                                                              \
+    if (zt) {                                                                                                    \
+      if (pbf16) return launch_int4<ActBF16, G_, true, true, true>(wt, st, zt, x, y, nullptr, nullptr, m, rows, cols, 0, s); \
+      return launch_int4<ActBF16, G_, true, false, true>(wt, st, zt, x, y, nullptr, nullptr, m, rows, cols, 0, s);  \
+    }                                                                                                            \
+    if (pbf16) return launch_int4<ActBF16, G_, false, true, true>(wt, st, zt, x, y, nullptr, nullptr, m, rows, cols, 0, s); \
+    return launch_int4<ActBF16, G_, false, false, true>(wt, st, zt, x, y, nullptr, nullptr, m, rows, cols, 0, s);   \
+  }
+  if (group == 128) SQX_F32G(128)
+  if (group == 64) SQX_F32G(64)
+  SQX_F32G(32)
+#undef SQX_F32G
 }
 
 // The decode step's fused linears (symmetric codes, fp32 scales, bf16 activations): the residual

@@ -28,6 +28,7 @@ from scratch_llm_amd.quant.int4_group import (  # noqa: F401  (module attributes
     TILED_GROUPS,
     dequantize_groupwise_int4,
     int4_linear_tiled,
+    int4_linear_tiled_f32,
     mse,
     quantize_groupwise_int4,
     tile_int4,
@@ -185,11 +186,14 @@ def awq_linear(x: Tensor, quant: AWQQuant, bias: Tensor | None = None) -> Tensor
     computed as the int4 linear of ``x / s`` against the codes of ``W * s``."""
     _lib.require_device(x, quant.q, quant.chan_scale, bias, fn="awq_linear")
     g = quant.group_size
-    if x.dtype not in (torch.bfloat16, torch.float16) or g not in TILED_GROUPS:
-        w_eff = awq_dequantize(quant).to(x.dtype)
-        return torch.nn.functional.linear(x, w_eff, bias)
+    if g not in TILED_GROUPS:
+        raise ValueError(f"awq_linear: group_size={g} is not supported by the MI355X kernels {TILED_GROUPS}")
+    if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise TypeError(f"awq_linear takes fp32, bf16 or fp16 activations, got {x.dtype}")
     tw = _tiled_cache.get((quant.q, quant.group_scales), (g,), lambda: tile_int4(quant.q, quant.group_scales, None, g))
     s = quant.chan_scale.to(torch.float32).contiguous()
+    if x.dtype == torch.float32:
+        return int4_linear_tiled_f32(x, tw, bias, col_scale=s)
     *batch, k = x.shape
     x2 = x.reshape(-1, k)
     if not x2.is_contiguous() or x2.data_ptr() % 16:

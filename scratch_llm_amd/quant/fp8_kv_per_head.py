@@ -118,82 +118,166 @@ def saturated_count(x: Tensor, scale: Tensor) -> int:
 
 
 class PerHeadFp8KVCache:
-    """Per-layer KV cache of E4M3 codes with static per-head scales (fp8_kv_per_head.py:120-223):
-    the plain decode contract ``length`` / ``append`` / ``get`` / ``advance``, scales calibrated on
-    the first block appended to a layer (or installed with ``set_scales``), clamped elements counted."""
+    """The decode-contract KV cache of fp8_kv_per_head.py:120-223 (``length`` / ``append`` / ``get`` /
+    ``advance``, ``scales`` / ``set_scales``, ``codes``, saturation counters, ``kv_bytes``) on a
+    device-resident layout of its own.
+
+    * **Storage.** Each layer owns one uint8 buffer ``[2, B, H, capacity, D]`` (plane 0 holds K codes,
+      plane 1 V codes), allocated by the first append and grown by doubling ``capacity`` along the
+      token axis when an append would not fit, so n appends copy O(n) tokens in total. The layer's
+      filled token count is ``_fill[layer]``; ``(B, H, D)`` are fixed by its first append.
+    * **Scales.** One fp32 device tensor ``[n_layers, 2, H]``; a layer's pair is either installed
+      (``set_scales``) or calibrated from the first block appended to it (``per_head_scale``) and is
+      static afterwards, as the reference's calibrate-once contract states.
+    * **Saturation.** The quantize kernel adds the count of clamped elements straight into a device
+      int64 pair ``[K, V]``, so an append issues device work only; reading ``k_saturated`` /
+      ``v_saturated`` / ``saturated_fraction()`` synchronises.
+    * ``kv_bytes`` counts the stored code bytes plus 4 bytes per head for each scale vector a layer
+      holds; ``get`` returns freshly dequantized ``(K, V)`` in ``dtype`` and ``codes`` fresh
+      ``float8_e4m3fn`` copies of the filled region.
+    """
 
     def __init__(self, n_layers: int, *, dtype: torch.dtype = torch.float32) -> None:
         if n_layers <= 0:
             raise ValueError("n_layers must be positive")
         self.n_layers = n_layers
         self.dtype = dtype
-        self._k: list[list[Tensor]] = [[] for _ in range(n_layers)]
-        self._v: list[list[Tensor]] = [[] for _ in range(n_layers)]
-        self._k_scale: list[Tensor | None] = [None] * n_layers
-        self._v_scale: list[Tensor | None] = [None] * n_layers
-        self._length = 0
-        self.kv_bytes = 0
-        self.k_saturated = 0
-        self.v_saturated = 0
-        self.n_elements = 0
+        self._buf: list[Tensor | None] = [None] * n_layers
+        self._fill = [0] * n_layers
+        self._scale_t: Tensor | None = None  # [n_layers, 2, H] fp32, created with the first scales
+        self._has_scale = [False] * n_layers
+        self._sat: Tensor | None = None  # int64 [2] on the cache's device
+        self._tokens = 0
 
+    # ------------------------------------------------------------------ bookkeeping
     @property
     def length(self) -> int:
-        return self._length
-
-    def scales(self, layer: int) -> tuple[Tensor | None, Tensor | None]:
-        return self._k_scale[layer], self._v_scale[layer]
-
-    def set_scales(self, layer: int, k_scale: Tensor, v_scale: Tensor) -> None:
-        for s in (k_scale, v_scale):
-            if s.ndim != 4 or s.shape[0] != 1 or s.shape[2] != 1 or s.shape[3] != 1:
-                raise ValueError(f"scale must be (1, H, 1, 1), got {tuple(s.shape)}")
-        self._k_scale[layer] = k_scale.to(torch.float32)
-        self._v_scale[layer] = v_scale.to(torch.float32)
-        self.kv_bytes += (k_scale.numel() + v_scale.numel()) * 4
-
-    def saturated_fraction(self) -> float:
-        if self.n_elements == 0:
-            return 0.0
-        return (self.k_saturated + self.v_saturated) / self.n_elements
-
-    def _scale_for(self, layer: int, x: Tensor, which: str) -> Tensor:
-        store = self._k_scale if which == "k" else self._v_scale
-        scale = store[layer]
-        if scale is None:
-            scale = per_head_scale(x)
-            store[layer] = scale
-            self.kv_bytes += scale.numel() * 4
-        return scale
-
-    def append(self, layer: int, k_new: Tensor, v_new: Tensor) -> None:
-        k_scale = self._scale_for(layer, k_new, "k")
-        v_scale = self._scale_for(layer, v_new, "v")
-        k_codes, k_sat = _quantize(k_new, k_scale, count=True)
-        v_codes, v_sat = _quantize(v_new, v_scale, count=True)
-        self.k_saturated += int(k_sat.item())
-        self.v_saturated += int(v_sat.item())
-        self._k[layer].append(k_codes)
-        self._v[layer].append(v_codes)
-        self.kv_bytes += k_codes.numel() + v_codes.numel()
-        self.n_elements += k_codes.numel() + v_codes.numel()
-
-    def get(self, layer: int) -> tuple[Tensor, Tensor] | None:
-        if not self._k[layer]:
-            return None
-        k_scale, v_scale = self._k_scale[layer], self._v_scale[layer]
-        assert k_scale is not None and v_scale is not None
-        k = torch.cat(self._k[layer], dim=2)
-        v = torch.cat(self._v[layer], dim=2)
-        return dequantize_per_head(k, k_scale, self.dtype), dequantize_per_head(v, v_scale, self.dtype)
-
-    def codes(self, layer: int) -> tuple[Tensor, Tensor] | None:
-        if not self._k[layer]:
-            return None
-        return torch.cat(self._k[layer], dim=2), torch.cat(self._v[layer], dim=2)
+        return self._tokens
 
     def advance(self, n: int) -> None:
-        self._length += n
+        self._tokens += n
+
+    @property
+    def n_elements(self) -> int:
+        """Code bytes stored across layers (one byte per K or V element)."""
+        return sum(0 if b is None else 2 * b.shape[1] * b.shape[2] * f * b.shape[4] for b, f in zip(self._buf, self._fill))
+
+    @property
+    def kv_bytes(self) -> int:
+        heads = 0 if self._scale_t is None else self._scale_t.shape[2]
+        return self.n_elements + sum(self._has_scale) * 2 * heads * 4
+
+    def _sat_counts(self) -> tuple[int, int]:
+        if self._sat is None:
+            return 0, 0
+        k, v = self._sat.tolist()
+        return int(k), int(v)
+
+    @property
+    def k_saturated(self) -> int:
+        return self._sat_counts()[0]
+
+    @property
+    def v_saturated(self) -> int:
+        return self._sat_counts()[1]
+
+    def saturated_fraction(self) -> float:
+        n = self.n_elements
+        return 0.0 if n == 0 else sum(self._sat_counts()) / n
+
+    # ------------------------------------------------------------------ scales
+    def _scale_rows(self, heads: int, device: torch.device) -> Tensor:
+        if self._scale_t is None:
+            self._scale_t = torch.zeros(self.n_layers, 2, heads, dtype=torch.float32, device=device)
+        elif self._scale_t.shape[2] != heads:
+            raise ValueError(f"this cache holds {self._scale_t.shape[2]} heads per layer, got {heads}")
+        return self._scale_t
+
+    def scales(self, layer: int) -> tuple[Tensor | None, Tensor | None]:
+        if not self._has_scale[layer]:
+            return None, None
+        row = self._scale_t[layer]
+        return row[0].view(1, -1, 1, 1), row[1].view(1, -1, 1, 1)
+
+    def set_scales(self, layer: int, k_scale: Tensor, v_scale: Tensor) -> None:
+        for sc in (k_scale, v_scale):
+            if sc.ndim != 4 or sc.shape[0] != 1 or sc.shape[2] != 1 or sc.shape[3] != 1:
+                raise ValueError(f"scale must be (1, H, 1, 1), got {tuple(sc.shape)}")
+        dev = _lib.require_device(k_scale, v_scale, fn="PerHeadFp8KVCache.set_scales")
+        rows = self._scale_rows(k_scale.shape[1], dev)
+        rows[layer, 0].copy_(k_scale.reshape(-1))
+        rows[layer, 1].copy_(v_scale.reshape(-1))
+        self._has_scale[layer] = True
+
+    # ------------------------------------------------------------------ storage
+    def _reserve(self, layer: int, like: Tensor, extra: int) -> Tensor:
+        b, h, _, d = like.shape
+        buf, fill = self._buf[layer], self._fill[layer]
+        if buf is not None and tuple(buf.shape[1:3]) + (buf.shape[4],) != (b, h, d):
+            raise ValueError(f"layer {layer} holds blocks of (B, H, D) = {(buf.shape[1], buf.shape[2], buf.shape[4])}, "
+                             f"got {(b, h, d)}")
+        cap = 0 if buf is None else buf.shape[3]
+        if fill + extra > cap:
+            new_cap = max(fill + extra, 2 * cap, 16)
+            grown = torch.empty(2, b, h, new_cap, d, dtype=torch.uint8, device=like.device)
+            if buf is not None and fill:
+                grown[:, :, :, :fill].copy_(buf[:, :, :, :fill])
+            self._buf[layer] = buf = grown
+        return buf
+
+    def append(self, layer: int, k_new: Tensor, v_new: Tensor) -> None:
+        for blk in (k_new, v_new):
+            if blk.ndim != 4:
+                raise ValueError(f"KV block must be (B, H, T, D), got shape {tuple(blk.shape)}")
+        if k_new.shape != v_new.shape:
+            raise ValueError(f"K and V blocks differ in shape: {tuple(k_new.shape)} vs {tuple(v_new.shape)}")
+        dev = _lib.require_device(k_new, v_new, fn="PerHeadFp8KVCache.append")
+        if not self._has_scale[layer]:  # calibrate once, on this block
+            self.set_scales(layer, per_head_scale(k_new), per_head_scale(v_new))
+        if self._sat is None:
+            self._sat = torch.zeros(2, dtype=torch.int64, device=dev)
+        t = k_new.shape[2]
+        buf = self._reserve(layer, k_new, t)
+        f0 = self._fill[layer]
+        kv_scales = self.scales(layer)
+        for plane, (blk, sc) in enumerate(zip((k_new, v_new), kv_scales)):
+            codes, _ = _quantize_into(blk, sc, self._sat[plane:plane + 1])
+            buf[plane, :, :, f0:f0 + t].copy_(codes)
+        self._fill[layer] = f0 + t
+
+    def _planes(self, layer: int) -> tuple[Tensor, Tensor] | None:
+        buf, fill = self._buf[layer], self._fill[layer]
+        if buf is None or fill == 0:
+            return None
+        return buf[0, :, :, :fill].contiguous(), buf[1, :, :, :fill].contiguous()
+
+    def get(self, layer: int) -> tuple[Tensor, Tensor] | None:
+        planes = self._planes(layer)
+        if planes is None:
+            return None
+        k_s, v_s = self.scales(layer)
+        return dequantize_per_head(planes[0], k_s, self.dtype), dequantize_per_head(planes[1], v_s, self.dtype)
+
+    def codes(self, layer: int) -> tuple[Tensor, Tensor] | None:
+        planes = self._planes(layer)
+        if planes is None:
+            return None
+        return planes[0].view(FP8_DTYPE), planes[1].view(FP8_DTYPE)
+
+
+def _quantize_into(x: Tensor, scale: Tensor, sat: Tensor) -> tuple[Tensor, Tensor]:
+    """E4M3 codes (uint8) of a block at a per-head scale, with the clamped count added to ``sat``."""
+    _check_scale(x, scale)
+    dev = _lib.require_device(x, scale, sat, fn="quantize_per_head")
+    xx = _f(x)
+    b, h, t, d = xx.shape
+    codes = torch.empty(xx.shape, dtype=torch.uint8, device=dev)
+    s = scale.to(torch.float32).contiguous()
+    with torch.cuda.device(dev):
+        rc = _lib.load().sqx_fp8_quantize_heads(_lib.ptr(xx), _lib.sqx_dtype(xx.dtype), b, h, t * d, _lib.ptr(s),
+                                                _lib.ptr(codes), _lib.ptr(sat), _lib.stream_ptr(dev))
+    _lib.check(rc, "quantize_per_head")
+    return codes, sat
 
 
 def bf16_reference_bytes(n_elements: int) -> int:

@@ -347,6 +347,36 @@ def int4_linear_skinny(
     return y.reshape(*batch, tw.rows)
 
 
+def int4_linear_tiled_f32(x: Tensor, tw: Int4Tiled, bias: Tensor | None = None,
+                          col_scale: Tensor | None = None) -> Tensor:
+    """``(x / col_scale) @ W.T (+ bias)`` for fp32 activations ``x [..., in]``, in fp32
+    (``sqx_int4_linear_f32``): x splits into three bf16 rows whose sum is x exactly (8 significant
+    bits each), which run through the int4 decode GEMV with fp32 outputs (exact code products, fp32
+    group scales; 64 rows per pass over the weight) and are then added.
+    ``col_scale`` is AWQ's per-input-channel scale (None: no division)."""
+    *batch, k = x.shape
+    if k != tw.cols:
+        raise ValueError(f"x has in_features={k}, weight expects {tw.cols}")
+    dev = _lib.require_device(x, tw.wt, bias, col_scale, fn="int4_linear_tiled_f32")
+    if x.dtype != torch.float32:
+        raise TypeError(f"int4_linear_tiled_f32 takes fp32 activations, got {x.dtype}")
+    x2 = x.reshape(-1, k).contiguous()
+    m = x2.shape[0]
+    y = torch.empty(m, tw.rows, dtype=torch.float32, device=dev)
+    b = None if bias is None else bias.to(torch.float32).contiguous()
+    cs = None if col_scale is None else col_scale.to(torch.float32).contiguous()
+    lib = _lib.load()
+    nb = int(lib.sqx_int4_linear_f32_workspace_bytes(m, tw.rows, tw.cols))
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.sqx_int4_linear_f32(
+            _lib.ptr(tw.wt), _lib.ptr(tw.st), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype), _lib.ptr(x2), _lib.ptr(cs),
+            _lib.ptr(y), _lib.ptr(b), m, tw.rows, tw.cols, tw.group_size, ws.data_ptr(), nb, _lib.stream_ptr(dev),
+        )
+    _lib.check(rc, "int4_linear_tiled_f32")
+    return y.reshape(*batch, tw.rows)
+
+
 _tiled_cache = _device.TensorKeyedCache()
 
 
@@ -363,19 +393,23 @@ def w4a16_linear(
     """W4A16 linear (int4_group.py:148-164): ``x [..., in]`` times INT4 weights ``q/scales``
     describing ``[out, in]``; returns ``[..., out]`` in ``x``'s dtype.
 
-    bf16/fp16 activations with ``group_size`` in (32, 64, 128) run the fused dequant kernel on a
-    tiled copy of ``q`` that is built on first use and cached until ``q`` or ``scales`` changes.
-    Other cases dequantize on the GPU (fp32, exactly as the reference) and call the library GEMM.
+    The fused dequant kernels run on a tiled copy of ``q`` that is built on first use and cached
+    until ``q`` or ``scales`` changes. bf16/fp16 activations run as they are; fp32 activations run
+    as three bf16 rows that sum to x exactly, with fp32 outputs (:func:`int4_linear_tiled_f32`). ``group_size`` must be 32, 64 or 128 (ValueError otherwise),
+    and x must be fp32, bf16 or fp16 (TypeError otherwise).
     """
-    dev = _lib.require_device(x, q, scales, bias, fn="w4a16_linear")
-    if x.dtype in (torch.bfloat16, torch.float16) and group_size in TILED_GROUPS:
-        if q.shape[1] % group_size != 0:
-            raise ValueError(f"in_features={q.shape[1]} not divisible by group_size={group_size}")
-        tw = _tiled_cache.get((q, scales), (group_size,), lambda: tile_int4(q, scales, None, group_size))
-        return int4_linear_tiled(x, tw, bias)
-    wdeq = dequantize_groupwise_int4(q, scales, group_size).to(x.dtype)
-    del dev
-    return torch.nn.functional.linear(x, wdeq, bias)
+    _lib.require_device(x, q, scales, bias, fn="w4a16_linear")
+    if group_size not in TILED_GROUPS:
+        raise ValueError(f"w4a16_linear: group_size={group_size} is not supported by the MI355X kernels "
+                         f"{TILED_GROUPS}")
+    if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise TypeError(f"w4a16_linear takes fp32, bf16 or fp16 activations, got {x.dtype}")
+    if q.shape[1] % group_size != 0:
+        raise ValueError(f"in_features={q.shape[1]} not divisible by group_size={group_size}")
+    tw = _tiled_cache.get((q, scales), (group_size,), lambda: tile_int4(q, scales, None, group_size))
+    if x.dtype == torch.float32:
+        return int4_linear_tiled_f32(x, tw, bias)
+    return int4_linear_tiled(x, tw, bias)
 
 
 # --------------------------------------------------------------------------- #

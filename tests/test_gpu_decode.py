@@ -353,7 +353,9 @@ def test_linear_rmsnorm_sumsq(lib, n, k, group):
     torch.cuda.synchronize()
     if n <= 28672:  # float64 product of the two-call form's normalised row and the dequantized weight
         w_eff = R.round_bf16(R.dequantize_groupwise_int4(q.cpu().numpy(), sc.cpu().numpy(), group))
-        _check_linear(y2, R.linear_f64(hn.float().cpu().numpy(), w_eff), f"rmsnorm from sums {k}->{n}")
+        y_ref = R.linear_f64(hn.float().cpu().numpy(), w_eff)
+        _check_linear(y2, y_ref, f"rmsnorm from sums {k}->{n}")
+        _check_linear(y1, y_ref, f"plain one-row linear {k}->{n}")  # at 28672 rows the 8-wave form
     d = (y1.float() - y2.float()).abs()
     assert float(d.max()) <= 2.0**-6 * float(y1.float().abs().max())
 

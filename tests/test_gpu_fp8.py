@@ -191,3 +191,67 @@ def test_per_head_kv_quantizers_bit_exact():
     assert K.saturated_count(over.to(DEV), scale) == F.saturated_count(over.numpy(), scale.cpu().numpy()) > 0
     with pytest.raises(ValueError, match="not per-head"):
         K.quantize_per_head(xd, scale.expand(2, -1, -1, -1))
+
+
+def _kv_block(batch=2, heads=4, tokens=16, dim=32, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(batch, heads, tokens, dim, generator=g)
+    return (x * torch.logspace(-2, 2, heads).view(1, heads, 1, 1)).to(DEV)
+
+
+def test_per_head_cache_contract():
+    """PerHeadFp8KVCache on the device: the decode contract and the laws the reference's tests state
+    (tests/quant/test_s1_s_r2.py:278-400): calibration on the first block, saturation counted and
+    landing on 448 * scale, one byte per element plus the scales once, installed scales used as given,
+    growth across appends keeps every stored code."""
+    from scratch_llm_amd.quant import fp8_kv_per_head as K
+
+    print_case("fp8 per-head cache")
+    cache = K.PerHeadFp8KVCache(n_layers=2)
+    assert cache.length == 0 and cache.get(0) is None and cache.codes(1) is None
+    assert cache.scales(0) == (None, None) and cache.saturated_fraction() == 0.0
+    x = _kv_block()
+    cache.append(0, x, x)
+    cache.advance(x.shape[2])
+    k_scale, v_scale = cache.scales(0)
+    assert torch.equal(k_scale, K.per_head_scale(x)) and torch.equal(v_scale, K.per_head_scale(x))
+    assert cache.k_saturated == 0 and cache.v_saturated == 0  # the calibration block fits its own amax
+    k_out, v_out = cache.get(0)
+    assert k_out.shape == x.shape and k_out.dtype == torch.float32
+    assert torch.equal(k_out, K.dequantize_per_head(K.quantize_per_head(x, k_scale), k_scale))
+    # a block past the calibrated range saturates, is counted, and lands on the top of the head's range
+    over = x[:, :, :1].clone()
+    over[:, 0] = over[:, 0].abs().clamp_min(1.0) * 1e4
+    n_over = K.saturated_count(over, k_scale)
+    assert n_over > 0
+    cache.append(0, over, over)
+    cache.advance(1)
+    assert cache.length == x.shape[2] + 1
+    assert cache.k_saturated == n_over and cache.v_saturated == n_over and cache.saturated_fraction() > 0
+    k_out, _ = cache.get(0)
+    assert not torch.isnan(k_out).any()
+    assert torch.allclose(k_out[:, 0, -1].abs(), torch.full_like(k_out[:, 0, -1], 448.0 * float(k_scale[0, 0, 0, 0])))
+    # many small appends grow the buffer and keep every code (the concatenation of the blocks)
+    blocks = [_kv_block(tokens=t, seed=10 + t) for t in (1, 3, 1, 40, 2)]
+    for b in blocks:
+        cache.append(1, b, -b)
+    codes_k, codes_v = cache.codes(1)
+    assert codes_k.dtype == torch.float8_e4m3fn and codes_k.element_size() == 1
+    ks, vs = cache.scales(1)
+    want_k = torch.cat([K.quantize_per_head(b, ks) for b in blocks], dim=2)
+    want_v = torch.cat([K.quantize_per_head(-b, vs) for b in blocks], dim=2)
+    assert torch.equal(codes_k.view(torch.uint8), want_k.view(torch.uint8))
+    assert torch.equal(codes_v.view(torch.uint8), want_v.view(torch.uint8))
+    n_el = 2 * (x.numel() + over.numel()) + 2 * sum(b.numel() for b in blocks)
+    assert cache.kv_bytes == n_el + 2 * 2 * x.shape[1] * 4
+    assert cache.kv_bytes < K.bf16_reference_bytes(n_el)
+    with pytest.raises(ValueError, match="holds blocks"):
+        cache.append(1, _kv_block(dim=64), _kv_block(dim=64))
+    # installed scales take precedence over calibration
+    c2 = K.PerHeadFp8KVCache(n_layers=1)
+    one = torch.ones(1, x.shape[1], 1, 1, device=DEV)
+    c2.set_scales(0, one, one)
+    c2.append(0, x * 10, x * 10)  # the loud heads pass 448 at scale 1
+    assert torch.equal(c2.scales(0)[0], one) and c2.k_saturated > 0
+    with pytest.raises(ValueError, match=r"\(1, H, 1, 1\)"):
+        c2.set_scales(0, one.view(-1), one)

@@ -148,7 +148,10 @@ def test_int8_weight_linear_config1(i8, m):
 
 
 @pytest.mark.parametrize("n,k,m,dtype", [(1000, 1024, 3, torch.bfloat16), (40, 200, 5, torch.float16),
-                                         (64, 4096, 64, torch.bfloat16), (16, 64, 100, torch.bfloat16)])
+                                         (64, 4096, 64, torch.bfloat16), (16, 64, 100, torch.bfloat16),
+                                         # the one-row form: ragged rows, fp16, a K tail, > 1024 tiles
+                                         (1000, 1024, 1, torch.bfloat16), (40, 200, 1, torch.float16),
+                                         (20000, 256, 1, torch.bfloat16)])
 def test_int8_weight_linear_ragged(i8, n, k, m, dtype):
     print_case("int8 ragged", n, k, m, dtype)
     g = torch.Generator(device=DEV).manual_seed(n + k + m)

@@ -82,3 +82,32 @@ def test_mxfp4_pair_refusals(packed, scale, match):
         modules.MXFP4Linear.from_packed(packed, scale)
     with pytest.raises(ValueError, match=match):
         nvfp4_mxfp4.dequantize_mxfp4(packed, scale)
+
+
+def test_tensor_keyed_cache_replaces_on_in_place_update():
+    """An in-place update rebuilds the derived value and replaces the entry: a weight updated twice
+    still holds one cached value, and the entry goes when the weight is garbage-collected."""
+    import gc
+
+    from scratch_llm_amd.quant import _device
+
+    cache = _device.TensorKeyedCache()
+    q = torch.arange(12, dtype=torch.int8).reshape(3, 4)
+    s = torch.ones(3, 1)
+    builds = []
+
+    def build():
+        builds.append(int(q.sum()))
+        return q.clone()
+
+    v0 = cache.get((q, s), (128,), build)
+    assert cache.get((q, s), (128,), build) is v0 and len(builds) == 1
+    for step in (1, 2):
+        q.add_(1)  # moves the version counter
+        v = cache.get((q, s), (128,), build)
+        assert torch.equal(v, q) and len(builds) == 1 + step
+        assert len(cache) == 1
+    assert cache.get((q, s), (64,), build) is not None and len(cache) == 2  # the extra key counts
+    del q, v, v0
+    gc.collect()
+    assert len(cache) == 0
