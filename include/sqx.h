@@ -536,6 +536,18 @@ int sqx_decode_attention_rope(const void* qkv, const int* lengths, const float* 
                               int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws, int64_t ws_bytes,
                               sqx_stream_t stream);
 
+/* sqx_decode_attention_rope without a workspace argument and without any allocation. No counterpart in
+ * the reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). The key-split partials go to a fixed 8 MiB device array
+ * inside the library (one per GPU, held until the process ends), so the shape must satisfy
+ * sqx_attn_workspace_bytes(B, H, Hkv, tmax) <= 8 MiB (e.g. B = 64, H = 32, Hkv = 8, tmax = 2048
+ * needs 4.3 MB); larger shapes return SQX_E_SPACE without launching. The stream's device must be the
+ * current device. Calls that overlap on one GPU share that array and race; calls in one stream are
+ * ordered. Other arguments and results as sqx_decode_attention_rope, bit for bit. */
+int sqx_decode_attention_rope_noalloc(const void* qkv, const int* lengths, const float* cos_t, const float* sin_t,
+                                      int64_t rope_rows, void* k_cache, void* v_cache, int64_t B, int64_t H,
+                                      int64_t Hkv, int64_t hd, int64_t tmax, void* out, sqx_stream_t stream);
+
 /* The two attention calls above on an FP8 cache (the per-head E4M3 cache of fp8_kv_per_head.py:120-223
  * as the slot cache): k/v hold E4M3 codes [B, Hkv, tmax, hd] (one byte each) with fp32 scales
  * k_scale, v_scale [Hkv]; attention runs on code * scale. The _rope variant quantizes the new key and

@@ -158,6 +158,10 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_i,
         [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p],
     ),
+    "sqx_decode_attention_rope_noalloc": (
+        _c_i,
+        [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p],
+    ),
     "sqx_decode_attention_fp8kv": (
         _c_i,
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p],

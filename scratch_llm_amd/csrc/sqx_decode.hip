@@ -11,6 +11,7 @@
 // j <= lengths[b] (write-then-mask, model.py:293-305). All arithmetic is fp32; each written tensor
 // is rounded to bf16 once (round to nearest even).
 #include <algorithm>
+#include <mutex>
 
 #include "sqx_common.h"
 
@@ -814,6 +815,60 @@ extern "C" int sqx_decode_attention_rope(const void* qkv, const int* lengths, co
   SQX_REQUIRE(cos_t != nullptr, SQX_E_ARG, "sqx_decode_attention_rope: null cos table");
   return decode_attention_impl(qkv, k_cache, v_cache, lengths, cos_t, sin_t, rope_rows, nullptr, nullptr, B, H, Hkv, hd,
                                tmax, out, ws, ws_bytes, stream, "sqx_decode_attention_rope");
+}
+
+// ---------------------------------------------------------------------------------------------
+// The allocation-free form of sqx_decode_attention_rope, for callers that cannot allocate (code under
+// HIP graph capture, tight serving loops): the key-split partials go to `scratch`, a file-scope device
+// array of kNoAllocScratchBytes, instead of a caller workspace. Every GPU the library runs on holds its
+// own copy until the process ends. In host code the array's name is not a device address: its address
+// on the current device comes from hipGetSymbolAddress, looked up once per device on the first call
+// with that device current and kept in scratch_ptr[]. Each call writes every partial the combine
+// reads (the chunks below the row's length), so nothing has to start cleared; calls that overlap on
+// one GPU share the array and race.
+// ---------------------------------------------------------------------------------------------
+constexpr int64_t kNoAllocScratchBytes = int64_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[kScratchDevices] = {};
+
+int scratch_on_current_device(void** out, const char* fn) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: hipGetDevice failed: %s", fn, hipGetErrorString(e));
+  SQX_REQUIRE(dev >= 0 && dev < kScratchDevices, SQX_E_ARG, "%s: device %d out of range", fn, dev);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    SQX_REQUIRE(e == hipSuccess && p != nullptr, SQX_E_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev,
+                hipGetErrorString(e));
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return SQX_OK;
+}
+}  // namespace
+
+extern "C" int sqx_decode_attention_rope_noalloc(const void* qkv, const int* lengths, const float* cos_t,
+                                                 const float* sin_t, int64_t rope_rows, void* k_cache, void* v_cache,
+                                                 int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax,
+                                                 void* out, sqx_stream_t stream) {
+  const char* fn = "sqx_decode_attention_rope_noalloc";
+  SQX_REQUIRE(cos_t != nullptr, SQX_E_ARG, "%s: null cos table", fn);
+  const int64_t need = sqx_attn_workspace_bytes(B, H, Hkv, tmax);
+  SQX_REQUIRE(need <= kNoAllocScratchBytes, SQX_E_SPACE,
+              "%s: B=%lld H=%lld Hkv=%lld tmax=%lld needs %lld bytes of partials, more than the fixed %lld bytes of "
+              "scratch (use sqx_decode_attention_rope with a workspace)",
+              fn, (long long)B, (long long)H, (long long)Hkv, (long long)tmax, (long long)need,
+              (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (int rc = scratch_on_current_device(&ws, fn)) return rc;
+  return decode_attention_impl(qkv, k_cache, v_cache, lengths, cos_t, sin_t, rope_rows, nullptr, nullptr, B, H, Hkv, hd,
+                               tmax, out, ws, kNoAllocScratchBytes, stream, fn);
 }
 
 extern "C" int sqx_decode_attention_fp8kv(const void* q, const void* k_codes, const void* v_codes, const float* k_scale,
