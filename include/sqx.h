@@ -35,6 +35,7 @@ enum {
   SQX_FP4_SCALE_MX_F32 = 0,  /* MXFP4 s_block as fp32 powers of two [rows, cols/32] */
   SQX_FP4_SCALE_MX_E8M0 = 1, /* MXFP4 scales as E8M0 bytes [rows, cols/32] (the on-disk form) */
   SQX_FP4_SCALE_NV_F32 = 2,  /* NVFP4 s_block as fp32 E4M3 values [rows, cols/16] */
+  SQX_FP4_SCALE_NV_E4M3 = 3, /* NVFP4 scales as E4M3 bytes [rows, cols/16] (sqx_nvfp4_ceil_quantize's) */
 };
 
 /* status codes */
@@ -296,10 +297,36 @@ int64_t sqx_fp4_tiled_scale_bytes(int64_t rows, int64_t cols, int fmt);
  * E2M1 codes, unpacked (codes_packed = 0, one per byte) or in the reference's packed row-major
  * stream (codes_packed = 1, pack_fp4 order, also the on-disk weight_packed of k3/checkpoint.py:92-144).
  * scales by scale_kind, one per `block` columns of a row: SQX_FP4_SCALE_MX_F32 (s_block fp32
- * [rows, cols/block], block a multiple of 32), SQX_FP4_SCALE_MX_E8M0 (bytes, same shape) or
- * SQX_FP4_SCALE_NV_F32 (s_block fp32 E4M3 values [rows, cols/block], block a multiple of 16). */
+ * [rows, cols/block], block a multiple of 32), SQX_FP4_SCALE_MX_E8M0 (bytes, same shape),
+ * SQX_FP4_SCALE_NV_F32 (s_block fp32 E4M3 values [rows, cols/block], block a multiple of 16) or
+ * SQX_FP4_SCALE_NV_E4M3 (the same scales as E4M3 bytes). */
 int sqx_fp4_tile(const uint8_t* codes, int codes_packed, const void* scales, int scale_kind, int64_t block,
                  int64_t rows, int64_t cols, uint8_t* wt, uint8_t* st, sqx_stream_t stream);
+
+/* The second NVFP4 convention, the b_r6 GEMM rung's operands (kernels/gemm/cuda/b_r6.py:155-244 with
+ * kernels/gemm/nvfp4_layout.py:341-416). Per block of 16 along k, in float64: scale = the smallest
+ * unsigned-E4M3 value >= amax / 6 (ceil onto the grid; no global scale; an all-zero block gets 0),
+ * code = the nearest E2M1 magnitude of x / scale with ties to the even magnitude index (saturating
+ * at 6), the sign bit only on a non-zero magnitude. x: [rows, k] of dtype (F32 / BF16 / F16), k a
+ * multiple of 16; packed: uint8 [rows, k/2], the lower k in the low nibble (the reference's bytes);
+ * scales: uint8 [rows, k/16] row-major E4M3 codes (the reference swizzles them for CUTLASS; this
+ * layout is the library's). *status (device int, zeroed by the caller) gets bit 0 for a NaN or Inf
+ * input and bit 1 for a block whose amax / 6 exceeds 448; the reference raises on both. */
+int sqx_nvfp4_ceil_quantize(const void* x, int dtype, int64_t rows, int64_t k, uint8_t* packed,
+                            uint8_t* scales, int* status, sqx_stream_t stream);
+
+/* dequantize_nvfp4 (b_r6.py:228-244): out = e2m1 value * scale, exact in F32 and in BF16 (out_dtype). */
+int sqx_nvfp4_ceil_dequantize(const uint8_t* packed, const uint8_t* scales, int64_t rows, int64_t k, void* out,
+                              int out_dtype, sqx_stream_t stream);
+
+/* Elementwise forms of the scalar rules (nvfp4_layout.py:341-416) over float64 device arrays:
+ * sqx_ue4m3_ceil: codes[i] = ue4m3_ceil_code(v[i] / divisor) and values[i] its value (values may be
+ * NULL); divisor 6 gives scale_for_amax (amax 0 -> code 0). Status bit 0: a negative or non-finite
+ * v; bit 1: v / divisor > 448 (the code is then 0). sqx_e2m1_round_rne: e2m1_round_code (status bit
+ * 0 for NaN or Inf). */
+int sqx_ue4m3_ceil(const double* v, int64_t n, double divisor, uint8_t* codes, double* values, int* status,
+                   sqx_stream_t stream);
+int sqx_e2m1_round_rne(const double* v, int64_t n, uint8_t* codes, int* status, sqx_stream_t stream);
 
 /* FP4 weight linear: y[m, r] = sum_c x[m, c] * W[r, c] (* *s_global for NVFP4) (+ bias[r]) with W the
  * dequantized tiled weight: the config-4 MXFP4 linear F.linear(x, mxfp4_dequantize(W).to(x.dtype))

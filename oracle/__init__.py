@@ -12,6 +12,9 @@ Modules:
               round-half-to-even), plus float64 linears for tolerance checks.
   torch_path  the reference's own CPU linear path (torch dequantize, then ``F.linear``), restated
               with torch on the CPU; timed as the CPU baseline.
+  nvfp4_ceil_ref  numpy restatement of the second NVFP4 convention (the b_r6 GEMM rung's operands:
+              ceil-rounded UE4M3 block scales, E2M1 ties to even), float64 as the reference.
+  decode_ref, fp8_ref  the decode step and the FP8 quantizers (see their docstrings).
 
 Pinning status of every function is listed in quant_ref's module docstring.
 """

@@ -24,6 +24,7 @@ FP4_NV = 1
 FP4_SCALE_MX_F32 = 0
 FP4_SCALE_MX_E8M0 = 1
 FP4_SCALE_NV_F32 = 2
+FP4_SCALE_NV_E4M3 = 3
 
 _TORCH_TO_SQX = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
 
@@ -109,6 +110,10 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_i,
         [_c_p, _c_p, _c_i, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
     ),
+    "sqx_nvfp4_ceil_quantize": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p]),
+    "sqx_nvfp4_ceil_dequantize": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i, _c_p]),
+    "sqx_ue4m3_ceil": (_c_i, [_c_p, _c_i64, ctypes.c_double, _c_p, _c_p, _c_p, _c_p]),
+    "sqx_e2m1_round_rne": (_c_i, [_c_p, _c_i64, _c_p, _c_p, _c_p]),
     "sqx_split_bf16": (_c_i, [_c_p, _c_i64, _c_p, _c_p, _c_p]),
     "sqx_sum_halves": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
     "sqx_int8_workspace_bytes": (_c_i64, []),

@@ -331,7 +331,8 @@ __global__ __launch_bounds__(256) void fp4_tile_weights_kernel(const uint8_t* __
 }
 
 // KIND: 0 = MXFP4 scales from fp32 powers of two (s_block), 1 = MXFP4 scales as E8M0 bytes,
-// 2 = NVFP4 scales from fp32 E4M3 values; the source holds one scale per `block` columns (a
+// 2 = NVFP4 scales from fp32 E4M3 values, 3 = NVFP4 scales as E4M3 bytes; the source holds one
+// scale per `block` columns (a
 // multiple of the 32 / 16 columns a scale byte covers). One thread per output scale byte.
 template <int KIND>
 __global__ __launch_bounds__(256) void fp4_tile_scales_kernel(const void* __restrict__ src, int64_t rows,
@@ -339,20 +340,21 @@ __global__ __launch_bounds__(256) void fp4_tile_scales_kernel(const void* __rest
                                                               int64_t n_out, uint8_t* __restrict__ st) {
   const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (o >= n_out) return;
-  constexpr int PER_BLOCK = KIND == 2 ? 128 : 64;
+  constexpr bool NVK = KIND >= 2;  // NVFP4: two 16-column scales per lane
+  constexpr int PER_BLOCK = NVK ? 128 : 64;
   const int64_t blk = o / PER_BLOCK;
   const int j = static_cast<int>(o - blk * PER_BLOCK);
-  const int L = KIND == 2 ? (j >> 1) : j;
+  const int L = NVK ? (j >> 1) : j;
   const int64_t t = blk / KB;
   const int64_t kb = blk - t * KB;
   const int64_t r = 16 * t + (L & 15);
-  const int64_t c0 = kb * 128 + 32 * (L >> 4) + (KIND == 2 ? 16 * (j & 1) : 0);
+  const int64_t c0 = kb * 128 + 32 * (L >> 4) + (NVK ? 16 * (j & 1) : 0);
   uint32_t byte = 0;
   if (r < rows && c0 < cols) {
     const int64_t si = r * (cols / block) + c0 / block;  // the source block holding column c0
     if (KIND == 2) {
       byte = e4m3_byte(static_cast<const float*>(src)[si]);
-    } else if (KIND == 1) {
+    } else if (KIND == 1 || KIND == 3) {
       byte = static_cast<const uint8_t*>(src)[si];
     } else {
       const float s = static_cast<const float*>(src)[si];
@@ -436,6 +438,141 @@ static hipError_t launch_fp4(const uint8_t* wt, const uint8_t* st, const float* 
   using W = WFp4<NV>;
   const typename W::Args a{wt, st, s_global};
   return gemv_launch<A, W, 4, 2, YF32>(a, x, y, bias, nullptr, m, rows, cols, k_slices, s);
+}
+
+// ----------------------------------------------------------------------------------------------
+// The second NVFP4 convention (the b_r6 rung's operands, kernels/gemm/cuda/b_r6.py:155-244 with the
+// scalar rules of kernels/gemm/nvfp4_layout.py:341-416): per block of 16 along k, in float64,
+// scale = the smallest unsigned-E4M3 value >= amax / 6 (no global scale), code = the nearest E2M1
+// magnitude of x / scale with ties to the even magnitude index, sign only on a non-zero magnitude,
+// two codes per byte with the lower k in the low nibble. Scales are stored as E4M3 codes in a
+// row-major [rows, k/16] byte array (this library's layout; the E4M3 byte of a positive value is its
+// unsigned-E4M3 code). Problems are reported through a status word: bit 0 = a NaN or Inf input,
+// bit 1 = a block whose amax / 6 exceeds 448.
+// ----------------------------------------------------------------------------------------------
+constexpr int kCeilNonFinite = 1, kCeilRange = 2;
+
+__device__ inline double ue4m3_value_d(uint32_t c) {
+  const uint32_t e = (c >> 3) & 15u, m = c & 7u;
+  return e == 0 ? static_cast<double>(m) * 0x1p-9 : ldexp(1.0 + static_cast<double>(m) * 0.125, static_cast<int>(e) - 7);
+}
+
+// Smallest unsigned-E4M3 code whose value is >= v, for finite v >= 0; 0x7F when v > 448. Every step
+// is exact in float64: the subnormal grid is m * 2^-9 (and code 8 is 2^-6), a normal value is
+// (1 + m/8) * 2^e, so the mantissa step of v's binade is one ceil of an exact scaled value.
+__device__ inline uint32_t ue4m3_ceil_d(double v) {
+  if (v <= 0.0) return 0u;
+  if (v <= 0x1p-6) return static_cast<uint32_t>(ceil(v * 512.0));
+  int e2;
+  const double f = frexp(v, &e2);  // v = f * 2^e2, f in [0.5, 1)
+  int ex = e2 - 1;
+  int m = static_cast<int>(ceil((2.0 * f - 1.0) * 8.0));
+  if (m == 8) {
+    m = 0;
+    ++ex;
+  }
+  const int eb = ex + 7;
+  if (eb > 15 || (eb == 15 && m == 7)) return 0x7Fu;
+  return static_cast<uint32_t>((eb << 3) | m);
+}
+
+// E2M1 magnitude index of a >= 0: round to nearest, ties to the even index, 7 (6.0) past 5.
+__device__ inline uint32_t e2m1_rne_index(double a) {
+  const uint32_t lo = (a > 0.25) + (a > 0.75) + (a > 1.25) + (a > 1.75) + (a > 2.5) + (a > 3.5) + (a > 5.0);
+  const uint32_t hi = (a >= 0.25) + (a >= 0.75) + (a >= 1.25) + (a >= 1.75) + (a >= 2.5) + (a >= 3.5) + (a >= 5.0);
+  return (hi > lo && (lo & 1u)) ? hi : lo;
+}
+
+__device__ inline uint32_t e2m1_rne_code(double y) {
+  const uint32_t i = e2m1_rne_index(fabs(y));
+  return i | ((y < 0.0 && i != 0u) ? 8u : 0u);
+}
+
+// One thread per block of 16: packed [rows, k/2] (8 bytes per block), scale codes [rows, k/16].
+__global__ __launch_bounds__(256) void nvfp4_ceil_quantize_kernel(const void* __restrict__ x, int dtype, int64_t nblk,
+                                                                  uint8_t* __restrict__ packed,
+                                                                  uint8_t* __restrict__ scales, int* __restrict__ status) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (b >= nblk) return;
+  float v[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) v[j] = load_as_f32(x, dtype, b * 16 + j);
+  float amax = 0.0f;
+  bool finite = true;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    finite = finite && isfinite(v[j]);
+    amax = fmaxf(amax, fabsf(v[j]));
+  }
+  int bad = finite ? 0 : kCeilNonFinite;
+  uint32_t code = 0u;
+  double scale = 0.0;
+  if (finite) {
+    code = ue4m3_ceil_d(static_cast<double>(amax) / 6.0);
+    if (code == 0x7Fu) {
+      bad |= kCeilRange;
+      code = 0u;
+    }
+    scale = ue4m3_value_d(code);
+  }
+  if (bad) atomicOr(status, bad);
+  const double div = scale > 0.0 ? scale : 1.0;
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t c = finite ? e2m1_rne_code(static_cast<double>(v[j]) / div) : 0u;
+    w[j >> 3] |= c << (4 * (j & 7));
+  }
+  *reinterpret_cast<u32x2v_t*>(packed + b * 8) = u32x2v_t{w[0], w[1]};
+  scales[b] = static_cast<uint8_t>(code);
+}
+
+// One thread per block of 16: fp32 (YB16 = false) or bf16 code value * scale (exact in both).
+template <bool YB16>
+__global__ __launch_bounds__(256) void nvfp4_ceil_dequantize_kernel(const uint8_t* __restrict__ packed,
+                                                                    const uint8_t* __restrict__ scales, int64_t nblk,
+                                                                    void* __restrict__ out) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (b >= nblk) return;
+  const u32x2v_t w = *reinterpret_cast<const u32x2v_t*>(packed + b * 8);
+  const float sc = static_cast<float>(ue4m3_value_d(scales[b]));
+  constexpr float kMag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t c = (w[j >> 3] >> (4 * (j & 7))) & 0xFu;
+    const float val = (c & 8u ? -kMag[c & 7u] : kMag[c & 7u]) * sc;
+    if (YB16)
+      static_cast<uint16_t*>(out)[b * 16 + j] = f32_to_bf16_bits(val);
+    else
+      static_cast<float*>(out)[b * 16 + j] = val;
+  }
+}
+
+// Elementwise: codes of the smallest unsigned-E4M3 value >= v / divisor (and that value), or the
+// E2M1 round-to-nearest-even codes of v (MODE 1).
+template <int MODE>
+__global__ __launch_bounds__(256) void nvfp4_ceil_elem_kernel(const double* __restrict__ v, int64_t n, double divisor,
+                                                              uint8_t* __restrict__ codes, double* __restrict__ values,
+                                                              int* __restrict__ status) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const double a = v[i];
+  uint32_t c = 0u;
+  int bad = 0;
+  if (!isfinite(a) || (MODE == 0 && a < 0.0)) {
+    bad = kCeilNonFinite;
+  } else if (MODE == 0) {
+    c = ue4m3_ceil_d(a / divisor);
+    if (c == 0x7Fu) {
+      bad = kCeilRange;
+      c = 0u;
+    }
+    if (values) values[i] = ue4m3_value_d(c);
+  } else {
+    c = e2m1_rne_code(a);
+  }
+  if (bad) atomicOr(status, bad);
+  codes[i] = static_cast<uint8_t>(c);
 }
 
 // ----------------------------------------------------------------------------------------------
@@ -595,9 +732,9 @@ extern "C" int sqx_fp4_tile(const uint8_t* codes, int codes_packed, const void* 
                             int64_t rows, int64_t cols, uint8_t* wt, uint8_t* st, sqx_stream_t stream) {
   SQX_REQUIRE(rows > 0 && cols > 0 && rows <= ((int64_t)1 << 30) && cols <= ((int64_t)1 << 30), SQX_E_ARG,
               "sqx_fp4_tile: bad shape [%lld, %lld]", (long long)rows, (long long)cols);
-  SQX_REQUIRE(scale_kind >= SQX_FP4_SCALE_MX_F32 && scale_kind <= SQX_FP4_SCALE_NV_F32, SQX_E_ARG,
+  SQX_REQUIRE(scale_kind >= SQX_FP4_SCALE_MX_F32 && scale_kind <= SQX_FP4_SCALE_NV_E4M3, SQX_E_ARG,
               "sqx_fp4_tile: bad scale_kind %d", scale_kind);
-  const bool nv = scale_kind == SQX_FP4_SCALE_NV_F32;
+  const bool nv = scale_kind == SQX_FP4_SCALE_NV_F32 || scale_kind == SQX_FP4_SCALE_NV_E4M3;
   SQX_REQUIRE(block > 0 && block % (nv ? 16 : 32) == 0 && cols % block == 0, SQX_E_ARG,
               "sqx_fp4_tile: block %lld must be a multiple of %d that divides cols=%lld", (long long)block,
               nv ? 16 : 32, (long long)cols);
@@ -617,8 +754,10 @@ extern "C" int sqx_fp4_tile(const uint8_t* codes, int codes_packed, const void* 
     hipLaunchKernelGGL(fp4_tile_scales_kernel<0>, grid_for(ns), dim3(256), 0, s, scales, rows, cols, block, KB, ns, st);
   else if (scale_kind == SQX_FP4_SCALE_MX_E8M0)
     hipLaunchKernelGGL(fp4_tile_scales_kernel<1>, grid_for(ns), dim3(256), 0, s, scales, rows, cols, block, KB, ns, st);
-  else
+  else if (scale_kind == SQX_FP4_SCALE_NV_F32)
     hipLaunchKernelGGL(fp4_tile_scales_kernel<2>, grid_for(ns), dim3(256), 0, s, scales, rows, cols, block, KB, ns, st);
+  else
+    hipLaunchKernelGGL(fp4_tile_scales_kernel<3>, grid_for(ns), dim3(256), 0, s, scales, rows, cols, block, KB, ns, st);
   SQX_LAUNCH_CHECK("sqx_fp4_tile");
   return SQX_OK;
 }
@@ -703,5 +842,62 @@ extern "C" int sqx_sum_halves(const float* y2, int64_t n, float* y, sqx_stream_t
   SQX_REQUIRE(y2 && y, SQX_E_ARG, "sqx_sum_halves: null pointer");
   hipLaunchKernelGGL(sum_halves_kernel, grid_for(n), dim3(256), 0, as_stream(stream), y2, n, y);
   SQX_LAUNCH_CHECK("sqx_sum_halves");
+  return SQX_OK;
+}
+
+extern "C" int sqx_nvfp4_ceil_quantize(const void* x, int dtype, int64_t rows, int64_t k, uint8_t* packed,
+                                       uint8_t* scales, int* status, sqx_stream_t stream) {
+  SQX_REQUIRE(is_float_dtype(dtype), SQX_E_ARG, "sqx_nvfp4_ceil_quantize: bad dtype %d", dtype);
+  SQX_REQUIRE(rows >= 0 && k > 0 && k % 16 == 0, SQX_E_ARG,
+              "quantize_nvfp4: K=%lld is not a multiple of SF_VEC_SIZE=16", (long long)k);
+  const int64_t nblk = rows * (k / 16);
+  if (nblk == 0) return SQX_OK;
+  SQX_REQUIRE(x && packed && scales && status, SQX_E_ARG, "sqx_nvfp4_ceil_quantize: null pointer");
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(packed) % 8 == 0, SQX_E_ARG,
+              "sqx_nvfp4_ceil_quantize: packed must be 8-byte aligned");
+  hipLaunchKernelGGL(nvfp4_ceil_quantize_kernel, grid_for(nblk), dim3(256), 0, as_stream(stream), x, dtype, nblk, packed,
+                     scales, status);
+  SQX_LAUNCH_CHECK("sqx_nvfp4_ceil_quantize");
+  return SQX_OK;
+}
+
+extern "C" int sqx_nvfp4_ceil_dequantize(const uint8_t* packed, const uint8_t* scales, int64_t rows, int64_t k,
+                                         void* out, int out_dtype, sqx_stream_t stream) {
+  SQX_REQUIRE(rows >= 0 && k > 0 && k % 16 == 0, SQX_E_ARG, "sqx_nvfp4_ceil_dequantize: bad shape");
+  SQX_REQUIRE(out_dtype == SQX_DTYPE_F32 || out_dtype == SQX_DTYPE_BF16, SQX_E_ARG,
+              "sqx_nvfp4_ceil_dequantize: out_dtype must be F32 or BF16");
+  const int64_t nblk = rows * (k / 16);
+  if (nblk == 0) return SQX_OK;
+  SQX_REQUIRE(packed && scales && out, SQX_E_ARG, "sqx_nvfp4_ceil_dequantize: null pointer");
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(packed) % 8 == 0, SQX_E_ARG,
+              "sqx_nvfp4_ceil_dequantize: packed must be 8-byte aligned");
+  if (out_dtype == SQX_DTYPE_BF16)
+    hipLaunchKernelGGL(nvfp4_ceil_dequantize_kernel<true>, grid_for(nblk), dim3(256), 0, as_stream(stream), packed,
+                       scales, nblk, out);
+  else
+    hipLaunchKernelGGL(nvfp4_ceil_dequantize_kernel<false>, grid_for(nblk), dim3(256), 0, as_stream(stream), packed,
+                       scales, nblk, out);
+  SQX_LAUNCH_CHECK("sqx_nvfp4_ceil_dequantize");
+  return SQX_OK;
+}
+
+extern "C" int sqx_ue4m3_ceil(const double* v, int64_t n, double divisor, uint8_t* codes, double* values, int* status,
+                              sqx_stream_t stream) {
+  SQX_REQUIRE(n >= 0 && divisor > 0.0, SQX_E_ARG, "sqx_ue4m3_ceil: bad n or divisor");
+  if (n == 0) return SQX_OK;
+  SQX_REQUIRE(v && codes && status, SQX_E_ARG, "sqx_ue4m3_ceil: null pointer");
+  hipLaunchKernelGGL(nvfp4_ceil_elem_kernel<0>, grid_for(n), dim3(256), 0, as_stream(stream), v, n, divisor, codes, values,
+                     status);
+  SQX_LAUNCH_CHECK("sqx_ue4m3_ceil");
+  return SQX_OK;
+}
+
+extern "C" int sqx_e2m1_round_rne(const double* v, int64_t n, uint8_t* codes, int* status, sqx_stream_t stream) {
+  SQX_REQUIRE(n >= 0, SQX_E_ARG, "sqx_e2m1_round_rne: negative n");
+  if (n == 0) return SQX_OK;
+  SQX_REQUIRE(v && codes && status, SQX_E_ARG, "sqx_e2m1_round_rne: null pointer");
+  hipLaunchKernelGGL(nvfp4_ceil_elem_kernel<1>, grid_for(n), dim3(256), 0, as_stream(stream), v, n, 1.0, codes, nullptr,
+                     status);
+  SQX_LAUNCH_CHECK("sqx_e2m1_round_rne");
   return SQX_OK;
 }
