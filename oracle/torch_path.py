@@ -47,3 +47,10 @@ def mxfp4_dequantize_packed(packed: torch.Tensor, e8m0: torch.Tensor, rows: int,
 def mxfp4_linear(x: torch.Tensor, packed: torch.Tensor, e8m0: torch.Tensor, rows: int, cols: int, bias=None):
     """BASELINE config 4 oracle composition: F.linear(x, mxfp4_dequantize(W).to(x.dtype))."""
     return F.linear(x, mxfp4_dequantize_packed(packed, e8m0, rows, cols).to(x.dtype), bias)
+
+
+def awq_linear(x: torch.Tensor, q: torch.Tensor, group_scales: torch.Tensor, chan_scale: torch.Tensor, bias=None,
+               group_size: int = 128):
+    """awq.py:178-192: W_eff = dequantize(q, group_scales) / chan_scale, cast to x's dtype, F.linear."""
+    w = dequantize_groupwise_int4(q, group_scales, group_size) / chan_scale.to(torch.float32).view(1, -1)
+    return F.linear(x, w.to(x.dtype), bias)
