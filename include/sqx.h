@@ -172,18 +172,20 @@ int sqx_int4_linear_silu(const uint8_t* wt, const float* st, const void* gate_up
  * after the norm forms the norm from those sums while it loads its activations. m must be 1.
  *
  * sqx_int4_linear_residual: res_out = bf16(res + bf16(x @ W^T)) [rows] (res_out may be res), and
- * ss_out[t] = sum of res_out[16t .. 16t+15]^2 (fp32, ceil(rows/16) entries). The linear is the GEMV
- * form of sqx_int4_linear with the same k_slices, bit for bit, and the add rounds as the reference's
- * bf16 tensor add. Weight format as sqx_int4_linear_rmsnorm. */
+ * ss_out[t] = sum of res_out[16t .. 16t+15]^2 (fp32, ceil(rows/16) entries). With gain_next (bf16
+ * [rows], the next RMSNorm's gain) it also writes hg_out = bf16(res_out * gain_next) [rows], the input
+ * sqx_int4_linear_rowscale_sumsq takes (both NULL otherwise). The linear is the GEMV form of
+ * sqx_int4_linear with the same k_slices, bit for bit, and the add rounds as the reference's bf16
+ * tensor add. Weight format as sqx_int4_linear_rmsnorm. */
 int sqx_int4_linear_residual(const uint8_t* wt, const float* st, const void* x, const void* res, void* res_out,
-                             float* ss_out, int64_t m, int64_t rows, int64_t cols, int64_t group, int k_slices,
-                             sqx_stream_t stream);
+                             float* ss_out, const void* gain_next, void* hg_out, int64_t m, int64_t rows, int64_t cols,
+                             int64_t group, int k_slices, sqx_stream_t stream);
 
 /* sqx_int4_linear_silu with the residual epilogue of sqx_int4_linear_residual (the MLP's down
  * projection). */
 int sqx_int4_linear_silu_residual(const uint8_t* wt, const float* st, const void* gate_up, const void* res,
-                                  void* res_out, float* ss_out, int64_t m, int64_t rows, int64_t cols, int64_t group,
-                                  int k_slices, sqx_stream_t stream);
+                                  void* res_out, float* ss_out, const void* gain_next, void* hg_out, int64_t m,
+                                  int64_t rows, int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
 
 /* y = rmsnorm(h) @ W^T for one row h [cols] whose sums of squares per 16 columns are ss [nss],
  * nss = ceil(cols/16) <= 512 (as sqx_int4_linear_residual leaves them): the norm is the reference's
@@ -194,6 +196,16 @@ int sqx_int4_linear_silu_residual(const uint8_t* wt, const float* st, const void
 int sqx_int4_linear_rmsnorm_sumsq(const uint8_t* wt, const float* st, const void* h, const float* ss, int64_t nss,
                                   const void* gain, float eps, void* y, int64_t m, int64_t rows, int64_t cols,
                                   int64_t group, int k_slices, sqx_stream_t stream);
+
+/* The same linear after RMSNorm with the norm's row factor moved past the product (one row):
+ * y = bf16(r * (hg @ W^T)), r = 1 / sqrt(sum(ss) / cols + eps), where hg = bf16(h * gain) as
+ * sqx_int4_linear_residual leaves it and ss the sums of squares of h per 16 columns (nss =
+ * ceil(cols/16) <= 512, 16-byte aligned). The reference rounds the normalised row bf16(h * r * gain)
+ * once before the product; here bf16(h * gain) is rounded and r scales the fp32 sum, the same bound
+ * with another rounding. The GEMV runs its plain one-row form, without a per-wave prologue. */
+int sqx_int4_linear_rowscale_sumsq(const uint8_t* wt, const float* st, const void* hg, const float* ss, int64_t nss,
+                                   float eps, void* y, int64_t m, int64_t rows, int64_t cols, int64_t group,
+                                   int k_slices, sqx_stream_t stream);
 
 /* Build-defined asymmetric uint4, group-wise (BASELINE config 2's "asymmetric, bf16 scale/zero";
  * no reference symbol: the 4-bit form of quantize_affine, int8.py:142-172, per group):

@@ -96,9 +96,14 @@ struct has_row_scale<W, std::void_t<decltype(W::kRowScale)>> : std::integral_con
 //                tiles, as the residual epilogue of the linear that wrote h leaves them:
 //                bf16(h * (1 / sqrt(sum(ss_in) / K + eps)) * gain), the standalone kernel's arithmetic
 //                with the sum of squares added in another order.
+//   kProScaleSum (one row) RMSNorm's row factor moved past the linear: x is bf16(h * gain) as given
+//                (the residual epilogue of the linear that wrote h can write it), and the output is
+//                r * (x W^T) with r = 1 / sqrt(sum(ss_in) / K + eps), ss_in as for kProNormSum. Wave 0
+//                copies the sums straight into LDS (buffer loads that write LDS, issued behind its
+//                activation slice, so no registers hold them) and forms r before the epilogue.
 // RES (one row): the residual epilogue. The output is res_out = bf16(res + bf16(x W^T)) (the decode
 // step's h = x + o_proj(...), model.py:365-372), and ss_out[t] is the sum of its squares over tile t.
-enum { kProPlain = 0, kProResNorm = 1, kProSiluGate = 2, kProNormSum = 3 };
+enum { kProPlain = 0, kProResNorm = 1, kProSiluGate = 2, kProNormSum = 3, kProScaleSum = 4 };
 static constexpr int kProMaxRows = 8;
 static constexpr int kNormSumMax = 512;  // tiles of sums of squares a kProNormSum prologue reads (K <= 8192)
 
@@ -107,11 +112,13 @@ struct ProArgs {
   const uint16_t* gain;   // kProResNorm, kProNormSum: RMSNorm gain [K]
   uint16_t* h_out;        // kProResNorm: x + delta [M, K] (written when delta is given)
   float eps;
-  const float* ss_in;     // kProNormSum: sums of squares of x per 16-column tile [nss]
+  const float* ss_in;     // kProNormSum, kProScaleSum: sums of squares of h per 16-column tile [nss]
   int nss;
   const uint16_t* res;    // RES: residual [N]
   uint16_t* res_out;      // RES: res + the linear's output [N] (may be res)
   float* ss_out;          // RES: sum of res_out^2 per 16-row tile [ceil(N / 16)]
+  const uint16_t* gain_next;  // RES: when set, hg_out = bf16(res_out * gain_next) [N] as well
+  uint16_t* hg_out;
 };
 
 template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32, int PRO = kProPlain, int ONE = 0,
@@ -122,9 +129,10 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
                                                     int kbw, const ProArgs pa) {
   static_assert(PRO == kProPlain || (XLDS && MCH == 1), "activation prologues need the LDS copy");
   static_assert(ONE == 0 || (XLDS && MCH == 1 && U == 4), "the one-row form reads four-block rounds from LDS");
-  static_assert(ONE < 2 || PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate,
+  static_assert(ONE < 2 || PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate || PRO == kProScaleSum,
                 "a prologue over the whole row needs the workgroup's copy of the activations");
-  static_assert(PRO != kProNormSum || ONE >= 2, "the norm from tile sums runs in each wave's own slice");
+  static_assert((PRO != kProNormSum && PRO != kProScaleSum) || ONE >= 2,
+                "the norm from tile sums runs in each wave's own slice");
   static_assert(!RES || ONE != 0, "the residual epilogue is a one-row form");
   static_assert(ONE == 0 || !YF32, "the one-row form writes 16-bit outputs");
   extern __shared__ f32x4_t smem[];  // [NW][MCH][64] partial accumulators, then (XLDS) the activations
@@ -140,6 +148,16 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
 
   const typename W::Ctx wc = W::ctx(wa, t, KB, lane);
   const rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * (PRO == kProSiluGate ? 4u : 2u));
+  // RES: wave 0 requests its lanes' residual (and next-norm gain) values now, so that the epilogue of
+  // small grids (wave 0 finishes the tile) does not wait for them; lanes 16..63 read neighbours or zero.
+  [[maybe_unused]] uint32_t res_pre = 0u, gain_pre = 0u;
+  if constexpr (RES) {
+    if (wave == 0) {  // wave-uniform
+      const uint32_t off = (uint32_t)(t * 16 + (lane & 15)) * 2u;
+      res_pre = bload16(make_rsrc(pa.res, (uint32_t)N * 2u), off, 0u);
+      if (pa.gain_next != nullptr) gain_pre = bload16(make_rsrc(pa.gain_next, (uint32_t)N * 2u), off, 0u);
+    }
+  }
   constexpr int KBLK = W::KBLK;
   constexpr int STEPS = W::STEPS;
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem + nw * MCH * 64);
@@ -171,6 +189,8 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
   uint16_t* xwave = xs + (ONE >= 2 ? wave * nx * 512 : 0);  // this wave's LDS slice (ONE = 2)
   [[maybe_unused]] u32x4_t gw[PRO == kProNormSum || PRO == kProSiluGate ? kXw : 1];  // gain, or the up half
   [[maybe_unused]] u32x4_t ssv[PRO == kProNormSum ? kNormSumMax / 256 : 1];
+  [[maybe_unused]] __shared__ float row_scale_lds;                              // kProScaleSum: r (wave 0)
+  [[maybe_unused]] __shared__ __attribute__((aligned(16))) float ss_lds[PRO == kProScaleSum ? kNormSumMax : 4];
   if constexpr (ONE >= 2) {
 #pragma unroll
     for (int i = 0; i < kXw; ++i)
@@ -189,6 +209,16 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
 #pragma unroll
       for (int i = 0; i < kNormSumMax / 256; ++i)  // four sums a lane per load; past nss the resource reads zero
         if (i * 256 < pa.nss) ssv[i] = bload128(sr, (uint32_t)(lane + 64 * i) * 16u, 0u);
+    }
+    if constexpr (PRO == kProScaleSum) {
+      if (wave == 0) {  // wave-uniform: the sums into LDS, behind the activation slice (zero past nss)
+        const rsrc_t sr = make_rsrc(pa.ss_in, (uint32_t)pa.nss * 4u);
+#pragma unroll
+        for (int i = 0; i < kNormSumMax / 256; ++i)
+          if (i * 256 < pa.nss)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(ss_lds + 256 * i), 16,
+                                                     (uint32_t)(lane + 64 * i) * 16u, 0, 0, 0);
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) W::load(wc, min(kb0 + u, kb1 - 1), w[u], p[u]);
@@ -434,6 +464,24 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
     }
   }
 
+  if constexpr (PRO == kProScaleSum) {
+    if (wave == 0) {  // the row factor from the sums in LDS, in a fixed order (the same in every workgroup)
+      wait_vmcnt<0>();  // the copies into LDS (long done: the weights behind them have been consumed)
+      asm volatile("" ::: "memory");
+      // the lane index formed afresh here (mbcnt), so that no offset derived from it in the prologue
+      // stays live (or spills) through the main loop
+      const int ln = static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+      float t = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kNormSumMax / 256; ++i)
+        if (i * 256 < pa.nss) {
+          const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(ss_lds + 256 * i + 4 * ln);
+          t += (v4[0] + v4[1]) + (v4[2] + v4[3]);
+        }
+      t = wave_sum(t);
+      if (lane == 0) row_scale_lds = 1.0f / sqrtf(t / static_cast<float>(K) + pa.eps);
+    }
+  }
   // One row, grids that fit the chip in about one round: lane l < 16 of each wave holds the partial of
   // output t*16 + l, and wave 0 sums them in wave order (the order of the general path below, so the
   // bits are the same) and applies the epilogue. Larger grids measured faster with the general path,
@@ -454,10 +502,13 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
           v = v * W::row_scale(wa, 0) * W::out_scale(wa, n);
         else
           v *= W::out_scale(wa, n);
+        if constexpr (PRO == kProScaleSum) v *= row_scale_lds;
         if (bias) v += A::to_f32(bias[n]);
         if constexpr (RES) {
-          const float h = A::to_f32(A::from_f32(A::to_f32(pa.res[n]) + A::to_f32(A::from_f32(v))));
+          const float rv = A::to_f32(static_cast<uint16_t>(res_pre));
+          const float h = A::to_f32(A::from_f32(rv + A::to_f32(A::from_f32(v))));
           pa.res_out[n] = A::from_f32(h);
+          if (pa.gain_next != nullptr) pa.hg_out[n] = A::from_f32(h * A::to_f32(static_cast<uint16_t>(gain_pre)));
           hsq = h * h;
         } else {
           static_cast<uint16_t*>(yv)[n] = A::from_f32(v);
@@ -490,10 +541,12 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
         v = v * W::row_scale(wa, m) * W::out_scale(wa, n);
       else
         v *= W::out_scale(wa, n);
+      if constexpr (PRO == kProScaleSum) v *= row_scale_lds;
       if (bias) v += A::to_f32(bias[n]);
       if constexpr (RES) {
         const float h = A::to_f32(A::from_f32(A::to_f32(pa.res[n]) + A::to_f32(A::from_f32(v))));
         pa.res_out[n] = A::from_f32(h);
+        if (pa.gain_next != nullptr) pa.hg_out[n] = A::from_f32(h * A::to_f32(pa.gain_next[n]));
         hsq = h * h;
       } else if constexpr (YF32) {
         static_cast<float*>(yv)[(int64_t)m * N + n] = v;
@@ -546,19 +599,21 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     constexpr bool kOneOk = has_sum_offset<W>::value && U1 == 4 && !YF32;
     int one_mode = 0;
     if (kOneOk && M == 1 && xlds)
-      one_mode = ((PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate) && colscale == nullptr &&
+      one_mode = ((PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate || PRO == kProScaleSum) &&
+                  colscale == nullptr &&
                   kbw <= kOneMaxKbw)
                      ? 2
                      : 1;
     if (PRO != kProPlain && (!xlds || m > kProMaxRows || cols % 8 != 0))
       return hipErrorNotSupported;  // the caller checks first
     // one-row forms only: the norm from tile sums, the residual epilogue
-    if ((PRO == kProNormSum && one_mode != 2) || (RES && one_mode == 0)) return hipErrorNotSupported;
+    if (((PRO == kProNormSum || PRO == kProScaleSum) && one_mode != 2) || (RES && one_mode == 0))
+      return hipErrorNotSupported;
     if (one_mode != 0) {
       if constexpr (kOneOk) {
         if (one_mode == 2) {
           const size_t lds = red + static_cast<size_t>(nw) * ((kbw * (KBLK / 8) + 63) / 64) * 1024;
-          if constexpr (PRO == kProPlain) {
+          if constexpr (PRO == kProPlain || PRO == kProScaleSum) {
             if (kbw <= U1 && T > 1024) {  // one round per wave, several rounds of workgroups
               if (ktail) SQX_GEMV1(1, U1, true, true, lds, 3); else SQX_GEMV1(1, U1, false, true, lds, 3);
             } else {
@@ -569,12 +624,12 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
           }
         } else {
           const size_t lds = red + gemv_xlds_bytes(M, KB, KBLK);
-          if constexpr (PRO != kProNormSum) {
+          if constexpr (PRO != kProNormSum && PRO != kProScaleSum) {
             if (ktail) SQX_GEMV1(1, U1, true, true, lds, 1); else SQX_GEMV1(1, U1, false, true, lds, 1);
           }
         }
       }
-    } else if constexpr (RES || PRO == kProNormSum) {
+    } else if constexpr (RES || PRO == kProNormSum || PRO == kProScaleSum) {
       return hipErrorNotSupported;
     } else if (PRO != kProPlain || xlds) {
       const size_t lds = red + gemv_xlds_bytes(M, KB, KBLK);

@@ -1003,23 +1003,27 @@ extern "C" int sqx_int4_linear_silu(const uint8_t* wt, const float* st, const vo
 }
 
 // Arguments of the one-row residual epilogue shared by the two entry points that end in it.
-static int int4_res_check(const void* res, const void* res_out, const float* ss_out, int64_t m, const char* fn) {
+static int int4_res_check(const void* res, const void* res_out, const float* ss_out, const void* gain_next,
+                          const void* hg_out, int64_t m, const char* fn) {
   SQX_REQUIRE(m == 1, SQX_E_ARG, "%s: the residual epilogue is the one-row (decode) form, m=%lld", fn, (long long)m);
   SQX_REQUIRE(res && res_out && ss_out, SQX_E_ARG, "%s: null residual or sums", fn);
+  SQX_REQUIRE((gain_next == nullptr) == (hg_out == nullptr), SQX_E_ARG, "%s: gain_next and hg_out go together", fn);
   return SQX_OK;
 }
 
 extern "C" int sqx_int4_linear_residual(const uint8_t* wt, const float* st, const void* x, const void* res,
-                                        void* res_out, float* ss_out, int64_t m, int64_t rows, int64_t cols,
-                                        int64_t group, int k_slices, sqx_stream_t stream) {
+                                        void* res_out, float* ss_out, const void* gain_next, void* hg_out, int64_t m,
+                                        int64_t rows, int64_t cols, int64_t group, int k_slices, sqx_stream_t stream) {
   const char* fn = "sqx_int4_linear_residual";
   int rc = int4_pro_check(wt, st, x, res_out, m, rows, cols, group, k_slices, fn);
-  if (rc == SQX_OK) rc = int4_res_check(res, res_out, ss_out, m, fn);
+  if (rc == SQX_OK) rc = int4_res_check(res, res_out, ss_out, gain_next, hg_out, m, fn);
   if (rc != SQX_OK) return rc;
   ProArgs pa{};
   pa.res = static_cast<const uint16_t*>(res);
   pa.res_out = static_cast<uint16_t*>(res_out);
   pa.ss_out = ss_out;
+  pa.gain_next = static_cast<const uint16_t*>(gain_next);
+  pa.hg_out = static_cast<uint16_t*>(hg_out);
   const hipError_t e = launch_int4_pro_res<kProPlain, true>(static_cast<int>(group), wt, st,
                                                             static_cast<const uint16_t*>(x), nullptr, m, rows, cols,
                                                             k_slices, as_stream(stream), pa);
@@ -1028,16 +1032,19 @@ extern "C" int sqx_int4_linear_residual(const uint8_t* wt, const float* st, cons
 }
 
 extern "C" int sqx_int4_linear_silu_residual(const uint8_t* wt, const float* st, const void* gate_up, const void* res,
-                                             void* res_out, float* ss_out, int64_t m, int64_t rows, int64_t cols,
-                                             int64_t group, int k_slices, sqx_stream_t stream) {
+                                             void* res_out, float* ss_out, const void* gain_next, void* hg_out,
+                                             int64_t m, int64_t rows, int64_t cols, int64_t group, int k_slices,
+                                             sqx_stream_t stream) {
   const char* fn = "sqx_int4_linear_silu_residual";
   int rc = int4_pro_check(wt, st, gate_up, res_out, m, rows, cols, group, k_slices, fn);
-  if (rc == SQX_OK) rc = int4_res_check(res, res_out, ss_out, m, fn);
+  if (rc == SQX_OK) rc = int4_res_check(res, res_out, ss_out, gain_next, hg_out, m, fn);
   if (rc != SQX_OK) return rc;
   ProArgs pa{};
   pa.res = static_cast<const uint16_t*>(res);
   pa.res_out = static_cast<uint16_t*>(res_out);
   pa.ss_out = ss_out;
+  pa.gain_next = static_cast<const uint16_t*>(gain_next);
+  pa.hg_out = static_cast<uint16_t*>(hg_out);
   const hipError_t e = launch_int4_pro_res<kProSiluGate, true>(static_cast<int>(group), wt, st,
                                                                static_cast<const uint16_t*>(gate_up), nullptr, m,
                                                                rows, cols, k_slices, as_stream(stream), pa);
@@ -1073,6 +1080,35 @@ extern "C" int sqx_int4_linear_rmsnorm_sumsq(const uint8_t* wt, const float* st,
   const hipError_t e = launch_int4_pro<kProNormSum>(static_cast<int>(group), wt, st, static_cast<const uint16_t*>(h),
                                                     static_cast<uint16_t*>(y), m, rows, cols, k_slices,
                                                     as_stream(stream), pa);
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_linear_rowscale_sumsq(const uint8_t* wt, const float* st, const void* hg, const float* ss,
+                                             int64_t nss, float eps, void* y, int64_t m, int64_t rows, int64_t cols,
+                                             int64_t group, int k_slices, sqx_stream_t stream) {
+  const char* fn = "sqx_int4_linear_rowscale_sumsq";
+  const int rc = int4_pro_check(wt, st, hg, y, m, rows, cols, group, k_slices, fn);
+  if (rc != SQX_OK) return rc;
+  SQX_REQUIRE(m == 1, SQX_E_ARG, "%s: the norm from tile sums is the one-row (decode) form, m=%lld", fn, (long long)m);
+  SQX_REQUIRE(nss == ceil_div(cols, 16) && nss <= kNormSumMax, SQX_E_ARG,
+              "%s: %lld sums of squares for %lld columns (one per 16 columns, at most %d)", fn, (long long)nss,
+              (long long)cols, kNormSumMax);
+  SQX_REQUIRE(ss != nullptr && reinterpret_cast<uintptr_t>(ss) % 16 == 0, SQX_E_ARG,
+              "%s: the sums must be 16-byte aligned", fn);
+  const int64_t KB = ceil_div(cols, 128);
+  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols) : k_slices;
+  if (nw > KB) nw = static_cast<int>(KB);
+  SQX_REQUIRE(ceil_div(KB, nw) <= kOneMaxKbw, SQX_E_ARG,
+              "%s: %lld k-blocks over %d waves: at most %d per wave (raise k_slices)", fn, (long long)KB, nw,
+              kOneMaxKbw);
+  ProArgs pa{};
+  pa.eps = eps;
+  pa.ss_in = ss;
+  pa.nss = static_cast<int>(nss);
+  const hipError_t e = launch_int4_pro<kProScaleSum>(static_cast<int>(group), wt, st, static_cast<const uint16_t*>(hg),
+                                                     static_cast<uint16_t*>(y), m, rows, cols, k_slices,
+                                                     as_stream(stream), pa);
   SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return SQX_OK;
 }

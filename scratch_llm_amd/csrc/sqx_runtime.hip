@@ -16,4 +16,4 @@ void set_error(const char* fmt, ...) {
 
 extern "C" const char* sqx_last_error(void) { return sqx::g_last_error; }
 
-extern "C" int sqx_abi_version(void) { return 1; }
+extern "C" int sqx_abi_version(void) { return 2; }

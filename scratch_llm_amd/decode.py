@@ -209,9 +209,9 @@ class Int4DecodeLM:
         self.fuse_norm = False
         self.fuse_silu = True
         # One-row steps: the o and down projections end in the residual add and leave the sums of
-        # squares per 16 columns, from which the next projection (qkv, gate/up) forms the norm while it
-        # loads its activations, so the norms inside the layers cost no launch (all but the first
-        # layer's and the final one).
+        # squares per 16 columns and bf16(h * gain) of the next norm; the next projection (qkv, gate/up,
+        # the lm_head) multiplies its product by the norm's row factor formed from the sums, so no norm
+        # after layer 0's costs a launch.
         self.fuse_norm_sums = True
         # Batched steps: when the o / down projection splits K, its fp32 partials go straight to the
         # next residual add + RMSNorm, which adds them in the linear's own order (no reduce launch).
@@ -360,14 +360,14 @@ class Int4DecodeLM:
             self._linear(st, tw, st.h, y, stream)
         return nxt
 
-    def _norm_sums_linear(self, st: DecodeState, h: Tensor, gain: Tensor, tw: i4.Int4Tiled, y: Tensor,
-                          stream: int) -> None:
-        """One row: ``tw`` applied to RMSNorm(h), the norm formed from ``st.ss`` (the sums of squares the
-        residual epilogue left) inside the linear."""
+    def _norm_sums_linear(self, st: DecodeState, tw: i4.Int4Tiled, y: Tensor, stream: int) -> None:
+        """One row: ``tw`` applied to RMSNorm(h) as ``r * (bf16(h * gain) @ W^T)``: ``st.h`` holds
+        bf16(h * gain) and ``st.ss`` the sums of squares of h, both left by the residual epilogue of
+        the linear that wrote h; the row factor r is formed from the sums in the linear's epilogue."""
         lib = _lib.load()
-        _lib.check(lib.sqx_int4_linear_rmsnorm_sumsq(
-            tw.wt.data_ptr(), tw.st.data_ptr(), h.data_ptr(), st.ss.data_ptr(), st.ss.numel(), gain.data_ptr(),
-            self.cfg.norm_eps, y.data_ptr(), 1, tw.rows, tw.cols, tw.group_size, 0, stream), "rmsnorm (sums) + int4 linear")
+        _lib.check(lib.sqx_int4_linear_rowscale_sumsq(
+            tw.wt.data_ptr(), tw.st.data_ptr(), st.h.data_ptr(), st.ss.data_ptr(), st.ss.numel(), self.cfg.norm_eps,
+            y.data_ptr(), 1, tw.rows, tw.cols, tw.group_size, 0, stream), "rmsnorm (row factor) + int4 linear")
 
     def step(self, st: DecodeState, tokens=None) -> Tensor:
         """Decode one token per row: logits of ``st.tokens`` (or ``tokens``) at each row's position,
@@ -389,7 +389,7 @@ class Int4DecodeLM:
             cur, delta, dsplit, have_ss = 0, None, 0, False
             for li, ly in enumerate(self.layers):
                 if have_ss:
-                    self._norm_sums_linear(st, st.x[cur], ly.attn_norm, ly.wqkv, st.qkv, s)
+                    self._norm_sums_linear(st, ly.wqkv, st.qkv, s)
                 else:
                     cur = self._norm_linear(st, cur, delta, ly.attn_norm, ly.wqkv, st.qkv, s, dsplit)
                 if st.kv_dtype == "fp8":
@@ -404,15 +404,20 @@ class Int4DecodeLM:
                         cfg.context_length, st.k[li].data_ptr(), st.v[li].data_ptr(), B, H, Hkv, hd, T,
                         st.attn.data_ptr(), st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention")
                 if sums:
+                    # o and down end in the residual add and leave bf16(h * gain) of the next norm with
+                    # the sums of squares of h; the linear after each norm applies its row factor
+                    gain_next = self.layers[li + 1].attn_norm if li + 1 < len(self.layers) else self.final_norm
                     ck(lib.sqx_int4_linear_residual(ly.wo.wt.data_ptr(), ly.wo.st.data_ptr(), st.attn.data_ptr(),
                                                     st.x[cur].data_ptr(), st.x[1 - cur].data_ptr(), st.ss.data_ptr(),
-                                                    1, ly.wo.rows, ly.wo.cols, ly.wo.group_size, 0, s), "o + residual")
+                                                    ly.ffn_norm.data_ptr(), st.h.data_ptr(), 1, ly.wo.rows,
+                                                    ly.wo.cols, ly.wo.group_size, 0, s), "o + residual")
                     cur = 1 - cur
-                    self._norm_sums_linear(st, st.x[cur], ly.ffn_norm, ly.w13, st.gu, s)
+                    self._norm_sums_linear(st, ly.w13, st.gu, s)
                     ck(lib.sqx_int4_linear_silu_residual(ly.w2.wt.data_ptr(), ly.w2.st.data_ptr(), st.gu.data_ptr(),
                                                          st.x[cur].data_ptr(), st.x[1 - cur].data_ptr(),
-                                                         st.ss.data_ptr(), 1, ly.w2.rows, ly.w2.cols,
-                                                         ly.w2.group_size, 0, s), "silu + down + residual")
+                                                         st.ss.data_ptr(), gain_next.data_ptr(), st.h.data_ptr(), 1,
+                                                         ly.w2.rows, ly.w2.cols, ly.w2.group_size, 0, s),
+                       "silu + down + residual")
                     cur, have_ss = 1 - cur, True
                     continue
                 delta, dsplit = self._delta_linear(st, ly.wo, st.attn, s)
@@ -425,10 +430,10 @@ class Int4DecodeLM:
                 else:
                     ck(lib.sqx_silu_mul(st.gu.data_ptr(), B, cfg.d_ff, st.act.data_ptr(), s), "silu_mul")
                     delta, dsplit = self._delta_linear(st, ly.w2, st.act, s)
-            # the final norm stays a kernel of its own: in front of the 8016-tile lm_head every wave would
-            # re-read its slice of the gain, which costs more than the launch it saves
-            cur = self._norm_linear(st, cur, None if have_ss else delta, self.final_norm, self.lm_head, st.logits, s,
-                                    0 if have_ss else dsplit)
+            if have_ss:  # the last down projection left bf16(h * final gain) and the sums of squares
+                self._norm_sums_linear(st, self.lm_head, st.logits, s)
+            else:
+                cur = self._norm_linear(st, cur, delta, self.final_norm, self.lm_head, st.logits, s, dsplit)
             ck(lib.sqx_argmax(st.logits.data_ptr(), B, cfg.vocab_size, st.tokens.data_ptr(), st.argmax_ws.data_ptr(),
                               st.argmax_ws.numel() * 4, s), "argmax")
             ck(lib.sqx_advance(st.lengths.data_ptr(), st.active.data_ptr(), B, s), "advance")

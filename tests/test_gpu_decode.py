@@ -308,11 +308,14 @@ def test_linear_residual_equals_two_calls(lib, n, k, group, silu):
     _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, src.data_ptr(), 1, y.data_ptr(), None, 1,
                                  n, k, group, ks, _s()))
     fn = lib.sqx_int4_linear_silu_residual if silu else lib.sqx_int4_linear_residual
-    _ok(lib, fn(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), res.data_ptr(), out.data_ptr(), ss.data_ptr(), 1, n, k,
-                group, 0, _s()))
+    gain = (1 + 0.1 * torch.randn(n, generator=g)).bfloat16().to(DEV)
+    hg = torch.empty(1, n, dtype=torch.bfloat16, device=DEV)
+    _ok(lib, fn(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), res.data_ptr(), out.data_ptr(), ss.data_ptr(),
+                gain.data_ptr(), hg.data_ptr(), 1, n, k, group, 0, _s()))
     torch.cuda.synchronize()
     want = (res.float() + y.float()).bfloat16()  # the reference's bf16 add
     assert torch.equal(out, want)
+    assert torch.equal(hg, (want.float() * gain.float()).bfloat16())  # bf16(h * gain): one rounding
     h = torch.zeros(nt * 16, dtype=torch.float64)
     h[:n] = out.cpu().double()[0]
     ref = (h * h).view(nt, 16).sum(1)
@@ -360,13 +363,60 @@ def test_linear_rmsnorm_sumsq(lib, n, k, group):
     assert float(d.max()) <= 2.0**-6 * float(y1.float().abs().max())
 
 
+@pytest.mark.parametrize("n,k,group", [(6144, 4096, 128), (28672, 4096, 128), (128256, 4096, 128), (1000, 1056, 32)])
+def test_linear_rowscale_sumsq(lib, n, k, group):
+    """sqx_int4_linear_rowscale_sumsq: RMSNorm's row factor applied to the product of bf16(h * gain)
+    against the oracle: the float64 product of the reference's normalised row bf16(h * r * gain) and the
+    bf16-cast dequantized weight, at the gate/up (8-wave form), qkv and lm_head shapes. Max-abs-rel
+    1e-2, and elementwise the bound the roundings give: the two sides round each activation at
+    different points (each within 2**-9, so 2**-8 apart), the reference rounds each weight to bf16
+    (2**-9), each output is rounded to bf16 (2**-9 each side): |y - y_ref| <= 2**-7 sum_k |w_k a_k| +
+    2**-8 |y_ref|."""
+    from oracle import quant_ref as R
+    from scratch_llm_amd.quant import int4_group as i4
+
+    print_case("linear rowscale sums", n, k, group)
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(n + group)) * 0.05).to(DEV)
+    q, sc = i4.quantize_groupwise_int4(w, group)
+    tw = i4.tile_int4(q, sc, None, group)
+    del w
+    g = torch.Generator().manual_seed(k + n)
+    h = (torch.randn(1, k, generator=g) * 2).bfloat16()
+    gain = (1 + 0.1 * torch.randn(k, generator=g)).bfloat16()
+    nt = -(-k // 16)
+    hp = torch.zeros(nt * 16, dtype=torch.float32)
+    hp[:k] = h.float()[0]
+    ss = (hp * hp).view(nt, 16).sum(1).to(DEV)
+    hg = (h.float() * gain.float()).bfloat16().to(DEV)
+    y = torch.empty(1, n, dtype=torch.bfloat16, device=DEV)
+    _ok(lib, lib.sqx_int4_linear_rowscale_sumsq(tw.wt.data_ptr(), tw.st.data_ptr(), hg.data_ptr(), ss.data_ptr(), nt,
+                                                1e-5, y.data_ptr(), 1, n, k, group, 0, _s()))
+    torch.cuda.synchronize()
+    hn = D.rmsnorm(h, gain, 1e-5)  # the reference's normalised row (bf16)
+    rows = torch.arange(0, n, max(1, n // 8192))
+    w_eff = R.round_bf16(R.dequantize_groupwise_int4(q[rows.to(DEV)].cpu().numpy(), sc[rows.to(DEV)].cpu().numpy(), group))
+    a = hn.float().numpy().astype(np.float64)
+    y_ref = R.linear_f64(a, w_eff)
+    got = y[:, rows.to(DEV)].float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - y_ref)
+    assert float(err.max() / np.abs(y_ref).max()) <= 1e-2
+    bound = 2.0**-7 * (np.abs(a) @ np.abs(w_eff.astype(np.float64)).T) + 2.0**-8 * np.abs(y_ref) + 1e-30
+    assert float((err / bound).max()) <= 1.0, f"rowscale {k}->{n}: {float((err / bound).max()):.2f}x the bound"
+
+
 def test_residual_forms_refuse(lib):
     tw = _tiled(64, 4096, 128, seed=3)
     x = torch.zeros(2, 4096, dtype=torch.bfloat16, device=DEV)
     ss = torch.zeros(256, dtype=torch.float32, device=DEV)
     assert lib.sqx_int4_linear_residual(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
-                                        ss.data_ptr(), 2, 64, 4096, 128, 0, _s()) == -1
+                                        ss.data_ptr(), None, None, 2, 64, 4096, 128, 0, _s()) == -1
     assert "one-row" in lib.sqx_last_error().decode()
+    assert lib.sqx_int4_linear_residual(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
+                                        ss.data_ptr(), x.data_ptr(), None, 1, 64, 4096, 128, 0, _s()) == -1
+    assert "go together" in lib.sqx_last_error().decode()
+    assert lib.sqx_int4_linear_rowscale_sumsq(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), ss.data_ptr(), 255,
+                                              1e-5, x.data_ptr(), 1, 64, 4096, 128, 0, _s()) == -1
+    assert "sums of squares" in lib.sqx_last_error().decode()
     assert lib.sqx_int4_linear_rmsnorm_sumsq(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), ss.data_ptr(), 255,
                                              x.data_ptr(), 1e-5, x.data_ptr(), 1, 64, 4096, 128, 0, _s()) == -1
     assert "sums of squares" in lib.sqx_last_error().decode()
