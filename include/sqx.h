@@ -207,6 +207,20 @@ int sqx_int4_linear_rowscale_sumsq(const uint8_t* wt, const float* st, const voi
                                    float eps, void* y, int64_t m, int64_t rows, int64_t cols, int64_t group,
                                    int k_slices, sqx_stream_t stream);
 
+/* The decode step's fused q|k|v projection at one row with RoPE and the slot-cache write in its epilogue
+ * (model.py:205-224, 281-305; kv_cache.py:194-205): the one-row GEMV of x [cols] (with ss given, the
+ * row factor of sqx_int4_linear_rowscale_sumsq: x is bf16(h * gain) and ss the sums of squares of h),
+ * rows = (n_heads + 2 n_kv_heads) * 128 laid out [q | k | v]. With p = lengths[0]: q and k are rotated
+ * at position min(p, rope_rows - 1) as sqx_rope_kv rotates them (bf16 outputs, separate fp32
+ * products and sums), q into q_out [n_heads * 128], k and v stored at row min(p, tmax - 1) of
+ * k_cache / v_cache [n_kv_heads, tmax, 128] (one layer, one slot; bf16). The rotated bf16 values
+ * equal sqx_rope_kv's on this linear's output. Fewer than 1024 row tiles. */
+int sqx_int4_linear_rope_kv(const uint8_t* wt, const float* st, const void* x, const float* ss, int64_t nss,
+                            float eps, const int* lengths, const float* cos_t, const float* sin_t, int64_t rope_rows,
+                            int64_t n_heads, int64_t n_kv_heads, int64_t tmax, void* q_out, void* k_cache,
+                            void* v_cache, int64_t rows, int64_t cols, int64_t group, int k_slices,
+                            sqx_stream_t stream);
+
 /* Build-defined asymmetric uint4, group-wise (BASELINE config 2's "asymmetric, bf16 scale/zero";
  * no reference symbol: the 4-bit form of quantize_affine, int8.py:142-172, per group):
  * lo = min(min(w_g), 0), hi = max(max(w_g), 0), s = max((hi - lo) / 15, 1e-12) (rounded to bf16 first

@@ -103,6 +103,12 @@ struct has_row_scale<W, std::void_t<decltype(W::kRowScale)>> : std::integral_con
 //                activation slice, so no registers hold them) and forms r before the epilogue.
 // RES (one row): the residual epilogue. The output is res_out = bf16(res + bf16(x W^T)) (the decode
 // step's h = x + o_proj(...), model.py:365-372), and ss_out[t] is the sum of its squares over tile t.
+// RKV (one row, fewer than 1024 tiles): the fused q|k|v projection's RoPE and cache write. Rows below
+// qn are q, rotated (model.py:205-224: interleaved pairs at position lengths[0], separate fp32
+// products and sums of the bf16 output, rounded to bf16) into q_out; rows [qn, qn + kn) are k,
+// rotated and stored at cache row min(lengths[0], tmax - 1) of k_cache [kn / 128, tmax, 128]
+// (kv_cache.py:194-205); the rest are v, stored there in v_cache. Wave 0 requests the length with
+// its activation slice and the pair's cos / sin behind it, so the epilogue finds them in registers.
 enum { kProPlain = 0, kProResNorm = 1, kProSiluGate = 2, kProNormSum = 3, kProScaleSum = 4 };
 static constexpr int kProMaxRows = 8;
 static constexpr int kNormSumMax = 512;  // tiles of sums of squares a kProNormSum prologue reads (K <= 8192)
@@ -119,10 +125,17 @@ struct ProArgs {
   float* ss_out;          // RES: sum of res_out^2 per 16-row tile [ceil(N / 16)]
   const uint16_t* gain_next;  // RES: when set, hg_out = bf16(res_out * gain_next) [N] as well
   uint16_t* hg_out;
+  const int* lengths;         // RKV: lengths[0], the row's position
+  const float* cos_t;         // RKV: RoPE tables [rope_rows, 64]
+  const float* sin_t;
+  int rope_rows, qn, kn, tmax;
+  uint16_t* q_out;            // RKV: rotated q [qn]
+  uint16_t* k_cache;          // RKV: [kn / 128, tmax, 128] bf16
+  uint16_t* v_cache;
 };
 
 template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32, int PRO = kProPlain, int ONE = 0,
-          bool RES = false>
+          bool RES = false, bool RKV = false>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ? 8 : 1))) void gemv_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
                                                     void* __restrict__ yv, const uint16_t* __restrict__ bias,
                                                     const float* __restrict__ colscale, int M, int N, int K, int KB,
@@ -134,6 +147,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
   static_assert((PRO != kProNormSum && PRO != kProScaleSum) || ONE >= 2,
                 "the norm from tile sums runs in each wave's own slice");
   static_assert(!RES || ONE != 0, "the residual epilogue is a one-row form");
+  static_assert(!RKV || (ONE >= 2 && !RES), "the RoPE epilogue is a one-row form of its own");
   static_assert(ONE == 0 || !YF32, "the one-row form writes 16-bit outputs");
   extern __shared__ f32x4_t smem[];  // [NW][MCH][64] partial accumulators, then (XLDS) the activations
   f32x4_t* red = smem;
@@ -151,6 +165,8 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
   // RES: wave 0 requests its lanes' residual (and next-norm gain) values now, so that the epilogue of
   // small grids (wave 0 finishes the tile) does not wait for them; lanes 16..63 read neighbours or zero.
   [[maybe_unused]] uint32_t res_pre = 0u, gain_pre = 0u;
+  [[maybe_unused]] int len_pre = 0;
+  [[maybe_unused]] float cos_pre = 0.0f, sin_pre = 0.0f;
   if constexpr (RES) {
     if (wave == 0) {  // wave-uniform
       const uint32_t off = (uint32_t)(t * 16 + (lane & 15)) * 2u;
@@ -209,6 +225,9 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
 #pragma unroll
       for (int i = 0; i < kNormSumMax / 256; ++i)  // four sums a lane per load; past nss the resource reads zero
         if (i * 256 < pa.nss) ssv[i] = bload128(sr, (uint32_t)(lane + 64 * i) * 16u, 0u);
+    }
+    if constexpr (RKV) {
+      if (wave == 0) len_pre = static_cast<int>(bload32(make_rsrc(pa.lengths, 4u), 0u, 0u));  // wave-uniform
     }
     if constexpr (PRO == kProScaleSum) {
       if (wave == 0) {  // wave-uniform: the sums into LDS, behind the activation slice (zero past nss)
@@ -273,6 +292,15 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
     // fragment reads above the stores
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
+    if constexpr (RKV) {
+      if (wave == 0) {  // the pair's cos / sin at the row's position (needed only in the epilogue)
+        const int pos = min(max(len_pre, 0), pa.rope_rows - 1);
+        const uint32_t pi = (uint32_t)(pos * 64 + (((t * 16 + (lane & 15)) & 127) >> 1)) * 4u;
+        const uint32_t tb = (uint32_t)pa.rope_rows * 64u * 4u;
+        cos_pre = __builtin_bit_cast(float, bload32(make_rsrc(pa.cos_t, tb), pi, 0u));
+        sin_pre = __builtin_bit_cast(float, bload32(make_rsrc(pa.sin_t, tb), pi, 0u));
+      }
+    }
   } else if constexpr (PRO == kProResNorm) {
     // The 256 threads of the standalone kernel are emulated by "virtual threads" vt (in passes when
     // the workgroup is smaller; a workgroup is a whole number of waves, so a virtual wave is a real
@@ -497,6 +525,28 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
       if (lane < 16)
         for (int ww = 0; ww < nw; ++ww) v += rf1[ww * 16 + lane];
       [[maybe_unused]] float hsq = 0.0f;
+      if constexpr (RKV) {
+#pragma clang fp contract(off)
+        if constexpr (PRO == kProScaleSum) v *= row_scale_lds;
+        const float xq = A::to_f32(A::from_f32(v));  // the projection's bf16 output
+        const float xp = __shfl_xor(xq, 1, 64);      // its RoPE partner (the other dim of the pair)
+        if (own) {
+          const int slot = min(max(len_pre, 0), pa.tmax - 1);
+          if (n < pa.qn + pa.kn) {
+            const float r = (n & 1) ? xp * sin_pre + xq * cos_pre : xq * cos_pre - xp * sin_pre;
+            if (n < pa.qn) {
+              pa.q_out[n] = A::from_f32(r);
+            } else {
+              const int kd = n - pa.qn;
+              pa.k_cache[((int64_t)(kd >> 7) * pa.tmax + slot) * 128 + (kd & 127)] = A::from_f32(r);
+            }
+          } else {
+            const int vd = n - pa.qn - pa.kn;
+            pa.v_cache[((int64_t)(vd >> 7) * pa.tmax + slot) * 128 + (vd & 127)] = A::from_f32(xq);
+          }
+        }
+        return;
+      }
       if (own) {
         if constexpr (has_row_scale<W>::value)
           v = v * W::row_scale(wa, 0) * W::out_scale(wa, n);
@@ -566,7 +616,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
 
 // Launch the GEMV for every 64-row pass of x. k_slices <= 0 picks the default. Returns 0 or the
 // HIP error of the launch.
-template <class A, class W, int U1, int U2, bool YF32, int PRO = kProPlain, bool RES = false>
+template <class A, class W, int U1, int U2, bool YF32, int PRO = kProPlain, bool RES = false, bool RKV = false>
 hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, const uint16_t* bias,
                        const float* colscale, int64_t m, int64_t rows, int64_t cols, int k_slices,
                        hipStream_t stream, const ProArgs& pa = ProArgs{nullptr, nullptr, nullptr, 0.0f}) {
@@ -591,8 +641,11 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     const bool xlds = mch == 1 && gemv_xlds_bytes(M, KB, KBLK) <= kXldsMax;
     if (colscale != nullptr && !xlds) return hipErrorNotSupported;  // column scaling happens in the LDS copy
 #define SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, ONE_)                                                              \
-  hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO, ONE_, RES>), grid, block, LDS_, stream, wp, xp, \
-                     yp, bias, colscale, M, N, K, iKB, kbw, pa)
+  do {                                                                                                        \
+    if constexpr (!RKV || ONE_ == 2)                                                                          \
+      hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO, ONE_, RES, RKV>), grid, block, LDS_, stream, \
+                         wp, xp, yp, bias, colscale, M, N, K, iKB, kbw, pa);                                  \
+  } while (0)
 #define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_) SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, 0)
     // the one-row form for formats whose offset costs sum(x) per group: 2 = each wave loads its own
     // k-slice of the activations, 1 = from the workgroup's LDS copy (prologues, column scales)
@@ -609,6 +662,8 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     // one-row forms only: the norm from tile sums, the residual epilogue
     if (((PRO == kProNormSum || PRO == kProScaleSum) && one_mode != 2) || (RES && one_mode == 0))
       return hipErrorNotSupported;
+    // the RoPE epilogue: the one-row form 2 with wave 0 finishing each tile (grids under 1024 tiles)
+    if (RKV && (one_mode != 2 || T >= 1024)) return hipErrorNotSupported;
     if (one_mode != 0) {
       if constexpr (kOneOk) {
         if (one_mode == 2) {

@@ -1112,3 +1112,67 @@ extern "C" int sqx_int4_linear_rowscale_sumsq(const uint8_t* wt, const float* st
   SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return SQX_OK;
 }
+
+extern "C" int sqx_int4_linear_rope_kv(const uint8_t* wt, const float* st, const void* x, const float* ss, int64_t nss,
+                                      float eps, const int* lengths, const float* cos_t, const float* sin_t,
+                                      int64_t rope_rows, int64_t n_heads, int64_t n_kv_heads, int64_t tmax,
+                                      void* q_out, void* k_cache, void* v_cache, int64_t rows, int64_t cols,
+                                      int64_t group, int k_slices, sqx_stream_t stream) {
+  const char* fn = "sqx_int4_linear_rope_kv";
+  const int rc = int4_pro_check(wt, st, x, q_out, 1, rows, cols, group, k_slices, fn);
+  if (rc != SQX_OK) return rc;
+  SQX_REQUIRE(n_heads > 0 && n_kv_heads > 0 && rows == (n_heads + 2 * n_kv_heads) * 128, SQX_E_ARG,
+              "%s: rows=%lld is not (%lld + 2 * %lld) heads of 128", fn, (long long)rows, (long long)n_heads,
+              (long long)n_kv_heads);
+  SQX_REQUIRE(ceil_div(rows, 16) < 1024, SQX_E_ARG, "%s: %lld rows: the RoPE epilogue needs fewer than 1024 tiles",
+              fn, (long long)rows);
+  SQX_REQUIRE(lengths && cos_t && sin_t && k_cache && v_cache, SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(rope_rows > 0 && rope_rows < (int64_t(1) << 24) && tmax > 0 && tmax < (int64_t(1) << 30), SQX_E_ARG,
+              "%s: bad rope_rows or tmax", fn);
+  SQX_REQUIRE(ss == nullptr || (nss == ceil_div(cols, 16) && nss <= kNormSumMax &&
+                                reinterpret_cast<uintptr_t>(ss) % 16 == 0),
+              SQX_E_ARG, "%s: %lld sums of squares for %lld columns (one per 16 columns, at most %d, 16-byte aligned)",
+              fn, (long long)nss, (long long)cols, kNormSumMax);
+  const int64_t KB = ceil_div(cols, 128);
+  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols) : k_slices;
+  if (nw > KB) nw = static_cast<int>(KB);
+  SQX_REQUIRE(ceil_div(KB, nw) <= kOneMaxKbw, SQX_E_ARG,
+              "%s: %lld k-blocks over %d waves: at most %d per wave (raise k_slices)", fn, (long long)KB, nw,
+              kOneMaxKbw);
+  ProArgs pa{};
+  pa.eps = eps;
+  pa.ss_in = ss;
+  pa.nss = static_cast<int>(nss);
+  pa.lengths = lengths;
+  pa.cos_t = cos_t;
+  pa.sin_t = sin_t;
+  pa.rope_rows = static_cast<int>(rope_rows);
+  pa.qn = static_cast<int>(n_heads * 128);
+  pa.kn = static_cast<int>(n_kv_heads * 128);
+  pa.tmax = static_cast<int>(tmax);
+  pa.q_out = static_cast<uint16_t*>(q_out);
+  pa.k_cache = static_cast<uint16_t*>(k_cache);
+  pa.v_cache = static_cast<uint16_t*>(v_cache);
+  hipError_t e;
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  hipStream_t s = as_stream(stream);
+#define SQX_RKV(G_)                                                                                               \
+  {                                                                                                               \
+    using W = WInt4<G_, false, false>;                                                                            \
+    const typename W::Args a{wt, st, nullptr};                                                                    \
+    if (ss != nullptr)                                                                                            \
+      e = gemv_launch<ActBF16, W, SQX_INT4_U1, SQX_INT4_U2, false, kProScaleSum, false, true>(a, xp, nullptr, nullptr, \
+                                                                                     nullptr, 1, rows, cols,     \
+                                                                                     k_slices, s, pa);           \
+    else                                                                                                          \
+      e = gemv_launch<ActBF16, W, SQX_INT4_U1, SQX_INT4_U2, false, kProPlain, false, true>(a, xp, nullptr, nullptr, \
+                                                                                  nullptr, 1, rows, cols,        \
+                                                                                  k_slices, s, pa);              \
+  }
+  if (group == 128) SQX_RKV(128)
+  else if (group == 64) SQX_RKV(64)
+  else SQX_RKV(32)
+#undef SQX_RKV
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
+}

@@ -129,6 +129,7 @@ class DecodeState:
         # wrote it for the norm in the next linear
         self.ss = torch.empty(-(-d // 16), dtype=torch.float32, device=dev)
         self.qkv = torch.empty(batch, (cfg.n_heads + 2 * hkv) * hd, **bf)
+        self.q = torch.empty(batch, cfg.n_heads * hd, **bf)  # rotated q (one-row steps: the qkv epilogue's)
         self.attn = torch.empty(batch, cfg.n_heads * hd, **bf)
         self.gu = torch.empty(batch, 2 * cfg.d_ff, **bf)
         self.act = torch.empty(batch, cfg.d_ff, **bf)
@@ -387,12 +388,30 @@ class Int4DecodeLM:
             ck(lib.sqx_embed(self.embed.data_ptr(), cfg.vocab_size, st.tokens.data_ptr(), B, d, st.x[0].data_ptr(), s),
                "embed")
             cur, delta, dsplit, have_ss = 0, None, 0, False
+            rope_in_qkv = sums and st.kv_dtype == "bf16"
             for li, ly in enumerate(self.layers):
-                if have_ss:
+                if rope_in_qkv:
+                    # one row: q|k|v with RoPE and the cache write in the projection's epilogue, then
+                    # attention over the cache as it stands
+                    if not have_ss:  # layer 0: the norm of the embedding row as a kernel of its own
+                        ck(lib.sqx_rmsnorm(st.x[cur].data_ptr(), None, ly.attn_norm.data_ptr(), cfg.norm_eps, B, d,
+                                           None, st.h.data_ptr(), s), "rmsnorm")
+                    ck(lib.sqx_int4_linear_rope_kv(
+                        ly.wqkv.wt.data_ptr(), ly.wqkv.st.data_ptr(), st.h.data_ptr(),
+                        st.ss.data_ptr() if have_ss else None, st.ss.numel(), cfg.norm_eps, st.lengths.data_ptr(),
+                        self.cos.data_ptr(), self.sin.data_ptr(), cfg.context_length, H, Hkv, T, st.q.data_ptr(),
+                        st.k[li].data_ptr(), st.v[li].data_ptr(), ly.wqkv.rows, ly.wqkv.cols, ly.wqkv.group_size, 0, s),
+                       "qkv + rope + cache write")
+                    ck(lib.sqx_decode_attention(st.q.data_ptr(), st.k[li].data_ptr(), st.v[li].data_ptr(),
+                                                st.lengths.data_ptr(), B, H, Hkv, hd, T, st.attn.data_ptr(),
+                                                st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention")
+                elif have_ss:
                     self._norm_sums_linear(st, ly.wqkv, st.qkv, s)
                 else:
                     cur = self._norm_linear(st, cur, delta, ly.attn_norm, ly.wqkv, st.qkv, s, dsplit)
-                if st.kv_dtype == "fp8":
+                if rope_in_qkv:
+                    pass  # attention ran above
+                elif st.kv_dtype == "fp8":
                     ck(lib.sqx_decode_attention_rope_fp8kv(
                         st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
                         cfg.context_length, st.k[li].data_ptr(), st.v[li].data_ptr(), st.k_scale[li].data_ptr(),

@@ -404,6 +404,55 @@ def test_linear_rowscale_sumsq(lib, n, k, group):
     assert float((err / bound).max()) <= 1.0, f"rowscale {k}->{n}: {float((err / bound).max()):.2f}x the bound"
 
 
+@pytest.mark.parametrize("H,Hkv,T,length,sums", [(32, 8, 2048, 2047, True), (32, 8, 2048, 0, False),
+                                                  (8, 2, 100, 140, True), (16, 16, 64, 37, False)])
+def test_linear_rope_kv_equals_two_calls(lib, H, Hkv, T, length, sums):
+    """sqx_int4_linear_rope_kv == the linear (sqx_int4_linear_rowscale_sumsq, or the plain one-row GEMV)
+    followed by sqx_rope_kv on its output, bit for bit: the rotated q, and the cache rows (only row
+    min(length, T - 1) changes), at a full slot and at position 0 too."""
+    from scratch_llm_amd.quant import int4_group as i4
+
+    print_case("linear rope kv", H, Hkv, T, length, sums)
+    hd, k = 128, 4096 if H == 32 else 1024
+    n = (H + 2 * Hkv) * hd
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(n + k)) * 0.05).to(DEV)
+    q, sc = i4.quantize_groupwise_int4(w)
+    tw = i4.tile_int4(q, sc)
+    del w
+    g = torch.Generator().manual_seed(H + T)
+    x = (torch.randn(1, k, generator=g) * 2).bfloat16().to(DEV)
+    nt = k // 16
+    ss = (torch.rand(nt, generator=g) * 50).to(DEV) if sums else None
+    ctx = max(T, length + 1) + 8
+    cos, sin = (t.to(DEV) for t in D.rope_tables(hd, ctx, 10000.0))
+    ln = torch.tensor([length], dtype=torch.int32, device=DEV)
+    cache = torch.randn(2, 1, Hkv, T, hd, generator=g).bfloat16().to(DEV)
+    # the two-call form
+    y = torch.empty(1, n, dtype=torch.bfloat16, device=DEV)
+    if sums:
+        _ok(lib, lib.sqx_int4_linear_rowscale_sumsq(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), ss.data_ptr(), nt,
+                                                    1e-5, y.data_ptr(), 1, n, k, 128, 0, _s()))
+    else:
+        _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, x.data_ptr(), 1, y.data_ptr(), None,
+                                     1, n, k, 128, 0, _s()))
+    q2 = torch.empty(1, H, hd, dtype=torch.bfloat16, device=DEV)
+    kc2, vc2 = cache[0].clone(), cache[1].clone()
+    _ok(lib, lib.sqx_rope_kv(y.data_ptr(), ln.data_ptr(), cos.data_ptr(), sin.data_ptr(), ctx, 1, H, Hkv, hd, T,
+                             q2.data_ptr(), kc2.data_ptr(), vc2.data_ptr(), _s()))
+    # the fused form
+    q1 = torch.empty(1, H * hd, dtype=torch.bfloat16, device=DEV)
+    kc1, vc1 = cache[0].clone(), cache[1].clone()
+    _ok(lib, lib.sqx_int4_linear_rope_kv(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(),
+                                         None if ss is None else ss.data_ptr(), nt, 1e-5, ln.data_ptr(), cos.data_ptr(),
+                                         sin.data_ptr(), ctx, H, Hkv, T, q1.data_ptr(), kc1.data_ptr(), vc1.data_ptr(),
+                                         n, k, 128, 0, _s()))
+    torch.cuda.synchronize()
+    assert torch.equal(q1.view(1, H, hd), q2)
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    slot = min(length, T - 1)
+    assert not torch.equal(kc1[:, :, slot], cache[0][:, :, slot])
+
+
 def test_residual_forms_refuse(lib):
     tw = _tiled(64, 4096, 128, seed=3)
     x = torch.zeros(2, 4096, dtype=torch.bfloat16, device=DEV)
