@@ -370,47 +370,66 @@ class Int4DecodeLM:
             tw.wt.data_ptr(), tw.st.data_ptr(), st.h.data_ptr(), st.ss.data_ptr(), st.ss.numel(), self.cfg.norm_eps,
             y.data_ptr(), 1, tw.rows, tw.cols, tw.group_size, 0, stream), "rmsnorm (row factor) + int4 linear")
 
-    def step(self, st: DecodeState, tokens=None) -> Tensor:
+    STEP_KINDS = ("qkv", "attention", "o", "gate_up", "down", "lm_head", "other")
+
+    def step(self, st: DecodeState, tokens=None, only: str | None = None) -> Tensor:
         """Decode one token per row: logits of ``st.tokens`` (or ``tokens``) at each row's position,
         written to ``st.logits``; the greedy picks replace ``st.tokens``; active rows advance. Returns
-        ``st.tokens``. Only device work is issued (no host synchronisation)."""
+        ``st.tokens``. Only device work is issued (no host synchronisation).
+
+        ``only`` (one of ``STEP_KINDS``) issues just the launches of that kind, with the arguments the
+        full step gives them, for timing each kind's share of the step; the results are then
+        meaningless. A norm that runs as a kernel of its own before a linear counts with the linear."""
         cfg, lib = self.cfg, _lib.load()
+        if only is not None and only not in self.STEP_KINDS:
+            raise ValueError(f"only must be one of {self.STEP_KINDS}, got {only!r}")
         if tokens is not None:
             st.set_tokens(tokens, cfg.vocab_size)
         _lib.require_device(st.tokens, self.embed, fn="Int4DecodeLM.step")
         B, d, H, Hkv, hd, T = st.batch, cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, st.max_ctx
         s = _lib.stream_ptr(self.device)
         ck = _lib.check
+
+        def go(kind: str) -> bool:
+            return only is None or only == kind
+
         fuse_silu = self.fuse_silu and lib.sqx_int4_prologue_fits(B, cfg.d_ff)
         sums = (self.fuse_norm_sums and B == 1 and d <= 8192 and lib.sqx_int4_prologue_fits(1, d)
                 and lib.sqx_int4_prologue_fits(1, cfg.d_ff))
+        # one row with a bf16 cache: RoPE and the cache write run in the q|k|v projection's epilogue
+        rope_in_qkv = sums and st.kv_dtype == "bf16"
         with torch.cuda.device(self.device):
-            ck(lib.sqx_embed(self.embed.data_ptr(), cfg.vocab_size, st.tokens.data_ptr(), B, d, st.x[0].data_ptr(), s),
-               "embed")
+            if go("other"):
+                ck(lib.sqx_embed(self.embed.data_ptr(), cfg.vocab_size, st.tokens.data_ptr(), B, d,
+                                 st.x[0].data_ptr(), s), "embed")
             cur, delta, dsplit, have_ss = 0, None, 0, False
-            rope_in_qkv = sums and st.kv_dtype == "bf16"
             for li, ly in enumerate(self.layers):
+                # ---- q|k|v (with the attention norm)
                 if rope_in_qkv:
-                    # one row: q|k|v with RoPE and the cache write in the projection's epilogue, then
-                    # attention over the cache as it stands
-                    if not have_ss:  # layer 0: the norm of the embedding row as a kernel of its own
+                    if not have_ss and go("qkv"):  # layer 0: the norm of the embedding row on its own
                         ck(lib.sqx_rmsnorm(st.x[cur].data_ptr(), None, ly.attn_norm.data_ptr(), cfg.norm_eps, B, d,
                                            None, st.h.data_ptr(), s), "rmsnorm")
-                    ck(lib.sqx_int4_linear_rope_kv(
-                        ly.wqkv.wt.data_ptr(), ly.wqkv.st.data_ptr(), st.h.data_ptr(),
-                        st.ss.data_ptr() if have_ss else None, st.ss.numel(), cfg.norm_eps, st.lengths.data_ptr(),
-                        self.cos.data_ptr(), self.sin.data_ptr(), cfg.context_length, H, Hkv, T, st.q.data_ptr(),
-                        st.k[li].data_ptr(), st.v[li].data_ptr(), ly.wqkv.rows, ly.wqkv.cols, ly.wqkv.group_size, 0, s),
-                       "qkv + rope + cache write")
+                    if go("qkv"):
+                        ck(lib.sqx_int4_linear_rope_kv(
+                            ly.wqkv.wt.data_ptr(), ly.wqkv.st.data_ptr(), st.h.data_ptr(),
+                            st.ss.data_ptr() if have_ss else None, st.ss.numel(), cfg.norm_eps,
+                            st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(), cfg.context_length, H,
+                            Hkv, T, st.q.data_ptr(), st.k[li].data_ptr(), st.v[li].data_ptr(), ly.wqkv.rows,
+                            ly.wqkv.cols, ly.wqkv.group_size, 0, s), "qkv + rope + cache write")
+                elif have_ss:
+                    if go("qkv"):
+                        self._norm_sums_linear(st, ly.wqkv, st.qkv, s)
+                elif go("qkv"):
+                    cur = self._norm_linear(st, cur, delta, ly.attn_norm, ly.wqkv, st.qkv, s, dsplit)
+                else:  # the residual stream advances as the norm's launch would have left it
+                    cur = cur if delta is None else 1 - cur
+                # ---- attention over the cache
+                if not go("attention"):
+                    pass
+                elif rope_in_qkv:
                     ck(lib.sqx_decode_attention(st.q.data_ptr(), st.k[li].data_ptr(), st.v[li].data_ptr(),
                                                 st.lengths.data_ptr(), B, H, Hkv, hd, T, st.attn.data_ptr(),
                                                 st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention")
-                elif have_ss:
-                    self._norm_sums_linear(st, ly.wqkv, st.qkv, s)
-                else:
-                    cur = self._norm_linear(st, cur, delta, ly.attn_norm, ly.wqkv, st.qkv, s, dsplit)
-                if rope_in_qkv:
-                    pass  # attention ran above
                 elif st.kv_dtype == "fp8":
                     ck(lib.sqx_decode_attention_rope_fp8kv(
                         st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
@@ -426,37 +445,61 @@ class Int4DecodeLM:
                     # o and down end in the residual add and leave bf16(h * gain) of the next norm with
                     # the sums of squares of h; the linear after each norm applies its row factor
                     gain_next = self.layers[li + 1].attn_norm if li + 1 < len(self.layers) else self.final_norm
-                    ck(lib.sqx_int4_linear_residual(ly.wo.wt.data_ptr(), ly.wo.st.data_ptr(), st.attn.data_ptr(),
-                                                    st.x[cur].data_ptr(), st.x[1 - cur].data_ptr(), st.ss.data_ptr(),
-                                                    ly.ffn_norm.data_ptr(), st.h.data_ptr(), 1, ly.wo.rows,
-                                                    ly.wo.cols, ly.wo.group_size, 0, s), "o + residual")
+                    if go("o"):
+                        ck(lib.sqx_int4_linear_residual(
+                            ly.wo.wt.data_ptr(), ly.wo.st.data_ptr(), st.attn.data_ptr(), st.x[cur].data_ptr(),
+                            st.x[1 - cur].data_ptr(), st.ss.data_ptr(), ly.ffn_norm.data_ptr(), st.h.data_ptr(), 1,
+                            ly.wo.rows, ly.wo.cols, ly.wo.group_size, 0, s), "o + residual")
                     cur = 1 - cur
-                    self._norm_sums_linear(st, ly.w13, st.gu, s)
-                    ck(lib.sqx_int4_linear_silu_residual(ly.w2.wt.data_ptr(), ly.w2.st.data_ptr(), st.gu.data_ptr(),
-                                                         st.x[cur].data_ptr(), st.x[1 - cur].data_ptr(),
-                                                         st.ss.data_ptr(), gain_next.data_ptr(), st.h.data_ptr(), 1,
-                                                         ly.w2.rows, ly.w2.cols, ly.w2.group_size, 0, s),
-                       "silu + down + residual")
+                    if go("gate_up"):
+                        self._norm_sums_linear(st, ly.w13, st.gu, s)
+                    if go("down"):
+                        ck(lib.sqx_int4_linear_silu_residual(
+                            ly.w2.wt.data_ptr(), ly.w2.st.data_ptr(), st.gu.data_ptr(), st.x[cur].data_ptr(),
+                            st.x[1 - cur].data_ptr(), st.ss.data_ptr(), gain_next.data_ptr(), st.h.data_ptr(), 1,
+                            ly.w2.rows, ly.w2.cols, ly.w2.group_size, 0, s), "silu + down + residual")
                     cur, have_ss = 1 - cur, True
                     continue
-                delta, dsplit = self._delta_linear(st, ly.wo, st.attn, s)
-                cur = self._norm_linear(st, cur, delta, ly.ffn_norm, ly.w13, st.gu, s, dsplit)
+                if go("o"):
+                    delta, dsplit = self._delta_linear(st, ly.wo, st.attn, s)
+                else:
+                    delta, dsplit = self._delta_plan(st, ly.wo)
+                if go("gate_up"):
+                    cur = self._norm_linear(st, cur, delta, ly.ffn_norm, ly.w13, st.gu, s, dsplit)
+                else:
+                    cur = cur if delta is None else 1 - cur
                 if fuse_silu:
-                    ck(lib.sqx_int4_linear_silu(ly.w2.wt.data_ptr(), ly.w2.st.data_ptr(), st.gu.data_ptr(),
-                                                st.delta.data_ptr(), B, ly.w2.rows, ly.w2.cols, ly.w2.group_size, 0, s),
-                       "silu + int4 linear")
+                    if go("down"):
+                        ck(lib.sqx_int4_linear_silu(ly.w2.wt.data_ptr(), ly.w2.st.data_ptr(), st.gu.data_ptr(),
+                                                    st.delta.data_ptr(), B, ly.w2.rows, ly.w2.cols,
+                                                    ly.w2.group_size, 0, s), "silu + int4 linear")
                     delta, dsplit = st.delta.data_ptr(), 0
                 else:
-                    ck(lib.sqx_silu_mul(st.gu.data_ptr(), B, cfg.d_ff, st.act.data_ptr(), s), "silu_mul")
-                    delta, dsplit = self._delta_linear(st, ly.w2, st.act, s)
-            if have_ss:  # the last down projection left bf16(h * final gain) and the sums of squares
+                    if go("down"):
+                        ck(lib.sqx_silu_mul(st.gu.data_ptr(), B, cfg.d_ff, st.act.data_ptr(), s), "silu_mul")
+                        delta, dsplit = self._delta_linear(st, ly.w2, st.act, s)
+                    else:
+                        delta, dsplit = self._delta_plan(st, ly.w2)
+            if not go("lm_head"):
+                pass
+            elif have_ss:  # the last down projection left bf16(h * final gain) and the sums of squares
                 self._norm_sums_linear(st, self.lm_head, st.logits, s)
             else:
-                cur = self._norm_linear(st, cur, delta, self.final_norm, self.lm_head, st.logits, s, dsplit)
-            ck(lib.sqx_argmax(st.logits.data_ptr(), B, cfg.vocab_size, st.tokens.data_ptr(), st.argmax_ws.data_ptr(),
-                              st.argmax_ws.numel() * 4, s), "argmax")
-            ck(lib.sqx_advance(st.lengths.data_ptr(), st.active.data_ptr(), B, s), "advance")
+                self._norm_linear(st, cur, delta, self.final_norm, self.lm_head, st.logits, s, dsplit)
+            if go("other"):
+                ck(lib.sqx_argmax(st.logits.data_ptr(), B, cfg.vocab_size, st.tokens.data_ptr(),
+                                  st.argmax_ws.data_ptr(), st.argmax_ws.numel() * 4, s), "argmax")
+                ck(lib.sqx_advance(st.lengths.data_ptr(), st.active.data_ptr(), B, s), "advance")
         return st.tokens
+
+    def _delta_plan(self, st: DecodeState, tw: i4.Int4Tiled) -> tuple[int, int]:
+        """What :meth:`_delta_linear` would return for ``tw``, without launching it."""
+        lib, B = _lib.load(), st.batch
+        if self.fuse_split_norm and 2 <= B <= _SKINNY_MAX_M:
+            S = lib.sqx_int4_skinny_default_splits(B, tw.rows, tw.cols)
+            if S >= 2:
+                return st.gemm_ws.data_ptr(), S
+        return st.delta.data_ptr(), 0
 
     def capture(self, st: DecodeState) -> torch.cuda.CUDAGraph:
         """Record one :meth:`step` on ``st`` in a HIP graph. Each ``replay()`` decodes the next token
