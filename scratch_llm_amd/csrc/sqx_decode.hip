@@ -469,6 +469,213 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
   }
 }
 
+// The same partials with the scores on the matrix unit (bf16 caches). Per 16 keys a wave computes
+// S^T = K Q^T as four v_mfma_f32_16x16x32_bf16 (A: the 16 key rows, lane l holding dims
+// 32i + 8 (l / 16) .. +8 of key l % 16; B: the G query heads as columns, zero past G; products exact,
+// fp32 sums), so lane l gets the scores of keys 4 (l / 16) + j (j < 4) for head l % 16. The softmax
+// runs in that layout: the step maximum of a head is shared by its four lane groups, so m is the
+// same in every lane of a head and the running l sums stay per lane until the end. The exponentials
+// p go through the wave's own LDS rows to the value layout of the VALU accumulation (lane group kl
+// holds value rows base + 4u + kl, each lane 8 dims, fp32 products and sums as above). This moves
+// the dot products and most of the softmax off the VALU, which bounds the kernel above at large
+// batch (every lane worked every head's scores, 4 fdot2 and 4 row reductions a key).
+template <int G, bool ROPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void attn_partial_mfma_kernel(const uint16_t* __restrict__ q, uint8_t* __restrict__ kc,
+                                                                uint8_t* __restrict__ vc, const int* __restrict__ lengths,
+                                                                const float* __restrict__ cos_t,
+                                                                const float* __restrict__ sin_t, int rope_rows, int H,
+                                                                int Hkv, int tmax, int chunk, int nchunk, float qscale,
+                                                                float* __restrict__ part) {
+  static_assert(G >= 1 && G <= 16, "query heads are the 16 columns of the score tile");
+  const int ch = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kl = lane >> 4, dl = lane & 15;  // value layout: key group, 8-dim slice; score layout: key quad, head
+  const int t0 = ch * chunk;
+  const int span = chunk / 4;
+  const int ws = t0 + wave * span;
+  const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd * 2;  // bytes
+  const int len = max(lengths[b], 0);
+  const int L = min(len + 1, tmax);
+  const int slot = min(len, tmax - 1);
+  if (t0 >= L) return;  // the combine reads only chunks below L
+  const int we = min(ws + span, L);
+
+  __shared__ float sm[4][G], sl[4][G];
+  __shared__ float so[4][G][kHd];
+  __shared__ __attribute__((aligned(16))) float sp[4][16][G < 4 ? 4 : G];  // per wave: p[key][head]
+  __shared__ __attribute__((aligned(16))) float sa[4][G < 4 ? 4 : G];      // per wave: the step's rescale
+
+  const uint16_t* qrow = q + static_cast<int64_t>(b) * (ROPE ? H + 2 * Hkv : H) * kHd;
+  const int64_t pr = ROPE ? static_cast<int64_t>(min(len, rope_rows - 1)) * (kHd / 2) : 0;
+  // the query heads as the B operand: lane l holds dims 32i + 8 kl .. +8 of head dl (zero past G)
+  u32x4_t qv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    u32x4_t v{0u, 0u, 0u, 0u};
+    if (dl < G) {
+      v = *reinterpret_cast<const u32x4_t*>(qrow + (kh * G + dl) * kHd + 32 * i + 8 * kl);
+      if constexpr (ROPE) {
+        float cs[4], sn[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          cs[j] = cos_t[pr + 16 * i + 4 * kl + j];
+          sn[j] = sin_t[pr + 16 * i + 4 * kl + j];
+        }
+        v = rope8(v, cs, sn);
+      }
+    }
+    qv[i] = v;
+  }
+  // ROPE: the new key and value in the value layout (dims 8 dl .. +8); the workgroup holding the
+  // slot writes them to the cache; the value (kept in LDS) stands in for the slot row below
+  __shared__ u32x4_t vnew_lds[ROPE ? 16 : 1];
+  if constexpr (ROPE) {
+    float cs[4], sn[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      cs[j] = cos_t[pr + dl * 4 + j];
+      sn[j] = sin_t[pr + dl * 4 + j];
+    }
+    if (wave == 0 && kl == 0) {
+      const u32x4_t knew = rope8(*reinterpret_cast<const u32x4_t*>(qrow + (H + kh) * kHd + dl * 8), cs, sn);
+      const u32x4_t vnew = *reinterpret_cast<const u32x4_t*>(qrow + (H + Hkv + kh) * kHd + dl * 8);
+      vnew_lds[dl] = vnew;
+      if (ch == slot / chunk) {  // one cache row each, from this workgroup only
+        *reinterpret_cast<u32x4_t*>(kc + head_off + (static_cast<int64_t>(slot) * kHd + dl * 8) * 2) = knew;
+        *reinterpret_cast<u32x4_t*>(vc + head_off + (static_cast<int64_t>(slot) * kHd + dl * 8) * 2) = vnew;
+      }
+    }
+    __syncthreads();
+  }
+  // the rows below L as buffer resources (streaming loads: each row is read once); loads of rows past
+  // them return zero
+  const rsrc_t kr = make_rsrc(kc + head_off, static_cast<uint32_t>(L) * kHd * 2u);
+  const rsrc_t vrs = make_rsrc(vc + head_off, static_cast<uint32_t>(L) * kHd * 2u);
+  float m = -INFINITY, l = 0.0f;  // score layout: head dl's running max (same in its 4 lane groups), lane's l
+  float o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[g][j] = 0.0f;
+
+  for (int base = ws; base < we; base += kKeysPerStep) {
+    // key rows: lane l reads key base + dl (score layout); value rows base + 4u + kl (value layout)
+    const int kk = base + dl;
+    const uint32_t kt = kk < we ? static_cast<uint32_t>(kk) : 0xFFFFFFu;  // past the range: zero rows (score masked)
+    u32x4_t kf[4], vr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kf[i] = bload128<2>(kr, kt * (kHd * 2u) + 16u * kl, 64u * i);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int tv = base + 4 * u + kl;  // rows past the wave's range read as zero (weight 0 meets no NaN)
+      vr[u] = bload128<2>(vrs, (tv < we ? static_cast<uint32_t>(tv) : 0xFFFFFFu) * (kHd * 2u) + 16u * dl, 0u);
+    }
+    if constexpr (ROPE) {
+      if (slot >= base && slot < base + kKeysPerStep) {  // wave-uniform: this step holds the new key
+        if (kk == slot) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float cs[4], sn[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              cs[j] = cos_t[pr + 16 * i + 4 * kl + j];
+              sn[j] = sin_t[pr + 16 * i + 4 * kl + j];
+            }
+            kf[i] = rope8(*reinterpret_cast<const u32x4_t*>(qrow + (H + kh) * kHd + 32 * i + 8 * kl), cs, sn);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (base + 4 * u + kl == slot) vr[u] = vnew_lds[dl];
+      }
+    }
+    f32x4_t sc{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc = ActBF16::mfma(kf[i], qv[i], sc);
+    // score layout: keys base + 4 kl + j of head dl
+    float s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = base + 4 * kl + j < we ? sc[j] * qscale : -INFINITY;
+    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx);
+    // a head whose keys are all masked so far keeps m = -inf and adds nothing
+    const float a = mn == -INFINITY ? 1.0f : exp2f(m - mn);
+    float p[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[j] = s[j] == -INFINITY ? 0.0f : exp2f(s[j] - mn);
+    l = fmaf(l, a, (p[0] + p[1]) + (p[2] + p[3]));
+    m = mn;
+    if (dl < G) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sp[wave][4 * kl + j][dl] = p[j];
+      if (kl == 0) sa[wave][dl] = a;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's own rows are written before it reads them
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+    float pv[4][G], av[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) av[g] = sa[wave][g];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int g = 0; g < G; ++g) pv[u][g] = sp[wave][4 * u + kl][g];
+    __builtin_amdgcn_wave_barrier();  // and the next step's writes after these reads
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float e = o[g][j] * av[g];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) e = fmaf(pv[u][g], (j & 1) ? bf16_hi(vr[u][j >> 1]) : bf16_lo(vr[u][j >> 1]), e);
+        o[g][j] = e;
+      }
+    }
+  }
+  // the lane groups of the wave: m is already common to a head's lanes, so l and o simply add
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      o[g][j] += __shfl_xor(o[g][j], 16, 64);
+      o[g][j] += __shfl_xor(o[g][j], 32, 64);
+    }
+  if (kl == 0) {
+    if (dl < G) {
+      sm[wave][dl] = m;
+      sl[wave][dl] = l;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) so[wave][g][dl * 8 + j] = o[g][j];
+  }
+  __syncthreads();
+  // merge the 4 waves: thread (g, dd) writes element dd of head g's partial
+  for (int idx = threadIdx.x; idx < G * kHd; idx += 256) {
+    const int g = idx / kHd, dd = idx % kHd;
+    const float M = fmaxf(fmaxf(sm[0][g], sm[1][g]), fmaxf(sm[2][g], sm[3][g]));
+    float lsum = 0.0f, osum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float a = sm[w][g] == -INFINITY ? 0.0f : exp2f(sm[w][g] - M);
+      lsum = fmaf(sl[w][g], a, lsum);
+      osum = fmaf(so[w][g][dd], a, osum);
+    }
+    float* pp = part + ((static_cast<int64_t>(b) * H + kh * G + g) * nchunk + ch) * (kHd + 2);
+    if (dd == 0) {
+      pp[0] = M;
+      pp[1] = lsum;
+    }
+    pp[2 + dd] = osum;
+  }
+}
+
 // out[b, h*hd + d] = bf16(sum_c 2^(m_c - M) o_c[d] / sum_c 2^(m_c - M) l_c) over the chunks c that
 // hold keys of row b. Row layout [B, H*hd] is the (B, 1, H*hd) view that o_proj takes (model.py:365).
 // One workgroup of 256 threads per (head, row): the chunk maxima and weights are formed in parallel
@@ -722,10 +929,19 @@ extern "C" int sqx_rope_kv(const void* qkv, const int* lengths, const float* cos
   return SQX_OK;
 }
 
-// Keys per workgroup: the smallest of 64..512 that still gives about 2048 workgroups.
+// Keys per workgroup: the smallest of 64..1024 that still gives about SQX_ATTN_TARGET_WG workgroups
+// (four resident per CU at the score kernel's register budget; longer walks per wave amortise each
+// workgroup's set-up and merge: measured at 2048 keys, B = 8 / 32 / 64 take 22 / 60 / 107 us against
+// 29 / 67 / 114 us with a 2048-workgroup target and 512-key chunks).
+#ifndef SQX_ATTN_TARGET_WG
+#define SQX_ATTN_TARGET_WG 1024
+#endif
+#ifndef SQX_ATTN_MAX_CHUNK
+#define SQX_ATTN_MAX_CHUNK 1024
+#endif
 extern "C" int sqx_attn_chunk(int64_t B, int64_t Hkv, int64_t tmax) {
   int c = 64;
-  while (c < 512 && B * Hkv * ceil_div(tmax, 2 * c) >= 2048) c *= 2;
+  while (c < SQX_ATTN_MAX_CHUNK && B * Hkv * ceil_div(tmax, 2 * c) >= SQX_ATTN_TARGET_WG) c *= 2;
   return c;
 }
 
@@ -787,11 +1003,24 @@ static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, co
     case 4: SQX_ATTN(4, R_, K8_); break;   \
     default: SQX_ATTN(8, R_, K8_); break;  \
   }
-  if (rope) {
-    if (kv8) { SQX_ATTN_G(true, true) } else { SQX_ATTN_G(true, false) }
-  } else {
-    if (kv8) { SQX_ATTN_G(false, true) } else { SQX_ATTN_G(false, false) }
+#define SQX_ATTN_M(G_, R_)                                                                                           \
+  hipLaunchKernelGGL((attn_partial_mfma_kernel<G_, R_>), grid, dim3(256), 0, s, qp, kp, vp, lengths, cos_t, sin_t, rr, \
+                     iH, iK, iT, chunk, nchunk, qscale, w)
+#define SQX_ATTN_MG(R_)                      \
+  switch (G) {                               \
+    case 1: SQX_ATTN_M(1, R_); break;        \
+    case 2: SQX_ATTN_M(2, R_); break;        \
+    case 4: SQX_ATTN_M(4, R_); break;        \
+    default: SQX_ATTN_M(8, R_); break;       \
   }
+  // bf16 caches: scores on the matrix unit; E4M3 caches: the VALU form (keys decoded per row)
+  if (rope) {
+    if (kv8) { SQX_ATTN_G(true, true) } else { SQX_ATTN_MG(true) }
+  } else {
+    if (kv8) { SQX_ATTN_G(false, true) } else { SQX_ATTN_MG(false) }
+  }
+#undef SQX_ATTN_MG
+#undef SQX_ATTN_M
 #undef SQX_ATTN_G
 #undef SQX_ATTN
   SQX_LAUNCH_CHECK(fn);
