@@ -479,6 +479,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
 // holds value rows base + 4u + kl, each lane 8 dims, fp32 products and sums as above). This moves
 // the dot products and most of the softmax off the VALU, which bounds the kernel above at large
 // batch (every lane worked every head's scores, 4 fdot2 and 4 row reductions a key).
+#ifndef SQX_ATTN_INTERLEAVE
+#define SQX_ATTN_INTERLEAVE 1
+#endif
 template <int G, bool ROPE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void attn_partial_mfma_kernel(const uint16_t* __restrict__ q, uint8_t* __restrict__ kc,
                                                                 uint8_t* __restrict__ vc, const int* __restrict__ lengths,
@@ -491,14 +494,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kl = lane >> 4, dl = lane & 15;  // value layout: key group, 8-dim slice; score layout: key quad, head
   const int t0 = ch * chunk;
+#if SQX_ATTN_INTERLEAVE
+  // the 4 waves take alternate 16-key blocks of the chunk: the workgroup streams one region
+  const int ws = t0 + wave * kKeysPerStep;
+  constexpr int kWaveStride = 4 * kKeysPerStep;
+#else
   const int span = chunk / 4;
   const int ws = t0 + wave * span;
+  constexpr int kWaveStride = kKeysPerStep;
+#endif
   const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd * 2;  // bytes
   const int len = max(lengths[b], 0);
   const int L = min(len + 1, tmax);
   const int slot = min(len, tmax - 1);
   if (t0 >= L) return;  // the combine reads only chunks below L
+#if SQX_ATTN_INTERLEAVE
+  const int we = min(t0 + chunk, L);
+#else
   const int we = min(ws + span, L);
+#endif
 
   __shared__ float sm[4][G], sl[4][G];
   __shared__ float so[4][G][kHd];
@@ -558,7 +572,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[g][j] = 0.0f;
 
-  for (int base = ws; base < we; base += kKeysPerStep) {
+  for (int base = ws; base < we; base += kWaveStride) {
     // key rows: lane l reads key base + dl (score layout); value rows base + 4u + kl (value layout)
     const int kk = base + dl;
     const uint32_t kt = kk < we ? static_cast<uint32_t>(kk) : 0xFFFFFFu;  // past the range: zero rows (score masked)
@@ -939,8 +953,11 @@ extern "C" int sqx_rope_kv(const void* qkv, const int* lengths, const float* cos
 #ifndef SQX_ATTN_MAX_CHUNK
 #define SQX_ATTN_MAX_CHUNK 1024
 #endif
+#ifndef SQX_ATTN_MIN_CHUNK
+#define SQX_ATTN_MIN_CHUNK 64
+#endif
 extern "C" int sqx_attn_chunk(int64_t B, int64_t Hkv, int64_t tmax) {
-  int c = 64;
+  int c = SQX_ATTN_MIN_CHUNK;
   while (c < SQX_ATTN_MAX_CHUNK && B * Hkv * ceil_div(tmax, 2 * c) >= SQX_ATTN_TARGET_WG) c *= 2;
   return c;
 }
