@@ -828,13 +828,15 @@ extern "C" int sqx_mxfp4_gemm_ws(const uint8_t* xt, const uint8_t* xst, const ui
 }
 
 namespace {
-// K splits for a shape: when the output tiles fill less than three quarters of the 256 CUs, enough
-// splits for one workgroup per CU, at least 4 stages (256 columns) per split, and no empty split.
+// K splits for a shape: when the output tiles fill less than three quarters of the 256 CUs, as many
+// splits as keep the workgroups within one round on the CUs (a second, partial round costs more than
+// the splits save, and every split adds M x N fp32 partials to write and reduce), at least 4 stages
+// (256 columns) per split, and no empty split.
 int dq_splits(int64_t m, int64_t rows, int64_t cols) {
   const int64_t tiles = ceil_div(m, dqg::kTile) * ceil_div(rows, dqg::kTile);
   const int64_t S = 2 * ceil_div(cols, 128);
   if (tiles >= 192) return 1;
-  const int64_t want = std::min<int64_t>(std::min<int64_t>(ceil_div(256, tiles), S / 4), 16);
+  const int64_t want = std::min<int64_t>(std::min<int64_t>(256 / tiles, S / 4), 16);
   if (want < 2) return 1;
   const int64_t per = ceil_div(S, want);
   return (int)ceil_div(S, per);

@@ -164,3 +164,24 @@ def test_quantize_uint4_asym_bitexact(param, n, k, group):
     assert np.array_equal(q.cpu().numpy(), qr)
     assert np.array_equal(bits(s.float().cpu().numpy()), bits(sr))
     assert np.array_equal(bits(z.float().cpu().numpy()), bits(zr))
+
+
+@pytest.mark.parametrize("rows,cols,dtype,offset", [(2048, 4096, torch.bfloat16, 0), (64, 14336, torch.float16, 0),
+                                                     (3, 100, torch.bfloat16, 0), (5, 4096, torch.bfloat16, 1)])
+def test_scale_columns_bitexact(aw, rows, cols, dtype, offset):
+    """sqx_scale_columns (the AWQ linear's x / s pass) is bf16/fp16(fp32 x / s) with IEEE division, bit
+    for bit: the 16-byte form (cols % 8 == 0, aligned) and the element form (ragged or unaligned)."""
+    from scratch_llm_amd import _lib
+
+    print_case("scale_columns", rows, cols, dtype, offset)
+    g = torch.Generator().manual_seed(rows + cols)
+    x = (torch.randn(rows * cols + offset, generator=g) * 3).to(dtype)
+    s = torch.exp(torch.empty(cols).uniform_(-2.0, 2.0, generator=g))
+    xd, sd = x.to(DEV), s.to(DEV)
+    out = torch.empty(rows * cols + offset, dtype=dtype, device=DEV)
+    lib = _lib.load()
+    _lib.check(lib.sqx_scale_columns(xd[offset:].data_ptr(), _lib.sqx_dtype(dtype), sd.data_ptr(), rows, cols,
+                                     out[offset:].data_ptr(), _lib.stream_ptr(xd.device)), "scale_columns")
+    torch.cuda.synchronize()
+    want = (x[offset:].view(rows, cols).float() / s).to(dtype)
+    assert torch.equal(out[offset:].cpu().view(rows, cols), want)
