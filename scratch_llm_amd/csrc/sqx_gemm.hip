@@ -351,7 +351,7 @@ struct DqW {
   static_assert(NP <= 16, "parameter copies fit two per wave");
 };
 
-template <class A, int FMT, bool ASYM, bool PBF16, int GROUP, int YKIND>
+template <class A, int FMT, bool ASYM, bool PBF16, int GROUP, int YKIND, int TMR = 256>
 __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict__ x, const uint8_t* __restrict__ wt,
                                                      const void* __restrict__ st, const void* __restrict__ zt,
                                                      const float* __restrict__ s_global, void* __restrict__ y,
@@ -359,10 +359,14 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
                                                      int tiles_m, int tiles_n, int lds16, int splits,
                                                      float* __restrict__ ws) {
   using P = DqW<FMT, ASYM, PBF16, GROUP>;
+  static_assert(TMR == 256 || TMR == 128, "256- or 128-row output tiles");
   constexpr int group = GROUP;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int NS = dqg::kStages;
-  constexpr int kPerStage = 4 + P::kWInstr + P::kPInstr;  // buffer -> LDS copies per wave per stage
+  constexpr int kXI = TMR / 64;   // activation copies per wave per stage (8 rows each)
+  constexpr int RPW = TMR / 8;    // activation rows a wave copies
+  constexpr int MT = TMR / 32;    // 16-row MFMA tiles of a wave (it owns TMR / 2 rows)
+  constexpr int kPerStage = kXI + P::kWInstr + P::kPInstr;  // buffer -> LDS copies per wave per stage
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int tm, tn;
@@ -390,15 +394,15 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
   auto issue = [&](int s, int slot) {
     uint8_t* base = smem + slot * dqg::kStage;
     const int kb = s >> 1, h = s & 1;
-    // activations: wave w copies rows 32w .. 32w+31 (8 rows of 8 chunks per instruction)
+    // activations: wave w copies rows RPW*w .. RPW*w + RPW-1 (8 rows of 8 chunks per instruction)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = 32 * wave + 8 * j + (lane >> 3);
+    for (int j = 0; j < kXI; ++j) {
+      const int r = RPW * wave + 8 * j + (lane >> 3);
       const int c = (lane & 7) ^ (r & 7);
-      const int R = tm * dqg::kTile + r, col = 64 * s + 8 * c;
+      const int R = tm * TMR + r, col = 64 * s + 8 * c;
       const bool ok = (R < m) & (col < K);  // no short-circuit: a select, not a branch
       const uint32_t off = ok ? ((uint32_t)R * (uint32_t)K + (uint32_t)col) * 2u : 0xFFFFFFF0u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(base + (32 * wave + 8 * j) * 128), 16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(base + (RPW * wave + 8 * j) * 128), 16, off, 0, 0, 0);
     }
     uint8_t* wbase = base + dqg::kXBytes;
     if (FMT == kDqInt4) {
@@ -448,9 +452,9 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
     }
   };
 
-  f32x4_t acc[8][4];
+  f32x4_t acc[MT][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
@@ -460,7 +464,7 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
   // p1: fp32 zero-points (asymmetric INT4 with fp32 parameters only)
   constexpr int kP1 = (FMT == kDqInt4 && ASYM && !PBF16) ? 4 : 1;
   struct Raw {
-    u32x4_t xo[8];   // activation operands of the 8 row tiles
+    u32x4_t xo[MT];  // activation operands of the wave's row tiles
     uint32_t wd[4];  // weight codes of the 4 column tiles
     uint32_t p0[4], p1[kP1];
   };
@@ -468,8 +472,8 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
   auto read = [&](int slot, int s, int q, Raw& o) {
     const uint8_t* base = smem + slot * dqg::kStage;
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) {
-      const int r = wm * 128 + 16 * mt + nl;
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = wm * (TMR / 2) + 16 * mt + nl;
       const int sl = (4 * q + jg) ^ (nl & 7);
       o.xo[mt] = *reinterpret_cast<const u32x4_t*>(base + r * 128 + sl * 16);
     }
@@ -546,7 +550,7 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
     for (int nt = 0; nt < 4; ++nt) {
       const u32x4_t b = decode(o, nt);
 #pragma unroll
-      for (int mt = 0; mt < 8; ++mt) acc[mt][nt] = A::mfma(b, o.xo[mt], acc[mt][nt]);
+      for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = A::mfma(b, o.xo[mt], acc[mt][nt]);
     }
   };
 
@@ -584,7 +588,7 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
   }
 
   // epilogue: acc[mt][nt][i] is y[m0 + 16mt + (l & 15)][n0 + 16nt + 4(l >> 4) + i]
-  const int m0 = tm * dqg::kTile + wm * 128;
+  const int m0 = tm * TMR + wm * (TMR / 2);
   const int n0 = tn * dqg::kTile + wn * 64;
   if (splits > 1) {
     // raw fp32 partial sums of this split; dq_reduce_kernel adds the splits in order
@@ -594,7 +598,7 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
       const int col = n0 + 16 * nt + 4 * jg;
       if (col >= n) continue;
 #pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
+      for (int mt = 0; mt < MT; ++mt) {
         const int row = m0 + 16 * mt + nl;
         if (row >= m) continue;
         float* dst = part + (int64_t)row * n + col;
@@ -623,7 +627,7 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
           if (n0 + cl + j < n) badd[j] = YKIND == 1 ? f16_bits_to_f32(bias[n0 + cl + j]) : bf16_bits_to_f32(bias[n0 + cl + j]);
       }
 #pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
+      for (int mt = 0; mt < MT; ++mt) {
         const int rl = 16 * mt + nl;
         float v[4];
 #pragma unroll
@@ -636,7 +640,7 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
     __builtin_amdgcn_wave_barrier();
     const int cc = (lane & 7) * 8;
 #pragma unroll 4
-    for (int p = 0; p < 16; ++p) {
+    for (int p = 0; p < TMR / 16; ++p) {
       const int rl = 8 * p + (lane >> 3);
       const int row = m0 + rl, col = n0 + cc;
       const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ep + rl * dqg::kEpiPitch + cc * 2);
@@ -651,7 +655,7 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
     const int col = n0 + 16 * nt + 4 * jg;
     if (col >= n) continue;
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       const int row = m0 + 16 * mt + nl;
       if (row >= m) continue;
       const int64_t o = (int64_t)row * n + col;
@@ -832,8 +836,14 @@ namespace {
 // splits as keep the workgroups within one round on the CUs (a second, partial round costs more than
 // the splits save, and every split adds M x N fp32 partials to write and reduce), at least 4 stages
 // (256 columns) per split, and no empty split.
+// Output-tile rows: 128 for M <= 128, where a 256-row tile is at least half padding (config 4's
+// bf16 activations at M = 128: 106 -> 74 us and 96 -> 65 us), else 256: a 128-row tile decodes each
+// weight for half as many MFMAs, and at M = 512 / 2048 it measured slower on the 14336-wide shapes
+// (97 -> 104 us, 298 -> 364 us) and within 6 % elsewhere.
+int dq_tile_rows(int64_t m, int64_t) { return m <= 128 ? 128 : 256; }
+
 int dq_splits(int64_t m, int64_t rows, int64_t cols) {
-  const int64_t tiles = ceil_div(m, dqg::kTile) * ceil_div(rows, dqg::kTile);
+  const int64_t tiles = ceil_div(m, dq_tile_rows(m, rows)) * ceil_div(rows, dqg::kTile);
   const int64_t S = 2 * ceil_div(cols, 128);
   if (tiles >= 192) return 1;
   const int64_t want = std::min<int64_t>(std::min<int64_t>(256 / tiles, S / 4), 16);
@@ -846,11 +856,12 @@ template <class A, int FMT, bool ASYM, bool PBF16, int GROUP, int YK>
 hipError_t launch_dq(const uint16_t* x, const uint8_t* wt, const void* st, const void* zt, const float* s_global,
                      void* y, const uint16_t* bias, int m, int n, int K, int KB, float* ws, int64_t ws_bytes,
                      hipStream_t s) {
-  const int tiles_m = (m + dqg::kTile - 1) / dqg::kTile, tiles_n = (n + dqg::kTile - 1) / dqg::kTile;
+  const int tmr = dq_tile_rows(m, n);
+  const int tiles_m = (m + tmr - 1) / tmr, tiles_n = (n + dqg::kTile - 1) / dqg::kTile;
   int splits = dq_splits(m, n, K);
   if (splits > 1 && (ws == nullptr || ws_bytes < (int64_t)splits * m * n * 4 || reinterpret_cast<uintptr_t>(ws) % 16))
     splits = 1;  // no (or too small a) workspace: one pass per tile
-  auto kern = dq_gemm_kernel<A, FMT, ASYM, PBF16, GROUP, YK>;
+  auto kern = tmr == 128 ? dq_gemm_kernel<A, FMT, ASYM, PBF16, GROUP, YK, 128> : dq_gemm_kernel<A, FMT, ASYM, PBF16, GROUP, YK, 256>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      dqg::kLds);
   if (e != hipSuccess) return e;
