@@ -97,6 +97,14 @@ int sqx_int4_tile(const int8_t* codes, int code_kind, const void* scales, const 
 int sqx_int4_tile_packed(const uint8_t* packed, const void* scales, int param_dtype, int64_t rows,
                          int64_t cols, int64_t group, uint8_t* wt, void* st, sqx_stream_t stream);
 
+/* The inverse of sqx_int4_tile (no reference counterpart: it gives back the reference's tensors from
+ * the kernel layout, so a module can hold the tiled copy only). codes: int8 [rows, cols] (code_kind 0:
+ * signed symmetric codes, 1: unsigned asymmetric codes); scales (and zeros for code_kind 1):
+ * [rows, cols/group] of param_dtype. Bit-exact round trip. */
+int sqx_int4_untile(const uint8_t* wt, const void* st, const void* zt, int param_dtype, int code_kind,
+                    int64_t rows, int64_t cols, int64_t group, int8_t* codes, void* scales, void* zeros,
+                    sqx_stream_t stream);
+
 /* Number of k-slices (waves per 16-row tile) the decode GEMV takes when sqx_int4_linear runs it
  * with k_slices <= 0; passing this value explicitly always selects the GEMV. */
 int sqx_int4_linear_default_kslices(int64_t m, int64_t rows, int64_t cols);
@@ -329,6 +337,12 @@ int64_t sqx_fp4_tiled_scale_bytes(int64_t rows, int64_t cols, int fmt);
 int sqx_fp4_tile(const uint8_t* codes, int codes_packed, const void* scales, int scale_kind, int64_t block,
                  int64_t rows, int64_t cols, uint8_t* wt, uint8_t* st, sqx_stream_t stream);
 
+/* The inverse of sqx_fp4_tile (no reference counterpart): packed uint8 [rows, cols/2] in the
+ * reference's pack_fp4 order (the on-disk weight_packed), scales uint8 row-major: E8M0 [rows, cols/32]
+ * (fmt SQX_FP4_MX) or E4M3 [rows, cols/16] (SQX_FP4_NV, one byte per 16-column block). */
+int sqx_fp4_untile(const uint8_t* wt, const uint8_t* st, int fmt, int64_t rows, int64_t cols, uint8_t* packed,
+                   uint8_t* scales, sqx_stream_t stream);
+
 /* The second NVFP4 convention, the b_r6 GEMM rung's operands (kernels/gemm/cuda/b_r6.py:155-244 with
  * kernels/gemm/nvfp4_layout.py:341-416). Per block of 16 along k, in float64: scale = the smallest
  * unsigned-E4M3 value >= amax / 6 (ceil onto the grid; no global scale; an all-zero block gets 0),
@@ -483,6 +497,9 @@ int64_t sqx_int8_tiled_weight_bytes(int64_t rows, int64_t cols);
 
 /* Re-lay symmetric int8 codes q [rows, cols] for sqx_int8_linear (no reference counterpart). */
 int sqx_int8_tile(const int8_t* q, int64_t rows, int64_t cols, uint8_t* wt, sqx_stream_t stream);
+
+/* The inverse of sqx_int8_tile (no reference counterpart): q int8 [rows, cols]. */
+int sqx_int8_untile(const uint8_t* wt, int64_t rows, int64_t cols, int8_t* q, sqx_stream_t stream);
 
 /* Int8 weight-only linear, BASELINE config 1 (quantize_symmetric(W, axis=0) + dequantize_symmetric,
  * int8.py:102-130, composed with F.linear): y[m, r] = scale[r] * sum_c x[m, c] * q[r, c] (+ bias[r]).

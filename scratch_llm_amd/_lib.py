@@ -44,6 +44,9 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sqx_int4_tiled_param_count": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "sqx_int4_tile": (_c_i, [_c_p, _c_i, _c_p, _c_p, _c_i, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p]),
     "sqx_int4_tile_packed": (_c_i, [_c_p, _c_p, _c_i, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "sqx_int4_untile": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_i, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p]),
+    "sqx_int8_untile": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_fp4_untile": (_c_i, [_c_p, _c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "sqx_int4_linear_default_kslices": (_c_i, [_c_i64, _c_i64, _c_i64]),
     "sqx_int4_linear": (
         _c_i,

@@ -364,6 +364,52 @@ __global__ __launch_bounds__(256) void fp4_tile_scales_kernel(const void* __rest
   st[o] = static_cast<uint8_t>(byte);
 }
 
+// The inverse re-layout. A lane's 16 tiled bytes are the reference's packed bytes of columns
+// c0 .. c0+31 of its row (even element in the low nibble), so each thread copies its chunk back to
+// packed [rows, cols/2] (byte by byte at a ragged end); each tiled scale byte goes back to the
+// row-major [rows, cols/32] (MXFP4 E8M0) or [rows, cols/16] (NVFP4 E4M3) array.
+__global__ __launch_bounds__(256) void fp4_untile_weights_kernel(const u32x4_t* __restrict__ wt, int64_t rows,
+                                                                 int64_t cols, int64_t KB, int64_t n_chunks,
+                                                                 uint8_t* __restrict__ packed) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= n_chunks) return;
+  const int L = static_cast<int>(q & 63);
+  const int64_t blk = q >> 6;
+  const int64_t t = blk / KB;
+  const int64_t kb = blk - t * KB;
+  const int64_t r = 16 * t + (L & 15);
+  const int64_t c0 = kb * 128 + 32 * (L >> 4);
+  if (r >= rows || c0 >= cols) return;
+  const u32x4_t v = wt[q];
+  uint8_t* dst = packed + r * (cols / 2) + c0 / 2;
+  if (c0 + 32 <= cols && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+    *reinterpret_cast<u32x4_t*>(dst) = v;
+  } else {
+    for (int b = 0; b < 16 && c0 + 2 * b < cols; ++b) {
+      const uint32_t w = v[b >> 2];  // through a scalar: hipcc's element access of a vector value
+      dst[b] = static_cast<uint8_t>(w >> (8 * (b & 3)));
+    }
+  }
+}
+
+template <bool NVK>
+__global__ __launch_bounds__(256) void fp4_untile_scales_kernel(const uint8_t* __restrict__ st, int64_t rows,
+                                                                int64_t cols, int64_t KB, int64_t n_in,
+                                                                uint8_t* __restrict__ scales) {
+  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= n_in) return;
+  constexpr int PER_BLOCK = NVK ? 128 : 64;
+  constexpr int BS = NVK ? 16 : 32;
+  const int64_t blk = o / PER_BLOCK;
+  const int j = static_cast<int>(o - blk * PER_BLOCK);
+  const int L = NVK ? (j >> 1) : j;
+  const int64_t t = blk / KB;
+  const int64_t kb = blk - t * KB;
+  const int64_t r = 16 * t + (L & 15);
+  const int64_t c0 = kb * 128 + 32 * (L >> 4) + (NVK ? 16 * (j & 1) : 0);
+  if (r < rows && c0 < cols) scales[r * (cols / BS) + c0 / BS] = st[o];
+}
+
 // ----------------------------------------------------------------------------------------------
 // GEMV policies
 // ----------------------------------------------------------------------------------------------
@@ -759,6 +805,29 @@ extern "C" int sqx_fp4_tile(const uint8_t* codes, int codes_packed, const void* 
   else
     hipLaunchKernelGGL(fp4_tile_scales_kernel<3>, grid_for(ns), dim3(256), 0, s, scales, rows, cols, block, KB, ns, st);
   SQX_LAUNCH_CHECK("sqx_fp4_tile");
+  return SQX_OK;
+}
+
+extern "C" int sqx_fp4_untile(const uint8_t* wt, const uint8_t* st, int fmt, int64_t rows, int64_t cols,
+                              uint8_t* packed, uint8_t* scales, sqx_stream_t stream) {
+  SQX_REQUIRE(fmt == SQX_FP4_MX || fmt == SQX_FP4_NV, SQX_E_ARG, "sqx_fp4_untile: bad fmt %d", fmt);
+  const int bs = fmt == SQX_FP4_NV ? 16 : 32;
+  SQX_REQUIRE(rows > 0 && cols > 0 && cols % bs == 0 && rows <= ((int64_t)1 << 30) && cols <= ((int64_t)1 << 30),
+              SQX_E_ARG, "sqx_fp4_untile: bad shape [%lld, %lld] (cols a multiple of %d)", (long long)rows,
+              (long long)cols, bs);
+  SQX_REQUIRE(wt && st && packed && scales, SQX_E_ARG, "sqx_fp4_untile: null pointer");
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0, SQX_E_ARG, "sqx_fp4_untile: wt must be 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  const int64_t KB = ceil_div(cols, 128);
+  const int64_t chunks = ceil_div(rows, 16) * KB * 64;
+  hipLaunchKernelGGL(fp4_untile_weights_kernel, grid_for(chunks), dim3(256), 0, s,
+                     reinterpret_cast<const u32x4_t*>(wt), rows, cols, KB, chunks, packed);
+  const int64_t ns = sqx_fp4_tiled_scale_bytes(rows, cols, fmt);
+  if (fmt == SQX_FP4_NV)
+    hipLaunchKernelGGL(fp4_untile_scales_kernel<true>, grid_for(ns), dim3(256), 0, s, st, rows, cols, KB, ns, scales);
+  else
+    hipLaunchKernelGGL(fp4_untile_scales_kernel<false>, grid_for(ns), dim3(256), 0, s, st, rows, cols, KB, ns, scales);
+  SQX_LAUNCH_CHECK("sqx_fp4_untile");
   return SQX_OK;
 }
 

@@ -323,6 +323,48 @@ __global__ __launch_bounds__(256) void int4_tile_params_kernel(const P* __restri
   dst[o] = (r < rows && g < n_groups) ? src[r * n_groups + g] : P(0);
 }
 
+// The inverse re-layout (tiles -> the reference's row-major codes and [rows, groups] parameters):
+// one thread per tiled dword writes its 8 codes (u - 8 for SIGNED), one per tiled parameter element
+// writes it back; padding rows and columns are skipped.
+template <bool SIGNED>
+__global__ __launch_bounds__(256) void int4_untile_weights_kernel(const uint32_t* __restrict__ wt, int64_t rows,
+                                                                  int64_t cols, int64_t KB, int64_t n_dwords,
+                                                                  int8_t* __restrict__ codes) {
+  const int64_t d = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= n_dwords) return;
+  const int i = static_cast<int>(d & 3);
+  const int L = static_cast<int>((d >> 2) & 63);
+  const int64_t blk = d >> 8;
+  const int64_t t = blk / KB;
+  const int64_t kb = blk - t * KB;
+  const int64_t r = 16 * t + (L & 15);
+  if (r >= rows) return;
+  const int64_t c0 = kb * 128 + 32 * i + 8 * (L >> 4);
+  const uint32_t word = wt[d];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t c = c0 + e;
+    if (c >= cols) break;
+    const int pos = (e & 1) ? 16 + 4 * (e >> 1) : 4 * (e >> 1);
+    const int u = static_cast<int>((word >> pos) & 0xFu);
+    codes[r * cols + c] = static_cast<int8_t>(SIGNED ? u - 8 : u);
+  }
+}
+
+template <typename P>
+__global__ __launch_bounds__(256) void int4_untile_params_kernel(const P* __restrict__ src, int64_t rows,
+                                                                 int64_t n_groups, int64_t Gp, int64_t n_in,
+                                                                 P* __restrict__ dst) {
+  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= n_in) return;
+  const int64_t nl = o & 15;
+  const int64_t tg = o >> 4;
+  const int64_t t = tg / Gp;
+  const int64_t g = tg - t * Gp;
+  const int64_t r = 16 * t + nl;
+  if (r < rows && g < n_groups) dst[r * n_groups + g] = src[o];
+}
+
 // ----------------------------------------------------------------------------------------------
 // The linear: the int4 weight policy of the shared GEMV (sqx_gemv.h)
 // ----------------------------------------------------------------------------------------------
@@ -791,6 +833,40 @@ extern "C" int sqx_int4_tile_packed(const uint8_t* packed, const void* scales, i
                      dim3(256), 0, s, packed, rows, cols, KB, n_dwords, reinterpret_cast<uint32_t*>(wt));
   tile_params(scales, param_dtype, rows, cols, group, st, s);
   SQX_LAUNCH_CHECK("sqx_int4_tile_packed");
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_untile(const uint8_t* wt, const void* st, const void* zt, int param_dtype, int code_kind,
+                               int64_t rows, int64_t cols, int64_t group, int8_t* codes, void* scales, void* zeros,
+                               sqx_stream_t stream) {
+  int rc = check_tile_args(rows, cols, group, param_dtype);
+  if (rc) return rc;
+  SQX_REQUIRE(code_kind == 0 || code_kind == 1, SQX_E_ARG, "sqx_int4_untile: code_kind must be 0 or 1");
+  SQX_REQUIRE(wt && st && codes && scales, SQX_E_ARG, "sqx_int4_untile: null pointer");
+  SQX_REQUIRE(code_kind == 0 || (zt && zeros), SQX_E_ARG, "sqx_int4_untile: asymmetric codes need zt and zeros");
+  hipStream_t s = as_stream(stream);
+  const int64_t KB = ceil_div(cols, 128);
+  const int64_t n_dwords = ceil_div(rows, 16) * KB * 256;
+  const dim3 grid(static_cast<unsigned>(ceil_div(n_dwords, 256)));
+  const uint32_t* w32 = reinterpret_cast<const uint32_t*>(wt);
+  if (code_kind == 0)
+    hipLaunchKernelGGL(int4_untile_weights_kernel<true>, grid, dim3(256), 0, s, w32, rows, cols, KB, n_dwords, codes);
+  else
+    hipLaunchKernelGGL(int4_untile_weights_kernel<false>, grid, dim3(256), 0, s, w32, rows, cols, KB, n_dwords, codes);
+  const int64_t n_groups = cols / group, Gp = KB * (128 / group);
+  const int64_t n_in = ceil_div(rows, 16) * Gp * 16;
+  const dim3 pgrid(static_cast<unsigned>(ceil_div(n_in, 256)));
+  for (int k = 0; k < (code_kind == 1 ? 2 : 1); ++k) {
+    const void* src = k == 0 ? st : zt;
+    void* dst = k == 0 ? scales : zeros;
+    if (param_dtype == SQX_DTYPE_F32)
+      hipLaunchKernelGGL(int4_untile_params_kernel<float>, pgrid, dim3(256), 0, s, static_cast<const float*>(src), rows,
+                         n_groups, Gp, n_in, static_cast<float*>(dst));
+    else
+      hipLaunchKernelGGL(int4_untile_params_kernel<uint16_t>, pgrid, dim3(256), 0, s,
+                         static_cast<const uint16_t*>(src), rows, n_groups, Gp, n_in, static_cast<uint16_t*>(dst));
+  }
+  SQX_LAUNCH_CHECK("sqx_int4_untile");
   return SQX_OK;
 }
 

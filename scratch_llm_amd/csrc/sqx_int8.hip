@@ -334,6 +334,27 @@ __global__ __launch_bounds__(256) void int8_tile_kernel(const int8_t* __restrict
   wt[d] = word;
 }
 
+// The inverse re-layout: one thread per tiled dword writes its 4 codes back to q [rows, cols].
+__global__ __launch_bounds__(256) void int8_untile_kernel(const uint32_t* __restrict__ wt, int64_t rows, int64_t cols,
+                                                          int64_t KB, int64_t n_dwords, int8_t* __restrict__ q) {
+  const int64_t d = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= n_dwords) return;
+  const int i = static_cast<int>(d & 3);
+  const int L = static_cast<int>((d >> 2) & 63);
+  const int64_t blk = d >> 8;
+  const int64_t t = blk / KB;
+  const int64_t kb = blk - t * KB;
+  const int64_t r = 16 * t + (L & 15);
+  if (r >= rows) return;
+  const int64_t c0 = kb * 64 + 16 * (L >> 4) + 4 * i;
+  const uint32_t word = wt[d];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t c = c0 + e;
+    if (c < cols) q[r * cols + c] = static_cast<int8_t>(static_cast<int>((word >> (8 * e)) & 0xffu) - 128);
+  }
+}
+
 }  // namespace sqx
 
 using namespace sqx;
@@ -487,6 +508,18 @@ extern "C" int sqx_int8_tile(const int8_t* q, int64_t rows, int64_t cols, uint8_
   hipLaunchKernelGGL(int8_tile_kernel, grid_for(nd), dim3(256), 0, as_stream(stream), q, rows, cols, KB, nd,
                      reinterpret_cast<uint32_t*>(wt));
   SQX_LAUNCH_CHECK("sqx_int8_tile");
+  return SQX_OK;
+}
+
+extern "C" int sqx_int8_untile(const uint8_t* wt, int64_t rows, int64_t cols, int8_t* q, sqx_stream_t stream) {
+  SQX_REQUIRE(rows > 0 && cols > 0 && rows <= ((int64_t)1 << 30) && cols <= ((int64_t)1 << 30), SQX_E_ARG,
+              "sqx_int8_untile: bad shape");
+  SQX_REQUIRE(q && wt, SQX_E_ARG, "sqx_int8_untile: null pointer");
+  const int64_t KB = ceil_div(cols, 64);
+  const int64_t nd = ceil_div(rows, 16) * KB * 256;
+  hipLaunchKernelGGL(int8_untile_kernel, grid_for(nd), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const uint32_t*>(wt), rows, cols, KB, nd, q);
+  SQX_LAUNCH_CHECK("sqx_int8_untile");
   return SQX_OK;
 }
 

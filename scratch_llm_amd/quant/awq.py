@@ -26,6 +26,7 @@ from scratch_llm_amd.quant import _device
 from scratch_llm_amd.quant.int4_group import (  # noqa: F401  (module attributes, as in the reference)
     GROUP_SIZE,
     TILED_GROUPS,
+    Int4Tiled,
     dequantize_groupwise_int4,
     int4_linear_tiled,
     int4_linear_tiled_f32,
@@ -188,10 +189,18 @@ def awq_linear(x: Tensor, quant: AWQQuant, bias: Tensor | None = None) -> Tensor
     g = quant.group_size
     if g not in TILED_GROUPS:
         raise ValueError(f"awq_linear: group_size={g} is not supported by the MI355X kernels {TILED_GROUPS}")
+    tw = _tiled_cache.get((quant.q, quant.group_scales), (g,), lambda: tile_int4(quant.q, quant.group_scales, None, g))
+    return awq_linear_tiled(x, tw, quant.chan_scale, bias)
+
+
+def awq_linear_tiled(x: Tensor, tw: Int4Tiled, chan_scale: Tensor, bias: Tensor | None = None) -> Tensor:
+    """:func:`awq_linear` on a tiled weight (the codes and group scales of ``W * s`` re-laid by
+    ``tile_int4``) and its per-input-channel scale ``s``."""
+    _lib.require_device(x, tw.wt, chan_scale, bias, fn="awq_linear")
     if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
         raise TypeError(f"awq_linear takes fp32, bf16 or fp16 activations, got {x.dtype}")
-    tw = _tiled_cache.get((quant.q, quant.group_scales), (g,), lambda: tile_int4(quant.q, quant.group_scales, None, g))
-    s = quant.chan_scale.to(torch.float32).contiguous()
+    g = tw.group_size
+    s = chan_scale.to(torch.float32).contiguous()
     if x.dtype == torch.float32:
         return int4_linear_tiled_f32(x, tw, bias, col_scale=s)
     *batch, k = x.shape

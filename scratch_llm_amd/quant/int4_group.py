@@ -253,6 +253,23 @@ def tile_int4_packed(packed: Tensor, scales: Tensor, shape: tuple[int, int], gro
     return Int4Tiled(wt, st, None, rows, cols, group_size)
 
 
+def untile_int4(tw: Int4Tiled) -> tuple[Tensor, Tensor, Tensor | None]:
+    """The reference's tensors back from a tiled weight (``sqx_int4_untile``, the exact inverse of the
+    tilers): int8 codes ``[out, in]`` (signed ``[-8, 7]`` for symmetric weights, unsigned ``[0, 15]``
+    when ``tw.zt`` is set), and the group scales (and zeros) ``[out, in/group]`` in the parameter dtype."""
+    dev = _lib.require_device(tw.wt, tw.st, tw.zt, fn="untile_int4")
+    lib = _lib.load()
+    g = tw.cols // tw.group_size
+    codes = torch.empty(tw.rows, tw.cols, dtype=torch.int8, device=dev)
+    scales = torch.empty(tw.rows, g, dtype=tw.st.dtype, device=dev)
+    zeros = None if tw.zt is None else torch.empty(tw.rows, g, dtype=tw.zt.dtype, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(lib.sqx_int4_untile(tw.wt.data_ptr(), tw.st.data_ptr(), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype),
+                                       0 if tw.zt is None else 1, tw.rows, tw.cols, tw.group_size, codes.data_ptr(),
+                                       scales.data_ptr(), _lib.ptr(zeros), _lib.stream_ptr(dev)), "untile_int4")
+    return codes, scales, zeros
+
+
 # Activation rows from which the tiled linears switch from the decode-regime kernels (the streaming
 # GEMV at one row; for 2..64 rows the library's choice among the GEMV and the row-tiled kernels, with
 # K split into a workspace) to the prefill GEMM.

@@ -256,6 +256,17 @@ def tile_int8(q: Tensor, s: Tensor) -> Int8Tiled:
     return Int8Tiled(wt, sc, rows, cols)
 
 
+def untile_int8(tw: Int8Tiled) -> Tensor:
+    """The int8 codes ``[out, in]`` back from a tiled weight (``sqx_int8_untile``, the exact inverse of
+    :func:`tile_int8`)."""
+    dev = _lib.require_device(tw.wt, fn="untile_int8")
+    q = torch.empty(tw.rows, tw.cols, dtype=torch.int8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().sqx_int8_untile(tw.wt.data_ptr(), tw.rows, tw.cols, q.data_ptr(), _lib.stream_ptr(dev)),
+                   "untile_int8")
+    return q
+
+
 def int8_linear_tiled(x: Tensor, tw: Int8Tiled, bias: Tensor | None = None, k_slices: int | None = None) -> Tensor:
     """``x @ (q * s).T (+ bias)`` for a tiled int8 weight; ``x`` bf16 / fp16 ``[..., in]``."""
     *batch, k = x.shape

@@ -18,7 +18,7 @@ import torch
 from torch import Tensor, nn
 
 from scratch_llm_amd import _lib
-from scratch_llm_amd.quant import _device, awq, int4_group, int8, nvfp4_mxfp4
+from scratch_llm_amd.quant import awq, int4_group, int8, nvfp4_mxfp4
 
 __all__ = [
     "DEFAULT_SKIP",
@@ -38,9 +38,6 @@ __all__ = [
 #: Layers left unquantized by default (fp8_weights.py:361-364): the LM head, whose error lands on
 #: the sampled token, and embeddings, which are a gather.
 DEFAULT_SKIP = ("lm_head", "embed", "wte", "output")
-
-_tiles = _device.TensorKeyedCache()
-
 
 def is_linear(m: nn.Module) -> bool:
     """``nn.Linear``, or a bias-free linear shaped like the reference's ``model.Linear``: a leaf module
@@ -74,13 +71,15 @@ class _QuantLinear(nn.Module):
 
 
 class Int4Linear(_QuantLinear):
-    """W4A16 with the reference's group-INT4 weight (int4_group.py:108-164): ``weight_packed`` the
-    ``pack_int4`` bytes of the row-major codes (two codes per byte), ``scales`` fp32 ``[out, in/g]``.
-    ``forward`` is ``w4a16_linear`` on the tiled copy: the streaming decode kernel up to 63 rows, the
-    prefill GEMM from 64 rows."""
+    """W4A16 with the reference's group-INT4 weight (int4_group.py:108-164). The module's state is the
+    kernels' tiled copy only (buffers ``wt``, ``st``): the constructor takes the reference's tensors
+    (``weight_packed``, the ``pack_int4`` bytes of the row-major codes, and fp32 ``scales``
+    ``[out, in/g]``) and re-lays them once; ``weight_packed``, ``scales`` and ``codes()`` give them back
+    bit for bit (``untile_int4``). ``forward`` is ``w4a16_linear`` on the tiles: the streaming decode
+    kernel up to 64 rows, the prefill GEMM beyond."""
 
-    weight_packed: Tensor
-    scales: Tensor
+    wt: Tensor
+    st: Tensor
     bias: Tensor | None
 
     def __init__(self, weight_packed: Tensor, scales: Tensor, bias: Tensor | None, in_features: int,
@@ -89,8 +88,9 @@ class Int4Linear(_QuantLinear):
         int4_group._check_tiled_group(group_size)
         if in_features % group_size:
             raise ValueError(f"in_features={in_features} not divisible by group_size={group_size}")
-        self.register_buffer("weight_packed", weight_packed)
-        self.register_buffer("scales", scales)
+        tw = int4_group.tile_int4_packed(weight_packed, scales, (out_features, in_features), group_size)
+        self.register_buffer("wt", tw.wt)
+        self.register_buffer("st", tw.st)
         self.register_buffer("bias", bias)
         self.in_features, self.out_features, self.group_size = in_features, out_features, group_size
 
@@ -101,37 +101,46 @@ class Int4Linear(_QuantLinear):
         return cls(int4_group.pack_int4(q.reshape(-1)), s, None if b is None else b.clone(), w.shape[1], w.shape[0],
                    group_size)
 
+    def tiled(self) -> int4_group.Int4Tiled:
+        return int4_group.Int4Tiled(self.wt, self.st, None, self.out_features, self.in_features, self.group_size)
+
     def codes(self) -> Tensor:
-        return int4_group.unpack_int4(self.weight_packed, self.out_features * self.in_features).reshape(
-            self.out_features, self.in_features)
+        return int4_group.untile_int4(self.tiled())[0]
+
+    @property
+    def scales(self) -> Tensor:
+        return int4_group.untile_int4(self.tiled())[1]
+
+    @property
+    def weight_packed(self) -> Tensor:
+        return int4_group.pack_int4(self.codes().reshape(-1))
 
     def dequantized_weight(self) -> Tensor:
         """``(out, in)`` fp32 ``q * s`` (int4_group.py:132-142)."""
-        return int4_group.dequantize_groupwise_int4(self.codes(), self.scales, self.group_size)
-
-    def tiled(self) -> int4_group.Int4Tiled:
-        return _tiles.get((self.weight_packed, self.scales), ("int4", self.group_size),
-                          lambda: int4_group.tile_int4_packed(self.weight_packed, self.scales,
-                                                              (self.out_features, self.in_features), self.group_size))
+        q, s, _ = int4_group.untile_int4(self.tiled())
+        return int4_group.dequantize_groupwise_int4(q, s, self.group_size)
 
     def forward(self, x: Tensor) -> Tensor:
-        _device_input(x, self.weight_packed, self.bias, fn="Int4Linear")
+        _device_input(x, self.wt, self.bias, fn="Int4Linear")
         return int4_group.int4_linear_tiled(x, self.tiled(), self.bias)
 
 
 class AWQLinear(_QuantLinear):
-    """W4A16 with an AWQ weight (awq.py:69-192): the group-INT4 codes ``q`` of ``W * s``, their
-    ``group_scales`` and the per-input-channel ``chan_scale``; ``forward`` is ``awq_linear``."""
+    """W4A16 with an AWQ weight (awq.py:69-192): the group-INT4 codes of ``W * s`` and their group
+    scales held as the kernels' tiled copy (buffers ``wt``, ``st``), and the per-input-channel
+    ``chan_scale``; ``q``, ``group_scales`` and ``quant()`` give the reference's tensors back bit for bit.
+    ``forward`` is ``awq_linear``."""
 
-    q: Tensor
-    group_scales: Tensor
+    wt: Tensor
+    st: Tensor
     chan_scale: Tensor
     bias: Tensor | None
 
     def __init__(self, quant: awq.AWQQuant, bias: Tensor | None = None) -> None:
         super().__init__()
-        self.register_buffer("q", quant.q)
-        self.register_buffer("group_scales", quant.group_scales)
+        tw = int4_group.tile_int4(quant.q, quant.group_scales, None, quant.group_size)
+        self.register_buffer("wt", tw.wt)
+        self.register_buffer("st", tw.st)
         self.register_buffer("chan_scale", quant.chan_scale)
         self.register_buffer("bias", bias)
         self.group_size = quant.group_size
@@ -144,34 +153,46 @@ class AWQLinear(_QuantLinear):
         quant = awq.quantize_awq_int4(w, x=x, chan_scale=chan_scale, group_size=group_size, grid=grid)
         return cls(quant, None if b is None else b.clone())
 
+    def tiled(self) -> int4_group.Int4Tiled:
+        return int4_group.Int4Tiled(self.wt, self.st, None, self.out_features, self.in_features, self.group_size)
+
+    @property
+    def q(self) -> Tensor:
+        return int4_group.untile_int4(self.tiled())[0]
+
+    @property
+    def group_scales(self) -> Tensor:
+        return int4_group.untile_int4(self.tiled())[1]
+
     def quant(self) -> awq.AWQQuant:
-        return awq.AWQQuant(q=self.q, group_scales=self.group_scales, chan_scale=self.chan_scale,
-                            group_size=self.group_size)
+        q, gs, _ = int4_group.untile_int4(self.tiled())
+        return awq.AWQQuant(q=q, group_scales=gs, chan_scale=self.chan_scale, group_size=self.group_size)
 
     def dequantized_weight(self) -> Tensor:
         return awq.awq_dequantize(self.quant())
 
     def forward(self, x: Tensor) -> Tensor:
-        _device_input(x, self.q, self.bias, fn="AWQLinear")
-        return awq.awq_linear(x, self.quant(), self.bias)
+        _device_input(x, self.wt, self.bias, fn="AWQLinear")
+        return awq.awq_linear_tiled(x, self.tiled(), self.chan_scale, self.bias)
 
 
 class Int8Linear(_QuantLinear):
-    """Weight-only int8: per-output-channel symmetric codes ``q`` int8
-    ``[out, in]`` and fp32 ``scale [out, 1]`` of ``quantize_symmetric(W.float(), axis=0)``
-    (int8.py:102-125); ``forward`` is ``F.linear(x, (q * s).to(x.dtype), bias)`` without materialising
-    the weight."""
+    """Weight-only int8: per-output-channel symmetric codes of
+    ``quantize_symmetric(W.float(), axis=0)`` (int8.py:102-125) held as the kernels' tiled copy (buffer
+    ``wt``) with the fp32 ``scale [out, 1]``; ``q`` gives the codes back bit for bit. ``forward`` is
+    ``F.linear(x, (q * s).to(x.dtype), bias)`` without materialising the weight."""
 
-    q: Tensor
+    wt: Tensor
     scale: Tensor
     bias: Tensor | None
 
     def __init__(self, q: Tensor, scale: Tensor, bias: Tensor | None = None) -> None:
         super().__init__()
-        self.register_buffer("q", q)
-        self.register_buffer("scale", scale)
-        self.register_buffer("bias", bias)
         self.out_features, self.in_features = q.shape
+        tw = int8.tile_int8(q, scale)
+        self.register_buffer("wt", tw.wt)
+        self.register_buffer("scale", tw.scale.reshape(-1, 1))
+        self.register_buffer("bias", bias)
 
     @classmethod
     def from_linear(cls, linear: nn.Module) -> Int8Linear:
@@ -179,31 +200,40 @@ class Int8Linear(_QuantLinear):
         q, s = int8.quantize_symmetric(w.float(), axis=0)
         return cls(q, s, None if b is None else b.clone())
 
+    def tiled(self) -> int8.Int8Tiled:
+        return int8.Int8Tiled(self.wt, self.scale.reshape(-1), self.out_features, self.in_features)
+
+    @property
+    def q(self) -> Tensor:
+        return int8.untile_int8(self.tiled())
+
     def dequantized_weight(self) -> Tensor:
         return int8.dequantize_symmetric(self.q, self.scale)
 
     def forward(self, x: Tensor) -> Tensor:
-        _device_input(x, self.q, self.bias, fn="Int8Linear")
-        return int8.int8_weight_linear(x, self.q, self.scale, self.bias)
+        _device_input(x, self.wt, self.bias, fn="Int8Linear")
+        return int8.int8_linear_tiled(x, self.tiled(), self.bias)
 
 
 class MXFP4Linear(_QuantLinear):
-    """MXFP4 weight in the on-disk compressed-tensors form (k3/checkpoint.py:92-144):
-    ``weight_packed`` uint8 ``[out, in/2]`` and E8M0 ``weight_scale`` uint8 ``[out, in/32]``, tiled for
-    the kernels with no host repack. ``forward`` is ``F.linear(x, mxfp4_dequantize(W).to(x.dtype))``
-    (BASELINE config 4); with ``quantize_activations`` the rows of ``x`` are MXFP4-quantized too and
-    the product runs on the block-scaled fp4 MFMA."""
+    """MXFP4 weight in the on-disk compressed-tensors form (k3/checkpoint.py:92-144): the constructor
+    takes ``weight_packed`` uint8 ``[out, in/2]`` and E8M0 ``weight_scale`` uint8 ``[out, in/32]`` and
+    holds only their tiled copy (buffers ``wt``, ``st``: a byte permutation, no repack on the host);
+    ``weight_packed`` / ``weight_scale`` give the pair back bit for bit. ``forward`` is
+    ``F.linear(x, mxfp4_dequantize(W).to(x.dtype))``; with ``quantize_activations``
+    the rows of ``x`` are MXFP4-quantized too and the product runs on the block-scaled fp4 MFMA."""
 
-    weight_packed: Tensor
-    weight_scale: Tensor
+    wt: Tensor
+    st: Tensor
     bias: Tensor | None
 
     def __init__(self, weight_packed: Tensor, weight_scale: Tensor, bias: Tensor | None = None, *,
                  quantize_activations: bool = False) -> None:
         super().__init__()
         rows, cols = nvfp4_mxfp4._check_mxfp4_pair(weight_packed, weight_scale)
-        self.register_buffer("weight_packed", weight_packed)
-        self.register_buffer("weight_scale", weight_scale)
+        tw = nvfp4_mxfp4.tile_mxfp4_packed(weight_packed, weight_scale)
+        self.register_buffer("wt", tw.wt)
+        self.register_buffer("st", tw.st)
         self.register_buffer("bias", bias)
         self.out_features, self.in_features = rows, cols
         self.quantize_activations = quantize_activations
@@ -221,15 +251,22 @@ class MXFP4Linear(_QuantLinear):
         reference loader refuses: non-uint8 halves, bad shapes, the NaN scale 0xFF)."""
         return cls(weight_packed, weight_scale, bias, quantize_activations=quantize_activations)
 
-    def dequantized_weight(self) -> Tensor:
-        return nvfp4_mxfp4.dequantize_mxfp4(self.weight_packed, self.weight_scale)
-
     def tiled(self) -> nvfp4_mxfp4.FP4Tiled:
-        return _tiles.get((self.weight_packed, self.weight_scale), ("mxfp4",),
-                          lambda: nvfp4_mxfp4.tile_mxfp4_packed(self.weight_packed, self.weight_scale))
+        return nvfp4_mxfp4.FP4Tiled(self.wt, self.st, _lib.FP4_MX, None, self.out_features, self.in_features)
+
+    @property
+    def weight_packed(self) -> Tensor:
+        return nvfp4_mxfp4.untile_fp4(self.tiled())[0]
+
+    @property
+    def weight_scale(self) -> Tensor:
+        return nvfp4_mxfp4.untile_fp4(self.tiled())[1]
+
+    def dequantized_weight(self) -> Tensor:
+        return nvfp4_mxfp4.dequantize_mxfp4(*nvfp4_mxfp4.untile_fp4(self.tiled()))
 
     def forward(self, x: Tensor) -> Tensor:
-        _device_input(x, self.weight_packed, self.bias, fn="MXFP4Linear")
+        _device_input(x, self.wt, self.bias, fn="MXFP4Linear")
         tw = self.tiled()
         if not self.quantize_activations:
             return nvfp4_mxfp4.fp4_linear_tiled(x, tw, self.bias)
@@ -239,11 +276,13 @@ class MXFP4Linear(_QuantLinear):
 
 
 class NVFP4Linear(_QuantLinear):
-    """NVFP4 weight (nvfp4_mxfp4.py:190-231): unpacked E2M1 ``codes`` ``(n_blocks, 16)``, E4M3
-    ``s_block`` and fp32 ``s_global``; ``forward`` is ``F.linear(x, nvfp4_dequantize(W).to(x.dtype))``."""
+    """NVFP4 weight (nvfp4_mxfp4.py:190-231), held as the kernels' tiled copy (buffers ``wt``, ``st``:
+    the E2M1 codes and the E4M3 bytes of the block scales) with the fp32 ``s_global``; ``tensor()``
+    gives the reference's ``NVFP4Tensor`` back bit for bit. ``forward`` is
+    ``F.linear(x, nvfp4_dequantize(W).to(x.dtype))``."""
 
-    codes: Tensor
-    s_block: Tensor
+    wt: Tensor
+    st: Tensor
     s_global: Tensor
     bias: Tensor | None
 
@@ -251,9 +290,10 @@ class NVFP4Linear(_QuantLinear):
         super().__init__()
         if len(q.shape) != 2:
             raise ValueError(f"a linear needs a 2-D weight, got shape {tuple(q.shape)}")
-        self.register_buffer("codes", q.codes)
-        self.register_buffer("s_block", q.s_block)
-        self.register_buffer("s_global", q.s_global)
+        tw = nvfp4_mxfp4.tile_fp4(q)
+        self.register_buffer("wt", tw.wt)
+        self.register_buffer("st", tw.st)
+        self.register_buffer("s_global", tw.s_global)
         self.register_buffer("bias", bias)
         self.block = q.block
         self.out_features, self.in_features = int(q.shape[0]), int(q.shape[1])
@@ -263,17 +303,24 @@ class NVFP4Linear(_QuantLinear):
         w, b = _weight_bias(linear)
         return cls(nvfp4_mxfp4.nvfp4_quantize(w, block), None if b is None else b.clone())
 
+    def tiled(self) -> nvfp4_mxfp4.FP4Tiled:
+        return nvfp4_mxfp4.FP4Tiled(self.wt, self.st, _lib.FP4_NV, self.s_global, self.out_features, self.in_features)
+
     def tensor(self) -> nvfp4_mxfp4.NVFP4Tensor:
-        return nvfp4_mxfp4.NVFP4Tensor(self.codes, self.s_global, self.s_block,
-                                       torch.Size((self.out_features, self.in_features)),
-                                       self.out_features * self.in_features, self.block)
+        packed, e4 = nvfp4_mxfp4.untile_fp4(self.tiled())
+        n = self.out_features * self.in_features
+        codes = nvfp4_mxfp4.unpack_fp4(packed.reshape(-1), n).reshape(-1, self.block)
+        # one E4M3 byte per 16 columns; a block of `block` columns repeats its scale
+        s_block = nvfp4_mxfp4.e4m3_values(e4[:, :: self.block // 16].reshape(-1))
+        return nvfp4_mxfp4.NVFP4Tensor(codes, self.s_global, s_block,
+                                       torch.Size((self.out_features, self.in_features)), n, self.block)
 
     def dequantized_weight(self) -> Tensor:
         return nvfp4_mxfp4.nvfp4_dequantize(self.tensor())
 
     def forward(self, x: Tensor) -> Tensor:
-        _device_input(x, self.codes, self.bias, fn="NVFP4Linear")
-        return nvfp4_mxfp4.nvfp4_linear(x, self.tensor(), self.bias)
+        _device_input(x, self.wt, self.bias, fn="NVFP4Linear")
+        return nvfp4_mxfp4.fp4_linear_tiled(x, self.tiled(), self.bias)
 
 
 # --------------------------------------------------------------------------------------------------

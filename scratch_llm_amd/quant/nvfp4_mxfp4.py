@@ -297,6 +297,34 @@ def tile_fp4(q: MXFP4Tensor | NVFP4Tensor) -> FP4Tiled:
     return FP4Tiled(wt, st, fmt, s_global, rows, cols)
 
 
+def untile_fp4(tw: FP4Tiled) -> tuple[Tensor, Tensor]:
+    """A tiled FP4 weight back in the reference's byte form (``sqx_fp4_untile``, the exact inverse of
+    the tilers): ``packed`` uint8 ``[out, in/2]`` in ``pack_fp4`` order (for MXFP4 the on-disk
+    ``weight_packed``) and the scale bytes, E8M0 ``[out, in/32]`` (MXFP4, the on-disk ``weight_scale``)
+    or E4M3 ``[out, in/16]`` (NVFP4, one per 16 columns)."""
+    dev = _lib.require_device(tw.wt, tw.st, fn="untile_fp4")
+    bs = 16 if tw.fmt == _lib.FP4_NV else 32
+    packed = torch.empty(tw.rows, tw.cols // 2, dtype=torch.uint8, device=dev)
+    scales = torch.empty(tw.rows, tw.cols // bs, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().sqx_fp4_untile(tw.wt.data_ptr(), tw.st.data_ptr(), tw.fmt, tw.rows, tw.cols,
+                                              packed.data_ptr(), scales.data_ptr(), _lib.stream_ptr(dev)), "untile_fp4")
+    return packed, scales
+
+
+def e4m3_values(codes: Tensor) -> Tensor:
+    """fp32 values of E4M3 bytes (every one exact in fp32), through the FP8 row decoder at scale 1."""
+    dev = _lib.require_device(codes, fn="e4m3_values")
+    c = codes.to(torch.uint8).reshape(1, -1).contiguous()
+    one = torch.ones(1, dtype=torch.float32, device=dev)
+    out = torch.empty(c.shape[1], dtype=torch.float32, device=dev)
+    if c.shape[1]:
+        with torch.cuda.device(dev):
+            _lib.check(_lib.load().sqx_fp8_dequantize_rows(c.data_ptr(), one.data_ptr(), 1, c.shape[1], out.data_ptr(),
+                                                           _lib.stream_ptr(dev)), "e4m3_values")
+    return out.reshape(codes.shape)
+
+
 def fp4_linear_tiled(x: Tensor, tw: FP4Tiled, bias: Tensor | None = None, out_dtype: torch.dtype | None = None,
                      k_slices: int | None = None) -> Tensor:
     """``x @ W.T (+ bias)`` for a tiled FP4 weight. ``x`` is ``[..., cols]``: bf16 / fp16 run as they

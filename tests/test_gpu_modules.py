@@ -168,3 +168,84 @@ def test_modules_refuse_cpu_input(mods):
     mods.convert_linears_to_int8(model)
     with pytest.raises(RuntimeError):
         model.blocks[0].up(torch.randn(2, 256))
+
+
+@pytest.mark.parametrize("rows,cols,group,kind,pdt", [(100, 384, 128, 0, torch.float32), (33, 96, 32, 1, torch.bfloat16),
+                                                      (16, 4096, 64, 1, torch.float32), (257, 1056, 32, 0, torch.float32)])
+def test_untile_int4_round_trip(mods, rows, cols, group, kind, pdt):
+    """untile_int4(tile_int4(q, s[, z])) gives q, s (and z) back bit for bit, ragged rows and columns
+    (padding rows and columns of the tiles are skipped)."""
+    from scratch_llm_amd.quant import int4_group as i4
+
+    print_case("untile int4", rows, cols, group, kind, pdt)
+    g = torch.Generator().manual_seed(rows * cols)
+    lo, hi = (-8, 8) if kind == 0 else (0, 16)
+    q = torch.randint(lo, hi, (rows, cols), generator=g, dtype=torch.int8).to(DEV)
+    s = torch.rand(rows, cols // group, generator=g).to(pdt).to(DEV)
+    z = None if kind == 0 else torch.randint(0, 16, (rows, cols // group), generator=g).to(pdt).to(DEV)
+    tw = i4.tile_int4(q, s, z, group)
+    q2, s2, z2 = i4.untile_int4(tw)
+    assert torch.equal(q2, q) and torch.equal(s2, s)
+    assert (z2 is None) if z is None else torch.equal(z2, z)
+
+
+@pytest.mark.parametrize("rows,cols", [(100, 200), (16, 64), (1000, 4096)])
+def test_untile_int8_round_trip(mods, rows, cols):
+    from scratch_llm_amd.quant import int8 as q8
+
+    print_case("untile int8", rows, cols)
+    q = torch.randint(-128, 128, (rows, cols), generator=torch.Generator().manual_seed(cols), dtype=torch.int8).to(DEV)
+    tw = q8.tile_int8(q, torch.ones(rows, device=DEV))
+    assert torch.equal(q8.untile_int8(tw), q)
+
+
+@pytest.mark.parametrize("rows,cols,nv", [(100, 96, False), (33, 4096, False), (64, 160, True), (5, 8192, True)])
+def test_untile_fp4_round_trip(mods, rows, cols, nv):
+    """untile_fp4 of a tiled pair gives the reference's packed bytes and scale bytes back, bit for bit."""
+    from scratch_llm_amd import _lib
+    from scratch_llm_amd.quant import nvfp4_mxfp4 as f4
+
+    print_case("untile fp4", rows, cols, nv)
+    g = torch.Generator().manual_seed(rows + cols)
+    packed = torch.randint(0, 256, (rows, cols // 2), generator=g, dtype=torch.uint8).to(DEV)
+    bs = 16 if nv else 32
+    if nv:
+        vals = f4.e4m3_values(torch.randint(0, 0x7F, (rows, cols // bs), generator=g, dtype=torch.uint8).to(DEV))
+        lib = _lib.load()
+        wt = torch.empty(lib.sqx_fp4_tiled_weight_bytes(rows, cols), dtype=torch.uint8, device=DEV)
+        st = torch.empty(lib.sqx_fp4_tiled_scale_bytes(rows, cols, _lib.FP4_NV), dtype=torch.uint8, device=DEV)
+        _lib.check(lib.sqx_fp4_tile(packed.data_ptr(), 1, vals.data_ptr(), _lib.FP4_SCALE_NV_F32, bs, rows, cols,
+                                    wt.data_ptr(), st.data_ptr(), _lib.stream_ptr(packed.device)), "tile")
+        tw = f4.FP4Tiled(wt, st, _lib.FP4_NV, torch.ones((), device=DEV), rows, cols)
+        p2, s2 = f4.untile_fp4(tw)
+        assert torch.equal(p2, packed) and torch.equal(f4.e4m3_values(s2), vals)
+    else:
+        e8 = torch.randint(100, 150, (rows, cols // bs), generator=g, dtype=torch.uint8).to(DEV)
+        p2, s2 = f4.untile_fp4(f4.tile_mxfp4_packed(packed, e8))
+        assert torch.equal(p2, packed) and torch.equal(s2, e8)
+
+
+def test_modules_hold_only_the_tiled_copy(mods):
+    """Every module's buffers are the tiled weight (plus its per-row / global scales, the AWQ channel
+    scale and the bias): no full-size copy in the reference's format stays beside it, and the
+    reference's tensors come back exactly from the tiles."""
+    from scratch_llm_amd.quant import int4_group as i4
+
+    lin = nn.Linear(1024, 512).to(DEV)
+    for name, make in [("int4", mods.Int4Linear.from_linear), ("int8", mods.Int8Linear.from_linear),
+                       ("mxfp4", mods.MXFP4Linear.from_linear), ("nvfp4", mods.NVFP4Linear.from_linear)]:
+        mod = make(lin)
+        names = {n for n, _ in mod.named_buffers()}
+        assert "wt" in names and not names & {"weight_packed", "q", "codes", "weight_scale"}, (name, names)
+        weight_bytes = sum(b.numel() * b.element_size() for n, b in mod.named_buffers() if n not in ("bias",))
+        per_weight = weight_bytes / (1024 * 512)
+        assert per_weight <= {"int4": 0.54, "int8": 1.01, "mxfp4": 0.54, "nvfp4": 0.57}[name], (name, per_weight)
+    mod = mods.Int4Linear.from_linear(lin)
+    q, s = i4.quantize_groupwise_int4(lin.weight.data)
+    assert torch.equal(mod.codes(), q) and torch.equal(mod.scales, s)
+    assert torch.equal(mod.weight_packed, i4.pack_int4(q.reshape(-1)))
+    awq_mod = mods.AWQLinear.from_linear(lin, chan_scale=torch.linspace(0.5, 2.0, 1024, device=DEV))
+    names = {n for n, _ in awq_mod.named_buffers()}
+    assert names == {"wt", "st", "chan_scale", "bias"}
+    qa = awq_mod.quant()
+    assert qa.q.dtype == torch.int8 and tuple(qa.q.shape) == (512, 1024)
