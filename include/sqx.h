@@ -87,7 +87,11 @@ int64_t sqx_int4_tiled_param_count(int64_t rows, int64_t cols, int64_t group);
  * format), 1 = unsigned asymmetric codes in [0, 15]. scales (and zeros when code_kind == 1): [rows,
  * cols/group] of param_dtype (F32 or BF16). group must be 32, 64 or 128, and cols % group == 0.
  * Outputs: wt (sqx_int4_tiled_weight_bytes bytes), st (and zt when code_kind == 1):
- * sqx_int4_tiled_param_count elements of param_dtype. Padding rows/columns hold a zero weight. */
+ * sqx_int4_tiled_param_count elements of param_dtype. Asymmetric codes with BF16 parameters instead
+ * keep each (scale, zero) pair in one dword of st (scale bits | zero bits << 16: 2 x
+ * sqx_int4_tiled_param_count BF16 elements), so the kernels fetch both with one load; zt is then
+ * neither written nor read, but must be non-NULL wherever it marks the codes asymmetric (pass st).
+ * Padding rows/columns hold a zero weight. */
 int sqx_int4_tile(const int8_t* codes, int code_kind, const void* scales, const void* zeros,
                   int param_dtype, int64_t rows, int64_t cols, int64_t group, uint8_t* wt,
                   void* st, void* zt, sqx_stream_t stream);

@@ -343,11 +343,14 @@ template <int FMT, bool ASYM, bool PBF16, int GROUP>
 struct DqW {
   // parameter bytes per stage and tile: INT4 scales (and zero-points) of the stage's groups;
   // MXFP4 32 E8M0 bytes (lanes 32h..32h+31 of the 64-byte block), NVFP4 64 E4M3 bytes
-  static constexpr int PB = PBF16 ? 2 : 4;
+  // asymmetric bf16 INT4 parameters are (scale, zero) pairs in one dword (sqx_int4_tile)
+  static constexpr bool PAIR = ASYM && PBF16;
+  static constexpr bool ZSEP = ASYM && !PBF16;  // zero-points in a buffer of their own
+  static constexpr int PB = (PBF16 && !PAIR) ? 2 : 4;
   static constexpr int kWInstr = FMT == kDqInt4 ? 4 : 1;  // weight copies per wave per stage
   static constexpr int kPInstr = 2;                        // parameter copies per wave per stage
   static constexpr int NGS = GROUP >= 64 ? 1 : 64 / GROUP;  // INT4 groups per stage
-  static constexpr int NP = FMT == kDqMx ? 2 : FMT == kDqNv ? 4 : (ASYM ? 2 : 1) * NGS * 16 * 16 * PB / 256;
+  static constexpr int NP = FMT == kDqMx ? 2 : FMT == kDqNv ? 4 : (ZSEP ? 2 : 1) * NGS * 16 * 16 * PB / 256;
   static_assert(NP <= 16, "parameter copies fit two per wave");
 };
 
@@ -431,8 +434,8 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
       if (FMT == kDqInt4) {
         // layout in LDS: [scales | zeros][group gi][tile f][row] of PB bytes; 256 bytes per copy
         constexpr int TPI = 256 / (16 * P::PB);  // tiles per copy
-        const int per_kind = np / (ASYM ? 2 : 1);
-        zsrc = ASYM && pr >= per_kind;
+        const int per_kind = np / (P::ZSEP ? 2 : 1);
+        zsrc = P::ZSEP && pr >= per_kind;
         const int q = pr - (zsrc ? per_kind : 0);
         const int gi = q / (16 / TPI);
         const int f = TPI * (q % (16 / TPI)) + lane / (64 / TPI);
@@ -487,9 +490,10 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const uint16_t* __restrict
         const int gi = GROUP >= 64 ? 0 : (32 * q) / GROUP;
         constexpr int zoff = P::NGS * 16 * 16 * P::PB;
         const int po = ((gi * 16 + f) * 16 + nl) * P::PB;
-        if (PBF16) {
-          const uint32_t sb = *reinterpret_cast<const uint16_t*>(pb + po);
-          o.p0[nt] = ASYM ? (sb | ((uint32_t)*reinterpret_cast<const uint16_t*>(pb + zoff + po) << 16)) : sb;
+        if (P::PAIR) {
+          o.p0[nt] = *reinterpret_cast<const uint32_t*>(pb + po);  // bf16 scale | bf16 zero << 16
+        } else if (PBF16) {
+          o.p0[nt] = *reinterpret_cast<const uint16_t*>(pb + po);
         } else {
           o.p0[nt] = *reinterpret_cast<const uint32_t*>(pb + po);
           if (ASYM) o.p1[nt % kP1] = *reinterpret_cast<const uint32_t*>(pb + zoff + po);

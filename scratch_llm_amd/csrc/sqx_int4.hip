@@ -323,6 +323,42 @@ __global__ __launch_bounds__(256) void int4_tile_params_kernel(const P* __restri
   dst[o] = (r < rows && g < n_groups) ? src[r * n_groups + g] : P(0);
 }
 
+// Asymmetric codes with bf16 parameters: the scale and zero of a (row, group) interleaved into one
+// dword (scale bits | zero bits << 16), so the kernels fetch both with one load.
+__global__ __launch_bounds__(256) void int4_tile_param_pairs_kernel(const uint16_t* __restrict__ sc,
+                                                                    const uint16_t* __restrict__ zr, int64_t rows,
+                                                                    int64_t n_groups, int64_t Gp, int64_t n_out,
+                                                                    uint32_t* __restrict__ dst) {
+  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= n_out) return;
+  const int64_t nl = o & 15;
+  const int64_t tg = o >> 4;
+  const int64_t t = tg / Gp;
+  const int64_t g = tg - t * Gp;
+  const int64_t r = 16 * t + nl;
+  dst[o] = (r < rows && g < n_groups) ? (static_cast<uint32_t>(sc[r * n_groups + g]) |
+                                         (static_cast<uint32_t>(zr[r * n_groups + g]) << 16))
+                                      : 0u;
+}
+
+__global__ __launch_bounds__(256) void int4_untile_param_pairs_kernel(const uint32_t* __restrict__ src, int64_t rows,
+                                                                      int64_t n_groups, int64_t Gp, int64_t n_in,
+                                                                      uint16_t* __restrict__ sc,
+                                                                      uint16_t* __restrict__ zr) {
+  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= n_in) return;
+  const int64_t nl = o & 15;
+  const int64_t tg = o >> 4;
+  const int64_t t = tg / Gp;
+  const int64_t g = tg - t * Gp;
+  const int64_t r = 16 * t + nl;
+  if (r < rows && g < n_groups) {
+    const uint32_t v = src[o];
+    sc[r * n_groups + g] = static_cast<uint16_t>(v & 0xffffu);
+    zr[r * n_groups + g] = static_cast<uint16_t>(v >> 16);
+  }
+}
+
 // The inverse re-layout (tiles -> the reference's row-major codes and [rows, groups] parameters):
 // one thread per tiled dword writes its 8 codes (u - 8 for SIGNED), one per tiled parameter element
 // writes it back; padding rows and columns are skipped.
@@ -385,7 +421,9 @@ struct WInt4 {
   static constexpr int KBLK = 128, STEPS = 4;
   static constexpr int NG = 128 / GROUP;  // groups per block
   static constexpr int MPG = 4 / NG;      // MFMA steps (of 32 columns) per group
-  static constexpr int PB = PBF16 ? 2 : 4;
+  // asymmetric bf16 parameters come as (scale, zero) pairs in one dword: one load per group
+  static constexpr bool PAIR = ASYM && PBF16;
+  static constexpr int PB = (PBF16 && !PAIR) ? 2 : 4;  // bytes per tiled parameter element
   struct Args {
     const uint8_t* wt;
     const void* st;
@@ -416,8 +454,14 @@ struct WInt4 {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const uint32_t off = (uint32_t)(kb * NG + g) * 16u * PB;
-      p.sc[g] = load_param<PBF16>(c.sr, c.pvo, off);
-      p.zf[g] = ASYM ? load_param<PBF16>(c.zr, c.pvo, off) : 8.0f;
+      if constexpr (PAIR) {
+        const uint32_t v = bload32(c.sr, c.pvo, off);
+        p.sc[g] = bf16_bits_to_f32(static_cast<uint16_t>(v & 0xffffu));
+        p.zf[g] = bf16_bits_to_f32(static_cast<uint16_t>(v >> 16));
+      } else {
+        p.sc[g] = load_param<PBF16>(c.sr, c.pvo, off);
+        p.zf[g] = ASYM ? load_param<PBF16>(c.zr, c.pvo, off) : 8.0f;
+      }
     }
   }
   __device__ static int xk(int i, int jg) { return 32 * i + 8 * jg; }
@@ -814,8 +858,16 @@ extern "C" int sqx_int4_tile(const int8_t* codes, int code_kind, const void* sca
   else
     hipLaunchKernelGGL((int4_tile_weights_kernel<false, false>), grid, dim3(256), 0, s, codes, rows, cols, KB,
                        n_dwords, reinterpret_cast<uint32_t*>(wt));
-  tile_params(scales, param_dtype, rows, cols, group, st, s);
-  if (code_kind == 1) tile_params(zeros, param_dtype, rows, cols, group, zt, s);
+  if (code_kind == 1 && param_dtype == SQX_DTYPE_BF16) {  // (scale, zero) pairs in st; zt unused
+    const int64_t Gp = KB * (128 / group);
+    const int64_t n_out = ceil_div(rows, 16) * Gp * 16;
+    hipLaunchKernelGGL(int4_tile_param_pairs_kernel, dim3(static_cast<unsigned>(ceil_div(n_out, 256))), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(scales), static_cast<const uint16_t*>(zeros), rows, cols / group,
+                       Gp, n_out, static_cast<uint32_t*>(st));
+  } else {
+    tile_params(scales, param_dtype, rows, cols, group, st, s);
+    if (code_kind == 1) tile_params(zeros, param_dtype, rows, cols, group, zt, s);
+  }
   SQX_LAUNCH_CHECK("sqx_int4_tile");
   return SQX_OK;
 }
@@ -856,6 +908,12 @@ extern "C" int sqx_int4_untile(const uint8_t* wt, const void* st, const void* zt
   const int64_t n_groups = cols / group, Gp = KB * (128 / group);
   const int64_t n_in = ceil_div(rows, 16) * Gp * 16;
   const dim3 pgrid(static_cast<unsigned>(ceil_div(n_in, 256)));
+  if (code_kind == 1 && param_dtype == SQX_DTYPE_BF16) {
+    hipLaunchKernelGGL(int4_untile_param_pairs_kernel, pgrid, dim3(256), 0, s, static_cast<const uint32_t*>(st), rows,
+                       n_groups, Gp, n_in, static_cast<uint16_t*>(scales), static_cast<uint16_t*>(zeros));
+    SQX_LAUNCH_CHECK("sqx_int4_untile");
+    return SQX_OK;
+  }
   for (int k = 0; k < (code_kind == 1 ? 2 : 1); ++k) {
     const void* src = k == 0 ? st : zt;
     void* dst = k == 0 ? scales : zeros;

@@ -167,8 +167,9 @@ class Int4Tiled:
     """INT4 codes re-laid for the MI355X linear kernels.
 
     ``wt``: uint8, 1 KiB per (16-row tile, 128-column block); ``st``/``zt``: per-group scale and
-    zero (``zt`` is None for symmetric codes) as ``[tiles][groups][16]``. ``rows``/``cols`` are the
-    logical weight shape ``[out, in]``.
+    zero (``zt`` is None for symmetric codes) as ``[tiles][groups][16]``. Asymmetric codes with bf16
+    parameters keep each (scale, zero) pair in one dword of ``st`` (``zt`` is then ``st`` itself, which
+    marks the codes asymmetric). ``rows``/``cols`` are the logical weight shape ``[out, in]``.
     """
 
     wt: Tensor
@@ -185,7 +186,7 @@ class Int4Tiled:
     @property
     def nbytes(self) -> int:
         return self.wt.numel() + self.st.numel() * self.st.element_size() + (
-            0 if self.zt is None else self.zt.numel() * self.zt.element_size()
+            0 if self.zt is None or self.zt is self.st else self.zt.numel() * self.zt.element_size()
         )
 
 
@@ -217,8 +218,9 @@ def tile_int4(
     lib = _lib.load()
     wt = torch.empty(lib.sqx_int4_tiled_weight_bytes(rows, cols), dtype=torch.uint8, device=dev)
     npar = lib.sqx_int4_tiled_param_count(rows, cols, group_size)
-    st = torch.empty(npar, dtype=pdt, device=dev)
-    zt = None if z is None else torch.empty(npar, dtype=pdt, device=dev)
+    pairs = z is not None and pdt == torch.bfloat16  # (scale, zero) interleaved in st
+    st = torch.empty(2 * npar if pairs else npar, dtype=pdt, device=dev)
+    zt = None if z is None else (st if pairs else torch.empty(npar, dtype=pdt, device=dev))
     q8 = q.to(torch.int8).contiguous()
     with torch.cuda.device(dev):
         rc = lib.sqx_int4_tile(
@@ -262,7 +264,7 @@ def untile_int4(tw: Int4Tiled) -> tuple[Tensor, Tensor, Tensor | None]:
     g = tw.cols // tw.group_size
     codes = torch.empty(tw.rows, tw.cols, dtype=torch.int8, device=dev)
     scales = torch.empty(tw.rows, g, dtype=tw.st.dtype, device=dev)
-    zeros = None if tw.zt is None else torch.empty(tw.rows, g, dtype=tw.zt.dtype, device=dev)
+    zeros = None if tw.zt is None else torch.empty(tw.rows, g, dtype=tw.st.dtype, device=dev)
     with torch.cuda.device(dev):
         _lib.check(lib.sqx_int4_untile(tw.wt.data_ptr(), tw.st.data_ptr(), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype),
                                        0 if tw.zt is None else 1, tw.rows, tw.cols, tw.group_size, codes.data_ptr(),
