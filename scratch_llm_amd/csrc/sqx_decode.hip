@@ -469,7 +469,20 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
   }
 }
 
-// The same partials with the scores on the matrix unit (bf16 caches). Per 16 keys a wave computes
+// 8 E4M3 codes (two dwords, code e in byte e) as 4 dwords of bf16 pairs in the same order; every
+// E4M3 value is exact in bf16.
+__device__ inline u32x4_t e4m3x8_to_bf16(u32x2v_t c) {
+  u32x4_t r;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t w = c[h];  // through a scalar: hipcc's element access of a vector value
+    r[2 * h] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+    r[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
+  }
+  return r;
+}
+
+// The same partials with the scores on the matrix unit. Per 16 keys a wave computes
 // S^T = K Q^T as four v_mfma_f32_16x16x32_bf16 (A: the 16 key rows, lane l holding dims
 // 32i + 8 (l / 16) .. +8 of key l % 16; B: the G query heads as columns, zero past G; products exact,
 // fp32 sums), so lane l gets the scores of keys 4 (l / 16) + j (j < 4) for head l % 16. The softmax
@@ -482,14 +495,19 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
 #ifndef SQX_ATTN_INTERLEAVE
 #define SQX_ATTN_INTERLEAVE 1
 #endif
-template <int G, bool ROPE>
+template <int G, bool ROPE, bool KV8>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void attn_partial_mfma_kernel(const uint16_t* __restrict__ q, uint8_t* __restrict__ kc,
                                                                 uint8_t* __restrict__ vc, const int* __restrict__ lengths,
                                                                 const float* __restrict__ cos_t,
-                                                                const float* __restrict__ sin_t, int rope_rows, int H,
+                                                                const float* __restrict__ sin_t,
+                                                                const float* __restrict__ kscale,
+                                                                const float* __restrict__ vscale, int rope_rows, int H,
                                                                 int Hkv, int tmax, int chunk, int nchunk, float qscale,
                                                                 float* __restrict__ part) {
   static_assert(G >= 1 && G <= 16, "query heads are the 16 columns of the score tile");
+  using R = KvRow<KV8>;
+  using Row = typename R::T;          // a lane's 8 dims of a cache row: 16 bytes bf16, 8 bytes E4M3
+  constexpr uint32_t ES = R::kBytes;  // bytes per element
   const int ch = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kl = lane >> 4, dl = lane & 15;  // value layout: key group, 8-dim slice; score layout: key quad, head
@@ -503,7 +521,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
   const int ws = t0 + wave * span;
   constexpr int kWaveStride = kKeysPerStep;
 #endif
-  const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd * 2;  // bytes
+  const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd * ES;  // bytes
   const int len = max(lengths[b], 0);
   const int L = min(len + 1, tmax);
   const int slot = min(len, tmax - 1);
@@ -519,6 +537,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
   __shared__ __attribute__((aligned(16))) float sp[4][16][G < 4 ? 4 : G];  // per wave: p[key][head]
   __shared__ __attribute__((aligned(16))) float sa[4][G < 4 ? 4 : G];      // per wave: the step's rescale
 
+  // E4M3 rows: the K scale folds into the query's scale, the V scale multiplies the partial
+  const float ks = KV8 ? kscale[kh] : 1.0f;
+  const float vs = KV8 ? vscale[kh] : 1.0f;
+  const float qs = qscale * ks;
   const uint16_t* qrow = q + static_cast<int64_t>(b) * (ROPE ? H + 2 * Hkv : H) * kHd;
   const int64_t pr = ROPE ? static_cast<int64_t>(min(len, rope_rows - 1)) * (kHd / 2) : 0;
   // the query heads as the B operand: lane l holds dims 32i + 8 kl .. +8 of head dl (zero past G)
@@ -542,7 +564,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
   }
   // ROPE: the new key and value in the value layout (dims 8 dl .. +8); the workgroup holding the
   // slot writes them to the cache; the value (kept in LDS) stands in for the slot row below
-  __shared__ u32x4_t vnew_lds[ROPE ? 16 : 1];
+  __shared__ Row vnew_lds[ROPE ? 16 : 1];
   if constexpr (ROPE) {
     float cs[4], sn[4];
 #pragma unroll
@@ -551,20 +573,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
       sn[j] = sin_t[pr + dl * 4 + j];
     }
     if (wave == 0 && kl == 0) {
-      const u32x4_t knew = rope8(*reinterpret_cast<const u32x4_t*>(qrow + (H + kh) * kHd + dl * 8), cs, sn);
-      const u32x4_t vnew = *reinterpret_cast<const u32x4_t*>(qrow + (H + Hkv + kh) * kHd + dl * 8);
+      const u32x4_t kb16 = rope8(*reinterpret_cast<const u32x4_t*>(qrow + (H + kh) * kHd + dl * 8), cs, sn);
+      const u32x4_t vb16 = *reinterpret_cast<const u32x4_t*>(qrow + (H + Hkv + kh) * kHd + dl * 8);
+      Row knew, vnew;
+      if constexpr (KV8) {  // quantized with the head's scales, as the cache stores them
+        knew = R::encode(kb16, ks);
+        vnew = R::encode(vb16, vs);
+      } else {
+        knew = kb16;
+        vnew = vb16;
+      }
       vnew_lds[dl] = vnew;
       if (ch == slot / chunk) {  // one cache row each, from this workgroup only
-        *reinterpret_cast<u32x4_t*>(kc + head_off + (static_cast<int64_t>(slot) * kHd + dl * 8) * 2) = knew;
-        *reinterpret_cast<u32x4_t*>(vc + head_off + (static_cast<int64_t>(slot) * kHd + dl * 8) * 2) = vnew;
+        *reinterpret_cast<Row*>(kc + head_off + (static_cast<int64_t>(slot) * kHd + dl * 8) * ES) = knew;
+        *reinterpret_cast<Row*>(vc + head_off + (static_cast<int64_t>(slot) * kHd + dl * 8) * ES) = vnew;
       }
     }
     __syncthreads();
   }
   // the rows below L as buffer resources (streaming loads: each row is read once); loads of rows past
   // them return zero
-  const rsrc_t kr = make_rsrc(kc + head_off, static_cast<uint32_t>(L) * kHd * 2u);
-  const rsrc_t vrs = make_rsrc(vc + head_off, static_cast<uint32_t>(L) * kHd * 2u);
+  const rsrc_t kr = make_rsrc(kc + head_off, static_cast<uint32_t>(L) * kHd * ES);
+  const rsrc_t vrs = make_rsrc(vc + head_off, static_cast<uint32_t>(L) * kHd * ES);
   float m = -INFINITY, l = 0.0f;  // score layout: head dl's running max (same in its 4 lane groups), lane's l
   float o[G][8];
 #pragma unroll
@@ -576,13 +606,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
     // key rows: lane l reads key base + dl (score layout); value rows base + 4u + kl (value layout)
     const int kk = base + dl;
     const uint32_t kt = kk < we ? static_cast<uint32_t>(kk) : 0xFFFFFFu;  // past the range: zero rows (score masked)
-    u32x4_t kf[4], vr[4];
+    u32x4_t kf[4];
+    Row vr[4];
+    if constexpr (KV8) {  // E4M3 keys to bf16 pairs (exact) for the MFMA
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kf[i] = bload128<2>(kr, kt * (kHd * 2u) + 16u * kl, 64u * i);
+      for (int i = 0; i < 4; ++i) kf[i] = e4m3x8_to_bf16(bload64<2>(kr, kt * kHd + 8u * kl, 32u * i));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kf[i] = bload128<2>(kr, kt * (kHd * 2u) + 16u * kl, 64u * i);
+    }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int tv = base + 4 * u + kl;  // rows past the wave's range read as zero (weight 0 meets no NaN)
-      vr[u] = bload128<2>(vrs, (tv < we ? static_cast<uint32_t>(tv) : 0xFFFFFFu) * (kHd * 2u) + 16u * dl, 0u);
+      const uint32_t vo = (tv < we ? static_cast<uint32_t>(tv) : 0xFFFFFFu) * (kHd * ES) + 8u * ES * dl;
+      if constexpr (KV8) vr[u] = bload64<2>(vrs, vo, 0u);
+      else vr[u] = bload128<2>(vrs, vo, 0u);
     }
     if constexpr (ROPE) {
       if (slot >= base && slot < base + kKeysPerStep) {  // wave-uniform: this step holds the new key
@@ -595,7 +633,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
               cs[j] = cos_t[pr + 16 * i + 4 * kl + j];
               sn[j] = sin_t[pr + 16 * i + 4 * kl + j];
             }
-            kf[i] = rope8(*reinterpret_cast<const u32x4_t*>(qrow + (H + kh) * kHd + 32 * i + 8 * kl), cs, sn);
+            const u32x4_t k16 = rope8(*reinterpret_cast<const u32x4_t*>(qrow + (H + kh) * kHd + 32 * i + 8 * kl), cs, sn);
+            if constexpr (KV8) kf[i] = e4m3x8_to_bf16(R::encode(k16, ks));  // the stored code, read back
+            else kf[i] = k16;
           }
         }
 #pragma unroll
@@ -609,7 +649,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
     // score layout: keys base + 4 kl + j of head dl
     float s[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s[j] = base + 4 * kl + j < we ? sc[j] * qscale : -INFINITY;
+    for (int j = 0; j < 4; ++j) s[j] = base + 4 * kl + j < we ? sc[j] * qs : -INFINITY;
     float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -638,13 +678,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
       for (int g = 0; g < G; ++g) pv[u][g] = sp[wave][4 * u + kl][g];
     __builtin_amdgcn_wave_barrier();  // and the next step's writes after these reads
     asm volatile("" ::: "memory");
+    float vf[KV8 ? 4 : 1][8];  // E4M3 values to fp32 once per step (exact)
+    if constexpr (KV8) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) R::to_f32(vr[u], vf[u]);
+    }
+    auto vval = [&](int u, int j) -> float {
+      if constexpr (KV8) return vf[u][j];
+      else return (j & 1) ? bf16_hi(vr[u][j >> 1]) : bf16_lo(vr[u][j >> 1]);
+    };
 #pragma unroll
     for (int g = 0; g < G; ++g) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         float e = o[g][j] * av[g];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) e = fmaf(pv[u][g], (j & 1) ? bf16_hi(vr[u][j >> 1]) : bf16_lo(vr[u][j >> 1]), e);
+        for (int u = 0; u < 4; ++u) e = fmaf(pv[u][g], vval(u, j), e);
         o[g][j] = e;
       }
     }
@@ -686,7 +735,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
       pp[0] = M;
       pp[1] = lsum;
     }
-    pp[2 + dd] = osum;
+    pp[2 + dd] = KV8 ? osum * vs : osum;
   }
 }
 
@@ -1020,21 +1069,21 @@ static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, co
     case 4: SQX_ATTN(4, R_, K8_); break;   \
     default: SQX_ATTN(8, R_, K8_); break;  \
   }
-#define SQX_ATTN_M(G_, R_)                                                                                           \
-  hipLaunchKernelGGL((attn_partial_mfma_kernel<G_, R_>), grid, dim3(256), 0, s, qp, kp, vp, lengths, cos_t, sin_t, rr, \
-                     iH, iK, iT, chunk, nchunk, qscale, w)
-#define SQX_ATTN_MG(R_)                      \
-  switch (G) {                               \
-    case 1: SQX_ATTN_M(1, R_); break;        \
-    case 2: SQX_ATTN_M(2, R_); break;        \
-    case 4: SQX_ATTN_M(4, R_); break;        \
-    default: SQX_ATTN_M(8, R_); break;       \
+#define SQX_ATTN_M(G_, R_, K8_)                                                                                      \
+  hipLaunchKernelGGL((attn_partial_mfma_kernel<G_, R_, K8_>), grid, dim3(256), 0, s, qp, kp, vp, lengths, cos_t, sin_t, \
+                     kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, w)
+#define SQX_ATTN_MG(R_, K8_)                      \
+  switch (G) {                                    \
+    case 1: SQX_ATTN_M(1, R_, K8_); break;        \
+    case 2: SQX_ATTN_M(2, R_, K8_); break;        \
+    case 4: SQX_ATTN_M(4, R_, K8_); break;        \
+    default: SQX_ATTN_M(8, R_, K8_); break;       \
   }
-  // bf16 caches: scores on the matrix unit; E4M3 caches: the VALU form (keys decoded per row)
+  // scores on the matrix unit (E4M3 keys decoded to bf16 pairs on the way in)
   if (rope) {
-    if (kv8) { SQX_ATTN_G(true, true) } else { SQX_ATTN_MG(true) }
+    if (kv8) { SQX_ATTN_MG(true, true) } else { SQX_ATTN_MG(true, false) }
   } else {
-    if (kv8) { SQX_ATTN_G(false, true) } else { SQX_ATTN_MG(false) }
+    if (kv8) { SQX_ATTN_MG(false, true) } else { SQX_ATTN_MG(false, false) }
   }
 #undef SQX_ATTN_MG
 #undef SQX_ATTN_M
