@@ -174,10 +174,8 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const uint16_t* __restrict
 // Workgroup (chunk, kh, b) takes keys [chunk*C, chunk*C + C) and writes, per query head, the fp32
 // partial (m, l, o[hd]) of that range: m the maximum score (log2 units: scores are scaled by
 // log2(e) / sqrt(hd) so that the exponentials are exp2), l = sum 2^(s - m), o = sum 2^(s - m) v.
-// Each of the 4 waves walks its own quarter of the range 16 keys at a time: lane group kl = lane/16
-// holds keys base + 4u + kl (u < 4) and each lane 8 of the 128 dims, so one load instruction of the
-// wave reads 4 consecutive 256-byte key rows. A lane group keeps its own running (m, l, o); the
-// groups and the waves are merged at the end. hd must be 128.
+// The 4 waves take alternate blocks of 16 keys (the kernel and its layouts are described at
+// attn_partial_mfma_kernel below); the waves' partials are merged at the end. hd must be 128.
 // ---------------------------------------------------------------------------------------------
 constexpr int kHd = 128;
 constexpr int kKeysPerStep = 16;
@@ -202,8 +200,6 @@ template <>
 struct KvRow<false> {
   using T = u32x4_t;
   static constexpr int kBytes = 2;  // per element
-  // element j (0..7) as fp32: rows stay packed in registers and are unpacked at each use
-  __device__ static float at(const T& r, int j) { return (j & 1) ? bf16_hi(r[j >> 1]) : bf16_lo(r[j >> 1]); }
 };
 template <>
 struct KvRow<true> {
@@ -234,240 +230,6 @@ struct KvRow<true> {
     return r;
   }
 };
-
-// ROPE: q is the fused projection row [q | k | v] (width (H + 2 Hkv) * hd) and the kernel also does
-// sqx_rope_kv's work: q and the new key are rotated in registers, the new key/value stand in for
-// cache row min(lengths[b], tmax - 1) (which the workgroup holding that row writes to the cache).
-// Otherwise q is the rotated [B, H, hd] tensor and the cache already holds this step's key.
-// KV8: the cache holds E4M3 codes with one scale per kv head (kscale/vscale [Hkv], the per-head FP8
-// cache of fp8_kv_per_head.py): attention runs on the dequantized values code * scale, with the K
-// scale folded into q and the V scale applied to the partial output; the new key/value are quantized
-// with the head's scales before they are used or stored.
-// PF: the first step's rows are requested before the row length is known (one global round trip
-// fewer per workgroup; it keeps those registers live through the query set-up, which costs the bf16
-// variants a wave per SIMD, so it pays where workgroups are few or the rows are E4M3).
-template <int G, bool ROPE, bool KV8, bool PF>
-__global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __restrict__ q, uint8_t* __restrict__ kc,
-                                                           uint8_t* __restrict__ vc, const int* __restrict__ lengths,
-                                                           const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-                                                           const float* __restrict__ kscale, const float* __restrict__ vscale,
-                                                           int rope_rows, int H, int Hkv, int tmax, int chunk, int nchunk,
-                                                           float qscale, float* __restrict__ part) {
-  using R = KvRow<KV8>;
-  using Row = typename R::T;
-  constexpr int ES = R::kBytes;
-  const int ch = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int kl = lane >> 4, dl = lane & 15;
-  const int t0 = ch * chunk;
-  const int span = chunk / 4;
-  const int ws = t0 + wave * span;
-  const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd * ES;  // bytes
-  const uint8_t* kb = kc + head_off + dl * 8 * ES;
-  const uint8_t* vb = vc + head_off + dl * 8 * ES;
-  // PF: the first step's rows are requested before the row's length is known (rows clamped into the
-  // cache; rows past the attended range are masked, and their values zeroed, once it is), so they
-  // travel with the length and the query instead of after them.
-  Row kr[4], vr[4];
-  if constexpr (PF) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int tc = min(ws + 4 * u + kl, tmax - 1);
-      kr[u] = *reinterpret_cast<const Row*>(kb + static_cast<int64_t>(tc) * kHd * ES);
-      vr[u] = *reinterpret_cast<const Row*>(vb + static_cast<int64_t>(tc) * kHd * ES);
-    }
-  }
-  const int len = max(lengths[b], 0);
-  const int L = min(len + 1, tmax);
-  const int slot = min(len, tmax - 1);
-  if (t0 >= L) return;  // the combine reads only chunks below L
-  const int we = min(ws + span, L);
-
-  __shared__ float sm[4][G], sl[4][G];
-  __shared__ float so[4][G][kHd];
-
-  const float ks = KV8 ? kscale[kh] : 1.0f;
-  const float vs = KV8 ? vscale[kh] : 1.0f;
-  const uint16_t* qrow = q + static_cast<int64_t>(b) * (ROPE ? H + 2 * Hkv : H) * kHd + dl * 8;
-  float cs[4], sn[4];
-  Row knew{}, vnew{};
-  if constexpr (ROPE) {
-    const int64_t pr = static_cast<int64_t>(min(len, rope_rows - 1)) * (kHd / 2) + dl * 4;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      cs[j] = cos_t[pr + j];
-      sn[j] = sin_t[pr + j];
-    }
-    const u32x4_t kb16 = rope8(*reinterpret_cast<const u32x4_t*>(qrow + (H + kh) * kHd), cs, sn);
-    const u32x4_t vb16 = *reinterpret_cast<const u32x4_t*>(qrow + (H + Hkv + kh) * kHd);
-    if constexpr (KV8) {
-      knew = R::encode(kb16, ks);
-      vnew = R::encode(vb16, vs);
-    } else {
-      knew = kb16;
-      vnew = vb16;
-    }
-  }
-  const float qs = qscale * ks;
-  // The query stays in bf16 pairs and a score is sum(q k) by v_dot2c_f32_bf16 (exact products, fp32
-  // sums), scaled once by qscale (and the K scale); E4M3 keys are decoded to bf16 pairs for it, which
-  // every E4M3 value is exactly.
-  u32x4_t qb[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    u32x4_t v = *reinterpret_cast<const u32x4_t*>(qrow + (kh * G + g) * kHd);
-    if constexpr (ROPE) v = rope8(v, cs, sn);
-    qb[g] = v;
-  }
-  float m[G], l[G], o[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[g][j] = 0.0f;
-  }
-  if constexpr (ROPE) {
-    if (ch == slot / chunk && wave == 0 && kl == 0) {  // one cache row each, from this workgroup only
-      *reinterpret_cast<Row*>(kc + head_off + (static_cast<int64_t>(slot) * kHd + dl * 8) * ES) = knew;
-      *reinterpret_cast<Row*>(vc + head_off + (static_cast<int64_t>(slot) * kHd + dl * 8) * ES) = vnew;
-    }
-  }
-
-  for (int base = ws; base < we; base += kKeysPerStep) {
-    bool ok[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) ok[u] = base + 4 * u + kl < we;
-    if (PF && base == ws) {
-      // the prefetched rows: a masked row may hold anything, and its weight 0 must not meet a NaN
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (!ok[u]) vr[u] = Row{};
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int tc = ok[u] ? base + 4 * u + kl : base;  // an in-range row; its score is masked below
-        kr[u] = *reinterpret_cast<const Row*>(kb + static_cast<int64_t>(tc) * kHd * ES);
-        vr[u] = *reinterpret_cast<const Row*>(vb + static_cast<int64_t>(tc) * kHd * ES);
-      }
-    }
-    if constexpr (ROPE) {
-      if (slot >= base && slot < base + kKeysPerStep) {  // wave-uniform: this step holds the new key
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (base + 4 * u + kl == slot) {
-            kr[u] = knew;
-            vr[u] = vnew;
-          }
-        }
-      }
-    }
-    // E4M3 rows: keys to bf16 pairs and values to fp32, once per step (two codes per conversion);
-    // bf16 rows are read in place
-    u32x4_t kb2[KV8 ? 4 : 1];
-    float vf[KV8 ? 4 : 1][8];
-    if constexpr (KV8) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint32_t w = kr[u][h];  // through a scalar: hipcc's element access of a vector value
-          kb2[u][2 * h] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
-          kb2[u][2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
-        }
-        R::to_f32(vr[u], vf[u]);
-      }
-    }
-    auto vval = [&](int u, int j) -> float {
-      if constexpr (KV8) return vf[u][j]; else return R::at(vr[u], j);
-    };
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float s[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        float acc = 0.0f;
-        if constexpr (KV8) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            // elements go through scalars: hipcc's bit_cast of a vector element reads element 0
-            const uint32_t qj = qb[g][j], kj = kb2[u][j];
-            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qj), __builtin_bit_cast(bf16x2_t, kj),
-                                                  acc, false);
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint32_t qj = qb[g][j], kj = kr[u][j];
-            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qj), __builtin_bit_cast(bf16x2_t, kj),
-                                                  acc, false);
-          }
-        }
-        s[u] = ok[u] ? row16_sum(acc) * qs : -INFINITY;
-      }
-      const float mn = fmaxf(fmaxf(m[g], fmaxf(s[0], s[1])), fmaxf(s[2], s[3]));
-      // a group whose keys are all masked so far keeps m = -inf and adds nothing
-      const float a = mn == -INFINITY ? 1.0f : exp2f(m[g] - mn);
-      float p[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) p[u] = ok[u] ? exp2f(s[u] - mn) : 0.0f;
-      l[g] = fmaf(l[g], a, (p[0] + p[1]) + (p[2] + p[3]));
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float e = o[g][j] * a;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) e = fmaf(p[u], vval(u, j), e);
-        o[g][j] = e;
-      }
-      m[g] = mn;
-    }
-  }
-  // merge the 4 lane groups of the wave (lane bits 4 and 5)
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-#pragma unroll
-    for (int off = 16; off < 64; off <<= 1) {
-      const float mo = __shfl_xor(m[g], off, 64), lo = __shfl_xor(l[g], off, 64);
-      const float mn = fmaxf(m[g], mo);
-      const float a = m[g] == -INFINITY ? 0.0f : exp2f(m[g] - mn);
-      const float c = mo == -INFINITY ? 0.0f : exp2f(mo - mn);
-      l[g] = l[g] * a + lo * c;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[g][j] = o[g][j] * a + __shfl_xor(o[g][j], off, 64) * c;
-      m[g] = mn;
-    }
-  }
-  if (kl == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      if (dl == 0) {
-        sm[wave][g] = m[g];
-        sl[wave][g] = l[g];
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) so[wave][g][dl * 8 + j] = o[g][j];
-    }
-  }
-  __syncthreads();
-  // merge the 4 waves: thread (g, dd) writes element dd of head g's partial
-  for (int idx = threadIdx.x; idx < G * kHd; idx += 256) {
-    const int g = idx / kHd, dd = idx % kHd;
-    const float M = fmaxf(fmaxf(sm[0][g], sm[1][g]), fmaxf(sm[2][g], sm[3][g]));
-    float lsum = 0.0f, osum = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float a = sm[w][g] == -INFINITY ? 0.0f : exp2f(sm[w][g] - M);
-      lsum = fmaf(sl[w][g], a, lsum);
-      osum = fmaf(so[w][g][dd], a, osum);
-    }
-    float* pp = part + ((static_cast<int64_t>(b) * H + kh * G + g) * nchunk + ch) * (kHd + 2);
-    if (dd == 0) {
-      pp[0] = M;
-      pp[1] = lsum;
-    }
-    pp[2 + dd] = KV8 ? osum * vs : osum;
-  }
-}
 
 // 8 E4M3 codes (two dwords, code e in byte e) as 4 dwords of bf16 pairs in the same order; every
 // E4M3 value is exact in bf16.
@@ -1050,25 +812,6 @@ static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, co
   float* w = static_cast<float*>(ws);
   const int iH = static_cast<int>(H), iK = static_cast<int>(Hkv), iT = static_cast<int>(tmax);
   const int rr = static_cast<int>(rope_rows);
-  // early row loads: always for E4M3 rows; for bf16 rows when the grid fits the CUs at two
-  // workgroups each (the bf16 variants lose a wave per SIMD to them)
-  const bool pf = kv8 || static_cast<int64_t>(nchunk) * Hkv * B <= 512;
-#define SQX_ATTN(G_, R_, K8_)                                                                                          \
-  do {                                                                                                             \
-    if (pf)                                                                                                        \
-      hipLaunchKernelGGL((attn_partial_kernel<G_, R_, K8_, true>), grid, dim3(256), 0, s, qp, kp, vp, lengths, cos_t, \
-                         sin_t, kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, w);                           \
-    else                                                                                                           \
-      hipLaunchKernelGGL((attn_partial_kernel<G_, R_, K8_, false>), grid, dim3(256), 0, s, qp, kp, vp, lengths,     \
-                         cos_t, sin_t, kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, w);                    \
-  } while (0)
-#define SQX_ATTN_G(R_, K8_)                \
-  switch (G) {                             \
-    case 1: SQX_ATTN(1, R_, K8_); break;   \
-    case 2: SQX_ATTN(2, R_, K8_); break;   \
-    case 4: SQX_ATTN(4, R_, K8_); break;   \
-    default: SQX_ATTN(8, R_, K8_); break;  \
-  }
 #define SQX_ATTN_M(G_, R_, K8_)                                                                                      \
   hipLaunchKernelGGL((attn_partial_mfma_kernel<G_, R_, K8_>), grid, dim3(256), 0, s, qp, kp, vp, lengths, cos_t, sin_t, \
                      kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, w)
@@ -1087,8 +830,6 @@ static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, co
   }
 #undef SQX_ATTN_MG
 #undef SQX_ATTN_M
-#undef SQX_ATTN_G
-#undef SQX_ATTN
   SQX_LAUNCH_CHECK(fn);
   hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(B)), dim3(256), 0, s, w,
                      lengths, iH, iT, chunk, nchunk, static_cast<uint16_t*>(out));
