@@ -254,11 +254,8 @@ __device__ inline u32x4_t e4m3x8_to_bf16(u32x2v_t c) {
 // holds value rows base + 4u + kl, each lane 8 dims, fp32 products and sums as above). This moves
 // the dot products and most of the softmax off the VALU, which bounds the kernel above at large
 // batch (every lane worked every head's scores, 4 fdot2 and 4 row reductions a key).
-#ifndef SQX_ATTN_INTERLEAVE
-#define SQX_ATTN_INTERLEAVE 1
-#endif
 template <int G, bool ROPE, bool KV8>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void attn_partial_mfma_kernel(const uint16_t* __restrict__ q, uint8_t* __restrict__ kc,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_partial_mfma_kernel(const uint16_t* __restrict__ q, uint8_t* __restrict__ kc,
                                                                 uint8_t* __restrict__ vc, const int* __restrict__ lengths,
                                                                 const float* __restrict__ cos_t,
                                                                 const float* __restrict__ sin_t,
@@ -274,25 +271,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kl = lane >> 4, dl = lane & 15;  // value layout: key group, 8-dim slice; score layout: key quad, head
   const int t0 = ch * chunk;
-#if SQX_ATTN_INTERLEAVE
   // the 4 waves take alternate 16-key blocks of the chunk: the workgroup streams one region
   const int ws = t0 + wave * kKeysPerStep;
   constexpr int kWaveStride = 4 * kKeysPerStep;
-#else
-  const int span = chunk / 4;
-  const int ws = t0 + wave * span;
-  constexpr int kWaveStride = kKeysPerStep;
-#endif
   const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd * ES;  // bytes
   const int len = max(lengths[b], 0);
   const int L = min(len + 1, tmax);
   const int slot = min(len, tmax - 1);
   if (t0 >= L) return;  // the combine reads only chunks below L
-#if SQX_ATTN_INTERLEAVE
   const int we = min(t0 + chunk, L);
-#else
-  const int we = min(ws + span, L);
-#endif
 
   __shared__ float sm[4][G], sl[4][G];
   __shared__ float so[4][G][kHd];
@@ -364,26 +351,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[g][j] = 0.0f;
 
-  for (int base = ws; base < we; base += kWaveStride) {
-    // key rows: lane l reads key base + dl (score layout); value rows base + 4u + kl (value layout)
-    const int kk = base + dl;
-    const uint32_t kt = kk < we ? static_cast<uint32_t>(kk) : 0xFFFFFFu;  // past the range: zero rows (score masked)
-    u32x4_t kf[4];
-    Row vr[4];
-    if constexpr (KV8) {  // E4M3 keys to bf16 pairs (exact) for the MFMA
+  // Two register sets in turn: block base + stride is requested before block base is worked on
+  // (loads past the range read zero from the buffer resources, so every iteration issues the same
+  // loads and the waits are exact counts)
+  auto load_block = [&](int bs, Row (&ko)[4], Row (&vo_)[4]) {
+    const int kq = bs + dl;
+    const uint32_t kt = kq < we ? static_cast<uint32_t>(kq) : 0xFFFFFFu;  // past the range: zero rows (score masked)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kf[i] = e4m3x8_to_bf16(bload64<2>(kr, kt * kHd + 8u * kl, 32u * i));
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) kf[i] = bload128<2>(kr, kt * (kHd * 2u) + 16u * kl, 64u * i);
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (KV8) ko[i] = bload64<2>(kr, kt * kHd + 8u * kl, 32u * i);
+      else ko[i] = bload128<2>(kr, kt * (kHd * 2u) + 16u * kl, 64u * i);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int tv = base + 4 * u + kl;  // rows past the wave's range read as zero (weight 0 meets no NaN)
+      const int tv = bs + 4 * u + kl;  // rows past the wave's range read as zero (weight 0 meets no NaN)
       const uint32_t vo = (tv < we ? static_cast<uint32_t>(tv) : 0xFFFFFFu) * (kHd * ES) + 8u * ES * dl;
-      if constexpr (KV8) vr[u] = bload64<2>(vrs, vo, 0u);
-      else vr[u] = bload128<2>(vrs, vo, 0u);
+      if constexpr (KV8) vo_[u] = bload64<2>(vrs, vo, 0u);
+      else vo_[u] = bload128<2>(vrs, vo, 0u);
     }
+  };
+  auto process = [&](int base, const Row (&kraw)[4], const Row (&vraw)[4]) {
+    const int kk = base + dl;
+    u32x4_t kf[4];
+    Row vr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (KV8) kf[i] = e4m3x8_to_bf16(kraw[i]);  // E4M3 keys to bf16 pairs (exact) for the MFMA
+      else kf[i] = kraw[i];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) vr[u] = vraw[u];
     if constexpr (ROPE) {
       if (slot >= base && slot < base + kKeysPerStep) {  // wave-uniform: this step holds the new key
         if (kk == slot) {
@@ -459,6 +456,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
         o[g][j] = e;
       }
     }
+  };
+  Row ka[4], va[4], kb[4], vb[4];
+  load_block(ws, ka, va);
+  for (int base = ws; base < we; base += 2 * kWaveStride) {
+    load_block(base + kWaveStride, kb, vb);
+    process(base, ka, va);
+    if (base + kWaveStride >= we) break;  // wave-uniform
+    load_block(base + 2 * kWaveStride, ka, va);
+    process(base + kWaveStride, kb, vb);
   }
   // the lane groups of the wave: m is already common to a head's lanes, so l and o simply add
   l += __shfl_xor(l, 16, 64);
@@ -754,12 +760,13 @@ extern "C" int sqx_rope_kv(const void* qkv, const int* lengths, const float* cos
   return SQX_OK;
 }
 
-// Keys per workgroup: the smallest of 64..1024 that still gives about SQX_ATTN_TARGET_WG workgroups
-// (four resident per CU at the score kernel's register budget; longer walks per wave amortise each
-// workgroup's set-up and merge: measured at 2048 keys, B = 8 / 32 / 64 take 22 / 60 / 107 us against
-// 29 / 67 / 114 us with a 2048-workgroup target and 512-key chunks).
+// Keys per workgroup: the smallest of 64..1024 that still gives about SQX_ATTN_TARGET_WG workgroups.
+// Long walks per wave amortise each workgroup's set-up and merge, and with the next block's rows in
+// flight during each block (two register sets) one workgroup per CU streams well: measured at 2048
+// keys (partial + combine), B = 1 / 8 / 32 / 64 take 9.5 / 17.8 / 48.8 / 91.1 us with a 256-workgroup
+// target, against 10.2 / 22.5 / 60.4 / 104.9 us for a single register set and a 1024 target.
 #ifndef SQX_ATTN_TARGET_WG
-#define SQX_ATTN_TARGET_WG 1024
+#define SQX_ATTN_TARGET_WG 256
 #endif
 #ifndef SQX_ATTN_MAX_CHUNK
 #define SQX_ATTN_MAX_CHUNK 1024
