@@ -55,7 +55,9 @@ __device__ inline void mx_tile_of(int bid, int tiles_m, int tiles_n, int& tm, in
 // Issue this wave's share of the global -> LDS copies of k-step kb into `stage`. The 32 fragment
 // copies of a step (16 of X, then 16 of W, 1 KiB per instruction) are split evenly over the NW
 // waves, and so are the 8 scale copies (256 bytes = 4 fragments' 64-byte blocks per instruction).
-// Fragment rows past the operand's last 16-row tile are clamped to it (their outputs are masked).
+// Fragment rows past the operand's last 16-row tile are not read: their copies go past the buffer
+// resource, which writes zeros without touching memory (the outputs they feed are masked), so an
+// operand of fewer than 256 rows costs only its own bytes.
 template <int NW>
 __device__ inline void mx_issue_step(uint8_t* stage, int wave, int lane, int kb, int KB, rsrc_t xr, rsrc_t xsr,
                                      rsrc_t wr, rsrc_t wsr, int x_t0, int x_tmax, int w_t0, int w_tmax) {
@@ -69,8 +71,9 @@ __device__ inline void mx_issue_step(uint8_t* stage, int wave, int lane, int kb,
   uint8_t* dst = stage + (is_w ? mxg::kOpBytes : 0) + f0 * 1024;
 #pragma unroll
   for (int j = 0; j < FPW; ++j) {
-    const int t = min(t0 + f0 + j, tmax);
-    const uint32_t off = ((uint32_t)t * (uint32_t)KB + (uint32_t)kb) * 1024u + (uint32_t)lane * 16u;
+    const int t = t0 + f0 + j;
+    const uint32_t off =
+        t <= tmax ? ((uint32_t)t * (uint32_t)KB + (uint32_t)kb) * 1024u + (uint32_t)lane * 16u : 0xFFFFFFF0u;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(fr, (lds_void*)(dst + j * 1024), 16, off, 0, 0, 0);
   }
 #pragma unroll
@@ -87,7 +90,8 @@ __device__ inline void mx_issue_step(uint8_t* stage, int wave, int lane, int kb,
 
 
 // WN: waves along n (2: four waves of 128 x 128; 4: eight waves of 128 x 64, two per SIMD).
-template <int NSTAGE, int YKIND, int WN>  // YKIND: 0 = bf16, 1 = fp16, 2 = fp32
+// SKIPR: X has at most 128 rows, so the waves of the tile's second 128 rows have nothing to compute.
+template <int NSTAGE, int YKIND, int WN, bool SKIPR = false>  // YKIND: 0 = bf16, 1 = fp16, 2 = fp32
 __global__ __launch_bounds__(128 * WN) void mxfp4_gemm_kernel(const uint8_t* __restrict__ xt,
                                                         const uint8_t* __restrict__ xst,
                                                         const uint8_t* __restrict__ wt,
@@ -174,15 +178,18 @@ __global__ __launch_bounds__(128 * WN) void mxfp4_gemm_kernel(const uint8_t* __r
   if (KB - 1 >= NSTAGE - 2) wait_vmcnt<kPerStep * (NSTAGE - 2)>();  // step 0 landed for this wave ...
   else wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();  // ... and for every wave
+  // SKIPR: the waves of rows 128..255 skip their operand reads and MFMAs (they still copy and wait
+  // with the others); otherwise every wave computes (no branch in the schedule)
+  const bool live = !SKIPR || wm == 0;  // wave-uniform
   Ops o0, o1;
-  read_ops(smem, 0, o0);
+  if (live) read_ops(smem, 0, o0);
   // steady state: every iteration issues a copy, and the copies of NSTAGE-3 later steps may stay
   // in flight at the barrier
   int kb = 0;
   for (; kb + NSTAGE - 1 < KB; ++kb) {
     const uint8_t* st = smem + (kb % NSTAGE) * mxg::kStage;
-    read_ops(st, 1, o1);
-    mma(o0);
+    if (live) read_ops(st, 1, o1);
+    if (live) mma(o0);
     __builtin_amdgcn_sched_barrier(0);
     wait_vmcnt<kPerStep * (NSTAGE - 3)>();
     __builtin_amdgcn_s_barrier();
@@ -190,20 +197,20 @@ __global__ __launch_bounds__(128 * WN) void mxfp4_gemm_kernel(const uint8_t* __r
     mx_issue_step<NW>(smem + ((kb + NSTAGE - 1) % NSTAGE) * mxg::kStage, wave, lane, kbeg + kb + NSTAGE - 1, KBall, xr,
                       xsr, wr,
                   wsr, x_t0, xT - 1, w_t0, wT - 1);
-    read_ops(smem + ((kb + 1) % NSTAGE) * mxg::kStage, 0, o0);
-    mma(o1);
+    if (live) read_ops(smem + ((kb + 1) % NSTAGE) * mxg::kStage, 0, o0);
+    if (live) mma(o1);
   }
   // tail: nothing left to issue; wait for everything still in flight
   for (; kb < KB; ++kb) {
     const uint8_t* st = smem + (kb % NSTAGE) * mxg::kStage;
-    read_ops(st, 1, o1);
-    mma(o0);
+    if (live) read_ops(st, 1, o1);
+    if (live) mma(o0);
     __builtin_amdgcn_sched_barrier(0);
     wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    if (kb + 1 < KB) read_ops(smem + ((kb + 1) % NSTAGE) * mxg::kStage, 0, o0);
-    mma(o1);
+    if (live && kb + 1 < KB) read_ops(smem + ((kb + 1) % NSTAGE) * mxg::kStage, 0, o0);
+    if (live) mma(o1);
   }
 
   // Epilogue. W is the MFMA's first operand, so acc[r][c][i] is
@@ -735,7 +742,10 @@ hipError_t launch_mx(const uint8_t* xt, const uint8_t* xst, const uint8_t* wt, c
   const int tiles_m = (m + mxg::kTile - 1) / mxg::kTile, tiles_n = (n + mxg::kTile - 1) / mxg::kTile;
   const size_t lds = (size_t)kMxStages * mxg::kStage;
   const int kps = (KB + splits - 1) / splits;
-  auto kern = splits > 1 ? mxfp4_gemm_kernel<kMxStages, 2, SQX_MX_WN> : mxfp4_gemm_kernel<kMxStages, YK, SQX_MX_WN>;
+  auto kern = m <= 128 ? (splits > 1 ? mxfp4_gemm_kernel<kMxStages, 2, SQX_MX_WN, true>
+                                     : mxfp4_gemm_kernel<kMxStages, YK, SQX_MX_WN, true>)
+                       : (splits > 1 ? mxfp4_gemm_kernel<kMxStages, 2, SQX_MX_WN>
+                                     : mxfp4_gemm_kernel<kMxStages, YK, SQX_MX_WN>);
   // more than 64 KiB of dynamic LDS has to be allowed per kernel
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)lds);
