@@ -820,11 +820,20 @@ def baseline_configs(dev) -> dict:
         for m in (1, 4, 8):
             x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
             y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            # what w4a16_linear runs (int4_linear_tiled): the GEMV at one row, the library's choice
+            # among the GEMV and the row-tiled kernels (K split into a workspace) for 2..64 rows
+            nb = int(lib.sqx_int4_skinny_workspace_bytes(m, n, k, 0))
+            ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
 
             def run(stream):
                 for tw in tws:
-                    lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), tw.zt.data_ptr(), _lib.DTYPE_BF16,
-                                        x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(), None, m, n, k, 128, 0, stream)
+                    if m == 1:
+                        lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), tw.zt.data_ptr(), _lib.DTYPE_BF16,
+                                            x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(), None, m, n, k, 128, 0, stream)
+                    else:
+                        lib.sqx_int4_skinny(tw.wt.data_ptr(), tw.st.data_ptr(), tw.zt.data_ptr(), _lib.DTYPE_BF16,
+                                            x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(), None, m, n, k, 128, -1, 0, 0,
+                                            0, ws.data_ptr() if nb > 0 else None, nb, stream)
                 return len(tws)
 
             byts = n * k // 2 + 2 * 2 * n * k // 128 + 2 * m * k + 2 * m * n
