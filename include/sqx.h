@@ -159,7 +159,7 @@ int sqx_int4_skinny_partials(const uint8_t* wt, const void* st, const void* zt, 
                              int64_t ws_bytes, sqx_stream_t stream);
 
 /* 1 when sqx_int4_linear_rmsnorm / sqx_int4_linear_silu take m activation rows of cols columns
- * (m <= 8, cols % 8 == 0, the rows fit the kernel's 64 KiB LDS copy), else 0. */
+ * (m <= 8, cols % 8 == 0, m * (cols rounded up to 128, + 8) * 2 <= 64 KiB), else 0. */
 int sqx_int4_prologue_fits(int64_t m, int64_t cols);
 
 /* A decode-step linear with the residual add and RMSNorm in front of it (TransformerBlock.forward,
@@ -273,7 +273,8 @@ int sqx_scale_columns(const void* x, int act_dtype, const float* s, int64_t rows
 /* AWQ linear (awq_linear, awq.py:184-192): the W4A16 linear of the codes of W*s with the per-input
  * channel AWQ scale s folded into the activations, y = (x / s) @ (q*gs)^T; x / s is computed in fp32
  * per element and rounded to act_dtype while the workgroup copies x into LDS. col_scale: fp32 [cols].
- * Needs m <= 16 and m*cols*2 <= 64 KiB (larger inputs: divide x first, then sqx_int4_linear).
+ * Needs m <= 16 and m * (cols rounded up to 128, + 8) * 2 <= 66 KiB (larger inputs: divide x first,
+ * then sqx_int4_linear).
  * Other arguments as sqx_int4_linear. */
 int sqx_int4_linear_colscaled(const uint8_t* wt, const void* st, const void* zt, int param_dtype,
                               const void* x, int act_dtype, const float* col_scale, void* y,

@@ -210,7 +210,7 @@ def awq_linear_tiled(x: Tensor, tw: Int4Tiled, chan_scale: Tensor, bias: Tensor 
     m = x2.shape[0]
     lib = _lib.load()
     with torch.cuda.device(x.device):
-        if m <= 16 and m * (-(-k // 128) * 128 + 8) * 2 <= 64 * 1024:
+        if m <= 16 and m * (-(-k // 128) * 128 + 8) * 2 <= 66 * 1024:  # the GEMV's LDS copy of the rows
             y = torch.empty(m, tw.rows, dtype=x.dtype, device=x.device)
             b = None if bias is None else bias.to(x.dtype).contiguous()
             _lib.check(lib.sqx_int4_linear_colscaled(tw.wt.data_ptr(), tw.st.data_ptr(), None, _lib.DTYPE_F32,
