@@ -689,7 +689,7 @@ def fp8_linears(dev) -> dict:
         for m in (1, 16):
             x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
             y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-            wsp = torch.empty(int(lib.sqx_fp8_linear_workspace_bytes(m, k)) // 4 + 4, dtype=torch.float32, device=dev)
+            wsp = torch.empty(int(lib.sqx_fp8_linear_workspace_bytes(m, n, k)) // 4 + 4, dtype=torch.float32, device=dev)
 
             def ours(stream):
                 for _, _, tw in ws:

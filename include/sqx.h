@@ -554,11 +554,25 @@ int sqx_fp8_tile(const uint8_t* codes, int64_t rows, int64_t cols, uint8_t* wt, 
 /* fp8_linear (fp8_weights.py:211-262): x [m, cols] (F32 / BF16 / F16) is quantized per token,
  * y[i, r] = (sum_c qx[i, c] * qw[r, c]) * s_x[i] * w_scale[r] (+ bias[r]) with exact products and fp32
  * accumulation; y [m, rows] of y_dtype (BF16, or F32 without bias); bias BF16 or NULL. wt from
- * sqx_fp8_tile; w_scale fp32 [rows]. cols % 8 == 0. ws: sqx_fp8_linear_workspace_bytes(m, cols) bytes
- * (the quantized activations), 16-byte aligned. */
-int64_t sqx_fp8_linear_workspace_bytes(int64_t m, int64_t cols);
+ * sqx_fp8_tile; w_scale fp32 [rows]. cols % 8 == 0. ws: sqx_fp8_linear_workspace_bytes(m, rows, cols)
+ * bytes (the quantized activations and, where the library's launch splits K, fp32 partial sums),
+ * 16-byte aligned. k_slices <= 0 lets the library pick the launch: for 2..64 rows and a BF16 output
+ * the kernel of sqx_fp8_skinny where it is faster, otherwise the GEMV (k_slices > 0: the GEMV with
+ * that many waves per tile). */
+int64_t sqx_fp8_linear_workspace_bytes(int64_t m, int64_t rows, int64_t cols);
 int sqx_fp8_linear(const uint8_t* wt, const float* w_scale, const void* x, int act_dtype, void* y, int y_dtype,
                    const void* bias, int64_t m, int64_t rows, int64_t cols, int k_slices, void* ws,
+                   int64_t ws_bytes, sqx_stream_t stream);
+
+/* sqx_fp8_linear (BF16 output, m <= 64) on the decode-regime kernel with an explicit launch shape:
+ * a workgroup owns `tiles` (2 or 4) tiles of 16 weight rows and applies each activation fragment to
+ * all of them, `waves` (1..8) waves split its k-blocks, `splits` workgroups split K (partials added
+ * in split order by a second kernel, which applies the scales). Same results as sqx_fp8_linear to
+ * its bound; fp32 sums in a different order. ws: sqx_fp8_skinny_workspace_bytes(m, rows, cols,
+ * splits) bytes. No counterpart in the reference (launch planning). */
+int64_t sqx_fp8_skinny_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int splits);
+int sqx_fp8_skinny(const uint8_t* wt, const float* w_scale, const void* x, int act_dtype, void* y, const void* bias,
+                   int64_t m, int64_t rows, int64_t cols, int tiles, int waves, int splits, void* ws,
                    int64_t ws_bytes, sqx_stream_t stream);
 
 /* ============================================================================================

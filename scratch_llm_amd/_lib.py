@@ -150,7 +150,10 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sqx_fp8_dequantize_heads": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_fp8_tiled_weight_bytes": (_c_i64, [_c_i64, _c_i64]),
     "sqx_fp8_tile": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
-    "sqx_fp8_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "sqx_fp8_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "sqx_fp8_skinny_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i]),
+    "sqx_fp8_skinny": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i, _c_i, _c_i, _c_p, _c_i64,
+                              _c_p]),
     "sqx_fp8_linear": (
         _c_i,
         [_c_p, _c_p, _c_p, _c_i, _c_p, _c_i, _c_p, _c_i64, _c_i64, _c_i64, _c_i, _c_p, _c_i64, _c_p],

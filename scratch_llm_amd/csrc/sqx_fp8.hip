@@ -13,7 +13,7 @@
 //
 // Tiled FP8 weights: block (t, kb) = 1 KiB covering 16 rows x 64 columns; lane L owns the 16 codes of
 // row 16t + (L & 15), columns kb*64 + 16(L >> 4) + e, code e in byte e. Padding holds code 0.
-#include "sqx_gemv.h"
+#include "sqx_skinny.h"
 
 namespace sqx {
 
@@ -237,6 +237,25 @@ struct WFp8 {
   __device__ static float out_scale(const Args& a, int n) { return a.wscale[n]; }
   __device__ static float row_scale(const Args& a, int m) { return a.xscale[m]; }
   static Args rows_from(const Args& a, int64_t m0) { return Args{a.wt, a.wscale, a.xscale + m0}; }
+  static const float* row_scales(const Args& a) { return a.xscale; }
+  static const float* out_scales(const Args& a) { return a.wscale; }
+
+  // The skinny linear's hooks: the decoded values are the weights themselves (no offset, no group
+  // scale), so each block's MFMAs chain straight into the output sums.
+  static constexpr int NG = 1, MPG = STEPS;
+  static constexpr bool kPlainBlocks = true, kConstOffset = true;
+  __device__ static Ctx ctx_tiles(const Args& a, int t, int nt, int KB, int lane) {
+    return Ctx{make_rsrc(a.wt + (int64_t)t * KB * 1024, (uint32_t)nt * (uint32_t)KB * 1024u), (uint32_t)lane * 16u};
+  }
+  template <class A>
+  __device__ static u32x4_t bfrag(const u32x4_t& w, int i) {
+    return u32x4_t{pair<false>(w[2 * i]), pair<true>(w[2 * i]), pair<false>(w[2 * i + 1]), pair<true>(w[2 * i + 1])};
+  }
+  template <class A>
+  __device__ static float const_offset() { return 0.0f; }
+  template <class A>
+  __device__ static float offset(const P&, int) { return 0.0f; }
+  __device__ static float scale(const P&, int) { return 1.0f; }
 };
 
 }  // namespace sqx
@@ -355,31 +374,70 @@ extern "C" int sqx_fp8_tile(const uint8_t* codes, int64_t rows, int64_t cols, ui
   return SQX_OK;
 }
 
-// Workspace of sqx_fp8_linear: the activations' E4M3 values as bf16 [m, cols] (rounded up to 256
-// bytes), then their per-token scales [m].
-static int64_t fp8_vals_bytes(int64_t m, int64_t cols) { return (m * cols * 2 + 255) / 256 * 256; }
+// Workspace of the FP8 linear: the activations' E4M3 values as bf16 [m, cols], their per-token
+// scales [m], then (when the launch splits K) the fp32 partials [S][m][rows]; each part starts on a
+// 256-byte boundary.
+static int64_t fp8_round256(int64_t b) { return (b + 255) / 256 * 256; }
+static int64_t fp8_vals_bytes(int64_t m, int64_t cols) { return fp8_round256(m * cols * 2); }
+static int64_t fp8_part_offset(int64_t m, int64_t cols) { return fp8_vals_bytes(m, cols) + fp8_round256(m * 4); }
 
-extern "C" int64_t sqx_fp8_linear_workspace_bytes(int64_t m, int64_t cols) {
-  if (m <= 0 || cols <= 0) return 0;
-  return fp8_vals_bytes(m, cols) + m * 4;
+// The launch the library picks for m rows (bf16 output), from a measured sweep of the Llama-3-8B
+// shapes (4096 -> 1024 / 4096 / 6144 / 28672, 14336 -> 4096) at m = 2..64. R tiles of 16 weight rows
+// per workgroup share each activation fragment, `waves` waves split its k-blocks, S workgroups split
+// K; `gemv` marks shapes where the GEMV (one workgroup per tile) is faster:
+//   >= 1024 tiles          R = 2 (m <= 8) or 4, 4 waves, no split;
+//   384 .. 1023 tiles      the GEMV for m <= 4, else R = 2 with 8 waves;
+//   fewer, K >= 8192       the GEMV for m <= 4, else 8 waves and 4 splits, R = 2 (m <= 8) or 4;
+//   fewer, shorter K       the GEMV for m <= 16, else R = 2, 8 waves, 2 splits (4 below 256 tiles).
+static SkinnyShape fp8_default_shape(int64_t m, int64_t rows, int64_t cols) {
+  const int64_t T = ceil_div(rows, 16);
+  const int64_t KB = ceil_div(cols, WFp8::KBLK);
+  SkinnyShape sh{0, 2, 8, 1, true};
+  if (m < 2 || m > 64) return sh;
+  if (T >= 1024) return SkinnyShape{0, m <= 8 ? 2 : 4, 4, 1, false};
+  if (T >= 384) return SkinnyShape{0, 2, 8, 1, m <= 4};
+  if (KB >= 128) return SkinnyShape{0, m <= 8 ? 2 : 4, 8, 4, m <= 4};
+  return SkinnyShape{0, 2, 8, T >= 256 ? 2 : 4, m <= 16};
 }
 
-extern "C" int sqx_fp8_linear(const uint8_t* wt, const float* w_scale, const void* x, int act_dtype, void* y, int y_dtype,
-                              const void* bias, int64_t m, int64_t rows, int64_t cols, int k_slices, void* ws,
-                              int64_t ws_bytes, sqx_stream_t stream) {
-  const char* fn = "sqx_fp8_linear";
+static int64_t fp8_ws_bytes(int64_t m, int64_t rows, int64_t cols, const SkinnyShape& sh) {
+  if (m <= 0 || rows <= 0 || cols <= 0) return 0;
+  const int S = sh.gemv ? 1 : skinny_splits(ceil_div(cols, WFp8::KBLK), sh.S);
+  return fp8_part_offset(m, cols) + skinny_workspace_bytes(m, rows, S);
+}
+
+extern "C" int64_t sqx_fp8_linear_workspace_bytes(int64_t m, int64_t rows, int64_t cols) {
+  return fp8_ws_bytes(m, rows, cols, fp8_default_shape(m, rows, cols));
+}
+
+extern "C" int64_t sqx_fp8_skinny_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int splits) {
+  return fp8_ws_bytes(m, rows, cols, SkinnyShape{0, 2, 8, splits > 0 ? splits : 1, false});
+}
+
+// Shared by sqx_fp8_linear (sh from fp8_default_shape unless k_slices > 0) and sqx_fp8_skinny.
+static int fp8_linear_impl(const uint8_t* wt, const float* w_scale, const void* x, int act_dtype, void* y, int y_dtype,
+                           const void* bias, int64_t m, int64_t rows, int64_t cols, int k_slices, SkinnyShape sh,
+                           void* ws, int64_t ws_bytes, sqx_stream_t stream, const char* fn) {
   SQX_REQUIRE(fp8_float_dtype(act_dtype), SQX_E_ARG, "%s: unsupported activation dtype %d", fn, act_dtype);
   SQX_REQUIRE(y_dtype == SQX_DTYPE_BF16 || y_dtype == SQX_DTYPE_F32, SQX_E_ARG, "%s: output must be BF16 or F32", fn);
   SQX_REQUIRE(m >= 0 && rows > 0 && cols > 0 && cols % 8 == 0 && rows < (int64_t(1) << 31) && m < (int64_t(1) << 31),
               SQX_E_ARG, "%s: bad shape m=%lld rows=%lld cols=%lld (cols %% 8 == 0)", fn, (long long)m, (long long)rows,
               (long long)cols);
-  SQX_REQUIRE(ceil_div(cols, 64) * 1024 < (int64_t(1) << 31) && 64 * cols * 2 < (int64_t(1) << 31), SQX_E_ARG,
-              "%s: shape too large for 32-bit buffer offsets", fn);
+  SQX_REQUIRE(ceil_div(cols, 64) * 1024 < (int64_t(1) << 31) && 64 * cols * 2 < (int64_t(1) << 31) &&
+                  ceil_div(rows, 16) * ceil_div(cols, 64) * 1024 < (int64_t(1) << 31),
+              SQX_E_ARG, "%s: shape too large for 32-bit buffer offsets", fn);
   SQX_REQUIRE(k_slices <= 16, SQX_E_ARG, "%s: k_slices %d > 16", fn, k_slices);
+  if (!sh.gemv) {
+    SQX_REQUIRE(m <= 64 && y_dtype == SQX_DTYPE_BF16, SQX_E_ARG, "%s: the skinny kernel takes m <= 64 and a BF16 output",
+                fn);
+    SQX_REQUIRE(sh.variant == 0 && (sh.R == 2 || sh.R == 4) && sh.waves >= 1 && sh.waves <= kSkinnyMaxWaves && sh.S >= 1,
+                SQX_E_ARG, "%s: bad launch shape (tiles %d, waves %d, splits %d)", fn, sh.R, sh.waves, sh.S);
+  }
   if (m == 0) return SQX_OK;
   SQX_REQUIRE(wt && w_scale && x && y && ws, SQX_E_ARG, "%s: null pointer", fn);
-  SQX_REQUIRE(ws_bytes >= sqx_fp8_linear_workspace_bytes(m, cols), SQX_E_SPACE, "%s: workspace of %lld bytes, %lld needed",
-              fn, (long long)ws_bytes, (long long)sqx_fp8_linear_workspace_bytes(m, cols));
+  const int64_t need = fp8_ws_bytes(m, rows, cols, sh);
+  SQX_REQUIRE(ws_bytes >= need, SQX_E_SPACE, "%s: workspace of %lld bytes, %lld needed", fn, (long long)ws_bytes,
+              (long long)need);
   SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(ws) % 16 == 0, SQX_E_ARG,
               "%s: wt and the workspace must be 16-byte aligned", fn);
   SQX_REQUIRE(bias == nullptr || y_dtype == SQX_DTYPE_BF16, SQX_E_ARG, "%s: bias needs a BF16 output", fn);
@@ -390,9 +448,33 @@ extern "C" int sqx_fp8_linear(const uint8_t* wt, const float* w_scale, const voi
   SQX_LAUNCH_CHECK(fn);
   const WFp8::Args a{wt, w_scale, xs};
   const uint16_t* b16 = static_cast<const uint16_t*>(bias);
-  const hipError_t e = y_dtype == SQX_DTYPE_F32
-                           ? gemv_launch<ActBF16, WFp8, 4, 2, true>(a, vals, y, b16, nullptr, m, rows, cols, k_slices, s)
-                           : gemv_launch<ActBF16, WFp8, 4, 2, false>(a, vals, y, b16, nullptr, m, rows, cols, k_slices, s);
+  hipError_t e;
+  if (!sh.gemv) {
+    float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + fp8_part_offset(m, cols));
+    e = skinny_launch<ActBF16, WFp8>(a, vals, static_cast<uint16_t*>(y), b16, m, rows, cols, sh, part,
+                                     ws_bytes - fp8_part_offset(m, cols), s);
+  } else {
+    e = y_dtype == SQX_DTYPE_F32
+            ? gemv_launch<ActBF16, WFp8, 4, 2, true>(a, vals, y, b16, nullptr, m, rows, cols, k_slices, s)
+            : gemv_launch<ActBF16, WFp8, 4, 2, false>(a, vals, y, b16, nullptr, m, rows, cols, k_slices, s);
+  }
   SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return SQX_OK;
+}
+
+extern "C" int sqx_fp8_linear(const uint8_t* wt, const float* w_scale, const void* x, int act_dtype, void* y, int y_dtype,
+                              const void* bias, int64_t m, int64_t rows, int64_t cols, int k_slices, void* ws,
+                              int64_t ws_bytes, sqx_stream_t stream) {
+  SkinnyShape sh = fp8_default_shape(m, rows, cols);
+  if (k_slices > 0 || y_dtype != SQX_DTYPE_BF16) sh.gemv = true;
+  return fp8_linear_impl(wt, w_scale, x, act_dtype, y, y_dtype, bias, m, rows, cols, k_slices, sh, ws, ws_bytes, stream,
+                         "sqx_fp8_linear");
+}
+
+extern "C" int sqx_fp8_skinny(const uint8_t* wt, const float* w_scale, const void* x, int act_dtype, void* y,
+                              const void* bias, int64_t m, int64_t rows, int64_t cols, int tiles, int waves, int splits,
+                              void* ws, int64_t ws_bytes, sqx_stream_t stream) {
+  const SkinnyShape sh{0, tiles, waves, splits, false};
+  return fp8_linear_impl(wt, w_scale, x, act_dtype, y, SQX_DTYPE_BF16, bias, m, rows, cols, 0, sh, ws, ws_bytes, stream,
+                         "sqx_fp8_skinny");
 }

@@ -25,6 +25,10 @@
 //   W::kConstOffset, W::const_offset<A>()  the offset when it is the same for every group
 //   W::offset<A>(p, g)                     magic + zero point of group g (lane's weight row)
 //   W::scale(p, g)                         group scale (lane's weight row)
+// A policy whose codes decode to the weight values themselves (no offset, no group scale) declares
+// kPlainBlocks = true instead: its MFMAs chain straight into the output sums. A per-token factor
+// (kRowScale, row_scale) is applied in the epilogue as in the GEMV, and with K splits by the reduce,
+// which takes the factors from W::row_scales(args) [m] and W::out_scales(args) [n].
 #pragma once
 
 #include "sqx_gemv.h"
@@ -32,6 +36,11 @@
 namespace sqx {
 
 static constexpr int kSkinnyMaxWaves = 8;
+
+template <class W, class = void>
+struct plain_blocks : std::false_type {};
+template <class W>
+struct plain_blocks<W, std::void_t<decltype(W::kPlainBlocks)>> : std::integral_constant<bool, W::kPlainBlocks> {};
 // KiB of weights in flight per compute wave of the LDS-staged variant (a ring of this many k-blocks
 // over the wave's R tiles)
 #ifndef SQX_SKINNY_RING_KIB
@@ -57,6 +66,15 @@ __device__ __forceinline__ void skinny_block(const u32x4_t (&xv)[MCH][W::STEPS],
                                              f32x4_t (&yacc)[R][MCH]) {
   constexpr int NG = W::NG;
   constexpr int MPG = W::MPG;
+  if constexpr (plain_blocks<W>::value) {
+#pragma unroll
+    for (int i = 0; i < W::STEPS; ++i)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int c = 0; c < MCH; ++c) yacc[r][c] = A::mfma(xv[c][i], b[r][i], yacc[r][c]);
+    return;
+  }
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
     f32x4_t xs[MCH];
@@ -211,7 +229,10 @@ __global__ __launch_bounds__((64 * skinny_max_waves(MCH, R, W::NG, W::kConstOffs
           if (split_out) {
             static_cast<float*>(out)[((int64_t)blockIdx.y * M + m) * N + n] = v;
           } else {
-            v *= W::out_scale(wa, n);
+            if constexpr (has_row_scale<W>::value)
+              v = v * W::row_scale(wa, m) * W::out_scale(wa, n);
+            else
+              v *= W::out_scale(wa, n);
             if (bias) v += A::to_f32(bias[n]);
             static_cast<uint16_t*>(out)[(int64_t)m * N + n] = A::from_f32(v);
           }
@@ -482,11 +503,13 @@ __global__ __launch_bounds__(256 * KG) void skinny_lds_kernel(const typename W::
   }
 }
 
-// y[m, n] = act(sum over s in order of part[s][m][n] + bias[n]); four outputs per thread.
+// y[m, n] = act(sum over s in order of part[s][m][n] (* rs[m] * cs[n] when rs is given) + bias[n]);
+// four outputs per thread.
 template <class A>
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ part, int S, int M, int N,
                                                             const uint16_t* __restrict__ bias,
-                                                            uint16_t* __restrict__ y) {
+                                                            uint16_t* __restrict__ y, const float* __restrict__ rs,
+                                                            const float* __restrict__ cs) {
   const int64_t total = (int64_t)M * N;
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i >= total) return;
@@ -500,6 +523,11 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
       for (int j = 0; j < 4; ++j) v[j] += q[j];
     }
     const int n = static_cast<int>(i % N);
+    if (rs) {
+      const float r = rs[i / N];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = v[j] * r * cs[n + j];
+    }
     uint32_t lo, hi;
     float o[4];
 #pragma unroll
@@ -511,6 +539,7 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
     for (int64_t e = i; e < i + 4 && e < total; ++e) {
       float v = part[e];
       for (int s = 1; s < S; ++s) v += part[(int64_t)s * total + e];
+      if (rs) v = v * rs[e / N] * cs[e % N];
       if (bias) v += A::to_f32(bias[e % N]);
       y[e] = A::from_f32(v);
     }
@@ -644,7 +673,7 @@ hipError_t skinny_lds_launch(const typename W::Args& wa, const uint16_t* x, uint
   if (e != hipSuccess || !split || !reduce) return e;
   const int64_t quads = ceil_div(m * rows, 4);
   hipLaunchKernelGGL(skinny_reduce_kernel<A>, dim3(static_cast<unsigned>(ceil_div(quads, 256))), dim3(256), 0, stream,
-                     ws, S, M, N, bias, y);
+                     ws, S, M, N, bias, y, nullptr, nullptr);
   return hipGetLastError();
 }
 
@@ -657,9 +686,13 @@ hipError_t skinny_launch(const typename W::Args& wa, const uint16_t* x, uint16_t
                          int64_t rows, int64_t cols, SkinnyShape sh, float* ws, int64_t ws_bytes, hipStream_t stream,
                          bool reduce = true) {
   constexpr int KBLK = W::KBLK;
-  if (sh.variant == 1)
-    return skinny_lds_launch<A, W>(wa, x, y, bias, m, rows, cols, sh.R, sh.waves / 4, sh.S, ws, ws_bytes, stream,
-                                   reduce);
+  if (sh.variant == 1) {
+    if constexpr (KBLK == 128 && !has_row_scale<W>::value)
+      return skinny_lds_launch<A, W>(wa, x, y, bias, m, rows, cols, sh.R, sh.waves / 4, sh.S, ws, ws_bytes, stream,
+                                     reduce);
+    else
+      return hipErrorInvalidValue;
+  }
   if (m < 1 || m > 64 || sh.waves < 1 || sh.waves > kSkinnyMaxWaves || (sh.R != 2 && sh.R != 4) || sh.S < 1)
     return hipErrorInvalidValue;
   const int64_t T = ceil_div(rows, 16);
@@ -700,8 +733,14 @@ hipError_t skinny_launch(const typename W::Args& wa, const uint16_t* x, uint16_t
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !split || !reduce) return e;
   const int64_t quads = ceil_div(m * rows, 4);
+  const float* rs = nullptr;
+  const float* cs = nullptr;
+  if constexpr (has_row_scale<W>::value) {
+    rs = W::row_scales(wa);
+    cs = W::out_scales(wa);
+  }
   hipLaunchKernelGGL(skinny_reduce_kernel<A>, dim3(static_cast<unsigned>(ceil_div(quads, 256))), dim3(256), 0, stream,
-                     ws, S, M, N, bias, y);
+                     ws, S, M, N, bias, y, rs, cs);
   return hipGetLastError();
 }
 

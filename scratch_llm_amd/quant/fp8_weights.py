@@ -178,7 +178,8 @@ def fp8_linear_tiled(x: Tensor, tw: Fp8Tiled, bias: Tensor | None = None, *, out
     lib = _lib.load()
     ydt = torch.bfloat16 if out_dtype == torch.bfloat16 else torch.float32
     y = torch.empty(m, tw.rows, dtype=ydt, device=dev)
-    ws = torch.empty(max(int(lib.sqx_fp8_linear_workspace_bytes(m, k)) // 4, 4), dtype=torch.float32, device=dev)
+    ws = torch.empty(max(-(-int(lib.sqx_fp8_linear_workspace_bytes(m, tw.rows, k)) // 4), 4), dtype=torch.float32,
+                     device=dev)
     b = None
     if bias is not None and ydt == torch.bfloat16:
         b = bias.to(torch.bfloat16).contiguous()

@@ -100,8 +100,11 @@ def test_linear_reference_case(f8):
 
 
 @pytest.mark.parametrize("m", [1, 4, 16, 64, 100])
-@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (4096, 14336), (520, 1056)])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (4096, 14336), (520, 1056), (16392, 1056), (6152, 4096)])
 def test_linear_within_derived_bound(f8, m, n, k):
+    """Every launch the library picks: the GEMV, and for 2..64 rows with a bf16 output the skinny
+    kernel where its table says so (16392 rows: 1025 tiles, the last one half full, K with a half
+    k-block at the end; 6152 rows: 385 tiles; 4096 x 14336: K split 4)."""
     print_case("fp8 linear", m, n, k)
     g = torch.Generator().manual_seed(m * 7 + n + k)
     w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16)
@@ -115,6 +118,63 @@ def test_linear_within_derived_bound(f8, m, n, k):
         ref, bound = _ref_bound(x, codes, scale, b, out_dtype)
         err = np.abs(got.double().cpu().numpy() - ref)
         assert np.all(err <= bound), f"{out_dtype}: {float((err / bound).max()):.3f}x the bound"
+
+
+@pytest.mark.parametrize("m", [2, 7, 16, 33, 64])
+@pytest.mark.parametrize("n,k,tiles,waves,splits", [(520, 1056, 2, 8, 1), (520, 1056, 4, 3, 4), (1000, 4104, 4, 8, 8),
+                                                    (4096, 14336, 4, 8, 4), (16392, 512, 2, 4, 1), (100, 64, 4, 8, 2)])
+def test_skinny_launch_shapes_within_bound(f8, m, n, k, tiles, waves, splits):
+    """sqx_fp8_skinny at explicit launch shapes (tiles per workgroup, waves, K splits, including
+    more splits than a wave's k-blocks allow and ragged rows and K), with a bias, within the derived
+    bound; the split partials are scaled by the reduce kernel."""
+    from scratch_llm_amd import _lib
+
+    print_case("fp8 skinny", m, n, k, tiles, waves, splits)
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(m * 5 + n + k + splits)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    x[:, :: max(1, k // 37)] *= 20.0
+    bias = torch.randn(n, generator=g).to(torch.bfloat16)
+    codes, scale = f8.quantize_per_channel(w.to(DEV))
+    tw = f8.tile_fp8(codes, scale)
+    xd, bd = x.to(DEV), bias.to(DEV)
+    y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+    nb = int(lib.sqx_fp8_skinny_workspace_bytes(m, n, k, splits))
+    ws = torch.empty(-(-nb // 4), dtype=torch.float32, device=DEV)
+    _lib.check(lib.sqx_fp8_skinny(tw.wt.data_ptr(), tw.scale.data_ptr(), xd.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(),
+                                  bd.data_ptr(), m, n, k, tiles, waves, splits, ws.data_ptr(), nb,
+                                  _lib.stream_ptr(torch.device(DEV))), "sqx_fp8_skinny")
+    ref, bound = _ref_bound(x, codes, scale, bias, torch.bfloat16)
+    err = np.abs(y.double().cpu().numpy() - ref)
+    assert np.all(err <= bound), f"{float((err / bound).max()):.3f}x the bound"
+    # a workspace one split short is refused before any launch
+    if splits > 1 and nb > int(lib.sqx_fp8_skinny_workspace_bytes(m, n, k, 1)):
+        assert lib.sqx_fp8_skinny(tw.wt.data_ptr(), tw.scale.data_ptr(), xd.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(),
+                                  None, m, n, k, tiles, waves, splits, ws.data_ptr(), nb - 4,
+                                  _lib.stream_ptr(torch.device(DEV))) != 0
+
+
+def test_skinny_refusals(f8):
+    from scratch_llm_amd import _lib
+
+    lib = _lib.load()
+    codes, scale = f8.quantize_per_channel(torch.randn(64, 128, device=DEV))
+    tw = f8.tile_fp8(codes, scale)
+    x = torch.randn(65, 128, device=DEV).to(torch.bfloat16)
+    y = torch.empty(65, 64, dtype=torch.bfloat16, device=DEV)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=DEV)
+    s = _lib.stream_ptr(torch.device(DEV))
+
+    def call(m, tiles, waves, splits):
+        return lib.sqx_fp8_skinny(tw.wt.data_ptr(), tw.scale.data_ptr(), x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(),
+                                  None, m, 64, 128, tiles, waves, splits, ws.data_ptr(), ws.numel(), s)
+
+    assert call(65, 2, 8, 1) != 0  # more than 64 rows
+    assert call(4, 3, 8, 1) != 0  # tiles must be 2 or 4
+    assert call(4, 2, 9, 1) != 0  # at most 8 waves
+    assert call(4, 2, 8, 0) != 0  # at least one split
+    assert call(4, 2, 8, 1) == 0
 
 
 def test_linear_shapes_and_refusals(f8):
