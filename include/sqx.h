@@ -597,6 +597,20 @@ int sqx_rmsnorm(const void* x, const void* delta, const void* w, float eps, int6
 int sqx_rmsnorm_partials(const void* x, const float* part, int splits, const void* w, float eps, int64_t rows,
                          int64_t d, void* h_out, void* y, sqx_stream_t stream);
 
+/* The attention block's o projection of one decode row with the attention combine folded into its
+ * activation load (MultiHeadSelfAttention.forward's output projection, model.py:349-366, after the
+ * flash-decoding merge of the key-chunk partials): x is not an input but the merge of the partials that
+ * sqx_decode_attention_partials left in `part` for this row (B = 1) at the row's length lengths[0]
+ * (tmax the cache length given to that call), computed per wave for its own columns with the
+ * arithmetic of sqx_attn_partials_combine, so the result equals sqx_attn_partials_combine followed by
+ * sqx_int4_linear_residual (same k_slices) bit for bit. Residual epilogue, outputs and weight format as
+ * sqx_int4_linear_residual; m = 1, cols = H * 128, two k-blocks per wave (k_slices = cols / 256,
+ * the default for cols = 4096), at most 8 key chunks (sqx_attn_partials_chunk). */
+int sqx_int4_linear_attn_residual(const uint8_t* wt, const float* st, const float* part, const int* lengths,
+                                  int64_t tmax, const void* res, void* res_out, float* ss_out, const void* gain_next,
+                                  void* hg_out, int64_t m, int64_t rows, int64_t cols, int64_t group, int k_slices,
+                                  sqx_stream_t stream);
+
 /* RoPE of q and k (RotaryPositionalEmbedding.forward, model.py:205-224: interleaved pairs, position
  * lengths[b], fp32 cos/sin tables [rope_rows, hd/2]) and the cache write of SlotKVCache.write_decode
  * (kv_cache.py:194-205, at min(lengths[b], tmax - 1)). qkv: bf16 [B, (H + 2 Hkv) hd] laid out
@@ -623,6 +637,25 @@ int sqx_decode_attention(const void* q, const void* k_cache, const void* v_cache
 int sqx_decode_attention_rope(const void* qkv, const int* lengths, const float* cos_t, const float* sin_t,
                               int64_t rope_rows, void* k_cache, void* v_cache, int64_t B, int64_t H,
                               int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws, int64_t ws_bytes,
+                              sqx_stream_t stream);
+
+/* The first half of sqx_decode_attention[_rope][_fp8kv] on its own: the key-chunk partials (m, l, o)
+ * of every row and query head, written to ws, without the combine, for the o projection that merges
+ * them in its prologue (sqx_int4_linear_attn_residual). cos_t == NULL: q is [B, H, hd] as
+ * sqx_decode_attention takes it; otherwise qkv as sqx_decode_attention_rope (RoPE and the cache write
+ * included). k_scale == v_scale == NULL: bf16 cache; both given: E4M3 cache as
+ * sqx_decode_attention_fp8kv. Chunks of sqx_attn_partials_chunk(tmax) keys (at most 8 per head for
+ * the merge), workspace of sqx_attn_partials_workspace_bytes(B, H, tmax) bytes: o as fp32
+ * [B][H][nchunk][hd], then (m, l) as fp32 [B][H][nchunk][2]. */
+int sqx_attn_partials_chunk(int64_t tmax);
+int64_t sqx_attn_partials_workspace_bytes(int64_t B, int64_t H, int64_t tmax);
+int sqx_decode_attention_partials(const void* q, const int* lengths, const float* cos_t, const float* sin_t,
+                                  int64_t rope_rows, void* k_cache, void* v_cache, const float* k_scale,
+                                  const float* v_scale, int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax,
+                                  void* ws, int64_t ws_bytes, sqx_stream_t stream);
+/* The second half: out[b, h*hd + d] (bf16 [B, H * hd]) from the partials of
+ * sqx_decode_attention_partials (same B, H, tmax and lengths), merged in ascending chunk order. */
+int sqx_attn_partials_combine(const void* ws, const int* lengths, int64_t B, int64_t H, int64_t tmax, void* out,
                               sqx_stream_t stream);
 
 /* sqx_decode_attention_rope without a workspace argument and without any allocation. No counterpart in

@@ -73,6 +73,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sqx_int4_linear_silu": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p]),
     "sqx_int4_linear_residual": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                         _c_i, _c_p]),
+    "sqx_int4_linear_attn_residual": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64,
+                                              _c_i64, _c_i64, _c_i64, _c_i, _c_p]),
     "sqx_int4_linear_silu_residual": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
                                              _c_i64, _c_i, _c_p]),
     "sqx_int4_linear_rmsnorm_sumsq": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, ctypes.c_float, _c_p, _c_i64, _c_i64,
@@ -166,6 +168,14 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "sqx_attn_chunk": (_c_i, [_c_i64, _c_i64, _c_i64]),
     "sqx_attn_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "sqx_attn_partials_chunk": (_c_i, [_c_i64]),
+    "sqx_attn_partials_combine": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_attn_partials_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "sqx_decode_attention_partials": (
+        _c_i,
+        [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
+         _c_p],
+    ),
     "sqx_decode_attention": (
         _c_i,
         [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p],

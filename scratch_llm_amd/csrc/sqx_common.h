@@ -263,6 +263,13 @@ __device__ inline float wave_sum(float v) {
   return v;
 }
 
+// The merge of a head's key-chunk attention partials (m, l, o) (flash decoding): with M the maximum
+// of the merged chunks' m, a chunk's weight is a = 2^(m - M) (0 for a chunk whose keys were all
+// masked), then l_sum = fmaf(l, a, l_sum) and o_sum = fmaf(o, a, o_sum) in ascending chunk order, and
+// out = bf16(o_sum / l_sum). Every merge of chunk partials (the combine kernel, the o projection's
+// prologue) runs exactly these operations, so they agree bit for bit.
+__device__ inline float attn_chunk_weight(float m, float M) { return m == -INFINITY ? 0.0f : exp2f(m - M); }
+
 // The two bf16 values of a 32-bit word as fp32 (low half first).
 __device__ inline float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ inline float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }

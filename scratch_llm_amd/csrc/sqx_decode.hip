@@ -174,8 +174,14 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const uint16_t* __restrict
 // Workgroup (chunk, kh, b) takes keys [chunk*C, chunk*C + C) and writes, per query head, the fp32
 // partial (m, l, o[hd]) of that range: m the maximum score (log2 units: scores are scaled by
 // log2(e) / sqrt(hd) so that the exponentials are exp2), l = sum 2^(s - m), o = sum 2^(s - m) v.
-// The 4 waves take alternate blocks of 16 keys (the kernel and its layouts are described at
-// attn_partial_mfma_kernel below); the waves' partials are merged at the end. hd must be 128.
+// The NWV waves (4, or 8 for the o projection's fused merge) take alternate blocks of 16 keys (the
+// kernel and its layouts are described at attn_partial_mfma_kernel below); the waves' partials are
+// merged at the end. hd must be 128.
+//
+// Partial layout in the workspace (16-byte aligned rows): o at po[((b*H + h)*nchunk + c)*hd + d], then
+// (m, l) at pml[((b*H + h)*nchunk + c)*2 + {0, 1}] with pml = po + B*H*nchunk*hd. The merge of a
+// head's chunks follows attn_chunk_weight (sqx_common.h) in ascending chunk order, shared by
+// attn_combine_kernel and the o projection's prologue (kProAttnCombine in sqx_gemv.h).
 // ---------------------------------------------------------------------------------------------
 constexpr int kHd = 128;
 constexpr int kKeysPerStep = 16;
@@ -254,16 +260,17 @@ __device__ inline u32x4_t e4m3x8_to_bf16(u32x2v_t c) {
 // holds value rows base + 4u + kl, each lane 8 dims, fp32 products and sums as above). This moves
 // the dot products and most of the softmax off the VALU, which bounds the kernel above at large
 // batch (every lane worked every head's scores, 4 fdot2 and 4 row reductions a key).
-template <int G, bool ROPE, bool KV8>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_partial_mfma_kernel(const uint16_t* __restrict__ q, uint8_t* __restrict__ kc,
+template <int G, bool ROPE, bool KV8, int NWV>
+__global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_partial_mfma_kernel(const uint16_t* __restrict__ q, uint8_t* __restrict__ kc,
                                                                 uint8_t* __restrict__ vc, const int* __restrict__ lengths,
                                                                 const float* __restrict__ cos_t,
                                                                 const float* __restrict__ sin_t,
                                                                 const float* __restrict__ kscale,
                                                                 const float* __restrict__ vscale, int rope_rows, int H,
                                                                 int Hkv, int tmax, int chunk, int nchunk, float qscale,
-                                                                float* __restrict__ part) {
+                                                                float* __restrict__ po, float* __restrict__ pml) {
   static_assert(G >= 1 && G <= 16, "query heads are the 16 columns of the score tile");
+  static_assert(NWV == 4 || NWV == 8, "4 or 8 waves per workgroup");
   using R = KvRow<KV8>;
   using Row = typename R::T;          // a lane's 8 dims of a cache row: 16 bytes bf16, 8 bytes E4M3
   constexpr uint32_t ES = R::kBytes;  // bytes per element
@@ -271,9 +278,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kl = lane >> 4, dl = lane & 15;  // value layout: key group, 8-dim slice; score layout: key quad, head
   const int t0 = ch * chunk;
-  // the 4 waves take alternate 16-key blocks of the chunk: the workgroup streams one region
+  // the NWV waves take alternate 16-key blocks of the chunk: the workgroup streams one region
   const int ws = t0 + wave * kKeysPerStep;
-  constexpr int kWaveStride = 4 * kKeysPerStep;
+  constexpr int kWaveStride = NWV * kKeysPerStep;
   const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd * ES;  // bytes
   const int len = max(lengths[b], 0);
   const int L = min(len + 1, tmax);
@@ -281,10 +288,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   if (t0 >= L) return;  // the combine reads only chunks below L
   const int we = min(t0 + chunk, L);
 
-  __shared__ float sm[4][G], sl[4][G];
-  __shared__ float so[4][G][kHd];
-  __shared__ __attribute__((aligned(16))) float sp[4][16][G < 4 ? 4 : G];  // per wave: p[key][head]
-  __shared__ __attribute__((aligned(16))) float sa[4][G < 4 ? 4 : G];      // per wave: the step's rescale
+  __shared__ float sm[NWV][G], sl[NWV][G];
+  __shared__ float so[NWV][G][kHd];
+  __shared__ __attribute__((aligned(16))) float sp[NWV][16][G < 4 ? 4 : G];  // per wave: p[key][head]
+  __shared__ __attribute__((aligned(16))) float sa[NWV][G < 4 ? 4 : G];      // per wave: the step's rescale
 
   // E4M3 rows: the K scale folds into the query's scale, the V scale multiplies the partial
   const float ks = KV8 ? kscale[kh] : 1.0f;
@@ -487,30 +494,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
       for (int j = 0; j < 8; ++j) so[wave][g][dl * 8 + j] = o[g][j];
   }
   __syncthreads();
-  // merge the 4 waves: thread (g, dd) writes element dd of head g's partial
-  for (int idx = threadIdx.x; idx < G * kHd; idx += 256) {
+  // merge the NWV waves: thread (g, dd) writes element dd of head g's partial
+  for (int idx = threadIdx.x; idx < G * kHd; idx += NWV * 64) {
     const int g = idx / kHd, dd = idx % kHd;
-    const float M = fmaxf(fmaxf(sm[0][g], sm[1][g]), fmaxf(sm[2][g], sm[3][g]));
+    float M = sm[0][g];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) M = fmaxf(M, sm[w][g]);
     float lsum = 0.0f, osum = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < NWV; ++w) {
       const float a = sm[w][g] == -INFINITY ? 0.0f : exp2f(sm[w][g] - M);
       lsum = fmaf(sl[w][g], a, lsum);
       osum = fmaf(so[w][g][dd], a, osum);
     }
-    float* pp = part + ((static_cast<int64_t>(b) * H + kh * G + g) * nchunk + ch) * (kHd + 2);
-    if (dd == 0) {
-      pp[0] = M;
-      pp[1] = lsum;
-    }
-    pp[2 + dd] = KV8 ? osum * vs : osum;
+    const int64_t row = (static_cast<int64_t>(b) * H + kh * G + g) * nchunk + ch;
+    if (dd == 0) *reinterpret_cast<f32x2_t*>(pml + row * 2) = f32x2_t{M, lsum};
+    po[row * kHd + dd] = KV8 ? osum * vs : osum;
   }
 }
 
 // out[b, h*hd + d] = bf16(sum_c 2^(m_c - M) o_c[d] / sum_c 2^(m_c - M) l_c) over the chunks c that
-// hold keys of row b. Row layout [B, H*hd] is the (B, 1, H*hd) view that o_proj takes (model.py:365).
-// One workgroup of 256 threads per (head, row): the chunk maxima and weights are formed in parallel
-// (one chunk per thread), then two halves of the workgroup sum alternate chunks of o.
+// hold keys of row b, merged as attn_chunk_weight describes, in ascending chunk order. Row layout [B, H*hd] is the
+// (B, 1, H*hd) view that o_proj takes (model.py:365). One workgroup of 128 threads per (head, row),
+// one output element per thread.
 constexpr int kMaxChunks = 1024;
 
 __device__ inline float wave_max(float v) {
@@ -519,43 +525,55 @@ __device__ inline float wave_max(float v) {
   return v;
 }
 
-__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part, const int* __restrict__ lengths,
-                                                           int H, int tmax, int chunk, int nchunk,
-                                                           uint16_t* __restrict__ out) {
-  __shared__ float sa[kMaxChunks];
-  __shared__ float red[2][4];
-  __shared__ float so[kHd];
-  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// Every load is requested at the start: the o values of the first kCombineBatch chunks (past nchunk the
+// buffer resource reads zero) before the row's length is known, one chunk's (m, l) per thread. The
+// chunk weights go through LDS; the sums then run over the chunks in ascending order with the results
+// past the length dropped by selects (those chunks were never written).
+constexpr int kCombineBatch = 32;
+__global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ po, const float* __restrict__ pml,
+                                                           const int* __restrict__ lengths, int H, int tmax, int chunk,
+                                                           int nchunk, uint16_t* __restrict__ out) {
+  __shared__ float sa[kMaxChunks + kCombineBatch], sl[kMaxChunks + kCombineBatch];  // a batch may read past `used`
+  __shared__ float red[2];
+  const int h = blockIdx.x, b = blockIdx.y, dd = threadIdx.x, lane = dd & 63, wave = dd >> 6;
+  const int64_t row0 = (static_cast<int64_t>(b) * H + h) * nchunk;
+  const rsrc_t ro = make_rsrc(po + row0 * kHd, static_cast<uint32_t>(nchunk) * kHd * 4u);
+  float ov[kCombineBatch];
+#pragma unroll
+  for (int i = 0; i < kCombineBatch; ++i)
+    ov[i] = __builtin_bit_cast(float, bload32(ro, static_cast<uint32_t>(i * kHd + dd) * 4u, 0u));
+  const f32x2_t* ml = reinterpret_cast<const f32x2_t*>(pml + row0 * 2);
   const int L = min(max(lengths[b], 0) + 1, tmax);
   const int used = (L + chunk - 1) / chunk;
-  const float* base = part + (static_cast<int64_t>(b) * H + h) * nchunk * (kHd + 2);
   float mx = -INFINITY;
-  for (int c = tid; c < used; c += 256) {
-    const float m = base[c * (kHd + 2)];
-    sa[c] = m;
-    mx = fmaxf(mx, m);
+  for (int c = dd; c < used; c += kHd) {
+    const f32x2_t v = ml[c];
+    sa[c] = v[0];
+    sl[c] = v[1];
+    mx = fmaxf(mx, v[0]);
   }
   mx = wave_max(mx);
-  if (lane == 0) red[0][wave] = mx;
+  if (lane == 0) red[wave] = mx;
   __syncthreads();
-  const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-  float ls = 0.0f;
-  for (int c = tid; c < used; c += 256) {
-    const float a = sa[c] == -INFINITY ? 0.0f : exp2f(sa[c] - M);
-    sa[c] = a;
-    ls = fmaf(base[c * (kHd + 2) + 1], a, ls);
+  const float M = fmaxf(red[0], red[1]);
+  for (int c = dd; c < used; c += kHd) sa[c] = attn_chunk_weight(sa[c], M);
+  __syncthreads();
+  float ls = 0.0f, os = 0.0f;
+  for (int c0 = 0; c0 < used; c0 += kCombineBatch) {
+    if (c0 > 0) {
+#pragma unroll
+      for (int i = 0; i < kCombineBatch; ++i)
+        ov[i] = __builtin_bit_cast(float, bload32(ro, static_cast<uint32_t>((c0 + i) * kHd + dd) * 4u, 0u));
+    }
+#pragma unroll
+    for (int i = 0; i < kCombineBatch; ++i) {
+      const bool u = c0 + i < used;
+      const float a = sa[c0 + i];
+      ls = u ? fmaf(sl[c0 + i], a, ls) : ls;
+      os = u ? fmaf(ov[i], a, os) : os;
+    }
   }
-  ls = wave_sum(ls);
-  if (lane == 0) red[1][wave] = ls;
-  __syncthreads();
-  const float lsum = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
-  const int dd = tid & (kHd - 1), half = tid >> 7;
-  float os = 0.0f;
-#pragma unroll 8
-  for (int c = half; c < used; c += 2) os = fmaf(base[c * (kHd + 2) + 2 + dd], sa[c], os);
-  if (half == 1) so[dd] = os;
-  __syncthreads();
-  if (half == 0) out[(static_cast<int64_t>(b) * H + h) * kHd + dd] = f32_to_bf16_bits((os + so[dd]) / lsum);
+  out[(static_cast<int64_t>(b) * H + h) * kHd + dd] = f32_to_bf16_bits(os / ls);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -785,10 +803,30 @@ extern "C" int64_t sqx_attn_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, i
   return B * H * ceil_div(tmax, sqx_attn_chunk(B, Hkv, tmax)) * (kHd + 2) * 4;
 }
 
+// Keys per workgroup of the partials that the o projection merges in its prologue
+// (sqx_decode_attention_partials): 8 waves per workgroup and at most kFoldMaxChunks chunks per head,
+// the smallest multiple of 128 keys (one 16-key block per wave) that gets there. Every workgroup of the
+// o projection merges every head's chunks, so few chunks keep that merge cheap; eight waves with the
+// two-block register ring keep a chunk of 256 keys per workgroup in flight.
+constexpr int kFoldMaxChunks = 8;
+constexpr int kFoldWaves = 8;
+extern "C" int sqx_attn_partials_chunk(int64_t tmax) {
+  if (tmax <= 0) return 0;
+  const int64_t step = kFoldWaves * kKeysPerStep;
+  return static_cast<int>(std::max<int64_t>(step, ceil_div(ceil_div(tmax, kFoldMaxChunks), step) * step));
+}
+
+extern "C" int64_t sqx_attn_partials_workspace_bytes(int64_t B, int64_t H, int64_t tmax) {
+  if (B <= 0 || H <= 0 || tmax <= 0) return 0;
+  return B * H * ceil_div(tmax, sqx_attn_partials_chunk(tmax)) * (kHd + 2) * 4;
+}
+
+// chunk > 0 with nwv = 8 and no combine: the partials for the o projection's merge; otherwise the
+// library's chunk with 4 waves per workgroup and the combine kernel.
 static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, const int* lengths, const float* cos_t,
                                  const float* sin_t, int64_t rope_rows, const float* kscale, const float* vscale,
                                  int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws,
-                                 int64_t ws_bytes, sqx_stream_t stream, const char* fn) {
+                                 int64_t ws_bytes, sqx_stream_t stream, const char* fn, bool partials_only = false) {
   const bool rope = cos_t != nullptr;
   const bool kv8 = kscale != nullptr;
   SQX_REQUIRE(!kv8 || vscale != nullptr, SQX_E_ARG, "%s: null V scale", fn);
@@ -802,12 +840,14 @@ static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, co
   SQX_REQUIRE(!rope || (sin_t != nullptr && rope_rows > 0 && rope_rows < (int64_t(1) << 31)), SQX_E_ARG,
               "%s: bad RoPE tables", fn);
   if (B == 0) return SQX_OK;
-  SQX_REQUIRE(q && k_cache && v_cache && lengths && out && ws, SQX_E_ARG, "%s: null pointer", fn);
-  SQX_REQUIRE(ws_bytes >= sqx_attn_workspace_bytes(B, H, Hkv, tmax), SQX_E_SPACE, "%s: workspace of %lld bytes, %lld needed",
-              fn, (long long)ws_bytes, (long long)sqx_attn_workspace_bytes(B, H, Hkv, tmax));
+  SQX_REQUIRE(q && k_cache && v_cache && lengths && ws && (out || partials_only), SQX_E_ARG, "%s: null pointer", fn);
+  const int64_t need = partials_only ? sqx_attn_partials_workspace_bytes(B, H, tmax)
+                                     : sqx_attn_workspace_bytes(B, H, Hkv, tmax);
+  SQX_REQUIRE(ws_bytes >= need, SQX_E_SPACE, "%s: workspace of %lld bytes, %lld needed", fn, (long long)ws_bytes,
+              (long long)need);
   SQX_REQUIRE(al16(q) && al16(k_cache) && al16(v_cache) && al16(ws), SQX_E_ARG,
               "%s: q, caches and workspace must be 16-byte aligned", fn);
-  const int chunk = sqx_attn_chunk(B, Hkv, tmax);
+  const int chunk = partials_only ? sqx_attn_partials_chunk(tmax) : sqx_attn_chunk(B, Hkv, tmax);
   const int nchunk = static_cast<int>(ceil_div(tmax, chunk));
   SQX_REQUIRE(nchunk <= kMaxChunks, SQX_E_ARG, "%s: %d key chunks of %d (at most %d)", fn, nchunk, chunk, kMaxChunks);
   hipStream_t s = as_stream(stream);
@@ -816,12 +856,20 @@ static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, co
   const auto* qp = static_cast<const uint16_t*>(q);
   auto* kp = static_cast<uint8_t*>(k_cache);
   auto* vp = static_cast<uint8_t*>(v_cache);
-  float* w = static_cast<float*>(ws);
+  float* po = static_cast<float*>(ws);
+  float* pml = po + B * H * nchunk * kHd;
   const int iH = static_cast<int>(H), iK = static_cast<int>(Hkv), iT = static_cast<int>(tmax);
   const int rr = static_cast<int>(rope_rows);
-#define SQX_ATTN_M(G_, R_, K8_)                                                                                      \
-  hipLaunchKernelGGL((attn_partial_mfma_kernel<G_, R_, K8_>), grid, dim3(256), 0, s, qp, kp, vp, lengths, cos_t, sin_t, \
-                     kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, w)
+#define SQX_ATTN_M(G_, R_, K8_)                                                                                     \
+  do {                                                                                                             \
+    if (partials_only)                                                                                             \
+      hipLaunchKernelGGL((attn_partial_mfma_kernel<G_, R_, K8_, kFoldWaves>), grid, dim3(kFoldWaves * 64), 0, s, qp, \
+                         kp, vp, lengths, cos_t, sin_t, kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, po,  \
+                         pml);                                                                                     \
+    else                                                                                                           \
+      hipLaunchKernelGGL((attn_partial_mfma_kernel<G_, R_, K8_, 4>), grid, dim3(256), 0, s, qp, kp, vp, lengths,    \
+                         cos_t, sin_t, kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, po, pml);             \
+  } while (0)
 #define SQX_ATTN_MG(R_, K8_)                      \
   switch (G) {                                    \
     case 1: SQX_ATTN_M(1, R_, K8_); break;        \
@@ -838,8 +886,37 @@ static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, co
 #undef SQX_ATTN_MG
 #undef SQX_ATTN_M
   SQX_LAUNCH_CHECK(fn);
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(B)), dim3(256), 0, s, w,
-                     lengths, iH, iT, chunk, nchunk, static_cast<uint16_t*>(out));
+  if (partials_only) return SQX_OK;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(B)), dim3(kHd), 0, s, po,
+                     pml, lengths, iH, iT, chunk, nchunk, static_cast<uint16_t*>(out));
+  SQX_LAUNCH_CHECK(fn);
+  return SQX_OK;
+}
+
+extern "C" int sqx_decode_attention_partials(const void* q, const int* lengths, const float* cos_t, const float* sin_t,
+                                             int64_t rope_rows, void* k_cache, void* v_cache, const float* k_scale,
+                                             const float* v_scale, int64_t B, int64_t H, int64_t Hkv, int64_t hd,
+                                             int64_t tmax, void* ws, int64_t ws_bytes, sqx_stream_t stream) {
+  const char* fn = "sqx_decode_attention_partials";
+  SQX_REQUIRE((k_scale == nullptr) == (v_scale == nullptr), SQX_E_ARG, "%s: give both scales or neither", fn);
+  return decode_attention_impl(q, k_cache, v_cache, lengths, cos_t, sin_t, rope_rows, k_scale, v_scale, B, H, Hkv, hd,
+                               tmax, nullptr, ws, ws_bytes, stream, fn, true);
+}
+
+extern "C" int sqx_attn_partials_combine(const void* ws, const int* lengths, int64_t B, int64_t H, int64_t tmax,
+                                         void* out, sqx_stream_t stream) {
+  const char* fn = "sqx_attn_partials_combine";
+  SQX_REQUIRE(B >= 0 && B < 65536 && H > 0 && H < 65536 && tmax > 0 && tmax < (int64_t(1) << 30), SQX_E_ARG,
+              "%s: bad shape", fn);
+  if (B == 0) return SQX_OK;
+  SQX_REQUIRE(ws && lengths && out, SQX_E_ARG, "%s: null pointer", fn);
+  const int chunk = sqx_attn_partials_chunk(tmax);
+  const int nchunk = static_cast<int>(ceil_div(tmax, chunk));
+  const float* po = static_cast<const float*>(ws);
+  const float* pml = po + B * H * nchunk * kHd;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(H), static_cast<unsigned>(B)), dim3(kHd), 0,
+                     as_stream(stream), po, pml, lengths, static_cast<int>(H), static_cast<int>(tmax), chunk, nchunk,
+                     static_cast<uint16_t*>(out));
   SQX_LAUNCH_CHECK(fn);
   return SQX_OK;
 }

@@ -110,7 +110,16 @@ struct has_row_scale<W, std::void_t<decltype(W::kRowScale)>> : std::integral_con
 // rotated and stored at cache row min(lengths[0], tmax - 1) of k_cache [kn / 128, tmax, 128]
 // (kv_cache.py:194-205); the rest are v, stored there in v_cache. Wave 0 requests the length with
 // its activation slice and the pair's cos / sin behind it, so the epilogue finds them in registers.
-enum { kProPlain = 0, kProResNorm = 1, kProSiluGate = 2, kProNormSum = 3, kProScaleSum = 4 };
+// kProAttnCombine (one row, two k-blocks per wave, 128-column blocks): x is the attention output of
+//                the decode step, formed here from the key-chunk partials that
+//                sqx_decode_attention_partials left (o then (m, l) per head and chunk, at most
+//                kAttnFoldChunks chunks of pa.chunk keys; the row attends min(lengths[0] + 1, tmax)
+//                keys): each lane merges 4 columns of its wave's slice (one head), as the combine
+//                kernel does (attn_chunk_weight, ascending chunks, bf16(o / l)), so the result is
+//                bit-identical to running that kernel first. Every load of it is unconditional (chunks
+//                past nchunk read past the buffer resource: zero, no traffic).
+enum { kProPlain = 0, kProResNorm = 1, kProSiluGate = 2, kProNormSum = 3, kProScaleSum = 4, kProAttnCombine = 5 };
+static constexpr int kAttnFoldChunks = 8;
 static constexpr int kProMaxRows = 8;
 static constexpr int kNormSumMax = 512;  // tiles of sums of squares a kProNormSum prologue reads (K <= 8192)
 
@@ -133,6 +142,8 @@ struct ProArgs {
   uint16_t* q_out;            // RKV: rotated q [qn]
   uint16_t* k_cache;          // RKV: [kn / 128, tmax, 128] bf16
   uint16_t* v_cache;
+  const float* part;          // kProAttnCombine: the attention partials (o [K/128][nchunk][128], then (m, l))
+  int nchunk, chunk;          // kProAttnCombine: chunks per head and keys per chunk (tmax, lengths as RKV)
 };
 
 template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32, int PRO = kProPlain, int ONE = 0,
@@ -143,8 +154,10 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
                                                     int kbw, const ProArgs pa) {
   static_assert(PRO == kProPlain || (XLDS && MCH == 1), "activation prologues need the LDS copy");
   static_assert(ONE == 0 || (XLDS && MCH == 1 && U == 4), "the one-row form reads four-block rounds from LDS");
-  static_assert(ONE < 2 || PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate || PRO == kProScaleSum,
+  static_assert(ONE < 2 || PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate || PRO == kProScaleSum ||
+                    PRO == kProAttnCombine,
                 "a prologue over the whole row needs the workgroup's copy of the activations");
+  static_assert(PRO != kProAttnCombine || (ONE >= 2 && W::KBLK == 128), "the attention merge runs in each wave's slice");
   static_assert((PRO != kProNormSum && PRO != kProScaleSum) || ONE >= 2,
                 "the norm from tile sums runs in each wave's own slice");
   static_assert(!RES || ONE != 0, "the residual epilogue is a one-row form");
@@ -208,10 +221,29 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
   [[maybe_unused]] u32x4_t ssv[PRO == kProNormSum ? kNormSumMax / 256 : 1];
   [[maybe_unused]] __shared__ float row_scale_lds;                              // kProScaleSum: r (wave 0)
   [[maybe_unused]] __shared__ __attribute__((aligned(16))) float ss_lds[PRO == kProScaleSum ? kNormSumMax : 4];
+  // kProAttnCombine: this lane's head (kb0 + lane / 32, two k-blocks per wave) and 4 dims; the (m, l)
+  // pairs of chunks 2i, 2i+1 and the o values of each chunk, requested ahead of the weights
+  [[maybe_unused]] u32x4_t cml[PRO == kProAttnCombine ? kAttnFoldChunks / 2 : 1];
+  [[maybe_unused]] u32x4_t cov[PRO == kProAttnCombine ? kAttnFoldChunks : 1];
+  [[maybe_unused]] int clen = 0;
+  if constexpr (PRO == kProAttnCombine) {
+    const int H = K / KBLK, nc = pa.nchunk;
+    const int h = kb0 + (lane >> 5), d0 = 4 * (lane & 31);
+    constexpr uint32_t kPast = 0x40000000u;  // past both resources: the load returns zero
+    const rsrc_t ro = make_rsrc(pa.part, (uint32_t)(H * nc * KBLK) * 4u);
+    const rsrc_t rml = make_rsrc(pa.part + (int64_t)H * nc * KBLK, (uint32_t)(H * nc) * 8u);
+    clen = static_cast<int>(bload32(make_rsrc(pa.lengths, 4u), 0u, 0u));
+#pragma unroll
+    for (int i = 0; i < kAttnFoldChunks / 2; ++i)
+      cml[i] = bload128(rml, 2 * i < nc ? (uint32_t)(h * nc + 2 * i) * 8u : kPast, 0u);
+#pragma unroll
+    for (int c = 0; c < kAttnFoldChunks; ++c)
+      cov[c] = bload128(ro, c < nc ? (uint32_t)((h * nc + c) * KBLK + d0) * 4u : kPast, 0u);
+  }
   if constexpr (ONE >= 2) {
 #pragma unroll
     for (int i = 0; i < kXw; ++i)
-      if (i < nx) xw[i] = bload128(xr, (uint32_t)(kb0 * KBLK + 8 * (lane + 64 * i)) * 2u, 0u);
+      if (PRO != kProAttnCombine && i < nx) xw[i] = bload128(xr, (uint32_t)(kb0 * KBLK + 8 * (lane + 64 * i)) * 2u, 0u);
     if constexpr (PRO == kProSiluGate) {  // xw holds the gate half [0, K) of the row, gw the up half
 #pragma unroll
       for (int i = 0; i < kXw; ++i)
@@ -242,6 +274,9 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) W::load(wc, min(kb0 + u, kb1 - 1), w[u], p[u]);
+    // the attention merge waits for its partials: keep the scheduler from hoisting it above the
+    // weight requests
+    if constexpr (PRO == kProAttnCombine) __builtin_amdgcn_sched_barrier(0);
   } else {
     if (kb0 < kb1) load_round(kb0, w, p);
   }
@@ -286,9 +321,46 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
           }
         }
     }
+    if constexpr (PRO == kProAttnCombine) {
+      // the merge of the head's chunks below the row's length, as attn_combine_kernel does
+      const int L = min(max(clen, 0) + 1, pa.tmax);
+      const int used = (L + pa.chunk - 1) / pa.chunk;  // <= nchunk
+      // each element through a scalar: hipcc's bit_cast of a vector element reads element 0
+      auto mof = [&](int c) {
+        const uint32_t v = cml[c >> 1][2 * (c & 1)];
+        return __builtin_bit_cast(float, v);
+      };
+      auto lof = [&](int c) {
+        const uint32_t v = cml[c >> 1][2 * (c & 1) + 1];
+        return __builtin_bit_cast(float, v);
+      };
+      // Every chunk's values are used and the results past `used` dropped by selects (chunks past the
+      // length were never written): a branch would let the compiler sink the loads into it, behind
+      // the weights, and wait for those as well.
+      float M = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kXw; ++i)
-      if (i < nx) *reinterpret_cast<u32x4_t*>(xwave + 8 * (lane + 64 * i)) = xw[i];
+      for (int c = 0; c < kAttnFoldChunks; ++c) M = c < used ? fmaxf(M, mof(c)) : M;
+      float ls = 0.0f, os[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < kAttnFoldChunks; ++c) {
+        const bool u = c < used;
+        const float a = attn_chunk_weight(mof(c), M);
+        ls = u ? fmaf(lof(c), a, ls) : ls;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t oj = cov[c][j];
+          os[j] = u ? fmaf(__builtin_bit_cast(float, oj), a, os[j]) : os[j];
+        }
+      }
+      uint32_t b[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = f32_to_bf16_bits(os[j] / ls);
+      *reinterpret_cast<u32x2v_t*>(xwave + 4 * lane) = u32x2v_t{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
+    } else {
+#pragma unroll
+      for (int i = 0; i < kXw; ++i)
+        if (i < nx) *reinterpret_cast<u32x4_t*>(xwave + 8 * (lane + 64 * i)) = xw[i];
+    }
     // LDS operations of one wave execute in issue order; only the compiler must not move the
     // fragment reads above the stores
     __builtin_amdgcn_wave_barrier();
@@ -653,7 +725,8 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     constexpr bool kOneOk = has_sum_offset<W>::value && U1 == 4 && !YF32;
     int one_mode = 0;
     if (kOneOk && M == 1 && xlds)
-      one_mode = ((PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate || PRO == kProScaleSum) &&
+      one_mode = ((PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate || PRO == kProScaleSum ||
+                   PRO == kProAttnCombine) &&
                   colscale == nullptr &&
                   kbw <= kOneMaxKbw)
                      ? 2
@@ -661,7 +734,11 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     if (PRO != kProPlain && (!xlds || m > kProMaxRows || cols % 8 != 0))
       return hipErrorNotSupported;  // the caller checks first
     // one-row forms only: the norm from tile sums, the residual epilogue
-    if (((PRO == kProNormSum || PRO == kProScaleSum) && one_mode != 2) || (RES && one_mode == 0))
+    if (((PRO == kProNormSum || PRO == kProScaleSum || PRO == kProAttnCombine) && one_mode != 2) ||
+        (RES && one_mode == 0))
+      return hipErrorNotSupported;
+    // the attention merge: two 128-column k-blocks per wave (4 columns a lane, one head each)
+    if (PRO == kProAttnCombine && (kbw != 2 || KBLK != 128 || K % 128 != 0 || pa.nchunk > kAttnFoldChunks))
       return hipErrorNotSupported;
     // the RoPE epilogue: the one-row form 2 with wave 0 finishing each tile (grids under 1024 tiles)
     if (RKV && (one_mode != 2 || T >= 1024)) return hipErrorNotSupported;
@@ -675,17 +752,17 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
             } else {
               if (ktail) SQX_GEMV1(1, U1, true, true, lds, 2); else SQX_GEMV1(1, U1, false, true, lds, 2);
             }
-          } else if constexpr (PRO == kProNormSum || PRO == kProSiluGate) {
+          } else if constexpr (PRO == kProNormSum || PRO == kProSiluGate || PRO == kProAttnCombine) {
             if (ktail) SQX_GEMV1(1, U1, true, true, lds, 2); else SQX_GEMV1(1, U1, false, true, lds, 2);
           }
         } else {
           const size_t lds = red + gemv_xlds_bytes(M, KB, KBLK);
-          if constexpr (PRO != kProNormSum && PRO != kProScaleSum) {
+          if constexpr (PRO != kProNormSum && PRO != kProScaleSum && PRO != kProAttnCombine) {
             if (ktail) SQX_GEMV1(1, U1, true, true, lds, 1); else SQX_GEMV1(1, U1, false, true, lds, 1);
           }
         }
       }
-    } else if constexpr (RES || PRO == kProNormSum || PRO == kProScaleSum) {
+    } else if constexpr (RES || PRO == kProNormSum || PRO == kProScaleSum || PRO == kProAttnCombine) {
       return hipErrorNotSupported;
     } else if (PRO != kProPlain || xlds) {
       const size_t lds = red + gemv_xlds_bytes(M, KB, KBLK);

@@ -1203,6 +1203,44 @@ extern "C" int sqx_int4_linear_residual(const uint8_t* wt, const float* st, cons
   return SQX_OK;
 }
 
+extern "C" int sqx_int4_linear_attn_residual(const uint8_t* wt, const float* st, const float* part, const int* lengths,
+                                             int64_t tmax, const void* res, void* res_out, float* ss_out,
+                                             const void* gain_next, void* hg_out, int64_t m, int64_t rows,
+                                             int64_t cols, int64_t group, int k_slices, sqx_stream_t stream) {
+  const char* fn = "sqx_int4_linear_attn_residual";
+  int rc = int4_pro_check(wt, st, part, res_out, m, rows, cols, group, k_slices, fn);
+  if (rc == SQX_OK) rc = int4_res_check(res, res_out, ss_out, gain_next, hg_out, m, fn);
+  if (rc != SQX_OK) return rc;
+  SQX_REQUIRE(lengths != nullptr && tmax > 0 && tmax < (int64_t(1) << 30), SQX_E_ARG, "%s: null lengths or bad tmax", fn);
+  SQX_REQUIRE(cols % 128 == 0, SQX_E_ARG, "%s: in_features=%lld is not a whole number of 128-dim heads", fn,
+              (long long)cols);
+  const int chunk = sqx_attn_partials_chunk(tmax);
+  const int64_t nchunk = ceil_div(tmax, chunk);
+  SQX_REQUIRE(nchunk <= kAttnFoldChunks, SQX_E_ARG, "%s: %lld key chunks (at most %d)", fn, (long long)nchunk,
+              kAttnFoldChunks);
+  const int64_t KB = cols / 128;
+  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols) : k_slices;
+  if (nw > KB) nw = static_cast<int>(KB);
+  SQX_REQUIRE(ceil_div(KB, nw) == 2 && nw <= 16, SQX_E_ARG,
+              "%s: the merge prologue runs two k-blocks per wave: %lld k-blocks over %d waves (k_slices)", fn,
+              (long long)KB, nw);
+  ProArgs pa{};
+  pa.res = static_cast<const uint16_t*>(res);
+  pa.res_out = static_cast<uint16_t*>(res_out);
+  pa.ss_out = ss_out;
+  pa.gain_next = static_cast<const uint16_t*>(gain_next);
+  pa.hg_out = static_cast<uint16_t*>(hg_out);
+  pa.lengths = lengths;
+  pa.tmax = static_cast<int>(tmax);
+  pa.part = part;
+  pa.nchunk = static_cast<int>(nchunk);
+  pa.chunk = chunk;
+  const hipError_t e = launch_int4_pro_res<kProAttnCombine, true>(static_cast<int>(group), wt, st, nullptr, nullptr, m,
+                                                                  rows, cols, nw, as_stream(stream), pa);
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
+}
+
 extern "C" int sqx_int4_linear_silu_residual(const uint8_t* wt, const float* st, const void* gate_up, const void* res,
                                              void* res_out, float* ss_out, const void* gain_next, void* hg_out,
                                              int64_t m, int64_t rows, int64_t cols, int64_t group, int k_slices,

@@ -135,7 +135,8 @@ class DecodeState:
         self.act = torch.empty(batch, cfg.d_ff, **bf)
         self.logits = torch.empty(batch, cfg.vocab_size, **bf)
         lib = _lib.load()
-        nb = int(lib.sqx_attn_workspace_bytes(batch, cfg.n_heads, hkv, max_ctx))
+        nb = max(int(lib.sqx_attn_workspace_bytes(batch, cfg.n_heads, hkv, max_ctx)),
+                 int(lib.sqx_attn_partials_workspace_bytes(batch, cfg.n_heads, max_ctx)))
         self.attn_ws = torch.empty(max(nb // 4, 4), dtype=torch.float32, device=dev)
         nb = int(lib.sqx_argmax_workspace_bytes(batch, cfg.vocab_size))
         self.argmax_ws = torch.empty(max(nb // 4, 4), dtype=torch.float32, device=dev)
@@ -217,6 +218,10 @@ class Int4DecodeLM:
         # Batched steps: when the o / down projection splits K, its fp32 partials go straight to the
         # next residual add + RMSNorm, which adds them in the linear's own order (no reduce launch).
         self.fuse_split_norm = True
+        # One-row steps, when set: attention leaves its key-chunk partials (at most 8 per head) and the
+        # o projection merges them while it loads its activations (no combine launch). Off: every
+        # o-projection workgroup merges every head, which cost more than the launch it saves.
+        self.fuse_attn_merge = False
         cos, sin = rope_tables(cfg.head_dim, cfg.context_length, cfg.rope_theta)
         self.cos = cos.to(self.device)
         self.sin = sin.to(self.device)
@@ -398,6 +403,10 @@ class Int4DecodeLM:
                 and lib.sqx_int4_prologue_fits(1, cfg.d_ff))
         # one row with a bf16 cache: RoPE and the cache write run in the q|k|v projection's epilogue
         rope_in_qkv = sums and st.kv_dtype == "bf16"
+        # one row: the attention combine runs in the o projection's activation load (two 128-column
+        # k-blocks per wave)
+        kb_o = d // 128
+        merge = (self.fuse_attn_merge and sums and d % 256 == 0 and kb_o // 2 <= 16 and H * hd == d)
         with torch.cuda.device(self.device):
             if go("other"):
                 ck(lib.sqx_embed(self.embed.data_ptr(), cfg.vocab_size, st.tokens.data_ptr(), B, d,
@@ -426,6 +435,14 @@ class Int4DecodeLM:
                 # ---- attention over the cache
                 if not go("attention"):
                     pass
+                elif merge:  # the partials only; the o projection merges them
+                    fp8 = st.kv_dtype == "fp8"
+                    ck(lib.sqx_decode_attention_partials(
+                        st.q.data_ptr() if rope_in_qkv else st.qkv.data_ptr(), st.lengths.data_ptr(),
+                        None if rope_in_qkv else self.cos.data_ptr(), None if rope_in_qkv else self.sin.data_ptr(),
+                        cfg.context_length, st.k[li].data_ptr(), st.v[li].data_ptr(),
+                        st.k_scale[li].data_ptr() if fp8 else None, st.v_scale[li].data_ptr() if fp8 else None,
+                        B, H, Hkv, hd, T, st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention partials")
                 elif rope_in_qkv:
                     ck(lib.sqx_decode_attention(st.q.data_ptr(), st.k[li].data_ptr(), st.v[li].data_ptr(),
                                                 st.lengths.data_ptr(), B, H, Hkv, hd, T, st.attn.data_ptr(),
@@ -445,7 +462,13 @@ class Int4DecodeLM:
                     # o and down end in the residual add and leave bf16(h * gain) of the next norm with
                     # the sums of squares of h; the linear after each norm applies its row factor
                     gain_next = self.layers[li + 1].attn_norm if li + 1 < len(self.layers) else self.final_norm
-                    if go("o"):
+                    if go("o") and merge:
+                        ck(lib.sqx_int4_linear_attn_residual(
+                            ly.wo.wt.data_ptr(), ly.wo.st.data_ptr(), st.attn_ws.data_ptr(), st.lengths.data_ptr(), T,
+                            st.x[cur].data_ptr(), st.x[1 - cur].data_ptr(), st.ss.data_ptr(), ly.ffn_norm.data_ptr(),
+                            st.h.data_ptr(), 1, ly.wo.rows, ly.wo.cols, ly.wo.group_size, kb_o // 2, s),
+                           "attention merge + o + residual")
+                    elif go("o"):
                         ck(lib.sqx_int4_linear_residual(
                             ly.wo.wt.data_ptr(), ly.wo.st.data_ptr(), st.attn.data_ptr(), st.x[cur].data_ptr(),
                             st.x[1 - cur].data_ptr(), st.ss.data_ptr(), ly.ffn_norm.data_ptr(), st.h.data_ptr(), 1,

@@ -454,6 +454,171 @@ def test_linear_rope_kv_equals_two_calls(lib, H, Hkv, T, length, sums):
     assert not torch.equal(kc1[:, :, slot], cache[0][:, :, slot])
 
 
+def _partials(lib, q, lengths, k, v, B, H, Hkv, T, cos=None, sin=None, rope_rows=0, ks=None, vs=None):
+    """sqx_decode_attention_partials into a fresh workspace (NaN-filled: only what it writes is read)."""
+    nb = lib.sqx_attn_partials_workspace_bytes(B, H, T)
+    ws = torch.full((nb // 4,), float("nan"), dtype=torch.float32, device=DEV)
+    _ok(lib, lib.sqx_decode_attention_partials(
+        q.data_ptr(), lengths.data_ptr(), None if cos is None else cos.data_ptr(), None if sin is None else sin.data_ptr(),
+        rope_rows, k.data_ptr(), v.data_ptr(), None if ks is None else ks.data_ptr(), None if vs is None else vs.data_ptr(),
+        B, H, Hkv, 128, T, ws.data_ptr(), nb, _s()))
+    return ws
+
+
+@pytest.mark.parametrize("B,H,Hkv,T,kv8", [(1, 32, 8, 2048, False), (3, 16, 2, 300, False), (4, 8, 8, 77, False),
+                                           (1, 32, 8, 2048, True), (3, 16, 8, 300, True)])
+def test_attention_partials_against_float64(lib, B, H, Hkv, T, kv8):
+    """The 8-wave partials (at most 8 chunks per head) merged by sqx_attn_partials_combine: softmax
+    attention within 2**-8 |ref| + 1e-5 max|v| of float64, for ragged lengths (0, mid-chunk, T - 1, past
+    T), bf16 and E4M3 caches."""
+    from oracle import fp8_ref as F8
+
+    print_case("attention partials", B, H, Hkv, T, kv8)
+    hd = 128
+    chunk = lib.sqx_attn_partials_chunk(T)
+    assert chunk % 128 == 0 and -(-T // chunk) <= 8
+    g = torch.Generator().manual_seed(B * 100 + T + kv8)
+    lengths = ([T - 1, 0, T // 2 + 3, T + 4] * B)[:B]
+    q = (torch.randn(B, H, hd, generator=g) * 2).bfloat16()
+    if kv8:
+        kc, vc = _valid_codes((B, Hkv, T, hd), g), _valid_codes((B, Hkv, T, hd), g)
+        ks = torch.rand(Hkv, generator=g) * 0.01 + 0.001
+        vs = torch.rand(Hkv, generator=g) * 0.01 + 0.001
+        kdeq = torch.from_numpy(F8.e4m3_decode(kc.numpy())).double() * ks.double().view(1, Hkv, 1, 1)
+        vdeq = torch.from_numpy(F8.e4m3_decode(vc.numpy())).double() * vs.double().view(1, Hkv, 1, 1)
+        ksd, vsd = ks.to(DEV), vs.to(DEV)
+    else:
+        kc = (torch.randn(B, Hkv, T, hd, generator=g) * 2).bfloat16()
+        vc = torch.randn(B, Hkv, T, hd, generator=g).bfloat16()
+        kdeq, vdeq = kc.double(), vc.double()
+        ksd = vsd = None
+    ln = torch.tensor(lengths, dtype=torch.int32, device=DEV)
+    ws = _partials(lib, q.to(DEV), ln, kc.to(DEV), vc.to(DEV), B, H, Hkv, T, ks=ksd, vs=vsd)
+    out = torch.empty(B, H * hd, dtype=torch.bfloat16, device=DEV)
+    _ok(lib, lib.sqx_attn_partials_combine(ws.data_ptr(), ln.data_ptr(), B, H, T, out.data_ptr(), _s()))
+    torch.cuda.synchronize()
+    G = H // Hkv
+    got = out.cpu().view(B, H, hd).double()
+    assert torch.isfinite(got).all()
+    for b in range(B):
+        L = min(max(lengths[b], 0) + 1, T)
+        kk = kdeq[b, :, :L].repeat_interleave(G, dim=0)
+        vv = vdeq[b, :, :L].repeat_interleave(G, dim=0)
+        p = torch.softmax(torch.einsum("hd,htd->ht", q[b].double(), kk) / math.sqrt(hd), dim=-1)
+        want = torch.einsum("ht,htd->hd", p, vv)
+        bound = 2.0**-8 * want.abs() + 1e-5 * vv.abs().max()
+        assert float(((got[b] - want).abs() / bound).max()) <= 1.0, f"row {b} (L={L})"
+
+
+@pytest.mark.parametrize("B,H,Hkv,T,kv8", [(1, 32, 8, 2048, False), (5, 16, 2, 300, False), (1, 32, 8, 2048, True)])
+def test_attention_partials_rope_equals_two_calls(lib, B, H, Hkv, T, kv8):
+    """The RoPE form of sqx_decode_attention_partials == sqx_rope_kv (the new row quantized with the
+    head's scales for an E4M3 cache) then the plain form, bit for bit (partials and caches)."""
+    print_case("attention partials rope", B, H, Hkv, T, kv8)
+    hd, ctx = 128, T + 16
+    g = torch.Generator().manual_seed(B * 7 + T + kv8)
+    lengths = torch.randint(0, T, (B,), generator=g)
+    lengths[0] = T - 1
+    if B > 1:
+        lengths[1] = 0
+    if B > 2:
+        lengths[2] = T + 9
+    qkv = (torch.randn(B, (H + 2 * Hkv) * hd, generator=g) * 2).bfloat16().to(DEV)
+    cos, sin = (t.to(DEV) for t in D.rope_tables(hd, ctx, 10000.0))
+    ln = lengths.to(torch.int32).to(DEV)
+    if kv8:
+        cache = [_valid_codes((B, Hkv, T, hd), g).to(DEV) for _ in range(2)]
+        ks = (torch.rand(Hkv, generator=g) * 0.01 + 0.004).to(DEV)
+        vs = (torch.rand(Hkv, generator=g) * 0.01 + 0.004).to(DEV)
+    else:
+        cache = [torch.randn(B, Hkv, T, hd, generator=g).bfloat16().to(DEV) for _ in range(2)]
+        ks = vs = None
+    # fused: RoPE, the cache write and the partials in one launch
+    kf, vf = cache[0].clone(), cache[1].clone()
+    wf = _partials(lib, qkv, ln, kf, vf, B, H, Hkv, T, cos, sin, ctx, ks, vs)
+    # two calls: rotate and write the row (bf16), or rotate into a bf16 scratch cache and quantize the
+    # new row with the head's scales (E4M3), then the plain partials on the rotated q
+    q = torch.empty(B, H * hd, dtype=torch.bfloat16, device=DEV)
+    k2, v2 = cache[0].clone(), cache[1].clone()
+    if kv8:
+        kb = torch.zeros(B, Hkv, T, hd, dtype=torch.bfloat16, device=DEV)
+        vb = torch.zeros_like(kb)
+        _ok(lib, lib.sqx_rope_kv(qkv.data_ptr(), ln.data_ptr(), cos.data_ptr(), sin.data_ptr(), ctx, B, H, Hkv, hd, T,
+                                 q.data_ptr(), kb.data_ptr(), vb.data_ptr(), _s()))
+        torch.cuda.synchronize()
+        from oracle import fp8_ref as F8
+
+        for b in range(B):
+            slot = min(int(lengths[b]), T - 1)
+            for t_, src, sc in ((k2, kb, ks), (v2, vb, vs)):
+                row = src[b, :, slot].float().cpu().numpy()  # [Hkv, hd]
+                t_[b, :, slot] = torch.from_numpy(
+                    F8.e4m3_encode_sat(row / sc.cpu().numpy()[:, None].astype(np.float32))).to(DEV)
+    else:
+        _ok(lib, lib.sqx_rope_kv(qkv.data_ptr(), ln.data_ptr(), cos.data_ptr(), sin.data_ptr(), ctx, B, H, Hkv, hd, T,
+                                 q.data_ptr(), k2.data_ptr(), v2.data_ptr(), _s()))
+    w2 = _partials(lib, q, ln, k2, v2, B, H, Hkv, T, ks=ks, vs=vs)
+    torch.cuda.synchronize()
+    assert torch.equal(kf, k2) and torch.equal(vf, v2)
+    o1, o2 = (torch.empty(B, H * hd, dtype=torch.bfloat16, device=DEV) for _ in range(2))
+    _ok(lib, lib.sqx_attn_partials_combine(wf.data_ptr(), ln.data_ptr(), B, H, T, o1.data_ptr(), _s()))
+    _ok(lib, lib.sqx_attn_partials_combine(w2.data_ptr(), ln.data_ptr(), B, H, T, o2.data_ptr(), _s()))
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+
+
+@pytest.mark.parametrize("H,Hkv,T,length,n", [(32, 8, 2048, 2047, 4096), (32, 8, 2048, 0, 4096),
+                                              (32, 8, 2048, 5000, 4096), (32, 8, 300, 150, 4096),
+                                              (8, 2, 1000, 700, 1024), (16, 16, 64, 63, 2048)])
+def test_linear_attn_residual_equals_two_calls(lib, H, Hkv, T, length, n):
+    """sqx_int4_linear_attn_residual (the combine in the o projection's activation load) ==
+    sqx_attn_partials_combine then sqx_int4_linear_residual with the same k_slices, bit for bit:
+    residual stream, sums of squares and bf16(h * gain); chunk counts 1, 3 and 8."""
+    print_case("linear attn residual", H, Hkv, T, length, n)
+    hd = 128
+    k = H * hd
+    tw = _tiled(n, k, 128, seed=H + T)
+    g = torch.Generator().manual_seed(T + length)
+    q = (torch.randn(1, H, hd, generator=g) * 2).bfloat16().to(DEV)
+    kc = (torch.randn(1, Hkv, T, hd, generator=g) * 2).bfloat16().to(DEV)
+    vc = torch.randn(1, Hkv, T, hd, generator=g).bfloat16().to(DEV)
+    ln = torch.tensor([length], dtype=torch.int32, device=DEV)
+    ws = _partials(lib, q, ln, kc, vc, 1, H, Hkv, T)
+    res = (torch.randn(1, n, generator=g) * 3).bfloat16().to(DEV)
+    gain = (1 + 0.1 * torch.randn(n, generator=g)).bfloat16().to(DEV)
+    att = torch.empty(1, k, dtype=torch.bfloat16, device=DEV)
+    nt = -(-n // 16)
+    out1, out2, hg1, hg2 = (torch.empty(1, n, dtype=torch.bfloat16, device=DEV) for _ in range(4))
+    ss1, ss2 = (torch.full((nt,), float("nan"), dtype=torch.float32, device=DEV) for _ in range(2))
+    ksl = k // 256
+    _ok(lib, lib.sqx_attn_partials_combine(ws.data_ptr(), ln.data_ptr(), 1, H, T, att.data_ptr(), _s()))
+    _ok(lib, lib.sqx_int4_linear_residual(tw.wt.data_ptr(), tw.st.data_ptr(), att.data_ptr(), res.data_ptr(),
+                                          out1.data_ptr(), ss1.data_ptr(), gain.data_ptr(), hg1.data_ptr(), 1, n, k, 128,
+                                          ksl, _s()))
+    _ok(lib, lib.sqx_int4_linear_attn_residual(tw.wt.data_ptr(), tw.st.data_ptr(), ws.data_ptr(), ln.data_ptr(), T,
+                                               res.data_ptr(), out2.data_ptr(), ss2.data_ptr(), gain.data_ptr(),
+                                               hg2.data_ptr(), 1, n, k, 128, ksl, _s()))
+    torch.cuda.synchronize()
+    assert torch.isfinite(att.float()).all()
+    assert torch.equal(out1, out2)
+    assert torch.equal(hg1, hg2)
+    assert torch.equal(ss1, ss2)
+
+
+def test_linear_attn_residual_refuses(lib):
+    """The merge prologue's limits come back as SQX_E_ARG: more than two k-blocks per wave, a width
+    that is not whole heads, more than one row."""
+    tw = _tiled(1024, 4096, 128, seed=1)
+    p = tw.wt.data_ptr()
+    buf = torch.zeros(8192, dtype=torch.float32, device=DEV)
+    b = buf.data_ptr()
+    assert lib.sqx_int4_linear_attn_residual(p, tw.st.data_ptr(), b, b, 2048, b, b, b, None, None, 1, 1024, 4096, 128,
+                                             8, _s()) == -1
+    assert "two k-blocks" in lib.sqx_last_error().decode()
+    assert lib.sqx_int4_linear_attn_residual(p, tw.st.data_ptr(), b, b, 2048, b, b, b, None, None, 2, 1024, 4096, 128,
+                                             16, _s()) == -1
+
+
 def test_residual_forms_refuse(lib):
     tw = _tiled(64, 4096, 128, seed=3)
     x = torch.zeros(2, 4096, dtype=torch.bfloat16, device=DEV)
@@ -719,6 +884,43 @@ def test_graph_replays_equal_eager_steps(small):
         assert torch.equal(a.tokens, b.tokens) and torch.equal(a.lengths, b.lengths)
     assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
     assert b.lengths.cpu().tolist() == [steps] * B
+
+
+@pytest.mark.parametrize("merge", [False, True])
+def test_one_row_graph_replays_equal_eager_steps(small, merge):
+    """The one-row step (norms in the residual epilogues, RoPE in the qkv epilogue; with `merge` the
+    attention combine in the o projection) captured and replayed equals eager steps bit for bit."""
+    model, _ = small
+    print_case("graph replay one row", merge)
+    try:
+        model.fuse_attn_merge = merge
+        a, b = model.new_state(1, 32), model.new_state(1, 32)
+        tok = torch.tensor([321])
+        a.set_tokens(tok, model.cfg.vocab_size)
+        b.set_tokens(tok, model.cfg.vocab_size)
+        graph = model.capture(b)
+        for t in range(5):
+            model.step(a)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(a.logits, b.logits), f"replay {t}"
+            assert torch.equal(a.tokens, b.tokens) and torch.equal(a.lengths, b.lengths)
+        assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
+    finally:
+        model.fuse_attn_merge = False
+
+
+def test_attn_merge_step_matches_reference_both_ways(small):
+    """One row with the attention combine in the o projection and with the combine launch (the
+    default): both within the reference bar of the step oracle (_run_and_compare)."""
+    model, refs = small
+    try:
+        for flag in (True, False):
+            model.fuse_attn_merge = flag
+            _run_and_compare(model, refs, 1, steps=5, seed=23)
+    finally:
+        model.fuse_attn_merge = False
 
 
 def test_inactive_slots_do_not_leak(small):
