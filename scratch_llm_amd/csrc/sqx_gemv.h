@@ -367,6 +367,9 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
     asm volatile("" ::: "memory");
     if constexpr (RKV) {
       if (wave == 0) {  // the pair's cos / sin at the row's position (needed only in the epilogue)
+        // kept in a vector register: moved to a scalar one, it would be waited for where it is loaded,
+        // before the wave's weights are requested
+        asm volatile("" : "+v"(len_pre));
         const int pos = min(max(len_pre, 0), pa.rope_rows - 1);
         const uint32_t pi = (uint32_t)(pos * 64 + (((t * 16 + (lane & 15)) & 127) >> 1)) * 4u;
         const uint32_t tb = (uint32_t)pa.rope_rows * 64u * 4u;
@@ -628,6 +631,9 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
         if constexpr (PRO == kProScaleSum) v *= row_scale_lds;
         if (bias) v += A::to_f32(bias[n]);
         if constexpr (RES) {
+          // opaque until here: otherwise the compiler converts the prefetched values where they are
+          // loaded and waits for them there, before wave 0 has issued its weights
+          asm volatile("" : "+v"(res_pre), "+v"(gain_pre));
           const float rv = A::to_f32(static_cast<uint16_t>(res_pre));
           const float h = A::to_f32(A::from_f32(rv + A::to_f32(A::from_f32(v))));
           pa.res_out[n] = A::from_f32(h);
