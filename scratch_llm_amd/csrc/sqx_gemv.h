@@ -509,7 +509,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
     constexpr int CPB = KBLK / 32;
     static_assert(ONE == 0 || (CPB * U <= 16 && 4 % CPB == 0), "a round's chunks fill the 16 MFMA rows");
     [[maybe_unused]] float sig[U][ONE ? kNgOf<W> : 1];
-    if constexpr (ONE != 0) {
+    if constexpr (ONE != 0 && has_sum_offset<W>::value) {
       const int r = lane & 15, b = r / CPB;
       const uint16_t* xrow = ONE >= 2 ? xwave + (kb - kb0) * KBLK : xs + kb * KBLK;
       u32x4_t a2 = u32x4_t{0u, 0u, 0u, 0u};
@@ -556,6 +556,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
         }
         if constexpr (ONE != 0) {
           if constexpr (has_sum_offset<W>::value) W::template mma_one<A>(w[u], p[u], xv[0], sig[u], y1);
+          else W::template mma<A, MCH>(w[u], p[u], xv, yacc);  // the 16 A rows are copies of the one row
         } else {
           W::template mma<A, MCH>(w[u], p[u], xv, yacc);
         }
@@ -568,6 +569,9 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
     }
   }
 
+  // formats without the sum offset: every row of the MFMA output is the one row's, so element 0 of a
+  // lane's accumulator is its weight row's partial
+  if constexpr (ONE != 0 && !has_sum_offset<W>::value) y1 = yacc[0][0];
   if constexpr (PRO == kProScaleSum) {
     if (wave == 0) {  // the row factor from the sums in LDS, in a fixed order (the same in every workgroup)
       wait_vmcnt<0>();  // the copies into LDS (long done: the weights behind them have been consumed)
@@ -728,15 +732,16 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
 #define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_) SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, 0)
     // the one-row form for formats whose offset costs sum(x) per group: 2 = each wave loads its own
     // k-slice of the activations, 1 = from the workgroup's LDS copy (prologues, column scales)
-    constexpr bool kOneOk = has_sum_offset<W>::value && U1 == 4 && !YF32;
+    // Formats without the sum offset (FP4, FP8) take the per-wave slice form only (their plain MFMA
+    // chain on copies of the row); they gain nothing from form 1.
+    constexpr bool kOneOk = U1 == 4 && !YF32;
     int one_mode = 0;
-    if (kOneOk && M == 1 && xlds)
-      one_mode = ((PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate || PRO == kProScaleSum ||
-                   PRO == kProAttnCombine) &&
-                  colscale == nullptr &&
-                  kbw <= kOneMaxKbw)
-                     ? 2
-                     : 1;
+    if (kOneOk && M == 1 && xlds) {
+      const bool slice = (PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate || PRO == kProScaleSum ||
+                          PRO == kProAttnCombine) &&
+                         colscale == nullptr && kbw <= kOneMaxKbw;
+      one_mode = slice ? 2 : (has_sum_offset<W>::value ? 1 : 0);
+    }
     if (PRO != kProPlain && (!xlds || m > kProMaxRows || cols % 8 != 0))
       return hipErrorNotSupported;  // the caller checks first
     // one-row forms only: the norm from tile sums, the residual epilogue
