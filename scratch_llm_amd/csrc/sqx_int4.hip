@@ -930,7 +930,7 @@ extern "C" int sqx_int4_untile(const uint8_t* wt, const void* st, const void* zt
 
 extern "C" int sqx_int4_linear_default_kslices(int64_t m, int64_t rows, int64_t cols) {
   if (m <= 0 || rows <= 0 || cols <= 0) return 1;
-  return gemv_default_kslices(rows, cols);
+  return gemv_default_kslices(rows, cols, 128, m);
 }
 
 static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, int param_dtype, const void* x,
@@ -1219,7 +1219,7 @@ extern "C" int sqx_int4_linear_attn_residual(const uint8_t* wt, const float* st,
   SQX_REQUIRE(nchunk <= kAttnFoldChunks, SQX_E_ARG, "%s: %lld key chunks (at most %d)", fn, (long long)nchunk,
               kAttnFoldChunks);
   const int64_t KB = cols / 128;
-  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols) : k_slices;
+  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols, 128, 1) : k_slices;
   if (nw > KB) nw = static_cast<int>(KB);
   SQX_REQUIRE(ceil_div(KB, nw) == 2 && nw <= 16, SQX_E_ARG,
               "%s: the merge prologue runs two k-blocks per wave: %lld k-blocks over %d waves (k_slices)", fn,
@@ -1277,7 +1277,7 @@ extern "C" int sqx_int4_linear_rmsnorm_sumsq(const uint8_t* wt, const float* st,
   SQX_REQUIRE(reinterpret_cast<uintptr_t>(gain) % 16 == 0 && reinterpret_cast<uintptr_t>(ss) % 4 == 0, SQX_E_ARG,
               "%s: gain must be 16-byte and the sums 4-byte aligned", fn);
   const int64_t KB = ceil_div(cols, 128);
-  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols) : k_slices;
+  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols, 128, 1) : k_slices;
   if (nw > KB) nw = static_cast<int>(KB);
   SQX_REQUIRE(ceil_div(KB, nw) <= kOneMaxKbw, SQX_E_ARG,
               "%s: %lld k-blocks over %d waves: at most %d per wave (raise k_slices)", fn, (long long)KB, nw,
@@ -1307,7 +1307,7 @@ extern "C" int sqx_int4_linear_rowscale_sumsq(const uint8_t* wt, const float* st
   SQX_REQUIRE(ss != nullptr && reinterpret_cast<uintptr_t>(ss) % 16 == 0, SQX_E_ARG,
               "%s: the sums must be 16-byte aligned", fn);
   const int64_t KB = ceil_div(cols, 128);
-  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols) : k_slices;
+  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols, 128, 1) : k_slices;
   if (nw > KB) nw = static_cast<int>(KB);
   SQX_REQUIRE(ceil_div(KB, nw) <= kOneMaxKbw, SQX_E_ARG,
               "%s: %lld k-blocks over %d waves: at most %d per wave (raise k_slices)", fn, (long long)KB, nw,
@@ -1344,7 +1344,7 @@ extern "C" int sqx_int4_linear_rope_kv(const uint8_t* wt, const float* st, const
               SQX_E_ARG, "%s: %lld sums of squares for %lld columns (one per 16 columns, at most %d, 16-byte aligned)",
               fn, (long long)nss, (long long)cols, kNormSumMax);
   const int64_t KB = ceil_div(cols, 128);
-  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols) : k_slices;
+  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols, 128, 1) : k_slices;
   if (nw > KB) nw = static_cast<int>(KB);
   SQX_REQUIRE(ceil_div(KB, nw) <= kOneMaxKbw, SQX_E_ARG,
               "%s: %lld k-blocks over %d waves: at most %d per wave (raise k_slices)", fn, (long long)KB, nw,
