@@ -853,8 +853,14 @@ namespace {
 // Output-tile rows: 128 for M <= 128, where a 256-row tile is at least half padding (config 4's
 // bf16 activations at M = 128: 106 -> 74 us and 96 -> 65 us), else 256: a 128-row tile decodes each
 // weight for half as many MFMAs, and at M = 512 / 2048 it measured slower on the 14336-wide shapes
-// (97 -> 104 us, 298 -> 364 us) and within 6 % elsewhere.
-int dq_tile_rows(int64_t m, int64_t) { return m <= 128 ? 128 : 256; }
+// (97 -> 104 us, 298 -> 364 us) and within 6 % elsewhere. Also 128 when 256-row tiles would number
+// fewer than 16, where the K splits that fill the CUs are the cost (4096->1024 at M = 512, which
+// splits 16 ways either way: 31.9 -> 28.3 us; 4096x4096 at M = 512 has 32 tiles: 44.3 us against
+// 43.0 us at its best 128-row split, so it stays).
+int dq_tile_rows(int64_t m, int64_t rows) {
+  if (m <= 128) return 128;
+  return ceil_div(m, 256) * ceil_div(rows, dqg::kTile) < 16 ? 128 : 256;
+}
 
 int dq_splits(int64_t m, int64_t rows, int64_t cols) {
   const int64_t tiles = ceil_div(m, dq_tile_rows(m, rows)) * ceil_div(rows, dqg::kTile);
