@@ -71,9 +71,10 @@ def test_skinny_matches_oracle(q4, n, k, group, m, variant, tiles, waves, splits
     assert torch.equal(y, again)  # fixed-order sums
 
 
-@pytest.mark.parametrize("m", [16, 32, 64])
-@pytest.mark.parametrize("n,k", [(6144, 4096), (28672, 4096), (4096, 14336)], ids=lambda v: str(v))
+@pytest.mark.parametrize("m", [16, 17, 32, 64])
+@pytest.mark.parametrize("n,k", [(6144, 4096), (28672, 4096), (4096, 14336), (1024, 4096)], ids=lambda v: str(v))
 def test_skinny_llama_shapes_default(q4, n, k, m):
+    """The library's launch shape for each row count, including four K splits on 64 tiles (1024)."""
     print_case("skinny llama", n, k, m)
     tw, w_eff = _sym(q4, n, k, 128, 7 * n + k, std=0.02)
     x = _act(m, k, m + 11).to(DEV)
