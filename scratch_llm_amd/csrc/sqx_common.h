@@ -272,6 +272,13 @@ __device__ inline float attn_chunk_weight(float m, float M) { return m == -INFIN
 
 // The two bf16 values of a 32-bit word as fp32 (low half first).
 __device__ inline float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+
+// SiLU in fp32, g * sigmoid(g) = g / (1 + e^-g), with the hardware reciprocal (1 ulp) in place of an
+// IEEE division: a division costs about ten instructions, and the decode step's fused SiLU prologue
+// sits in front of the first MFMA of every wave. e^-g overflowing to inf gives a signed zero, as the
+// division does. Every SiLU of the library goes through this one function, so the fused prologues
+// and the standalone kernel stay bit-identical.
+__device__ inline float silu_f32(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 __device__ inline float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
 constexpr float kE4M3Max = 448.0f;

@@ -588,8 +588,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   const uint32_t g2 = *reinterpret_cast<const uint32_t*>(gu + b * 2 * F + c);
   const uint32_t u2 = *reinterpret_cast<const uint32_t*>(gu + b * 2 * F + F + c);
   const float g0 = bf16_lo(g2), g1 = bf16_hi(g2);
-  const float r0 = g0 / (1.0f + __expf(-g0)) * bf16_lo(u2);
-  const float r1 = g1 / (1.0f + __expf(-g1)) * bf16_hi(u2);
+  const float r0 = silu_f32(g0) * bf16_lo(u2);
+  const float r1 = silu_f32(g1) * bf16_hi(u2);
   *reinterpret_cast<uint32_t*>(out + i) = ActBF16::pack_rne(r0, r1);
 }
 

@@ -296,8 +296,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
           for (int j = 0; j < 4; ++j) {
             const uint32_t g2 = xw[i][j], u2 = gw[i][j];
             const float g0 = bf16_lo(g2), g1 = bf16_hi(g2);
-            const uint32_t v = ActBF16::pack_rne(g0 / (1.0f + __expf(-g0)) * bf16_lo(u2),
-                                                 g1 / (1.0f + __expf(-g1)) * bf16_hi(u2));
+            const uint32_t v = ActBF16::pack_rne(silu_f32(g0) * bf16_lo(u2), silu_f32(g1) * bf16_hi(u2));
             xw[i][j] = in ? v : 0u;
           }
         }
@@ -463,7 +462,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float g0 = bf16_lo(g2[j]), g1 = bf16_hi(g2[j]);
-          v[j] = ActBF16::pack_rne(g0 / (1.0f + __expf(-g0)) * bf16_lo(u2[j]), g1 / (1.0f + __expf(-g1)) * bf16_hi(u2[j]));
+          v[j] = ActBF16::pack_rne(silu_f32(g0) * bf16_lo(u2[j]), silu_f32(g1) * bf16_hi(u2[j]));
         }
       }
       *reinterpret_cast<u32x4_t*>(xs + r * xpitch + col) = v;
