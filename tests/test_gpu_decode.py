@@ -657,7 +657,7 @@ def test_attention_rejects_bad_shapes(lib):
                                     ws.data_ptr(), ws.data_ptr(), 64, _s()) == -3
 
 
-@pytest.mark.parametrize("B,F", [(1, 14336), (5, 96), (64, 2048)])
+@pytest.mark.parametrize("B,F", [(1, 14336), (5, 96), (64, 2048), (3, 100)])  # F = 100: the two-element kernel
 def test_silu_mul(lib, B, F):
     print_case("silu_mul", B, F)
     g = torch.Generator().manual_seed(F)
