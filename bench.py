@@ -533,18 +533,22 @@ def measured_traffic(dom, m: int):
 def _graph_call_us(fn, calls: int = 4, reps: int = 5) -> float:
     """us per call of ``fn`` (device work on the current stream, any host-side allocation graph-safe),
     captured ``calls`` times back to back in one HIP graph and replayed ``reps`` times between HIP
-    events: GPU time without the host's launch gaps."""
+    events: GPU time without the host's launch gaps. ``fn`` may be a list of callables (one per
+    rotating weight copy), captured once each in order."""
     import torch
 
+    fns = list(fn) if isinstance(fn, (list, tuple)) else [fn] * calls
+    calls = len(fns)
     cs = torch.cuda.Stream()
     cs.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(cs):
-        fn()  # warm any lazily built state outside the capture
+        for f in dict.fromkeys(fns):
+            f()  # warm any lazily built state outside the capture
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=cs):
-        for _ in range(calls):
-            fn()
+        for f in fns:
+            f()
     graph.replay()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -769,11 +773,12 @@ def prefill_gemms(dev) -> dict:
 
 def baseline_configs(dev) -> dict:
     """Every case of BASELINE.json's configs 1-4 on one GPU (config 5 is ``decode``; config 4 at M = 4096
-    and config 3's M = 2048 on 4096->14336 are also in ``prefill``). Memory-bound cases (M <= 16, the
-    MXFP4 GEMV at M = 1) are timed as a captured graph of back-to-back launches over >= 1 GB of
-    rotating weights and reported in GB/s of algorithmic bytes; GEMMs as captured graphs of
-    back-to-back calls (no host launch gaps) in TFLOP/s against the dtype's dense peak. Weights ~N(0, 0.02), activations bf16 ~N(0, 1) as the configs
-    state; config 3's activation scale ~log-uniform[0.5, 2] and 1% of channels x20."""
+    and config 3's M = 2048 on 4096->14336 are also in ``prefill``). Every case is a captured graph of
+    back-to-back calls, each on the next of >= 1.1 GB of rotating weight copies (more than four times
+    the 256 MB Infinity Cache, so the weights come from HBM): memory-bound cases (M <= 16, the MXFP4
+    GEMV at M = 1) reported in GB/s of algorithmic bytes, GEMMs in TFLOP/s against the dtype's dense
+    peak. Weights ~N(0, 0.02), activations bf16 ~N(0, 1) as the configs state; config 3's activation
+    scale ~log-uniform[0.5, 2] and 1% of channels x20."""
     import torch
 
     from scratch_llm_amd import _lib
@@ -786,7 +791,7 @@ def baseline_configs(dev) -> dict:
            "config4_mxfp4": {}}
 
     def rotating(n, k, make, per_weight_bytes):
-        copies = max(2, min(40, int(1.2e9 // per_weight_bytes)))
+        copies = max(2, min(1024, -(-int(1.1e9) // per_weight_bytes)))
         return [make(torch.randn(n, k, generator=g, device=dev) * 0.02) for _ in range(copies)]
 
     def gbs_entry(us, byts):
@@ -843,20 +848,19 @@ def baseline_configs(dev) -> dict:
 
     # config 3: AWQ int4 g128 prefill GEMM, M in {64, 512, 2048}
     for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
-        w = torch.randn(n, k, generator=g, device=dev) * 0.02
         sc = torch.exp(torch.empty(k, device=dev).uniform_(-0.6931, 0.6931, generator=g))
-        quant = awq.quantize_awq_int4(w, chan_scale=sc)
-        del w
+        quants = rotating(n, k, lambda w: awq.quantize_awq_int4(w, chan_scale=sc), n * k // 2 + n * k // 32)
         for m in (64, 512, 2048):
             x = torch.randn(m, k, generator=g, device=dev)
             x[:, torch.randperm(k, generator=torch.Generator().manual_seed(k))[: k // 100].to(dev)] *= 20.0
             x = x.to(torch.bfloat16)
-            us = _graph_call_us(lambda: awq.awq_linear(x, quant))
+            us = _graph_call_us([lambda q=q: awq.awq_linear(x, q) for q in quants])
             fl = 2.0 * m * n * k
             res["config3_awq_int4_g128"][f"{k}->{n} M={m}"] = {
                 "us": round(us, 1), "tflops": round(fl / us / 1e6, 1),
-                "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4)}
-        del quant
+                "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4),
+                "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1), "rotating_copies": len(quants)}
+        del quants
         torch.cuda.empty_cache()
 
     # config 4: MXFP4 weights (e2m1 + e8m0 per 32 along K), bf16 or MXFP4 activations, M in {1, 128}
@@ -873,22 +877,30 @@ def baseline_configs(dev) -> dict:
 
         byts = n * k // 2 + n * k // 32 + 2 * k + 2 * n
         res["config4_mxfp4"][f"bf16_x {k}->{n} M=1"] = gbs_entry(_graph_us(run), byts)
-        tw = tws[0]
-        del tws[1:]
+        # MXFP4 activations at M = 1: what mxfp4_linear(quantize_activations=True) runs (the row's
+        # quantize-dequantize, then the weight GEMV), and the fp4 MFMA GEMM on the same row
+        us = _graph_call_us([lambda tw=tw: f4.fp4_linear_tiled(f4.mxfp4_fake_quant_rows(x1), tw) for tw in tws])
+        e = gbs_entry(us, byts)
+        e["path"] = "mxfp4_fake_quant_rows + FP4 GEMV (two launches)"
+        res["config4_mxfp4"][f"mxfp4_x {k}->{n} M=1"] = e
+        xq1 = f4.mxfp4_quantize_tiled(x1)
+        e = gbs_entry(_graph_call_us([lambda tw=tw: f4.mxfp4_gemm(xq1, tw) for tw in tws]), byts)
+        e["path"] = "fp4 MFMA GEMM (activations quantized beforehand)"
+        res["config4_mxfp4"][f"mxfp4_x {k}->{n} M=1 GEMM"] = e
         m = 128
         x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
         fl = 2.0 * m * n * k
-        us = _graph_call_us(lambda: f4.fp4_linear_tiled(x, tw))
+        us = _graph_call_us([lambda tw=tw: f4.fp4_linear_tiled(x, tw) for tw in tws])
         res["config4_mxfp4"][f"bf16_x {k}->{n} M={m}"] = {
             "us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4),
-            "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1)}
+            "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1), "rotating_copies": len(tws)}
         xq = f4.mxfp4_quantize_tiled(x)
-        us = _graph_call_us(lambda: f4.mxfp4_gemm(xq, tw))
+        us = _graph_call_us([lambda tw=tw: f4.mxfp4_gemm(xq, tw) for tw in tws])
         res["config4_mxfp4"][f"mxfp4_x {k}->{n} M={m}"] = {
             "us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "frac_of_fp4_peak": round(fl / us * 1e6 / FP4_PEAK, 4),
-            "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1),
+            "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1), "rotating_copies": len(tws),
             "quantize_x_us": round(_graph_call_us(lambda: f4.mxfp4_quantize_tiled(x)), 1)}
-        del tw, tws
+        del tws
         torch.cuda.empty_cache()
     return res
 

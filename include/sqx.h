@@ -24,6 +24,7 @@ enum {
   SQX_DTYPE_F32 = 0,
   SQX_DTYPE_BF16 = 1,
   SQX_DTYPE_F16 = 2,
+  SQX_DTYPE_F64 = 3, /* accepted by sqx_nvfp4_ceil_quantize only */
 };
 
 /* FP4 weight formats and the source of their scales for sqx_fp4_tile */
@@ -309,6 +310,12 @@ int sqx_quantize_e8m0(const float* v, int64_t n, float* out, sqx_stream_t stream
 int sqx_mxfp4_quantize(const void* x, int dtype, int64_t n, int64_t block, uint8_t* codes,
                        float* s_block, uint8_t* e8m0, sqx_stream_t stream);
 
+/* mxfp4_dequantize(mxfp4_quantize(x)) (nvfp4_mxfp4.py:257-272) of each row of x [m, k] (dtype F32 /
+ * BF16 / F16, k a multiple of 32, 16-byte aligned), written as bf16 rows out [m, k]: every value is
+ * exact in bf16 where it is finite in fp32. Config 4's activation-quantized linear at a few rows runs
+ * these rows through the MXFP4 weight GEMV (the products of the two dequantized operands). */
+int sqx_mxfp4_fake_quant_rows(const void* x, int dtype, int64_t m, int64_t k, uint16_t* out, sqx_stream_t stream);
+
 /* mxfp4_dequantize (nvfp4_mxfp4.py:268-272): out[i] = decode(codes[i]) * s_block[i / block], i < n. */
 int sqx_mxfp4_dequantize(const uint8_t* codes, const float* s_block, int64_t n, int64_t block,
                          float* out, sqx_stream_t stream);
@@ -348,11 +355,19 @@ int sqx_fp4_tile(const uint8_t* codes, int codes_packed, const void* scales, int
 int sqx_fp4_untile(const uint8_t* wt, const uint8_t* st, int fmt, int64_t rows, int64_t cols, uint8_t* packed,
                    uint8_t* scales, sqx_stream_t stream);
 
+/* dequantize_mxfp4 into float64 (k3/checkpoint.py:92-144): out[r, c] = E2M1(code) * 2**(s - 127) for
+ * the on-disk pair, packed uint8 [rows, cols/2] (low nibble = even column) and E8M0 bytes uint8
+ * [rows, cols/32]; every value is exact in float64. out: float64 [rows, cols], 16-byte aligned. The
+ * caller refuses scale byte 0xFF (NaN) beforehand, as the reference does. */
+int sqx_mxfp4_pair_dequantize_f64(const uint8_t* packed, const uint8_t* scales, int64_t rows, int64_t cols,
+                                  double* out, sqx_stream_t stream);
+
 /* The second NVFP4 convention, the b_r6 GEMM rung's operands (kernels/gemm/cuda/b_r6.py:155-244 with
  * kernels/gemm/nvfp4_layout.py:341-416). Per block of 16 along k, in float64: scale = the smallest
  * unsigned-E4M3 value >= amax / 6 (ceil onto the grid; no global scale; an all-zero block gets 0),
  * code = the nearest E2M1 magnitude of x / scale with ties to the even magnitude index (saturating
- * at 6), the sign bit only on a non-zero magnitude. x: [rows, k] of dtype (F32 / BF16 / F16), k a
+ * at 6), the sign bit only on a non-zero magnitude. x: [rows, k] of dtype (F32 / BF16 / F16 / F64; the
+ * block amax and every quotient are float64, as the reference's x.to(float64)), k a
  * multiple of 16; packed: uint8 [rows, k/2], the lower k in the low nibble (the reference's bytes);
  * scales: uint8 [rows, k/16] row-major E4M3 codes (the reference swizzles them for CUTLASS; this
  * layout is the library's). *status (device int, zeroed by the caller) gets bit 0 for a NaN or Inf
@@ -368,7 +383,8 @@ int sqx_nvfp4_ceil_dequantize(const uint8_t* packed, const uint8_t* scales, int6
  * sqx_ue4m3_ceil: codes[i] = ue4m3_ceil_code(v[i] / divisor) and values[i] its value (values may be
  * NULL); divisor 6 gives scale_for_amax (amax 0 -> code 0). Status bit 0: a negative or non-finite
  * v; bit 1: v / divisor > 448 (the code is then 0). sqx_e2m1_round_rne: e2m1_round_code (status bit
- * 0 for NaN or Inf). */
+ * 0 for NaN or Inf), with the scalar rule's sign bit: set for every v < 0, so a negative v that
+ * rounds to magnitude 0 gives 0x8 (nvfp4_layout.py:402), unlike the quantizer's canonical +0. */
 int sqx_ue4m3_ceil(const double* v, int64_t n, double divisor, uint8_t* codes, double* values, int* status,
                    sqx_stream_t stream);
 int sqx_e2m1_round_rne(const double* v, int64_t n, uint8_t* codes, int* status, sqx_stream_t stream);

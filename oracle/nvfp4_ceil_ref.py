@@ -10,7 +10,9 @@ src/scratch_llm/kernels/gemm/nvfp4_layout.py:341-416):
     block gets code 0 (scale 0) and divides by 1;
   * ``y = x / scale`` in float64, then the nearest E2M1 magnitude (0, .5, 1, 1.5, 2, 3, 4, 6) with
     ties to the even magnitude index (5 -> 4, 0.75 -> 1, 0.25 -> 0), saturating at 6;
-  * the sign bit only for a non-zero magnitude (zero is always code 0x0);
+  * in the quantizer, the sign bit only for a non-zero magnitude (zero is always code 0x0,
+    b_r6.py:217-223); the scalar helper ``e2m1_round_code`` (nvfp4_layout.py:390-416) sets it for
+    every negative input instead, so -0.2 gives 0x8;
   * two codes per byte, the lower k in the low nibble; NaN or Inf anywhere raises.
 No global scale. The reference stores the scale bytes in the CUTLASS tile swizzle; here (and in
 the build) they are a row-major ``[rows, k/16]`` uint8 array of UE4M3 codes, the build's own layout.
@@ -19,7 +21,9 @@ Pinning (tests/test_oracle_nvfp4_ceil.py): the reference test's tie table
 (tests/kernels/gemm/test_k1_b_r6.py:452-469) and ceil-scale theorem and tightness checks (:472-500),
 the round-trip bound and idempotence (:517-561), zero blocks, non-finite refusal and nibble order
 (:564-611); independently, the UE4M3 ceiling against torch's ``float8_e4m3fn`` cast (the same
-grid, round to nearest even) and the E2M1 rounding against a brute-force nearest search.
+grid, round to nearest even) and the E2M1 rounding against a brute-force nearest search; the two
+sign rules by code-byte known answers read off nvfp4_layout.py:399-416 and b_r6.py:217-223
+(tests/golden/known_answers.json, ``e2m1_round_code_scalar``).
 """
 
 from __future__ import annotations
@@ -73,18 +77,31 @@ def scale_for_amax(amax) -> tuple[np.ndarray, np.ndarray]:
 _MIDS = np.array([0.5 * (E2M1_MAGNITUDES[i] + E2M1_MAGNITUDES[i + 1]) for i in range(7)])  # b_r6.py:123-128
 
 
-def e2m1_round_code(y) -> np.ndarray:
-    """nvfp4_layout.py:390-416 / b_r6.py:205-216: nearest E2M1 magnitude, ties to the even magnitude
-    index, saturating at 6; the sign bit only on a non-zero magnitude (b_r6.py:217-223)."""
-    y = np.asarray(y, np.float64)
-    if not np.all(np.isfinite(y)):
-        raise ValueError("e2m1_round_code: E2M1 encodes neither NaN nor Inf (NanInfEncoding::NONE)")
+def _e2m1_magnitude(y) -> np.ndarray:
+    """nvfp4_layout.py:403-416 / b_r6.py:205-216: index of the nearest E2M1 magnitude, ties to the
+    even index, saturating at 6 (index 7)."""
     a = np.abs(y)
     lo = np.searchsorted(_MIDS, a, side="left")  # ties round down
     hi = np.searchsorted(_MIDS, a, side="right")  # ties round up
-    mag = np.where((hi > lo) & (lo % 2 == 1), hi, lo)
-    sign = np.where((y < 0) & (mag > 0), 8, 0)
-    return (mag | sign).astype(np.uint8)
+    return np.where((hi > lo) & (lo % 2 == 1), hi, lo)
+
+
+def e2m1_round_code(y) -> np.ndarray:
+    """nvfp4_layout.py:390-416, the scalar helper: the magnitude index with the sign bit set for every
+    ``y < 0`` (``code = 8 if value < 0 else 0``, :402), so a negative value that rounds to magnitude 0
+    gives 0x8 while -0.0 (not below zero) gives 0x0."""
+    y = np.asarray(y, np.float64)
+    if not np.all(np.isfinite(y)):
+        raise ValueError("e2m1_round_code: E2M1 encodes neither NaN nor Inf (NanInfEncoding::NONE)")
+    return (_e2m1_magnitude(y) | np.where(y < 0, 8, 0)).astype(np.uint8)
+
+
+def _e2m1_quant_code(y) -> np.ndarray:
+    """b_r6.py:205-223, the quantizer's codes: the same magnitude, but the sign bit only on a non-zero
+    magnitude (zero is stored as canonical +0)."""
+    y = np.asarray(y, np.float64)
+    mag = _e2m1_magnitude(y)
+    return (mag | np.where((y < 0) & (mag > 0), 8, 0)).astype(np.uint8)
 
 
 def e2m1_value(code) -> np.ndarray:
@@ -109,7 +126,7 @@ def quantize(x) -> tuple[np.ndarray, np.ndarray]:
     amax = np.abs(blocks).max(axis=-1)
     code, scale = scale_for_amax(amax)
     y = blocks / np.where(scale > 0, scale, 1.0)[..., None]
-    codes = e2m1_round_code(y).reshape(rows, k)
+    codes = _e2m1_quant_code(y).reshape(rows, k)
     packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
     return packed, code.reshape(rows, k // SF_VEC_SIZE)
 

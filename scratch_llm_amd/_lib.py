@@ -19,6 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libsqx_hip.so"
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_F16 = 2
+DTYPE_F64 = 3  # sqx_nvfp4_ceil_quantize only
 FP4_MX = 0
 FP4_NV = 1
 FP4_SCALE_MX_F32 = 0
@@ -47,6 +48,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sqx_int4_untile": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_i, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p]),
     "sqx_int8_untile": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_fp4_untile": (_c_i, [_c_p, _c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "sqx_mxfp4_pair_dequantize_f64": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_int4_linear_default_kslices": (_c_i, [_c_i64, _c_i64, _c_i64]),
     "sqx_int4_linear": (
         _c_i,
@@ -90,6 +92,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sqx_quantize_e4m3": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
     "sqx_quantize_e8m0": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
     "sqx_mxfp4_quantize": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p]),
+    "sqx_mxfp4_fake_quant_rows": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_mxfp4_dequantize": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_nvfp4_workspace_bytes": (_c_i64, []),
     "sqx_nvfp4_quantize": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p]),

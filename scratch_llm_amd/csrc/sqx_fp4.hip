@@ -250,6 +250,61 @@ __global__ __launch_bounds__(256) void mxfp4_quantize_tiled_kernel(const void* _
   xst[q] = static_cast<uint8_t>(sbyte);
 }
 
+// bf16(mxfp4_dequantize(mxfp4_quantize(row))) for each row of x [m, k] (k % 32 == 0): one thread per
+// 32-element block, the same code and scale as mxfp4_quantize_tiled_kernel, then code value * 2**e.
+// Every such value is exact in bf16 wherever it is finite in fp32 (the two share the exponent range,
+// and an E2M1 value has 2 significant bits), so these rows times a weight are the products of the two
+// dequantized operands.
+template <int DT>
+__global__ __launch_bounds__(256) void mxfp4_fake_quant_rows_kernel(const void* __restrict__ x, int64_t n_blocks,
+                                                                    uint16_t* __restrict__ out) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= n_blocks) return;
+  float v[32];
+  const int64_t base = b * 32;
+  if (DT == SQX_DTYPE_F32) {
+    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(static_cast<const float*>(x) + base);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const u32x4_t w = p[j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t u = w[e];
+        v[4 * j + e] = __builtin_bit_cast(float, u);
+      }
+    }
+  } else {
+    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + base);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4_t w = p[j];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t h = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+        v[8 * j + e] = DT == SQX_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+      }
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) amax = amax_step(amax, v[e]);
+  const int ex = mx_exponent(amax);
+  const float inv = ex == 128 ? __builtin_nanf("") : ldexpf(1.0f, -ex);
+  const float sc = ex == 128 ? __builtin_nanf("") : ldexpf(1.0f, ex);
+  constexpr float kMag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  uint32_t o[16];
+#pragma unroll
+  for (int e = 0; e < 32; e += 2) {
+    const uint32_t c0 = e2m1_code(v[e] * inv), c1 = e2m1_code(v[e + 1] * inv);
+    const float d0 = (c0 & 8u ? -kMag[c0 & 7u] : kMag[c0 & 7u]) * sc;
+    const float d1 = (c1 & 8u ? -kMag[c1 & 7u] : kMag[c1 & 7u]) * sc;
+    o[e >> 1] = static_cast<uint32_t>(f32_to_bf16_bits(d0)) | (static_cast<uint32_t>(f32_to_bf16_bits(d1)) << 16);
+  }
+  u32x4_t* q = reinterpret_cast<u32x4_t*>(out + base);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) q[j] = u32x4_t{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+}
+
 // NVFP4 global amax: P partial maxima, then s_global = max(amax / (448 * 6), 1e-30) from them.
 static constexpr int kAmaxParts = 512;
 
@@ -529,9 +584,16 @@ __device__ inline uint32_t e2m1_rne_index(double a) {
   return (hi > lo && (lo & 1u)) ? hi : lo;
 }
 
+// The quantizer's code (b_r6.py:205-223): a value that rounds to magnitude 0 is stored as +0.
 __device__ inline uint32_t e2m1_rne_code(double y) {
   const uint32_t i = e2m1_rne_index(fabs(y));
   return i | ((y < 0.0 && i != 0u) ? 8u : 0u);
+}
+
+// The scalar helper's code (nvfp4_layout.py:390-416): the sign bit is set for every y < 0, so a
+// negative value that rounds to magnitude 0 gives 0x8; -0.0 is not below zero and gives 0x0.
+__device__ inline uint32_t e2m1_rne_code_signed(double y) {
+  return e2m1_rne_index(fabs(y)) | (y < 0.0 ? 8u : 0u);
 }
 
 // One thread per block of 16: packed [rows, k/2] (8 bytes per block), scale codes [rows, k/16].
@@ -540,21 +602,24 @@ __global__ __launch_bounds__(256) void nvfp4_ceil_quantize_kernel(const void* __
                                                                   uint8_t* __restrict__ scales, int* __restrict__ status) {
   const int64_t b = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (b >= nblk) return;
-  float v[16];
+  // float64 throughout, as the reference's x.to(float64): every fp32 / bf16 / fp16 value is exact in it.
+  double v[16];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) v[j] = load_as_f32(x, dtype, b * 16 + j);
-  float amax = 0.0f;
+  for (int j = 0; j < 16; ++j)
+    v[j] = dtype == SQX_DTYPE_F64 ? static_cast<const double*>(x)[b * 16 + j]
+                                  : static_cast<double>(load_as_f32(x, dtype, b * 16 + j));
+  double amax = 0.0;
   bool finite = true;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     finite = finite && isfinite(v[j]);
-    amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmax(amax, fabs(v[j]));
   }
   int bad = finite ? 0 : kCeilNonFinite;
   uint32_t code = 0u;
   double scale = 0.0;
   if (finite) {
-    code = ue4m3_ceil_d(static_cast<double>(amax) / 6.0);
+    code = ue4m3_ceil_d(amax / 6.0);
     if (code == 0x7Fu) {
       bad |= kCeilRange;
       code = 0u;
@@ -566,7 +631,7 @@ __global__ __launch_bounds__(256) void nvfp4_ceil_quantize_kernel(const void* __
   uint32_t w[2] = {0u, 0u};
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const uint32_t c = finite ? e2m1_rne_code(static_cast<double>(v[j]) / div) : 0u;
+    const uint32_t c = finite ? e2m1_rne_code(v[j] / div) : 0u;
     w[j >> 3] |= c << (4 * (j & 7));
   }
   *reinterpret_cast<u32x2v_t*>(packed + b * 8) = u32x2v_t{w[0], w[1]};
@@ -615,7 +680,7 @@ __global__ __launch_bounds__(256) void nvfp4_ceil_elem_kernel(const double* __re
     }
     if (values) values[i] = ue4m3_value_d(c);
   } else {
-    c = e2m1_rne_code(a);
+    c = e2m1_rne_code_signed(a);
   }
   if (bad) atomicOr(status, bad);
   codes[i] = static_cast<uint8_t>(c);
@@ -831,6 +896,65 @@ extern "C" int sqx_fp4_untile(const uint8_t* wt, const uint8_t* st, int fmt, int
   return SQX_OK;
 }
 
+// The on-disk MXFP4 pair in float64 (k3/checkpoint.py:136-144): one thread per packed byte (columns
+// 2j and 2j + 1 of its row, the low nibble first); the E8M0 byte s becomes 2**(s - 127) by writing
+// s - 127 + 1023 into float64's exponent field, so every value and product is exact.
+__global__ __launch_bounds__(256) void mxfp4_pair_f64_kernel(const uint8_t* __restrict__ packed,
+                                                             const uint8_t* __restrict__ scales, int64_t half,
+                                                             int64_t groups, int64_t nbytes, double* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= nbytes) return;
+  const int64_t r = i / half;
+  const int64_t j = i - r * half;
+  const uint32_t b = packed[i];
+  const uint64_t sb = scales[r * groups + (2 * j) / 32];
+  const double sc = __longlong_as_double(static_cast<long long>((sb + (1023 - 127)) << 52));
+  constexpr double kMag[8] = {0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0};
+  const uint32_t lo = b & 0xFu, hi = b >> 4;
+  double2 v;
+  v.x = (lo & 8u ? -kMag[lo & 7u] : kMag[lo & 7u]) * sc;
+  v.y = (hi & 8u ? -kMag[hi & 7u] : kMag[hi & 7u]) * sc;
+  reinterpret_cast<double2*>(out)[i] = v;
+}
+
+extern "C" int sqx_mxfp4_pair_dequantize_f64(const uint8_t* packed, const uint8_t* scales, int64_t rows, int64_t cols,
+                                             double* out, sqx_stream_t stream) {
+  SQX_REQUIRE(rows >= 0 && cols > 0 && cols % 32 == 0, SQX_E_ARG,
+              "sqx_mxfp4_pair_dequantize_f64: bad shape [%lld, %lld] (cols a multiple of 32)", (long long)rows,
+              (long long)cols);
+  const int64_t nbytes = rows * (cols / 2);
+  if (nbytes == 0) return SQX_OK;
+  SQX_REQUIRE(packed && scales && out, SQX_E_ARG, "sqx_mxfp4_pair_dequantize_f64: null pointer");
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(out) % 16 == 0, SQX_E_ARG,
+              "sqx_mxfp4_pair_dequantize_f64: out must be 16-byte aligned");
+  hipLaunchKernelGGL(mxfp4_pair_f64_kernel, grid_for(nbytes), dim3(256), 0, as_stream(stream), packed, scales,
+                     cols / 2, cols / 32, nbytes, out);
+  SQX_LAUNCH_CHECK("sqx_mxfp4_pair_dequantize_f64");
+  return SQX_OK;
+}
+
+extern "C" int sqx_mxfp4_fake_quant_rows(const void* x, int dtype, int64_t m, int64_t k, uint16_t* out,
+                                         sqx_stream_t stream) {
+  SQX_REQUIRE(is_float_dtype(dtype), SQX_E_ARG, "sqx_mxfp4_fake_quant_rows: bad dtype %d", dtype);
+  SQX_REQUIRE(m >= 0 && k > 0 && k % 32 == 0 && m <= ((int64_t)1 << 31) && k <= ((int64_t)1 << 30), SQX_E_ARG,
+              "sqx_mxfp4_fake_quant_rows: bad shape [%lld, %lld] (k must be a multiple of 32)", (long long)m,
+              (long long)k);
+  if (m == 0) return SQX_OK;
+  SQX_REQUIRE(x && out, SQX_E_ARG, "sqx_mxfp4_fake_quant_rows: null pointer");
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0, SQX_E_ARG,
+              "sqx_mxfp4_fake_quant_rows: x and out must be 16-byte aligned");
+  const int64_t nb = m * (k / 32);
+  hipStream_t s = as_stream(stream);
+  if (dtype == SQX_DTYPE_BF16)
+    hipLaunchKernelGGL(mxfp4_fake_quant_rows_kernel<SQX_DTYPE_BF16>, grid_for(nb), dim3(256), 0, s, x, nb, out);
+  else if (dtype == SQX_DTYPE_F16)
+    hipLaunchKernelGGL(mxfp4_fake_quant_rows_kernel<SQX_DTYPE_F16>, grid_for(nb), dim3(256), 0, s, x, nb, out);
+  else
+    hipLaunchKernelGGL(mxfp4_fake_quant_rows_kernel<SQX_DTYPE_F32>, grid_for(nb), dim3(256), 0, s, x, nb, out);
+  SQX_LAUNCH_CHECK("sqx_mxfp4_fake_quant_rows");
+  return SQX_OK;
+}
+
 extern "C" int sqx_mxfp4_quantize_tiled(const void* x, int dtype, int64_t m, int64_t k, uint8_t* xt, uint8_t* xst,
                                         sqx_stream_t stream) {
   SQX_REQUIRE(is_float_dtype(dtype), SQX_E_ARG, "sqx_mxfp4_quantize_tiled: bad dtype %d", dtype);
@@ -916,7 +1040,8 @@ extern "C" int sqx_sum_halves(const float* y2, int64_t n, float* y, sqx_stream_t
 
 extern "C" int sqx_nvfp4_ceil_quantize(const void* x, int dtype, int64_t rows, int64_t k, uint8_t* packed,
                                        uint8_t* scales, int* status, sqx_stream_t stream) {
-  SQX_REQUIRE(is_float_dtype(dtype), SQX_E_ARG, "sqx_nvfp4_ceil_quantize: bad dtype %d", dtype);
+  SQX_REQUIRE(is_float_dtype(dtype) || dtype == SQX_DTYPE_F64, SQX_E_ARG, "sqx_nvfp4_ceil_quantize: bad dtype %d",
+              dtype);
   SQX_REQUIRE(rows >= 0 && k > 0 && k % 16 == 0, SQX_E_ARG,
               "quantize_nvfp4: K=%lld is not a multiple of SF_VEC_SIZE=16", (long long)k);
   const int64_t nblk = rows * (k / 16);

@@ -401,8 +401,9 @@ class Int4DecodeLM:
         fuse_silu = self.fuse_silu and lib.sqx_int4_prologue_fits(B, cfg.d_ff)
         sums = (self.fuse_norm_sums and B == 1 and d <= 8192 and lib.sqx_int4_prologue_fits(1, d)
                 and lib.sqx_int4_prologue_fits(1, cfg.d_ff))
-        # one row with a bf16 cache: RoPE and the cache write run in the q|k|v projection's epilogue
-        rope_in_qkv = sums and st.kv_dtype == "bf16"
+        # one row with a bf16 cache: RoPE and the cache write run in the q|k|v projection's epilogue,
+        # which takes fewer than 1024 row tiles of 16 (wider projections keep the separate RoPE)
+        rope_in_qkv = sums and st.kv_dtype == "bf16" and (H + 2 * Hkv) * hd // 16 < 1024
         # one row: the attention combine runs in the o projection's activation load (two 128-column
         # k-blocks per wave)
         kb_o = d // 128

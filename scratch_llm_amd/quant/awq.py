@@ -33,6 +33,7 @@ from scratch_llm_amd.quant.int4_group import (  # noqa: F401  (module attributes
     mse,
     quantize_groupwise_int4,
     tile_int4,
+    tiled_group,
 )
 
 __all__ = [
@@ -187,8 +188,11 @@ def awq_linear(x: Tensor, quant: AWQQuant, bias: Tensor | None = None) -> Tensor
     computed as the int4 linear of ``x / s`` against the codes of ``W * s``."""
     _lib.require_device(x, quant.q, quant.chan_scale, bias, fn="awq_linear")
     g = quant.group_size
-    if g not in TILED_GROUPS:
-        raise ValueError(f"awq_linear: group_size={g} is not supported by the MI355X kernels {TILED_GROUPS}")
+    try:
+        tiled_group(g)
+    except ValueError:
+        raise ValueError(f"awq_linear: group_size={g} is not supported by the MI355X kernels (one of "
+                         f"{TILED_GROUPS} or a multiple of 32)") from None
     tw = _tiled_cache.get((quant.q, quant.group_scales), (g,), lambda: tile_int4(quant.q, quant.group_scales, None, g))
     return awq_linear_tiled(x, tw, quant.chan_scale, bias)
 

@@ -196,7 +196,9 @@ class PerHeadFp8KVCache:
     def scales(self, layer: int) -> tuple[Tensor | None, Tensor | None]:
         if not self._has_scale[layer]:
             return None, None
-        row = self._scale_t[layer]
+        # copies: a later set_scales rewrites the device rows in place, and the reference hands out
+        # tensors that a later install replaces rather than changes
+        row = self._scale_t[layer].clone()
         return row[0].view(1, -1, 1, 1), row[1].view(1, -1, 1, 1)
 
     def set_scales(self, layer: int, k_scale: Tensor, v_scale: Tensor) -> None:
@@ -246,10 +248,11 @@ class PerHeadFp8KVCache:
         self._fill[layer] = f0 + t
 
     def _planes(self, layer: int) -> tuple[Tensor, Tensor] | None:
+        """Views of the filled K and V code planes (aliases of the internal buffer)."""
         buf, fill = self._buf[layer], self._fill[layer]
         if buf is None or fill == 0:
             return None
-        return buf[0, :, :, :fill].contiguous(), buf[1, :, :, :fill].contiguous()
+        return buf[0, :, :, :fill], buf[1, :, :, :fill]
 
     def get(self, layer: int) -> tuple[Tensor, Tensor] | None:
         planes = self._planes(layer)
@@ -259,10 +262,12 @@ class PerHeadFp8KVCache:
         return dequantize_per_head(planes[0], k_s, self.dtype), dequantize_per_head(planes[1], v_s, self.dtype)
 
     def codes(self, layer: int) -> tuple[Tensor, Tensor] | None:
+        """Fresh contiguous copies of the stored codes (``float8_e4m3fn``), as the reference's
+        ``torch.cat`` returns: writing to them leaves the cache unchanged."""
         planes = self._planes(layer)
         if planes is None:
             return None
-        return planes[0].view(FP8_DTYPE), planes[1].view(FP8_DTYPE)
+        return tuple(p.clone(memory_format=torch.contiguous_format).view(FP8_DTYPE) for p in planes)
 
 
 def _quantize_into(x: Tensor, scale: Tensor, sat: Tensor) -> tuple[Tensor, Tensor]:

@@ -263,18 +263,11 @@ def convert_linears_to_fp8(root: nn.Module, *, skip: tuple[str, ...] = DEFAULT_S
                            use_fast_accum: bool = DEFAULT_FAST_ACCUM) -> list[str]:
     """Replace every ``nn.Linear`` under ``root`` with :class:`Fp8Linear`, in place; returns the
     qualified names replaced (fp8_weights.py:368-400: a child whose local name contains a ``skip``
-    entry, or whose ``in_features`` is not a multiple of ``min_in_features``, is left alone)."""
-    replaced: list[str] = []
-    for name, child in list(root.named_children()):
-        if isinstance(child, nn.Linear):
-            if any(s in name for s in skip) or child.in_features % min_in_features != 0:
-                continue
-            setattr(root, name, Fp8Linear.from_linear(child, use_fast_accum=use_fast_accum))
-            replaced.append(name)
-        else:
-            replaced.extend(
-                f"{name}.{sub}"
-                for sub in convert_linears_to_fp8(child, skip=skip, min_in_features=min_in_features,
-                                                  use_fast_accum=use_fast_accum)
-            )
-    return replaced
+    entry, or whose ``in_features`` is not a multiple of ``min_in_features``, is left alone). The walk
+    is the one every converter of this package shares (``modules._convert``), restricted to
+    ``nn.Linear`` as the reference's FP8 converter is."""
+    from scratch_llm_amd.quant import modules  # the module converters import this one's neighbours
+
+    return modules._convert(
+        root, lambda m: Fp8Linear.from_linear(m, use_fast_accum=use_fast_accum),
+        lambda m: isinstance(m, nn.Linear) and m.in_features % min_in_features == 0, skip)

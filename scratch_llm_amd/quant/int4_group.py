@@ -177,7 +177,8 @@ class Int4Tiled:
     zt: Tensor | None
     rows: int
     cols: int
-    group_size: int
+    group_size: int  # the kernels' group: 32, 64 or 128
+    param_repeat: int = 1  # consecutive kernel groups that share one parameter of the source group
 
     @property
     def device(self) -> torch.device:
@@ -190,9 +191,24 @@ class Int4Tiled:
         )
 
 
+def tiled_group(group_size: int) -> int:
+    """The kernels' group (128, 64 or 32) for groups of ``group_size`` columns: the largest of them
+    that divides it. A wider group (e.g. the reference tests' ``group_size = in_features``) runs as
+    ``group_size // tiled_group`` kernel groups with its parameters repeated, so the dequantized
+    weights are the same. ValueError for a group that is not a multiple of 32."""
+    for g in (128, 64, 32):
+        if group_size > 0 and group_size % g == 0:
+            return g
+    raise ValueError(f"group_size={group_size} is not supported by the tiled kernels (one of {TILED_GROUPS} "
+                     "or a multiple of 32)")
+
+
 def _check_tiled_group(group_size: int) -> None:
-    if group_size not in TILED_GROUPS:
-        raise ValueError(f"group_size={group_size} is not supported by the tiled kernels {TILED_GROUPS}")
+    tiled_group(group_size)
+
+
+def _repeat_params(t: Tensor | None, rep: int) -> Tensor | None:
+    return t if t is None or rep == 1 else t.repeat_interleave(rep, dim=1)
 
 
 def tile_int4(
@@ -208,13 +224,15 @@ def tile_int4(
     rows, cols = q.shape
     if cols % group_size != 0:
         raise ValueError(f"in_features={cols} not divisible by group_size={group_size}")
-    _check_tiled_group(group_size)
+    tg = tiled_group(group_size)
+    rep = group_size // tg
     dev = _lib.require_device(q, scales, zeros, fn="tile_int4")
     pdt = torch.float32 if zeros is None else scales.dtype
     if pdt not in (torch.float32, torch.bfloat16):
         pdt = torch.float32
-    s = scales.to(pdt).contiguous()
-    z = None if zeros is None else zeros.to(pdt).contiguous()
+    s = _repeat_params(scales.to(pdt), rep).contiguous()
+    z = None if zeros is None else _repeat_params(zeros.to(pdt), rep).contiguous()
+    group_size = tg
     lib = _lib.load()
     wt = torch.empty(lib.sqx_int4_tiled_weight_bytes(rows, cols), dtype=torch.uint8, device=dev)
     npar = lib.sqx_int4_tiled_param_count(rows, cols, group_size)
@@ -228,7 +246,7 @@ def tile_int4(
             group_size, _lib.ptr(wt), _lib.ptr(st), _lib.ptr(zt), _lib.stream_ptr(dev),
         )
     _lib.check(rc, "tile_int4")
-    return Int4Tiled(wt, st, zt, rows, cols, group_size)
+    return Int4Tiled(wt, st, zt, rows, cols, group_size, rep)
 
 
 def tile_int4_packed(packed: Tensor, scales: Tensor, shape: tuple[int, int], group_size: int = GROUP_SIZE) -> Int4Tiled:
@@ -237,13 +255,15 @@ def tile_int4_packed(packed: Tensor, scales: Tensor, shape: tuple[int, int], gro
     rows, cols = shape
     if cols % group_size != 0:
         raise ValueError(f"in_features={cols} not divisible by group_size={group_size}")
-    _check_tiled_group(group_size)
+    tg = tiled_group(group_size)
+    rep = group_size // tg
     if packed.numel() != (rows * cols + 1) // 2:
         raise ValueError(f"packed has {packed.numel()} bytes, expected {(rows * cols + 1) // 2} for {shape}")
     dev = _lib.require_device(packed, scales, fn="tile_int4_packed")
     lib = _lib.load()
     p8 = packed.to(torch.uint8).contiguous()
-    s = scales.to(torch.float32).contiguous()
+    s = _repeat_params(scales.to(torch.float32), rep).contiguous()
+    group_size = tg
     wt = torch.empty(lib.sqx_int4_tiled_weight_bytes(rows, cols), dtype=torch.uint8, device=dev)
     st = torch.empty(lib.sqx_int4_tiled_param_count(rows, cols, group_size), dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
@@ -252,7 +272,7 @@ def tile_int4_packed(packed: Tensor, scales: Tensor, shape: tuple[int, int], gro
             _lib.stream_ptr(dev),
         )
     _lib.check(rc, "tile_int4_packed")
-    return Int4Tiled(wt, st, None, rows, cols, group_size)
+    return Int4Tiled(wt, st, None, rows, cols, group_size, rep)
 
 
 def untile_int4(tw: Int4Tiled) -> tuple[Tensor, Tensor, Tensor | None]:
@@ -269,6 +289,9 @@ def untile_int4(tw: Int4Tiled) -> tuple[Tensor, Tensor, Tensor | None]:
         _lib.check(lib.sqx_int4_untile(tw.wt.data_ptr(), tw.st.data_ptr(), _lib.ptr(tw.zt), _lib.sqx_dtype(tw.st.dtype),
                                        0 if tw.zt is None else 1, tw.rows, tw.cols, tw.group_size, codes.data_ptr(),
                                        scales.data_ptr(), _lib.ptr(zeros), _lib.stream_ptr(dev)), "untile_int4")
+    if tw.param_repeat > 1:  # one parameter per source group
+        scales = scales[:, ::tw.param_repeat].contiguous()
+        zeros = None if zeros is None else zeros[:, ::tw.param_repeat].contiguous()
     return codes, scales, zeros
 
 
@@ -414,13 +437,17 @@ def w4a16_linear(
 
     The fused dequant kernels run on a tiled copy of ``q`` that is built on first use and cached
     until ``q`` or ``scales`` changes. bf16/fp16 activations run as they are; fp32 activations run
-    as three bf16 rows that sum to x exactly, with fp32 outputs (:func:`int4_linear_tiled_f32`). ``group_size`` must be 32, 64 or 128 (ValueError otherwise),
-    and x must be fp32, bf16 or fp16 (TypeError otherwise).
+    as three bf16 rows that sum to x exactly, with fp32 outputs (:func:`int4_linear_tiled_f32`).
+    ``group_size`` must be a multiple of 32 (ValueError otherwise; a group wider than 128 runs as
+    groups of 128, 64 or 32 with its scale repeated), and x must be fp32, bf16 or fp16 (TypeError
+    otherwise).
     """
     _lib.require_device(x, q, scales, bias, fn="w4a16_linear")
-    if group_size not in TILED_GROUPS:
+    try:
+        tiled_group(group_size)
+    except ValueError:
         raise ValueError(f"w4a16_linear: group_size={group_size} is not supported by the MI355X kernels "
-                         f"{TILED_GROUPS}")
+                         f"(one of {TILED_GROUPS} or a multiple of 32)") from None
     if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
         raise TypeError(f"w4a16_linear takes fp32, bf16 or fp16 activations, got {x.dtype}")
     if q.shape[1] % group_size != 0:

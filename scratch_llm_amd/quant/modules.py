@@ -102,7 +102,9 @@ class Int4Linear(_QuantLinear):
                    group_size)
 
     def tiled(self) -> int4_group.Int4Tiled:
-        return int4_group.Int4Tiled(self.wt, self.st, None, self.out_features, self.in_features, self.group_size)
+        tg = int4_group.tiled_group(self.group_size)
+        return int4_group.Int4Tiled(self.wt, self.st, None, self.out_features, self.in_features, tg,
+                                    self.group_size // tg)
 
     def codes(self) -> Tensor:
         return int4_group.untile_int4(self.tiled())[0]
@@ -154,7 +156,9 @@ class AWQLinear(_QuantLinear):
         return cls(quant, None if b is None else b.clone())
 
     def tiled(self) -> int4_group.Int4Tiled:
-        return int4_group.Int4Tiled(self.wt, self.st, None, self.out_features, self.in_features, self.group_size)
+        tg = int4_group.tiled_group(self.group_size)
+        return int4_group.Int4Tiled(self.wt, self.st, None, self.out_features, self.in_features, tg,
+                                    self.group_size // tg)
 
     @property
     def q(self) -> Tensor:

@@ -106,13 +106,16 @@ def quantize_nvfp4(x: Tensor) -> NVFP4Operand:
         raise ValueError(f"quantize_nvfp4: K={k} is not a multiple of SF_VEC_SIZE={SF_VEC_SIZE}; a partial "
                          "scale block has no encoding")
     dev = _lib.require_device(x, fn="quantize_nvfp4")
-    xx = x if x.dtype in (torch.float32, torch.bfloat16, torch.float16) else x.to(torch.float32)
+    # The kernel works in float64 as the reference's x.to(float64); fp32 / bf16 / fp16 / fp64 are read
+    # as they are, any other real dtype is widened to float64 first (exact below 2**53).
+    xx = x if x.dtype in (torch.float32, torch.bfloat16, torch.float16, torch.float64) else x.to(torch.float64)
     xx = xx.contiguous()
+    dt = _lib.DTYPE_F64 if xx.dtype == torch.float64 else _lib.sqx_dtype(xx.dtype)
     packed = torch.empty(rows, k // 2, dtype=torch.uint8, device=dev)
     scales = torch.empty(rows, k // SF_VEC_SIZE, dtype=torch.uint8, device=dev)
     status = torch.zeros(1, dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
-        _lib.check(_lib.load().sqx_nvfp4_ceil_quantize(xx.data_ptr(), _lib.sqx_dtype(xx.dtype), rows, k,
+        _lib.check(_lib.load().sqx_nvfp4_ceil_quantize(xx.data_ptr(), dt, rows, k,
                                                        packed.data_ptr(), scales.data_ptr(), status.data_ptr(),
                                                        _stream(xx)), "quantize_nvfp4")
     _raise_on(status, "quantize_nvfp4")
@@ -221,6 +224,8 @@ def scale_for_amax(amax: Tensor) -> tuple[Tensor, Tensor]:
 
 
 def e2m1_round_code(values: Tensor) -> Tensor:
-    """Nearest E2M1 code of already-scaled values, ties to even, saturating at ±6, zero as +0
-    (nvfp4_layout.py:390-416, b_r6.py:217-223)."""
+    """Nearest E2M1 code of already-scaled values, ties to even, saturating at ±6, with the sign bit
+    set for every negative value (nvfp4_layout.py:390-416: ``code = 8 if value < 0``, so -0.2 gives
+    0x8 and -0.0 gives 0x0). ``quantize_nvfp4`` instead stores a value that rounds to zero as +0
+    (b_r6.py:217-223)."""
     return _elementwise(values, "e2m1_round_code", None)[0]

@@ -10,7 +10,8 @@ quantized weight without materialising it (``F.linear(x, dequ
 and :func:`quant_linear_nvfp4` keeps the reference's signature. Config 4's MXFP4-activation variant
 (``mxfp4_linear(..., quantize_activations=True)``) quantizes the activation rows into the same tiled
 layout (:func:`mxfp4_quantize_tiled`) and multiplies on CDNA4's block-scaled fp4 MFMA
-(:func:`mxfp4_gemm`).
+(:func:`mxfp4_gemm`); at a few bf16 rows it streams the weight through the FP4 GEMV with the
+dequantized activation rows instead (:func:`mxfp4_fake_quant_rows`, exact in bf16).
 """
 
 from __future__ import annotations
@@ -34,6 +35,7 @@ __all__ = [
     "MXFP4_GROUP",
     "dequantize_mxfp4",
     "mxfp4_dequantize",
+    "mxfp4_fake_quant_rows",
     "mxfp4_gemm",
     "mxfp4_pack_weight",
     "mxfp4_linear",
@@ -446,11 +448,20 @@ def tile_mxfp4_packed(weight_packed: Tensor, weight_scale: Tensor) -> FP4Tiled:
 
 def dequantize_mxfp4(weight_packed: Tensor, weight_scale: Tensor, *, dtype: torch.dtype = torch.float32) -> Tensor:
     """``w[r, c] = E2M1(code[r, c]) * 2**(weight_scale[r, c // 32] - 127)`` as ``[out, in]`` in ``dtype``
-    (k3/checkpoint.py:92-144): the E2M1 decode and the scaling run in the HIP kernels in fp32, where every
-    value below 2**128 is exact (E8M0 code 0 is 2**-127, a subnormal); values that overflow fp32, and
-    casts to ``dtype`` that change a value, raise ``ValueError`` as in the reference."""
+    (k3/checkpoint.py:92-144). ``dtype=float64``: one HIP kernel decodes straight into float64, where
+    every value of every E8M0 code is exact (so nothing raises, as in the reference). Other dtypes: the
+    E2M1 decode and the scaling run in the HIP kernels in fp32, where every value below 2**128 is exact
+    (E8M0 code 0 is 2**-127, a subnormal); values that overflow fp32, and casts to ``dtype`` that change
+    a value, raise ``ValueError`` as in the reference."""
     rows, cols = _check_mxfp4_pair(weight_packed, weight_scale)
-    _lib.require_device(weight_packed, weight_scale, fn="dequantize_mxfp4")
+    dev = _lib.require_device(weight_packed, weight_scale, fn="dequantize_mxfp4")
+    if dtype == torch.float64:
+        out = torch.empty(rows, cols, dtype=torch.float64, device=dev)
+        with torch.cuda.device(dev):
+            _lib.check(_lib.load().sqx_mxfp4_pair_dequantize_f64(
+                weight_packed.contiguous().data_ptr(), weight_scale.contiguous().data_ptr(), rows, cols,
+                out.data_ptr(), _stream(out)), "dequantize_mxfp4")
+        return out
     codes = unpack_fp4(weight_packed.reshape(-1), rows * cols)
     b = weight_scale.reshape(-1).to(torch.int32)
     s_block = torch.where(b == 0, torch.full_like(b, 0x00400000), b << 23).view(torch.float32)
@@ -523,10 +534,12 @@ def mxfp4_linear(x: Tensor, q: MXFP4Tensor, bias: Tensor | None = None, quantize
     (BASELINE config 4's composition), without materialising the weight. Output in ``x.dtype``.
 
     ``quantize_activations=True`` is config 4's MXFP4-activation variant: each row of ``x`` goes
-    through ``mxfp4_quantize`` too, and the product of the two dequantized operands runs on the
-    block-scaled fp4 MFMA (exact products, fp32 accumulation). It matches the composition with
-    ``.to(x.dtype)`` wherever the dequantized values are representable in ``x.dtype`` (always for
-    bf16 and fp32)."""
+    through ``mxfp4_quantize`` too, and the product of the two dequantized operands is formed with
+    exact products and fp32 accumulation: on the block-scaled fp4 MFMA GEMM, or, for bf16 ``x`` of at
+    most ``MXFP4_ACT_GEMV_MAX_M`` rows, as the dequantized rows (exact in bf16,
+    ``sqx_mxfp4_fake_quant_rows``) through the weight-streaming FP4 GEMV. It matches the composition
+    with ``.to(x.dtype)`` wherever the dequantized values are representable in ``x.dtype`` (always
+    for bf16 and fp32)."""
     tw = _tiled(q)
     if not quantize_activations:
         return fp4_linear_tiled(x, tw, bias)
@@ -535,8 +548,37 @@ def mxfp4_linear(x: Tensor, q: MXFP4Tensor, bias: Tensor | None = None, quantize
         raise ValueError(f"x has in_features={k}, weight expects {tw.cols}")
     if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
         raise TypeError(f"the FP4 linear takes fp32, bf16 or fp16 activations, got {x.dtype}")
-    xq = mxfp4_quantize_tiled(x.reshape(-1, k))
+    x2 = x.reshape(-1, k)
+    if x.dtype == torch.bfloat16 and x2.shape[0] <= MXFP4_ACT_GEMV_MAX_M:
+        return fp4_linear_tiled(mxfp4_fake_quant_rows(x2), tw, bias).reshape(*batch, tw.rows)
+    xq = mxfp4_quantize_tiled(x2)
     return mxfp4_gemm(xq, tw, bias, x.dtype).reshape(*batch, tw.rows)
+
+
+# Rows up to which config 4's activation-quantized linear streams the weight through the FP4 GEMV
+# instead of the 256-row fp4 MFMA GEMM (Llama-3-70B MLP shapes, rotating weights: at M = 1 the GEMV
+# path takes 29.6 / 33.1 us against 64.1 / 43.5 us, at M = 2 37.5 / 44.5 against 63.3 / 43.6 us; from
+# M = 4 the GEMM is as fast or faster).
+MXFP4_ACT_GEMV_MAX_M = 2
+
+
+def mxfp4_fake_quant_rows(x: Tensor) -> Tensor:
+    """``mxfp4_dequantize(mxfp4_quantize(row))`` of each row of a 2-D ``x`` ``[m, k]`` (``k % 32 == 0``)
+    as bf16 ``[m, k]``, exact (an E2M1 value times a power of two has 2 significant bits)."""
+    if x.dim() != 2:
+        raise ValueError(f"expected 2-D activations [m, k], got shape {tuple(x.shape)}")
+    m, k = int(x.shape[0]), int(x.shape[1])
+    if k % 32 != 0:
+        raise ValueError(f"K={k} must be a multiple of 32 for per-row MXFP4 activation blocks")
+    dev = _lib.require_device(x, fn="mxfp4_fake_quant_rows")
+    xc = _float_input(x, "mxfp4_fake_quant_rows")
+    if not xc.is_contiguous() or xc.data_ptr() % 16:
+        xc = xc.contiguous()
+    out = torch.empty(m, k, dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().sqx_mxfp4_fake_quant_rows(xc.data_ptr(), _lib.sqx_dtype(xc.dtype), m, k,
+                                                         out.data_ptr(), _stream(xc)), "mxfp4_fake_quant_rows")
+    return out
 
 
 def nvfp4_linear(x: Tensor, q: NVFP4Tensor, bias: Tensor | None = None) -> Tensor:

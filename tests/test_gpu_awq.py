@@ -137,6 +137,24 @@ def test_awq_linear_config3(aw, n, k, m):
     _check_linear(y[:rows], R.linear_f64(x[:rows].float().cpu().numpy(), w_eff), f"awq {k}->{n} M={m}")
 
 
+@pytest.mark.parametrize("group,m", [(256, 1), (512, 8), (4096, 64), (1024, 300)])
+def test_awq_linear_wide_groups(aw, group, m):
+    """AWQ with groups wider than 128 (awq.py:184-192 takes any group dividing in_features)."""
+    print_case("awq wide group", group, m)
+    n, k = 512, 4096
+    g = torch.Generator(device=DEV).manual_seed(group + m)
+    w = torch.randn(n, k, generator=g, device=DEV) * 0.02
+    s = _chan_scale(k, group).to(DEV)
+    quant = aw.quantize_awq_int4(w, chan_scale=s, group_size=group)
+    assert quant.group_scales.shape == (n, k // group)
+    x = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16)
+    y = aw.awq_linear(x, quant)
+    rows = min(m, 64)
+    w_eff = R.round_bf16(R.awq_dequantize(quant.q.cpu().numpy(), quant.group_scales.cpu().numpy(),
+                                          quant.chan_scale.cpu().numpy(), group))
+    _check_linear(y[:rows], R.linear_f64(x[:rows].float().cpu().numpy(), w_eff), f"awq g{group} M={m}")
+
+
 def test_awq_linear_bias_fp16(aw):
     w, x32, _ = awq_layer(5, n_tokens=32)
     wt = torch.from_numpy(w).to(DEV)

@@ -187,12 +187,14 @@ def test_config5_full_model_graph_equals_eager(B):
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("B", [1, 8])
+@pytest.mark.parametrize("B", [1, 8, 32, 64])
 def test_config5_full_width_against_oracle(B):
     """A two-layer model at Llama-3-8B width (d 4096, 32 q / 8 kv heads, SwiGLU 14336, vocab 128256,
     context 2048 with 2046 random cached keys per row) for two steps against the decode oracle's bf16
     composition and fp32 run on 8192 sampled logits; the second layer reads the first's residual sums
-    at B = 1. Codes of the quantized weights are bit-exact with the oracle quantizer on sampled rows,
+    at B = 1. At B = 32 and 64 the step runs every row (the row-tiled linears, K-split partials folded
+    into the norms, 1024-key attention chunks) and the oracle follows 8 sampled rows (rows do not
+    interact). Codes of the quantized weights are bit-exact with the oracle quantizer on sampled rows,
     and the oracle dequantizes the same codes."""
     from scratch_llm_amd.decode import LLAMA3_8B, Int4DecodeLM
     from scratch_llm_amd.quant import int4_group as i4
@@ -240,12 +242,17 @@ def test_config5_full_width_against_oracle(B):
 
     st = model.new_state(B, ctx)
     _fill_cache(st, 17 + B, ctx - 2)  # the two steps write positions 2046 and 2047, the last RoPE rows
+    if B <= 8:
+        rows = list(range(B))
+    else:
+        rows = sorted({0, B - 1, *np.random.default_rng(B).choice(B, 6, replace=False).tolist()})
+    rt = torch.tensor(rows)
     caches = {}
     for dt in (torch.bfloat16, torch.float32):
-        c = D.RefCache.empty(ref32, B, ctx, dt)
+        c = D.RefCache.empty(ref32, len(rows), ctx, dt)
         for li in range(cfg.n_layers):
-            c.k[li].copy_(st.k[li].cpu().to(dt))
-            c.v[li].copy_(st.v[li].cpu().to(dt))
+            c.k[li].copy_(st.k[li][rt.to(DEV)].cpu().to(dt))
+            c.v[li].copy_(st.v[li][rt.to(DEV)].cpu().to(dt))
         c.lengths[:] = ctx - 2
         caches[dt] = c
     tok = torch.randint(0, cfg.vocab_size, (B,), generator=torch.Generator().manual_seed(B + 1))
@@ -253,15 +260,16 @@ def test_config5_full_width_against_oracle(B):
         print_case("config5 full width step", B, t)
         nxt = model.step(st, tok)
         torch.cuda.synchronize()
-        got = st.logits[:, colt].float().cpu()
-        l16 = D.decode_step(ref16, caches[torch.bfloat16], tok, torch.bfloat16).float()
-        l32 = D.decode_step(ref32, caches[torch.float32], tok, torch.float32)
+        got = st.logits[rt.to(DEV)][:, colt].float().cpu()
+        l16 = D.decode_step(ref16, caches[torch.bfloat16], tok[rt], torch.bfloat16).float()
+        l32 = D.decode_step(ref32, caches[torch.float32], tok[rt], torch.float32)
         scale = float(l32.abs().max())
         e_hip = float((got - l32).abs().max())
         e_ref = float((l16 - l32).abs().max())
         assert e_hip <= 2 * e_ref + 2.0**-9 * scale, f"B={B} t={t}: |hip-f32| {e_hip:.4g} vs |bf16 ref-f32| {e_ref:.4g}"
         assert torch.equal(nxt.cpu().long(), st.logits.float().argmax(-1).cpu())
-        assert st.lengths.cpu().tolist() == caches[torch.float32].lengths.tolist()
+        assert st.lengths.cpu().tolist() == [ctx - 1 + t] * B
+        assert caches[torch.float32].lengths.tolist() == [ctx - 1 + t] * len(rows)
         tok = nxt.cpu().long()
     del model, st, p
     torch.cuda.empty_cache()

@@ -131,9 +131,11 @@ def _attn_case(lib, B, H, Hkv, T, lengths, seed):
 
 
 def test_attention_rows_independent_of_batch(lib):
-    """A row's output does not depend on the other rows of the batch: B = 2 and B = 3 (both with
-    128-key chunks) agree bit for bit on rows 0 and 1, and cache rows past each length, filled with
-    NaN, reach neither."""
+    """A row's output does not depend on the other rows of the batch at a given key-chunk size: B = 2
+    and B = 3 (both with 128-key chunks) agree bit for bit on rows 0 and 1. The chunk size is chosen
+    from B, so B = 8 (512-key chunks) may differ in the last bits; rows 0 and 1 of B = 2 and B = 8 are
+    each within the attention bound of float64. Cache rows past each length, filled with NaN, reach
+    none of them."""
     print_case("attention early rows")
     B, H, Hkv, T, hd = 8, 32, 8, 2048, 128
     g = torch.Generator().manual_seed(77)
@@ -161,6 +163,7 @@ def test_attention_rows_independent_of_batch(lib):
     assert torch.equal(outs[2], outs[3][:2])
     G = H // Hkv
     got = outs[8].view(B, H, hd).double()
+    got2 = outs[2].view(2, H, hd).double()
     for b in range(B):
         L = lengths[b] + 1
         kk = k[b, :, :L].double().repeat_interleave(G, dim=0)
@@ -169,6 +172,11 @@ def test_attention_rows_independent_of_batch(lib):
         want = torch.einsum("ht,htd->hd", p, vv)
         bound = 2.0**-8 * want.abs() + 1e-5 * vv.abs().max()
         assert float(((got[b] - want).abs() / bound).max()) <= 1.0, f"row {b}"
+        if b < 2:
+            # B = 8 takes 512-key chunks, B = 2 128-key chunks: the row's bits may differ between
+            # the two, but both stay within the attention bound, so they agree to twice that bound
+            assert float(((got2[b] - want).abs() / bound).max()) <= 1.0, f"row {b} at B=2"
+            assert float(((got2[b] - got[b]).abs() / (2 * bound)).max()) <= 1.0, f"row {b}: B=2 vs B=8"
 
 
 @pytest.mark.parametrize("H,Hkv", [(32, 8), (8, 8), (16, 8), (16, 2)])
@@ -921,6 +929,33 @@ def test_attn_merge_step_matches_reference_both_ways(small):
             _run_and_compare(model, refs, 1, steps=5, seed=23)
     finally:
         model.fuse_attn_merge = False
+
+
+def test_one_row_step_with_1024_or_more_qkv_tiles():
+    """A one-row step whose fused q|k|v projection has 1024 or more row tiles of 16 (MHA, 43 heads:
+    129 heads of 128 rows = 1032 tiles) keeps the separate RoPE (the epilogue form takes fewer than
+    1024 tiles): eager steps match the reference and graph replays equal them."""
+    from scratch_llm_amd.decode import DecodeConfig, Int4DecodeLM
+
+    print_case("one-row step, 1032 qkv tiles")
+    dims = dict(vocab=512, d_model=43 * 128, n_layers=1, n_heads=43, n_kv_heads=43, d_ff=512)
+    p = D.random_params(**dims, seed=5, std=0.02)
+    cfg = DecodeConfig(vocab_size=dims["vocab"], d_model=dims["d_model"], n_layers=1, n_heads=43, n_kv_heads=43,
+                       d_ff=dims["d_ff"], context_length=16)
+    model = Int4DecodeLM.from_state_dict(cfg, lambda n: p[n], DEV)
+    refs = {dt: D.int4_model(p, n_layers=1, n_heads=43, n_kv_heads=43, context_length=16, dtype=dt)
+            for dt in (torch.bfloat16, torch.float32)}
+    _run_and_compare(model, refs, 1, steps=3, seed=3, max_ctx=8)
+    a, b = model.new_state(1, 8), model.new_state(1, 8)
+    a.set_tokens(torch.tensor([7]), cfg.vocab_size)
+    b.set_tokens(torch.tensor([7]), cfg.vocab_size)
+    graph = model.capture(b)
+    for t in range(3):
+        model.step(a)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(a.logits, b.logits), f"replay {t}"
 
 
 def test_inactive_slots_do_not_leak(small):

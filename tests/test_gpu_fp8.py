@@ -315,3 +315,16 @@ def test_per_head_cache_contract():
     assert torch.equal(c2.scales(0)[0], one) and c2.k_saturated > 0
     with pytest.raises(ValueError, match=r"\(1, H, 1, 1\)"):
         c2.set_scales(0, one.view(-1), one)
+    # codes() and scales() hand out copies, as the reference's torch.cat and replaced scale tensors:
+    # a 16-token block fills the first buffer exactly, where a view would alias the storage
+    c3 = K.PerHeadFp8KVCache(n_layers=1)
+    c3.append(0, x, x)
+    before = c3.get(0)[0].clone()
+    ck, cv = c3.codes(0)
+    ck.view(torch.uint8).fill_(0)
+    cv.view(torch.uint8).fill_(0x7E)
+    assert torch.equal(c3.get(0)[0], before)
+    old_k, _ = c3.scales(0)
+    kept = old_k.clone()
+    c3.set_scales(0, one * 3, one * 3)
+    assert torch.equal(old_k, kept) and torch.equal(c3.scales(0)[0], one * 3)

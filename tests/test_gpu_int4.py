@@ -199,6 +199,66 @@ def test_linear_ragged_shapes(q4, n, k, group, m):
     assert y.shape == (m, n) and y.dtype == torch.bfloat16
 
 
+@pytest.mark.parametrize(
+    "n,k,group,m",
+    [
+        (256, 768, 768, 3),  # group = in_features (the reference tests' per-row scale): 6 groups of 128
+        (128, 4096, 4096, 1),  # one group per row at a Llama width, the one-row GEMV
+        (96, 1024, 256, 8),
+        (64, 288, 96, 2),  # 96 = 3 groups of 32
+        (64, 320, 320, 64),  # 320 = 5 groups of 64, the row-tiled kernels
+        (32, 512, 512, 100),  # the prefill GEMM
+    ],
+)
+def test_linear_wide_groups(q4, n, k, group, m):
+    """Groups wider than the kernels' 32 / 64 / 128 run as narrower groups with the scale repeated
+    (int4_group.py:148-164 takes any group dividing in_features): the linear matches the oracle, and
+    the tiles give back the reference's codes and one scale per source group."""
+    print_case("wide group", n, k, group, m)
+    w = _weight((n, k), n + k + group, std=0.05).to(DEV)
+    q, s = q4.quantize_groupwise_int4(w, group)
+    assert s.shape == (n, k // group)
+    x = _act(m, k, m + 1).to(DEV)
+    y = q4.w4a16_linear(x, q, s, group_size=group)
+    w_eff = R.round_bf16(R.dequantize_groupwise_int4(q.cpu().numpy(), s.cpu().numpy(), group))
+    _check_linear(y, R.linear_f64(x.float().cpu().numpy(), w_eff), f"{k}->{n} g{group} M={m}")
+    tw = q4.tile_int4(q, s, None, group)
+    assert tw.group_size == q4.tiled_group(group) and tw.param_repeat * tw.group_size == group
+    qb, sb, _ = q4.untile_int4(tw)
+    assert torch.equal(qb, q) and torch.equal(sb, s)
+    tp = q4.tile_int4_packed(q4.pack_int4(q.reshape(-1)), s, (n, k), group)
+    assert torch.equal(tp.wt, tw.wt) and torch.equal(tp.st, tw.st)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        q4.w4a16_linear(x, q, s, group_size=48)
+
+
+def test_wide_group_module_and_asymmetric(q4):
+    from scratch_llm_amd.quant import modules
+
+    print_case("wide group module")
+    lin = torch.nn.Linear(1024, 200, bias=True).to(DEV)
+    mod = modules.Int4Linear.from_linear(lin, group_size=512)
+    q, s = q4.quantize_groupwise_int4(lin.weight.detach(), 512)
+    assert torch.equal(mod.codes(), q) and torch.equal(mod.scales, s)
+    assert torch.equal(mod.dequantized_weight(), q4.dequantize_groupwise_int4(q, s, 512))
+    x = _act(5, 1024, 3).to(DEV)
+    assert torch.equal(mod(x), q4.w4a16_linear(x, q, s, bias=lin.bias.detach(), group_size=512))
+    # the build-defined asymmetric format with bf16 (scale, zero) pairs and 256-column groups
+    w = _weight((64, 1024), 4, dtype=torch.float32).numpy()
+    qa, sa, za = R.quantize_groupwise_uint4_asym(w, 256, param="bf16")
+    tw = q4.tile_int4(torch.from_numpy(qa).to(DEV), torch.from_numpy(sa).to(torch.bfloat16).to(DEV),
+                      torch.from_numpy(za).to(torch.bfloat16).to(DEV), 256)
+    for m in (1, 8, 80):
+        x = _act(m, 1024, 40 + m).to(DEV)
+        y = q4.int4_linear_tiled(x, tw)
+        w_eff = R.round_bf16(R.dequantize_groupwise_uint4_asym(qa, sa, za, 256))
+        _check_linear(y, R.linear_f64(x.float().cpu().numpy(), w_eff), f"asym g256 M={m}")
+    qb, sb, zb = q4.untile_int4(tw)
+    assert np.array_equal(qb.cpu().numpy(), qa)
+    assert torch.equal(sb.cpu(), torch.from_numpy(sa).to(torch.bfloat16))
+    assert torch.equal(zb.cpu(), torch.from_numpy(za).to(torch.bfloat16))
+
+
 def test_linear_zero_and_outlier_rows_bias_fp16(q4):
     n, k = 256, 1024
     w = _weight((n, k), 9, std=0.02, dtype=torch.float32)

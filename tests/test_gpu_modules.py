@@ -153,6 +153,18 @@ def test_mxfp4_pair_loads_straight_into_the_kernel(mods):
     with pytest.raises(ValueError, match="not exact"):
         f4.dequantize_mxfp4(torch.full((1, 16), 0x07, dtype=torch.uint8, device=DEV),
                             torch.full((1, 1), 254, dtype=torch.uint8, device=DEV))
+    # float64 holds every value of every E8M0 code exactly (k3/checkpoint.py:136-144): scale byte 254
+    # with the largest codes (6 * 2**127 = 1.5 * 2**129) and every other code, against the oracle
+    big = f4.dequantize_mxfp4(torch.full((1, 16), 0xF7, dtype=torch.uint8, device=DEV),
+                              torch.full((1, 1), 254, dtype=torch.uint8, device=DEV), dtype=torch.float64).cpu()
+    assert big.dtype == torch.float64 and big[0, :2].tolist() == [6 * 2.0**127, -6 * 2.0**127]
+    rng = np.random.default_rng(3)
+    pk = rng.integers(0, 256, (255, 64), dtype=np.uint8)
+    e8 = np.repeat(np.arange(255, dtype=np.uint8)[:, None], 4, axis=1)  # every finite code, one per row
+    e8[::7, 1] = 0
+    got = f4.dequantize_mxfp4(torch.from_numpy(pk).to(DEV), torch.from_numpy(e8).to(DEV), dtype=torch.float64).cpu()
+    want = R.dequantize_mxfp4_checkpoint(pk, e8)
+    assert np.array_equal(got.numpy().view(np.uint64), want.view(np.uint64))
     # a linear on realistic scales: the pair of a quantized N(0, 0.02) weight
     wt = torch.randn(384, 1024, device=DEV) * 0.02
     q = f4.mxfp4_quantize(wt, 32)

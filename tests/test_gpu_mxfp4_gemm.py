@@ -308,6 +308,47 @@ def test_mxfp4_gemm_config4_sampled(f4, n, k, m):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("m", [1, 8])
+@pytest.mark.parametrize("n,k", [(28672, 8192), (8192, 28672)])
+def test_mxfp4_act_linear_config4_small_m(f4, n, k, m):
+    """Config 4's MXFP4-activation variant at M = 1 (and 8) on both Llama-3-70B MLP shapes: through
+    ``mxfp4_linear(quantize_activations=True)`` (the FP4 GEMV on the dequantized rows) and through the
+    fp4 MFMA GEMM, each against the product of the oracle's dequantized operands on 160 columns."""
+    print_case("mxfp4 act-quant linear config4", f"m={m}", f"n={n}", f"k={k}")
+    g = torch.Generator(device=DEV).manual_seed(2000 + n + m)
+    w = torch.randn(n, k, generator=g, device=DEV) * 0.02
+    x = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16)
+    q = f4.mxfp4_quantize(w, 32)
+    y = f4.mxfp4_linear(x, q, quantize_activations=True)
+    yg = f4.mxfp4_gemm(f4.mxfp4_quantize_tiled(x), f4.tile_fp4(q))
+    torch.cuda.synchronize()
+    assert y.shape == (m, n) and y.dtype == torch.bfloat16
+    ci = np.sort(np.concatenate([[0, n - 1], np.random.default_rng(n + m).choice(n, 158, replace=False)]))
+    _, _, xd = oracle_rows(x.float().cpu().numpy())
+    _, _, wd = oracle_rows(w[torch.from_numpy(ci).to(DEV)].cpu().numpy())
+    y_ref = xd @ wd.T
+    mag = np.abs(xd) @ np.abs(wd).T
+    cols = torch.from_numpy(ci).to(DEV)
+    _check_gemm(y[:, cols], y_ref, mag, torch.bfloat16, f"act-quant GEMV {m}x{n}x{k}", k, splits=16)
+    _check_gemm(yg[:, cols], y_ref, mag, torch.bfloat16, f"act-quant GEMM {m}x{n}x{k}", k, splits=16)
+    del w, q, y, yg
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_mxfp4_fake_quant_rows_bitexact(f4, dtype):
+    """bf16(mxfp4_dequantize(mxfp4_quantize(row))) per row equals the oracle bit for bit, including
+    all-zero blocks and values across many binades."""
+    print_case("mxfp4 fake-quant rows", dtype)
+    x = _values((40, 1024), 9)
+    x[3, :32] = 0.0
+    xt = _dev(x, dtype)
+    got = f4.mxfp4_fake_quant_rows(xt)
+    _, _, xd = oracle_rows(xt.float().cpu().numpy())
+    assert got.dtype == torch.bfloat16
+    assert np.array_equal(got.float().cpu().numpy(), xd.astype(np.float32))
+
+
 def test_mxfp4_gemm_rejects(f4):
     x = torch.randn(4, 64, device=DEV)
     xq = f4.mxfp4_quantize_tiled(x)

@@ -110,6 +110,52 @@ def test_elementwise_rules(nc, known_answers):
         nc.ue4m3_ceil_code(torch.tensor([500.0], device=DEV))
 
 
+def test_e2m1_sign_rules_code_bytes(nc, known_answers):
+    """As code bytes: the scalar helper keeps the sign of negatives that round to zero (-0.2 -> 0x8,
+    nvfp4_layout.py:402), the quantizer stores them as +0 (b_r6.py:217-223)."""
+    ka = known_answers["nvfp4_ceil"]
+    sc = ka["e2m1_scalar_codes"]
+    got = nc.e2m1_round_code(torch.tensor(sc["in"], dtype=torch.float64, device=DEV)).cpu().tolist()
+    assert got == sc["out"]
+    qc = ka["e2m1_quantizer_codes"]
+    vals = [v for v in qc["in"] if abs(v) > 1e-30 or v == 0.0]
+    row = torch.zeros(1, 16, dtype=torch.float32)
+    row[0, 0] = 6.0
+    row[0, 1:1 + len(vals)] = torch.tensor(vals)
+    op = nc.quantize_nvfp4(row.to(DEV))
+    p = op.packed.cpu()
+    codes = torch.stack((p & 0xF, p >> 4), dim=-1).reshape(-1).tolist()
+    assert int(op.scales.item()) == 0x38
+    assert codes == [7] + [qc["out"][qc["in"].index(v)] for v in vals] + [0] * (15 - len(vals))
+
+
+def test_quantize_float64_operand(nc):
+    """A float64 operand is quantized in float64, as the reference's ``x.to(float64)``: quotients one
+    float64 ulp off an E2M1 midpoint (which fp32 would round onto it) take the side they lie on."""
+    print_case("nvfp4 ceil quantize float64")
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((64, 256)) * np.exp2(rng.uniform(-10, 6, (64, 1)))
+    mids = np.array(C._MIDS)
+    for r in range(8):  # blocks of amax 6 (scale 1) whose entries sit just off every midpoint
+        x[r, :16] = 0.0
+        x[r, 0] = 6.0
+        x[r, 1:8] = np.nextafter(mids, 10.0 if r % 2 else -10.0)
+        x[r, 8:15] = -x[r, 1:8]
+        x[r, 15] = 1e-300 if r < 4 else -1e-300
+    xt = torch.from_numpy(x).to(DEV)
+    op = nc.quantize_nvfp4(xt)
+    pr, sr = C.quantize(x)
+    assert np.array_equal(op.scales.cpu().numpy(), sr) and np.array_equal(op.packed.cpu().numpy(), pr)
+    # the same operand read as fp32 would round those quotients onto the midpoints: different codes
+    p32, _ = C.quantize(x.astype(np.float32))
+    assert not np.array_equal(p32[:8], pr[:8])
+    # integer operands are widened to float64 as well
+    xi = torch.randint(-300, 300, (16, 64), dtype=torch.int32)
+    opi = nc.quantize_nvfp4(xi.to(DEV))
+    pi, si = C.quantize(xi.numpy().astype(np.float64))
+    assert np.array_equal(opi.packed.cpu().numpy(), pi) and np.array_equal(opi.scales.cpu().numpy(), si)
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 256, 512), (64, 384, 1024), (200, 128, 4096), (8, 4096, 4096)])
 def test_b_r6_gemm_against_dequantized_product(nc, m, n, k):
     print_case("b_r6 gemm", m, n, k)

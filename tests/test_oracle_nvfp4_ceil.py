@@ -37,9 +37,32 @@ def test_rne_tie_table(known_answers):
         C.e2m1_round_code(np.inf)
 
 
+def test_e2m1_sign_rules_code_bytes(known_answers):
+    """The two sign rules, compared as code bytes (decoded values cannot tell 0x8 from 0x0): the
+    scalar helper sets the sign for every negative input (nvfp4_layout.py:402), the quantizer only
+    for a non-zero magnitude (b_r6.py:217-223), which a quantized block shows as well."""
+    ka = known_answers["nvfp4_ceil"]
+    sc = ka["e2m1_scalar_codes"]
+    assert C.e2m1_round_code(np.array(sc["in"])).tolist() == sc["out"]
+    for v, want in zip(sc["in"], sc["out"]):
+        assert int(C.e2m1_round_code(v)) == want, v
+    qc = ka["e2m1_quantizer_codes"]
+    assert C._e2m1_quant_code(np.array(qc["in"])).tolist() == qc["out"]
+    # a block whose amax is 6 has scale 1 (code 0x38), so y = x and the codes are the quantizer's
+    vals = [v for v in qc["in"] if abs(v) > 1e-30 or v == 0.0]
+    row = np.zeros(16, np.float32)
+    row[0] = 6.0
+    row[1:1 + len(vals)] = vals
+    packed, scales = C.quantize(row[None, :])
+    codes = np.stack((packed & 0xF, packed >> 4), axis=-1).reshape(-1)
+    want = [7] + [qc["out"][qc["in"].index(v)] for v in vals] + [0] * (15 - len(vals))
+    assert int(scales[0, 0]) == 0x38 and codes.tolist() == want
+
+
 def test_e2m1_rounding_brute_force():
     """Every midpoint, its float64 neighbours, the grid, a dense sweep and negatives: the nearest
-    magnitude by exact float64 distance, ties to the even index, sign only on non-zero."""
+    magnitude by exact float64 distance, ties to the even index (the sign bits are pinned by the
+    code-byte known answers above)."""
     mags = np.array(C.E2M1_MAGNITUDES)
     pts = [np.linspace(0, 8, 20001)]
     for m in list(C._MIDS) + list(mags):
@@ -51,8 +74,8 @@ def test_e2m1_rounding_brute_force():
     cand = d == best
     # among tied candidates the even index (mantissa 0) wins
     idx = np.where(cand.sum(1) > 1, np.argmax(cand & (np.arange(8) % 2 == 0), axis=1), np.argmax(cand, axis=1))
-    want = idx | np.where((a < 0) & (idx > 0), 8, 0)
-    assert np.array_equal(C.e2m1_round_code(a), want.astype(np.uint8))
+    assert np.array_equal(C.e2m1_round_code(a) & 7, idx.astype(np.uint8))
+    assert np.array_equal(C._e2m1_quant_code(a) & 7, idx.astype(np.uint8))
     # past the grid it saturates (float64 distances to every anchor tie there, so not brute force)
     assert C.e2m1_round_code([7.0, 1e300, -1e300]).tolist() == [7, 7, 15]
 
