@@ -133,7 +133,10 @@ int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt, int param
  * activation fragments to all of them; the codes' offset is removed through per-group activation
  * sums. variant 0: `waves` (1..8) split each workgroup's k-blocks, tiles 2 or 4. variant 1: the
  * activations are staged through LDS and shared by `waves` compute waves (4, or 8 as two k-groups)
- * that own disjoint tiles (tiles 1, 2 or 4). splits >= 1 workgroups split K further and write fp32
+ * that own disjoint tiles (tiles 1, 2 or 4). variant 2: the multi-row GEMV (2 <= m <= 8; one
+ * workgroup per tile whose `waves` (0: default, at most 16) take k-slices of at most 8 blocks for
+ * m <= 4 or 4 blocks for m <= 8, each wave copying its slice of the rows into LDS; tiles ignored,
+ * splits 1). splits >= 1 workgroups split K further and write fp32
  * partials to ws, added in split order by a second kernel. variant < 0 is the library's choice for
  * the shape, the decode GEMV included when tiles, waves and splits are all <= 0; tiles, waves or
  * splits <= 0 pick the default of the variant (splits > 1 only when ws is given). The library may
@@ -174,15 +177,22 @@ int sqx_int4_linear_rmsnorm(const uint8_t* wt, const float* st, const void* x, c
                             int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
 
 /* SwiGLU's down projection with its gate in front (model.py:227-237): y = bf16(silu(g) * u) @ W^T with
- * gate_up = bf16 [m, 2 cols] laid out [g | u]. Bit-identical to sqx_silu_mul followed by the GEMV
- * form of sqx_int4_linear, as for sqx_int4_linear_rmsnorm, whose weight format it takes. */
+ * gate_up = bf16 [m, 2 cols] laid out [g | u]. Bit-identical to sqx_silu_mul followed by the linear
+ * the library picks for those rows: where that is the multi-row GEMV (2 <= m <= 8, k_slices <= 0;
+ * sqx_int4_skinny's variant 2), each wave applies the gate to its own slice of the rows; otherwise the
+ * GEMV form of sqx_int4_linear, as for sqx_int4_linear_rmsnorm, whose weight format it takes. */
 int sqx_int4_linear_silu(const uint8_t* wt, const float* st, const void* gate_up, void* y, int64_t m,
                          int64_t rows, int64_t cols, int64_t group, int k_slices, sqx_stream_t stream);
+
+/* 1 when sqx_int4_linear_silu takes m rows of a [rows, cols] weight with k_slices <= 0 (the
+ * multi-row GEMV's slices, or sqx_int4_prologue_fits), else 0. No reference counterpart. */
+int sqx_int4_linear_silu_fits(int64_t m, int64_t rows, int64_t cols);
 
 /* The one-row decode step with the RMSNorm between the linears folded away (model.py:365-372, the
  * block's h = x + attn(attn_norm(x)) and h + ffn(ffn_norm(h))). A linear that feeds the residual
  * stream ends in the residual add and leaves the sums of squares the next norm needs; the linear
- * after the norm forms the norm from those sums while it loads its activations. m must be 1.
+ * after the norm forms the norm from those sums while it loads its activations. m is 1, or 2..8 rows
+ * through the multi-row form (sqx_int4_rows_fits; sqx_int4_linear_attn_residual takes one row only).
  *
  * sqx_int4_linear_residual: res_out = bf16(res + bf16(x @ W^T)) [rows] (res_out may be res), and
  * ss_out[t] = sum of res_out[16t .. 16t+15]^2 (fp32, ceil(rows/16) entries). With gain_next (bf16
@@ -227,12 +237,22 @@ int sqx_int4_linear_rowscale_sumsq(const uint8_t* wt, const float* st, const voi
  * at position min(p, rope_rows - 1) as sqx_rope_kv rotates them (bf16 outputs, separate fp32
  * products and sums), q into q_out [n_heads * 128], k and v stored at row min(p, tmax - 1) of
  * k_cache / v_cache [n_kv_heads, tmax, 128] (one layer, one slot; bf16). The rotated bf16 values
- * equal sqx_rope_kv's on this linear's output. Fewer than 1024 row tiles. */
+ * equal sqx_rope_kv's on this linear's output. One row: fewer than 1024 row tiles. 2..8 rows (m): the
+ * multi-row form below, row r at position lengths[r], x, q_out and the sums row after row, k_cache /
+ * v_cache [m, n_kv_heads, tmax, 128] (one layer, m slots). */
 int sqx_int4_linear_rope_kv(const uint8_t* wt, const float* st, const void* x, const float* ss, int64_t nss,
                             float eps, const int* lengths, const float* cos_t, const float* sin_t, int64_t rope_rows,
                             int64_t n_heads, int64_t n_kv_heads, int64_t tmax, void* q_out, void* k_cache,
-                            void* v_cache, int64_t rows, int64_t cols, int64_t group, int k_slices,
+                            void* v_cache, int64_t m, int64_t rows, int64_t cols, int64_t group, int k_slices,
                             sqx_stream_t stream);
+
+/* 2..8 rows of the decode step's fused linears (sqx_int4_linear_residual, _silu_residual,
+ * _rowscale_sumsq, _rope_kv with m >= 2) run on the multi-row GEMV (sqx_int4_skinny's variant 2):
+ * every array is row after row ([m, cols] inputs, [m, rows] outputs, sums of squares [m, ceil(n/16)]
+ * with n the columns they cover, a multiple of 4 for the row factor), each row computed as the one-row
+ * form computes it, k_slices <= 0 the form's default waves. 1 when that form takes m rows of a [rows,
+ * cols] weight (scale_sum: with the row factor's sums in LDS), else 0. No reference counterpart. */
+int sqx_int4_rows_fits(int64_t m, int64_t rows, int64_t cols, int scale_sum);
 
 /* Build-defined asymmetric uint4, group-wise (BASELINE config 2's "asymmetric, bf16 scale/zero";
  * no reference symbol: the 4-bit form of quantize_affine, int8.py:142-172, per group):

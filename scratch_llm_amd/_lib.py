@@ -73,6 +73,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_p, _c_p, _c_p, _c_p, _c_p, ctypes.c_float, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p],
     ),
     "sqx_int4_linear_silu": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p]),
+    "sqx_int4_linear_silu_fits": (_c_i, [_c_i64, _c_i64, _c_i64]),
     "sqx_int4_linear_residual": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                         _c_i, _c_p]),
     "sqx_int4_linear_attn_residual": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64,
@@ -84,7 +85,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sqx_int4_linear_rowscale_sumsq": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, ctypes.c_float, _c_p, _c_i64, _c_i64,
                                               _c_i64, _c_i64, _c_i, _c_p]),
     "sqx_int4_linear_rope_kv": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, ctypes.c_float, _c_p, _c_p, _c_p, _c_i64, _c_i64,
-                                       _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i, _c_p]),
+                                       _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p]),
+    "sqx_int4_rows_fits": (_c_i, [_c_i64, _c_i64, _c_i64, _c_i]),
     "sqx_e2m1_round": (_c_i, [_c_p, _c_i, _c_i64, _c_p, _c_p]),
     "sqx_e2m1_decode": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),
     "sqx_fp4_pack": (_c_i, [_c_p, _c_i64, _c_p, _c_p]),

@@ -282,6 +282,36 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
   const int ws = t0 + wave * kKeysPerStep;
   constexpr int kWaveStride = NWV * kKeysPerStep;
   const int64_t head_off = (static_cast<int64_t>(b) * Hkv + kh) * tmax * kHd * ES;  // bytes
+
+  // Two register sets in turn: block base + stride is requested before block base is worked on
+  // (loads past the range read zero from the buffer resources, so every iteration issues the same
+  // loads and the waits are exact counts)
+  auto load_block = [&](const rsrc_t& kr, const rsrc_t& vrs, int lim, int bs, Row (&ko)[4], Row (&vo_)[4]) {
+    const int kq = bs + dl;
+    const uint32_t kt = kq < lim ? static_cast<uint32_t>(kq) : 0xFFFFFFu;  // past the range: zero rows (score masked)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (KV8) ko[i] = bload64<2>(kr, kt * kHd + 8u * kl, 32u * i);
+      else ko[i] = bload128<2>(kr, kt * (kHd * 2u) + 16u * kl, 64u * i);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int tv = bs + 4 * u + kl;  // rows past the wave's range read as zero (weight 0 meets no NaN)
+      const uint32_t vo = (tv < lim ? static_cast<uint32_t>(tv) : 0xFFFFFFu) * (kHd * ES) + 8u * ES * dl;
+      if constexpr (KV8) vo_[u] = bload64<2>(vrs, vo, 0u);
+      else vo_[u] = bload128<2>(vrs, vo, 0u);
+    }
+  };
+  // The wave's first block is requested before the row's length is known, through resources that end
+  // at tmax: its rows at or past the length (unwritten cache rows, possibly NaN) are masked where they
+  // are used (scores to -inf, value rows to zero). Later blocks read through resources that end at
+  // the length, so their rows past it read as zero.
+  Row ka[4], va[4], kb[4], vb[4];
+  {
+    const rsrc_t kt0 = make_rsrc(kc + head_off, static_cast<uint32_t>(tmax) * kHd * ES);
+    const rsrc_t vt0 = make_rsrc(vc + head_off, static_cast<uint32_t>(tmax) * kHd * ES);
+    load_block(kt0, vt0, min(t0 + chunk, tmax), ws, ka, va);
+  }
   const int len = max(lengths[b], 0);
   const int L = min(len + 1, tmax);
   const int slot = min(len, tmax - 1);
@@ -358,25 +388,6 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[g][j] = 0.0f;
 
-  // Two register sets in turn: block base + stride is requested before block base is worked on
-  // (loads past the range read zero from the buffer resources, so every iteration issues the same
-  // loads and the waits are exact counts)
-  auto load_block = [&](int bs, Row (&ko)[4], Row (&vo_)[4]) {
-    const int kq = bs + dl;
-    const uint32_t kt = kq < we ? static_cast<uint32_t>(kq) : 0xFFFFFFu;  // past the range: zero rows (score masked)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (KV8) ko[i] = bload64<2>(kr, kt * kHd + 8u * kl, 32u * i);
-      else ko[i] = bload128<2>(kr, kt * (kHd * 2u) + 16u * kl, 64u * i);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int tv = bs + 4 * u + kl;  // rows past the wave's range read as zero (weight 0 meets no NaN)
-      const uint32_t vo = (tv < we ? static_cast<uint32_t>(tv) : 0xFFFFFFu) * (kHd * ES) + 8u * ES * dl;
-      if constexpr (KV8) vo_[u] = bload64<2>(vrs, vo, 0u);
-      else vo_[u] = bload128<2>(vrs, vo, 0u);
-    }
-  };
   auto process = [&](int base, const Row (&kraw)[4], const Row (&vraw)[4]) {
     const int kk = base + dl;
     u32x4_t kf[4];
@@ -388,6 +399,11 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) vr[u] = vraw[u];
+    if (base == ws) {  // wave-uniform: the first block was read up to tmax
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (base + 4 * u + kl >= we) vr[u] = Row{};
+    }
     if constexpr (ROPE) {
       if (slot >= base && slot < base + kKeysPerStep) {  // wave-uniform: this step holds the new key
         if (kk == slot) {
@@ -464,13 +480,11 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
       }
     }
   };
-  Row ka[4], va[4], kb[4], vb[4];
-  load_block(ws, ka, va);
   for (int base = ws; base < we; base += 2 * kWaveStride) {
-    load_block(base + kWaveStride, kb, vb);
+    load_block(kr, vrs, we, base + kWaveStride, kb, vb);
     process(base, ka, va);
     if (base + kWaveStride >= we) break;  // wave-uniform
-    load_block(base + 2 * kWaveStride, ka, va);
+    load_block(kr, vrs, we, base + 2 * kWaveStride, ka, va);
     process(base + kWaveStride, kb, vb);
   }
   // the lane groups of the wave: m is already common to a head's lanes, so l and o simply add

@@ -799,4 +799,351 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
   return hipSuccess;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Two to eight activation rows (formats whose codes carry an offset charged through sum(x), i.e. the
+// int4 tiles): the one-row form carried to M rows. One workgroup per 16-row tile, its waves on
+// contiguous k-slices as in the one-row form.
+//  * Each wave copies its own k-slice of the M rows (nx 16-byte loads a lane per row, requested
+//    ahead of its first weight round) into its own LDS area: no workgroup copy, no barrier before
+//    the MFMAs. Columns at or past K read zero (a buffer resource per row).
+//  * MFMA A rows are the activation rows (A row r reads row min(r, M - 1); outputs of rows >= M are
+//    dropped), B the weight codes as exact (magic + code) bf16 pairs: 4 MFMAs a block for all M
+//    rows, as for one row.
+//  * The code offset -(magic + zero) * sum(x over the group) is charged per row from activation
+//    sums: per round of four blocks one MFMA per row puts the row's 16 chunks of 32 activations in
+//    the A rows against a B of ones (lane group u then holds block u's chunk sums), instead of the
+//    second MFMA chain per block of the general path. Lane (nl, jg) holds outputs of rows 4 jg + j
+//    (j < 4) for weight row nl, so rows 0..3 sit in lane group 0 and rows 4..7 in lane group 1.
+//  * The wave partials are summed through LDS in wave order (deterministic for a given wave count).
+// MR (4 or 8) is the largest M a build takes; XW the largest nx (k-slices of up to 4 XW blocks).
+// The decode step's fusions of the one-row form, per row (layouts [M][...] row after row):
+//   PRO = kProSiluGate  x is the fused gate|up activation [M, 2K]; each wave forms bf16(silu(g) * u)
+//                       of its slice on the way into LDS, as the standalone SiLU kernel does;
+//   PRO = kProScaleSum  RMSNorm's row factor past the linear: x is bf16(h * gain) and row m's output is
+//                       r_m * (x W^T), r_m = 1 / sqrt(sum(ss_in[m][0..nss)) / K + eps), the sums copied
+//                       into LDS behind the activation slice and added in the one-row form's order;
+//   RES                 the residual epilogue: res_out[m] = bf16(res[m] + bf16(y[m])), hg_out[m] =
+//                       bf16(res_out[m] * gain_next) when gain_next is given, ss_out[m][t] = sum of
+//                       res_out[m]^2 over tile t (16 outputs, summed by a fixed shuffle tree);
+//   RKV                 the q|k|v projection's RoPE and cache write at row m's position lengths[m]:
+//                       q_out [M][qn], k_cache / v_cache [M][kn / 128][tmax][128].
+// The epilogue's residual, gain and length values are requested at kernel start (cos / sin behind the
+// activation slice), by the threads that use them.
+template <class A, class W, int MR, int XW, int PRO = kProPlain, bool RES = false, bool RKV = false>
+__global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
+                                                         uint16_t* __restrict__ y, const uint16_t* __restrict__ bias,
+                                                         int M, int N, int K, int KB, int kbw, const ProArgs pa) {
+  static_assert(has_sum_offset<W>::value && W::KBLK == 128 && W::STEPS == 4, "int4 tiles: 128-column blocks");
+  static_assert(MR == 4 || MR == 8, "4 or 8 rows");
+  static_assert(PRO == kProPlain || PRO == kProSiluGate || PRO == kProScaleSum, "plain rows, SiLU gate or row factor");
+  static_assert(!(RES && RKV), "one epilogue");
+  constexpr int KBLK = 128, U = 4, NG = kNgOf<W>, CPB = 4, CPG = CPB / NG, MPG = 4 / NG;
+  constexpr int kJ = 16 * MR;  // epilogue threads: output j = (lane l = j / 4, element e = j % 4)
+  extern __shared__ f32x4_t smem[];  // [NW][64] partial accumulators, then each wave's activation rows
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int t = blockIdx.x;
+  const int kb0 = wave * kbw;
+  const int kb1 = min(KB, kb0 + kbw);
+  const int nl = lane & 15, jg = lane >> 4;
+  const typename W::Ctx wc = W::ctx(wa, t, KB, lane);
+  const int nx = (kbw * (KBLK / 8) + 63) / 64;
+  // LDS row pitch: nx KiB plus 64 bytes, so that rows start 16 banks apart
+  const int pitch = nx * 512 + 32;
+  uint16_t* xwave = reinterpret_cast<uint16_t*>(smem + nw * 64) + wave * MR * pitch;
+  // the epilogue's output of this thread (at most one, as blockDim >= 64 and kJ <= 128 outputs are
+  // spread over the first kJ threads)
+  const int jo = threadIdx.x;
+  const int mo = 4 * ((jo >> 2) >> 4) + (jo & 3);
+  const int no = t * 16 + ((jo >> 2) & 15);
+  const bool own = jo < kJ && mo < M && no < N;
+  [[maybe_unused]] uint32_t res_pre = 0u, gain_pre = 0u;
+  [[maybe_unused]] int len_pre = 0;
+  [[maybe_unused]] float cos_pre = 0.0f, sin_pre = 0.0f;
+  if constexpr (RES) {
+    if (own) {
+      res_pre = bload16(make_rsrc(pa.res, (uint32_t)M * N * 2u), (uint32_t)(mo * N + no) * 2u, 0u);
+      if (pa.gain_next != nullptr) gain_pre = bload16(make_rsrc(pa.gain_next, (uint32_t)N * 2u), (uint32_t)no * 2u, 0u);
+    }
+  }
+  if constexpr (RKV) {
+    if (own) len_pre = static_cast<int>(bload32(make_rsrc(pa.lengths, (uint32_t)M * 4u), (uint32_t)mo * 4u, 0u));
+  }
+
+  // this wave's k-slice of every row (and of the up half for the SiLU gate), requested ahead of the
+  // weights
+  constexpr int RS = PRO == kProSiluGate ? 2 : 1;  // row stride in units of K
+  u32x4_t xw[MR][XW];
+  [[maybe_unused]] u32x4_t gw[PRO == kProSiluGate ? MR : 1][XW];
+#pragma unroll
+  for (int r = 0; r < MR; ++r) {
+    if (r < M) {  // wave-uniform
+      const rsrc_t rr = make_rsrc(x + static_cast<int64_t>(r) * RS * K, static_cast<uint32_t>(K) * 2u);
+#pragma unroll
+      for (int i = 0; i < XW; ++i)
+        if (i < nx) xw[r][i] = bload128(rr, (uint32_t)(kb0 * KBLK + 8 * (lane + 64 * i)) * 2u, 0u);
+      if constexpr (PRO == kProSiluGate) {
+        const rsrc_t ru = make_rsrc(x + static_cast<int64_t>(r) * RS * K + K, static_cast<uint32_t>(K) * 2u);
+#pragma unroll
+        for (int i = 0; i < XW; ++i)
+          if (i < nx) gw[r][i] = bload128(ru, (uint32_t)(kb0 * KBLK + 8 * (lane + 64 * i)) * 2u, 0u);
+      }
+    }
+  }
+  // kProScaleSum: row r's sums of squares into LDS (buffer loads that write LDS), by wave r mod nw
+  [[maybe_unused]] __shared__ __attribute__((aligned(16))) float ss_lds[PRO == kProScaleSum ? MR : 1]
+                                                                        [PRO == kProScaleSum ? kNormSumMax : 4];
+  [[maybe_unused]] __shared__ float row_scale_lds[MR];
+  if constexpr (PRO == kProScaleSum) {
+    for (int r = wave; r < M; r += nw) {  // wave-uniform
+      const rsrc_t sr = make_rsrc(pa.ss_in + static_cast<int64_t>(r) * pa.nss, (uint32_t)pa.nss * 4u);
+#pragma unroll
+      for (int i = 0; i < kNormSumMax / 256; ++i)
+        if (i * 256 < pa.nss)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(&ss_lds[r][256 * i]), 16,
+                                                   (uint32_t)(lane + 64 * i) * 16u, 0, 0, 0);
+    }
+  }
+  // the first weight round is unconditional (blocks past kb1 clamped and unused): the wait before the
+  // LDS stores then counts exactly the weight loads still in flight
+  u32x4_t w[U];
+  typename W::P p[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) W::load(wc, min(kb0 + u, kb1 - 1), w[u], p[u]);
+#pragma unroll
+  for (int r = 0; r < MR; ++r) {
+    if (r < M) {
+#pragma unroll
+      for (int i = 0; i < XW; ++i)
+        if (i < nx) {
+          u32x4_t v = xw[r][i];
+          if constexpr (PRO == kProSiluGate) {  // past K both halves read zero, and silu(0) * 0 = 0
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint32_t g2 = v[j], u2 = gw[r][i][j];
+              v[j] = ActBF16::pack_rne(silu_f32(bf16_lo(g2)) * bf16_lo(u2), silu_f32(bf16_hi(g2)) * bf16_hi(u2));
+            }
+          }
+          *reinterpret_cast<u32x4_t*>(xwave + r * pitch + 8 * (lane + 64 * i)) = v;
+        }
+    }
+  }
+  // LDS operations of one wave execute in issue order; only the compiler must not move the fragment
+  // reads above the stores
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+  if constexpr (RKV) {
+    if (own) {  // the pair's cos / sin at the row's position (needed only in the epilogue)
+      asm volatile("" : "+v"(len_pre));
+      const int pos = min(max(len_pre, 0), pa.rope_rows - 1);
+      const uint32_t pi = (uint32_t)(pos * 64 + ((no & 127) >> 1)) * 4u;
+      const uint32_t tb = (uint32_t)pa.rope_rows * 64u * 4u;
+      cos_pre = __builtin_bit_cast(float, bload32(make_rsrc(pa.cos_t, tb), pi, 0u));
+      sin_pre = __builtin_bit_cast(float, bload32(make_rsrc(pa.sin_t, tb), pi, 0u));
+    }
+  }
+
+  const uint16_t* xfrag = xwave + min(nl, M - 1) * pitch;  // this lane's A row
+  const uint32_t one = A::pair_from_f32(1.0f);
+  const u32x4_t ones = u32x4_t{one, one, one, one};
+  float yv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto load_round = [&](int kr, u32x4_t (&wo)[U], typename W::P (&po)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (kr + u < kb1) W::load(wc, kr + u, wo[u], po[u]);  // wave-uniform condition
+  };
+  for (int kb = kb0; kb < kb1; kb += U) {
+    u32x4_t wn[U];
+    typename W::P pn[U];
+    if (kb + U < kb1) load_round(kb + U, wn, pn);
+    // the round's chunk sums per row: A row c = chunk c % 4 of block c / 4 (lane l gets the chunk sums
+    // of block l >> 4)
+    f32x4_t cs[MR];
+    {
+      const int c = lane & 15, b = c / CPB;
+      const bool live = kb + b < kb1;
+#pragma unroll
+      for (int r = 0; r < MR; ++r) {
+        cs[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if (r < M) {  // wave-uniform
+          u32x4_t a2 = u32x4_t{0u, 0u, 0u, 0u};
+          if (live)
+            a2 = *reinterpret_cast<const u32x4_t*>(xwave + r * pitch + (kb - kb0 + b) * KBLK + 32 * (c % CPB) + 8 * jg);
+          cs[r] = A::mfma(a2, ones, cs[r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (kb + u < kb1) {  // wave-uniform
+        const int kk = kb + u;
+        u32x4_t xv[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          xv[i] = *reinterpret_cast<const u32x4_t*>(xfrag + (kk - kb0) * KBLK + W::xk(i, jg));
+          b[i] = W::template bfrag<A>(w[u], i);
+        }
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int i = g * MPG; i < (g + 1) * MPG; ++i) acc = A::mfma(xv[i], b[i], acc);
+          const float off = W::template offset<A>(p[u], g), sc = W::scale(p[u], g);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            // the group's sum of row j (and of row 4 + j for lane group 1), a wave-uniform value
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CPG; ++i) s0 += cs[j][g * CPG + i];
+            s0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s0), 16 * u));
+            if constexpr (MR == 8) {
+#pragma unroll
+              for (int i = 0; i < CPG; ++i) s1 += cs[4 + j][g * CPG + i];
+              s1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s1), 16 * u));
+              s0 = jg == 1 ? s1 : s0;
+            }
+            yv[j] = fmaf(sc, fmaf(-off, s0, acc[j]), yv[j]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      w[u] = wn[u];
+      p[u] = pn[u];
+    }
+  }
+
+  if constexpr (PRO == kProScaleSum) {
+    for (int r = wave; r < M; r += nw) {  // wave-uniform: row r's factor, in the one-row form's order
+      wait_vmcnt<0>();  // the copies into LDS (long done: the weights behind them have been consumed)
+      asm volatile("" ::: "memory");
+      const int ln = static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+      float tt = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kNormSumMax / 256; ++i)
+        if (i * 256 < pa.nss) {
+          const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(&ss_lds[r][256 * i + 4 * ln]);
+          tt += (v4[0] + v4[1]) + (v4[2] + v4[3]);
+        }
+      tt = wave_sum(tt);
+      if (lane == 0) row_scale_lds[r] = 1.0f / sqrtf(tt / static_cast<float>(K) + pa.eps);
+    }
+  }
+  // Sum the wave partials in wave order. Float j of a wave's block is (lane l, row r).
+  f32x4_t* red = smem;
+  red[wave * 64 + lane] = f32x4_t{yv[0], yv[1], yv[2], yv[3]};
+  __syncthreads();
+  if (jo >= kJ) return;  // whole waves
+  const float* rf = reinterpret_cast<const float*>(red);
+  float v = 0.0f;
+  if (own) {
+    for (int ww = 0; ww < nw; ++ww) v += rf[ww * 256 + jo];
+    v *= W::out_scale(wa, no);
+    if constexpr (PRO == kProScaleSum) v *= row_scale_lds[mo];
+  }
+  if constexpr (RKV) {
+#pragma clang fp contract(off)
+    const float xq = A::to_f32(A::from_f32(v));  // the projection's bf16 output
+    const float xp = __shfl_xor(xq, 4, 64);      // its RoPE partner (the other dim of the pair, lane ^ 4)
+    if (own) {
+      const int slot = min(max(len_pre, 0), pa.tmax - 1);
+      const int nh = pa.kn >> 7;  // kv heads
+      if (no < pa.qn + pa.kn) {
+        const float r = (no & 1) ? xp * sin_pre + xq * cos_pre : xq * cos_pre - xp * sin_pre;
+        if (no < pa.qn) {
+          pa.q_out[static_cast<int64_t>(mo) * pa.qn + no] = A::from_f32(r);
+        } else {
+          const int kd = no - pa.qn;
+          pa.k_cache[((static_cast<int64_t>(mo) * nh + (kd >> 7)) * pa.tmax + slot) * 128 + (kd & 127)] = A::from_f32(r);
+        }
+      } else {
+        const int vd = no - pa.qn - pa.kn;
+        pa.v_cache[((static_cast<int64_t>(mo) * nh + (vd >> 7)) * pa.tmax + slot) * 128 + (vd & 127)] = A::from_f32(xq);
+      }
+    }
+    return;
+  } else if constexpr (RES) {
+    float hsq = 0.0f;
+    asm volatile("" : "+v"(res_pre), "+v"(gain_pre));
+    if (own) {
+      if (bias) v += A::to_f32(bias[no]);
+      const float rv = A::to_f32(static_cast<uint16_t>(res_pre));
+      const float h = A::to_f32(A::from_f32(rv + A::to_f32(A::from_f32(v))));
+      pa.res_out[static_cast<int64_t>(mo) * N + no] = A::from_f32(h);
+      if (pa.gain_next != nullptr)
+        pa.hg_out[static_cast<int64_t>(mo) * N + no] = A::from_f32(h * A::to_f32(static_cast<uint16_t>(gain_pre)));
+      hsq = h * h;
+    }
+    // the tile's 16 outputs of row mo sit in lanes 4 nl + e of this wave: a fixed shuffle tree
+    hsq += __shfl_xor(hsq, 4, 64);
+    hsq += __shfl_xor(hsq, 8, 64);
+    hsq += __shfl_xor(hsq, 16, 64);
+    hsq += __shfl_xor(hsq, 32, 64);
+    if (((jo >> 2) & 15) == 0 && mo < M) pa.ss_out[static_cast<int64_t>(mo) * gridDim.x + t] = hsq;
+  } else {
+    if (own) {
+      if (bias) v += A::to_f32(bias[no]);
+      y[static_cast<int64_t>(mo) * N + no] = A::from_f32(v);
+    }
+  }
+}
+
+// Waves per tile of the multi-row form: one round of four blocks per wave up to 16 waves (the one-row
+// rule), so k-slices grow past four blocks only beyond 64 blocks.
+inline int gemv_rows_default_waves(int64_t rows, int64_t cols) {
+  const int64_t KB = ceil_div(cols, 128);
+  return static_cast<int>(std::min<int64_t>(16, std::max<int64_t>(1, ceil_div(KB, 4))));
+}
+
+// LDS bytes of the multi-row form for a launch of nw waves over k-slices of kbw blocks (dynamic, plus
+// the row factor's sums in the kProScaleSum form).
+inline size_t gemv_rows_lds_bytes(int64_t m, int nw, int kbw, bool scale_sum = false) {
+  const int MR = m <= 4 ? 4 : 8;
+  const int nx = (kbw * 16 + 63) / 64;
+  return static_cast<size_t>(nw) * 64 * sizeof(f32x4_t) + static_cast<size_t>(nw) * MR * (nx * 512 + 32) * 2 +
+         (scale_sum ? static_cast<size_t>(MR) * (kNormSumMax + 1) * 4 : 0);
+}
+
+// Whether the multi-row form takes m rows of a [rows, cols] weight with nw waves per tile (0: default);
+// scale_sum: the row factor's form.
+inline bool gemv_rows_fits(int64_t m, int64_t rows, int64_t cols, int nw = 0, bool scale_sum = false) {
+  if (m < 2 || m > 8 || rows <= 0 || cols <= 0) return false;
+  const int64_t KB = ceil_div(cols, 128);
+  if (nw <= 0) nw = gemv_rows_default_waves(rows, cols);
+  if (nw > 16) return false;
+  if (nw > KB) nw = static_cast<int>(KB);
+  const int kbw = static_cast<int>(ceil_div(KB, nw));
+  nw = static_cast<int>(ceil_div(KB, kbw));
+  const int XW = m <= 4 ? 2 : 1;
+  // the epilogue's outputs of rows 4..7 are threads 64..127: two waves at least
+  return kbw <= 4 * XW && (m <= 4 || nw >= 2) && gemv_rows_lds_bytes(m, nw, kbw, scale_sum) <= 160 * 1024;
+}
+
+template <class A, class W, int PRO = kProPlain, bool RES = false, bool RKV = false>
+hipError_t gemv_rows_launch(const typename W::Args& wa, const uint16_t* x, uint16_t* y, const uint16_t* bias,
+                            int64_t m, int64_t rows, int64_t cols, int waves, hipStream_t stream,
+                            const ProArgs& pa = ProArgs{nullptr, nullptr, nullptr, 0.0f}) {
+  if (!gemv_rows_fits(m, rows, cols, waves, PRO == kProScaleSum)) return hipErrorNotSupported;
+  const int64_t T = ceil_div(rows, 16);
+  const int64_t KB = ceil_div(cols, 128);
+  int nw = waves > 0 ? waves : gemv_rows_default_waves(rows, cols);
+  if (nw > KB) nw = static_cast<int>(KB);
+  const int kbw = static_cast<int>(ceil_div(KB, nw));
+  nw = static_cast<int>(ceil_div(KB, kbw));
+  const size_t lds = gemv_rows_lds_bytes(m, nw, kbw);  // the row factor's sums are static LDS
+  const dim3 grid(static_cast<unsigned>(T)), block(static_cast<unsigned>(64 * nw));
+  const int M = static_cast<int>(m), N = static_cast<int>(rows), K = static_cast<int>(cols), iKB = static_cast<int>(KB);
+  // columns at or past K (a k tail) read zero through the row resources, so the padded blocks need no
+  // masking
+  if (m <= 4)
+    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 2, PRO, RES, RKV>), grid, block, lds, stream, wa, x, y, bias, M, N, K,
+                       iKB, kbw, pa);
+  else
+    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 8, 1, PRO, RES, RKV>), grid, block, lds, stream, wa, x, y, bias, M, N, K,
+                       iKB, kbw, pa);
+  return hipGetLastError();
+}
+
 }  // namespace sqx

@@ -608,6 +608,22 @@ static hipError_t launch_int4_skinny(int group, const uint8_t* wt, const void* s
 }
 
 template <class A, bool ASYM, bool PBF16>
+static hipError_t launch_int4_rows(int group, const uint8_t* wt, const void* st, const void* zt, const uint16_t* x,
+                                   uint16_t* y, const uint16_t* bias, int64_t m, int64_t rows, int64_t cols, int waves,
+                                   hipStream_t s) {
+#define SQX_ROWG(G_)                                                                        \
+  {                                                                                         \
+    using W = WInt4<G_, ASYM, PBF16>;                                                       \
+    const typename W::Args a{wt, st, zt};                                                   \
+    return gemv_rows_launch<A, W>(a, x, y, bias, m, rows, cols, waves, s);                  \
+  }
+  if (group == 128) SQX_ROWG(128)
+  if (group == 64) SQX_ROWG(64)
+  SQX_ROWG(32)
+#undef SQX_ROWG
+}
+
+template <class A, bool ASYM, bool PBF16>
 static hipError_t launch_int4_g(int group, const uint8_t* wt, const void* st, const void* zt, const uint16_t* x,
                                 uint16_t* y, const uint16_t* bias, const float* colscale, int64_t m, int64_t rows,
                                 int64_t cols, int k_slices, hipStream_t s) {
@@ -1033,9 +1049,13 @@ static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, i
               SQX_E_ARG, "%s: shape too large for 32-bit buffer offsets", fn);
   SQX_REQUIRE(sh.S >= 1 &&
                   ((sh.variant == 0 && (sh.R == 2 || sh.R == 4) && sh.waves >= 1 && sh.waves <= kSkinnyMaxWaves) ||
-                   (sh.variant == 1 && (sh.R == 1 || sh.R == 2 || sh.R == 4) && (sh.waves == 4 || sh.waves == 8))),
+                   (sh.variant == 1 && (sh.R == 1 || sh.R == 2 || sh.R == 4) && (sh.waves == 4 || sh.waves == 8)) ||
+                   (sh.variant == 2 && sh.S == 1 && sh.waves >= 0 && sh.waves <= 16)),
               SQX_E_ARG, "%s: bad launch shape (variant %d, tiles %d, waves %d, splits %d)", fn, sh.variant, sh.R,
               sh.waves, sh.S);
+  SQX_REQUIRE(sh.variant != 2 || m == 0 || gemv_rows_fits(m, rows, cols, sh.waves), SQX_E_ARG,
+              "%s: the multi-row GEMV (variant 2) takes 2..8 rows with k-slices of at most %d blocks (m=%lld, "
+              "cols=%lld, waves %d)", fn, m <= 4 ? 8 : 4, (long long)m, (long long)cols, sh.waves);
   if (m == 0) return SQX_OK;
   SQX_REQUIRE(wt && st && x && (y || !reduce), SQX_E_ARG, "%s: null pointer", fn);
   SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, SQX_E_ARG,
@@ -1056,6 +1076,20 @@ static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, i
   float* wsp = static_cast<float*>(ws);
   const int g = static_cast<int>(group);
   hipError_t e;
+  if (sh.variant == 2) {
+    SQX_REQUIRE(reduce, SQX_E_ARG, "%s: the multi-row GEMV leaves no partials", fn);
+#define SQX_ROWL(ACT, ASYM, PBF) e = launch_int4_rows<ACT, ASYM, PBF>(g, wt, st, zt, xp, yp, b16, m, rows, cols, sh.waves, s)
+    if (act_dtype == SQX_DTYPE_BF16) {
+      if (asym) { if (pbf) SQX_ROWL(ActBF16, true, true); else SQX_ROWL(ActBF16, true, false); }
+      else { if (pbf) SQX_ROWL(ActBF16, false, true); else SQX_ROWL(ActBF16, false, false); }
+    } else {
+      if (asym) { if (pbf) SQX_ROWL(ActF16, true, true); else SQX_ROWL(ActF16, true, false); }
+      else { if (pbf) SQX_ROWL(ActF16, false, true); else SQX_ROWL(ActF16, false, false); }
+    }
+#undef SQX_ROWL
+    SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    return SQX_OK;
+  }
 #define SQX_SKL(ACT, ASYM, PBF) \
   e = launch_int4_skinny<ACT, ASYM, PBF>(g, wt, st, zt, xp, yp, b16, m, rows, cols, sh, wsp, ws_bytes, s, reduce)
   if (act_dtype == SQX_DTYPE_BF16) {
@@ -1107,8 +1141,9 @@ extern "C" int sqx_int4_skinny(const uint8_t* wt, const void* st, const void* zt
     return int4_linear_impl(wt, st, zt, param_dtype, x, act_dtype, y, bias, nullptr, m, rows, cols, group,
                             sqx_int4_linear_default_kslices(m, rows, cols), stream, "sqx_int4_skinny");
   if (variant >= 0 && (variant != sh.variant || sh.gemv))  // the variant's own defaults
-    sh = variant == 0 ? SkinnyShape{0, 2, 8, 1, false} : SkinnyShape{1, 2, 4, 1, false};
-  if (variant > 1) sh.variant = variant;  // refused below
+    sh = variant == 0 ? SkinnyShape{0, 2, 8, 1, false}
+                      : (variant == 2 ? SkinnyShape{2, 1, 0, 1, false} : SkinnyShape{1, 2, 4, 1, false});
+  if (variant > 2) sh.variant = variant;  // refused below
   if (tiles > 0) sh.R = tiles;
   if (waves > 0) sh.waves = waves;
   if (splits > 0) sh.S = splits;
@@ -1161,9 +1196,38 @@ extern "C" int sqx_int4_linear_rmsnorm(const uint8_t* wt, const float* st, const
   return SQX_OK;
 }
 
+// Whether the SiLU gate runs in the slices of the multi-row GEMV: where the library's plain linear of
+// these rows is that kernel (so the fused and the two-call forms share one kernel and its sums).
+static bool int4_silu_rows(int64_t m, int64_t rows, int64_t cols, int k_slices) {
+  return k_slices <= 0 && m >= 2 && m <= 8 && rows > 0 && cols > 0 && cols % 8 == 0 &&
+         skinny_default_shape(m, rows, cols, 128, true).variant == 2;
+}
+
+extern "C" int sqx_int4_linear_silu_fits(int64_t m, int64_t rows, int64_t cols) {
+  return int4_silu_rows(m, rows, cols, 0) || sqx_int4_prologue_fits(m, cols);
+}
+
 extern "C" int sqx_int4_linear_silu(const uint8_t* wt, const float* st, const void* gate_up, void* y, int64_t m,
                                     int64_t rows, int64_t cols, int64_t group, int k_slices, sqx_stream_t stream) {
   const char* fn = "sqx_int4_linear_silu";
+  if (int4_silu_rows(m, rows, cols, k_slices) && (group == 32 || group == 64 || group == 128) && cols % group == 0 &&
+      rows < ((int64_t)1 << 31)) {
+    SQX_REQUIRE(wt && st && gate_up && y, SQX_E_ARG, "%s: null pointer", fn);
+    SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(gate_up) % 16 == 0, SQX_E_ARG,
+                "%s: wt and gate_up must be 16-byte aligned", fn);
+    hipError_t e;
+#define SQX_ROWSILU(G_)                                                                                          \
+  {                                                                                                              \
+    using W = WInt4<G_, false, false>;                                                                           \
+    const typename W::Args a{wt, st, nullptr};                                                                   \
+    e = gemv_rows_launch<ActBF16, W, kProSiluGate>(a, static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(y), \
+                                                   nullptr, m, rows, cols, 0, as_stream(stream));                \
+  }
+    if (group == 128) SQX_ROWSILU(128) else if (group == 64) SQX_ROWSILU(64) else SQX_ROWSILU(32)
+#undef SQX_ROWSILU
+    SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    return SQX_OK;
+  }
   const int rc = int4_pro_check(wt, st, gate_up, y, m, rows, cols, group, k_slices, fn);
   if (rc != SQX_OK) return rc;
   const hipError_t e = launch_int4_pro<kProSiluGate>(static_cast<int>(group), wt, st,
@@ -1174,10 +1238,50 @@ extern "C" int sqx_int4_linear_silu(const uint8_t* wt, const float* st, const vo
   return SQX_OK;
 }
 
-// Arguments of the one-row residual epilogue shared by the two entry points that end in it.
+// The decode step's fused forms at 2..8 rows: the multi-row GEMV (symmetric codes, fp32 scales, bf16).
+template <int PRO, bool RES, bool RKV>
+static hipError_t launch_int4_rows_fused(int group, const uint8_t* wt, const float* st, const uint16_t* x, uint16_t* y,
+                                         int64_t m, int64_t rows, int64_t cols, int k_slices, hipStream_t s,
+                                         const ProArgs& pa) {
+#define SQX_RF(G_)                                                                                           \
+  {                                                                                                          \
+    using W = WInt4<G_, false, false>;                                                                       \
+    const typename W::Args a{wt, st, nullptr};                                                               \
+    return gemv_rows_launch<ActBF16, W, PRO, RES, RKV>(a, x, y, nullptr, m, rows, cols, k_slices, s, pa);    \
+  }
+  if (group == 128) SQX_RF(128)
+  if (group == 64) SQX_RF(64)
+  SQX_RF(32)
+#undef SQX_RF
+}
+
+static int int4_rows_check(const uint8_t* wt, const float* st, const void* x, const void* y, int64_t m, int64_t rows,
+                           int64_t cols, int64_t group, int k_slices, bool scale_sum, const char* fn) {
+  SQX_REQUIRE(rows > 0 && cols > 0 && rows < ((int64_t)1 << 31) && m * rows < ((int64_t)1 << 31) &&
+                  m * cols * 2 < ((int64_t)1 << 31),
+              SQX_E_ARG, "%s: bad shape", fn);
+  SQX_REQUIRE(group == 32 || group == 64 || group == 128, SQX_E_ARG, "%s: group_size %lld unsupported (32, 64 or 128)",
+              fn, (long long)group);
+  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld", (long long)cols,
+              (long long)group);
+  SQX_REQUIRE(k_slices <= 16, SQX_E_ARG, "%s: k_slices %d > 16", fn, k_slices);
+  SQX_REQUIRE(gemv_rows_fits(m, rows, cols, k_slices, scale_sum), SQX_E_ARG,
+              "%s: m=%lld rows of %lld columns do not fit the multi-row form (2..8 rows; k-slices of at most 8 "
+              "blocks for m <= 4, 4 for m <= 8; see sqx_int4_rows_fits)", fn, (long long)m, (long long)cols);
+  SQX_REQUIRE(wt && st && x && y, SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, SQX_E_ARG,
+              "%s: wt and x must be 16-byte aligned", fn);
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_rows_fits(int64_t m, int64_t rows, int64_t cols, int scale_sum) {
+  return gemv_rows_fits(m, rows, cols, 0, scale_sum != 0) ? 1 : 0;
+}
+
+// Arguments of the residual epilogue shared by the entry points that end in it.
 static int int4_res_check(const void* res, const void* res_out, const float* ss_out, const void* gain_next,
                           const void* hg_out, int64_t m, const char* fn) {
-  SQX_REQUIRE(m == 1, SQX_E_ARG, "%s: the residual epilogue is the one-row (decode) form, m=%lld", fn, (long long)m);
+  SQX_REQUIRE(m >= 1 && m <= 8, SQX_E_ARG, "%s: the residual epilogue takes 1..8 rows, m=%lld", fn, (long long)m);
   SQX_REQUIRE(res && res_out && ss_out, SQX_E_ARG, "%s: null residual or sums", fn);
   SQX_REQUIRE((gain_next == nullptr) == (hg_out == nullptr), SQX_E_ARG, "%s: gain_next and hg_out go together", fn);
   return SQX_OK;
@@ -1187,7 +1291,8 @@ extern "C" int sqx_int4_linear_residual(const uint8_t* wt, const float* st, cons
                                         void* res_out, float* ss_out, const void* gain_next, void* hg_out, int64_t m,
                                         int64_t rows, int64_t cols, int64_t group, int k_slices, sqx_stream_t stream) {
   const char* fn = "sqx_int4_linear_residual";
-  int rc = int4_pro_check(wt, st, x, res_out, m, rows, cols, group, k_slices, fn);
+  int rc = m >= 2 ? int4_rows_check(wt, st, x, res_out, m, rows, cols, group, k_slices, false, fn)
+                  : int4_pro_check(wt, st, x, res_out, m, rows, cols, group, k_slices, fn);
   if (rc == SQX_OK) rc = int4_res_check(res, res_out, ss_out, gain_next, hg_out, m, fn);
   if (rc != SQX_OK) return rc;
   ProArgs pa{};
@@ -1196,9 +1301,12 @@ extern "C" int sqx_int4_linear_residual(const uint8_t* wt, const float* st, cons
   pa.ss_out = ss_out;
   pa.gain_next = static_cast<const uint16_t*>(gain_next);
   pa.hg_out = static_cast<uint16_t*>(hg_out);
-  const hipError_t e = launch_int4_pro_res<kProPlain, true>(static_cast<int>(group), wt, st,
-                                                            static_cast<const uint16_t*>(x), nullptr, m, rows, cols,
-                                                            k_slices, as_stream(stream), pa);
+  const hipError_t e =
+      m >= 2 ? launch_int4_rows_fused<kProPlain, true, false>(static_cast<int>(group), wt, st,
+                                                              static_cast<const uint16_t*>(x), nullptr, m, rows, cols,
+                                                              k_slices, as_stream(stream), pa)
+             : launch_int4_pro_res<kProPlain, true>(static_cast<int>(group), wt, st, static_cast<const uint16_t*>(x),
+                                                    nullptr, m, rows, cols, k_slices, as_stream(stream), pa);
   SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return SQX_OK;
 }
@@ -1208,6 +1316,7 @@ extern "C" int sqx_int4_linear_attn_residual(const uint8_t* wt, const float* st,
                                              const void* gain_next, void* hg_out, int64_t m, int64_t rows,
                                              int64_t cols, int64_t group, int k_slices, sqx_stream_t stream) {
   const char* fn = "sqx_int4_linear_attn_residual";
+  SQX_REQUIRE(m == 1, SQX_E_ARG, "%s: the attention merge is the one-row (decode) form, m=%lld", fn, (long long)m);
   int rc = int4_pro_check(wt, st, part, res_out, m, rows, cols, group, k_slices, fn);
   if (rc == SQX_OK) rc = int4_res_check(res, res_out, ss_out, gain_next, hg_out, m, fn);
   if (rc != SQX_OK) return rc;
@@ -1246,7 +1355,8 @@ extern "C" int sqx_int4_linear_silu_residual(const uint8_t* wt, const float* st,
                                              int64_t m, int64_t rows, int64_t cols, int64_t group, int k_slices,
                                              sqx_stream_t stream) {
   const char* fn = "sqx_int4_linear_silu_residual";
-  int rc = int4_pro_check(wt, st, gate_up, res_out, m, rows, cols, group, k_slices, fn);
+  int rc = m >= 2 ? int4_rows_check(wt, st, gate_up, res_out, m, rows, cols, group, k_slices, false, fn)
+                  : int4_pro_check(wt, st, gate_up, res_out, m, rows, cols, group, k_slices, fn);
   if (rc == SQX_OK) rc = int4_res_check(res, res_out, ss_out, gain_next, hg_out, m, fn);
   if (rc != SQX_OK) return rc;
   ProArgs pa{};
@@ -1255,9 +1365,13 @@ extern "C" int sqx_int4_linear_silu_residual(const uint8_t* wt, const float* st,
   pa.ss_out = ss_out;
   pa.gain_next = static_cast<const uint16_t*>(gain_next);
   pa.hg_out = static_cast<uint16_t*>(hg_out);
-  const hipError_t e = launch_int4_pro_res<kProSiluGate, true>(static_cast<int>(group), wt, st,
-                                                               static_cast<const uint16_t*>(gate_up), nullptr, m,
-                                                               rows, cols, k_slices, as_stream(stream), pa);
+  const hipError_t e =
+      m >= 2 ? launch_int4_rows_fused<kProSiluGate, true, false>(static_cast<int>(group), wt, st,
+                                                                 static_cast<const uint16_t*>(gate_up), nullptr, m, rows,
+                                                                 cols, k_slices, as_stream(stream), pa)
+             : launch_int4_pro_res<kProSiluGate, true>(static_cast<int>(group), wt, st,
+                                                       static_cast<const uint16_t*>(gate_up), nullptr, m, rows, cols,
+                                                       k_slices, as_stream(stream), pa);
   SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return SQX_OK;
 }
@@ -1298,14 +1412,26 @@ extern "C" int sqx_int4_linear_rowscale_sumsq(const uint8_t* wt, const float* st
                                              int64_t nss, float eps, void* y, int64_t m, int64_t rows, int64_t cols,
                                              int64_t group, int k_slices, sqx_stream_t stream) {
   const char* fn = "sqx_int4_linear_rowscale_sumsq";
-  const int rc = int4_pro_check(wt, st, hg, y, m, rows, cols, group, k_slices, fn);
+  SQX_REQUIRE(m >= 1 && m <= 8, SQX_E_ARG, "%s: the norm from tile sums takes 1..8 rows, m=%lld", fn, (long long)m);
+  const int rc = m >= 2 ? int4_rows_check(wt, st, hg, y, m, rows, cols, group, k_slices, true, fn)
+                        : int4_pro_check(wt, st, hg, y, m, rows, cols, group, k_slices, fn);
   if (rc != SQX_OK) return rc;
-  SQX_REQUIRE(m == 1, SQX_E_ARG, "%s: the norm from tile sums is the one-row (decode) form, m=%lld", fn, (long long)m);
   SQX_REQUIRE(nss == ceil_div(cols, 16) && nss <= kNormSumMax, SQX_E_ARG,
               "%s: %lld sums of squares for %lld columns (one per 16 columns, at most %d)", fn, (long long)nss,
               (long long)cols, kNormSumMax);
-  SQX_REQUIRE(ss != nullptr && reinterpret_cast<uintptr_t>(ss) % 16 == 0, SQX_E_ARG,
-              "%s: the sums must be 16-byte aligned", fn);
+  SQX_REQUIRE(ss != nullptr && reinterpret_cast<uintptr_t>(ss) % 16 == 0 && (m == 1 || nss % 4 == 0), SQX_E_ARG,
+              "%s: the sums must be 16-byte aligned (and a multiple of 4 a row)", fn);
+  if (m >= 2) {
+    ProArgs pa{};
+    pa.eps = eps;
+    pa.ss_in = ss;
+    pa.nss = static_cast<int>(nss);
+    const hipError_t e = launch_int4_rows_fused<kProScaleSum, false, false>(
+        static_cast<int>(group), wt, st, static_cast<const uint16_t*>(hg), static_cast<uint16_t*>(y), m, rows, cols,
+        k_slices, as_stream(stream), pa);
+    SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    return SQX_OK;
+  }
   const int64_t KB = ceil_div(cols, 128);
   int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols, 128, 1) : k_slices;
   if (nw > KB) nw = static_cast<int>(KB);
@@ -1326,27 +1452,29 @@ extern "C" int sqx_int4_linear_rowscale_sumsq(const uint8_t* wt, const float* st
 extern "C" int sqx_int4_linear_rope_kv(const uint8_t* wt, const float* st, const void* x, const float* ss, int64_t nss,
                                       float eps, const int* lengths, const float* cos_t, const float* sin_t,
                                       int64_t rope_rows, int64_t n_heads, int64_t n_kv_heads, int64_t tmax,
-                                      void* q_out, void* k_cache, void* v_cache, int64_t rows, int64_t cols,
+                                      void* q_out, void* k_cache, void* v_cache, int64_t m, int64_t rows, int64_t cols,
                                       int64_t group, int k_slices, sqx_stream_t stream) {
   const char* fn = "sqx_int4_linear_rope_kv";
-  const int rc = int4_pro_check(wt, st, x, q_out, 1, rows, cols, group, k_slices, fn);
+  SQX_REQUIRE(m >= 1 && m <= 8, SQX_E_ARG, "%s: the RoPE epilogue takes 1..8 rows, m=%lld", fn, (long long)m);
+  const int rc = m >= 2 ? int4_rows_check(wt, st, x, q_out, m, rows, cols, group, k_slices, ss != nullptr, fn)
+                        : int4_pro_check(wt, st, x, q_out, 1, rows, cols, group, k_slices, fn);
   if (rc != SQX_OK) return rc;
   SQX_REQUIRE(n_heads > 0 && n_kv_heads > 0 && rows == (n_heads + 2 * n_kv_heads) * 128, SQX_E_ARG,
               "%s: rows=%lld is not (%lld + 2 * %lld) heads of 128", fn, (long long)rows, (long long)n_heads,
               (long long)n_kv_heads);
-  SQX_REQUIRE(ceil_div(rows, 16) < 1024, SQX_E_ARG, "%s: %lld rows: the RoPE epilogue needs fewer than 1024 tiles",
-              fn, (long long)rows);
+  SQX_REQUIRE(m >= 2 || ceil_div(rows, 16) < 1024, SQX_E_ARG,
+              "%s: %lld rows: the one-row RoPE epilogue needs fewer than 1024 tiles", fn, (long long)rows);
   SQX_REQUIRE(lengths && cos_t && sin_t && k_cache && v_cache, SQX_E_ARG, "%s: null pointer", fn);
   SQX_REQUIRE(rope_rows > 0 && rope_rows < (int64_t(1) << 24) && tmax > 0 && tmax < (int64_t(1) << 30), SQX_E_ARG,
               "%s: bad rope_rows or tmax", fn);
   SQX_REQUIRE(ss == nullptr || (nss == ceil_div(cols, 16) && nss <= kNormSumMax &&
-                                reinterpret_cast<uintptr_t>(ss) % 16 == 0),
+                                reinterpret_cast<uintptr_t>(ss) % 16 == 0 && (m == 1 || nss % 4 == 0)),
               SQX_E_ARG, "%s: %lld sums of squares for %lld columns (one per 16 columns, at most %d, 16-byte aligned)",
               fn, (long long)nss, (long long)cols, kNormSumMax);
   const int64_t KB = ceil_div(cols, 128);
   int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols, 128, 1) : k_slices;
   if (nw > KB) nw = static_cast<int>(KB);
-  SQX_REQUIRE(ceil_div(KB, nw) <= kOneMaxKbw, SQX_E_ARG,
+  SQX_REQUIRE(m >= 2 || ceil_div(KB, nw) <= kOneMaxKbw, SQX_E_ARG,
               "%s: %lld k-blocks over %d waves: at most %d per wave (raise k_slices)", fn, (long long)KB, nw,
               kOneMaxKbw);
   ProArgs pa{};
@@ -1366,6 +1494,14 @@ extern "C" int sqx_int4_linear_rope_kv(const uint8_t* wt, const float* st, const
   hipError_t e;
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   hipStream_t s = as_stream(stream);
+  if (m >= 2) {
+    e = ss != nullptr ? launch_int4_rows_fused<kProScaleSum, false, true>(static_cast<int>(group), wt, st, xp, nullptr, m,
+                                                                         rows, cols, k_slices, s, pa)
+                      : launch_int4_rows_fused<kProPlain, false, true>(static_cast<int>(group), wt, st, xp, nullptr, m,
+                                                                      rows, cols, k_slices, s, pa);
+    SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    return SQX_OK;
+  }
 #define SQX_RKV(G_)                                                                                               \
   {                                                                                                               \
     using W = WInt4<G_, false, false>;                                                                            \

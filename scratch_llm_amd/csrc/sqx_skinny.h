@@ -547,7 +547,9 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
 }
 
 // The launch shape the library picks for an m-row linear (m <= 64) over rows x cols weights, from
-// measured sweeps of the Llama-3-8B shapes (4096 -> 1024..128256, 14336 -> 4096; m = 8..64):
+// measured sweeps of the Llama-3-8B shapes (4096 -> 1024..128256, 14336 -> 4096; m = 2..64):
+//   m <= 8        the multi-row GEMV (gemv_rows_kernel) on up to 384 row tiles (512 for m <= 4, and
+//                 below 4096 for m = 2) where its k-slices fit; otherwise as below;
 //   m <= 16       waves splitting K: 4 tiles x 4 waves from 1024 row tiles, 2 x 8 from 384; from 4096
 //                 tiles the LDS-staged variant (4 tiles, 4 waves); below 384 tiles the decode GEMV,
 //                 except for long K (>= 64 blocks) with a workspace (2 x 8 waves, 2 splits);
@@ -559,7 +561,7 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
 //                 from 1024 tiles; below, 1 tile per wave (2 for long K) and, with a workspace, K split
 //                 to about 192 workgroups.
 struct SkinnyShape {
-  int variant;  // 0: waves splitting K (skinny_kernel); 1: LDS-staged (skinny_lds_kernel)
+  int variant;  // 0: waves splitting K (skinny_kernel); 1: LDS-staged (skinny_lds_kernel); 2: gemv_rows_kernel
   int R;        // row tiles per wave: 1, 2 or 4 (the K-split variant: 2 or 4)
   int waves;    // K-split: 1..8 waves per workgroup; LDS-staged: 4 or 8 compute waves (1 or 2 k-groups)
   int S;        // workgroups along K (S > 1 needs a workspace of S*m*rows fp32)
@@ -578,6 +580,14 @@ inline SkinnyShape skinny_default_shape(int64_t m, int64_t rows, int64_t cols, i
   };
   if (m <= 1) {
     s.gemv = true;
+  } else if (m <= 8 && kblk == 128 && gemv_rows_fits(m, rows, cols) &&
+             (T <= 384 || (m <= 4 && T <= 512) || (m == 2 && T < 4096))) {
+    // the multi-row GEMV (rotating weights, asymmetric bf16 parameters, M = 2 / 4 / 8 against the
+    // kernels below): 4096^2 5.13 / 5.30 / 5.84 -> 4.64 / 4.80 / 5.59 us, 4096->1024 4.33 / 4.65 / 5.18 ->
+    // 3.94 / 4.14 / 5.12 us, 14336->4096 13.64 / 12.05 -> 10.29 / 10.45 us (M = 2 / 4), 4096->6144
+    // 6.69 / 6.78 / 6.89 -> 5.41 / 5.81 / 6.74 us; 4096->14336 (896 tiles) 9.79 -> 9.33 us at M = 2 only,
+    // 4096->28672 15.66 -> 15.13 us at M = 2 only
+    s = SkinnyShape{2, 1, 0, 1, false};
   } else if (m <= 16) {
     if (T >= 4096) s = SkinnyShape{1, 4, 4, 1, false};
     else if (T >= 1024) s = SkinnyShape{0, 4, 4, 1, false};

@@ -125,9 +125,10 @@ class DecodeState:
         self.x = [torch.empty(batch, d, **bf), torch.empty(batch, d, **bf)]  # residual stream (ping-pong)
         self.h = torch.empty(batch, d, **bf)  # normalised input of the next projection
         self.delta = torch.empty(batch, d, **bf)  # o_proj / w2 output
-        # one-row steps: sums of squares of the residual stream per 16 columns, left by the linear that
-        # wrote it for the norm in the next linear
-        self.ss = torch.empty(-(-d // 16), dtype=torch.float32, device=dev)
+        # steps without norm launches: sums of squares of the residual stream per 16 columns [batch, d/16],
+        # left by the linear that wrote it for the norm in the next linear
+        self.nss = -(-d // 16)
+        self.ss = torch.empty(batch, self.nss, dtype=torch.float32, device=dev)
         self.qkv = torch.empty(batch, (cfg.n_heads + 2 * hkv) * hd, **bf)
         self.q = torch.empty(batch, cfg.n_heads * hd, **bf)  # rotated q (one-row steps: the qkv epilogue's)
         self.attn = torch.empty(batch, cfg.n_heads * hd, **bf)
@@ -367,13 +368,13 @@ class Int4DecodeLM:
         return nxt
 
     def _norm_sums_linear(self, st: DecodeState, tw: i4.Int4Tiled, y: Tensor, stream: int) -> None:
-        """One row: ``tw`` applied to RMSNorm(h) as ``r * (bf16(h * gain) @ W^T)``: ``st.h`` holds
+        """``tw`` applied to RMSNorm(h) as ``r * (bf16(h * gain) @ W^T)`` per row: ``st.h`` holds
         bf16(h * gain) and ``st.ss`` the sums of squares of h, both left by the residual epilogue of
         the linear that wrote h; the row factor r is formed from the sums in the linear's epilogue."""
         lib = _lib.load()
         _lib.check(lib.sqx_int4_linear_rowscale_sumsq(
-            tw.wt.data_ptr(), tw.st.data_ptr(), st.h.data_ptr(), st.ss.data_ptr(), st.ss.numel(), self.cfg.norm_eps,
-            y.data_ptr(), 1, tw.rows, tw.cols, tw.group_size, 0, stream), "rmsnorm (row factor) + int4 linear")
+            tw.wt.data_ptr(), tw.st.data_ptr(), st.h.data_ptr(), st.ss.data_ptr(), st.nss, self.cfg.norm_eps,
+            y.data_ptr(), st.batch, tw.rows, tw.cols, tw.group_size, 0, stream), "rmsnorm (row factor) + int4 linear")
 
     STEP_KINDS = ("qkv", "attention", "o", "gate_up", "down", "lm_head", "other")
 
@@ -398,16 +399,25 @@ class Int4DecodeLM:
         def go(kind: str) -> bool:
             return only is None or only == kind
 
-        fuse_silu = self.fuse_silu and lib.sqx_int4_prologue_fits(B, cfg.d_ff)
-        sums = (self.fuse_norm_sums and B == 1 and d <= 8192 and lib.sqx_int4_prologue_fits(1, d)
-                and lib.sqx_int4_prologue_fits(1, cfg.d_ff))
-        # one row with a bf16 cache: RoPE and the cache write run in the q|k|v projection's epilogue,
-        # which takes fewer than 1024 row tiles of 16 (wider projections keep the separate RoPE)
-        rope_in_qkv = sums and st.kv_dtype == "bf16" and (H + 2 * Hkv) * hd // 16 < 1024
+        fuse_silu = self.fuse_silu and lib.sqx_int4_linear_silu_fits(B, d, cfg.d_ff)
+        # no norm launches: each residual add ends a linear and leaves the sums of squares its norm needs,
+        # and the linear after the norm applies the row factor (one row: the one-row GEMV; 2..8 rows:
+        # the multi-row GEMV, where it takes every linear of the step)
+        qkv_rows = (H + 2 * Hkv) * hd
+        if B == 1:
+            sums = (self.fuse_norm_sums and d <= 8192 and lib.sqx_int4_prologue_fits(1, d)
+                    and lib.sqx_int4_prologue_fits(1, cfg.d_ff))
+        else:
+            rf = lib.sqx_int4_rows_fits
+            sums = (self.fuse_norm_sums and d <= 8192 and d % 64 == 0 and rf(B, qkv_rows, d, 1) and rf(B, d, d, 0)
+                    and rf(B, 2 * cfg.d_ff, d, 1) and rf(B, d, cfg.d_ff, 0) and rf(B, cfg.vocab_size, d, 1))
+        # with a bf16 cache: RoPE and the cache write run in the q|k|v projection's epilogue (the one-row
+        # form takes fewer than 1024 row tiles of 16; wider projections keep the separate RoPE)
+        rope_in_qkv = sums and st.kv_dtype == "bf16" and (B > 1 or qkv_rows // 16 < 1024)
         # one row: the attention combine runs in the o projection's activation load (two 128-column
         # k-blocks per wave)
         kb_o = d // 128
-        merge = (self.fuse_attn_merge and sums and d % 256 == 0 and kb_o // 2 <= 16 and H * hd == d)
+        merge = (self.fuse_attn_merge and sums and B == 1 and d % 256 == 0 and kb_o // 2 <= 16 and H * hd == d)
         with torch.cuda.device(self.device):
             if go("other"):
                 ck(lib.sqx_embed(self.embed.data_ptr(), cfg.vocab_size, st.tokens.data_ptr(), B, d,
@@ -422,9 +432,9 @@ class Int4DecodeLM:
                     if go("qkv"):
                         ck(lib.sqx_int4_linear_rope_kv(
                             ly.wqkv.wt.data_ptr(), ly.wqkv.st.data_ptr(), st.h.data_ptr(),
-                            st.ss.data_ptr() if have_ss else None, st.ss.numel(), cfg.norm_eps,
+                            st.ss.data_ptr() if have_ss else None, st.nss, cfg.norm_eps,
                             st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(), cfg.context_length, H,
-                            Hkv, T, st.q.data_ptr(), st.k[li].data_ptr(), st.v[li].data_ptr(), ly.wqkv.rows,
+                            Hkv, T, st.q.data_ptr(), st.k[li].data_ptr(), st.v[li].data_ptr(), B, ly.wqkv.rows,
                             ly.wqkv.cols, ly.wqkv.group_size, 0, s), "qkv + rope + cache write")
                 elif have_ss:
                     if go("qkv"):
@@ -472,7 +482,7 @@ class Int4DecodeLM:
                     elif go("o"):
                         ck(lib.sqx_int4_linear_residual(
                             ly.wo.wt.data_ptr(), ly.wo.st.data_ptr(), st.attn.data_ptr(), st.x[cur].data_ptr(),
-                            st.x[1 - cur].data_ptr(), st.ss.data_ptr(), ly.ffn_norm.data_ptr(), st.h.data_ptr(), 1,
+                            st.x[1 - cur].data_ptr(), st.ss.data_ptr(), ly.ffn_norm.data_ptr(), st.h.data_ptr(), B,
                             ly.wo.rows, ly.wo.cols, ly.wo.group_size, 0, s), "o + residual")
                     cur = 1 - cur
                     if go("gate_up"):
@@ -480,7 +490,7 @@ class Int4DecodeLM:
                     if go("down"):
                         ck(lib.sqx_int4_linear_silu_residual(
                             ly.w2.wt.data_ptr(), ly.w2.st.data_ptr(), st.gu.data_ptr(), st.x[cur].data_ptr(),
-                            st.x[1 - cur].data_ptr(), st.ss.data_ptr(), gain_next.data_ptr(), st.h.data_ptr(), 1,
+                            st.x[1 - cur].data_ptr(), st.ss.data_ptr(), gain_next.data_ptr(), st.h.data_ptr(), B,
                             ly.w2.rows, ly.w2.cols, ly.w2.group_size, 0, s), "silu + down + residual")
                     cur, have_ss = 1 - cur, True
                     continue

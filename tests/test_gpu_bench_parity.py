@@ -187,7 +187,7 @@ def test_config5_full_model_graph_equals_eager(B):
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("B", [1, 8, 32, 64])
+@pytest.mark.parametrize("B", [1, 3, 8, 32, 64])
 def test_config5_full_width_against_oracle(B):
     """A two-layer model at Llama-3-8B width (d 4096, 32 q / 8 kv heads, SwiGLU 14336, vocab 128256,
     context 2048 with 2046 random cached keys per row) for two steps against the decode oracle's bf16

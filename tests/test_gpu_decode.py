@@ -275,59 +275,93 @@ def test_linear_rmsnorm_equals_two_calls(lib, m, k, group, with_delta):
         assert torch.equal(h1, h2)
 
 
-@pytest.mark.parametrize("m,f", [(1, 14336), (2, 14336), (5, 2048)])
-def test_linear_silu_equals_two_calls(lib, m, f):
-    print_case("linear+silu", m, f)
-    n = 4096 if f == 14336 else 1000
-    tw = _tiled(n, f, 128, seed=f)
+@pytest.mark.parametrize("m,f,n", [(1, 14336, 4096), (2, 14336, 4096), (3, 14336, 4096), (4, 14336, 4096),
+                                   (5, 2048, 1000), (7, 4096, 1024), (2, 1056, 200)])
+def test_linear_silu_equals_two_calls(lib, m, f, n):
+    """sqx_int4_linear_silu == sqx_silu_mul then the linear, bit for bit: with the library's choice
+    (k_slices 0: the multi-row GEMV's slices where the library's linear of those rows is that kernel)
+    against sqx_int4_skinny's choice, and with explicit waves (the GEMV's LDS copy) against
+    sqx_int4_linear with the same waves."""
+    print_case("linear+silu", m, f, n)
+    tw = _tiled(n, f, 32 if f == 1056 else 128, seed=f + m)
+    group = tw.group_size
     gu = (torch.randn(m, 2 * f, generator=torch.Generator().manual_seed(m)) * 3).bfloat16().to(DEV)
     act = torch.empty(m, f, dtype=torch.bfloat16, device=DEV)
     y1, y2 = (torch.empty(m, n, dtype=torch.bfloat16, device=DEV) for _ in range(2))
     _ok(lib, lib.sqx_silu_mul(gu.data_ptr(), m, f, act.data_ptr(), _s()))
-    ks = lib.sqx_int4_linear_default_kslices(m, n, f)  # the GEMV the fused kernel runs
-    _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, act.data_ptr(), 1, y1.data_ptr(), None, m, n,
-                                 f, 128, ks, _s()))
-    _ok(lib, lib.sqx_int4_linear_silu(tw.wt.data_ptr(), tw.st.data_ptr(), gu.data_ptr(), y2.data_ptr(), m, n, f, 128, 0,
-                                      _s()))
+    assert lib.sqx_int4_linear_silu_fits(m, n, f) == 1
+    if m == 1:
+        ks = lib.sqx_int4_linear_default_kslices(m, n, f)  # the GEMV the fused kernel runs
+        _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, act.data_ptr(), 1, y1.data_ptr(), None,
+                                     m, n, f, group, ks, _s()))
+    else:
+        nb = lib.sqx_int4_skinny_workspace_bytes(m, n, f, 0)
+        ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=DEV)
+        _ok(lib, lib.sqx_int4_skinny(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, act.data_ptr(), 1, y1.data_ptr(), None,
+                                     m, n, f, group, -1, 0, 0, 0, ws.data_ptr() if nb > 0 else None, nb, _s()))
+    _ok(lib, lib.sqx_int4_linear_silu(tw.wt.data_ptr(), tw.st.data_ptr(), gu.data_ptr(), y2.data_ptr(), m, n, f, group,
+                                      0, _s()))
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
+    if lib.sqx_int4_prologue_fits(m, f):  # explicit waves: the GEMV with the workgroup's copy
+        ks = 4
+        _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, act.data_ptr(), 1, y1.data_ptr(), None,
+                                     m, n, f, group, ks, _s()))
+        _ok(lib, lib.sqx_int4_linear_silu(tw.wt.data_ptr(), tw.st.data_ptr(), gu.data_ptr(), y2.data_ptr(), m, n, f,
+                                          group, ks, _s()))
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2)
 
 
-@pytest.mark.parametrize("n,k,group,silu", [(4096, 4096, 128, False), (4096, 14336, 128, True), (1000, 1056, 32, False),
-                                            (200, 2048, 64, True)])
-def test_linear_residual_equals_two_calls(lib, n, k, group, silu):
-    """sqx_int4_linear_residual / _silu_residual: the residual stream bit for bit as the GEMV form of
-    the linear followed by the bf16 add, and the sums of squares per 16 outputs against float64
-    (fp32 sums of 16 squares: 16 roundings of at most 2**-24 of the sum)."""
-    print_case("linear+residual", n, k, group, silu)
+def _rows_linear(lib, tw, x, m, n, k, group):
+    """The linear the fused forms run: the one-row GEMV (m = 1) or the multi-row GEMV (variant 2)."""
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    if m == 1:
+        ks = lib.sqx_int4_linear_default_kslices(1, n, k)
+        _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, x.data_ptr(), 1, y.data_ptr(), None,
+                                     1, n, k, group, ks, _s()))
+    else:
+        _ok(lib, lib.sqx_int4_skinny(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, x.data_ptr(), 1, y.data_ptr(), None,
+                                     m, n, k, group, 2, 0, 0, 1, None, 0, _s()))
+    return y
+
+
+@pytest.mark.parametrize("n,k,group,silu,m", [(4096, 4096, 128, False, 1), (4096, 14336, 128, True, 1),
+                                              (1000, 1056, 32, False, 1), (200, 2048, 64, True, 1),
+                                              (4096, 4096, 128, False, 2), (4096, 14336, 128, True, 3),
+                                              (4096, 14336, 128, True, 4), (1000, 1056, 32, False, 4),
+                                              (200, 2048, 64, True, 8), (4096, 4096, 128, False, 7)])
+def test_linear_residual_equals_two_calls(lib, n, k, group, silu, m):
+    """sqx_int4_linear_residual / _silu_residual: the residual stream bit for bit as the linear they run
+    (the one-row GEMV, or for 2..8 rows the multi-row GEMV) followed by the bf16 add, and the sums of
+    squares per row and 16 outputs against float64 (fp32 sums of 16 squares: 16 roundings of at most
+    2**-24 of the sum)."""
+    print_case("linear+residual", n, k, group, silu, m)
     tw = _tiled(n, k, group, seed=n + k)
-    g = torch.Generator().manual_seed(n)
-    x = (torch.randn(1, 2 * k if silu else k, generator=g) * 2).bfloat16().to(DEV)
-    res = (torch.randn(1, n, generator=g) * 3).bfloat16().to(DEV)
-    act = torch.empty(1, k, dtype=torch.bfloat16, device=DEV)
-    y = torch.empty(1, n, dtype=torch.bfloat16, device=DEV)
-    out = torch.empty(1, n, dtype=torch.bfloat16, device=DEV)
+    g = torch.Generator().manual_seed(n + m)
+    x = (torch.randn(m, 2 * k if silu else k, generator=g) * 2).bfloat16().to(DEV)
+    res = (torch.randn(m, n, generator=g) * 3).bfloat16().to(DEV)
+    act = torch.empty(m, k, dtype=torch.bfloat16, device=DEV)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
     nt = -(-n // 16)
-    ss = torch.full((nt,), float("nan"), dtype=torch.float32, device=DEV)
+    ss = torch.full((m, nt), float("nan"), dtype=torch.float32, device=DEV)
     src = x
     if silu:
-        _ok(lib, lib.sqx_silu_mul(x.data_ptr(), 1, k, act.data_ptr(), _s()))
+        _ok(lib, lib.sqx_silu_mul(x.data_ptr(), m, k, act.data_ptr(), _s()))
         src = act
-    ks = lib.sqx_int4_linear_default_kslices(1, n, k)
-    _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, src.data_ptr(), 1, y.data_ptr(), None, 1,
-                                 n, k, group, ks, _s()))
+    y = _rows_linear(lib, tw, src, m, n, k, group)
     fn = lib.sqx_int4_linear_silu_residual if silu else lib.sqx_int4_linear_residual
     gain = (1 + 0.1 * torch.randn(n, generator=g)).bfloat16().to(DEV)
-    hg = torch.empty(1, n, dtype=torch.bfloat16, device=DEV)
+    hg = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
     _ok(lib, fn(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), res.data_ptr(), out.data_ptr(), ss.data_ptr(),
-                gain.data_ptr(), hg.data_ptr(), 1, n, k, group, 0, _s()))
+                gain.data_ptr(), hg.data_ptr(), m, n, k, group, 0, _s()))
     torch.cuda.synchronize()
     want = (res.float() + y.float()).bfloat16()  # the reference's bf16 add
     assert torch.equal(out, want)
     assert torch.equal(hg, (want.float() * gain.float()).bfloat16())  # bf16(h * gain): one rounding
-    h = torch.zeros(nt * 16, dtype=torch.float64)
-    h[:n] = out.cpu().double()[0]
-    ref = (h * h).view(nt, 16).sum(1)
+    h = torch.zeros(m, nt * 16, dtype=torch.float64)
+    h[:, :n] = out.cpu().double()
+    ref = (h * h).view(m, nt, 16).sum(2)
     got = ss.cpu().double()
     assert torch.isfinite(got).all()
     assert float(((got - ref).abs() / (16 * 2.0**-24 * ref + 1e-30)).max()) <= 1.0
@@ -372,8 +406,10 @@ def test_linear_rmsnorm_sumsq(lib, n, k, group):
     assert float(d.max()) <= 2.0**-6 * float(y1.float().abs().max())
 
 
-@pytest.mark.parametrize("n,k,group", [(6144, 4096, 128), (28672, 4096, 128), (128256, 4096, 128), (1000, 1056, 32)])
-def test_linear_rowscale_sumsq(lib, n, k, group):
+@pytest.mark.parametrize("n,k,group,m", [(6144, 4096, 128, 1), (28672, 4096, 128, 1), (128256, 4096, 128, 1),
+                                         (1000, 1056, 32, 1), (6144, 4096, 128, 2), (28672, 4096, 128, 4),
+                                         (128256, 4096, 128, 3), (1000, 1024, 32, 8)])
+def test_linear_rowscale_sumsq(lib, n, k, group, m):
     """sqx_int4_linear_rowscale_sumsq: RMSNorm's row factor applied to the product of bf16(h * gain)
     against the oracle: the float64 product of the reference's normalised row bf16(h * r * gain) and the
     bf16-cast dequantized weight, at the gate/up (8-wave form), qkv and lm_head shapes. Max-abs-rel
@@ -384,24 +420,24 @@ def test_linear_rowscale_sumsq(lib, n, k, group):
     from oracle import quant_ref as R
     from scratch_llm_amd.quant import int4_group as i4
 
-    print_case("linear rowscale sums", n, k, group)
+    print_case("linear rowscale sums", n, k, group, m)
     w = (torch.randn(n, k, generator=torch.Generator().manual_seed(n + group)) * 0.05).to(DEV)
     q, sc = i4.quantize_groupwise_int4(w, group)
     tw = i4.tile_int4(q, sc, None, group)
     del w
-    g = torch.Generator().manual_seed(k + n)
-    h = (torch.randn(1, k, generator=g) * 2).bfloat16()
+    g = torch.Generator().manual_seed(k + n + m)
+    h = (torch.randn(m, k, generator=g) * 2 * torch.linspace(0.5, 4, m)[:, None]).bfloat16()  # rows of other scales
     gain = (1 + 0.1 * torch.randn(k, generator=g)).bfloat16()
     nt = -(-k // 16)
-    hp = torch.zeros(nt * 16, dtype=torch.float32)
-    hp[:k] = h.float()[0]
-    ss = (hp * hp).view(nt, 16).sum(1).to(DEV)
+    hp = torch.zeros(m, nt * 16, dtype=torch.float32)
+    hp[:, :k] = h.float()
+    ss = (hp * hp).view(m, nt, 16).sum(2).contiguous().to(DEV)
     hg = (h.float() * gain.float()).bfloat16().to(DEV)
-    y = torch.empty(1, n, dtype=torch.bfloat16, device=DEV)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
     _ok(lib, lib.sqx_int4_linear_rowscale_sumsq(tw.wt.data_ptr(), tw.st.data_ptr(), hg.data_ptr(), ss.data_ptr(), nt,
-                                                1e-5, y.data_ptr(), 1, n, k, group, 0, _s()))
+                                                1e-5, y.data_ptr(), m, n, k, group, 0, _s()))
     torch.cuda.synchronize()
-    hn = D.rmsnorm(h, gain, 1e-5)  # the reference's normalised row (bf16)
+    hn = D.rmsnorm(h, gain, 1e-5)  # the reference's normalised rows (bf16)
     rows = torch.arange(0, n, max(1, n // 8192))
     w_eff = R.round_bf16(R.dequantize_groupwise_int4(q[rows.to(DEV)].cpu().numpy(), sc[rows.to(DEV)].cpu().numpy(), group))
     a = hn.float().numpy().astype(np.float64)
@@ -413,53 +449,57 @@ def test_linear_rowscale_sumsq(lib, n, k, group):
     assert float((err / bound).max()) <= 1.0, f"rowscale {k}->{n}: {float((err / bound).max()):.2f}x the bound"
 
 
-@pytest.mark.parametrize("H,Hkv,T,length,sums", [(32, 8, 2048, 2047, True), (32, 8, 2048, 0, False),
-                                                  (8, 2, 100, 140, True), (16, 16, 64, 37, False)])
-def test_linear_rope_kv_equals_two_calls(lib, H, Hkv, T, length, sums):
-    """sqx_int4_linear_rope_kv == the linear (sqx_int4_linear_rowscale_sumsq, or the plain one-row GEMV)
-    followed by sqx_rope_kv on its output, bit for bit: the rotated q, and the cache rows (only row
-    min(length, T - 1) changes), at a full slot and at position 0 too."""
+@pytest.mark.parametrize("H,Hkv,T,length,sums,m", [(32, 8, 2048, 2047, True, 1), (32, 8, 2048, 0, False, 1),
+                                                    (8, 2, 100, 140, True, 1), (16, 16, 64, 37, False, 1),
+                                                    (32, 8, 2048, 2040, True, 4), (8, 2, 100, 50, False, 2),
+                                                    (16, 16, 64, 37, True, 8)])
+def test_linear_rope_kv_equals_two_calls(lib, H, Hkv, T, length, sums, m):
+    """sqx_int4_linear_rope_kv == the linear (sqx_int4_linear_rowscale_sumsq, or the plain one-row /
+    multi-row GEMV) followed by sqx_rope_kv on its output, bit for bit: the rotated q, and the cache
+    rows (only row min(length, T - 1) of each slot changes; rows of m slots sit at positions length,
+    length + 3, ...), at a full slot and at position 0 too."""
     from scratch_llm_amd.quant import int4_group as i4
 
-    print_case("linear rope kv", H, Hkv, T, length, sums)
+    print_case("linear rope kv", H, Hkv, T, length, sums, m)
     hd, k = 128, 4096 if H == 32 else 1024
     n = (H + 2 * Hkv) * hd
     w = (torch.randn(n, k, generator=torch.Generator().manual_seed(n + k)) * 0.05).to(DEV)
     q, sc = i4.quantize_groupwise_int4(w)
     tw = i4.tile_int4(q, sc)
     del w
-    g = torch.Generator().manual_seed(H + T)
-    x = (torch.randn(1, k, generator=g) * 2).bfloat16().to(DEV)
+    g = torch.Generator().manual_seed(H + T + m)
+    x = (torch.randn(m, k, generator=g) * 2).bfloat16().to(DEV)
     nt = k // 16
-    ss = (torch.rand(nt, generator=g) * 50).to(DEV) if sums else None
-    ctx = max(T, length + 1) + 8
+    ss = (torch.rand(m, nt, generator=g) * 50).to(DEV) if sums else None
+    lens = [length + 3 * r for r in range(m)]
+    ctx = max(T, max(lens) + 1) + 8
     cos, sin = (t.to(DEV) for t in D.rope_tables(hd, ctx, 10000.0))
-    ln = torch.tensor([length], dtype=torch.int32, device=DEV)
-    cache = torch.randn(2, 1, Hkv, T, hd, generator=g).bfloat16().to(DEV)
+    ln = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    cache = torch.randn(2, m, Hkv, T, hd, generator=g).bfloat16().to(DEV)
     # the two-call form
-    y = torch.empty(1, n, dtype=torch.bfloat16, device=DEV)
     if sums:
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
         _ok(lib, lib.sqx_int4_linear_rowscale_sumsq(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), ss.data_ptr(), nt,
-                                                    1e-5, y.data_ptr(), 1, n, k, 128, 0, _s()))
+                                                    1e-5, y.data_ptr(), m, n, k, 128, 0, _s()))
     else:
-        _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, 0, x.data_ptr(), 1, y.data_ptr(), None,
-                                     1, n, k, 128, 0, _s()))
-    q2 = torch.empty(1, H, hd, dtype=torch.bfloat16, device=DEV)
+        y = _rows_linear(lib, tw, x, m, n, k, 128)
+    q2 = torch.empty(m, H, hd, dtype=torch.bfloat16, device=DEV)
     kc2, vc2 = cache[0].clone(), cache[1].clone()
-    _ok(lib, lib.sqx_rope_kv(y.data_ptr(), ln.data_ptr(), cos.data_ptr(), sin.data_ptr(), ctx, 1, H, Hkv, hd, T,
+    _ok(lib, lib.sqx_rope_kv(y.data_ptr(), ln.data_ptr(), cos.data_ptr(), sin.data_ptr(), ctx, m, H, Hkv, hd, T,
                              q2.data_ptr(), kc2.data_ptr(), vc2.data_ptr(), _s()))
     # the fused form
-    q1 = torch.empty(1, H * hd, dtype=torch.bfloat16, device=DEV)
+    q1 = torch.empty(m, H * hd, dtype=torch.bfloat16, device=DEV)
     kc1, vc1 = cache[0].clone(), cache[1].clone()
     _ok(lib, lib.sqx_int4_linear_rope_kv(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(),
                                          None if ss is None else ss.data_ptr(), nt, 1e-5, ln.data_ptr(), cos.data_ptr(),
                                          sin.data_ptr(), ctx, H, Hkv, T, q1.data_ptr(), kc1.data_ptr(), vc1.data_ptr(),
-                                         n, k, 128, 0, _s()))
+                                         m, n, k, 128, 0, _s()))
     torch.cuda.synchronize()
-    assert torch.equal(q1.view(1, H, hd), q2)
+    assert torch.equal(q1.view(m, H, hd), q2)
     assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
-    slot = min(length, T - 1)
-    assert not torch.equal(kc1[:, :, slot], cache[0][:, :, slot])
+    for r in range(m):
+        slot = min(lens[r], T - 1)
+        assert not torch.equal(kc1[r, :, slot], cache[0][r, :, slot])
 
 
 def _partials(lib, q, lengths, k, v, B, H, Hkv, T, cos=None, sin=None, rope_rows=0, ks=None, vs=None):
@@ -629,11 +669,17 @@ def test_linear_attn_residual_refuses(lib):
 
 def test_residual_forms_refuse(lib):
     tw = _tiled(64, 4096, 128, seed=3)
-    x = torch.zeros(2, 4096, dtype=torch.bfloat16, device=DEV)
-    ss = torch.zeros(256, dtype=torch.float32, device=DEV)
+    x = torch.zeros(9, 4096, dtype=torch.bfloat16, device=DEV)
+    ss = torch.zeros(9 * 256, dtype=torch.float32, device=DEV)
     assert lib.sqx_int4_linear_residual(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
-                                        ss.data_ptr(), None, None, 2, 64, 4096, 128, 0, _s()) == -1
-    assert "one-row" in lib.sqx_last_error().decode()
+                                        ss.data_ptr(), None, None, 9, 64, 4096, 128, 0, _s()) == -1
+    assert "2..8 rows" in lib.sqx_last_error().decode()
+    tw14 = _tiled(64, 14336, 128, seed=4)  # 112 k-blocks: k-slices of 7 blocks, more than 5 rows take
+    x14 = torch.zeros(5, 14336, dtype=torch.bfloat16, device=DEV)
+    assert lib.sqx_int4_rows_fits(5, 64, 14336, 0) == 0 and lib.sqx_int4_rows_fits(4, 64, 14336, 0) == 1
+    assert lib.sqx_int4_linear_residual(tw14.wt.data_ptr(), tw14.st.data_ptr(), x14.data_ptr(), x.data_ptr(),
+                                        x.data_ptr(), ss.data_ptr(), None, None, 5, 64, 14336, 128, 0, _s()) == -1
+    assert "multi-row form" in lib.sqx_last_error().decode()
     assert lib.sqx_int4_linear_residual(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
                                         ss.data_ptr(), x.data_ptr(), None, 1, 64, 4096, 128, 0, _s()) == -1
     assert "go together" in lib.sqx_last_error().decode()
@@ -778,24 +824,34 @@ def test_decode_step_matches_reference(small, B):
     _run_and_compare(model, refs, B, steps=6 if B < 64 else 3, seed=B)
 
 
-@pytest.mark.parametrize("B", [1, 2, 5])
+@pytest.mark.parametrize("B", [1, 2, 4, 5])
 def test_fused_step_equals_unfused_step(small, B):
-    """The norm and SiLU gate folded into the linears change no bit of the step."""
+    """The SiLU gate folded into the down projection changes no bit of the step (both forms run the
+    library's linear for the batch). The norm folded into the GEMV's LDS copy (fuse_norm) is
+    bit-identical at one row; at more rows the two-call form's linear may be the multi-row GEMV,
+    which sums in another order, so the logits agree to the bf16 rounding of the step."""
     model, _ = small
     print_case("fused vs unfused step", B)
-    a, b = model.new_state(B, 32), model.new_state(B, 32)
-    tok = torch.arange(B) * 97 % model.cfg.vocab_size
     try:
         model.fuse_norm_sums = False  # its norm adds the sum of squares in another order (tested below)
-        for t in range(4):
-            model.fuse_norm = model.fuse_silu = True
-            model.step(a, tok if t == 0 else None)
-            model.fuse_norm = model.fuse_silu = False
-            model.step(b, tok if t == 0 else None)
-            torch.cuda.synchronize()
-            assert torch.equal(a.logits, b.logits), f"step {t}"
-            assert torch.equal(a.tokens, b.tokens)
-        assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
+        for fuse_norm in (False, True):
+            a, b = model.new_state(B, 32), model.new_state(B, 32)
+            tok = torch.arange(B) * 97 % model.cfg.vocab_size
+            for t in range(4):
+                model.fuse_norm, model.fuse_silu = fuse_norm, True
+                model.step(a, tok if t == 0 else None)
+                model.fuse_norm = model.fuse_silu = False
+                model.step(b, tok if t == 0 else None)
+                torch.cuda.synchronize()
+                if fuse_norm and B > 1:
+                    scale = float(b.logits.float().abs().max())
+                    assert float((a.logits.float() - b.logits.float()).abs().max()) <= 2.0**-5 * scale, f"step {t}"
+                    b.tokens.copy_(a.tokens)  # follow the same tokens
+                    continue
+                assert torch.equal(a.logits, b.logits), f"fuse_norm={fuse_norm} step {t}"
+                assert torch.equal(a.tokens, b.tokens)
+            if not (fuse_norm and B > 1):
+                assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
     finally:
         model.fuse_norm, model.fuse_silu, model.fuse_norm_sums = False, True, True
 
@@ -861,14 +917,22 @@ def test_rmsnorm_partials_equals_reduce_then_norm(lib):
     assert "does not split" in lib.sqx_last_error().decode()
 
 
-def test_norm_sums_step_matches_reference_both_ways(small):
-    """One row with the norms folded into the residual epilogues (the default) and without: both
-    within the reference bar of the step oracle at every step (_run_and_compare), from the same tokens."""
+@pytest.mark.parametrize("B", [1, 2, 4, 8])
+def test_norm_sums_step_matches_reference_both_ways(small, B):
+    """The step with the norms folded into the residual epilogues (the default: the one-row GEMV at one
+    row, the multi-row GEMV at 2..8 rows) and without: both within the reference bar of the step
+    oracle at every step (_run_and_compare), from the same tokens."""
     model, refs = small
+    from scratch_llm_amd import _lib
+
+    lib = _lib.load()
+    cfg = model.cfg
+    if B > 1:  # the small model's linears all fit the multi-row form, so the default step is the fused one
+        assert lib.sqx_int4_rows_fits(B, cfg.d_model, cfg.d_ff, 0) == 1
     try:
         for flag in (True, False):
             model.fuse_norm_sums = flag
-            _run_and_compare(model, refs, 1, steps=5, seed=11)
+            _run_and_compare(model, refs, B, steps=5, seed=11 + B)
     finally:
         model.fuse_norm_sums = True
 
@@ -892,6 +956,27 @@ def test_graph_replays_equal_eager_steps(small):
         assert torch.equal(a.tokens, b.tokens) and torch.equal(a.lengths, b.lengths)
     assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
     assert b.lengths.cpu().tolist() == [steps] * B
+
+
+@pytest.mark.parametrize("B", [2, 5])
+def test_fused_rows_graph_replays_equal_eager_steps(small, B):
+    """The 2..8-row step without norm launches (residual epilogues, row factors, RoPE in the qkv
+    epilogue on the multi-row GEMV) captured and replayed equals eager steps bit for bit."""
+    model, _ = small
+    print_case("graph replay fused rows", B)
+    a, b = model.new_state(B, 32), model.new_state(B, 32)
+    tok = torch.arange(B) * 131 % model.cfg.vocab_size
+    a.set_tokens(tok, model.cfg.vocab_size)
+    b.set_tokens(tok, model.cfg.vocab_size)
+    graph = model.capture(b)
+    for t in range(5):
+        model.step(a)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(a.logits, b.logits), f"replay {t}"
+        assert torch.equal(a.tokens, b.tokens) and torch.equal(a.lengths, b.lengths)
+    assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
 
 
 @pytest.mark.parametrize("merge", [False, True])

@@ -83,6 +83,51 @@ def test_skinny_llama_shapes_default(q4, n, k, m):
     _check_linear(y, R.linear_f64(x.float().cpu().numpy(), w_eff), f"{k}->{n} M={m}")
 
 
+@pytest.mark.parametrize(
+    "n,k,group,m,waves",
+    [
+        (4096, 4096, 128, 2, 0), (4096, 4096, 128, 4, 0), (4096, 4096, 128, 8, 0), (4096, 4096, 128, 3, 4),
+        (1024, 4096, 128, 5, 8), (6144, 4096, 128, 7, 16), (4096, 14336, 128, 4, 0), (4096, 14336, 128, 2, 16),
+        (1000, 1056, 32, 6, 0),  # rows not a multiple of 16, a K tail with four groups per block
+        (200, 96, 32, 3, 0),  # columns not a multiple of 128, one block
+        (48, 2048, 64, 8, 4), (300, 4096, 32, 4, 4),
+    ],
+)
+def test_rows_gemv_matches_oracle(q4, n, k, group, m, waves):
+    """The multi-row GEMV (variant 2): 2..8 rows, the per-row activation sums charging the code offset."""
+    print_case("rows gemv", n, k, group, m, waves)
+    tw, w_eff = _sym(q4, n, k, group, 5 * n + k + m)
+    x = _act(m, k, 7 * m + k).to(DEV)
+    y = q4.int4_linear_skinny(x, tw, variant=2, waves=waves)
+    torch.cuda.synchronize()
+    _check_linear(y, R.linear_f64(x.float().cpu().numpy(), w_eff), f"rows {k}->{n} g{group} M={m} waves={waves}")
+    assert torch.equal(y, q4.int4_linear_skinny(x, tw, variant=2, waves=waves))  # fixed-order sums
+    # each row alone through the one-row GEMV agrees to bf16 precision
+    for r in (0, m - 1):
+        y1 = q4.int4_linear_tiled(x[r:r + 1], tw)
+        assert float((y1.float() - y[r:r + 1].float()).abs().max()) <= 2.0**-7 * float(y1.float().abs().max())
+
+
+def test_rows_gemv_asymmetric_fp16_bias(q4):
+    n, k = 400, 2048
+    w = _weight((n, k), 23, dtype=torch.float32).numpy()
+    for group, param in ((128, "bf16"), (64, "f32"), (32, "bf16")):
+        qa, sa, za = R.quantize_groupwise_uint4_asym(w, group, param=param)
+        pdt = torch.bfloat16 if param == "bf16" else torch.float32
+        tw = q4.tile_int4(torch.from_numpy(qa).to(DEV), torch.from_numpy(sa).to(pdt).to(DEV),
+                          torch.from_numpy(za).to(pdt).to(DEV), group)
+        w_eff = R.dequantize_groupwise_uint4_asym(qa, sa, za, group)
+        for dt, rnd in ((torch.bfloat16, "bf16"), (torch.float16, "f16")):
+            for m in (2, 4, 8):
+                print_case("rows gemv asym", group, param, dt, m)
+                x = _act(m, k, group + m, dtype=dt).to(DEV)
+                bias = torch.randn(n, dtype=dt, device=DEV)
+                y = q4.int4_linear_skinny(x, tw, bias, variant=2)
+                assert y.dtype == dt
+                y_ref = R.linear_f64(x.float().cpu().numpy(), R.round_to(w_eff, rnd), bias.float().cpu().numpy())
+                _check_linear(y, y_ref, f"rows asym g{group} {param} {dt} M={m}")
+
+
 def test_skinny_asymmetric_fp16_bias(q4):
     n, k = 160, 1024
     w = _weight((n, k), 21, dtype=torch.float32).numpy()
@@ -139,7 +184,9 @@ def test_skinny_rejects(q4):
     assert lib.sqx_int4_skinny(*args, 0, 1, 2, 1, None, 0, st) == E_ARG  # waves splitting K: tiles 2 or 4
     assert lib.sqx_int4_skinny(*args, 0, 2, 9, 1, None, 0, st) == E_ARG  # waves <= 8
     assert lib.sqx_int4_skinny(*args, 1, 2, 6, 1, None, 0, st) == E_ARG  # LDS-staged: 4 or 8 compute waves
-    assert lib.sqx_int4_skinny(*args, 2, 2, 4, 1, None, 0, st) == E_ARG  # no variant 2
+    assert lib.sqx_int4_skinny(*args, 3, 2, 4, 1, None, 0, st) == E_ARG  # no variant 3
+    assert lib.sqx_int4_skinny(*args, 2, 0, 17, 1, None, 0, st) == E_ARG  # multi-row GEMV: at most 16 waves
+    assert lib.sqx_int4_skinny(*args, 2, 0, 0, 2, None, 0, st) == E_ARG  # multi-row GEMV: no K split
     assert lib.sqx_int4_skinny(*args, 0, 2, 1, 2, None, 0, st) == E_ARG  # splits need a workspace
     assert "workspace" in lib.sqx_last_error().decode()
     assert lib.sqx_int4_skinny_workspace_bytes(8, 64, 256, 2) == 2 * 8 * 64 * 4
