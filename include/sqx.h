@@ -135,8 +135,10 @@ int sqx_int4_linear(const uint8_t* wt, const void* st, const void* zt, int param
  * activations are staged through LDS and shared by `waves` compute waves (4, or 8 as two k-groups)
  * that own disjoint tiles (tiles 1, 2 or 4). variant 2: the multi-row GEMV (2 <= m <= 8; one
  * workgroup per tile whose `waves` (0: default, at most 16) take k-slices of at most 8 blocks for
- * m <= 4 or 4 blocks for m <= 8, each wave copying its slice of the rows into LDS; tiles ignored,
- * splits 1). splits >= 1 workgroups split K further and write fp32
+ * m <= 4 or 4 blocks for 5..8 rows in one workgroup, each wave copying its slice of the rows into LDS;
+ * tiles = the row groups: 1 = one workgroup per tile, 2 = (5..8 rows) two workgroups of four rows per
+ * tile on one XCD, 0 = the library's choice; splits 1). splits >= 1 workgroups split K further and
+ * write fp32
  * partials to ws, added in split order by a second kernel. variant < 0 is the library's choice for
  * the shape, the decode GEMV included when tiles, waves and splits are all <= 0; tiles, waves or
  * splits <= 0 pick the default of the variant (splits > 1 only when ws is given). The library may

@@ -829,21 +829,45 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
 //                       q_out [M][qn], k_cache / v_cache [M][kn / 128][tmax][128].
 // The epilogue's residual, gain and length values are requested at kernel start (cos / sin behind the
 // activation slice), by the threads that use them.
-template <class A, class W, int MR, int XW, int PRO = kProPlain, bool RES = false, bool RKV = false>
-__global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
-                                                         uint16_t* __restrict__ y, const uint16_t* __restrict__ bias,
-                                                         int M, int N, int K, int KB, int kbw, const ProArgs pa) {
+// RG = 2 (MR = 4, 5..8 rows): two workgroups per tile, rows 0..3 and 4..7. Workgroups b and b + 8 take
+// the same tile: the hardware hands workgroups to the eight XCDs in turn, so both run on one XCD and
+// the second finds the tile's weights in that XCD's L2 (the grid covers whole groups of 8 tiles).
+template <class A, class W, int MR, int XW, int PRO = kProPlain, bool RES = false, bool RKV = false, int RG = 1>
+__global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args wa, const uint16_t* __restrict__ x_,
+                                                         uint16_t* __restrict__ y_, const uint16_t* __restrict__ bias,
+                                                         int M_, int N, int K, int KB, int kbw, const ProArgs pa_) {
   static_assert(has_sum_offset<W>::value && W::KBLK == 128 && W::STEPS == 4, "int4 tiles: 128-column blocks");
   static_assert(MR == 4 || MR == 8, "4 or 8 rows");
   static_assert(PRO == kProPlain || PRO == kProSiluGate || PRO == kProScaleSum, "plain rows, SiLU gate or row factor");
   static_assert(!(RES && RKV), "one epilogue");
+  static_assert(RG == 1 || (RG == 2 && MR == 4), "two groups of four rows");
   constexpr int KBLK = 128, U = 4, NG = kNgOf<W>, CPB = 4, CPG = CPB / NG, MPG = 4 / NG;
   constexpr int kJ = 16 * MR;  // epilogue threads: output j = (lane l = j / 4, element e = j % 4)
+  constexpr int RS = PRO == kProSiluGate ? 2 : 1;  // activation row stride in units of K
   extern __shared__ f32x4_t smem[];  // [NW][64] partial accumulators, then each wave's activation rows
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
-  const int t = blockIdx.x;
+  const int T = (N + 15) / 16;
+  const int b = static_cast<int>(blockIdx.x);
+  const int t = RG == 1 ? b : (((b >> 4) << 3) | (b & 7));
+  const int rb = RG == 1 ? 0 : 4 * ((b >> 3) & 1);  // first row of this workgroup
+  const int M = RG == 1 ? M_ : min(4, M_ - rb);
+  if (RG == 2 && (t >= T || M <= 0)) return;  // the whole workgroup: padding tiles, or rows 4..7 of M <= 4
+  const uint16_t* x = x_ + static_cast<int64_t>(rb) * RS * K;
+  uint16_t* y = y_ == nullptr ? nullptr : y_ + static_cast<int64_t>(rb) * N;
+  ProArgs pa = pa_;
+  if (RG == 2 && rb > 0) {  // this workgroup's rows of every row-major array
+    if (pa.res) pa.res += static_cast<int64_t>(rb) * N;
+    if (pa.res_out) pa.res_out += static_cast<int64_t>(rb) * N;
+    if (pa.hg_out) pa.hg_out += static_cast<int64_t>(rb) * N;
+    if (pa.ss_out) pa.ss_out += static_cast<int64_t>(rb) * T;
+    if (pa.ss_in) pa.ss_in += static_cast<int64_t>(rb) * pa.nss;
+    if (pa.lengths) pa.lengths += rb;
+    if (pa.q_out) pa.q_out += static_cast<int64_t>(rb) * pa.qn;
+    if (pa.k_cache) pa.k_cache += static_cast<int64_t>(rb) * pa.kn * pa.tmax;
+    if (pa.v_cache) pa.v_cache += static_cast<int64_t>(rb) * pa.kn * pa.tmax;
+  }
   const int kb0 = wave * kbw;
   const int kb1 = min(KB, kb0 + kbw);
   const int nl = lane & 15, jg = lane >> 4;
@@ -873,7 +897,6 @@ __global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args 
 
   // this wave's k-slice of every row (and of the up half for the SiLU gate), requested ahead of the
   // weights
-  constexpr int RS = PRO == kProSiluGate ? 2 : 1;  // row stride in units of K
   u32x4_t xw[MR][XW];
   [[maybe_unused]] u32x4_t gw[PRO == kProSiluGate ? MR : 1][XW];
 #pragma unroll
@@ -1081,7 +1104,7 @@ __global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args 
     hsq += __shfl_xor(hsq, 8, 64);
     hsq += __shfl_xor(hsq, 16, 64);
     hsq += __shfl_xor(hsq, 32, 64);
-    if (((jo >> 2) & 15) == 0 && mo < M) pa.ss_out[static_cast<int64_t>(mo) * gridDim.x + t] = hsq;
+    if (((jo >> 2) & 15) == 0 && mo < M) pa.ss_out[static_cast<int64_t>(mo) * T + t] = hsq;
   } else {
     if (own) {
       if (bias) v += A::to_f32(bias[no]);
@@ -1106,43 +1129,65 @@ inline size_t gemv_rows_lds_bytes(int64_t m, int nw, int kbw, bool scale_sum = f
          (scale_sum ? static_cast<size_t>(MR) * (kNormSumMax + 1) * 4 : 0);
 }
 
-// Whether the multi-row form takes m rows of a [rows, cols] weight with nw waves per tile (0: default);
-// scale_sum: the row factor's form.
-inline bool gemv_rows_fits(int64_t m, int64_t rows, int64_t cols, int nw = 0, bool scale_sum = false) {
-  if (m < 2 || m > 8 || rows <= 0 || cols <= 0) return false;
+// Row groups of the multi-row form for m rows (groups = 0: the library's choice): 1 (one workgroup per
+// tile, MR = 4 for m <= 4, MR = 8 above) or 2 (5..8 rows: two workgroups of four rows per tile).
+// Whether it takes m rows of a [rows, cols] weight with nw waves per tile (0: default); scale_sum: the
+// row factor's form. Returns the row groups it runs (0 when it does not fit).
+inline int gemv_rows_groups(int64_t m, int64_t rows, int64_t cols, int nw = 0, bool scale_sum = false, int groups = 0) {
+  if (m < 2 || m > 8 || rows <= 0 || cols <= 0 || groups < 0 || groups > 2) return 0;
   const int64_t KB = ceil_div(cols, 128);
   if (nw <= 0) nw = gemv_rows_default_waves(rows, cols);
-  if (nw > 16) return false;
+  if (nw > 16) return 0;
   if (nw > KB) nw = static_cast<int>(KB);
   const int kbw = static_cast<int>(ceil_div(KB, nw));
   nw = static_cast<int>(ceil_div(KB, kbw));
-  const int XW = m <= 4 ? 2 : 1;
-  // the epilogue's outputs of rows 4..7 are threads 64..127: two waves at least
-  return kbw <= 4 * XW && (m <= 4 || nw >= 2) && gemv_rows_lds_bytes(m, nw, kbw, scale_sum) <= 160 * 1024;
+  // four rows (or two groups of four): k-slices of up to 8 blocks
+  const bool four = kbw <= 8 && gemv_rows_lds_bytes(4, nw, kbw, scale_sum) <= 160 * 1024;
+  if (m <= 4) return (groups <= 1 && four) ? 1 : 0;
+  // eight rows in one workgroup: k-slices of up to 4 blocks, and two waves at least (the epilogue's
+  // outputs of rows 4..7 are threads 64..127)
+  const bool eight = kbw <= 4 && nw >= 2 && gemv_rows_lds_bytes(8, nw, kbw, scale_sum) <= 160 * 1024;
+  if (groups == 1) return eight ? 1 : 0;
+  if (groups == 2) return four ? 2 : 0;
+  // the library's choice. Two groups only on small grids: with rotating weights at 6 / 8 rows,
+  // 4096->1024 (64 tiles) 5.04 -> 4.41 us, but 4096->28672 17.3 / 18.1 -> 25.6 / 26.6 us, 14336->4096
+  // (where eight rows do not fit) 18.1 us against 15.6 us for the row-tiled kernel: the second
+  // workgroup of a tile does not find the weights in L2 often enough on larger grids.
+  if (four && ceil_div(rows, 16) <= 64) return 2;
+  return eight ? 1 : 0;
+}
+
+inline bool gemv_rows_fits(int64_t m, int64_t rows, int64_t cols, int nw = 0, bool scale_sum = false) {
+  return gemv_rows_groups(m, rows, cols, nw, scale_sum) != 0;
 }
 
 template <class A, class W, int PRO = kProPlain, bool RES = false, bool RKV = false>
 hipError_t gemv_rows_launch(const typename W::Args& wa, const uint16_t* x, uint16_t* y, const uint16_t* bias,
                             int64_t m, int64_t rows, int64_t cols, int waves, hipStream_t stream,
-                            const ProArgs& pa = ProArgs{nullptr, nullptr, nullptr, 0.0f}) {
-  if (!gemv_rows_fits(m, rows, cols, waves, PRO == kProScaleSum)) return hipErrorNotSupported;
+                            const ProArgs& pa = ProArgs{nullptr, nullptr, nullptr, 0.0f}, int groups = 0) {
+  const int rgs = gemv_rows_groups(m, rows, cols, waves, PRO == kProScaleSum, groups);
+  if (rgs == 0) return hipErrorNotSupported;
   const int64_t T = ceil_div(rows, 16);
   const int64_t KB = ceil_div(cols, 128);
   int nw = waves > 0 ? waves : gemv_rows_default_waves(rows, cols);
   if (nw > KB) nw = static_cast<int>(KB);
   const int kbw = static_cast<int>(ceil_div(KB, nw));
   nw = static_cast<int>(ceil_div(KB, kbw));
-  const size_t lds = gemv_rows_lds_bytes(m, nw, kbw);  // the row factor's sums are static LDS
-  const dim3 grid(static_cast<unsigned>(T)), block(static_cast<unsigned>(64 * nw));
+  const bool eight = m > 4 && rgs == 1;
+  const size_t lds = gemv_rows_lds_bytes(eight ? 8 : 4, nw, kbw);  // the row factor's sums are static LDS
+  const dim3 block(static_cast<unsigned>(64 * nw));
   const int M = static_cast<int>(m), N = static_cast<int>(rows), K = static_cast<int>(cols), iKB = static_cast<int>(KB);
   // columns at or past K (a k tail) read zero through the row resources, so the padded blocks need no
   // masking
-  if (m <= 4)
-    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 2, PRO, RES, RKV>), grid, block, lds, stream, wa, x, y, bias, M, N, K,
-                       iKB, kbw, pa);
+  if (rgs == 2)
+    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 2, PRO, RES, RKV, 2>), dim3(static_cast<unsigned>(ceil_div(T, 8) * 16)),
+                       block, lds, stream, wa, x, y, bias, M, N, K, iKB, kbw, pa);
+  else if (!eight)
+    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 2, PRO, RES, RKV>), dim3(static_cast<unsigned>(T)), block, lds, stream,
+                       wa, x, y, bias, M, N, K, iKB, kbw, pa);
   else
-    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 8, 1, PRO, RES, RKV>), grid, block, lds, stream, wa, x, y, bias, M, N, K,
-                       iKB, kbw, pa);
+    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 8, 1, PRO, RES, RKV>), dim3(static_cast<unsigned>(T)), block, lds, stream,
+                       wa, x, y, bias, M, N, K, iKB, kbw, pa);
   return hipGetLastError();
 }
 

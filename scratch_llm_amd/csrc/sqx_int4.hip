@@ -610,12 +610,12 @@ static hipError_t launch_int4_skinny(int group, const uint8_t* wt, const void* s
 template <class A, bool ASYM, bool PBF16>
 static hipError_t launch_int4_rows(int group, const uint8_t* wt, const void* st, const void* zt, const uint16_t* x,
                                    uint16_t* y, const uint16_t* bias, int64_t m, int64_t rows, int64_t cols, int waves,
-                                   hipStream_t s) {
+                                   int groups, hipStream_t s) {
 #define SQX_ROWG(G_)                                                                        \
   {                                                                                         \
     using W = WInt4<G_, ASYM, PBF16>;                                                       \
     const typename W::Args a{wt, st, zt};                                                   \
-    return gemv_rows_launch<A, W>(a, x, y, bias, m, rows, cols, waves, s);                  \
+    return gemv_rows_launch<A, W>(a, x, y, bias, m, rows, cols, waves, s, ProArgs{}, groups); \
   }
   if (group == 128) SQX_ROWG(128)
   if (group == 64) SQX_ROWG(64)
@@ -1050,12 +1050,13 @@ static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, i
   SQX_REQUIRE(sh.S >= 1 &&
                   ((sh.variant == 0 && (sh.R == 2 || sh.R == 4) && sh.waves >= 1 && sh.waves <= kSkinnyMaxWaves) ||
                    (sh.variant == 1 && (sh.R == 1 || sh.R == 2 || sh.R == 4) && (sh.waves == 4 || sh.waves == 8)) ||
-                   (sh.variant == 2 && sh.S == 1 && sh.waves >= 0 && sh.waves <= 16)),
+                   (sh.variant == 2 && sh.S == 1 && sh.R >= 0 && sh.R <= 2 && sh.waves >= 0 && sh.waves <= 16)),
               SQX_E_ARG, "%s: bad launch shape (variant %d, tiles %d, waves %d, splits %d)", fn, sh.variant, sh.R,
               sh.waves, sh.S);
-  SQX_REQUIRE(sh.variant != 2 || m == 0 || gemv_rows_fits(m, rows, cols, sh.waves), SQX_E_ARG,
-              "%s: the multi-row GEMV (variant 2) takes 2..8 rows with k-slices of at most %d blocks (m=%lld, "
-              "cols=%lld, waves %d)", fn, m <= 4 ? 8 : 4, (long long)m, (long long)cols, sh.waves);
+  SQX_REQUIRE(sh.variant != 2 || m == 0 || gemv_rows_groups(m, rows, cols, sh.waves, false, sh.R) != 0, SQX_E_ARG,
+              "%s: the multi-row GEMV (variant 2) takes 2..8 rows with k-slices of at most 8 blocks (4 for 5..8 rows "
+              "in one workgroup, tiles 1) (m=%lld, cols=%lld, waves %d, tiles %d)", fn, (long long)m, (long long)cols,
+              sh.waves, sh.R);
   if (m == 0) return SQX_OK;
   SQX_REQUIRE(wt && st && x && (y || !reduce), SQX_E_ARG, "%s: null pointer", fn);
   SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, SQX_E_ARG,
@@ -1078,7 +1079,8 @@ static int int4_skinny_impl(const uint8_t* wt, const void* st, const void* zt, i
   hipError_t e;
   if (sh.variant == 2) {
     SQX_REQUIRE(reduce, SQX_E_ARG, "%s: the multi-row GEMV leaves no partials", fn);
-#define SQX_ROWL(ACT, ASYM, PBF) e = launch_int4_rows<ACT, ASYM, PBF>(g, wt, st, zt, xp, yp, b16, m, rows, cols, sh.waves, s)
+#define SQX_ROWL(ACT, ASYM, PBF) \
+  e = launch_int4_rows<ACT, ASYM, PBF>(g, wt, st, zt, xp, yp, b16, m, rows, cols, sh.waves, sh.R, s)
     if (act_dtype == SQX_DTYPE_BF16) {
       if (asym) { if (pbf) SQX_ROWL(ActBF16, true, true); else SQX_ROWL(ActBF16, true, false); }
       else { if (pbf) SQX_ROWL(ActBF16, false, true); else SQX_ROWL(ActBF16, false, false); }
@@ -1142,7 +1144,7 @@ extern "C" int sqx_int4_skinny(const uint8_t* wt, const void* st, const void* zt
                             sqx_int4_linear_default_kslices(m, rows, cols), stream, "sqx_int4_skinny");
   if (variant >= 0 && (variant != sh.variant || sh.gemv))  // the variant's own defaults
     sh = variant == 0 ? SkinnyShape{0, 2, 8, 1, false}
-                      : (variant == 2 ? SkinnyShape{2, 1, 0, 1, false} : SkinnyShape{1, 2, 4, 1, false});
+                      : (variant == 2 ? SkinnyShape{2, 0, 0, 1, false} : SkinnyShape{1, 2, 4, 1, false});
   if (variant > 2) sh.variant = variant;  // refused below
   if (tiles > 0) sh.R = tiles;
   if (waves > 0) sh.waves = waves;

@@ -562,7 +562,7 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
 //                 to about 192 workgroups.
 struct SkinnyShape {
   int variant;  // 0: waves splitting K (skinny_kernel); 1: LDS-staged (skinny_lds_kernel); 2: gemv_rows_kernel
-  int R;        // row tiles per wave: 1, 2 or 4 (the K-split variant: 2 or 4)
+  int R;        // row tiles per wave: 1, 2 or 4 (the K-split variant: 2 or 4); variant 2: row groups (0 = default)
   int waves;    // K-split: 1..8 waves per workgroup; LDS-staged: 4 or 8 compute waves (1 or 2 k-groups)
   int S;        // workgroups along K (S > 1 needs a workspace of S*m*rows fp32)
   bool gemv;    // the decode GEMV is the better kernel for this shape
@@ -587,7 +587,7 @@ inline SkinnyShape skinny_default_shape(int64_t m, int64_t rows, int64_t cols, i
     // 3.94 / 4.14 / 5.12 us, 14336->4096 13.64 / 12.05 -> 10.29 / 10.45 us (M = 2 / 4), 4096->6144
     // 6.69 / 6.78 / 6.89 -> 5.41 / 5.81 / 6.74 us; 4096->14336 (896 tiles) 9.79 -> 9.33 us at M = 2 only,
     // 4096->28672 15.66 -> 15.13 us at M = 2 only
-    s = SkinnyShape{2, 1, 0, 1, false};
+    s = SkinnyShape{2, 0, 0, 1, false};
   } else if (m <= 16) {
     if (T >= 4096) s = SkinnyShape{1, 4, 4, 1, false};
     else if (T >= 1024) s = SkinnyShape{0, 4, 4, 1, false};

@@ -674,11 +674,12 @@ def test_residual_forms_refuse(lib):
     assert lib.sqx_int4_linear_residual(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
                                         ss.data_ptr(), None, None, 9, 64, 4096, 128, 0, _s()) == -1
     assert "2..8 rows" in lib.sqx_last_error().decode()
-    tw14 = _tiled(64, 14336, 128, seed=4)  # 112 k-blocks: k-slices of 7 blocks, more than 5 rows take
-    x14 = torch.zeros(5, 14336, dtype=torch.bfloat16, device=DEV)
-    assert lib.sqx_int4_rows_fits(5, 64, 14336, 0) == 0 and lib.sqx_int4_rows_fits(4, 64, 14336, 0) == 1
-    assert lib.sqx_int4_linear_residual(tw14.wt.data_ptr(), tw14.st.data_ptr(), x14.data_ptr(), x.data_ptr(),
-                                        x.data_ptr(), ss.data_ptr(), None, None, 5, 64, 14336, 128, 0, _s()) == -1
+    # 160 k-blocks: k-slices of 10 blocks over 16 waves, more than the multi-row form takes
+    tw20 = _tiled(64, 20480, 128, seed=4)
+    x20 = torch.zeros(5, 20480, dtype=torch.bfloat16, device=DEV)
+    assert lib.sqx_int4_rows_fits(5, 64, 20480, 0) == 0 and lib.sqx_int4_rows_fits(5, 64, 14336, 0) == 1
+    assert lib.sqx_int4_linear_residual(tw20.wt.data_ptr(), tw20.st.data_ptr(), x20.data_ptr(), x.data_ptr(),
+                                        x.data_ptr(), ss.data_ptr(), None, None, 5, 64, 20480, 128, 0, _s()) == -1
     assert "multi-row form" in lib.sqx_last_error().decode()
     assert lib.sqx_int4_linear_residual(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
                                         ss.data_ptr(), x.data_ptr(), None, 1, 64, 4096, 128, 0, _s()) == -1

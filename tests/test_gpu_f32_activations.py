@@ -95,15 +95,27 @@ def test_awq_linear_fp32_x(mods, m):
     _check_f32(y, x.cpu().numpy(), aw.awq_dequantize(quant).cpu().numpy(), None, f"awq fp32 M={m}")
 
 
-def test_unsupported_group_and_dtype_raise(mods):
+def test_wide_groups_and_unsupported_group_and_dtype(mods):
+    """A group of 256 runs as two 128-column groups with the scale repeated: bit for bit the linear of
+    the repeated scales, fp32 activations included; a group that is not a multiple of 32 raises, and
+    so does a float64 activation."""
     i4, aw = mods
     w = torch.randn(16, 512, device=DEV) * 0.02
+    x = torch.randn(3, 512, device=DEV)
     q, s = i4.quantize_groupwise_int4(w, 256)
-    with pytest.raises(ValueError, match="group_size=256"):
-        i4.w4a16_linear(torch.randn(1, 512, device=DEV), q, s, group_size=256)
+    y = i4.w4a16_linear(x, q, s, group_size=256)
+    assert torch.equal(y, i4.w4a16_linear(x, q, s.repeat_interleave(2, dim=1).contiguous(), group_size=128))
+    q48, s48 = i4.quantize_groupwise_int4(w[:, :480], 48)
+    with pytest.raises(ValueError, match="group_size=48"):
+        i4.w4a16_linear(x[:, :480], q48, s48, group_size=48)
     q, s = i4.quantize_groupwise_int4(w)
     with pytest.raises(TypeError):
         i4.w4a16_linear(torch.randn(1, 512, device=DEV, dtype=torch.float64), q, s)
     quant = aw.quantize_awq_int4(w, chan_scale=torch.ones(512, device=DEV), group_size=256)
-    with pytest.raises(ValueError, match="group_size=256"):
-        aw.awq_linear(torch.randn(1, 512, device=DEV), quant)
+    ya = aw.awq_linear(x, quant)
+    q2 = aw.AWQQuant(q=quant.q, group_scales=quant.group_scales.repeat_interleave(2, dim=1).contiguous(),
+                     chan_scale=quant.chan_scale, group_size=128)
+    assert torch.equal(ya, aw.awq_linear(x, q2))
+    quant48 = aw.quantize_awq_int4(w[:, :480], chan_scale=torch.ones(480, device=DEV), group_size=48)
+    with pytest.raises(ValueError, match="group_size=48"):
+        aw.awq_linear(x[:, :480], quant48)

@@ -84,24 +84,29 @@ def test_skinny_llama_shapes_default(q4, n, k, m):
 
 
 @pytest.mark.parametrize(
-    "n,k,group,m,waves",
+    "n,k,group,m,waves,groups",
     [
-        (4096, 4096, 128, 2, 0), (4096, 4096, 128, 4, 0), (4096, 4096, 128, 8, 0), (4096, 4096, 128, 3, 4),
-        (1024, 4096, 128, 5, 8), (6144, 4096, 128, 7, 16), (4096, 14336, 128, 4, 0), (4096, 14336, 128, 2, 16),
-        (1000, 1056, 32, 6, 0),  # rows not a multiple of 16, a K tail with four groups per block
-        (200, 96, 32, 3, 0),  # columns not a multiple of 128, one block
-        (48, 2048, 64, 8, 4), (300, 4096, 32, 4, 4),
+        (4096, 4096, 128, 2, 0, 0), (4096, 4096, 128, 4, 0, 0), (4096, 4096, 128, 8, 0, 1), (4096, 4096, 128, 8, 0, 2),
+        (4096, 4096, 128, 3, 4, 0), (1024, 4096, 128, 5, 8, 1), (1024, 4096, 128, 5, 8, 2), (6144, 4096, 128, 7, 16, 0),
+        (4096, 14336, 128, 4, 0, 0), (4096, 14336, 128, 2, 16, 0), (4096, 14336, 128, 8, 0, 2),
+        (4096, 14336, 128, 6, 16, 2),
+        (1000, 1056, 32, 6, 0, 1), (1000, 1056, 32, 6, 0, 2),  # rows not a multiple of 16, a K tail, four groups a block
+        (200, 96, 32, 3, 0, 0),  # columns not a multiple of 128, one block
+        (200, 2048, 64, 7, 0, 2),  # 13 tiles: the two-group grid covers 16
+        (48, 2048, 64, 8, 4, 1), (300, 4096, 32, 4, 4, 0),
     ],
 )
-def test_rows_gemv_matches_oracle(q4, n, k, group, m, waves):
-    """The multi-row GEMV (variant 2): 2..8 rows, the per-row activation sums charging the code offset."""
-    print_case("rows gemv", n, k, group, m, waves)
+def test_rows_gemv_matches_oracle(q4, n, k, group, m, waves, groups):
+    """The multi-row GEMV (variant 2): 2..8 rows, the per-row activation sums charging the code offset;
+    5..8 rows in one workgroup (groups 1) or as two workgroups of four rows per tile (groups 2)."""
+    print_case("rows gemv", n, k, group, m, waves, groups)
     tw, w_eff = _sym(q4, n, k, group, 5 * n + k + m)
     x = _act(m, k, 7 * m + k).to(DEV)
-    y = q4.int4_linear_skinny(x, tw, variant=2, waves=waves)
+    y = q4.int4_linear_skinny(x, tw, variant=2, waves=waves, tiles=groups)
     torch.cuda.synchronize()
-    _check_linear(y, R.linear_f64(x.float().cpu().numpy(), w_eff), f"rows {k}->{n} g{group} M={m} waves={waves}")
-    assert torch.equal(y, q4.int4_linear_skinny(x, tw, variant=2, waves=waves))  # fixed-order sums
+    _check_linear(y, R.linear_f64(x.float().cpu().numpy(), w_eff),
+                  f"rows {k}->{n} g{group} M={m} waves={waves} groups={groups}")
+    assert torch.equal(y, q4.int4_linear_skinny(x, tw, variant=2, waves=waves, tiles=groups))  # fixed-order sums
     # each row alone through the one-row GEMV agrees to bf16 precision
     for r in (0, m - 1):
         y1 = q4.int4_linear_tiled(x[r:r + 1], tw)
@@ -186,6 +191,7 @@ def test_skinny_rejects(q4):
     assert lib.sqx_int4_skinny(*args, 1, 2, 6, 1, None, 0, st) == E_ARG  # LDS-staged: 4 or 8 compute waves
     assert lib.sqx_int4_skinny(*args, 3, 2, 4, 1, None, 0, st) == E_ARG  # no variant 3
     assert lib.sqx_int4_skinny(*args, 2, 0, 17, 1, None, 0, st) == E_ARG  # multi-row GEMV: at most 16 waves
+    assert lib.sqx_int4_skinny(*args, 2, 3, 0, 1, None, 0, st) == E_ARG  # multi-row GEMV: 1 or 2 row groups
     assert lib.sqx_int4_skinny(*args, 2, 0, 0, 2, None, 0, st) == E_ARG  # multi-row GEMV: no K split
     assert lib.sqx_int4_skinny(*args, 0, 2, 1, 2, None, 0, st) == E_ARG  # splits need a workspace
     assert "workspace" in lib.sqx_last_error().decode()
