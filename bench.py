@@ -104,10 +104,13 @@ def main() -> int:
     ap.add_argument("--kslices", type=int, default=0, help="waves per 16-row tile (0 = library default)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM measurements")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode-step measurement")
-    ap.add_argument("--decode-batches", default="1,8,32,64", help="batch sizes of the decode-step measurement")
+    ap.add_argument("--decode-batches", default="1,2,8,32,64", help="batch sizes of the decode-step measurement")
     ap.add_argument("--decode-fp8kv-batches", default="32,64", help="batch sizes also timed with the FP8 KV cache")
     ap.add_argument("--no-fp8", action="store_true", help="skip the FP8 W8A8 linear measurement")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config cases of BASELINE configs 1-4")
+    ap.add_argument("--config-ids", default="1,2,3,4", help="which of BASELINE configs 1-4 the per-config cases run")
+    ap.add_argument("--rotate-gb", type=float, default=1.1,
+                    help="bytes of rotating weight copies per per-config case (2 copies at least; 0 for counter runs)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -327,7 +330,7 @@ def main() -> int:
 
     configs = None
     if not args.no_configs:
-        configs = baseline_configs(dev)
+        configs = baseline_configs(dev, [int(c) for c in args.config_ids.split(",") if c], args.rotate_gb)
         log("configs:", json.dumps(configs))
 
     decode = None
@@ -771,7 +774,7 @@ def prefill_gemms(dev) -> dict:
     return res
 
 
-def baseline_configs(dev) -> dict:
+def baseline_configs(dev, ids=(1, 2, 3, 4), rotate_gb: float = 1.1) -> dict:
     """Every case of BASELINE.json's configs 1-4 on one GPU (config 5 is ``decode``; config 4 at M = 4096
     and config 3's M = 2048 on 4096->14336 are also in ``prefill``). Every case is a captured graph of
     back-to-back calls, each on the next of >= 1.1 GB of rotating weight copies (more than four times
@@ -791,7 +794,7 @@ def baseline_configs(dev) -> dict:
            "config4_mxfp4": {}}
 
     def rotating(n, k, make, per_weight_bytes):
-        copies = max(2, min(1024, -(-int(1.1e9) // per_weight_bytes)))
+        copies = max(2, min(1024, -(-int(rotate_gb * 1e9) // per_weight_bytes)))
         return [make(torch.randn(n, k, generator=g, device=dev) * 0.02) for _ in range(copies)]
 
     def gbs_entry(us, byts):
@@ -799,109 +802,113 @@ def baseline_configs(dev) -> dict:
                 "frac_of_hbm_peak": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
 
     # config 1: int8 weight-only 4096x4096, per-output-channel symmetric, M in {1, 16}
-    n = k = 4096
-    tws = rotating(n, k, lambda w: q8.tile_int8(*q8.quantize_symmetric(w, axis=0)), n * k)
-    for m in (1, 16):
-        x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
-        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-
-        def run(stream):
-            for tw in tws:
-                lib.sqx_int8_linear(tw.wt.data_ptr(), tw.scale.data_ptr(), x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(),
-                                    None, m, n, k, 0, stream)
-            return len(tws)
-
-        res["config1_int8_weight_only"][f"{k}->{n} M={m}"] = gbs_entry(_graph_us(run), n * k + 4 * n + 2 * m * k + 2 * m * n)
-    del tws
-    torch.cuda.empty_cache()
-
-    # config 2: int4 g128 asymmetric (uint4 codes, bf16 scale and zero per group), M in {1, 4, 8}
-    for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
-        def make(w):
-            q, s_, z = i4.quantize_groupwise_uint4_asym(w, 128, torch.bfloat16)
-            return i4.tile_int4(q, s_, z, 128)
-
-        tws = rotating(n, k, make, n * k // 2)
-        for m in (1, 4, 8):
+    if 1 in ids:
+        n = k = 4096
+        tws = rotating(n, k, lambda w: q8.tile_int8(*q8.quantize_symmetric(w, axis=0)), n * k)
+        for m in (1, 16):
             x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
             y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-            # what w4a16_linear runs (int4_linear_tiled): the GEMV at one row, the library's choice
-            # among the GEMV and the row-tiled kernels (K split into a workspace) for 2..64 rows
-            nb = int(lib.sqx_int4_skinny_workspace_bytes(m, n, k, 0))
-            ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
 
             def run(stream):
                 for tw in tws:
-                    if m == 1:
-                        lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), tw.zt.data_ptr(), _lib.DTYPE_BF16,
-                                            x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(), None, m, n, k, 128, 0, stream)
-                    else:
-                        lib.sqx_int4_skinny(tw.wt.data_ptr(), tw.st.data_ptr(), tw.zt.data_ptr(), _lib.DTYPE_BF16,
-                                            x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(), None, m, n, k, 128, -1, 0, 0,
-                                            0, ws.data_ptr() if nb > 0 else None, nb, stream)
+                    lib.sqx_int8_linear(tw.wt.data_ptr(), tw.scale.data_ptr(), x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(),
+                                        None, m, n, k, 0, stream)
                 return len(tws)
 
-            byts = n * k // 2 + 2 * 2 * n * k // 128 + 2 * m * k + 2 * m * n
-            res["config2_int4_g128_asym"][f"{k}->{n} M={m}"] = gbs_entry(_graph_us(run), byts)
+            res["config1_int8_weight_only"][f"{k}->{n} M={m}"] = gbs_entry(_graph_us(run), n * k + 4 * n + 2 * m * k + 2 * m * n)
         del tws
         torch.cuda.empty_cache()
+
+    # config 2: int4 g128 asymmetric (uint4 codes, bf16 scale and zero per group), M in {1, 4, 8}
+    if 2 in ids:
+        for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
+            def make(w):
+                q, s_, z = i4.quantize_groupwise_uint4_asym(w, 128, torch.bfloat16)
+                return i4.tile_int4(q, s_, z, 128)
+
+            tws = rotating(n, k, make, n * k // 2)
+            for m in (1, 4, 8):
+                x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+                y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+                # what w4a16_linear runs (int4_linear_tiled): the GEMV at one row, the library's choice
+                # among the GEMV and the row-tiled kernels (K split into a workspace) for 2..64 rows
+                nb = int(lib.sqx_int4_skinny_workspace_bytes(m, n, k, 0))
+                ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
+
+                def run(stream):
+                    for tw in tws:
+                        if m == 1:
+                            lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), tw.zt.data_ptr(), _lib.DTYPE_BF16,
+                                                x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(), None, m, n, k, 128, 0, stream)
+                        else:
+                            lib.sqx_int4_skinny(tw.wt.data_ptr(), tw.st.data_ptr(), tw.zt.data_ptr(), _lib.DTYPE_BF16,
+                                                x.data_ptr(), _lib.DTYPE_BF16, y.data_ptr(), None, m, n, k, 128, -1, 0, 0,
+                                                0, ws.data_ptr() if nb > 0 else None, nb, stream)
+                    return len(tws)
+
+                byts = n * k // 2 + 2 * 2 * n * k // 128 + 2 * m * k + 2 * m * n
+                res["config2_int4_g128_asym"][f"{k}->{n} M={m}"] = gbs_entry(_graph_us(run), byts)
+            del tws
+            torch.cuda.empty_cache()
 
     # config 3: AWQ int4 g128 prefill GEMM, M in {64, 512, 2048}
-    for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
-        sc = torch.exp(torch.empty(k, device=dev).uniform_(-0.6931, 0.6931, generator=g))
-        quants = rotating(n, k, lambda w: awq.quantize_awq_int4(w, chan_scale=sc), n * k // 2 + n * k // 32)
-        for m in (64, 512, 2048):
-            x = torch.randn(m, k, generator=g, device=dev)
-            x[:, torch.randperm(k, generator=torch.Generator().manual_seed(k))[: k // 100].to(dev)] *= 20.0
-            x = x.to(torch.bfloat16)
-            us = _graph_call_us([lambda q=q: awq.awq_linear(x, q) for q in quants])
-            fl = 2.0 * m * n * k
-            res["config3_awq_int4_g128"][f"{k}->{n} M={m}"] = {
-                "us": round(us, 1), "tflops": round(fl / us / 1e6, 1),
-                "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4),
-                "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1), "rotating_copies": len(quants)}
-        del quants
-        torch.cuda.empty_cache()
+    if 3 in ids:
+        for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
+            sc = torch.exp(torch.empty(k, device=dev).uniform_(-0.6931, 0.6931, generator=g))
+            quants = rotating(n, k, lambda w: awq.quantize_awq_int4(w, chan_scale=sc), n * k // 2 + n * k // 32)
+            for m in (64, 512, 2048):
+                x = torch.randn(m, k, generator=g, device=dev)
+                x[:, torch.randperm(k, generator=torch.Generator().manual_seed(k))[: k // 100].to(dev)] *= 20.0
+                x = x.to(torch.bfloat16)
+                us = _graph_call_us([lambda q=q: awq.awq_linear(x, q) for q in quants])
+                fl = 2.0 * m * n * k
+                res["config3_awq_int4_g128"][f"{k}->{n} M={m}"] = {
+                    "us": round(us, 1), "tflops": round(fl / us / 1e6, 1),
+                    "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4),
+                    "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1), "rotating_copies": len(quants)}
+            del quants
+            torch.cuda.empty_cache()
 
     # config 4: MXFP4 weights (e2m1 + e8m0 per 32 along K), bf16 or MXFP4 activations, M in {1, 128}
-    for n, k in ((28672, 8192), (8192, 28672)):
-        tws = rotating(n, k, lambda w: f4.tile_fp4(f4.mxfp4_quantize(w, 32)), n * k // 2)
-        x1 = torch.randn(1, k, generator=g, device=dev).to(torch.bfloat16)
-        y1 = torch.empty(1, n, dtype=torch.bfloat16, device=dev)
+    if 4 in ids:
+        for n, k in ((28672, 8192), (8192, 28672)):
+            tws = rotating(n, k, lambda w: f4.tile_fp4(f4.mxfp4_quantize(w, 32)), n * k // 2)
+            x1 = torch.randn(1, k, generator=g, device=dev).to(torch.bfloat16)
+            y1 = torch.empty(1, n, dtype=torch.bfloat16, device=dev)
 
-        def run(stream):
-            for tw in tws:
-                lib.sqx_fp4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), tw.fmt, _lib.ptr(tw.s_global), x1.data_ptr(),
-                                   _lib.DTYPE_BF16, y1.data_ptr(), _lib.DTYPE_BF16, None, 1, n, k, 0, stream)
-            return len(tws)
+            def run(stream):
+                for tw in tws:
+                    lib.sqx_fp4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), tw.fmt, _lib.ptr(tw.s_global), x1.data_ptr(),
+                                       _lib.DTYPE_BF16, y1.data_ptr(), _lib.DTYPE_BF16, None, 1, n, k, 0, stream)
+                return len(tws)
 
-        byts = n * k // 2 + n * k // 32 + 2 * k + 2 * n
-        res["config4_mxfp4"][f"bf16_x {k}->{n} M=1"] = gbs_entry(_graph_us(run), byts)
-        # MXFP4 activations at M = 1: what mxfp4_linear(quantize_activations=True) runs (the row's
-        # quantize-dequantize, then the weight GEMV), and the fp4 MFMA GEMM on the same row
-        us = _graph_call_us([lambda tw=tw: f4.fp4_linear_tiled(f4.mxfp4_fake_quant_rows(x1), tw) for tw in tws])
-        e = gbs_entry(us, byts)
-        e["path"] = "mxfp4_fake_quant_rows + FP4 GEMV (two launches)"
-        res["config4_mxfp4"][f"mxfp4_x {k}->{n} M=1"] = e
-        xq1 = f4.mxfp4_quantize_tiled(x1)
-        e = gbs_entry(_graph_call_us([lambda tw=tw: f4.mxfp4_gemm(xq1, tw) for tw in tws]), byts)
-        e["path"] = "fp4 MFMA GEMM (activations quantized beforehand)"
-        res["config4_mxfp4"][f"mxfp4_x {k}->{n} M=1 GEMM"] = e
-        m = 128
-        x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
-        fl = 2.0 * m * n * k
-        us = _graph_call_us([lambda tw=tw: f4.fp4_linear_tiled(x, tw) for tw in tws])
-        res["config4_mxfp4"][f"bf16_x {k}->{n} M={m}"] = {
-            "us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4),
-            "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1), "rotating_copies": len(tws)}
-        xq = f4.mxfp4_quantize_tiled(x)
-        us = _graph_call_us([lambda tw=tw: f4.mxfp4_gemm(xq, tw) for tw in tws])
-        res["config4_mxfp4"][f"mxfp4_x {k}->{n} M={m}"] = {
-            "us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "frac_of_fp4_peak": round(fl / us * 1e6 / FP4_PEAK, 4),
-            "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1), "rotating_copies": len(tws),
-            "quantize_x_us": round(_graph_call_us(lambda: f4.mxfp4_quantize_tiled(x)), 1)}
-        del tws
-        torch.cuda.empty_cache()
+            byts = n * k // 2 + n * k // 32 + 2 * k + 2 * n
+            res["config4_mxfp4"][f"bf16_x {k}->{n} M=1"] = gbs_entry(_graph_us(run), byts)
+            # MXFP4 activations at M = 1: what mxfp4_linear(quantize_activations=True) runs (the row's
+            # quantize-dequantize, then the weight GEMV), and the fp4 MFMA GEMM on the same row
+            us = _graph_call_us([lambda tw=tw: f4.fp4_linear_tiled(f4.mxfp4_fake_quant_rows(x1), tw) for tw in tws])
+            e = gbs_entry(us, byts)
+            e["path"] = "mxfp4_fake_quant_rows + FP4 GEMV (two launches)"
+            res["config4_mxfp4"][f"mxfp4_x {k}->{n} M=1"] = e
+            xq1 = f4.mxfp4_quantize_tiled(x1)
+            e = gbs_entry(_graph_call_us([lambda tw=tw: f4.mxfp4_gemm(xq1, tw) for tw in tws]), byts)
+            e["path"] = "fp4 MFMA GEMM (activations quantized beforehand)"
+            res["config4_mxfp4"][f"mxfp4_x {k}->{n} M=1 GEMM"] = e
+            m = 128
+            x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+            fl = 2.0 * m * n * k
+            us = _graph_call_us([lambda tw=tw: f4.fp4_linear_tiled(x, tw) for tw in tws])
+            res["config4_mxfp4"][f"bf16_x {k}->{n} M={m}"] = {
+                "us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "frac_of_bf16_peak": round(fl / us * 1e6 / BF16_PEAK, 4),
+                "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1), "rotating_copies": len(tws)}
+            xq = f4.mxfp4_quantize_tiled(x)
+            us = _graph_call_us([lambda tw=tw: f4.mxfp4_gemm(xq, tw) for tw in tws])
+            res["config4_mxfp4"][f"mxfp4_x {k}->{n} M={m}"] = {
+                "us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "frac_of_fp4_peak": round(fl / us * 1e6 / FP4_PEAK, 4),
+                "weight_gbs": round((n * k // 2 + n * k // 32) / us / 1e3, 1), "rotating_copies": len(tws),
+                "quantize_x_us": round(_graph_call_us(lambda: f4.mxfp4_quantize_tiled(x)), 1)}
+            del tws
+            torch.cuda.empty_cache()
     return res
 
 
