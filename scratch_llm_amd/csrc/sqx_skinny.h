@@ -48,6 +48,24 @@ struct plain_blocks<W, std::void_t<decltype(W::kPlainBlocks)>> : std::integral_c
 #endif
 template <int R>
 constexpr int skinny_ring() { return SQX_SKINNY_RING_KIB / R > 1 ? SQX_SKINNY_RING_KIB / R : 1; }
+// LDS stages of activations in the LDS-staged variant. A wave's loads complete in issue order, so
+// the wait for the copy of block s also waits for every weight load issued before it: with the
+// copy issued NS-1 steps ahead, a step can take no less than the loaded memory latency / NS. More
+// stages (up to the ring depth, within 160 KiB per workgroup) keep more weight bytes in flight.
+// (The count of loads a wait may leave outstanding, (NS-1) x R x LOADS + (NS-2) x MCH, stays below
+// vmcnt's 64.)
+constexpr int kSkinnyLdsBytes = 160 * 1024;
+#ifndef SQX_SKINNY_MAX_STAGES
+#define SQX_SKINNY_MAX_STAGES 4
+#endif
+template <int MCH, int R, int D, int KG, int LOADS>
+constexpr int skinny_stages() {
+  const int fit = kSkinnyLdsBytes / (KG * MCH * 16 * 256);
+  int ns = fit < D ? fit : D;
+  ns = ns < 3 ? 3 : (ns > SQX_SKINNY_MAX_STAGES ? SQX_SKINNY_MAX_STAGES : ns);
+  while (ns > 3 && (ns - 1) * R * LOADS + (ns - 2) * MCH >= 64) --ns;
+  return ns;
+}
 
 // Waves per workgroup a variant may use: variants that need more than the 256 registers a wave
 // gets at two waves per SIMD (4 chunks x 4 tiles; 8 chunk-tiles with several groups per block or
@@ -253,11 +271,12 @@ __global__ __launch_bounds__((64 * skinny_max_waves(MCH, R, W::NG, W::kConstOffs
 //    q) holds chunk q ^ (r & 15) of the row, so the 16 rows a fragment read touches fall in 16
 //    different bank groups. Rows at or beyond M and columns at or beyond K are copied as zeros.
 //  * Every wave keeps the weights of the next D k-blocks in flight in a register ring.
-//  * Every step issues the same loads in the same order (copy of block s+2, then the ring refill of
-//    block s+D; past the k-group's last block, zero-size buffer resources and out-of-range offsets
-//    keep the count without touching memory), so at step s the copy of block s is complete once at
-//    most 2 x (ring loads) + MCH loads are outstanding. After that wait the barrier B_s tells every
-//    wave that block s is in LDS and that the slot of block s-1 may be refilled.
+//  * Every step issues the same loads in the same order (copy of block s+A with A = NS-1, then the
+//    ring refill of block s+D; past the k-group's last block, zero-size buffer resources and
+//    out-of-range offsets keep the count without touching memory), so at step s the copy of block s
+//    is complete once at most A x (ring loads) + (A-1) x MCH loads are outstanding. After that wait
+//    the barrier B_s tells every wave that block s is in LDS and that the slot of block s-1 may be
+//    refilled.
 template <class A, class W, int MCH, int R, int D, int KG>
 __global__ __launch_bounds__(256 * KG) void skinny_lds_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
                                                               void* __restrict__ out, const uint16_t* __restrict__ bias,
@@ -269,8 +288,10 @@ __global__ __launch_bounds__(256 * KG) void skinny_lds_kernel(const typename W::
   constexpr int STEPS = W::STEPS;
   constexpr int NG = W::NG;
   constexpr int kStage = MCH * 16 * 256;
-  constexpr int NS = 3;
-  constexpr int kWaitN = 2 * R * W::kLoads + MCH;  // loads issued after a block's copy by its step
+  constexpr int NS = skinny_stages<MCH, R, D, KG, W::kLoads>();
+  constexpr int AH = NS - 1;  // steps a copy is issued ahead of its use
+  static_assert(AH <= D, "the prologue issues the first copies among the first ring loads");
+  constexpr int kWaitN = AH * R * W::kLoads + (AH - 1) * MCH;  // loads issued after a block's copy by its step
   static_assert(kWaitN < 64, "vmcnt is 6 bits");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_skinny[];
   const int lane = threadIdx.x & 63;
@@ -282,29 +303,45 @@ __global__ __launch_bounds__(256 * KG) void skinny_lds_kernel(const typename W::
   const int nh = (n + KG - 1) / KG;        // steps every wave walks
   const int k0 = ks0 + kg * nh;            // the k-group's first block
   const int nk = max(0, min(nh, n - kg * nh));  // its real blocks; later steps load zeros
-  // Step s reads block k0 + (s + rot) mod nk. Workgroups resident together start at different
-  // blocks: their tiles are KB KiB apart, so in lockstep they would read addresses equal modulo that
-  // stride and crowd the same HBM channels.
-  const int rot = nk > 0 ? static_cast<int>(blockIdx.x % static_cast<unsigned>(nk)) : 0;
-  auto kb_of = [&](int s) {
-    int j = s + rot;
-    if (j >= nk) j -= nk;
-    return k0 + j;
-  };
+  // Step s reads block k0 + s: every workgroup walks its tiles from the k-group's first block (a
+  // start rotated per workgroup measured about 10 % slower).
+  auto kb_of = [&](int s) { return k0 + s; };
   uint8_t* ring = smem_skinny + kg * NS * kStage;
   const rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
+  const rsrc_t xnull = make_rsrc(x, 0u);  // zero-size: copies of steps past the range write zeros
+  // Per-lane offsets of the copies within a k-block, fixed for the whole walk (the block's column
+  // offset goes in the scalar offset). Rows at or beyond M copy row M-1: they only feed output rows
+  // that are never stored. Keeping the per-step copies free of vector arithmetic matters: a
+  // temporary there takes a register of the weight ring, and the compiler then drains every
+  // outstanding load before writing it, once per unrolled round of steps. (A vector, not an array:
+  // hipcc drops the host stub of a kernel whose lambda indexes a captured array in this builtin.)
+  static_assert(MCH <= 4, "one offset per chunk in a 4-vector");
+  u32x4_t xoff = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int q = 0; q < MCH; ++q) {
+    const int r = 4 * (tg + 4 * q) + (lane >> 4);
+    xoff[q] = ((uint32_t)min(r, M - 1) * (uint32_t)K + 8u * (uint32_t)((lane & 15) ^ (r & 15))) * 2u;
+  }
   auto issue_x = [&](int s, int slot) {  // this wave's MCH copies of step s
     const bool live = s < nk;
     const int kb = live ? kb_of(s) : 0;
     uint8_t* base = ring + slot * kStage;
+    if (live && (kb + 1) * KBLK > K) {  // the partial last block: columns at or beyond K copy zeros
 #pragma unroll
-    for (int q = 0; q < MCH; ++q) {
-      const int j = tg + 4 * q;  // rows 4j .. 4j+3
-      const int r = 4 * j + (lane >> 4);
-      const int col = kb * KBLK + 8 * ((lane & 15) ^ (r & 15));
-      const bool ok = live & (r < M) & (col < K);  // a select, not a branch
-      const uint32_t off = ok ? ((uint32_t)r * (uint32_t)K + (uint32_t)col) * 2u : 0xFFFFFFF0u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(base + j * 1024), 16, off, 0, 0, 0);
+      for (int q = 0; q < MCH; ++q) {
+        const int j = tg + 4 * q;  // rows 4j .. 4j+3
+        const int r = 4 * j + (lane >> 4);
+        const int col = kb * KBLK + 8 * ((lane & 15) ^ (r & 15));
+        const bool ok = (r < M) & (col < K);  // a select, not a branch
+        const uint32_t off = ok ? ((uint32_t)r * (uint32_t)K + (uint32_t)col) * 2u : 0xFFFFFFF0u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(base + j * 1024), 16, off, 0, 0, 0);
+      }
+    } else {
+      const rsrc_t& rs = live ? xr : xnull;
+      const uint32_t so = (uint32_t)(kb * KBLK) * 2u;
+#pragma unroll
+      for (int q = 0; q < MCH; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(base + (tg + 4 * q) * 1024), 16, xoff[q], so, 0, 0);
     }
   };
 
@@ -336,18 +373,17 @@ __global__ __launch_bounds__(256 * KG) void skinny_lds_kernel(const typename W::
 #pragma unroll
     for (int r = 0; r < R; ++r) W::load(c, r * KB + kb, wring[slot][r], pring[slot][r]);
   };
-  // prologue in the steady state's issue order: ring blocks 0 .. D-3 first (older than every copy),
-  // then copy 0, ring D-2, copy 1, ring D-1
+  // prologue in the steady state's issue order: ring blocks 0 .. D-A-1 first (older than every
+  // copy), then copy j and ring D-A+j for j < A
 #pragma unroll
-  for (int d = 0; d < D - 2; ++d) load_step(d, d);
-  __builtin_amdgcn_sched_barrier(0);
-  issue_x(0, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  load_step(D - 2, D - 2);
-  __builtin_amdgcn_sched_barrier(0);
-  issue_x(1, 1);
-  __builtin_amdgcn_sched_barrier(0);
-  load_step(D - 1, D - 1);
+  for (int d = 0; d < D - AH; ++d) load_step(d, d);
+#pragma unroll
+  for (int j = 0; j < AH; ++j) {
+    __builtin_amdgcn_sched_barrier(0);
+    issue_x(j, j);
+    __builtin_amdgcn_sched_barrier(0);
+    load_step(D - AH + j, D - AH + j);
+  }
 
   // Software pipeline (one group per block): the weights of step s+1 are decoded while the MFMAs
   // of step s run, so the decode's VALU work issues between independent MFMAs. Blocks with several
@@ -383,7 +419,7 @@ __global__ __launch_bounds__(256 * KG) void skinny_lds_kernel(const typename W::
           pcur[r] = pring[d][r];
         }
       }
-      issue_x(s + 2, (s + 2) % NS);
+      issue_x(s + AH, (s + AH) % NS);
       __builtin_amdgcn_sched_barrier(0);
       load_step(s + D, d);
       __builtin_amdgcn_sched_barrier(0);
@@ -589,16 +625,19 @@ inline SkinnyShape skinny_default_shape(int64_t m, int64_t rows, int64_t cols, i
     // 4096->28672 15.66 -> 15.13 us at M = 2 only
     s = SkinnyShape{2, 0, 0, 1, false};
   } else if (m <= 16) {
-    if (T >= 4096) s = SkinnyShape{1, 4, 4, 1, false};
+    // (sweep of the LDS-staged shapes at M = 16 / 32 / 48 / 64, symmetric int4, rotating weights:
+    // the lm_head 62.6 / 73.7 -> 54.1 / 64.7 us with 2 tiles per wave and 4 waves, gate/up at M = 32
+    // 23.0 -> 20.5 us with 2 tiles per wave, down at M = 16 15.2 -> 13.4 us with 4 K splits)
+    if (T >= 4096) s = SkinnyShape{1, 2, 4, 1, false};
     else if (T >= 1024) s = SkinnyShape{0, 4, 4, 1, false};
     else if (T >= 384) s = SkinnyShape{0, 2, 8, 1, false};
-    else if (have_ws && KB >= 64) s = SkinnyShape{0, 2, 8, 2, false};
+    else if (have_ws && KB >= 64) s = m == 16 ? SkinnyShape{1, 1, 8, 4, false} : SkinnyShape{0, 2, 8, 2, false};
     else s.gemv = true;
   } else if (m <= 32) {
     if (T >= 4096) {
-      s = SkinnyShape{1, 1, 4, 1, false};
+      s = SkinnyShape{1, 2, 4, 1, false};
     } else if (T >= 1024) {
-      s = SkinnyShape{1, 1, 8, 1, false};
+      s = SkinnyShape{1, 2, 8, 1, false};
     } else if (have_ws && KB >= 64) {
       s = SkinnyShape{1, 1, 8, 1, false};
       split_to_192();
@@ -656,18 +695,20 @@ hipError_t skinny_lds_launch(const typename W::Args& wa, const uint16_t* x, uint
   const bool split = S > 1;
   if (split && (ws == nullptr || ws_bytes < skinny_workspace_bytes(m, rows, S))) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(ceil_div(T, 4 * R)), static_cast<unsigned>(S));
-  const size_t lds = static_cast<size_t>(KG) * 3 * mch * 16 * 256;
+  const size_t lds = static_cast<size_t>(KG) * mch * 16 * 256;  // times the kernel's stage count
   void* o = split ? static_cast<void*>(ws) : static_cast<void*>(y);
   const int M = static_cast<int>(m), N = static_cast<int>(rows), K = static_cast<int>(cols), iKB = static_cast<int>(KB),
             iT = static_cast<int>(T);
 #define SQX_SL(MCH_, R_)                                                                                            \
   do {                                                                                                              \
     if (KG == 1)                                                                                                    \
-      hipLaunchKernelGGL((skinny_lds_kernel<A, W, MCH_, R_, skinny_ring<R_>(), 1>), grid, dim3(256), lds, stream, wa, \
-                         x, o, bias, M, N, K, iKB, iT, kbs, split ? 1 : 0);                                        \
+      hipLaunchKernelGGL((skinny_lds_kernel<A, W, MCH_, R_, skinny_ring<R_>(), 1>), grid, dim3(256),              \
+                         lds * (skinny_stages<MCH_, R_, skinny_ring<R_>(), 1, W::kLoads>()), stream, wa, x, o,     \
+                         bias, M, N, K, iKB, iT, kbs, split ? 1 : 0);                                              \
     else                                                                                                            \
-      hipLaunchKernelGGL((skinny_lds_kernel<A, W, MCH_, R_, skinny_ring<R_>(), 2>), grid, dim3(512), lds, stream, wa, \
-                         x, o, bias, M, N, K, iKB, iT, kbs, split ? 1 : 0);                                        \
+      hipLaunchKernelGGL((skinny_lds_kernel<A, W, MCH_, R_, skinny_ring<R_>(), 2>), grid, dim3(512),              \
+                         lds * (skinny_stages<MCH_, R_, skinny_ring<R_>(), 2, W::kLoads>()), stream, wa, x, o,     \
+                         bias, M, N, K, iKB, iT, kbs, split ? 1 : 0);                                              \
   } while (0)
   if (mch == 1) {
     if (R == 1) SQX_SL(1, 1);
