@@ -421,8 +421,8 @@ def _host_stats(fn, warmup: int = 20, iters: int = 50) -> dict:
 
 def cpu_baselines(dev, cpu_sample, xs, m: int, per_shape: dict) -> dict:
     """The reference's CPU path (torch dequantize, then F.linear; oracle/torch_path.py) on this host's
-    cores: variant (i) dequantizes on every call (what the reference
-    does), variant (ii) keeps the dequantized weight (a CPU upper bound); each timed over 50 calls
+    cores in two variants: (i) dequantizes on every call (what the reference does), (ii) keeps the
+    dequantized weight (a CPU upper bound); each timed over 50 calls
     after 20 warm-ups on the host clock, median and p20-p80. Legs: config 2's int4 format over layer
     0's seven projections at the bench's M (the headline leg, ``value``), config 1's int8 4096 x 4096
     at M = 1 and 16, config 3's AWQ 4096 x 4096 at M = 64, and config 4's MXFP4 8192 -> 28672 at
