@@ -232,6 +232,16 @@ int sqx_int4_linear_rowscale_sumsq(const uint8_t* wt, const float* st, const voi
                                    float eps, void* y, int64_t m, int64_t rows, int64_t cols, int64_t group,
                                    int k_slices, sqx_stream_t stream);
 
+/* sqx_int4_linear_rowscale_sumsq for the decode step's fused gate|up weight with SwiGLU's product in
+ * the epilogue (model.py:223-237, SwiGLU.forward's silu(w1 x) * w3 x): the weight's rows alternate in
+ * groups of 8 (rows 16t..16t+7 are gate rows 8t..8t+7, rows 16t+8..16t+15 the matching up rows, so
+ * rows = 2 d_ff, a multiple of 16), each output is rounded to bf16 as sqx_int4_linear_rowscale_sumsq
+ * writes it, and y [m, rows / 2] = bf16(silu(g) * u) per pair, bit for bit sqx_int4_linear_rowscale_sumsq
+ * followed by sqx_silu_mul_pairs8. m is 1 (rows the one-row form takes) or 2..8 (sqx_int4_rows_fits). */
+int sqx_int4_linear_rowscale_swiglu(const uint8_t* wt, const float* st, const void* hg, const float* ss, int64_t nss,
+                                    float eps, void* y, int64_t m, int64_t rows, int64_t cols, int64_t group,
+                                    int k_slices, sqx_stream_t stream);
+
 /* The decode step's fused q|k|v projection at one row with RoPE and the slot-cache write in its epilogue
  * (model.py:205-224, 281-305; kv_cache.py:194-205): the one-row GEMV of x [cols] (with ss given, the
  * row factor of sqx_int4_linear_rowscale_sumsq: x is bf16(h * gain) and ss the sums of squares of h),
@@ -725,6 +735,11 @@ int sqx_decode_attention_rope_fp8kv(const void* qkv, const int* lengths, const f
 /* SwiGLU's gate (model.py:227-237): out = bf16(silu(g) * u) from gate_up = bf16 [B, 2F] laid out
  * [g | u] (the w1 and w3 outputs side by side); out: bf16 [B, F]. */
 int sqx_silu_mul(const void* gate_up, int64_t B, int64_t F, void* out, sqx_stream_t stream);
+
+/* sqx_silu_mul for a gate_up row laid out in 8-element groups [g 8j..8j+7 | u 8j..8j+7] (what a fused
+ * gate|up weight with alternating 8-row groups writes); the same arithmetic per element. F a multiple
+ * of 8; 16-byte aligned buffers. */
+int sqx_silu_mul_pairs8(const void* gate_up, int64_t B, int64_t F, void* out, sqx_stream_t stream);
 
 /* Embedding.forward (model.py:136-145): out[b] = table[tokens[b]]; table bf16 [V, d]. An id outside
  * [0, V) gives a zero row (the reference raises; callers validate host-side ids). */

@@ -84,6 +84,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                              _c_i64, _c_i64, _c_i, _c_p]),
     "sqx_int4_linear_rowscale_sumsq": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, ctypes.c_float, _c_p, _c_i64, _c_i64,
                                               _c_i64, _c_i64, _c_i, _c_p]),
+    "sqx_int4_linear_rowscale_swiglu": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, ctypes.c_float, _c_p, _c_i64, _c_i64,
+                                              _c_i64, _c_i64, _c_i, _c_p]),
     "sqx_int4_linear_rope_kv": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, ctypes.c_float, _c_p, _c_p, _c_p, _c_i64, _c_i64,
                                        _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i, _c_p]),
     "sqx_int4_rows_fits": (_c_i, [_c_i64, _c_i64, _c_i64, _c_i]),
@@ -203,6 +205,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_i64, _c_p],
     ),
     "sqx_silu_mul": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_silu_mul_pairs8": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_embed": (_c_i, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_argmax_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
     "sqx_argmax": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p]),

@@ -609,14 +609,17 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
 
 // Eight elements per thread (16-byte loads and stores) when F is a multiple of 8 and the buffers are
 // 16-byte aligned, so eight consecutive elements never cross a row; the same arithmetic per element
-// as silu_mul_kernel.
+// as silu_mul_kernel. PAIRS8: the row is laid out in 8-element groups [g 8j .. 8j+7 | u 8j .. 8j+7], as
+// a fused gate|up weight with alternating 8-row groups writes it.
+template <bool PAIRS8 = false>
 __global__ __launch_bounds__(256) void silu_mul8_kernel(const uint16_t* __restrict__ gu, int F, int64_t n,
                                                         uint16_t* __restrict__ out) {
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
   if (i >= n) return;
   const int64_t b = i / F, c = i % F;
-  const u32x4_t g4 = *reinterpret_cast<const u32x4_t*>(gu + b * 2 * F + c);
-  const u32x4_t u4 = *reinterpret_cast<const u32x4_t*>(gu + b * 2 * F + F + c);
+  const uint16_t* gp = gu + b * 2 * F + (PAIRS8 ? 2 * c : c);
+  const u32x4_t g4 = *reinterpret_cast<const u32x4_t*>(gp);
+  const u32x4_t u4 = *reinterpret_cast<const u32x4_t*>(gp + (PAIRS8 ? 8 : F));
   u32x4_t r;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -1052,7 +1055,7 @@ extern "C" int sqx_silu_mul(const void* gate_up, int64_t B, int64_t F, void* out
               "sqx_silu_mul: pointers must be 4-byte aligned");
   const int64_t n = B * F;
   if (F % 8 == 0 && reinterpret_cast<uintptr_t>(gate_up) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0)
-    hipLaunchKernelGGL(silu_mul8_kernel, dim3(static_cast<unsigned>(ceil_div(n / 8, 256))), dim3(256), 0,
+    hipLaunchKernelGGL(silu_mul8_kernel<false>, dim3(static_cast<unsigned>(ceil_div(n / 8, 256))), dim3(256), 0,
                        as_stream(stream), static_cast<const uint16_t*>(gate_up), static_cast<int>(F), n,
                        static_cast<uint16_t*>(out));
   else
@@ -1060,6 +1063,22 @@ extern "C" int sqx_silu_mul(const void* gate_up, int64_t B, int64_t F, void* out
                        as_stream(stream), static_cast<const uint16_t*>(gate_up), static_cast<int>(F), n,
                        static_cast<uint16_t*>(out));
   SQX_LAUNCH_CHECK("sqx_silu_mul");
+  return SQX_OK;
+}
+
+extern "C" int sqx_silu_mul_pairs8(const void* gate_up, int64_t B, int64_t F, void* out, sqx_stream_t stream) {
+  const char* fn = "sqx_silu_mul_pairs8";
+  SQX_REQUIRE(B >= 0 && F > 0 && F % 8 == 0 && B * F < (int64_t(1) << 40), SQX_E_ARG,
+              "%s: bad shape (F must be a multiple of 8)", fn);
+  if (B == 0) return SQX_OK;
+  SQX_REQUIRE(gate_up && out, SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(gate_up) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0, SQX_E_ARG,
+              "%s: pointers must be 16-byte aligned", fn);
+  const int64_t n = B * F;
+  hipLaunchKernelGGL(silu_mul8_kernel<true>, dim3(static_cast<unsigned>(ceil_div(n / 8, 256))), dim3(256), 0,
+                     as_stream(stream), static_cast<const uint16_t*>(gate_up), static_cast<int>(F), n,
+                     static_cast<uint16_t*>(out));
+  SQX_LAUNCH_CHECK(fn);
   return SQX_OK;
 }
 

@@ -115,6 +115,10 @@ struct has_row_scale<W, std::void_t<decltype(W::kRowScale)>> : std::integral_con
 // rotated and stored at cache row min(lengths[0], tmax - 1) of k_cache [kn / 128, tmax, 128]
 // (kv_cache.py:194-205); the rest are v, stored there in v_cache. Wave 0 requests the length with
 // its activation slice and the pair's cos / sin behind it, so the epilogue finds them in registers.
+// SWI (one-row forms): the SwiGLU pair epilogue for a fused gate|up weight whose rows alternate in
+// groups of 8 (tile t holds gate rows 8t..8t+7 then the matching up rows): each output is rounded to
+// bf16 as the GEMV writes it and y[8t + i] = bf16(silu(g_i) * u_i), as the standalone SiLU kernel
+// computes it from those bf16 values (model.py:223-237's silu(w1 x) * w3 x). y has N / 2 entries a row.
 // kProAttnCombine (one row, two k-blocks per wave, 128-column blocks): x is the attention output of
 //                the decode step, formed here from the key-chunk partials that
 //                sqx_decode_attention_partials left (o then (m, l) per head and chunk, at most
@@ -152,7 +156,7 @@ struct ProArgs {
 };
 
 template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32, int PRO = kProPlain, int ONE = 0,
-          bool RES = false, bool RKV = false>
+          bool RES = false, bool RKV = false, bool SWI = false>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ? 8 : 1))) void gemv_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
                                                     void* __restrict__ yv, const uint16_t* __restrict__ bias,
                                                     const float* __restrict__ colscale, int M, int N, int K, int KB,
@@ -168,6 +172,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
   static_assert(!RES || ONE != 0, "the residual epilogue is a one-row form");
   static_assert(!RKV || (ONE >= 2 && !RES), "the RoPE epilogue is a one-row form of its own");
   static_assert(ONE == 0 || !YF32, "the one-row form writes 16-bit outputs");
+  static_assert(!SWI || (ONE != 0 && !RES && !RKV), "the SwiGLU pair epilogue is a one-row form of its own");
   extern __shared__ f32x4_t smem[];  // [NW][MCH][64] partial accumulators, then (XLDS) the activations
   f32x4_t* red = smem;
   const int lane = threadIdx.x & 63;
@@ -638,7 +643,9 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
           v *= W::out_scale(wa, n);
         if constexpr (PRO == kProScaleSum) v *= row_scale_lds;
         if (bias) v += A::to_f32(bias[n]);
-        if constexpr (RES) {
+        if constexpr (SWI) {
+          // the pair is formed below, by the whole wave
+        } else if constexpr (RES) {
           // opaque until here: otherwise the compiler converts the prefetched values where they are
           // loaded and waits for them there, before wave 0 has issued its weights
           asm volatile("" : "+v"(res_pre), "+v"(gain_pre));
@@ -654,6 +661,12 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
       if constexpr (RES) {
         hsq = wave_sum(hsq);
         if (lane == 0) pa.ss_out[t] = hsq;
+      }
+      if constexpr (SWI) {
+        const float q = own ? A::to_f32(A::from_f32(v)) : 0.0f;  // this row's bf16 output
+        const float u = __shfl_xor(q, 8, 64);                     // lane l < 8: its up row (lane l + 8)
+        if (own && lane < 8)
+          static_cast<uint16_t*>(yv)[t * 8 + lane] = static_cast<uint16_t>(A::pack_rne(silu_f32(q) * u, 0.0f));
       }
     }
     return;
@@ -680,7 +693,9 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
         v *= W::out_scale(wa, n);
       if constexpr (PRO == kProScaleSum) v *= row_scale_lds;
       if (bias) v += A::to_f32(bias[n]);
-      if constexpr (RES) {
+      if constexpr (SWI) {
+        // below, by the whole wave
+      } else if constexpr (RES) {
         const float h = A::to_f32(A::from_f32(A::to_f32(pa.res[n]) + A::to_f32(A::from_f32(v))));
         pa.res_out[n] = A::from_f32(h);
         if (pa.gain_next != nullptr) pa.hg_out[n] = A::from_f32(h * A::to_f32(pa.gain_next[n]));
@@ -698,12 +713,23 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
         if (j == 0) pa.ss_out[t] = hsq;
       }
     }
+    if constexpr (SWI) {
+      // output n's up row n + 8 is output j ^ 32 (l ^ 8, same row m), in this wave and iteration: every
+      // iteration covers whole waves (kOut and the block are multiples of 64)
+      const bool ok = m < M && n < N;
+      const float q = ok ? A::to_f32(A::from_f32(v)) : 0.0f;
+      const float u = __shfl_xor(q, 32, 64);
+      if (ok && (l & 15) < 8)
+        static_cast<uint16_t*>(yv)[(int64_t)m * (N / 2) + t * 8 + (l & 15)] =
+            static_cast<uint16_t>(A::pack_rne(silu_f32(q) * u, 0.0f));
+    }
   }
 }
 
 // Launch the GEMV for every 64-row pass of x. k_slices <= 0 picks the default. Returns 0 or the
 // HIP error of the launch.
-template <class A, class W, int U1, int U2, bool YF32, int PRO = kProPlain, bool RES = false, bool RKV = false>
+template <class A, class W, int U1, int U2, bool YF32, int PRO = kProPlain, bool RES = false, bool RKV = false,
+          bool SWI = false>
 hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, const uint16_t* bias,
                        const float* colscale, int64_t m, int64_t rows, int64_t cols, int k_slices,
                        hipStream_t stream, const ProArgs& pa = ProArgs{nullptr, nullptr, nullptr, 0.0f}) {
@@ -730,7 +756,7 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
 #define SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, ONE_)                                                              \
   do {                                                                                                        \
     if constexpr (!RKV || ONE_ == 2)                                                                          \
-      hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO, ONE_, RES, RKV>), grid, block, LDS_, stream, \
+      hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO, ONE_, RES, RKV, SWI>), grid, block, LDS_, stream, \
                          wp, xp, yp, bias, colscale, M, N, K, iKB, kbw, pa);                                  \
   } while (0)
 #define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_) SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, 0)
@@ -757,6 +783,8 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
       return hipErrorNotSupported;
     // the RoPE epilogue: the one-row form 2 with wave 0 finishing each tile (grids under 1024 tiles)
     if (RKV && (one_mode != 2 || T >= 1024)) return hipErrorNotSupported;
+    // the SwiGLU pair epilogue: one-row forms over whole 16-row tiles
+    if (SWI && (one_mode != 2 || N % 16 != 0)) return hipErrorNotSupported;
     if (one_mode != 0) {
       if constexpr (kOneOk) {
         if (one_mode == 2) {
@@ -826,20 +854,23 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
 //                       bf16(res_out[m] * gain_next) when gain_next is given, ss_out[m][t] = sum of
 //                       res_out[m]^2 over tile t (16 outputs, summed by a fixed shuffle tree);
 //   RKV                 the q|k|v projection's RoPE and cache write at row m's position lengths[m]:
-//                       q_out [M][qn], k_cache / v_cache [M][kn / 128][tmax][128].
+//                       q_out [M][qn], k_cache / v_cache [M][kn / 128][tmax][128];
+//   SWI                 the SwiGLU pair epilogue of the one-row form (rows of 8-row gate / up groups):
+//                       y [M][N / 2].
 // The epilogue's residual, gain and length values are requested at kernel start (cos / sin behind the
 // activation slice), by the threads that use them.
 // RG = 2 (MR = 4, 5..8 rows): two workgroups per tile, rows 0..3 and 4..7. Workgroups b and b + 8 take
 // the same tile: the hardware hands workgroups to the eight XCDs in turn, so both run on one XCD and
 // the second finds the tile's weights in that XCD's L2 (the grid covers whole groups of 8 tiles).
-template <class A, class W, int MR, int XW, int PRO = kProPlain, bool RES = false, bool RKV = false, int RG = 1>
+template <class A, class W, int MR, int XW, int PRO = kProPlain, bool RES = false, bool RKV = false, int RG = 1,
+          bool SWI = false>
 __global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args wa, const uint16_t* __restrict__ x_,
                                                          uint16_t* __restrict__ y_, const uint16_t* __restrict__ bias,
                                                          int M_, int N, int K, int KB, int kbw, const ProArgs pa_) {
   static_assert(has_sum_offset<W>::value && W::KBLK == 128 && W::STEPS == 4, "int4 tiles: 128-column blocks");
   static_assert(MR == 4 || MR == 8, "4 or 8 rows");
   static_assert(PRO == kProPlain || PRO == kProSiluGate || PRO == kProScaleSum, "plain rows, SiLU gate or row factor");
-  static_assert(!(RES && RKV), "one epilogue");
+  static_assert(!(RES && RKV) && !(SWI && (RES || RKV)), "one epilogue");
   static_assert(RG == 1 || (RG == 2 && MR == 4), "two groups of four rows");
   constexpr int KBLK = 128, U = 4, NG = kNgOf<W>, CPB = 4, CPG = CPB / NG, MPG = 4 / NG;
   constexpr int kJ = 16 * MR;  // epilogue threads: output j = (lane l = j / 4, element e = j % 4)
@@ -855,7 +886,7 @@ __global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args 
   const int M = RG == 1 ? M_ : min(4, M_ - rb);
   if (RG == 2 && (t >= T || M <= 0)) return;  // the whole workgroup: padding tiles, or rows 4..7 of M <= 4
   const uint16_t* x = x_ + static_cast<int64_t>(rb) * RS * K;
-  uint16_t* y = y_ == nullptr ? nullptr : y_ + static_cast<int64_t>(rb) * N;
+  uint16_t* y = y_ == nullptr ? nullptr : y_ + static_cast<int64_t>(rb) * (SWI ? N / 2 : N);
   ProArgs pa = pa_;
   if (RG == 2 && rb > 0) {  // this workgroup's rows of every row-major array
     if (pa.res) pa.res += static_cast<int64_t>(rb) * N;
@@ -1105,6 +1136,14 @@ __global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args 
     hsq += __shfl_xor(hsq, 16, 64);
     hsq += __shfl_xor(hsq, 32, 64);
     if (((jo >> 2) & 15) == 0 && mo < M) pa.ss_out[static_cast<int64_t>(mo) * T + t] = hsq;
+  } else if constexpr (SWI) {
+    // output no's up row no + 8 is thread jo ^ 32 (same row mo), in this wave
+    if (own && bias) v += A::to_f32(bias[no]);
+    const float q = own ? A::to_f32(A::from_f32(v)) : 0.0f;
+    const float u = __shfl_xor(q, 32, 64);
+    if (own && ((jo >> 2) & 8) == 0)
+      y[static_cast<int64_t>(mo) * (N / 2) + t * 8 + ((jo >> 2) & 7)] =
+          static_cast<uint16_t>(A::pack_rne(silu_f32(q) * u, 0.0f));
   } else {
     if (own) {
       if (bias) v += A::to_f32(bias[no]);
@@ -1161,7 +1200,7 @@ inline bool gemv_rows_fits(int64_t m, int64_t rows, int64_t cols, int nw = 0, bo
   return gemv_rows_groups(m, rows, cols, nw, scale_sum) != 0;
 }
 
-template <class A, class W, int PRO = kProPlain, bool RES = false, bool RKV = false>
+template <class A, class W, int PRO = kProPlain, bool RES = false, bool RKV = false, bool SWI = false>
 hipError_t gemv_rows_launch(const typename W::Args& wa, const uint16_t* x, uint16_t* y, const uint16_t* bias,
                             int64_t m, int64_t rows, int64_t cols, int waves, hipStream_t stream,
                             const ProArgs& pa = ProArgs{nullptr, nullptr, nullptr, 0.0f}, int groups = 0) {
@@ -1179,15 +1218,17 @@ hipError_t gemv_rows_launch(const typename W::Args& wa, const uint16_t* x, uint1
   const int M = static_cast<int>(m), N = static_cast<int>(rows), K = static_cast<int>(cols), iKB = static_cast<int>(KB);
   // columns at or past K (a k tail) read zero through the row resources, so the padded blocks need no
   // masking
+  if (SWI && rows % 16 != 0) return hipErrorNotSupported;  // whole gate / up tiles
   if (rgs == 2)
-    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 2, PRO, RES, RKV, 2>), dim3(static_cast<unsigned>(ceil_div(T, 8) * 16)),
-                       block, lds, stream, wa, x, y, bias, M, N, K, iKB, kbw, pa);
+    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 2, PRO, RES, RKV, 2, SWI>),
+                       dim3(static_cast<unsigned>(ceil_div(T, 8) * 16)), block, lds, stream, wa, x, y, bias, M, N, K, iKB,
+                       kbw, pa);
   else if (!eight)
-    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 2, PRO, RES, RKV>), dim3(static_cast<unsigned>(T)), block, lds, stream,
-                       wa, x, y, bias, M, N, K, iKB, kbw, pa);
+    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 2, PRO, RES, RKV, 1, SWI>), dim3(static_cast<unsigned>(T)), block, lds,
+                       stream, wa, x, y, bias, M, N, K, iKB, kbw, pa);
   else
-    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 8, 1, PRO, RES, RKV>), dim3(static_cast<unsigned>(T)), block, lds, stream,
-                       wa, x, y, bias, M, N, K, iKB, kbw, pa);
+    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 8, 1, PRO, RES, RKV, 1, SWI>), dim3(static_cast<unsigned>(T)), block, lds,
+                       stream, wa, x, y, bias, M, N, K, iKB, kbw, pa);
   return hipGetLastError();
 }
 

@@ -567,7 +567,7 @@ hipError_t int4_gemv_f32out(const uint8_t* wt, const void* st, const void* zt, b
 // The decode step's fused linears (symmetric codes, fp32 scales, bf16 activations): the residual
 // add + RMSNorm, or the SiLU gate, computed in the LDS copy of the activations.
 // RES: the residual epilogue (one row): y is unused, pa.res_out and pa.ss_out are written.
-template <int PRO, bool RES>
+template <int PRO, bool RES, bool SWI = false>
 static hipError_t launch_int4_pro_res(int group, const uint8_t* wt, const float* st, const uint16_t* x, uint16_t* y,
                                       int64_t m, int64_t rows, int64_t cols, int k_slices, hipStream_t s,
                                       const ProArgs& pa) {
@@ -575,8 +575,8 @@ static hipError_t launch_int4_pro_res(int group, const uint8_t* wt, const float*
   {                                                                                                                 \
     using W = WInt4<G_, false, false>;                                                                              \
     const typename W::Args a{wt, st, nullptr};                                                                      \
-    return gemv_launch<ActBF16, W, SQX_INT4_U1, SQX_INT4_U2, false, PRO, RES>(a, x, y, nullptr, nullptr, m, rows,   \
-                                                                              cols, k_slices, s, pa);              \
+    return gemv_launch<ActBF16, W, SQX_INT4_U1, SQX_INT4_U2, false, PRO, RES, false, SWI>(                          \
+        a, x, y, nullptr, nullptr, m, rows, cols, k_slices, s, pa);                                                 \
   }
   if (group == 128) SQX_PRO(128)
   if (group == 64) SQX_PRO(64)
@@ -1241,15 +1241,15 @@ extern "C" int sqx_int4_linear_silu(const uint8_t* wt, const float* st, const vo
 }
 
 // The decode step's fused forms at 2..8 rows: the multi-row GEMV (symmetric codes, fp32 scales, bf16).
-template <int PRO, bool RES, bool RKV>
+template <int PRO, bool RES, bool RKV, bool SWI = false>
 static hipError_t launch_int4_rows_fused(int group, const uint8_t* wt, const float* st, const uint16_t* x, uint16_t* y,
                                          int64_t m, int64_t rows, int64_t cols, int k_slices, hipStream_t s,
                                          const ProArgs& pa) {
-#define SQX_RF(G_)                                                                                           \
-  {                                                                                                          \
-    using W = WInt4<G_, false, false>;                                                                       \
-    const typename W::Args a{wt, st, nullptr};                                                               \
-    return gemv_rows_launch<ActBF16, W, PRO, RES, RKV>(a, x, y, nullptr, m, rows, cols, k_slices, s, pa);    \
+#define SQX_RF(G_)                                                                                                 \
+  {                                                                                                                \
+    using W = WInt4<G_, false, false>;                                                                             \
+    const typename W::Args a{wt, st, nullptr};                                                                     \
+    return gemv_rows_launch<ActBF16, W, PRO, RES, RKV, SWI>(a, x, y, nullptr, m, rows, cols, k_slices, s, pa);     \
   }
   if (group == 128) SQX_RF(128)
   if (group == 64) SQX_RF(64)
@@ -1447,6 +1447,49 @@ extern "C" int sqx_int4_linear_rowscale_sumsq(const uint8_t* wt, const float* st
   const hipError_t e = launch_int4_pro<kProScaleSum>(static_cast<int>(group), wt, st, static_cast<const uint16_t*>(hg),
                                                      static_cast<uint16_t*>(y), m, rows, cols, k_slices,
                                                      as_stream(stream), pa);
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return SQX_OK;
+}
+
+extern "C" int sqx_int4_linear_rowscale_swiglu(const uint8_t* wt, const float* st, const void* hg, const float* ss,
+                                             int64_t nss, float eps, void* y, int64_t m, int64_t rows, int64_t cols,
+                                             int64_t group, int k_slices, sqx_stream_t stream) {
+  const char* fn = "sqx_int4_linear_rowscale_swiglu";
+  SQX_REQUIRE(m >= 1 && m <= 8, SQX_E_ARG, "%s: the norm from tile sums takes 1..8 rows, m=%lld", fn, (long long)m);
+  const int rc = m >= 2 ? int4_rows_check(wt, st, hg, y, m, rows, cols, group, k_slices, true, fn)
+                        : int4_pro_check(wt, st, hg, y, m, rows, cols, group, k_slices, fn);
+  if (rc != SQX_OK) return rc;
+  SQX_REQUIRE(rows % 16 == 0, SQX_E_ARG, "%s: rows=%lld: the gate / up pairs fill whole 16-row tiles", fn, (long long)rows);
+  SQX_REQUIRE(nss == ceil_div(cols, 16) && nss <= kNormSumMax, SQX_E_ARG,
+              "%s: %lld sums of squares for %lld columns (one per 16 columns, at most %d)", fn, (long long)nss,
+              (long long)cols, kNormSumMax);
+  SQX_REQUIRE(ss != nullptr && reinterpret_cast<uintptr_t>(ss) % 16 == 0 && (m == 1 || nss % 4 == 0), SQX_E_ARG,
+              "%s: the sums must be 16-byte aligned (and a multiple of 4 a row)", fn);
+  if (m >= 2) {
+    ProArgs pa{};
+    pa.eps = eps;
+    pa.ss_in = ss;
+    pa.nss = static_cast<int>(nss);
+    const hipError_t e = launch_int4_rows_fused<kProScaleSum, false, false, true>(
+        static_cast<int>(group), wt, st, static_cast<const uint16_t*>(hg), static_cast<uint16_t*>(y), m, rows, cols,
+        k_slices, as_stream(stream), pa);
+    SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    return SQX_OK;
+  }
+  const int64_t KB = ceil_div(cols, 128);
+  int nw = k_slices <= 0 ? gemv_default_kslices(rows, cols, 128, 1) : k_slices;
+  if (nw > KB) nw = static_cast<int>(KB);
+  SQX_REQUIRE(ceil_div(KB, nw) <= kOneMaxKbw, SQX_E_ARG,
+              "%s: %lld k-blocks over %d waves: at most %d per wave (raise k_slices)", fn, (long long)KB, nw,
+              kOneMaxKbw);
+  ProArgs pa{};
+  pa.eps = eps;
+  pa.ss_in = ss;
+  pa.nss = static_cast<int>(nss);
+  const hipError_t e = launch_int4_pro_res<kProScaleSum, false, true>(static_cast<int>(group), wt, st,
+                                                                     static_cast<const uint16_t*>(hg),
+                                                                     static_cast<uint16_t*>(y), m, rows, cols, k_slices,
+                                                                     as_stream(stream), pa);
   SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return SQX_OK;
 }

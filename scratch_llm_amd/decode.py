@@ -205,12 +205,12 @@ class Int4DecodeLM:
         self.final_norm = final_norm
         self.lm_head = lm_head
         self.device = embed.device
-        # Which small-batch prologues run inside the linears. The SiLU gate pays (one launch fewer, and
-        # a 256-workgroup down projection recomputes it cheaply); the norm does not (every workgroup of
-        # the wide qkv / gate-up / lm_head projections would recompute the whole row's norm), so it
-        # stays a kernel of its own unless asked for.
+        # Whether the general step's norm runs inside the next linear's prologue: it does not pay (every
+        # workgroup of the wide qkv / gate-up / lm_head projections would recompute the whole row's
+        # norm), so it stays a kernel of its own unless asked for. SwiGLU's product needs no prologue:
+        # the fused gate|up weight's rows alternate in groups of 8, so the fused step forms silu(g) * u
+        # in the gate/up epilogue and the general step runs the SiLU kernel of that layout.
         self.fuse_norm = False
-        self.fuse_silu = True
         # One-row steps: the o and down projections end in the residual add and leave the sums of
         # squares per 16 columns and bf16(h * gain) of the next norm; the next projection (qkv, gate/up,
         # the lm_head) multiplies its product by the norm's row factor formed from the sums, so no norm
@@ -239,11 +239,16 @@ class Int4DecodeLM:
         dev = torch.device(device)
         g = cfg.group_size
 
-        def qw(*names: str) -> i4.Int4Tiled:
+        def qw(*names: str, pairs8: bool = False) -> i4.Int4Tiled:
             qs = [i4.quantize_groupwise_int4(get(n).to(dev, torch.float32), g) for n in names]
-            q = torch.cat([a for a, _ in qs]) if len(qs) > 1 else qs[0][0]
-            s = torch.cat([b for _, b in qs]) if len(qs) > 1 else qs[0][1]
-            return i4.tile_int4(q, s, None, g)
+            if pairs8:  # gate and up rows alternate in groups of 8: tile t holds gate 8t.. then up 8t..
+                (q1, s1), (q3, s3) = qs
+                q = torch.stack([q1.view(-1, 8, q1.shape[1]), q3.view(-1, 8, q3.shape[1])], 1).reshape(-1, q1.shape[1])
+                s = torch.stack([s1.view(-1, 8, s1.shape[1]), s3.view(-1, 8, s3.shape[1])], 1).reshape(-1, s1.shape[1])
+            else:
+                q = torch.cat([a for a, _ in qs]) if len(qs) > 1 else qs[0][0]
+                s = torch.cat([b for _, b in qs]) if len(qs) > 1 else qs[0][1]
+            return i4.tile_int4(q.contiguous(), s.contiguous(), None, g)
 
         def vec(name: str) -> Tensor:
             return get(name).to(dev, torch.bfloat16).contiguous()
@@ -256,7 +261,7 @@ class Int4DecodeLM:
                 wqkv=qw(p + "attn.q_proj.weight", p + "attn.k_proj.weight", p + "attn.v_proj.weight"),
                 wo=qw(p + "attn.o_proj.weight"),
                 ffn_norm=vec(p + "ffn_norm.weight"),
-                w13=qw(p + "ffn.w1.weight", p + "ffn.w3.weight"),
+                w13=qw(p + "ffn.w1.weight", p + "ffn.w3.weight", pairs8=True),
                 w2=qw(p + "ffn.w2.weight"),
             ))
         embed = get("token_emb.weight").to(dev, torch.bfloat16).contiguous()
@@ -376,6 +381,15 @@ class Int4DecodeLM:
             tw.wt.data_ptr(), tw.st.data_ptr(), st.h.data_ptr(), st.ss.data_ptr(), st.nss, self.cfg.norm_eps,
             y.data_ptr(), st.batch, tw.rows, tw.cols, tw.group_size, 0, stream), "rmsnorm (row factor) + int4 linear")
 
+    def _norm_sums_swiglu(self, st: DecodeState, tw: i4.Int4Tiled, y: Tensor, stream: int) -> None:
+        """:meth:`_norm_sums_linear` for the fused gate|up weight (gate and up rows alternating in groups
+        of 8) with SwiGLU's product in the epilogue: ``y`` [B, d_ff] = bf16(silu(g) * u)."""
+        lib = _lib.load()
+        _lib.check(lib.sqx_int4_linear_rowscale_swiglu(
+            tw.wt.data_ptr(), tw.st.data_ptr(), st.h.data_ptr(), st.ss.data_ptr(), st.nss, self.cfg.norm_eps,
+            y.data_ptr(), st.batch, tw.rows, tw.cols, tw.group_size, 0, stream),
+            "rmsnorm (row factor) + gate|up + silu * up")
+
     STEP_KINDS = ("qkv", "attention", "o", "gate_up", "down", "lm_head", "other")
 
     def step(self, st: DecodeState, tokens=None, only: str | None = None) -> Tensor:
@@ -399,7 +413,6 @@ class Int4DecodeLM:
         def go(kind: str) -> bool:
             return only is None or only == kind
 
-        fuse_silu = self.fuse_silu and lib.sqx_int4_linear_silu_fits(B, d, cfg.d_ff)
         # no norm launches: each residual add ends a linear and leaves the sums of squares its norm needs,
         # and the linear after the norm applies the row factor (one row: the one-row GEMV; 2..8 rows:
         # the multi-row GEMV, where it takes every linear of the step)
@@ -486,12 +499,12 @@ class Int4DecodeLM:
                             ly.wo.rows, ly.wo.cols, ly.wo.group_size, 0, s), "o + residual")
                     cur = 1 - cur
                     if go("gate_up"):
-                        self._norm_sums_linear(st, ly.w13, st.gu, s)
+                        self._norm_sums_swiglu(st, ly.w13, st.act, s)
                     if go("down"):
-                        ck(lib.sqx_int4_linear_silu_residual(
-                            ly.w2.wt.data_ptr(), ly.w2.st.data_ptr(), st.gu.data_ptr(), st.x[cur].data_ptr(),
+                        ck(lib.sqx_int4_linear_residual(
+                            ly.w2.wt.data_ptr(), ly.w2.st.data_ptr(), st.act.data_ptr(), st.x[cur].data_ptr(),
                             st.x[1 - cur].data_ptr(), st.ss.data_ptr(), gain_next.data_ptr(), st.h.data_ptr(), B,
-                            ly.w2.rows, ly.w2.cols, ly.w2.group_size, 0, s), "silu + down + residual")
+                            ly.w2.rows, ly.w2.cols, ly.w2.group_size, 0, s), "down + residual")
                     cur, have_ss = 1 - cur, True
                     continue
                 if go("o"):
@@ -502,18 +515,11 @@ class Int4DecodeLM:
                     cur = self._norm_linear(st, cur, delta, ly.ffn_norm, ly.w13, st.gu, s, dsplit)
                 else:
                     cur = cur if delta is None else 1 - cur
-                if fuse_silu:
-                    if go("down"):
-                        ck(lib.sqx_int4_linear_silu(ly.w2.wt.data_ptr(), ly.w2.st.data_ptr(), st.gu.data_ptr(),
-                                                    st.delta.data_ptr(), B, ly.w2.rows, ly.w2.cols,
-                                                    ly.w2.group_size, 0, s), "silu + int4 linear")
-                    delta, dsplit = st.delta.data_ptr(), 0
+                if go("down"):
+                    ck(lib.sqx_silu_mul_pairs8(st.gu.data_ptr(), B, cfg.d_ff, st.act.data_ptr(), s), "silu_mul")
+                    delta, dsplit = self._delta_linear(st, ly.w2, st.act, s)
                 else:
-                    if go("down"):
-                        ck(lib.sqx_silu_mul(st.gu.data_ptr(), B, cfg.d_ff, st.act.data_ptr(), s), "silu_mul")
-                        delta, dsplit = self._delta_linear(st, ly.w2, st.act, s)
-                    else:
-                        delta, dsplit = self._delta_plan(st, ly.w2)
+                    delta, dsplit = self._delta_plan(st, ly.w2)
             if not go("lm_head"):
                 pass
             elif have_ss:  # the last down projection left bf16(h * final gain) and the sums of squares

@@ -449,6 +449,57 @@ def test_linear_rowscale_sumsq(lib, n, k, group, m):
     assert float((err / bound).max()) <= 1.0, f"rowscale {k}->{n}: {float((err / bound).max()):.2f}x the bound"
 
 
+@pytest.mark.parametrize("dff,k,m", [(14336, 4096, 1), (2048, 1024, 1), (1024, 4096, 1), (14336, 4096, 2),
+                                      (2048, 1024, 3), (1024, 4096, 4), (1024, 1024, 6), (512, 1024, 8)])
+def test_rowscale_swiglu_equals_two_calls(lib, dff, k, m):
+    """sqx_int4_linear_rowscale_swiglu == sqx_int4_linear_rowscale_sumsq on the same weight (gate and up
+    rows alternating in groups of 8) followed by sqx_silu_mul_pairs8, bit for bit, and that SiLU of the
+    pairs == sqx_silu_mul of the [g | u] row, bit for bit: the Llama gate/up at one row (1792 tiles,
+    the 8-waves-per-SIMD form), smaller one-row grids (under 1024 tiles) and 2..8 rows (the multi-row
+    GEMV, one and two row groups)."""
+    from scratch_llm_amd.quant import int4_group as i4
+
+    print_case("rowscale swiglu", dff, k, m)
+    gen = torch.Generator().manual_seed(dff + k + m)
+    w1 = torch.randn(dff, k, generator=gen) * 0.05
+    w3 = torch.randn(dff, k, generator=gen) * 0.05
+    w = torch.stack([w1.view(-1, 8, k), w3.view(-1, 8, k)], 1).reshape(2 * dff, k).to(DEV)
+    q, sc = i4.quantize_groupwise_int4(w, 128)
+    tw = i4.tile_int4(q, sc, None, 128)
+    del w
+    h = (torch.randn(m, k, generator=gen) * 2).bfloat16()
+    gain = (1 + 0.1 * torch.randn(k, generator=gen)).bfloat16()
+    nt = k // 16
+    ss = (h.float() * h.float()).view(m, nt, 16).sum(2).contiguous().to(DEV)
+    hg = (h.float() * gain.float()).bfloat16().to(DEV)
+    n = 2 * dff
+    gu = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    want = torch.empty(m, dff, dtype=torch.bfloat16, device=DEV)
+    got = torch.empty(m, dff, dtype=torch.bfloat16, device=DEV)
+    _ok(lib, lib.sqx_int4_linear_rowscale_sumsq(tw.wt.data_ptr(), tw.st.data_ptr(), hg.data_ptr(), ss.data_ptr(), nt,
+                                                1e-5, gu.data_ptr(), m, n, k, 128, 0, _s()))
+    _ok(lib, lib.sqx_silu_mul_pairs8(gu.data_ptr(), m, dff, want.data_ptr(), _s()))
+    _ok(lib, lib.sqx_int4_linear_rowscale_swiglu(tw.wt.data_ptr(), tw.st.data_ptr(), hg.data_ptr(), ss.data_ptr(), nt,
+                                                 1e-5, got.data_ptr(), m, n, k, 128, 0, _s()))
+    # the pairs' SiLU against the [g | u] kernel on the de-interleaved row
+    flat = gu.view(m, dff // 8, 2, 8)
+    side = torch.cat([flat[:, :, 0].reshape(m, dff), flat[:, :, 1].reshape(m, dff)], 1).contiguous()
+    ref = torch.empty(m, dff, dtype=torch.bfloat16, device=DEV)
+    _ok(lib, lib.sqx_silu_mul(side.data_ptr(), m, dff, ref.data_ptr(), _s()))
+    torch.cuda.synchronize()
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(want, ref), "silu of the 8-row pairs != silu of the [g | u] row"
+    assert torch.equal(got, want), f"{k}->{n} m={m}: epilogue != two calls"
+
+
+def test_rowscale_swiglu_refuses(lib):
+    """Rows that are not whole 16-row tiles, or more rows than the fused forms take, are refused."""
+    rc = lib.sqx_int4_linear_rowscale_swiglu(None, None, None, None, 64, 1e-5, None, 1, 1000, 1024, 128, 0, None)
+    assert rc != 0
+    rc = lib.sqx_int4_linear_rowscale_swiglu(None, None, None, None, 64, 1e-5, None, 9, 2048, 1024, 128, 0, None)
+    assert rc != 0 and "1..8 rows" in lib.sqx_last_error().decode()
+
+
 @pytest.mark.parametrize("H,Hkv,T,length,sums,m", [(32, 8, 2048, 2047, True, 1), (32, 8, 2048, 0, False, 1),
                                                     (8, 2, 100, 140, True, 1), (16, 16, 64, 37, False, 1),
                                                     (32, 8, 2048, 2040, True, 4), (8, 2, 100, 50, False, 2),
@@ -827,10 +878,9 @@ def test_decode_step_matches_reference(small, B):
 
 @pytest.mark.parametrize("B", [1, 2, 4, 5])
 def test_fused_step_equals_unfused_step(small, B):
-    """The SiLU gate folded into the down projection changes no bit of the step (both forms run the
-    library's linear for the batch). The norm folded into the GEMV's LDS copy (fuse_norm) is
-    bit-identical at one row; at more rows the two-call form's linear may be the multi-row GEMV,
-    which sums in another order, so the logits agree to the bf16 rounding of the step."""
+    """The norm folded into the GEMV's LDS copy (fuse_norm) is bit-identical at one row; at more rows
+    the two-call form's linear may be the multi-row GEMV, which sums in another order, so the logits
+    agree to the bf16 rounding of the step."""
     model, _ = small
     print_case("fused vs unfused step", B)
     try:
@@ -839,9 +889,9 @@ def test_fused_step_equals_unfused_step(small, B):
             a, b = model.new_state(B, 32), model.new_state(B, 32)
             tok = torch.arange(B) * 97 % model.cfg.vocab_size
             for t in range(4):
-                model.fuse_norm, model.fuse_silu = fuse_norm, True
+                model.fuse_norm = fuse_norm
                 model.step(a, tok if t == 0 else None)
-                model.fuse_norm = model.fuse_silu = False
+                model.fuse_norm = False
                 model.step(b, tok if t == 0 else None)
                 torch.cuda.synchronize()
                 if fuse_norm and B > 1:
@@ -854,7 +904,7 @@ def test_fused_step_equals_unfused_step(small, B):
             if not (fuse_norm and B > 1):
                 assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
     finally:
-        model.fuse_norm, model.fuse_silu, model.fuse_norm_sums = False, True, True
+        model.fuse_norm, model.fuse_norm_sums = False, True
 
 
 @pytest.mark.parametrize("B", [20, 64])
