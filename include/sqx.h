@@ -232,6 +232,15 @@ int sqx_int4_linear_rowscale_sumsq(const uint8_t* wt, const float* st, const voi
                                    float eps, void* y, int64_t m, int64_t rows, int64_t cols, int64_t group,
                                    int k_slices, sqx_stream_t stream);
 
+/* The SwiGLU linear of a fused gate|up weight in the layout of sqx_int4_linear_rowscale_swiglu (rows
+ * alternating in groups of 8, rows a multiple of 16), without the norm's row factor: y [m, rows / 2] =
+ * bf16(silu(g) * u) with g, u the bf16 outputs of sqx_int4_linear / sqx_int4_skinny on x [m, cols]
+ * (model.py:223-237). 1..64 rows: the one-row GEMV, the multi-row GEMV or a row-tiled kernel by the
+ * library's shape choice without K splits; bit for bit that linear (same kernel and shape) followed by
+ * sqx_silu_mul_pairs8. Symmetric int4 tiles, fp32 group scales, bf16 x. */
+int sqx_int4_linear_swiglu(const uint8_t* wt, const float* st, const void* x, void* y, int64_t m, int64_t rows,
+                           int64_t cols, int64_t group, sqx_stream_t stream);
+
 /* sqx_int4_linear_rowscale_sumsq for the decode step's fused gate|up weight with SwiGLU's product in
  * the epilogue (model.py:223-237, SwiGLU.forward's silu(w1 x) * w3 x): the weight's rows alternate in
  * groups of 8 (rows 16t..16t+7 are gate rows 8t..8t+7, rows 16t+8..16t+15 the matching up rows, so

@@ -84,6 +84,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                              _c_i64, _c_i64, _c_i, _c_p]),
     "sqx_int4_linear_rowscale_sumsq": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, ctypes.c_float, _c_p, _c_i64, _c_i64,
                                               _c_i64, _c_i64, _c_i, _c_p]),
+    "sqx_int4_linear_swiglu": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p]),
     "sqx_int4_linear_rowscale_swiglu": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, ctypes.c_float, _c_p, _c_i64, _c_i64,
                                               _c_i64, _c_i64, _c_i, _c_p]),
     "sqx_int4_linear_rope_kv": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i64, ctypes.c_float, _c_p, _c_p, _c_p, _c_i64, _c_i64,

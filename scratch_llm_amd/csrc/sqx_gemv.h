@@ -755,7 +755,7 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     if (colscale != nullptr && !xlds) return hipErrorNotSupported;  // column scaling happens in the LDS copy
 #define SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, ONE_)                                                              \
   do {                                                                                                        \
-    if constexpr (!RKV || ONE_ == 2)                                                                          \
+    if constexpr ((!RKV || ONE_ == 2) && (!SWI || ONE_ >= 2))                                                \
       hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO, ONE_, RES, RKV, SWI>), grid, block, LDS_, stream, \
                          wp, xp, yp, bias, colscale, M, N, K, iKB, kbw, pa);                                  \
   } while (0)

@@ -1451,6 +1451,51 @@ extern "C" int sqx_int4_linear_rowscale_sumsq(const uint8_t* wt, const float* st
   return SQX_OK;
 }
 
+extern "C" int sqx_int4_linear_swiglu(const uint8_t* wt, const float* st, const void* x, void* y, int64_t m,
+                                     int64_t rows, int64_t cols, int64_t group, sqx_stream_t stream) {
+  const char* fn = "sqx_int4_linear_swiglu";
+  SQX_REQUIRE(m >= 1 && m <= 64, SQX_E_ARG, "%s: 1..64 rows, m=%lld", fn, (long long)m);
+  SQX_REQUIRE(rows > 0 && rows % 16 == 0 && cols > 0 && rows < ((int64_t)1 << 31) && m * rows < ((int64_t)1 << 31),
+              SQX_E_ARG, "%s: rows=%lld: the gate / up pairs fill whole 16-row tiles", fn, (long long)rows);
+  SQX_REQUIRE(group == 32 || group == 64 || group == 128, SQX_E_ARG, "%s: group_size %lld unsupported (32, 64 or 128)",
+              fn, (long long)group);
+  SQX_REQUIRE(cols % group == 0, SQX_E_ARG, "in_features=%lld not divisible by group_size=%lld", (long long)cols,
+              (long long)group);
+  SQX_REQUIRE(wt && st && x && y, SQX_E_ARG, "%s: null pointer", fn);
+  SQX_REQUIRE(reinterpret_cast<uintptr_t>(wt) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, SQX_E_ARG,
+              "%s: the tiles and x must be 16-byte aligned", fn);
+  const hipStream_t s = as_stream(stream);
+  hipError_t e = hipErrorNotSupported;
+  if (m == 1) {
+    e = launch_int4_pro_res<kProPlain, false, true>(static_cast<int>(group), wt, st, static_cast<const uint16_t*>(x),
+                                                    static_cast<uint16_t*>(y), m, rows, cols, 0, s, ProArgs{});
+  } else {
+    SkinnyShape sh = skinny_default_shape(m, rows, cols, 128, false);
+    if (sh.variant == 2 || (sh.gemv && gemv_rows_fits(m, rows, cols))) {
+      e = launch_int4_rows_fused<kProPlain, false, false, true>(static_cast<int>(group), wt, st,
+                                                               static_cast<const uint16_t*>(x),
+                                                               static_cast<uint16_t*>(y), m, rows, cols, 0, s, ProArgs{});
+    } else {
+      if (sh.gemv || sh.variant == 2) sh = SkinnyShape{0, 2, 8, 1, false};
+      sh.S = 1;
+#define SQX_SWG(G_)                                                                                          \
+  {                                                                                                          \
+    using W = WInt4<G_, false, false>;                                                                       \
+    const typename W::Args a{wt, st, nullptr};                                                               \
+    e = skinny_launch<ActBF16, W>(a, static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), nullptr, m, \
+                                  rows, cols, sh, nullptr, 0, s, true, true);                                \
+  }
+      if (group == 128) SQX_SWG(128)
+      else if (group == 64) SQX_SWG(64)
+      else SQX_SWG(32)
+#undef SQX_SWG
+    }
+  }
+  SQX_REQUIRE(e == hipSuccess, SQX_E_HIP, "%s: m=%lld rows of %lld columns: launch failed: %s", fn, (long long)m,
+              (long long)cols, hipGetErrorString(e));
+  return SQX_OK;
+}
+
 extern "C" int sqx_int4_linear_rowscale_swiglu(const uint8_t* wt, const float* st, const void* hg, const float* ss,
                                              int64_t nss, float eps, void* y, int64_t m, int64_t rows, int64_t cols,
                                              int64_t group, int k_slices, sqx_stream_t stream) {

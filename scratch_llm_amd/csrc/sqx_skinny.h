@@ -15,6 +15,9 @@
 //    optionally, S workgroups split K further: each writes fp32 partials [S][M][N] to the caller's
 //    workspace and skinny_reduce_kernel adds them in split order. Deterministic for a given
 //    (R, waves, S).
+// The kernels' split_out argument: 0 writes bf16 y [M][N]; 1 the fp32 partials; 2 (no K split, N a
+// multiple of 16) SwiGLU pairs for a fused gate|up weight whose rows alternate in groups of 8: each
+// output rounded to bf16, then y [M][N / 2] = bf16(silu(g) * u) per pair, as the SiLU kernel does.
 //
 // Weight policies opt in with these members (WInt4 provides them):
 //   W::ctx_tiles(args, t0, nt, KB, lane)   buffer resources covering tiles t0 .. t0+nt-1 (loads of
@@ -243,6 +246,20 @@ __global__ __launch_bounds__((64 * skinny_max_waves(MCH, R, W::NG, W::kConstOffs
         const int l = (j >> 2) & 63;
         const int m = c * 16 + 4 * (l >> 4) + (j & 3);
         const int n = (t0 + r) * 16 + (l & 15);
+        if (split_out == 2) {  // SwiGLU pairs: output n's up row n + 8 is j ^ 32, in this wave and iteration
+          const bool ok = m < M && n < N;
+          float q = 0.0f;
+          if (ok) {
+            v *= W::out_scale(wa, n);
+            if (bias) v += A::to_f32(bias[n]);
+            q = A::to_f32(A::from_f32(v));
+          }
+          const float u = __shfl_xor(q, 32, 64);
+          if (ok && (l & 15) < 8)
+            static_cast<uint16_t*>(out)[(int64_t)m * (N / 2) + (t0 + r) * 8 + (l & 15)] =
+                static_cast<uint16_t>(A::pack_rne(silu_f32(q) * u, 0.0f));
+          continue;
+        }
         if (m < M && n < N) {
           if (split_out) {
             static_cast<float*>(out)[((int64_t)blockIdx.y * M + m) * N + n] = v;
@@ -515,6 +532,28 @@ __global__ __launch_bounds__(256 * KG) void skinny_lds_kernel(const typename W::
   }
 
   // yacc[r][c][j] is y[c*16 + 4(l >> 4) + j][(tw0 + r)*16 + (l & 15)]
+  if (split_out == 2) {  // SwiGLU pairs (N a multiple of 16): output n's up row n + 8 is lane ^ 8
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r >= nt) break;
+      const int nn = (tw0 + r) * 16 + nl;
+      const float os = W::out_scale(wa, nn);
+      const float bv = bias ? A::to_f32(bias[nn]) : 0.0f;
+#pragma unroll
+      for (int c = 0; c < MCH; ++c) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = c * 16 + 4 * jg + j;
+          const float q = A::to_f32(A::from_f32(yacc[r][c][j] * os + bv));
+          const float u = __shfl_xor(q, 8, 64);
+          if (m < M && nl < 8)
+            static_cast<uint16_t*>(out)[(int64_t)m * (N / 2) + (tw0 + r) * 8 + nl] =
+                static_cast<uint16_t>(A::pack_rne(silu_f32(q) * u, 0.0f));
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if (r >= nt) break;
@@ -674,7 +713,7 @@ inline int skinny_splits(int64_t KB, int S) {
 template <class A, class W>
 hipError_t skinny_lds_launch(const typename W::Args& wa, const uint16_t* x, uint16_t* y, const uint16_t* bias,
                              int64_t m, int64_t rows, int64_t cols, int R, int KG, int S, float* ws, int64_t ws_bytes,
-                             hipStream_t stream, bool reduce = true) {
+                             hipStream_t stream, bool reduce = true, bool swiglu = false) {
   constexpr int KBLK = W::KBLK;
   if (m < 1 || m > 64 || (R != 1 && R != 2 && R != 4) || (KG != 1 && KG != 2) || S < 1) return hipErrorInvalidValue;
   // per-group zero points with two or four groups per block hold more parameters per tile: fewer
@@ -694,6 +733,8 @@ hipError_t skinny_lds_launch(const typename W::Args& wa, const uint16_t* x, uint
   S = static_cast<int>(ceil_div(KB, kbs));
   const bool split = S > 1;
   if (split && (ws == nullptr || ws_bytes < skinny_workspace_bytes(m, rows, S))) return hipErrorInvalidValue;
+  if (swiglu && (split || rows % 16 != 0)) return hipErrorInvalidValue;  // the pairs need whole tiles, one pass
+  const int mode = split ? 1 : (swiglu ? 2 : 0);
   const dim3 grid(static_cast<unsigned>(ceil_div(T, 4 * R)), static_cast<unsigned>(S));
   const size_t lds = static_cast<size_t>(KG) * mch * 16 * 256;  // times the kernel's stage count
   void* o = split ? static_cast<void*>(ws) : static_cast<void*>(y);
@@ -704,11 +745,11 @@ hipError_t skinny_lds_launch(const typename W::Args& wa, const uint16_t* x, uint
     if (KG == 1)                                                                                                    \
       hipLaunchKernelGGL((skinny_lds_kernel<A, W, MCH_, R_, skinny_ring<R_>(), 1>), grid, dim3(256),              \
                          lds * (skinny_stages<MCH_, R_, skinny_ring<R_>(), 1, W::kLoads>()), stream, wa, x, o,     \
-                         bias, M, N, K, iKB, iT, kbs, split ? 1 : 0);                                              \
+                         bias, M, N, K, iKB, iT, kbs, mode);                                                       \
     else                                                                                                            \
       hipLaunchKernelGGL((skinny_lds_kernel<A, W, MCH_, R_, skinny_ring<R_>(), 2>), grid, dim3(512),              \
                          lds * (skinny_stages<MCH_, R_, skinny_ring<R_>(), 2, W::kLoads>()), stream, wa, x, o,     \
-                         bias, M, N, K, iKB, iT, kbs, split ? 1 : 0);                                              \
+                         bias, M, N, K, iKB, iT, kbs, mode);                                                       \
   } while (0)
   if (mch == 1) {
     if (R == 1) SQX_SL(1, 1);
@@ -739,12 +780,12 @@ template <class A, class W>
 // consumer adds them in split order as skinny_reduce_kernel does.
 hipError_t skinny_launch(const typename W::Args& wa, const uint16_t* x, uint16_t* y, const uint16_t* bias, int64_t m,
                          int64_t rows, int64_t cols, SkinnyShape sh, float* ws, int64_t ws_bytes, hipStream_t stream,
-                         bool reduce = true) {
+                         bool reduce = true, bool swiglu = false) {
   constexpr int KBLK = W::KBLK;
   if (sh.variant == 1) {
     if constexpr (KBLK == 128 && !has_row_scale<W>::value)
       return skinny_lds_launch<A, W>(wa, x, y, bias, m, rows, cols, sh.R, sh.waves / 4, sh.S, ws, ws_bytes, stream,
-                                     reduce);
+                                     reduce, swiglu);
     else
       return hipErrorInvalidValue;
   }
@@ -766,6 +807,7 @@ hipError_t skinny_launch(const typename W::Args& wa, const uint16_t* x, uint16_t
   nw = static_cast<int>(ceil_div(kbs, kbw));
   const bool split = S > 1;
   if (split && (ws == nullptr || ws_bytes < skinny_workspace_bytes(m, rows, S))) return hipErrorInvalidValue;
+  if (swiglu && (split || rows % 16 != 0 || has_row_scale<W>::value)) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(ceil_div(T, sh.R)), static_cast<unsigned>(S));
   const dim3 block(static_cast<unsigned>(64 * nw));
   const size_t lds = static_cast<size_t>(nw) * mch * 64 * sizeof(f32x4_t);
@@ -774,7 +816,7 @@ hipError_t skinny_launch(const typename W::Args& wa, const uint16_t* x, uint16_t
             iT = static_cast<int>(T);
 #define SQX_SK(MCH_, R_)                                                                                            \
   hipLaunchKernelGGL((skinny_kernel<A, W, MCH_, R_>), grid, block, lds, stream, wa, x, o, bias, M, N, K, iKB, iT, kbs, \
-                     kbw, split ? 1 : 0)
+                     kbw, split ? 1 : (swiglu ? 2 : 0))
   if (mch == 1) {
     if (sh.R == 2) SQX_SK(1, 2); else SQX_SK(1, 4);
   } else if (mch == 2) {

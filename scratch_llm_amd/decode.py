@@ -349,27 +349,35 @@ class Int4DecodeLM:
         return st.delta.data_ptr(), 0
 
     def _norm_linear(self, st: DecodeState, cur: int, delta: int | None, gain: Tensor, tw: i4.Int4Tiled, y: Tensor,
-                     stream: int, splits: int = 0) -> int:
+                     stream: int, splits: int = 0, swiglu: bool = False) -> int:
         """RMSNorm of the residual stream (after adding ``delta`` when given: a bf16 row, or with
         ``splits`` >= 2 the fp32 partials of a K-split linear) feeding ``tw``; returns the index of the
         buffer that holds the residual stream afterwards. Small batches run it as one kernel when
         ``fuse_norm`` is set (the norm computed in the linear's LDS copy of the activations), otherwise
-        as two."""
+        as two. ``swiglu``: ``tw`` is the fused gate|up weight and ``y`` [B, d_ff] receives
+        bf16(silu(g) * u), formed in the linear's epilogue up to 64 rows."""
         cfg, lib, B, d = self.cfg, _lib.load(), st.batch, self.cfg.d_model
         nxt = cur if delta is None else 1 - cur
         h_out = None if delta is None else st.x[nxt].data_ptr()
-        if splits >= 2:
-            _lib.check(lib.sqx_rmsnorm_partials(st.x[cur].data_ptr(), delta, splits, gain.data_ptr(), cfg.norm_eps, B, d,
-                                                h_out, st.h.data_ptr(), stream), "rmsnorm (partials)")
-            self._linear(st, tw, st.h, y, stream)
-        elif self.fuse_norm and lib.sqx_int4_prologue_fits(B, d):
+        lin_out = st.gu if swiglu else y
+        if self.fuse_norm and splits < 2 and lib.sqx_int4_prologue_fits(B, d):
             _lib.check(lib.sqx_int4_linear_rmsnorm(
                 tw.wt.data_ptr(), tw.st.data_ptr(), st.x[cur].data_ptr(), delta, gain.data_ptr(), cfg.norm_eps, h_out,
-                y.data_ptr(), B, tw.rows, tw.cols, tw.group_size, 0, stream), "rmsnorm + int4 linear")
+                lin_out.data_ptr(), B, tw.rows, tw.cols, tw.group_size, 0, stream), "rmsnorm + int4 linear")
         else:
-            _lib.check(lib.sqx_rmsnorm(st.x[cur].data_ptr(), delta, gain.data_ptr(), cfg.norm_eps, B, d, h_out,
-                                       st.h.data_ptr(), stream), "rmsnorm")
-            self._linear(st, tw, st.h, y, stream)
+            if splits >= 2:
+                _lib.check(lib.sqx_rmsnorm_partials(st.x[cur].data_ptr(), delta, splits, gain.data_ptr(), cfg.norm_eps,
+                                                    B, d, h_out, st.h.data_ptr(), stream), "rmsnorm (partials)")
+            else:
+                _lib.check(lib.sqx_rmsnorm(st.x[cur].data_ptr(), delta, gain.data_ptr(), cfg.norm_eps, B, d, h_out,
+                                           st.h.data_ptr(), stream), "rmsnorm")
+            if swiglu and B <= _SKINNY_MAX_M:
+                _lib.check(lib.sqx_int4_linear_swiglu(tw.wt.data_ptr(), tw.st.data_ptr(), st.h.data_ptr(), y.data_ptr(),
+                                                      B, tw.rows, tw.cols, tw.group_size, stream), "gate|up + silu * up")
+                return nxt
+            self._linear(st, tw, st.h, lin_out, stream)
+        if swiglu:
+            _lib.check(lib.sqx_silu_mul_pairs8(st.gu.data_ptr(), B, cfg.d_ff, y.data_ptr(), stream), "silu_mul")
         return nxt
 
     def _norm_sums_linear(self, st: DecodeState, tw: i4.Int4Tiled, y: Tensor, stream: int) -> None:
@@ -512,11 +520,10 @@ class Int4DecodeLM:
                 else:
                     delta, dsplit = self._delta_plan(st, ly.wo)
                 if go("gate_up"):
-                    cur = self._norm_linear(st, cur, delta, ly.ffn_norm, ly.w13, st.gu, s, dsplit)
+                    cur = self._norm_linear(st, cur, delta, ly.ffn_norm, ly.w13, st.act, s, dsplit, swiglu=True)
                 else:
                     cur = cur if delta is None else 1 - cur
                 if go("down"):
-                    ck(lib.sqx_silu_mul_pairs8(st.gu.data_ptr(), B, cfg.d_ff, st.act.data_ptr(), s), "silu_mul")
                     delta, dsplit = self._delta_linear(st, ly.w2, st.act, s)
                 else:
                     delta, dsplit = self._delta_plan(st, ly.w2)

@@ -492,6 +492,38 @@ def test_rowscale_swiglu_equals_two_calls(lib, dff, k, m):
     assert torch.equal(got, want), f"{k}->{n} m={m}: epilogue != two calls"
 
 
+@pytest.mark.parametrize("dff,k,m", [(14336, 4096, 1), (14336, 4096, 2), (14336, 4096, 8), (14336, 4096, 16),
+                                      (14336, 4096, 33), (14336, 4096, 64), (1024, 1024, 3), (1024, 1024, 20)])
+def test_linear_swiglu_equals_two_calls(lib, dff, k, m):
+    """sqx_int4_linear_swiglu == the library's linear for the shape (sqx_int4_linear at one row,
+    sqx_int4_skinny without a workspace above) followed by sqx_silu_mul_pairs8, bit for bit: the
+    one-row GEMV, the multi-row GEMV and both row-tiled kernels at the Llama gate/up shape."""
+    from scratch_llm_amd import _lib
+    from scratch_llm_amd.quant import int4_group as i4
+
+    print_case("linear swiglu", dff, k, m)
+    gen = torch.Generator(device=DEV).manual_seed(dff + k + m)
+    q, sc = i4.quantize_groupwise_int4(torch.randn(2 * dff, k, generator=gen, device=DEV) * 0.05, 128)
+    tw = i4.tile_int4(q, sc, None, 128)
+    x = torch.randn(m, k, generator=gen, device=DEV).to(torch.bfloat16)
+    n = 2 * dff
+    gu = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    want = torch.empty(m, dff, dtype=torch.bfloat16, device=DEV)
+    got = torch.empty(m, dff, dtype=torch.bfloat16, device=DEV)
+    if m == 1:
+        _ok(lib, lib.sqx_int4_linear(tw.wt.data_ptr(), tw.st.data_ptr(), None, _lib.DTYPE_F32, x.data_ptr(),
+                                     _lib.DTYPE_BF16, gu.data_ptr(), None, 1, n, k, 128, 0, _s()))
+    else:
+        _ok(lib, lib.sqx_int4_skinny(tw.wt.data_ptr(), tw.st.data_ptr(), None, _lib.DTYPE_F32, x.data_ptr(),
+                                     _lib.DTYPE_BF16, gu.data_ptr(), None, m, n, k, 128, -1, 0, 0, 0, None, 0, _s()))
+    _ok(lib, lib.sqx_silu_mul_pairs8(gu.data_ptr(), m, dff, want.data_ptr(), _s()))
+    _ok(lib, lib.sqx_int4_linear_swiglu(tw.wt.data_ptr(), tw.st.data_ptr(), x.data_ptr(), got.data_ptr(), m, n, k,
+                                        128, _s()))
+    torch.cuda.synchronize()
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(got, want), f"{k}->{n} m={m}: epilogue != two calls"
+
+
 def test_rowscale_swiglu_refuses(lib):
     """Rows that are not whole 16-row tiles, or more rows than the fused forms take, are refused."""
     rc = lib.sqx_int4_linear_rowscale_swiglu(None, None, None, None, 64, 1e-5, None, 1, 1000, 1024, 128, 0, None)
