@@ -10,6 +10,7 @@
 // scale of lane L's 32 columns; NVFP4 128 bytes, bytes 2L and 2L+1 the E4M3 scales of lane L's two
 // 16-column halves. Padding rows / columns hold code 0 and scale byte 0.
 #include "sqx_gemv.h"
+#include "sqx_mx.h"
 
 #include <float.h>
 
@@ -19,48 +20,11 @@ namespace sqx {
 // Codecs (nvfp4_mxfp4.py:85-174)
 // ----------------------------------------------------------------------------------------------
 __device__ __constant__ float kFp4Mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
-static constexpr float kTiny = 1e-30f;  // _TINY
-
-// e2m1_round_to_code (:85-98): the first index of the smallest fp32 distance |a - m| over the eight
-// magnitudes (torch.argmin), so exact midpoints go to the lower magnitude and inputs whose distances
-// all round equal (above ~2**25, infinities) and NaN take index 0; sign bit = x < 0.
-__device__ inline uint32_t e2m1_code_argmin(float x) {
-  const float a = fabsf(x);
-  uint32_t idx = 0;
-  float best = a;
-#pragma unroll
-  for (int i = 1; i < 8; ++i) {
-    const float d = fabsf(a - kFp4Mag[i]);
-    if (d < best) {
-      best = d;
-      idx = static_cast<uint32_t>(i);
-    }
-  }
-  return (x < 0.0f ? 8u : 0u) | idx;
-}
-
-// The same code in ~10 instructions instead of ~28. Below 2**22 every distance |a - m| is exact in
-// fp32 (a and the magnitudes are multiples of a's ulp), so the first minimum is the number of
-// midpoints between consecutive magnitudes (0.25 0.75 1.25 1.75 2.5 3.5 5) strictly below a, found
-// by a three-level comparison; larger inputs, infinities and NaN take the argmin above. Checked
-// equal to e2m1_code_argmin on all 2**32 fp32 bit patterns.
-__device__ inline uint32_t e2m1_code(float x) {
-  const float a = fabsf(x);
-  if (!(a < 4194304.0f)) return e2m1_code_argmin(x);
-  const bool hi = a > 1.75f;
-  const bool b1 = a > (hi ? 3.5f : 0.75f);
-  const bool b0 = a > (hi ? (b1 ? 5.0f : 2.5f) : (b1 ? 1.25f : 0.25f));
-  return (x < 0.0f ? 8u : 0u) | (hi ? 4u : 0u) | (b1 ? 2u : 0u) | (b0 ? 1u : 0u);
-}
 
 __device__ inline float e2m1_value(uint32_t c) {
   const float m = kFp4Mag[c & 7u];
   return (c & 8u) ? -m : m;
 }
-
-// fp32 log2 correctly rounded (double log2, one rounding): what torch's CPU log2 returns for the
-// reference's inputs (pinned by golden vectors at and around every power of two in range).
-__device__ inline float log2_f32(float v) { return static_cast<float>(log2(static_cast<double>(v))); }
 
 // quantize_e4m3 (:135-147): nearest E4M3 value, half to even, binade exponent clamped to [-6, 8]
 // (subnormal step 2**-9), saturating at 448, non-positive and NaN -> 0. floor(log2 v) is taken from
@@ -94,23 +58,6 @@ __device__ inline float quantize_e8m0(float v) {
   float e = __builtin_rintf(log2_f32(c));
   e = fminf(fmaxf(e, -127.0f), 127.0f);
   return v > 0.0f ? ldexpf(1.0f, static_cast<int>(e)) : 0.0f;
-}
-
-// _e8m0_no_overflow_scale (:162-174) as an exponent: clamp(ceil(log2(max(amax/6, 1e-30))), +-127).
-// The 1e-30 floor makes the exponent >= -99, so the reference's later clamp_min(1e-30) of 2**e is a
-// no-op. NaN amax gives a NaN scale (returned as exponent 128).
-__device__ inline int mx_exponent(float amax) {
-  float t = __fdiv_rn(amax, 6.0f);
-  if (t < kTiny) t = kTiny;
-  if (t != t) return 128;
-  const float e = fminf(fmaxf(ceilf(log2_f32(t)), -127.0f), 127.0f);
-  return static_cast<int>(e);
-}
-
-// NaN-propagating max of |v| (torch amax propagates NaN).
-__device__ inline float amax_step(float m, float v) {
-  const float a = fabsf(v);
-  return (a > m || a != a) ? a : m;
 }
 
 // ----------------------------------------------------------------------------------------------
@@ -289,17 +236,9 @@ __global__ __launch_bounds__(256) void mxfp4_fake_quant_rows_kernel(const void* 
 #pragma unroll
   for (int e = 0; e < 32; ++e) amax = amax_step(amax, v[e]);
   const int ex = mx_exponent(amax);
-  const float inv = ex == 128 ? __builtin_nanf("") : ldexpf(1.0f, -ex);
-  const float sc = ex == 128 ? __builtin_nanf("") : ldexpf(1.0f, ex);
-  constexpr float kMag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
   uint32_t o[16];
 #pragma unroll
-  for (int e = 0; e < 32; e += 2) {
-    const uint32_t c0 = e2m1_code(v[e] * inv), c1 = e2m1_code(v[e + 1] * inv);
-    const float d0 = (c0 & 8u ? -kMag[c0 & 7u] : kMag[c0 & 7u]) * sc;
-    const float d1 = (c1 & 8u ? -kMag[c1 & 7u] : kMag[c1 & 7u]) * sc;
-    o[e >> 1] = static_cast<uint32_t>(f32_to_bf16_bits(d0)) | (static_cast<uint32_t>(f32_to_bf16_bits(d1)) << 16);
-  }
+  for (int e = 0; e < 32; e += 2) o[e >> 1] = mx_fake_pair(v[e], v[e + 1], ex);
   u32x4_t* q = reinterpret_cast<u32x4_t*>(out + base);
 #pragma unroll
   for (int j = 0; j < 4; ++j) q[j] = u32x4_t{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
