@@ -158,6 +158,27 @@ def test_mxfp4_scale_edges_golden(f4, ref_vectors):
     assert q.codes[:, :5].reshape(-1).cpu().tolist() == g["codes_head"]
 
 
+def test_mxfp4_scale_mantissa_sweep(f4):
+    """The block exponent takes the correctly rounded fp32 log2 only when amax / 6 has a mantissa of
+    1..63 and reads the float's exponent otherwise: blocks whose amax / 6 lands on every mantissa
+    0..80 and the top 80 below the next power of two, at exponents -99..127, against the oracle's
+    log2 form (E8M0 scales and codes)."""
+    e = np.arange(-99, 128, dtype=np.int64)
+    m = np.concatenate([np.arange(0, 81), np.arange(2**23 - 80, 2**23)]).astype(np.int64)
+    t = (((e[:, None] + 127) << 23) | m[None, :]).astype(np.uint32).view(np.float32).reshape(-1)
+    with np.errstate(over="ignore"):  # the top binade's amax overflows and is dropped
+        amax = (t.astype(np.float64) * 6.0).astype(np.float32)  # amax / 6 rounds to t or a neighbour of it
+    amax = amax[np.isfinite(amax)]
+    x = np.zeros((amax.size, 32), np.float32)
+    x[:, 0] = amax
+    x[:, 1] = -amax * np.float32(0.3)
+    print_case("mxfp4 scale mantissa sweep", amax.size)
+    q = f4.mxfp4_quantize(dev(x), 32)
+    codes, s_block, _, _, _ = R.mxfp4_quantize(x, 32)
+    assert np.array_equal(bits(q.s_block.cpu().numpy()), bits(s_block))
+    assert np.array_equal(q.codes.cpu().numpy(), codes)
+
+
 @pytest.mark.parametrize("shape,block", [((64, 256), 16), ((1024, 48), 16), ((33, 96), 32), ((999,), 16)])
 def test_nvfp4_quantize_bitexact(f4, shape, block):
     print_case("nvfp4 quantize", shape, block)
