@@ -843,7 +843,7 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
 //    second MFMA chain per block of the general path. Lane (nl, jg) holds outputs of rows 4 jg + j
 //    (j < 4) for weight row nl, so rows 0..3 sit in lane group 0 and rows 4..7 in lane group 1.
 //  * The wave partials are summed through LDS in wave order (deterministic for a given wave count).
-// MR (4 or 8) is the largest M a build takes; XW the largest nx (k-slices of up to 4 XW blocks).
+// MR (2, 4 or 8) is the largest M a build takes; XW the largest nx (k-slices of up to 4 XW blocks).
 // The decode step's fusions of the one-row form, per row (layouts [M][...] row after row):
 //   PRO = kProSiluGate  x is the fused gate|up activation [M, 2K]; each wave forms bf16(silu(g) * u)
 //                       of its slice on the way into LDS, as the standalone SiLU kernel does;
@@ -868,12 +868,12 @@ __global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args 
                                                          uint16_t* __restrict__ y_, const uint16_t* __restrict__ bias,
                                                          int M_, int N, int K, int KB, int kbw, const ProArgs pa_) {
   static_assert(has_sum_offset<W>::value && W::KBLK == 128 && W::STEPS == 4, "int4 tiles: 128-column blocks");
-  static_assert(MR == 4 || MR == 8, "4 or 8 rows");
+  static_assert(MR == 2 || MR == 4 || MR == 8, "2, 4 or 8 rows");
   static_assert(PRO == kProPlain || PRO == kProSiluGate || PRO == kProScaleSum, "plain rows, SiLU gate or row factor");
   static_assert(!(RES && RKV) && !(SWI && (RES || RKV)), "one epilogue");
   static_assert(RG == 1 || (RG == 2 && MR == 4), "two groups of four rows");
   constexpr int KBLK = 128, U = 4, NG = kNgOf<W>, CPB = 4, CPG = CPB / NG, MPG = 4 / NG;
-  constexpr int kJ = 16 * MR;  // epilogue threads: output j = (lane l = j / 4, element e = j % 4)
+  constexpr int kJ = 16 * (MR < 4 ? 4 : MR);  // epilogue threads: output j = (lane l = j / 4, element e = j % 4)
   constexpr int RS = PRO == kProSiluGate ? 2 : 1;  // activation row stride in units of K
   extern __shared__ f32x4_t smem[];  // [NW][64] partial accumulators, then each wave's activation rows
   const int lane = threadIdx.x & 63;
@@ -1046,6 +1046,7 @@ __global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args 
           const float off = W::template offset<A>(p[u], g), sc = W::scale(p[u], g);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
+            if (j >= MR) break;  // rows past a two-row build (their outputs are dropped)
             // the group's sum of row j (and of row 4 + j for lane group 1), a wave-uniform value
             float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
@@ -1162,7 +1163,7 @@ inline int gemv_rows_default_waves(int64_t rows, int64_t cols) {
 // LDS bytes of the multi-row form for a launch of nw waves over k-slices of kbw blocks (dynamic, plus
 // the row factor's sums in the kProScaleSum form).
 inline size_t gemv_rows_lds_bytes(int64_t m, int nw, int kbw, bool scale_sum = false) {
-  const int MR = m <= 4 ? 4 : 8;
+  const int MR = m <= 2 ? 2 : (m <= 4 ? 4 : 8);
   const int nx = (kbw * 16 + 63) / 64;
   return static_cast<size_t>(nw) * 64 * sizeof(f32x4_t) + static_cast<size_t>(nw) * MR * (nx * 512 + 32) * 2 +
          (scale_sum ? static_cast<size_t>(MR) * (kNormSumMax + 1) * 4 : 0);
@@ -1213,7 +1214,8 @@ hipError_t gemv_rows_launch(const typename W::Args& wa, const uint16_t* x, uint1
   const int kbw = static_cast<int>(ceil_div(KB, nw));
   nw = static_cast<int>(ceil_div(KB, kbw));
   const bool eight = m > 4 && rgs == 1;
-  const size_t lds = gemv_rows_lds_bytes(eight ? 8 : 4, nw, kbw);  // the row factor's sums are static LDS
+  const bool two = m <= 2 && rgs == 1;  // the two-row build: 92-96 VGPRs against 104-112, half the LDS slice
+  const size_t lds = gemv_rows_lds_bytes(eight ? 8 : (two ? 2 : 4), nw, kbw);  // the row factor's sums are static LDS
   const dim3 block(static_cast<unsigned>(64 * nw));
   const int M = static_cast<int>(m), N = static_cast<int>(rows), K = static_cast<int>(cols), iKB = static_cast<int>(KB);
   // columns at or past K (a k tail) read zero through the row resources, so the padded blocks need no
@@ -1223,6 +1225,9 @@ hipError_t gemv_rows_launch(const typename W::Args& wa, const uint16_t* x, uint1
     hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 2, PRO, RES, RKV, 2, SWI>),
                        dim3(static_cast<unsigned>(ceil_div(T, 8) * 16)), block, lds, stream, wa, x, y, bias, M, N, K, iKB,
                        kbw, pa);
+  else if (two)
+    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 2, 2, PRO, RES, RKV, 1, SWI>), dim3(static_cast<unsigned>(T)), block, lds,
+                       stream, wa, x, y, bias, M, N, K, iKB, kbw, pa);
   else if (!eight)
     hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 2, PRO, RES, RKV, 1, SWI>), dim3(static_cast<unsigned>(T)), block, lds,
                        stream, wa, x, y, bias, M, N, K, iKB, kbw, pa);
