@@ -863,7 +863,7 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
 // the same tile: the hardware hands workgroups to the eight XCDs in turn, so both run on one XCD and
 // the second finds the tile's weights in that XCD's L2 (the grid covers whole groups of 8 tiles).
 template <class A, class W, int MR, int XW, int PRO = kProPlain, bool RES = false, bool RKV = false, int RG = 1,
-          bool SWI = false>
+          bool SWI = false, bool R1 = false>
 __global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args wa, const uint16_t* __restrict__ x_,
                                                          uint16_t* __restrict__ y_, const uint16_t* __restrict__ bias,
                                                          int M_, int N, int K, int KB, int kbw, const ProArgs pa_) {
@@ -1008,9 +1008,12 @@ __global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args 
       if (kr + u < kb1) W::load(wc, kr + u, wo[u], po[u]);  // wave-uniform condition
   };
   for (int kb = kb0; kb < kb1; kb += U) {
-    u32x4_t wn[U];
-    typename W::P pn[U];
-    if (kb + U < kb1) load_round(kb + U, wn, pn);
+    // R1: every wave's k-slice is a single round (kbw <= 4), so no next round is held in registers
+    [[maybe_unused]] u32x4_t wn[R1 ? 1 : U];
+    [[maybe_unused]] typename W::P pn[R1 ? 1 : U];
+    if constexpr (!R1) {
+      if (kb + U < kb1) load_round(kb + U, wn, pn);
+    }
     // the round's chunk sums per row: A row c = chunk c % 4 of block c / 4 (lane l gets the chunk sums
     // of block l >> 4)
     f32x4_t cs[MR];
@@ -1063,10 +1066,14 @@ __global__ __launch_bounds__(1024) void gemv_rows_kernel(const typename W::Args 
         }
       }
     }
+    if constexpr (R1) {
+      break;
+    } else {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      w[u] = wn[u];
-      p[u] = pn[u];
+      for (int u = 0; u < U; ++u) {
+        w[u] = wn[u];
+        p[u] = pn[u];
+      }
     }
   }
 
@@ -1189,12 +1196,14 @@ inline int gemv_rows_groups(int64_t m, int64_t rows, int64_t cols, int nw = 0, b
   const bool eight = kbw <= 4 && nw >= 2 && gemv_rows_lds_bytes(8, nw, kbw, scale_sum) <= 160 * 1024;
   if (groups == 1) return eight ? 1 : 0;
   if (groups == 2) return four ? 2 : 0;
-  // the library's choice. Two groups only on small grids: with rotating weights at 6 / 8 rows,
-  // 4096->1024 (64 tiles) 5.04 -> 4.41 us, but 4096->28672 17.3 / 18.1 -> 25.6 / 26.6 us, 14336->4096
-  // (where eight rows do not fit) 18.1 us against 15.6 us for the row-tiled kernel: the second
-  // workgroup of a tile does not find the weights in L2 often enough on larger grids.
-  if (four && ceil_div(rows, 16) <= 64) return 2;
-  return eight ? 1 : 0;
+  // the library's choice: eight rows in one workgroup where they fit (its single-round build, at
+  // most 97 VGPRs, beat two groups of four on 4096->1024 at 6 / 8 rows: 4.39 / 4.42 -> 4.16 / 4.32 us
+  // with rotating weights), else two groups on small grids only: 4096->28672 at 6 / 8 rows took
+  // 24.9 / 26.5 us in two groups, and 14336->4096 (where eight rows do not fit) 17.6 us against
+  // 12.3 us on the row-tiled kernel, as the second workgroup of a tile does not find the weights in
+  // L2 often enough on larger grids.
+  if (eight) return 1;
+  return (four && ceil_div(rows, 16) <= 64) ? 2 : 0;
 }
 
 inline bool gemv_rows_fits(int64_t m, int64_t rows, int64_t cols, int nw = 0, bool scale_sum = false) {
@@ -1225,15 +1234,21 @@ hipError_t gemv_rows_launch(const typename W::Args& wa, const uint16_t* x, uint1
     hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 2, PRO, RES, RKV, 2, SWI>),
                        dim3(static_cast<unsigned>(ceil_div(T, 8) * 16)), block, lds, stream, wa, x, y, bias, M, N, K, iKB,
                        kbw, pa);
+  else if (two && kbw <= 4)
+    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 2, 1, PRO, RES, RKV, 1, SWI, true>), dim3(static_cast<unsigned>(T)), block,
+                       lds, stream, wa, x, y, bias, M, N, K, iKB, kbw, pa);
   else if (two)
     hipLaunchKernelGGL((gemv_rows_kernel<A, W, 2, 2, PRO, RES, RKV, 1, SWI>), dim3(static_cast<unsigned>(T)), block, lds,
                        stream, wa, x, y, bias, M, N, K, iKB, kbw, pa);
+  else if (!eight && kbw <= 4)
+    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 1, PRO, RES, RKV, 1, SWI, true>), dim3(static_cast<unsigned>(T)), block,
+                       lds, stream, wa, x, y, bias, M, N, K, iKB, kbw, pa);
   else if (!eight)
     hipLaunchKernelGGL((gemv_rows_kernel<A, W, 4, 2, PRO, RES, RKV, 1, SWI>), dim3(static_cast<unsigned>(T)), block, lds,
                        stream, wa, x, y, bias, M, N, K, iKB, kbw, pa);
   else
-    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 8, 1, PRO, RES, RKV, 1, SWI>), dim3(static_cast<unsigned>(T)), block, lds,
-                       stream, wa, x, y, bias, M, N, K, iKB, kbw, pa);
+    hipLaunchKernelGGL((gemv_rows_kernel<A, W, 8, 1, PRO, RES, RKV, 1, SWI, true>), dim3(static_cast<unsigned>(T)), block,
+                       lds, stream, wa, x, y, bias, M, N, K, iKB, kbw, pa);
   return hipGetLastError();
 }
 

@@ -655,13 +655,16 @@ inline SkinnyShape skinny_default_shape(int64_t m, int64_t rows, int64_t cols, i
   };
   if (m <= 1) {
     s.gemv = true;
-  } else if (m <= 8 && kblk == 128 && gemv_rows_fits(m, rows, cols) &&
-             (T <= 384 || (m <= 4 && T <= 512) || (m == 2 && T < 4096))) {
+  } else if (m <= 8 && kblk == 128 && gemv_rows_fits(m, rows, cols) && (T <= 384 || m <= 4)) {
     // the multi-row GEMV (rotating weights, asymmetric bf16 parameters, M = 2 / 4 / 8 against the
     // kernels below): 4096^2 5.13 / 5.30 / 5.84 -> 4.64 / 4.80 / 5.59 us, 4096->1024 4.33 / 4.65 / 5.18 ->
     // 3.94 / 4.14 / 5.12 us, 14336->4096 13.64 / 12.05 -> 10.29 / 10.45 us (M = 2 / 4), 4096->6144
-    // 6.69 / 6.78 / 6.89 -> 5.41 / 5.81 / 6.74 us; 4096->14336 (896 tiles) 9.79 -> 9.33 us at M = 2 only,
-    // 4096->28672 15.66 -> 15.13 us at M = 2 only
+    // 6.69 / 6.78 / 6.89 -> 5.41 / 5.81 / 6.74 us. Its single-round builds (k-slices of at most four
+    // blocks: 60-74 VGPRs at 2..4 rows) also take the large grids at 2..4 rows (the row-tiled kernels
+    // these grids took before -> the multi-row GEMV): 4096->28672 (symmetric) at M = 3 / 4 16.1 / 15.9
+    // -> 13.5 / 13.8 us, 4096->128256 at M = 2 / 3 / 4 52.3 / 52.0 / 52.8 -> 43.2 / 46.7 / 50.6 us,
+    // 4096->14336 (asymmetric) at M = 3 / 4 9.6 / 9.7 -> 9.1 / 8.8 us; at 5..8 rows the row-tiled
+    // kernel stays ahead on them.
     s = SkinnyShape{2, 0, 0, 1, false};
   } else if (m <= 16) {
     // (sweep of the LDS-staged shapes at M = 16 / 32 / 48 / 64, symmetric int4, rotating weights:
