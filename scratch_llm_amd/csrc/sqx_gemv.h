@@ -156,7 +156,7 @@ struct ProArgs {
 };
 
 template <class A, class W, int MCH, int U, bool KTAIL, bool XLDS, bool YF32, int PRO = kProPlain, int ONE = 0,
-          bool RES = false, bool RKV = false, bool SWI = false>
+          bool RES = false, bool RKV = false, bool SWI = false, bool R1 = false>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ? 8 : 1))) void gemv_kernel(const typename W::Args wa, const uint16_t* __restrict__ x,
                                                     void* __restrict__ yv, const uint16_t* __restrict__ bias,
                                                     const float* __restrict__ colscale, int M, int N, int K, int KB,
@@ -509,9 +509,12 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
         }
       }
     }
-    u32x4_t wn[U];
-    typename W::P pn[U];
-    if (kb + U < kb1) load_round(kb + U, wn, pn);
+    // R1: every wave's k-slice is a single round (kbw <= U), so no next round is held in registers
+    [[maybe_unused]] u32x4_t wn[R1 ? 1 : U];
+    [[maybe_unused]] typename W::P pn[R1 ? 1 : U];
+    if constexpr (!R1) {
+      if (kb + U < kb1) load_round(kb + U, wn, pn);
+    }
     // ONE: activation sums of the round's blocks. With CPB chunks of 32 columns per block, row
     // r = CPB*b + c of the MFMA holds chunk c of block kb + b; lane l receives rows 4(l >> 4) .. +3,
     // i.e. the chunk sums of block u at lane group CPB*u/4, elements CPB*u%4 onward.
@@ -571,10 +574,14 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
         }
       }
     }
+    if constexpr (R1) {
+      break;
+    } else {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      w[u] = wn[u];
-      p[u] = pn[u];
+      for (int u = 0; u < U; ++u) {
+        w[u] = wn[u];
+        p[u] = pn[u];
+      }
     }
   }
 
@@ -753,11 +760,17 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     const size_t red = static_cast<size_t>(nw) * mch * 64 * sizeof(f32x4_t);
     const bool xlds = mch == 1 && gemv_xlds_bytes(M, KB, KBLK) <= kXldsMax;
     if (colscale != nullptr && !xlds) return hipErrorNotSupported;  // column scaling happens in the LDS copy
+// the one-row forms have a single-round build (R1) for k-slices of at most one round
 #define SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, ONE_)                                                              \
   do {                                                                                                        \
-    if constexpr ((!RKV || ONE_ == 2) && (!SWI || ONE_ >= 2))                                                \
-      hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO, ONE_, RES, RKV, SWI>), grid, block, LDS_, stream, \
-                         wp, xp, yp, bias, colscale, M, N, K, iKB, kbw, pa);                                  \
+    if constexpr ((!RKV || ONE_ == 2) && (!SWI || ONE_ >= 2)) {                                              \
+      if (ONE_ >= 2 && kbw <= U_)                                                                             \
+        hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO, ONE_, RES, RKV, SWI, (ONE_ >= 2)>), grid, \
+                           block, LDS_, stream, wp, xp, yp, bias, colscale, M, N, K, iKB, kbw, pa);           \
+      else                                                                                                    \
+        hipLaunchKernelGGL((gemv_kernel<A, W, MCH_, U_, KT_, XL_, YF32, PRO, ONE_, RES, RKV, SWI>), grid, block, LDS_, \
+                           stream, wp, xp, yp, bias, colscale, M, N, K, iKB, kbw, pa);                        \
+    }                                                                                                         \
   } while (0)
 #define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_) SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, 0)
     // the one-row form for formats whose offset costs sum(x) per group: 2 = each wave loads its own
