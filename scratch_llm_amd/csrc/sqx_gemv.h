@@ -55,16 +55,16 @@ inline int64_t gemv_xlds_bytes(int64_t m, int64_t KB, int kblk = 128) { return m
 inline int gemv_mch(int64_t m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
 
 // Waves per tile the library picks. One row (the one-row forms): one round of four k-blocks per
-// wave, at most 16 waves, and 4 waves beyond 2048 tiles (measured on the Llama shapes: int4
-// 4096->1024 3.71 -> 3.40 us and 4096x4096 4.28 -> 4.18 us at 8 waves instead of 16, MXFP4
-// 8192->28672 25.7 -> 22.3 us and 28672->8192 28.5 -> 26.0 us at 16 instead of 8; the others
-// unchanged). More rows: 16 for up to 256 tiles, 8 up to 2048 tiles, 4 beyond. At least 2 blocks
-// per wave either way.
+// wave, at most 16 waves (measured on the Llama shapes: int4 4096->1024 3.71 -> 3.40 us and
+// 4096x4096 4.28 -> 4.18 us at 8 waves instead of 16, MXFP4 8192->28672 25.7 -> 22.3 us and
+// 28672->8192 28.5 -> 26.0 us at 16 instead of 8; the others unchanged; with the single-round
+// builds the int4 lm_head 4096->128256, 8016 tiles, 45.2 -> 44.2 us at 8 waves instead of 4). More
+// rows: 16 for up to 256 tiles, 8 up to 2048 tiles, 4 beyond. At least 2 blocks per wave either way.
 inline int gemv_default_kslices(int64_t rows, int64_t cols, int kblk = 128, int64_t m = 2) {
   const int64_t T = ceil_div(rows, 16);
   const int64_t KB = ceil_div(cols, kblk);
   int64_t s = T <= 256 ? 16 : (T <= 2048 ? 8 : 4);
-  if (m == 1 && T <= 2048) s = std::min<int64_t>(16, std::max<int64_t>(1, KB / 4));
+  if (m == 1) s = std::min<int64_t>(16, std::max<int64_t>(1, KB / 4));
   int64_t cap = KB / 2;
   if (cap < 1) cap = 1;
   if (s > cap) s = cap;
