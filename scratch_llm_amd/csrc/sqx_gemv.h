@@ -162,7 +162,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
                                                     const float* __restrict__ colscale, int M, int N, int K, int KB,
                                                     int kbw, const ProArgs pa) {
   static_assert(PRO == kProPlain || (XLDS && MCH == 1), "activation prologues need the LDS copy");
-  static_assert(ONE == 0 || (XLDS && MCH == 1 && U == 4), "the one-row form reads four-block rounds from LDS");
+  static_assert(ONE == 0 || (XLDS && MCH == 1 && (U == 4 || U == 8)), "the one-row form reads rounds of four or eight blocks from LDS");
   static_assert(ONE < 2 || PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate || PRO == kProScaleSum ||
                     PRO == kProAttnCombine,
                 "a prologue over the whole row needs the workgroup's copy of the activations");
@@ -515,29 +515,37 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
     if constexpr (!R1) {
       if (kb + U < kb1) load_round(kb + U, wn, pn);
     }
-    // ONE: activation sums of the round's blocks. With CPB chunks of 32 columns per block, row
-    // r = CPB*b + c of the MFMA holds chunk c of block kb + b; lane l receives rows 4(l >> 4) .. +3,
-    // i.e. the chunk sums of block u at lane group CPB*u/4, elements CPB*u%4 onward.
+    // ONE: activation sums of the round's blocks. With CPB chunks of 32 columns per block, one MFMA
+    // covers 16 chunks: row r = CPB*b + c of MFMA h holds chunk c of block kb + 16h/CPB + b; lane l
+    // receives rows 4(l >> 4) .. +3, i.e. the chunk sums of block u at lane group (CPB*u % 16)/4,
+    // elements CPB*u%4 onward, of MFMA CPB*u/16.
     constexpr int CPB = KBLK / 32;
-    static_assert(ONE == 0 || (CPB * U <= 16 && 4 % CPB == 0), "a round's chunks fill the 16 MFMA rows");
+    constexpr int NH = (CPB * U + 15) / 16;  // MFMAs for the round's chunk sums
+    static_assert(ONE == 0 || ((CPB * U <= 16 || (CPB * U) % 16 == 0) && 4 % CPB == 0),
+                  "a round's chunks fill whole 16-row MFMAs");
     [[maybe_unused]] float sig[U][ONE ? kNgOf<W> : 1];
     if constexpr (ONE != 0 && has_sum_offset<W>::value) {
-      const int r = lane & 15, b = r / CPB;
       const uint16_t* xrow = ONE >= 2 ? xwave + (kb - kb0) * KBLK : xs + kb * KBLK;
-      u32x4_t a2 = u32x4_t{0u, 0u, 0u, 0u};
-      if (b < U && kb + b < kb1) a2 = *reinterpret_cast<const u32x4_t*>(xrow + b * KBLK + 32 * (r % CPB) + 8 * jg);
       const uint32_t one = A::pair_from_f32(1.0f);
-      const f32x4_t cs = A::mfma(a2, u32x4_t{one, one, one, one}, f32x4_t{0.f, 0.f, 0.f, 0.f});
+      f32x4_t cs[NH];
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        const int r = lane & 15, b = 16 * h / CPB + r / CPB;
+        u32x4_t a2 = u32x4_t{0u, 0u, 0u, 0u};
+        if (b < U && kb + b < kb1) a2 = *reinterpret_cast<const u32x4_t*>(xrow + b * KBLK + 32 * (r % CPB) + 8 * jg);
+        cs[h] = A::mfma(a2, u32x4_t{one, one, one, one}, f32x4_t{0.f, 0.f, 0.f, 0.f});
+      }
       constexpr int NG = kNgOf<W>;
       constexpr int CPG = CPB / NG;  // chunks per group
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
+          const int h = (CPB * u) / 16, uu = (CPB * u) % 16;
           float v = 0.0f;
 #pragma unroll
-          for (int i = 0; i < CPG; ++i) v += cs[(CPB * u) % 4 + g * CPG + i];
-          sig[u][g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * ((CPB * u) / 4)));
+          for (int i = 0; i < CPG; ++i) v += cs[h][uu % 4 + g * CPG + i];
+          sig[u][g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * (uu / 4)));
         }
     }
 #pragma unroll
@@ -773,6 +781,13 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     }                                                                                                         \
   } while (0)
 #define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_) SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, 0)
+// the one-row form 2 in a single round of eight blocks (int4 tiles, 5..8 blocks a wave)
+#define SQX_GEMV8(KT_, LDS_)                                                                                   \
+  do {                                                                                                        \
+    if constexpr (has_sum_offset<W>::value)                                                                   \
+      hipLaunchKernelGGL((gemv_kernel<A, W, 1, 2 * U1, KT_, true, YF32, PRO, 2, RES, RKV, SWI, true>), grid, block, \
+                         LDS_, stream, wp, xp, yp, bias, colscale, M, N, K, iKB, kbw, pa);                    \
+  } while (0)
     // the one-row form for formats whose offset costs sum(x) per group: 2 = each wave loads its own
     // k-slice of the activations, 1 = from the workgroup's LDS copy (prologues, column scales)
     // Formats without the sum offset (FP4, FP8) take the per-wave slice form only (their plain MFMA
@@ -805,6 +820,9 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
           if constexpr (PRO == kProPlain || PRO == kProScaleSum) {
             if (kbw <= U1 && T > 1024) {  // one round per wave, several rounds of workgroups
               if (ktail) SQX_GEMV1(1, U1, true, true, lds, 3); else SQX_GEMV1(1, U1, false, true, lds, 3);
+            } else if (has_sum_offset<W>::value && kbw > U1 && kbw <= 2 * U1) {
+              // 5..8 blocks a wave (the 14336-column down projection): one round of eight blocks
+              if (ktail) SQX_GEMV8(true, lds); else SQX_GEMV8(false, lds);
             } else {
               if (ktail) SQX_GEMV1(1, U1, true, true, lds, 2); else SQX_GEMV1(1, U1, false, true, lds, 2);
             }
@@ -834,6 +852,7 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     }
 #undef SQX_GEMV
 #undef SQX_GEMV1
+#undef SQX_GEMV8
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
