@@ -164,7 +164,8 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(ONE == 3 ?
                                                     const float* __restrict__ colscale, int M, int N, int K, int KB,
                                                     int kbw, const ProArgs pa) {
   static_assert(PRO == kProPlain || (XLDS && MCH == 1), "activation prologues need the LDS copy");
-  static_assert(ONE == 0 || (XLDS && MCH == 1 && (U == 4 || U == 8)), "the one-row form reads rounds of four or eight blocks from LDS");
+  static_assert(ONE == 0 || (XLDS && MCH == 1 && (U == 4 || U == 8 || (U == 16 && !has_sum_offset<W>::value))),
+                "the one-row form reads rounds of 4 or 8 blocks (16 without the sum offset) from LDS");
   static_assert(ONE < 2 || PRO == kProPlain || PRO == kProNormSum || PRO == kProSiluGate || PRO == kProScaleSum ||
                     PRO == kProAttnCombine,
                 "a prologue over the whole row needs the workgroup's copy of the activations");
@@ -783,13 +784,11 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     }                                                                                                         \
   } while (0)
 #define SQX_GEMV(MCH_, U_, KT_, XL_, LDS_) SQX_GEMV1(MCH_, U_, KT_, XL_, LDS_, 0)
-// the one-row form 2 in a single round of eight blocks (int4 tiles, 5..8 blocks a wave)
-#define SQX_GEMV8(KT_, LDS_)                                                                                   \
-  do {                                                                                                        \
-    if constexpr (has_sum_offset<W>::value)                                                                   \
-      hipLaunchKernelGGL((gemv_kernel<A, W, 1, 2 * U1, KT_, true, YF32, PRO, 2, RES, RKV, SWI, true>), grid, block, \
-                         LDS_, stream, wp, xp, yp, bias, colscale, M, N, K, iKB, kbw, pa);                    \
-  } while (0)
+// the one-row form 2 in a single round of U_ blocks (int4 tiles: 8 for 5..8 blocks a wave; formats
+// without the sum offset: 16 for 9..16 blocks a wave)
+#define SQX_GEMVU(U_, KT_, LDS_)                                                                               \
+  hipLaunchKernelGGL((gemv_kernel<A, W, 1, U_, KT_, true, YF32, PRO, 2, RES, RKV, SWI, true>), grid, block, LDS_, \
+                     stream, wp, xp, yp, bias, colscale, M, N, K, iKB, kbw, pa)
     // the one-row form for formats whose offset costs sum(x) per group: 2 = each wave loads its own
     // k-slice of the activations, 1 = from the workgroup's LDS copy (prologues, column scales)
     // Formats without the sum offset (FP4, FP8) take the per-wave slice form only (their plain MFMA
@@ -822,9 +821,16 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
           if constexpr (PRO == kProPlain || PRO == kProScaleSum) {
             if (kbw <= U1 && T > 1024) {  // one round per wave, several rounds of workgroups
               if (ktail) SQX_GEMV1(1, U1, true, true, lds, 3); else SQX_GEMV1(1, U1, false, true, lds, 3);
-            } else if (has_sum_offset<W>::value && kbw > U1 && kbw <= 2 * U1) {
+            } else if (kbw > U1 && kbw <= 2 * U1 && has_sum_offset<W>::value) {
               // 5..8 blocks a wave (the 14336-column down projection): one round of eight blocks
-              if (ktail) SQX_GEMV8(true, lds); else SQX_GEMV8(false, lds);
+              if constexpr (has_sum_offset<W>::value) {
+                if (ktail) SQX_GEMVU(2 * U1, true, lds); else SQX_GEMVU(2 * U1, false, lds);
+              }
+            } else if (kbw > U1 && kbw <= 4 * U1 && !has_sum_offset<W>::value && PRO == kProPlain && !RES) {
+              // FP4 / FP8 waves of 5..16 blocks (MXFP4 28672->8192: 14): one round of sixteen
+              if constexpr (!has_sum_offset<W>::value && PRO == kProPlain && !RES) {
+                if (ktail) SQX_GEMVU(4 * U1, true, lds); else SQX_GEMVU(4 * U1, false, lds);
+              }
             } else {
               if (ktail) SQX_GEMV1(1, U1, true, true, lds, 2); else SQX_GEMV1(1, U1, false, true, lds, 2);
             }
@@ -854,7 +860,7 @@ hipError_t gemv_launch(const typename W::Args& wa, const uint16_t* x, void* y, c
     }
 #undef SQX_GEMV
 #undef SQX_GEMV1
-#undef SQX_GEMV8
+#undef SQX_GEMVU
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
