@@ -32,7 +32,8 @@
 //    blocks by one MFMA whose 16 A rows hold the round's 16 chunks of 32 activations (against a
 //    B of ones; two MFMAs for a round of eight blocks), instead of an MFMA chain per block against
 //    the constant offset. R1: waves whose k-slice is a single round keep no registers for a next
-//    round (int4 waves of five to eight blocks run one round of eight). ONE = 2 also
+//    round (int4 waves of five to eight blocks run one round of eight, FP4 / FP8 waves of nine to
+//    sixteen one round of sixteen). ONE = 2 also
 //    drops the workgroup's copy of the activations: each wave loads only its own k-slice (issued
 //    before its weights) into its own LDS area, so no workgroup barrier precedes the MFMAs; the SiLU
 //    gate and the norm from tile sums (kProNormSum) are applied to that slice on the way in. ONE = 3
