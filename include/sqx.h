@@ -683,7 +683,9 @@ int64_t sqx_attn_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t tmax
 /* One-token GQA attention over the slot cache (MultiHeadSelfAttention.forward's SlotKVCache branch,
  * model.py:281-305 and :313-349): out[b, h] = softmax(q[b,h] k[b,h/G]^T / sqrt(hd)) v[b,h/G] over the
  * keys j <= lengths[b] (G = H / Hkv in {1, 2, 4, 8}; hd == 128). out: bf16 [B, H * hd]. Split over
- * the keys into fp32 partials in ws (sqx_attn_workspace_bytes) and combined in a second launch. */
+ * the keys into fp32 partials in ws (sqx_attn_workspace_bytes) and combined in a second launch; with
+ * one chunk per row (sqx_attn_chunk >= tmax, as when B * Hkv >= 256) one launch writes out, with the
+ * bits the combine of that single chunk would give. */
 int sqx_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* lengths,
                          int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws,
                          int64_t ws_bytes, sqx_stream_t stream);

@@ -193,7 +193,7 @@ def test_config5_full_width_against_oracle(B):
     context 2048 with 2046 random cached keys per row) for two steps against the decode oracle's bf16
     composition and fp32 run on 8192 sampled logits; the second layer reads the first's residual sums
     at B = 1. At B = 32 and 64 the step runs every row (the row-tiled linears, K-split partials folded
-    into the norms, 1024-key attention chunks) and the oracle follows 8 sampled rows (rows do not
+    into the norms, one attention chunk per row) and the oracle follows 8 sampled rows (rows do not
     interact). Codes of the quantized weights are bit-exact with the oracle quantizer on sampled rows,
     and the oracle dequantizes the same codes."""
     from scratch_llm_amd.decode import LLAMA3_8B, Int4DecodeLM

@@ -197,6 +197,65 @@ def test_attention_config5_context(lib, B):
     _attn_case(lib, B, 32, 8, T, lengths, seed=B)
 
 
+@pytest.mark.parametrize("B,H,Hkv,T,kv8", [(32, 32, 8, 3000, False), (16, 32, 16, 2500, True)])
+def test_attention_one_chunk_long_context(lib, B, H, Hkv, T, kv8):
+    """With B * Hkv >= 256 each (row, kv head) takes all its keys as one chunk and the partial kernel
+    writes the output itself (no combine launch): within the attention bound of float64 at contexts
+    past the multi-chunk walks' 1024 keys, bf16 and E4M3 caches, ragged lengths (0, chunk-walk
+    boundaries, T - 1, a full slot), with NaN in every cache row past a row's length."""
+    from oracle import fp8_ref as F8
+
+    print_case("attention one chunk", B, H, Hkv, T, kv8)
+    assert B * Hkv >= 256 and lib.sqx_attn_chunk(B, Hkv, T) >= T
+    hd, G = 128, H // Hkv
+    g = torch.Generator().manual_seed(B + T)
+    lengths = torch.randint(0, T, (B,), generator=g).tolist()
+    lengths[:6] = [T - 1, 0, 1023, 1024, 2047, T + 5]
+    q = (torch.randn(B, H, hd, generator=g) * 2).bfloat16()
+    if kv8:
+        k, v = _valid_codes((B, Hkv, T, hd), g), _valid_codes((B, Hkv, T, hd), g)
+        ks = torch.rand(Hkv, generator=g) * 0.01 + 0.001
+        vs = torch.rand(Hkv, generator=g) * 0.01 + 0.001
+    else:
+        k = (torch.randn(B, Hkv, T, hd, generator=g) * 2).bfloat16()
+        v = torch.randn(B, Hkv, T, hd, generator=g).bfloat16()
+    for b, n in enumerate(lengths):  # never read: NaN there would reach the output
+        if kv8:
+            k[b, :, n + 1:] = 0x7F
+            v[b, :, n + 1:] = 0x7F
+        else:
+            k[b, :, n + 1:] = float("nan")
+            v[b, :, n + 1:] = float("nan")
+    out = torch.full((B, H * hd), float("nan"), dtype=torch.bfloat16, device=DEV)
+    nb = lib.sqx_attn_workspace_bytes(B, H, Hkv, T)
+    ws = torch.empty(nb // 4, dtype=torch.float32, device=DEV)
+    ln = torch.tensor(lengths, dtype=torch.int32, device=DEV)
+    kd, vd = k.to(DEV), v.to(DEV)
+    if kv8:
+        ksd, vsd = ks.to(DEV), vs.to(DEV)
+        _ok(lib, lib.sqx_decode_attention_fp8kv(q.to(DEV).data_ptr(), kd.data_ptr(), vd.data_ptr(), ksd.data_ptr(),
+                                                vsd.data_ptr(), ln.data_ptr(), B, H, Hkv, hd, T, out.data_ptr(),
+                                                ws.data_ptr(), nb, _s()))
+    else:
+        _ok(lib, lib.sqx_decode_attention(q.to(DEV).data_ptr(), kd.data_ptr(), vd.data_ptr(), ln.data_ptr(), B, H, Hkv,
+                                          hd, T, out.data_ptr(), ws.data_ptr(), nb, _s()))
+    torch.cuda.synchronize()
+    got = out.cpu().view(B, H, hd).double()
+    assert torch.isfinite(got).all()
+    for b in range(B):
+        L = min(lengths[b] + 1, T)
+        if kv8:
+            kk = torch.from_numpy(F8.e4m3_decode(k[b, :, :L].numpy())).double() * ks.double().view(Hkv, 1, 1)
+            vv = torch.from_numpy(F8.e4m3_decode(v[b, :, :L].numpy())).double() * vs.double().view(Hkv, 1, 1)
+        else:
+            kk, vv = k[b, :, :L].double(), v[b, :, :L].double()
+        kk, vv = kk.repeat_interleave(G, dim=0), vv.repeat_interleave(G, dim=0)
+        p = torch.softmax(torch.einsum("hd,htd->ht", q[b].double(), kk) / math.sqrt(hd), dim=-1)
+        want = torch.einsum("ht,htd->hd", p, vv)
+        bound = 2.0**-8 * want.abs() + 1e-5 * vv.abs().max()
+        assert float(((got[b] - want).abs() / bound).max()) <= 1.0, f"row {b} (L={L})"
+
+
 @pytest.mark.parametrize("B,H,Hkv,T", [(5, 32, 8, 300), (1, 32, 8, 2048), (3, 16, 16, 64), (64, 32, 8, 2048)])
 def test_fused_rope_attention_equals_two_calls(lib, B, H, Hkv, T):
     """sqx_decode_attention_rope == sqx_rope_kv then sqx_decode_attention, bit for bit (output and cache),
