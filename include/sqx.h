@@ -721,8 +721,8 @@ int sqx_attn_partials_combine(const void* ws, const int* lengths, int64_t B, int
  * the reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). The key-split partials go to a fixed 8 MiB device array
  * inside the library (one per GPU, held until the process ends), so the shape must satisfy
- * sqx_attn_workspace_bytes(B, H, Hkv, tmax) <= 8 MiB (e.g. B = 64, H = 32, Hkv = 8, tmax = 2048
- * needs 4.3 MB); larger shapes return SQX_E_SPACE without launching. The stream's device must be the
+ * sqx_attn_workspace_bytes(B, H, Hkv, tmax) <= 8 MiB (e.g. B = 16, H = 32, Hkv = 8, tmax = 2048
+ * needs 0.5 MB, B = 64 with one key chunk per row 1.1 MB); larger shapes return SQX_E_SPACE without launching. The stream's device must be the
  * current device. Calls that overlap on one GPU share that array and race; calls in one stream are
  * ordered. Other arguments and results as sqx_decode_attention_rope, bit for bit. */
 int sqx_decode_attention_rope_noalloc(const void* qkv, const int* lengths, const float* cos_t, const float* sin_t,
@@ -742,6 +742,19 @@ int sqx_decode_attention_rope_fp8kv(const void* qkv, const int* lengths, const f
                                     int64_t rope_rows, void* k_codes, void* v_codes, const float* k_scale,
                                     const float* v_scale, int64_t B, int64_t H, int64_t Hkv, int64_t hd,
                                     int64_t tmax, void* out, void* ws, int64_t ws_bytes, sqx_stream_t stream);
+
+/* sqx_decode_attention_rope (k_scale == v_scale == NULL) or sqx_decode_attention_rope_fp8kv (both
+ * given) with the q|k|v rows given as the fp32 partials of a K-split projection (MultiHeadSelfAttention's
+ * fused qkv projection, model.py:313-320, run by sqx_int4_skinny_partials): qkv_parts fp32
+ * [splits][B][(H + 2 Hkv) hd], 16-byte aligned, 1 <= splits <= 64. Each row value is the partials
+ * added in split order and rounded to bf16, the bits sqx_int4_skinny's reduce writes, so the result
+ * (output and cache) equals that reduce followed by the bf16-row call, bit for bit, in one launch
+ * fewer. */
+int sqx_decode_attention_rope_parts(const float* qkv_parts, int64_t splits, const int* lengths, const float* cos_t,
+                                    const float* sin_t, int64_t rope_rows, void* k_cache, void* v_cache,
+                                    const float* k_scale, const float* v_scale, int64_t B, int64_t H, int64_t Hkv,
+                                    int64_t hd, int64_t tmax, void* out, void* ws, int64_t ws_bytes,
+                                    sqx_stream_t stream);
 
 /* SwiGLU's gate (model.py:227-237): out = bf16(silu(g) * u) from gate_up = bf16 [B, 2F] laid out
  * [g | u] (the w1 and w3 outputs side by side); out: bf16 [B, F]. */

@@ -205,7 +205,12 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p,
          _c_i64, _c_p],
     ),
-    "sqx_silu_mul": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "sqx_decode_attention_rope_parts": (
+        _c_i,
+        [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p,
+         _c_p, _c_i64, _c_p],
+    ),
+    "sqx_silu_mul":(_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_silu_mul_pairs8": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_embed": (_c_i, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "sqx_argmax_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),

@@ -12,6 +12,7 @@
 // is rounded to bf16 once (round to nearest even).
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "sqx_common.h"
 
@@ -260,7 +261,7 @@ __device__ inline u32x4_t e4m3x8_to_bf16(u32x2v_t c) {
 // holds value rows base + 4u + kl, each lane 8 dims, fp32 products and sums as above). This moves
 // the dot products and most of the softmax off the VALU, which bounds the kernel above at large
 // batch (every lane worked every head's scores, 4 fdot2 and 4 row reductions a key).
-template <int G, bool ROPE, bool KV8, int NWV>
+template <int G, bool ROPE, bool KV8, int NWV, bool QP = false>
 __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_partial_mfma_kernel(const uint16_t* __restrict__ q, uint8_t* __restrict__ kc,
                                                                 uint8_t* __restrict__ vc, const int* __restrict__ lengths,
                                                                 const float* __restrict__ cos_t,
@@ -269,7 +270,8 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
                                                                 const float* __restrict__ vscale, int rope_rows, int H,
                                                                 int Hkv, int tmax, int chunk, int nchunk, float qscale,
                                                                 float* __restrict__ po, float* __restrict__ pml,
-                                                                uint16_t* __restrict__ out) {
+                                                                uint16_t* __restrict__ out,
+                                                                const float* __restrict__ qpart, int qsplits) {
   static_assert(G >= 1 && G <= 16, "query heads are the 16 columns of the score tile");
   static_assert(NWV == 4 || NWV == 8, "4 or 8 waves per workgroup");
   using R = KvRow<KV8>;
@@ -328,30 +330,85 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
   const float ks = KV8 ? kscale[kh] : 1.0f;
   const float vs = KV8 ? vscale[kh] : 1.0f;
   const float qs = qscale * ks;
-  const uint16_t* qrow = q + static_cast<int64_t>(b) * (ROPE ? H + 2 * Hkv : H) * kHd;
+  const int width = (ROPE ? H + 2 * Hkv : H) * kHd;
+  const uint16_t* qrow = q + static_cast<int64_t>(b) * width;
+  // rows(cols, v): v[n] = the 8 consecutive values of the row from column cols[n], as bf16 pairs,
+  // every load issued before the first use. QP (with ROPE): the q|k|v row is the sum of the qsplits
+  // fp32 partials [S][B][width] of a K-split projection, added in split order and rounded to bf16 as
+  // skinny_reduce_kernel does (the bits that reduce writes); the first two partials load together
+  // with no branch between them (for S = 1 the second, read at stride 0, is dropped by a select), so
+  // up to two splits cost one round trip.
+  auto rows = [&](const auto& cols, auto& v) {
+    constexpr int N = std::extent<std::remove_reference_t<decltype(cols)>>::value;
+    if constexpr (!QP) {
+#pragma unroll
+      for (int n = 0; n < N; ++n) v[n] = *reinterpret_cast<const u32x4_t*>(qrow + cols[n]);
+    } else {
+      const int64_t stride = static_cast<int64_t>(gridDim.z) * width;
+      const float* p = qpart + static_cast<int64_t>(b) * width;
+      const bool two = qsplits > 1;
+      const float* p1 = p + (two ? stride : 0);
+      f32x4_t a[N][2], c[N][2];
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          a[n][h] = *reinterpret_cast<const f32x4_t*>(p + cols[n] + 4 * h);
+          c[n][h] = *reinterpret_cast<const f32x4_t*>(p1 + cols[n] + 4 * h);
+        }
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a[n][h][j] = two ? a[n][h][j] + c[n][h][j] : a[n][h][j];
+      for (int sp = 2; sp < qsplits; ++sp) {
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const f32x4_t d = *reinterpret_cast<const f32x4_t*>(p + sp * stride + cols[n] + 4 * h);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a[n][h][j] += d[j];
+          }
+      }
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4_t& x = a[n][j >> 1];
+          v[n][j] = static_cast<uint32_t>(f32_to_bf16_bits(x[2 * (j & 1)])) |
+                    (static_cast<uint32_t>(f32_to_bf16_bits(x[2 * (j & 1) + 1])) << 16);
+        }
+    }
+  };
   const int64_t pr = ROPE ? static_cast<int64_t>(min(len, rope_rows - 1)) * (kHd / 2) : 0;
   // the query heads as the B operand: lane l holds dims 32i + 8 kl .. +8 of head dl (zero past G)
   u32x4_t qv[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    u32x4_t v{0u, 0u, 0u, 0u};
-    if (dl < G) {
-      v = *reinterpret_cast<const u32x4_t*>(qrow + (kh * G + dl) * kHd + 32 * i + 8 * kl);
-      if constexpr (ROPE) {
-        float cs[4], sn[4];
+  for (int i = 0; i < 4; ++i) qv[i] = u32x4_t{0u, 0u, 0u, 0u};
+  if (dl < G) {
+    int cq[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cq[i] = (kh * G + dl) * kHd + 32 * i + 8 * kl;
+    rows(cq, qv);
+    if constexpr (ROPE) {
+      float cs[4][4], sn[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          cs[j] = cos_t[pr + 16 * i + 4 * kl + j];
-          sn[j] = sin_t[pr + 16 * i + 4 * kl + j];
+          cs[i][j] = cos_t[pr + 16 * i + 4 * kl + j];
+          sn[i][j] = sin_t[pr + 16 * i + 4 * kl + j];
         }
-        v = rope8(v, cs, sn);
-      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qv[i] = rope8(qv[i], cs[i], sn[i]);
     }
-    qv[i] = v;
   }
   // ROPE: the new key and value in the value layout (dims 8 dl .. +8); the workgroup holding the
-  // slot writes them to the cache; the value (kept in LDS) stands in for the slot row below
-  __shared__ Row vnew_lds[ROPE ? 16 : 1];
+  // slot writes them to the cache; the key and value (kept in LDS, the key as stored) stand in for
+  // the slot row below
+  __shared__ Row knew_lds[ROPE ? 16 : 1], vnew_lds[ROPE ? 16 : 1];
   if constexpr (ROPE) {
     float cs[4], sn[4];
 #pragma unroll
@@ -360,8 +417,11 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
       sn[j] = sin_t[pr + dl * 4 + j];
     }
     if (wave == 0 && kl == 0) {
-      const u32x4_t kb16 = rope8(*reinterpret_cast<const u32x4_t*>(qrow + (H + kh) * kHd + dl * 8), cs, sn);
-      const u32x4_t vb16 = *reinterpret_cast<const u32x4_t*>(qrow + (H + Hkv + kh) * kHd + dl * 8);
+      const int ckv[2] = {(H + kh) * kHd + dl * 8, (H + Hkv + kh) * kHd + dl * 8};
+      u32x4_t kv16[2];
+      rows(ckv, kv16);
+      const u32x4_t kb16 = rope8(kv16[0], cs, sn);
+      const u32x4_t vb16 = kv16[1];
       Row knew, vnew;
       if constexpr (KV8) {  // quantized with the head's scales, as the cache stores them
         knew = R::encode(kb16, ks);
@@ -370,6 +430,7 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
         knew = kb16;
         vnew = vb16;
       }
+      knew_lds[dl] = knew;
       vnew_lds[dl] = vnew;
       if (ch == slot / chunk) {  // one cache row each, from this workgroup only
         *reinterpret_cast<Row*>(kc + head_off + (static_cast<int64_t>(slot) * kHd + dl * 8) * ES) = knew;
@@ -407,18 +468,11 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
     }
     if constexpr (ROPE) {
       if (slot >= base && slot < base + kKeysPerStep) {  // wave-uniform: this step holds the new key
-        if (kk == slot) {
+        if (kk == slot) {  // dims 32 i + 8 kl .. +8 of the new key as stored (E4M3: the code, read back)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            float cs[4], sn[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              cs[j] = cos_t[pr + 16 * i + 4 * kl + j];
-              sn[j] = sin_t[pr + 16 * i + 4 * kl + j];
-            }
-            const u32x4_t k16 = rope8(*reinterpret_cast<const u32x4_t*>(qrow + (H + kh) * kHd + 32 * i + 8 * kl), cs, sn);
-            if constexpr (KV8) kf[i] = e4m3x8_to_bf16(R::encode(k16, ks));  // the stored code, read back
-            else kf[i] = k16;
+            if constexpr (KV8) kf[i] = e4m3x8_to_bf16(knew_lds[4 * i + kl]);
+            else kf[i] = knew_lds[4 * i + kl];
           }
         }
 #pragma unroll
@@ -875,7 +929,8 @@ extern "C" int64_t sqx_attn_partials_workspace_bytes(int64_t B, int64_t H, int64
 static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, const int* lengths, const float* cos_t,
                                  const float* sin_t, int64_t rope_rows, const float* kscale, const float* vscale,
                                  int64_t B, int64_t H, int64_t Hkv, int64_t hd, int64_t tmax, void* out, void* ws,
-                                 int64_t ws_bytes, sqx_stream_t stream, const char* fn, bool partials_only = false) {
+                                 int64_t ws_bytes, sqx_stream_t stream, const char* fn, bool partials_only = false,
+                                 const float* qpart = nullptr, int qsplits = 0) {
   const bool rope = cos_t != nullptr;
   const bool kv8 = kscale != nullptr;
   SQX_REQUIRE(!kv8 || vscale != nullptr, SQX_E_ARG, "%s: null V scale", fn);
@@ -916,25 +971,33 @@ static int decode_attention_impl(const void* q, void* k_cache, void* v_cache, co
     if (partials_only)                                                                                             \
       hipLaunchKernelGGL((attn_partial_mfma_kernel<G_, R_, K8_, kFoldWaves>), grid, dim3(kFoldWaves * 64), 0, s, qp, \
                          kp, vp, lengths, cos_t, sin_t, kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, po,  \
-                         pml, nullptr);                                                                            \
+                         pml, nullptr, nullptr, 0);                                                                \
     else                                                                                                           \
       hipLaunchKernelGGL((attn_partial_mfma_kernel<G_, R_, K8_, 4>), grid, dim3(256), 0, s, qp, kp, vp, lengths,    \
-                         cos_t, sin_t, kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, po, pml, direct);     \
+                         cos_t, sin_t, kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, po, pml, direct,      \
+                         nullptr, 0);                                                                              \
   } while (0)
-#define SQX_ATTN_MG(R_, K8_)                      \
+#define SQX_ATTN_MQ(G_, K8_)                                                                                        \
+  hipLaunchKernelGGL((attn_partial_mfma_kernel<G_, true, K8_, 4, true>), grid, dim3(256), 0, s, qp, kp, vp, lengths, \
+                     cos_t, sin_t, kscale, vscale, rr, iH, iK, iT, chunk, nchunk, qscale, po, pml, direct, qpart,     \
+                     qsplits)
+#define SQX_ATTN_MG(M_, ...)                      \
   switch (G) {                                    \
-    case 1: SQX_ATTN_M(1, R_, K8_); break;        \
-    case 2: SQX_ATTN_M(2, R_, K8_); break;        \
-    case 4: SQX_ATTN_M(4, R_, K8_); break;        \
-    default: SQX_ATTN_M(8, R_, K8_); break;       \
+    case 1: M_(1, __VA_ARGS__); break;            \
+    case 2: M_(2, __VA_ARGS__); break;            \
+    case 4: M_(4, __VA_ARGS__); break;            \
+    default: M_(8, __VA_ARGS__); break;           \
   }
   // scores on the matrix unit (E4M3 keys decoded to bf16 pairs on the way in)
-  if (rope) {
-    if (kv8) { SQX_ATTN_MG(true, true) } else { SQX_ATTN_MG(true, false) }
+  if (rope && qsplits > 0) {
+    if (kv8) { SQX_ATTN_MG(SQX_ATTN_MQ, true) } else { SQX_ATTN_MG(SQX_ATTN_MQ, false) }
+  } else if (rope) {
+    if (kv8) { SQX_ATTN_MG(SQX_ATTN_M, true, true) } else { SQX_ATTN_MG(SQX_ATTN_M, true, false) }
   } else {
-    if (kv8) { SQX_ATTN_MG(false, true) } else { SQX_ATTN_MG(false, false) }
+    if (kv8) { SQX_ATTN_MG(SQX_ATTN_M, false, true) } else { SQX_ATTN_MG(SQX_ATTN_M, false, false) }
   }
 #undef SQX_ATTN_MG
+#undef SQX_ATTN_MQ
 #undef SQX_ATTN_M
   SQX_LAUNCH_CHECK(fn);
   if (partials_only || direct != nullptr) return SQX_OK;
@@ -1050,6 +1113,23 @@ extern "C" int sqx_decode_attention_fp8kv(const void* q, const void* k_codes, co
   return decode_attention_impl(q, const_cast<void*>(k_codes), const_cast<void*>(v_codes), lengths, nullptr, nullptr, 0,
                                k_scale, v_scale, B, H, Hkv, hd, tmax, out, ws, ws_bytes, stream,
                                "sqx_decode_attention_fp8kv");
+}
+
+// sqx_decode_attention_rope[_fp8kv] reading the q|k|v rows as the fp32 partials of a K-split
+// projection (sqx_int4_skinny_partials), which it adds as that projection's reduce would.
+extern "C" int sqx_decode_attention_rope_parts(const float* qkv_parts, int64_t splits, const int* lengths,
+                                               const float* cos_t, const float* sin_t, int64_t rope_rows,
+                                               void* k_cache, void* v_cache, const float* k_scale,
+                                               const float* v_scale, int64_t B, int64_t H, int64_t Hkv, int64_t hd,
+                                               int64_t tmax, void* out, void* ws, int64_t ws_bytes,
+                                               sqx_stream_t stream) {
+  const char* fn = "sqx_decode_attention_rope_parts";
+  SQX_REQUIRE(cos_t != nullptr, SQX_E_ARG, "%s: null cos table", fn);
+  SQX_REQUIRE((k_scale == nullptr) == (v_scale == nullptr), SQX_E_ARG, "%s: give both scales or neither", fn);
+  SQX_REQUIRE(splits >= 1 && splits <= 64, SQX_E_ARG, "%s: %lld splits (1 to 64)", fn, (long long)splits);
+  return decode_attention_impl(qkv_parts, k_cache, v_cache, lengths, cos_t, sin_t, rope_rows, k_scale, v_scale, B, H,
+                               Hkv, hd, tmax, out, ws, ws_bytes, stream, fn, false, qkv_parts,
+                               static_cast<int>(splits));
 }
 
 extern "C" int sqx_decode_attention_rope_fp8kv(const void* qkv, const int* lengths, const float* cos_t,

@@ -219,6 +219,9 @@ class Int4DecodeLM:
         # Batched steps: when the o / down projection splits K, its fp32 partials go straight to the
         # next residual add + RMSNorm, which adds them in the linear's own order (no reduce launch).
         self.fuse_split_norm = True
+        # Batched steps: when the q|k|v projection splits K, the attention kernel adds its fp32 partials
+        # (in the projection's own order) as it loads q and the new key and value (no reduce launch).
+        self.fuse_qkv_parts = True
         # One-row steps, when set: attention leaves its key-chunk partials (at most 8 per head) and the
         # o projection merges them while it loads its activations (no combine launch). Off: every
         # o-projection workgroup merges every head, which cost more than the launch it saves.
@@ -349,18 +352,19 @@ class Int4DecodeLM:
         return st.delta.data_ptr(), 0
 
     def _norm_linear(self, st: DecodeState, cur: int, delta: int | None, gain: Tensor, tw: i4.Int4Tiled, y: Tensor,
-                     stream: int, splits: int = 0, swiglu: bool = False) -> int:
+                     stream: int, splits: int = 0, swiglu: bool = False, parts: bool = False) -> int:
         """RMSNorm of the residual stream (after adding ``delta`` when given: a bf16 row, or with
         ``splits`` >= 2 the fp32 partials of a K-split linear) feeding ``tw``; returns the index of the
         buffer that holds the residual stream afterwards. Small batches run it as one kernel when
         ``fuse_norm`` is set (the norm computed in the linear's LDS copy of the activations), otherwise
         as two. ``swiglu``: ``tw`` is the fused gate|up weight and ``y`` [B, d_ff] receives
-        bf16(silu(g) * u), formed in the linear's epilogue up to 64 rows."""
+        bf16(silu(g) * u), formed in the linear's epilogue up to 64 rows. ``parts``: the linear splits K
+        and leaves its fp32 partials in ``st.gemm_ws`` for the next kernel to add (``y`` unused)."""
         cfg, lib, B, d = self.cfg, _lib.load(), st.batch, self.cfg.d_model
         nxt = cur if delta is None else 1 - cur
         h_out = None if delta is None else st.x[nxt].data_ptr()
         lin_out = st.gu if swiglu else y
-        if self.fuse_norm and splits < 2 and lib.sqx_int4_prologue_fits(B, d):
+        if self.fuse_norm and splits < 2 and not parts and lib.sqx_int4_prologue_fits(B, d):
             _lib.check(lib.sqx_int4_linear_rmsnorm(
                 tw.wt.data_ptr(), tw.st.data_ptr(), st.x[cur].data_ptr(), delta, gain.data_ptr(), cfg.norm_eps, h_out,
                 lin_out.data_ptr(), B, tw.rows, tw.cols, tw.group_size, 0, stream), "rmsnorm + int4 linear")
@@ -374,6 +378,11 @@ class Int4DecodeLM:
             if swiglu and B <= _SKINNY_MAX_M:
                 _lib.check(lib.sqx_int4_linear_swiglu(tw.wt.data_ptr(), tw.st.data_ptr(), st.h.data_ptr(), y.data_ptr(),
                                                       B, tw.rows, tw.cols, tw.group_size, stream), "gate|up + silu * up")
+                return nxt
+            if parts:
+                _lib.check(lib.sqx_int4_skinny_partials(
+                    tw.wt.data_ptr(), tw.st.data_ptr(), None, _lib.DTYPE_F32, st.h.data_ptr(), _lib.DTYPE_BF16, B,
+                    tw.rows, tw.cols, tw.group_size, *_lib.ws_args(st.gemm_ws), stream), "int4 linear (partials)")
                 return nxt
             self._linear(st, tw, st.h, lin_out, stream)
         if swiglu:
@@ -439,6 +448,12 @@ class Int4DecodeLM:
         # k-blocks per wave)
         kb_o = d // 128
         merge = (self.fuse_attn_merge and sums and B == 1 and d % 256 == 0 and kb_o // 2 <= 16 and H * hd == d)
+        # a K-split q|k|v projection (the general step, B >= 48 at Llama-3-8B shapes) leaves its fp32
+        # partials and the attention kernel adds them as the projection's reduce would (no reduce launch)
+        qkv_split = 0
+        if not sums and self.fuse_qkv_parts and 2 <= B <= _SKINNY_MAX_M:
+            S = lib.sqx_int4_skinny_default_splits(B, qkv_rows, d)
+            qkv_split = S if S >= 2 else 0
         with torch.cuda.device(self.device):
             if go("other"):
                 ck(lib.sqx_embed(self.embed.data_ptr(), cfg.vocab_size, st.tokens.data_ptr(), B, d,
@@ -461,7 +476,8 @@ class Int4DecodeLM:
                     if go("qkv"):
                         self._norm_sums_linear(st, ly.wqkv, st.qkv, s)
                 elif go("qkv"):
-                    cur = self._norm_linear(st, cur, delta, ly.attn_norm, ly.wqkv, st.qkv, s, dsplit)
+                    cur = self._norm_linear(st, cur, delta, ly.attn_norm, ly.wqkv, st.qkv, s, dsplit,
+                                            parts=qkv_split > 0)
                 else:  # the residual stream advances as the norm's launch would have left it
                     cur = cur if delta is None else 1 - cur
                 # ---- attention over the cache
@@ -479,6 +495,14 @@ class Int4DecodeLM:
                     ck(lib.sqx_decode_attention(st.q.data_ptr(), st.k[li].data_ptr(), st.v[li].data_ptr(),
                                                 st.lengths.data_ptr(), B, H, Hkv, hd, T, st.attn.data_ptr(),
                                                 st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s), "attention")
+                elif qkv_split:
+                    fp8 = st.kv_dtype == "fp8"
+                    ck(lib.sqx_decode_attention_rope_parts(
+                        st.gemm_ws.data_ptr(), qkv_split, st.lengths.data_ptr(), self.cos.data_ptr(),
+                        self.sin.data_ptr(), cfg.context_length, st.k[li].data_ptr(), st.v[li].data_ptr(),
+                        st.k_scale[li].data_ptr() if fp8 else None, st.v_scale[li].data_ptr() if fp8 else None,
+                        B, H, Hkv, hd, T, st.attn.data_ptr(), st.attn_ws.data_ptr(), st.attn_ws.numel() * 4, s),
+                       "attention (q|k|v partials)")
                 elif st.kv_dtype == "fp8":
                     ck(lib.sqx_decode_attention_rope_fp8kv(
                         st.qkv.data_ptr(), st.lengths.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),

@@ -296,6 +296,69 @@ def test_fused_rope_attention_equals_two_calls(lib, B, H, Hkv, T):
     assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
 
 
+@pytest.mark.parametrize("B,T,S,kv8", [(5, 300, 2, False), (64, 2048, 2, False), (64, 2048, 2, True),
+                                       (9, 500, 3, True), (20, 100, 8, False)])
+def test_attention_rope_parts_equals_reduce_then_rope(lib, B, T, S, kv8):
+    """sqx_decode_attention_rope_parts == the S partials added in split order in fp32 and rounded to
+    bf16 (what sqx_int4_skinny's reduce writes), then sqx_decode_attention_rope[_fp8kv], bit for bit:
+    output and every cache byte, with one key chunk per row (B = 64) and several."""
+    print_case("rope attention from partials", B, T, S, kv8)
+    H, Hkv, hd, ctx = 32, 8, 128, T + 16
+    g = torch.Generator().manual_seed(B * 7 + T + S)
+    lengths = torch.randint(0, T, (B,), generator=g)
+    lengths[0], lengths[1], lengths[2] = T - 1, 0, T + 3
+    parts = torch.randn(S, B, (H + 2 * Hkv) * hd, generator=g) * 1.5
+    acc = parts[0].clone()
+    for s in range(1, S):
+        acc += parts[s]
+    qkv = acc.bfloat16().to(DEV)
+    if kv8:
+        cache = (_valid_codes((B, Hkv, T, hd), g), _valid_codes((B, Hkv, T, hd), g))
+        ksd = (torch.rand(Hkv, generator=g) * 0.02 + 0.002).to(DEV)
+        vsd = (torch.rand(Hkv, generator=g) * 0.02 + 0.002).to(DEV)
+    else:
+        cache = (torch.randn(B, Hkv, T, hd, generator=g).bfloat16(), torch.randn(B, Hkv, T, hd, generator=g).bfloat16())
+    cos, sin = (t.to(DEV) for t in D.rope_tables(hd, ctx, 10000.0))
+    ln = lengths.to(torch.int32).to(DEV)
+    pd = parts.to(DEV)
+    nb = lib.sqx_attn_workspace_bytes(B, H, Hkv, T)
+    ws = torch.empty(nb // 4, dtype=torch.float32, device=DEV)
+    outs, caches = [], []
+    for from_parts in (True, False):
+        kc, vc = cache[0].to(DEV), cache[1].to(DEV)
+        out = torch.empty(B, H * hd, dtype=torch.bfloat16, device=DEV)
+        if from_parts:
+            _ok(lib, lib.sqx_decode_attention_rope_parts(
+                pd.data_ptr(), S, ln.data_ptr(), cos.data_ptr(), sin.data_ptr(), ctx, kc.data_ptr(), vc.data_ptr(),
+                ksd.data_ptr() if kv8 else None, vsd.data_ptr() if kv8 else None, B, H, Hkv, hd, T, out.data_ptr(),
+                ws.data_ptr(), nb, _s()))
+        elif kv8:
+            _ok(lib, lib.sqx_decode_attention_rope_fp8kv(
+                qkv.data_ptr(), ln.data_ptr(), cos.data_ptr(), sin.data_ptr(), ctx, kc.data_ptr(), vc.data_ptr(),
+                ksd.data_ptr(), vsd.data_ptr(), B, H, Hkv, hd, T, out.data_ptr(), ws.data_ptr(), nb, _s()))
+        else:
+            _ok(lib, lib.sqx_decode_attention_rope(
+                qkv.data_ptr(), ln.data_ptr(), cos.data_ptr(), sin.data_ptr(), ctx, kc.data_ptr(), vc.data_ptr(), B, H,
+                Hkv, hd, T, out.data_ptr(), ws.data_ptr(), nb, _s()))
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+        caches.append((kc.cpu(), vc.cpu()))
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    for a, b in zip(caches[0], caches[1]):
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+
+
+def test_attention_rope_parts_refuses(lib):
+    """Split counts outside 1..64 and a missing scale of an E4M3 cache are refused before any launch."""
+    print_case("rope attention from partials refuses")
+    d = torch.zeros(64, dtype=torch.float32, device=DEV)
+    p = d.data_ptr()
+    for S, ks, vs in ((0, None, None), (65, None, None), (2, p, None)):
+        rc = lib.sqx_decode_attention_rope_parts(p, S, p, p, p, 64, p, p, ks, vs, 1, 32, 8, 128, 64, p, p, 1 << 20, _s())
+        assert rc != 0
+        assert "sqx_decode_attention_rope_parts" in lib.sqx_last_error().decode()
+
+
 def _tiled(n, k, group, seed):
     from scratch_llm_amd.quant import int4_group as i4
 
@@ -1000,31 +1063,34 @@ def test_fused_step_equals_unfused_step(small, B):
 
 @pytest.mark.parametrize("B", [20, 64])
 def test_split_partials_norm_step_equals_reduce_step(small, B):
-    """The K-split o / down partials added by the norm (no reduce launch) change no bit of the step:
-    at B = 20 both o and down split in the small model, at B = 64 down does."""
+    """The K-split o / down partials added by the norm and the q|k|v partials added by the attention
+    kernel (no reduce launches) change no bit of the step or the cache: at B = 20 o, down and q|k|v
+    split in the small model, at B = 64 down does."""
     from scratch_llm_amd import _lib
 
     model, _ = small
     lib = _lib.load()
     cfg = model.cfg
     splits = [lib.sqx_int4_skinny_default_splits(B, cfg.d_model, cfg.n_heads * cfg.head_dim),
-              lib.sqx_int4_skinny_default_splits(B, cfg.d_model, cfg.d_ff)]
+              lib.sqx_int4_skinny_default_splits(B, cfg.d_model, cfg.d_ff),
+              lib.sqx_int4_skinny_default_splits(B, (cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim, cfg.d_model)]
     assert max(splits) >= 2, splits
+    assert B != 20 or min(splits) >= 2, splits
     print_case("split partials norm step", B, splits)
     a, b = model.new_state(B, 32), model.new_state(B, 32)
     tok = torch.arange(B) * 31 % cfg.vocab_size
     try:
         for t in range(3):
-            model.fuse_split_norm = True
+            model.fuse_split_norm = model.fuse_qkv_parts = True
             model.step(a, tok if t == 0 else None)
-            model.fuse_split_norm = False
+            model.fuse_split_norm = model.fuse_qkv_parts = False
             model.step(b, tok if t == 0 else None)
             torch.cuda.synchronize()
             assert torch.equal(a.logits, b.logits), f"step {t}"
             assert torch.equal(a.tokens, b.tokens)
         assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
     finally:
-        model.fuse_split_norm = True
+        model.fuse_split_norm = model.fuse_qkv_parts = True
 
 
 def test_rmsnorm_partials_equals_reduce_then_norm(lib):
