@@ -315,21 +315,6 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
     const rsrc_t vt0 = make_rsrc(vc + head_off, static_cast<uint32_t>(tmax) * kHd * ES);
     load_block(kt0, vt0, min(t0 + chunk, tmax), ws, ka, va);
   }
-  const int len = max(lengths[b], 0);
-  const int L = min(len + 1, tmax);
-  const int slot = min(len, tmax - 1);
-  if (t0 >= L) return;  // the combine reads only chunks below L
-  const int we = min(t0 + chunk, L);
-
-  __shared__ float sm[NWV][G], sl[NWV][G];
-  __shared__ float so[NWV][G][kHd];
-  __shared__ __attribute__((aligned(16))) float sp[NWV][16][G < 4 ? 4 : G];  // per wave: p[key][head]
-  __shared__ __attribute__((aligned(16))) float sa[NWV][G < 4 ? 4 : G];      // per wave: the step's rescale
-
-  // E4M3 rows: the K scale folds into the query's scale, the V scale multiplies the partial
-  const float ks = KV8 ? kscale[kh] : 1.0f;
-  const float vs = KV8 ? vscale[kh] : 1.0f;
-  const float qs = qscale * ks;
   const int width = (ROPE ? H + 2 * Hkv : H) * kHd;
   const uint16_t* qrow = q + static_cast<int64_t>(b) * width;
   // rows(cols, v): v[n] = the 8 consecutive values of the row from column cols[n], as bf16 pairs,
@@ -382,8 +367,8 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
         }
     }
   };
-  const int64_t pr = ROPE ? static_cast<int64_t>(min(len, rope_rows - 1)) * (kHd / 2) : 0;
-  // the query heads as the B operand: lane l holds dims 32i + 8 kl .. +8 of head dl (zero past G)
+  // The query slices and (ROPE, wave 0) the new key and value rows are requested with the first block,
+  // before the row's length is known; only RoPE's tables depend on it.
   u32x4_t qv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) qv[i] = u32x4_t{0u, 0u, 0u, 0u};
@@ -392,6 +377,32 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
     for (int i = 0; i < 4; ++i) cq[i] = (kh * G + dl) * kHd + 32 * i + 8 * kl;
     rows(cq, qv);
+  }
+  [[maybe_unused]] u32x4_t kv16[2] = {u32x4_t{0u, 0u, 0u, 0u}, u32x4_t{0u, 0u, 0u, 0u}};
+  if constexpr (ROPE) {
+    if (wave == 0 && kl == 0) {
+      const int ckv[2] = {(H + kh) * kHd + dl * 8, (H + Hkv + kh) * kHd + dl * 8};
+      rows(ckv, kv16);
+    }
+  }
+  const int len = max(lengths[b], 0);
+  const int L = min(len + 1, tmax);
+  const int slot = min(len, tmax - 1);
+  if (t0 >= L) return;  // the combine reads only chunks below L
+  const int we = min(t0 + chunk, L);
+
+  __shared__ float sm[NWV][G], sl[NWV][G];
+  __shared__ float so[NWV][G][kHd];
+  __shared__ __attribute__((aligned(16))) float sp[NWV][16][G < 4 ? 4 : G];  // per wave: p[key][head]
+  __shared__ __attribute__((aligned(16))) float sa[NWV][G < 4 ? 4 : G];      // per wave: the step's rescale
+
+  // E4M3 rows: the K scale folds into the query's scale, the V scale multiplies the partial
+  const float ks = KV8 ? kscale[kh] : 1.0f;
+  const float vs = KV8 ? vscale[kh] : 1.0f;
+  const float qs = qscale * ks;
+  const int64_t pr = ROPE ? static_cast<int64_t>(min(len, rope_rows - 1)) * (kHd / 2) : 0;
+  // the query heads as the B operand: lane l holds dims 32i + 8 kl .. +8 of head dl (zero past G)
+  if (dl < G) {
     if constexpr (ROPE) {
       float cs[4][4], sn[4][4];
 #pragma unroll
@@ -417,9 +428,6 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2))) v
       sn[j] = sin_t[pr + dl * 4 + j];
     }
     if (wave == 0 && kl == 0) {
-      const int ckv[2] = {(H + kh) * kHd + dl * 8, (H + Hkv + kh) * kHd + dl * 8};
-      u32x4_t kv16[2];
-      rows(ckv, kv16);
       const u32x4_t kb16 = rope8(kv16[0], cs, sn);
       const u32x4_t vb16 = kv16[1];
       Row knew, vnew;
