@@ -625,7 +625,7 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
 // measured sweeps of the Llama-3-8B shapes (4096 -> 1024..128256, 14336 -> 4096; m = 2..64):
 //   m <= 8        the multi-row GEMV (gemv_rows_kernel) on up to 384 row tiles (512 for m <= 4, and
 //                 below 4096 for m = 2) where its k-slices fit; otherwise as below;
-//   m <= 16       waves splitting K: 4 tiles x 4 waves from 1024 row tiles, 2 x 8 from 384; from 4096
+//   m <= 16       waves splitting K: 4 tiles x 4 waves above 1024 row tiles, 4 x 8 from 640, 2 x 8 from 384; from 4096
 //                 tiles the LDS-staged variant (4 tiles, 4 waves); below 384 tiles the decode GEMV,
 //                 except for long K (>= 64 blocks) with a workspace (2 x 8 waves, 2 splits);
 //   m <= 32       the LDS-staged variant from 1024 tiles (1 tile per wave, 8 compute waves, or 4 from
@@ -669,9 +669,15 @@ inline SkinnyShape skinny_default_shape(int64_t m, int64_t rows, int64_t cols, i
   } else if (m <= 16) {
     // (sweep of the LDS-staged shapes at M = 16 / 32 / 48 / 64, symmetric int4, rotating weights:
     // the lm_head 62.6 / 73.7 -> 54.1 / 64.7 us with 2 tiles per wave and 4 waves, gate/up at M = 32
-    // 23.0 -> 20.5 us with 2 tiles per wave, down at M = 16 15.2 -> 13.4 us with 4 K splits)
+    // 23.0 -> 20.5 us with 2 tiles per wave, down at M = 16 15.2 -> 13.4 us with 4 K splits.)
+    // 640..1024 tiles: 4 tiles with 8 waves, at most one workgroup per CU (rotating weights, M = 8 /
+    // 16, symmetric and asymmetric int4: 4096->16384 13.4 / 13.8 -> 10.1 / 10.9 us, 4096->14336
+    // 10.8 / 12.9 -> 9.7 / 10.5 us, 4096->12288 10.7 / 12.9 -> 9.4 / 10.3 us); beyond 1024 tiles
+    // (gate/up 4096->28672 15.1 against 17.5 us at M = 8) and below 640 (4096->8192, 4096->6144)
+    // the shapes as before stay ahead.
     if (T >= 4096) s = SkinnyShape{1, 2, 4, 1, false};
-    else if (T >= 1024) s = SkinnyShape{0, 4, 4, 1, false};
+    else if (T > 1024) s = SkinnyShape{0, 4, 4, 1, false};
+    else if (T >= 640) s = SkinnyShape{0, 4, 8, 1, false};
     else if (T >= 384) s = SkinnyShape{0, 2, 8, 1, false};
     else if (have_ws && KB >= 64) s = m == 16 ? SkinnyShape{1, 1, 8, 4, false} : SkinnyShape{0, 2, 8, 2, false};
     else s.gemv = true;
