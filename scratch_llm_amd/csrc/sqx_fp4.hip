@@ -197,51 +197,45 @@ __global__ __launch_bounds__(256) void mxfp4_quantize_tiled_kernel(const void* _
   xst[q] = static_cast<uint8_t>(sbyte);
 }
 
-// bf16(mxfp4_dequantize(mxfp4_quantize(row))) for each row of x [m, k] (k % 32 == 0): one thread per
-// 32-element block, the same code and scale as mxfp4_quantize_tiled_kernel, then code value * 2**e.
-// Every such value is exact in bf16 wherever it is finite in fp32 (the two share the exponent range,
-// and an E2M1 value has 2 significant bits), so these rows times a weight are the products of the two
-// dequantized operands.
+// bf16(mxfp4_dequantize(mxfp4_quantize(row))) for each row of x [m, k] (k % 32 == 0): eight lanes per
+// 32-element block, four elements each, the same code and scale as mxfp4_quantize_tiled_kernel, then
+// code value * 2**e. The block maximum joins the lanes' maxima (amax_step of two maxima is their joint
+// maximum, NaN included). Every such value is exact in bf16 wherever it is finite in fp32 (the two
+// share the exponent range, and an E2M1 value has 2 significant bits), so these rows times a weight
+// are the products of the two dequantized operands. A single row of 8192 columns spreads over eight
+// workgroups instead of one (one thread per block took 7.5 us at M = 1).
 template <int DT>
 __global__ __launch_bounds__(256) void mxfp4_fake_quant_rows_kernel(const void* __restrict__ x, int64_t n_blocks,
                                                                     uint16_t* __restrict__ out) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= n_blocks) return;
-  float v[32];
-  const int64_t base = b * 32;
-  if (DT == SQX_DTYPE_F32) {
-    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(static_cast<const float*>(x) + base);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const u32x4_t w = p[j];
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = (t >> 3) < n_blocks;  // the eight lanes of a block are live or not together
+  const int64_t base = t * 4;
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (live) {
+    if (DT == SQX_DTYPE_F32) {
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(static_cast<const float*>(x) + base);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t u = w[e];
-        v[4 * j + e] = __builtin_bit_cast(float, u);
+        const uint32_t u = w[e];  // an element copy first: bit-casting the subscript reads element 0
+        v[e] = __builtin_bit_cast(float, u);
       }
-    }
-  } else {
-    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + base);
+    } else {
+      const u32x2v_t w = *reinterpret_cast<const u32x2v_t*>(static_cast<const uint16_t*>(x) + base);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const u32x4_t w = p[j];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < 4; ++e) {
         const uint16_t h = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
-        v[8 * j + e] = DT == SQX_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+        v[e] = DT == SQX_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
       }
     }
   }
   float amax = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 32; ++e) amax = amax_step(amax, v[e]);
+  for (int e = 0; e < 4; ++e) amax = amax_step(amax, v[e]);
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) amax = amax_step(amax, __shfl_xor(amax, o, 64));
+  if (!live) return;
   const int ex = mx_exponent(amax);
-  uint32_t o[16];
-#pragma unroll
-  for (int e = 0; e < 32; e += 2) o[e >> 1] = mx_fake_pair(v[e], v[e + 1], ex);
-  u32x4_t* q = reinterpret_cast<u32x4_t*>(out + base);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) q[j] = u32x4_t{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+  *reinterpret_cast<u32x2v_t*>(out + base) = u32x2v_t{mx_fake_pair(v[0], v[1], ex), mx_fake_pair(v[2], v[3], ex)};
 }
 
 // NVFP4 global amax: P partial maxima, then s_global = max(amax / (448 * 6), 1e-30) from them.
@@ -883,13 +877,16 @@ extern "C" int sqx_mxfp4_fake_quant_rows(const void* x, int dtype, int64_t m, in
   SQX_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0, SQX_E_ARG,
               "sqx_mxfp4_fake_quant_rows: x and out must be 16-byte aligned");
   const int64_t nb = m * (k / 32);
+  SQX_REQUIRE(nb < (int64_t(1) << 36), SQX_E_ARG, "sqx_mxfp4_fake_quant_rows: %lld blocks (fewer than 2^36)",
+              (long long)nb);
   hipStream_t s = as_stream(stream);
+  const dim3 grid = grid_for(nb * 8);  // eight lanes per block
   if (dtype == SQX_DTYPE_BF16)
-    hipLaunchKernelGGL(mxfp4_fake_quant_rows_kernel<SQX_DTYPE_BF16>, grid_for(nb), dim3(256), 0, s, x, nb, out);
+    hipLaunchKernelGGL(mxfp4_fake_quant_rows_kernel<SQX_DTYPE_BF16>, grid, dim3(256), 0, s, x, nb, out);
   else if (dtype == SQX_DTYPE_F16)
-    hipLaunchKernelGGL(mxfp4_fake_quant_rows_kernel<SQX_DTYPE_F16>, grid_for(nb), dim3(256), 0, s, x, nb, out);
+    hipLaunchKernelGGL(mxfp4_fake_quant_rows_kernel<SQX_DTYPE_F16>, grid, dim3(256), 0, s, x, nb, out);
   else
-    hipLaunchKernelGGL(mxfp4_fake_quant_rows_kernel<SQX_DTYPE_F32>, grid_for(nb), dim3(256), 0, s, x, nb, out);
+    hipLaunchKernelGGL(mxfp4_fake_quant_rows_kernel<SQX_DTYPE_F32>, grid, dim3(256), 0, s, x, nb, out);
   SQX_LAUNCH_CHECK("sqx_mxfp4_fake_quant_rows");
   return SQX_OK;
 }

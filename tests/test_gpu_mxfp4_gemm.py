@@ -336,17 +336,41 @@ def test_mxfp4_act_linear_config4_small_m(f4, n, k, m):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
-def test_mxfp4_fake_quant_rows_bitexact(f4, dtype):
+@pytest.mark.parametrize("shape", [(40, 1024), (1, 28672), (3, 1184)])
+def test_mxfp4_fake_quant_rows_bitexact(f4, dtype, shape):
     """bf16(mxfp4_dequantize(mxfp4_quantize(row))) per row equals the oracle bit for bit, including
-    all-zero blocks and values across many binades."""
-    print_case("mxfp4 fake-quant rows", dtype)
-    x = _values((40, 1024), 9)
-    x[3, :32] = 0.0
+    all-zero blocks and values across many binades; one long row, and a grid whose last workgroup is
+    partly past the blocks."""
+    print_case("mxfp4 fake-quant rows", dtype, shape)
+    x = _values(shape, 9 + shape[1])
+    x[min(3, shape[0] - 1), :32] = 0.0
     xt = _dev(x, dtype)
     got = f4.mxfp4_fake_quant_rows(xt)
     _, _, xd = oracle_rows(xt.float().cpu().numpy())
     assert got.dtype == torch.bfloat16
     assert np.array_equal(got.float().cpu().numpy(), xd.astype(np.float32))
+
+
+def test_mxfp4_fake_quant_rows_specials(f4):
+    """Blocks holding NaN, +-inf or the largest float, each at a different lane of the eight that share
+    a block (the block maximum joins the lanes' maxima). A block holding NaN has a NaN amax, so the
+    reference's scale 2**ceil(log2(NaN)) is NaN and every dequantized value of the block is NaN (the
+    oracle's integer exponent is undefined there); every other block equals the oracle bit for bit
+    (an infinity's block decodes to signed zeros, the largest float's to 4 * 2**126 = inf)."""
+    print_case("mxfp4 fake-quant rows specials")
+    x = _values((2, 512), 5)
+    fmax = np.finfo(np.float32).max
+    for j, val in enumerate([np.nan, np.inf, -np.inf, fmax, -fmax, np.nan, np.inf, fmax]):
+        x[0, 32 * j + 4 * j + 1] = val  # lane j of block j
+    x[1, 32 * 3 + 30] = np.nan
+    x[1, 32 * 5 + 2] = -np.inf
+    xt = _dev(x, torch.float32)
+    got = f4.mxfp4_fake_quant_rows(xt).float().cpu().numpy()
+    nan_block = np.repeat(np.isnan(x.reshape(2, -1, 32)).any(axis=2), 32, axis=1)
+    assert np.isnan(got[nan_block]).all()
+    with np.errstate(invalid="ignore", over="ignore"):
+        _, _, xd = oracle_rows(x)
+    np.testing.assert_array_equal(got[~nan_block], xd.astype(np.float32)[~nan_block])
 
 
 def test_mxfp4_gemm_rejects(f4):
